@@ -1,0 +1,113 @@
+/*
+ * mamba3_scan.h -- C ABI of the MI355X (gfx950) Mamba3 SISO state-scan operator.
+ *
+ * Plain pointers and sizes only.  Every device pointer is a HIP device
+ * address; `stream` is a hipStream_t passed as void* (NULL = default stream).
+ * All calls are asynchronous on `stream`, allocate nothing, keep no per-call
+ * state and may be issued concurrently from several host threads.  Return
+ * value: 0 on success, else an M3_E* code; m3_last_error() then describes it
+ * (thread-local string).
+ *
+ * Shapes and layouts (row-major, contiguous) follow the reference call
+ * signature mamba3_siso_triton(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles,
+ * D, Z, chunk_size) of bold-lab-ai/sigma-0, src/base_model/models/
+ * mamba3_ops.py:1116-1127 (batched form :1052-1110):
+ *   Q, K    (B, L, Hqk, N)  io dtype, Hqk divides H (head h reads h / (H/Hqk))
+ *   V, Z    (B, L, H, P)    io dtype (Z may be NULL: no gate)
+ *   ADT, DT, Trap (B, H, L) float32 (Trap = pre-sigmoid logits)
+ *   Q_bias, K_bias (H, N)   float32
+ *   Angles  (B, L, H, R)    float32 raw rotation rates, 0 <= R <= N/2
+ *   D       (H,)            float32 or NULL (no feedthrough)
+ *   Out     (B, L, H, P)    io dtype
+ */
+#ifndef MAMBA3_SCAN_H_
+#define MAMBA3_SCAN_H_
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define M3_DTYPE_F32 0
+#define M3_DTYPE_BF16 1
+
+#define M3_OK 0
+#define M3_E_ARG 1      /* invalid shape, dtype, mode or NULL pointer */
+#define M3_E_ALIGN 2    /* a pointer is not 16-byte aligned */
+#define M3_E_UNSUPPORTED 3
+#define M3_E_LAUNCH 4   /* HIP launch error (message from hipGetErrorString) */
+
+/* Kernel selected by m3_chunk_scan_fwd for a shape. */
+#define M3_IMPL_NONE 0
+#define M3_IMPL_CHUNKED_MFMA 1
+#define M3_IMPL_GENERIC 2
+
+/* ABI version (major * 100 + minor). */
+int m3_abi_version(void);
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* m3_last_error(void);
+
+/* Which prefill kernel serves this shape (M3_IMPL_*), without launching. */
+int m3_chunk_scan_impl(int io_dtype, int N, int P, int R, int chunk_size);
+
+/*
+ * Chunked prefill scan, forward.  Replaces the Triton forward launch of
+ * mamba3_siso_triton (src/base_model/models/mamba3_ops.py:158-340, the
+ * triton_call at :287-308; batched entry :1052-1110) and the CUDA phases 4-6
+ * launch siso_state_scan_launch + reduce_y_off_launch
+ * (src/base_model/kernels/mamba3_cuda/ffi/state_scan_ffi.cu:24-38) with one
+ * launch covering phases 1-7 of mamba3_ssd_chunked_jax
+ * (src/base_model/models/mamba3_jax.py:327-419).  Out = y (B, L, H, P).
+ */
+int m3_chunk_scan_fwd(const void* Q, const void* K, const void* V,
+                      const float* ADT, const float* DT, const float* Trap,
+                      const float* Q_bias, const float* K_bias, const float* Angles,
+                      const float* D, const void* Z, void* Out,
+                      int B, int L, int H, int Hqk, int N, int P, int R,
+                      int chunk_size, int io_dtype, void* stream);
+
+/*
+ * Prefill with the recurrent carry in and out (prefill -> decode handoff).
+ * The carry is the decode layout of Mamba3SSM.__call_rnn__ (mamba3.py:478-483,
+ * layers.py:243-256 without the singleton dims), all float32:
+ *   theta (B, H, R), ssm (B, H, P, N), k (B, H, N), v (B, H, P).
+ * init_* may all be NULL (zero carry); fin_* may all be NULL (not returned).
+ * Counterpart of the Triton kernel's HAS_INITIAL_STATES / RETURN_FINAL_STATES
+ * paths (src/base_model/kernels/mamba3_triton/siso_fwd.py:76-77, 281-300,
+ * 373-378), expressed in the decode carry.
+ */
+int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
+                            const float* ADT, const float* DT, const float* Trap,
+                            const float* Q_bias, const float* K_bias, const float* Angles,
+                            const float* D, const void* Z, void* Out,
+                            const float* init_theta, const float* init_ssm,
+                            const float* init_k, const float* init_v,
+                            float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                            int B, int L, int H, int Hqk, int N, int P, int R,
+                            int chunk_size, int io_dtype, void* stream);
+
+/*
+ * One decode step for a batch, in place on the carry.  Replaces the body of
+ * rnn_step inside Mamba3SSM.__call_rnn__ (src/base_model/models/mamba3.py:498-562)
+ * vmapped over batch (lob_seq_model.py:747-751):
+ *   carry (in/out, float32): theta (B,H,R), ssm (B,H,P,N), k (B,H,N), v (B,H,P)
+ *   step inputs: x, z (B,H,P) and Bt, Ct (B,H,N) in in_dtype (z may be NULL);
+ *                adt, dt, trap (B,H) float32, trap AFTER the sigmoid
+ *                (mamba3.py:489); angle (B,H,R) float32 raw rates
+ *   B_bias, C_bias (H,N) float32; D (H,) float32 or NULL
+ *   y (B,H,P) in out_dtype
+ * angle_mode: 1 = "wrapped" (default), 0 = "legacy_unbounded"
+ * diag_mode:  0 = "current" (default), 1 = "legacy_double"  (mamba3.py:28-45)
+ */
+int m3_decode_step(float* theta, float* ssm, float* k, float* v,
+                   const void* x, const void* z, const void* Bt, const void* Ct,
+                   const float* adt, const float* dt, const float* trap, const float* angle,
+                   const float* B_bias, const float* C_bias, const float* D, void* y,
+                   int B, int H, int N, int P, int R,
+                   int in_dtype, int out_dtype, int angle_mode, int diag_mode, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA3_SCAN_H_ */

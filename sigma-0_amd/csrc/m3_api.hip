@@ -1,0 +1,161 @@
+// C ABI of the Mamba3 scan operator: argument validation and kernel dispatch.
+//
+// Stateless: nothing is cached between calls (device properties included), so
+// concurrent calls from several host threads and devices are safe.  Errors are
+// reported through the return code plus a thread-local message, the C
+// analogue of the reference handler's ffi::Error::Internal(cudaGetErrorString)
+// (src/base_model/kernels/mamba3_cuda/ffi/state_scan_ffi.cu:64-66) and of its
+// Python shape asserts (src/base_model/kernels/mamba3_triton/siso_fwd.py:466-482).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/mamba3_scan.h"
+#include "m3_scan.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(M3_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  g_err[0] = '\0';
+  return M3_OK;
+}
+
+int impl_for(int io_dtype, int N, int P, int R, int chunk_size) {
+  const bool bf = io_dtype == M3_DTYPE_BF16;
+  if (m3::scan_chunked_supported(bf, chunk_size, N, P, R)) return M3_IMPL_CHUNKED_MFMA;
+  if (m3::scan_generic_supported(N, P, R)) return M3_IMPL_GENERIC;
+  return M3_IMPL_NONE;
+}
+
+}  // namespace
+
+namespace m3 {
+bool decode_supported(int N, int P, int R) {
+  const int rowl = N / 4;
+  return N >= 4 && N <= 256 && (N % 4) == 0 && (rowl & (rowl - 1)) == 0 && P >= 1 &&
+         P <= 256 && (long)P * N <= 16384 && R >= 0 && 2 * R <= N;
+}
+}  // namespace m3
+
+extern "C" {
+
+int m3_abi_version(void) { return 100; }
+
+const char* m3_last_error(void) { return g_err; }
+
+int m3_chunk_scan_impl(int io_dtype, int N, int P, int R, int chunk_size) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16) return M3_IMPL_NONE;
+  return impl_for(io_dtype, N, P, R, chunk_size);
+}
+
+int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
+                            const float* ADT, const float* DT, const float* Trap,
+                            const float* Q_bias, const float* K_bias, const float* Angles,
+                            const float* D, const void* Z, void* Out,
+                            const float* init_theta, const float* init_ssm,
+                            const float* init_k, const float* init_v,
+                            float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                            int B, int L, int H, int Hqk, int N, int P, int R,
+                            int chunk_size, int io_dtype, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
+    return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d H=%d Hqk=%d N=%d P=%d R=%d chunk=%d)",
+                B, L, H, Hqk, N, P, R, chunk_size);
+  if (H % Hqk != 0) return fail(M3_E_ARG, "nheads (%d) must be divisible by nheads_qk (%d)", H, Hqk);
+  if (2 * R > N) return fail(M3_E_ARG, "num rope angles R=%d must be <= d_state/2 = %d", R, N / 2);
+  const bool any_init = init_theta || init_ssm || init_k || init_v;
+  const bool all_init = init_theta && init_ssm && init_k && init_v;
+  const bool any_fin = fin_theta || fin_ssm || fin_k || fin_v;
+  const bool all_fin = fin_theta && fin_ssm && fin_k && fin_v;
+  if (any_init && !all_init) return fail(M3_E_ARG, "initial carry: pass all of theta, ssm, k, v or none");
+  if (any_fin && !all_fin) return fail(M3_E_ARG, "final carry: pass all of theta, ssm, k, v or none");
+  if (R > 0 && (init_theta == nullptr) && any_init) return fail(M3_E_ARG, "initial theta missing");
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;  // empty batch or sequence: nothing to compute
+  }
+  if (!Q || !K || !V || !ADT || !DT || !Trap || !Q_bias || !K_bias || !Out || (R > 0 && !Angles))
+    return fail(M3_E_ARG, "NULL required pointer");
+  const void* vec_ptrs[] = {Q, K, V, Z, Out, Q_bias, K_bias};
+  for (const void* p : vec_ptrs)
+    if (!aligned16(p)) return fail(M3_E_ALIGN, "Q, K, V, Z, Out and the biases must be 16-byte aligned");
+  const int impl = impl_for(io_dtype, N, P, R, chunk_size);
+  if (impl == M3_IMPL_NONE)
+    return fail(M3_E_UNSUPPORTED, "no kernel for d_state=%d headdim=%d R=%d (generic limits: N even <= 512, "
+                "P <= 512, P*N*4 <= 64 KiB)", N, P, R);
+  m3::ScanArgs a;
+  a.q = Q; a.k = K; a.v = V; a.adt = ADT; a.dt = DT; a.trap = Trap;
+  a.qbias = Q_bias; a.kbias = K_bias; a.ang = Angles; a.D = D; a.z = Z; a.out = Out;
+  a.init_theta = init_theta; a.init_h = init_ssm; a.init_k = init_k; a.init_v = init_v;
+  a.fin_theta = fin_theta; a.fin_h = fin_ssm; a.fin_k = fin_k; a.fin_v = fin_v;
+  a.B = B; a.L = L; a.H = H; a.Hqk = Hqk; a.N = N; a.P = P; a.R = R; a.CS = chunk_size;
+  const bool bf = io_dtype == M3_DTYPE_BF16;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (impl == M3_IMPL_CHUNKED_MFMA) return check_launch(m3::scan_chunked_launch(a, bf, st), "chunk scan");
+  return check_launch(m3::scan_generic_launch(a, bf, st), "generic scan");
+}
+
+int m3_chunk_scan_fwd(const void* Q, const void* K, const void* V,
+                      const float* ADT, const float* DT, const float* Trap,
+                      const float* Q_bias, const float* K_bias, const float* Angles,
+                      const float* D, const void* Z, void* Out,
+                      int B, int L, int H, int Hqk, int N, int P, int R,
+                      int chunk_size, int io_dtype, void* stream) {
+  return m3_chunk_scan_fwd_carry(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out,
+                                 nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                 B, L, H, Hqk, N, P, R, chunk_size, io_dtype, stream);
+}
+
+int m3_decode_step(float* theta, float* ssm, float* k, float* v,
+                   const void* x, const void* z, const void* Bt, const void* Ct,
+                   const float* adt, const float* dt, const float* trap, const float* angle,
+                   const float* B_bias, const float* C_bias, const float* D, void* y,
+                   int B, int H, int N, int P, int R,
+                   int in_dtype, int out_dtype, int angle_mode, int diag_mode, void* stream) {
+  if ((in_dtype != M3_DTYPE_F32 && in_dtype != M3_DTYPE_BF16) ||
+      (out_dtype != M3_DTYPE_F32 && out_dtype != M3_DTYPE_BF16))
+    return fail(M3_E_ARG, "dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16 (in=%d out=%d)", in_dtype, out_dtype);
+  if (angle_mode != 0 && angle_mode != 1)
+    return fail(M3_E_ARG, "angle_mode must be 1 (wrapped) or 0 (legacy_unbounded), got %d", angle_mode);
+  if (diag_mode != 0 && diag_mode != 1)
+    return fail(M3_E_ARG, "diag_mode must be 0 (current) or 1 (legacy_double), got %d", diag_mode);
+  if (B < 0 || H <= 0 || N <= 0 || P <= 0 || R < 0)
+    return fail(M3_E_ARG, "non-positive dimension (B=%d H=%d N=%d P=%d R=%d)", B, H, N, P, R);
+  if (2 * R > N) return fail(M3_E_ARG, "num rope angles R=%d must be <= d_state/2 = %d", R, N / 2);
+  if (!m3::decode_supported(N, P, R))
+    return fail(M3_E_UNSUPPORTED, "decode needs d_state a multiple of 4 with d_state/4 a power of two "
+                "<= 64, headdim <= 256 and headdim*d_state <= 16384 (got N=%d P=%d)", N, P);
+  if (B == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!theta && R > 0) return fail(M3_E_ARG, "NULL angle state");
+  if (!ssm || !k || !v || !x || !Bt || !Ct || !adt || !dt || !trap || !B_bias || !C_bias || !y ||
+      (R > 0 && !angle))
+    return fail(M3_E_ARG, "NULL required pointer");
+  if (!aligned16(ssm)) return fail(M3_E_ALIGN, "ssm state must be 16-byte aligned");
+  m3::DecodeArgs a;
+  a.theta = theta; a.h = ssm; a.kprev = k; a.vprev = v;
+  a.x = x; a.z = z; a.bt = Bt; a.ct = Ct; a.adt = adt; a.dt = dt; a.trap = trap; a.ang = angle;
+  a.bbias = B_bias; a.cbias = C_bias; a.D = D; a.y = y;
+  a.B = B; a.H = H; a.N = N; a.P = P; a.R = R;
+  a.wrapped = angle_mode; a.legacy_double = diag_mode;
+  return check_launch(m3::decode_step_launch(a, in_dtype == M3_DTYPE_BF16, out_dtype == M3_DTYPE_BF16,
+                                             reinterpret_cast<hipStream_t>(stream)),
+                      "decode step");
+}
+
+}  // extern "C"

@@ -1,0 +1,196 @@
+// Single-token Mamba3 decode state update (bandwidth-bound).
+//
+// Restates the recurrence of rnn_step, src/base_model/models/mamba3.py:498-562,
+// for a whole batch at once (the model vmaps it over batch,
+// lob_seq_model.py:747-751):
+//   theta += tanh(angle_t) * pi * dt_t            (wrapped mod 2pi by default)
+//   B_rot  = rope(B_t + B_bias, theta)   C_rot = rope(C_t + C_bias, theta)
+//   h      = d h + (1 - trap) dt d (v_prev (x) k_prev) + trap dt (x_t (x) B_rot),  d = e^{adt}
+//   y      = (C_rot . h + D x_t [+ gamma (C_rot . B_rot) x_t]) * silu(z_t)
+//   carry <- (theta, h, B_rot, x_t)
+//
+// Layout in HBM (all row-major, contiguous): theta (B,H,R) f32, h (B,H,P,N) f32,
+// k_prev (B,H,N) f32, v_prev (B,H,P) f32, x/z (B,H,P), B_t/C_t (B,H,N) in the
+// input dtype, adt/dt/trap (B,H) f32 with trap post-sigmoid, angle (B,H,R) f32,
+// B_bias/C_bias (H,N) f32, D (H,) f32, y (B,H,P) in the output dtype.
+//
+// One 256-thread workgroup per (b, h).  The P*N fp32 state is streamed as
+// float4 with consecutive threads on consecutive 16-byte words, so each wave
+// reads and writes whole 1 KiB spans; those loads are issued before the small
+// per-head preamble (angles, rope, carries) so HBM latency overlaps it.  The
+// output dot C_rot . h reduces over the N/4 lanes holding one state row.
+#include "m3_scan.h"
+
+namespace m3 {
+
+
+
+template <typename T>
+__device__ __forceinline__ float ld_f(const void* p, long i) {
+  return Elem<T>::to_f(reinterpret_cast<const T*>(p)[i]);
+}
+
+constexpr int kDecThreads = 256;
+constexpr int kDecMaxP = 256;
+constexpr int kDecMaxN = 256;
+
+// ROWL = N/4 lanes per state row (a power of two <= 64); MAXV = ceil(P*N/4/256)
+// float4 words per thread for the largest P*N this instantiation serves.
+template <typename TI, typename TO, int ROWL, int MAXV>
+__global__ __launch_bounds__(kDecThreads)
+void decode_step_kernel(DecodeArgs a) {
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int hh = bh % a.H;
+  const int N = a.N, P = a.P, R = a.R;
+  const int nvec = P * N / 4;
+
+  __shared__ float sCos[kDecMaxN / 2], sSin[kDecMaxN / 2];
+  __shared__ float sB[kDecMaxN], sKp[kDecMaxN], sC[kDecMaxN];
+  __shared__ float sX[kDecMaxP], sVp[kDecMaxP], sY[kDecMaxP];
+  __shared__ float sQK;
+
+  // 1. issue the state loads first
+  float4* hrow = reinterpret_cast<float4*>(a.h + (long)bh * P * N);
+  float4 hv[MAXV];
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int v = tid + i * kDecThreads;
+    if (v < nvec) hv[i] = hrow[v];
+  }
+
+  // 2. preamble: carries and step inputs into LDS, angle update
+  const long bhN = (long)bh * N, bhP = (long)bh * P, bhR = (long)bh * R;
+  const float dtv = a.dt[bh];
+  const float trv = a.trap[bh];
+  const float dec = exp_fast(a.adt[bh]);
+  for (int n = tid; n < N; n += kDecThreads) sKp[n] = a.kprev[bhN + n];
+  for (int p = tid; p < P; p += kDecThreads) {
+    sVp[p] = a.vprev[bhP + p];
+    sX[p] = ld_f<TI>(a.x, bhP + p);
+  }
+  for (int r = tid; r < R; r += kDecThreads) {
+    float th = a.theta[bhR + r] + tanh_fast(a.ang[bhR + r]) * kPi * dtv;
+    if (a.wrapped) th = wrap_2pi(th);
+    a.theta[bhR + r] = th;
+    float c, s;
+    if (a.wrapped) {
+      sincos_wrapped(th, &c, &s);
+    } else {
+      c = cosf(th);
+      s = sinf(th);
+    }
+    sCos[r] = c;
+    sSin[r] = s;
+  }
+  if (tid == 0) sQK = 0.0f;
+  __syncthreads();
+
+  // 3. rotated key/query for this step; new carries
+  float qk_part = 0.0f;
+  for (int j = tid; j < N / 2; j += kDecThreads) {
+    const int n0 = 2 * j;
+    float b0 = ld_f<TI>(a.bt, bhN + n0) + a.bbias[(long)hh * N + n0];
+    float b1 = ld_f<TI>(a.bt, bhN + n0 + 1) + a.bbias[(long)hh * N + n0 + 1];
+    float c0 = ld_f<TI>(a.ct, bhN + n0) + a.cbias[(long)hh * N + n0];
+    float c1 = ld_f<TI>(a.ct, bhN + n0 + 1) + a.cbias[(long)hh * N + n0 + 1];
+    if (j < R) {
+      const float cs = sCos[j], sn = sSin[j];
+      float t0 = b0 * cs - b1 * sn, t1 = b0 * sn + b1 * cs;
+      b0 = t0; b1 = t1;
+      t0 = c0 * cs - c1 * sn; t1 = c0 * sn + c1 * cs;
+      c0 = t0; c1 = t1;
+    }
+    sB[n0] = b0; sB[n0 + 1] = b1;
+    sC[n0] = c0; sC[n0 + 1] = c1;
+    a.kprev[bhN + n0] = b0;
+    a.kprev[bhN + n0 + 1] = b1;
+    qk_part += c0 * b0 + c1 * b1;
+  }
+  if (a.legacy_double) atomicAdd(&sQK, qk_part);
+  for (int p = tid; p < P; p += kDecThreads) a.vprev[bhP + p] = sX[p];
+  __syncthreads();
+
+  // 4. state update + output partial dot over n
+  const float c_prev = (1.0f - trv) * dtv * dec;   // (1 - trap) * dt * decay
+  const float c_cur = trv * dtv;                   // trap * dt
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int v = tid + i * kDecThreads;
+    float part = 0.0f;
+    int p = 0;
+    if (v < nvec) {
+      p = v / ROWL;
+      const int n = (v % ROWL) * 4;
+      const float vp = sVp[p], xp = sX[p];
+      float4 hn = hv[i];
+      float* hc = reinterpret_cast<float*>(&hn);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float t = dec * hc[q];
+        t = t + c_prev * (vp * sKp[n + q]);
+        t = t + c_cur * (xp * sB[n + q]);
+        hc[q] = t;
+        part += sC[n + q] * t;
+      }
+      hrow[v] = hn;
+    }
+    part = group_sum<ROWL>(part);
+    if (v < nvec && (v % ROWL) == 0) sY[p] = part;
+  }
+  __syncthreads();
+
+  // 5. output
+  const float Dh = a.D ? a.D[hh] : 0.0f;
+  const float qk = a.legacy_double ? sQK * (dtv * trv) : 0.0f;
+  for (int p = tid; p < P; p += kDecThreads) {
+    float yv = sY[p] + Dh * sX[p];
+    if (a.legacy_double) yv += qk * sX[p];
+    if (a.z) yv *= silu_fast(ld_f<TI>(a.z, bhP + p));
+    reinterpret_cast<TO*>(a.y)[bhP + p] = Elem<TO>::from_f(yv);
+  }
+}
+
+template <typename TI, typename TO, int ROWL>
+static hipError_t launch_rowl(const DecodeArgs& a, hipStream_t st) {
+  const int nvec = a.P * a.N / 4;
+  const int per = (nvec + kDecThreads - 1) / kDecThreads;
+  dim3 grid(a.B * a.H), block(kDecThreads);
+  if (per <= 1) {
+    hipLaunchKernelGGL((decode_step_kernel<TI, TO, ROWL, 1>), grid, block, 0, st, a);
+  } else if (per <= 2) {
+    hipLaunchKernelGGL((decode_step_kernel<TI, TO, ROWL, 2>), grid, block, 0, st, a);
+  } else if (per <= 4) {
+    hipLaunchKernelGGL((decode_step_kernel<TI, TO, ROWL, 4>), grid, block, 0, st, a);
+  } else if (per <= 8) {
+    hipLaunchKernelGGL((decode_step_kernel<TI, TO, ROWL, 8>), grid, block, 0, st, a);
+  } else if (per <= 16) {
+    hipLaunchKernelGGL((decode_step_kernel<TI, TO, ROWL, 16>), grid, block, 0, st, a);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename TI, typename TO>
+static hipError_t launch_types(const DecodeArgs& a, hipStream_t st) {
+  switch (a.N / 4) {
+    case 1: return launch_rowl<TI, TO, 1>(a, st);
+    case 2: return launch_rowl<TI, TO, 2>(a, st);
+    case 4: return launch_rowl<TI, TO, 4>(a, st);
+    case 8: return launch_rowl<TI, TO, 8>(a, st);
+    case 16: return launch_rowl<TI, TO, 16>(a, st);
+    case 32: return launch_rowl<TI, TO, 32>(a, st);
+    case 64: return launch_rowl<TI, TO, 64>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t decode_step_launch(const DecodeArgs& a, bool in_bf16, bool out_bf16, hipStream_t st) {
+  if (in_bf16) {
+    return out_bf16 ? launch_types<bf16, bf16>(a, st) : launch_types<bf16, float>(a, st);
+  }
+  return out_bf16 ? launch_types<float, bf16>(a, st) : launch_types<float, float>(a, st);
+}
+
+}  // namespace m3

@@ -1,0 +1,564 @@
+// Chunked Mamba3 SISO prefill scan on CDNA4 matrix cores.
+//
+// Computes the reference's mamba3_ssd_chunked_jax (phases 1-7,
+// src/base_model/models/mamba3_jax.py:327-419) in one kernel:
+//   phase 1  per-chunk decay prefix (wave64 scan), rotation-angle prefix
+//            (wave64 scans over the chunk, carried across chunks and range
+//            reduced mod 2pi), trapezoid weights, biases, QK-dot skip, rope,
+//            key scaling                                        (:236-324)
+//   phase 3  S^T = K_s Q_r^T on MFMA, causal decay mask in registers, then
+//            Y_diag = M V on MFMA straight from the S^T accumulators (:371-393)
+//   phase 4-6 Y_off = e^{A_cum} (Q_r h^T) on MFMA; h <- e^{A_end} h +
+//            (K_s w)^T V on MFMA, h kept in fp32 accumulators      (:177-233)
+//   phase 7  (Y_diag + Y_off + (D + QK) V) * silu(Z), 16-byte stores (:402-419)
+//
+// One workgroup (4 waves) per (batch, head) walks the chunks in order; the
+// P x N fp32 state never leaves the CU.  While a chunk's matrix work runs,
+// the next chunk's inputs are already in flight into registers, so every
+// input byte is read from HBM exactly once and the output written once.
+//
+// MFMA tile conventions (32x32, verified lane layouts):
+//   A (32 x K): lane i holds row i%32, k = (i/32)*KPL + [0, KPL)
+//   B (K x 32): lane i holds col i%32, k = (i/32)*KPL + [0, KPL)
+//   C (32x32):  lane i, reg r holds col i%32, row 8*(r/4) + 4*(i/32) + r%4
+// bf16: v_mfma_f32_32x32x16_bf16 (KPL = 8); fp32: v_mfma_f32_32x32x2_f32 (KPL = 1).
+// The S^T accumulator is reused as the A operand of M V by permuting the
+// contraction index consistently in the V operand (fragVperm).
+#include <type_traits>
+
+#include "m3_scan.h"
+
+namespace m3 {
+
+template <typename T> struct MF;
+template <> struct MF<bf16> {
+  static constexpr int KSTEP = 16, KPL = 8, PAD = 8;
+  typedef bf16x8 frag;
+  __device__ __forceinline__ static f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // row (row0 + lane%32), KPL contiguous elements at column k0 + (lane/32)*KPL
+  __device__ __forceinline__ static frag ld(const bf16* buf, int ldm, int row0, int k0, int lane) {
+    return *reinterpret_cast<const bf16x8*>(buf + (row0 + (lane & 31)) * ldm + k0 + (lane >> 5) * 8);
+  }
+  // k-step j of the S^T C tile as an A operand: C regs 8j .. 8j+7
+  __device__ __forceinline__ static frag from_acc(const f32x16& c, int j) {
+    frag f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) f[q] = (bf16)c[8 * j + q];
+    return f;
+  }
+  // V operand matching from_acc's contraction order: row p of Vt holds V[:, p];
+  // slots 0..3 <-> s = 16j + 4(lane/32) + 0..3, slots 4..7 <-> s + 8
+  __device__ __forceinline__ static frag vperm(const bf16* vt, int ldv, int p0, int s0, int j, int lane) {
+    const bf16* r = vt + (p0 + (lane & 31)) * ldv + s0 + 16 * j + 4 * (lane >> 5);
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(r);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(r + 8);
+    frag f;
+    f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+    f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+    return f;
+  }
+  // A operand K^T: row n = n0 + lane%32, k = s = s0 + 8(lane/32) + q, read from row-major K[s][n]
+  __device__ __forceinline__ static frag kt(const bf16* k, int ldk, int n0, int s0, int lane) {
+    const bf16* c = k + (s0 + 8 * (lane >> 5)) * ldk + n0 + (lane & 31);
+    frag f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) f[q] = c[q * ldk];
+    return f;
+  }
+  // B operand w-scaled V for the state update: precomputed V^T * w in vwt
+  __device__ __forceinline__ static frag vw(const bf16* vwt, const bf16*, const float*, int ldv, int p0, int s0, int lane) {
+    return ld(vwt, ldv, p0, s0, lane);
+  }
+  // write rows n0 + 8g + 4(lane/32) + 0..3 of column p of a C tile into hb[p][n]
+  __device__ __forceinline__ static void store_ht(bf16* hb, int ldh, int p, int n0, const f32x16& c, int lane) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      bf16x4 v;
+      v[0] = (bf16)c[4 * g]; v[1] = (bf16)c[4 * g + 1]; v[2] = (bf16)c[4 * g + 2]; v[3] = (bf16)c[4 * g + 3];
+      *reinterpret_cast<bf16x4*>(hb + p * ldh + n0 + 8 * g + 4 * (lane >> 5)) = v;
+    }
+  }
+};
+
+template <> struct MF<float> {
+  static constexpr int KSTEP = 2, KPL = 1, PAD = 4;
+  typedef float frag;
+  __device__ __forceinline__ static f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag ld(const float* buf, int ldm, int row0, int k0, int lane) {
+    return buf[(row0 + (lane & 31)) * ldm + k0 + (lane >> 5)];
+  }
+  __device__ __forceinline__ static frag from_acc(const f32x16& c, int j) { return c[j]; }
+  // slot <-> s = 8(j/4) + 4(lane/32) + j%4
+  __device__ __forceinline__ static frag vperm(const float* vt, int ldv, int p0, int s0, int j, int lane) {
+    return vt[(p0 + (lane & 31)) * ldv + s0 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)];
+  }
+  __device__ __forceinline__ static frag kt(const float* k, int ldk, int n0, int s0, int lane) {
+    return k[(s0 + (lane >> 5)) * ldk + n0 + (lane & 31)];
+  }
+  __device__ __forceinline__ static frag vw(const float*, const float* vt, const float* w, int ldv, int p0, int s0, int lane) {
+    const int s = s0 + (lane >> 5);
+    return vt[(p0 + (lane & 31)) * ldv + s] * w[s];
+  }
+  __device__ __forceinline__ static void store_ht(float* hb, int ldh, int p, int n0, const f32x16& c, int lane) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      *reinterpret_cast<float4*>(hb + p * ldh + n0 + 8 * g + 4 * (lane >> 5)) =
+          make_float4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]);
+    }
+  }
+};
+
+// Compile-time geometry of one instantiation.
+template <typename T, int CS_, int N_, int P_, int NW_>
+struct Geo {
+  static constexpr bool BF = std::is_same<T, bf16>::value;
+  static constexpr int CS = CS_, N = N_, P = P_, NW = NW_, NT = 64 * NW_;
+  static constexpr int KSTEP = MF<T>::KSTEP;
+  static constexpr int LB = CS / 32, PB = P / 32, NB = N / 32;
+  static constexpr int LDQ = N + MF<T>::PAD;      // sQ, sK rows
+  static constexpr int LDV = CS + MF<T>::PAD;     // sVt, sVwT rows
+  static constexpr int LDH = N + MF<T>::PAD;      // sHB rows
+  static constexpr int LDY = P + 4;               // sY rows (fp32)
+  static constexpr int RMAX = N / 2;
+  static constexpr int LDA = RMAX + 1;            // angle tables rows (fp32)
+  static constexpr int QV = (CS * N / 8 + NT - 1) / NT;     // 8-wide Q/K vectors per thread
+  static constexpr int VV = (CS * P / 8 + NT - 1) / NT;     // 8-wide V/Z vectors per thread
+  static constexpr int AV = (CS * RMAX + NT - 1) / NT;      // angle scalars per thread (max R)
+  static constexpr int HT = (NB * PB + NW - 1) / NW;        // state tiles per wave
+  static constexpr bool VWT = BF;                           // precomputed w-scaled V^T
+  static constexpr int TS = BF ? 2 : 4;
+  static constexpr int YB = CS * LDY * 4, AB = 2 * CS * LDA * 4;
+  static constexpr int COMMON = 2 * CS * LDQ * TS + (VWT ? 2 : 1) * P * LDV * TS +
+                                (YB > AB ? YB : AB) + 7 * CS * 4 + 64;
+  static constexpr int HBB = P * LDH * TS;
+  // two state-operand buffers (no barrier between the output and state-update
+  // MFMAs) when they fit in the 160 KiB of LDS, else one
+  static constexpr int NHB = (COMMON + 2 * HBB <= 160 * 1024 - 512) ? 2 : 1;
+};
+
+template <typename G>
+struct __attribute__((aligned(16))) Smem {
+  typedef typename std::conditional<G::BF, bf16, float>::type T;
+  T q[G::CS * G::LDQ];
+  T k[G::CS * G::LDQ];
+  T vt[G::P * G::LDV];
+  T vwt[G::VWT ? G::P * G::LDV : 1];
+  T hb[G::NHB][G::P * G::LDH];
+  union __attribute__((aligned(16))) U {
+    float y[G::CS * G::LDY];
+    struct A { float c[G::CS * G::LDA]; float s[G::CS * G::LDA]; } ang;
+  } u;
+  float ac2[G::CS];    // A_cum * log2(e)
+  float expa[G::CS];   // e^{A_cum}
+  float w[G::CS];      // e^{A_end - A_cum}
+  float gam[G::CS];
+  float scl[G::CS];
+  float dtv[G::CS];
+  float qk[G::CS];
+  float dec;
+};
+
+template <typename T, int CS, int N, int P, int NW>
+__global__ __launch_bounds__(64 * NW, 1)
+void scan_chunked_kernel(ScanArgs a) {
+  typedef Geo<T, CS, N, P, NW> G;
+  typedef MF<T> M;
+  static_assert(sizeof(Smem<G>) <= 160 * 1024, "LDS budget");
+  __shared__ Smem<G> sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh = blockIdx.x;
+  const int b = bh / a.H, h = bh % a.H;
+  const int hq = h / (a.H / a.Hqk);
+  const int L = a.L, H = a.H, HQ = a.Hqk, R = a.R;
+  const int nc = (L + CS - 1) / CS;
+  const T* gQ = reinterpret_cast<const T*>(a.q);
+  const T* gK = reinterpret_cast<const T*>(a.k);
+  const T* gV = reinterpret_cast<const T*>(a.v);
+  const T* gZ = reinterpret_cast<const T*>(a.z);
+  T* gO = reinterpret_cast<T*>(a.out);
+  const float* gadt = a.adt + (long)bh * L;
+  const float* gdt = a.dt + (long)bh * L;
+  const float* gtr = a.trap + (long)bh * L;
+  const float Dh = a.D ? a.D[h] : 0.0f;
+  const bool has_z = gZ != nullptr;
+  const int rshift = R > 0 ? __builtin_ctz(R) : 0;  // R is 0 or a power of two
+
+  // ---- per-thread constants: column group of the Q/K vectors, biases
+  constexpr int QG = N / 8;
+  const int qg = tid % QG;
+  float qb[8], kb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    qb[i] = a.qbias[(long)h * N + 8 * qg + i];
+    kb[i] = a.kbias[(long)h * N + 8 * qg + i];
+  }
+
+  // ---- raw input registers (next chunk) and the current chunk's V/Z
+  Vec8<T> rq[G::QV], rk[G::QV], rv[G::VV], rz[G::VV], cv[G::VV], cz[G::VV];
+  float ra[G::AV];
+  float s_adt = 0.f, s_dt = 0.f, s_tr = 0.f, s_dtn = 0.f, s_trn = 0.f;
+
+  auto load_chunk = [&](int c) {
+    const int t0 = c * CS;
+#pragma unroll
+    for (int i = 0; i < G::QV; ++i) {
+      const int v = tid + i * G::NT;
+      const int t = v / QG;
+      if (v < CS * QG && t0 + t < L) {
+        const long off = (((long)b * L + t0 + t) * HQ + hq) * N + 8 * qg;
+        rq[i].load(gQ + off);
+        rk[i].load(gK + off);
+      } else {
+        rq[i].zero();
+        rk[i].zero();
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G::VV; ++i) {
+      const int v = tid + i * G::NT;
+      const int t = v / (P / 8), g8 = v % (P / 8);
+      if (v < CS * (P / 8) && t0 + t < L) {
+        const long off = (((long)b * L + t0 + t) * H + h) * P + 8 * g8;
+        rv[i].load(gV + off);
+        if (has_z) rz[i].load(gZ + off); else rz[i].zero();
+      } else {
+        rv[i].zero();
+        rz[i].zero();
+      }
+    }
+    const int na = CS * R;
+#pragma unroll
+    for (int i = 0; i < G::AV; ++i) {
+      const int e = tid + i * G::NT;
+      const int t = e >> rshift, r = e & (R - 1);
+      ra[i] = (e < na && t0 + t < L) ? a.ang[(((long)b * L + t0 + t) * H + h) * R + r] : 0.0f;
+    }
+    if (wave == 0) {
+      const int t = t0 + lane;
+      const bool ok = lane < CS && t < L;
+      s_adt = ok ? gadt[t] : 0.f;
+      s_dt = ok ? gdt[t] : 0.f;
+      s_tr = ok ? gtr[t] : 0.f;
+      const bool okn = lane == CS - 1 && t0 + CS < L;
+      s_dtn = okn ? gdt[t0 + CS] : 0.f;
+      s_trn = okn ? gtr[t0 + CS] : 0.f;
+    }
+  };
+
+  // wave 0: decay prefix, trapezoid weights for the chunk whose scalars are in s_*
+  auto scalar_stage = [&]() {
+    const float sig = sigmoid_fast(s_tr);
+    const float gam = s_dt * sig;
+    const float u = s_dt * (1.0f - sig);            // dt (1 - sigmoid) of this token
+    float un = __shfl_down(u, 1, 64);               // ... of the next token
+    if (lane == CS - 1) un = s_dtn * (1.0f - sigmoid_fast(s_trn));
+    const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
+    const float aend = __shfl(acum, CS - 1, 64);
+    if (lane < CS) {
+      sm.ac2[lane] = acum * kLog2e;
+      sm.expa[lane] = exp2_fast(acum * kLog2e);
+      sm.w[lane] = exp2_fast((aend - acum) * kLog2e);
+      sm.gam[lane] = gam;
+      sm.scl[lane] = gam + un;
+      sm.dtv[lane] = s_dt;
+    }
+    if (lane == 0) sm.dec = exp2_fast(aend * kLog2e);
+  };
+
+  // ---- state accumulators: tiles z = wave + NW*m of h^T (rows n, cols p)
+  f32x16 hacc[G::HT];
+  float carry[(G::RMAX + NW - 1) / NW];
+#pragma unroll
+  for (int m = 0; m < (G::RMAX + NW - 1) / NW; ++m) {
+    const int r = wave + NW * m;
+    carry[m] = (a.init_theta && r < R) ? a.init_theta[(long)bh * R + r] : 0.0f;
+  }
+  {
+    // effective entering state: h0 + (1 - sigmoid(trap_0)) dt_0 (v0 (x) k0)
+    float cinit = 0.0f;
+    if (a.init_h && L > 0) cinit = (1.0f - sigmoid_fast(gtr[0])) * gdt[0];
+#pragma unroll
+    for (int m = 0; m < G::HT; ++m) {
+      const int z = wave + NW * m;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) hacc[m][r] = 0.0f;
+      if (a.init_h && z < G::NB * G::PB) {
+        const int nb = z / G::PB, pb = z % G::PB;
+        const int p = 32 * pb + (lane & 31);
+        const float v0 = a.init_v[(long)bh * P + p];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int n = 32 * nb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          hacc[m][r] = a.init_h[((long)bh * P + p) * N + n] + cinit * v0 * a.init_k[(long)bh * N + n];
+        }
+      }
+      if (z < G::NB * G::PB) {
+        const int nb = z / G::PB, pb = z % G::PB;
+        M::store_ht(sm.hb[0], G::LDH, 32 * pb + (lane & 31), 32 * nb, hacc[m], lane);
+      }
+    }
+  }
+
+  load_chunk(0);
+  if (wave == 0) scalar_stage();
+  __syncthreads();
+
+  for (int c = 0; c < nc; ++c) {
+    const int t0 = c * CS;
+    const int hcur = c % G::NHB, hnext = (c + 1) % G::NHB;
+
+    // ---- phase 1a: per-element rotation increments tanh(theta) pi dt -> angle table
+    {
+      const int na = CS * R;
+#pragma unroll
+      for (int i = 0; i < G::AV; ++i) {
+        const int e = tid + i * G::NT;
+        if (e < na) {
+          const int t = e >> rshift, r = e & (R - 1);
+          sm.u.ang.c[t * G::LDA + r] = tanh_fast(ra[i]) * kPi * sm.dtv[t];
+        }
+      }
+    }
+    __syncthreads();
+    // ---- phase 1b: prefix over the chunk per rotation column, carry, wrap, cos/sin
+#pragma unroll
+    for (int m = 0; m < (G::RMAX + NW - 1) / NW; ++m) {
+      const int r = wave + NW * m;
+      if (r < R) {
+        const float d = lane < CS ? sm.u.ang.c[lane * G::LDA + r] : 0.0f;
+        const float th = wrap_2pi(carry[m] + wave_incl_scan(d));
+        carry[m] = __shfl(th, CS - 1, 64);
+        if (lane < CS) {
+          float cs, sn;
+          sincos_wrapped(th, &cs, &sn);
+          sm.u.ang.c[lane * G::LDA + r] = cs;
+          sm.u.ang.s[lane * G::LDA + r] = sn;
+        }
+      }
+    }
+    __syncthreads();
+    // ---- phase 1c: biases, QK skip, rope, key scale -> sQ, sK; V^T, (w V)^T
+#pragma unroll
+    for (int i = 0; i < G::QV; ++i) {
+      const int v = tid + i * G::NT;
+      const int t = v / QG;
+      float qf[8], kf[8];
+      rq[i].to_f(qf);
+      rk[i].to_f(kf);
+      float dot = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qf[e] += qb[e];
+        kf[e] += kb[e];
+        dot += qf[e] * kf[e];
+      }
+      dot = group_sum<QG>(dot);
+      if (v < CS * QG) {
+        const bool real = t0 + t < L;
+        if (qg == 0) sm.qk[t] = real ? dot * sm.gam[t] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int j = 4 * qg + q;
+          if (j < R) {
+            const float cs = sm.u.ang.c[t * G::LDA + j], sn = sm.u.ang.s[t * G::LDA + j];
+            const float q0 = qf[2 * q], q1 = qf[2 * q + 1];
+            qf[2 * q] = q0 * cs - q1 * sn;
+            qf[2 * q + 1] = q0 * sn + q1 * cs;
+            const float k0 = kf[2 * q], k1 = kf[2 * q + 1];
+            kf[2 * q] = k0 * cs - k1 * sn;
+            kf[2 * q + 1] = k0 * sn + k1 * cs;
+          }
+        }
+        if (a.fin_k && t0 + t == L - 1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a.fin_k[(long)bh * N + 8 * qg + e] = kf[e];
+        }
+        const float sc = sm.scl[t];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          qf[e] = real ? qf[e] : 0.0f;
+          kf[e] = real ? kf[e] * sc : 0.0f;
+        }
+        store8(&sm.q[t * G::LDQ + 8 * qg], qf);
+        store8(&sm.k[t * G::LDQ + 8 * qg], kf);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G::VV; ++i) {
+      const int v = tid + i * G::NT;
+      cv[i] = rv[i];
+      cz[i] = rz[i];
+      if (v < CS * (P / 8)) {
+        const int t = v / (P / 8), g8 = v % (P / 8);
+        float vf[8];
+        rv[i].to_f(vf);
+        const float wt = sm.w[t];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          sm.vt[(8 * g8 + q) * G::LDV + t] = Elem<T>::from_f(vf[q]);
+          if (G::VWT) sm.vwt[(8 * g8 + q) * G::LDV + t] = Elem<T>::from_f(vf[q] * wt);
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- next chunk's inputs go in flight under the matrix work
+    if (c + 1 < nc) load_chunk(c + 1);
+
+    // ---- phase 3 + 6: Y = mask(K_s Q_r^T)^T V + e^{A_cum} Q_r h^T  -> sY
+    for (int y = wave; y < G::LB * G::PB; y += NW) {
+      const int lb = y / G::PB, pb = y % G::PB;
+      f32x16 yd, yo;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { yd[r] = 0.0f; yo[r] = 0.0f; }
+      const int l = 32 * lb + (lane & 31);
+      const float al = sm.ac2[l];
+      for (int sb = 0; sb <= lb; ++sb) {
+        f32x16 st;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[r] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < N / G::KSTEP; ++kk) {
+          st = M::mma(M::ld(sm.k, G::LDQ, 32 * sb, kk * G::KSTEP, lane),
+                      M::ld(sm.q, G::LDQ, 32 * lb, kk * G::KSTEP, lane), st);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int s = 32 * sb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          st[r] = s < l ? st[r] * exp2_fast(al - sm.ac2[s]) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 32 / G::KSTEP; ++j) {
+          yd = M::mma(M::from_acc(st, j), M::vperm(sm.vt, G::LDV, 32 * pb, 32 * sb, j, lane), yd);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < N / G::KSTEP; ++kk) {
+        yo = M::mma(M::ld(sm.q, G::LDQ, 32 * lb, kk * G::KSTEP, lane),
+                    M::ld(sm.hb[hcur], G::LDH, 32 * pb, kk * G::KSTEP, lane), yo);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = 32 * lb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        sm.u.y[lr * G::LDY + 32 * pb + (lane & 31)] = yd[r] + sm.expa[lr] * yo[r];
+      }
+    }
+    if (G::NHB == 1) __syncthreads();  // single state buffer: all reads of hb done
+
+    // ---- phase 4-5: h <- e^{A_end} h + (K_s)^T (w V)
+    {
+      const float dec = sm.dec;
+#pragma unroll
+      for (int m = 0; m < G::HT; ++m) {
+        const int z = wave + NW * m;
+        if (z < G::NB * G::PB) {
+          const int nb = z / G::PB, pb = z % G::PB;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) hacc[m][r] *= dec;
+#pragma unroll
+          for (int j = 0; j < CS / G::KSTEP; ++j) {
+            hacc[m] = M::mma(M::kt(sm.k, G::LDQ, 32 * nb, j * G::KSTEP, lane),
+                             M::vw(sm.vwt, sm.vt, sm.w, G::LDV, 32 * pb, j * G::KSTEP, lane), hacc[m]);
+          }
+          M::store_ht(sm.hb[hnext], G::LDH, 32 * pb + (lane & 31), 32 * nb, hacc[m], lane);
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- phase 7: (Y + (D + QK) V) * silu(Z) -> out
+#pragma unroll
+    for (int i = 0; i < G::VV; ++i) {
+      const int v = tid + i * G::NT;
+      const int t = v / (P / 8), g8 = v % (P / 8);
+      if (v < CS * (P / 8) && t0 + t < L) {
+        float vf[8], zf[8], yv[8];
+        cv[i].to_f(vf);
+        cz[i].to_f(zf);
+        const float4 y0 = *reinterpret_cast<const float4*>(&sm.u.y[t * G::LDY + 8 * g8]);
+        const float4 y1 = *reinterpret_cast<const float4*>(&sm.u.y[t * G::LDY + 8 * g8 + 4]);
+        yv[0] = y0.x; yv[1] = y0.y; yv[2] = y0.z; yv[3] = y0.w;
+        yv[4] = y1.x; yv[5] = y1.y; yv[6] = y1.z; yv[7] = y1.w;
+        const float dq = Dh + sm.qk[t];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          float o = yv[q] + dq * vf[q];
+          if (has_z) o *= silu_fast(zf[q]);
+          yv[q] = o;
+        }
+        const long off = (((long)b * L + t0 + t) * H + h) * P + 8 * g8;
+        store8(gO + off, yv);
+        if (a.fin_v && t0 + t == L - 1) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) a.fin_v[(long)bh * P + 8 * g8 + q] = vf[q];
+        }
+      }
+    }
+    if (wave == 0 && c + 1 < nc) scalar_stage();
+    __syncthreads();
+  }
+
+  if (a.fin_h) {
+#pragma unroll
+    for (int m = 0; m < G::HT; ++m) {
+      const int z = wave + NW * m;
+      if (z < G::NB * G::PB) {
+        const int nb = z / G::PB, pb = z % G::PB;
+        const int p = 32 * pb + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int n = 32 * nb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          a.fin_h[((long)bh * P + p) * N + n] = hacc[m][r];
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < (G::RMAX + NW - 1) / NW; ++m) {
+      const int r = wave + NW * m;
+      if (r < R && lane == 0) a.fin_theta[(long)bh * R + r] = carry[m];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+template <typename T, int CS, int N, int P>
+static hipError_t launch_one(const ScanArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((scan_chunked_kernel<T, CS, N, P, 4>), dim3(a.B * a.H), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+#define M3_CHUNK_SHAPES(X)                                                        \
+  X(bf16, 64, 128, 64) X(bf16, 64, 64, 64) X(bf16, 64, 128, 128) X(bf16, 64, 64, 32)  \
+  X(bf16, 64, 128, 32) X(bf16, 32, 128, 64) X(bf16, 32, 64, 64) X(bf16, 32, 64, 32)   \
+  X(bf16, 32, 128, 32) X(bf16, 64, 32, 32) X(bf16, 64, 32, 64) X(bf16, 32, 32, 32)     \
+  X(float, 64, 64, 64) X(float, 64, 64, 32) X(float, 32, 64, 64) X(float, 32, 64, 32)  \
+  X(float, 64, 32, 32) X(float, 64, 32, 64) X(float, 32, 32, 32)
+
+static bool r_ok(int N, int R) { return R == 0 || (R > 0 && 2 * R <= N && (R & (R - 1)) == 0); }
+
+bool scan_chunked_supported(bool bf16_io, int CS, int N, int P, int R) {
+  if (!r_ok(N, R)) return false;
+#define X(T, cs, n, p) \
+  if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && N == n && P == p) return true;
+  M3_CHUNK_SHAPES(X)
+#undef X
+  return false;
+}
+
+hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
+#define X(T, cs, n, p)                                                                  \
+  if ((std::is_same<T, bf16>::value == bf16_io) && a.CS == cs && a.N == n && a.P == p) \
+    return launch_one<T, cs, n, p>(a, st);
+  M3_CHUNK_SHAPES(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+}  // namespace m3

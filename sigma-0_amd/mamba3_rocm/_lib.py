@@ -1,0 +1,72 @@
+"""ctypes binding of the C ABI in include/mamba3_scan.h.
+
+The library is loaded once, after ``import torch`` so that it binds to the HIP
+runtime torch already loaded (both carry the soname libamdhip64.so.7).  There
+is no fallback: if the library is missing or does not export the ABI, every
+entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (load torch's HIP runtime first)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmamba3_rocm.so")
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+IMPL_NONE, IMPL_CHUNKED_MFMA, IMPL_GENERIC = 0, 1, 2
+
+EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_scan_fwd",
+           "m3_chunk_scan_fwd_carry", "m3_decode_step")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SIGS = {
+    "m3_abi_version": ([], _I),
+    "m3_last_error": ([], ctypes.c_char_p),
+    "m3_chunk_scan_impl": ([_I] * 5, _I),
+    "m3_chunk_scan_fwd": ([_P] * 12 + [_I] * 9 + [_P], _I),
+    "m3_chunk_scan_fwd_carry": ([_P] * 20 + [_I] * 9 + [_P], _I),
+    "m3_decode_step": ([_P] * 16 + [_I] * 9 + [_P], _I),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class Mamba3LibraryError(RuntimeError):
+    """The HIP library is missing, stale, or a call into it failed."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises Mamba3LibraryError if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise Mamba3LibraryError(
+                    f"{LIB_PATH} is not built; run `python sigma-0_amd/build.py` (hipcc, gfx950)")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in _SIGS.items():
+                fn = getattr(lib, name, None)
+                if fn is None:
+                    raise Mamba3LibraryError(f"{LIB_PATH} does not export {name}")
+                fn.argtypes = args
+                fn.restype = res
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().m3_last_error().decode(errors="replace")
+        raise Mamba3LibraryError(f"{what} failed (code {rc}): {msg}")
+
+
+def impl_for(io_dtype: int, N: int, P: int, R: int, chunk_size: int) -> int:
+    return load().m3_chunk_scan_impl(io_dtype, N, P, R, chunk_size)

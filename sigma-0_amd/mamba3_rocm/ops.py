@@ -1,0 +1,160 @@
+"""Prefill entry points with the reference's call signatures (torch tensors on a
+ROCm device; torch provides device memory and the stream only).
+
+``mamba3_siso_hip`` keeps the argument order and meaning of the reference's
+``mamba3_siso_triton(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z,
+chunk_size)`` (src/base_model/models/mamba3_ops.py:1116-1127): unbatched
+arrays as ``nn.vmap`` hands them over, or the batched layout of its vmap rule
+(:1121-1127, :1052-1110).  ``mamba3_ssd_chunked_hip`` keeps the oracle's
+order (src/base_model/models/mamba3_jax.py:327-331).  Shape contracts raise
+ValueError with the reference's assert messages
+(src/base_model/kernels/mamba3_triton/siso_fwd.py:466-482); the result is
+returned in ``V.dtype`` (mamba3_ops.py:273).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+_IO = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _dev(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a ROCm device tensor (got device {t.device}); "
+                         "the Mamba3 HIP operator has no CPU path")
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.float32).contiguous()
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z):
+    """Validate and normalise to the batched contiguous layout of the C ABI."""
+    unbatched = V.dim() == 3
+    if unbatched:
+        Q, K, V = Q[None], K[None], V[None]
+        ADT, DT, Trap = ADT[None], DT[None], Trap[None]
+        Angles = Angles[None]
+        if Z is not None and Z.dim() == 3:
+            Z = Z[None]
+    _req(V.dim() == 4, f"V must be (L, H, P) or (B, L, H, P), got {tuple(V.shape)}")
+    B, L, HQ, N = Q.shape
+    _, _, H, P = V.shape
+    for name, t in (("Q", Q), ("K", K), ("V", V)):
+        _dev(t, name)
+    _req(L > 0 or B == 0, "Sequence length must be greater than 0")
+    _req(tuple(Q.shape) == tuple(K.shape), f"Q and K shape mismatch: {tuple(Q.shape)} vs {tuple(K.shape)}")
+    _req(H % HQ == 0, f"nheads ({H}) must be divisible by nheads_qk ({HQ})")
+    _req(tuple(V.shape[:2]) == (B, L), f"V shape {tuple(V.shape)} does not match Q {tuple(Q.shape)}")
+    _req(tuple(ADT.shape) == (B, H, L), f"ADT must be {(B, H, L)}, got {tuple(ADT.shape)}")
+    _req(tuple(DT.shape) == (B, H, L), f"DT must be {(B, H, L)}, got {tuple(DT.shape)}")
+    _req(tuple(Trap.shape) == (B, H, L), f"Trap must be {(B, H, L)}, got {tuple(Trap.shape)}")
+    _req(tuple(Q_bias.shape) == (H, N), f"Q_bias must be {(H, N)}, got {tuple(Q_bias.shape)}")
+    _req(tuple(K_bias.shape) == (H, N), f"K_bias must be {(H, N)}, got {tuple(K_bias.shape)}")
+    _req(Angles.dim() == 4 and tuple(Angles.shape[:3]) == (B, L, H),
+         f"Angles must be {(B, L, H, '<R>')}, got {tuple(Angles.shape)}")
+    R = Angles.shape[-1]
+    _req(R <= N // 2, f"headdim_angles ({R}) must be <= headdim_qk // 2 ({N // 2})")
+    if D is not None:
+        _req(tuple(D.shape) == (H,), f"D must be {(H,)}, got {tuple(D.shape)}")
+    if Z is not None:
+        _req(tuple(Z.shape) == (B, L, H, P), f"Z must be {(B, L, H, P)}, got {tuple(Z.shape)}")
+    dt = V.dtype
+    _req(dt in _IO, f"V dtype must be float32 or bfloat16, got {dt}")
+    Q, K, V = (t.to(dt).contiguous() for t in (Q, K, V))
+    Z = None if Z is None else Z.to(dt).contiguous()
+    prepared = dict(
+        Q=Q, K=K, V=V, ADT=_f32(ADT), DT=_f32(DT), Trap=_f32(Trap), Q_bias=_f32(Q_bias),
+        K_bias=_f32(K_bias), Angles=_f32(Angles), D=None if D is None else _f32(D), Z=Z)
+    return prepared, (B, L, H, HQ, N, P, R), unbatched
+
+
+def _launch(p, dims, chunk_size, out, init=None, fin=None):
+    B, L, H, HQ, N, P, R = dims
+    lib = _lib.load()
+    io = _IO[p["V"].dtype]
+    common = (_ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]),
+              _ptr(p["Trap"]), _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]),
+              _ptr(p["D"]), _ptr(p["Z"]), _ptr(out))
+    tail = (B, L, H, HQ, N, P, R, int(chunk_size), io, _stream(p["V"]))
+    if init is None and fin is None:
+        rc = lib.m3_chunk_scan_fwd(*common, *tail)
+    else:
+        ip = tuple(_ptr(t) for t in init) if init is not None else (None,) * 4
+        fp = tuple(_ptr(t) for t in fin) if fin is not None else (None,) * 4
+        rc = lib.m3_chunk_scan_fwd_carry(*common, *ip, *fp, *tail)
+    _lib.check(rc, "m3_chunk_scan_fwd")
+
+
+def mamba3_siso_hip(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
+                    chunk_size: int = 64) -> torch.Tensor:
+    """Mamba3 SISO chunked scan forward on gfx950.
+
+    Same arguments as the reference's mamba3_siso_triton (mamba3_ops.py:1116):
+    Q, K (L, Hqk, N); V, Z (L, H, P); ADT, DT, Trap (H, L) with Trap the
+    pre-sigmoid logits; Q_bias, K_bias (H, N); Angles (L, H, R) raw rates;
+    D (H,) or None; Z or None; or all of them with a leading batch dim.
+    Returns Out with V's shape and dtype.
+    """
+    p, dims, unbatched = _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z)
+    out = torch.empty_like(p["V"])
+    if out.numel():
+        _launch(p, dims, chunk_size, out)
+    return out[0] if unbatched else out
+
+
+def mamba3_ssd_chunked_hip(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z,
+                           chunk_size: int = 64) -> torch.Tensor:
+    """The oracle's signature (mamba3_jax.py:327-331): angles 7th, D and Z required
+    there (None accepted here).  Same computation as mamba3_siso_hip."""
+    return mamba3_siso_hip(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, angles, D, Z, chunk_size)
+
+
+def new_carry(B: int, H: int, N: int, P: int, R: int, device) -> Tuple[torch.Tensor, ...]:
+    """Zero recurrent carry (theta (B,H,R), ssm (B,H,P,N), k (B,H,N), v (B,H,P)), the
+    layout of the reference's Mamba3 decode carry (layers.py:243-256 without the
+    singleton dims)."""
+    z = dict(device=device, dtype=torch.float32)
+    return (torch.zeros(B, H, R, **z), torch.zeros(B, H, P, N, **z),
+            torch.zeros(B, H, N, **z), torch.zeros(B, H, P, **z))
+
+
+def mamba3_siso_hip_carry(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
+                          chunk_size: int = 64, initial_carry=None):
+    """Prefill that also consumes and returns the recurrent carry, so decode can
+    continue where prefill stopped (the Triton kernel's HAS_INITIAL_STATES /
+    RETURN_FINAL_STATES, siso_fwd.py:76-77).  Batched inputs only.
+    Returns (Out, (theta, ssm, k, v))."""
+    p, dims, unbatched = _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z)
+    _req(not unbatched, "mamba3_siso_hip_carry takes batched (B, L, ...) inputs")
+    B, L, H, HQ, N, P, R = dims
+    out = torch.empty_like(p["V"])
+    fin = new_carry(B, H, N, P, R, p["V"].device)
+    init = None
+    if initial_carry is not None:
+        init = tuple(_f32(t) for t in initial_carry)
+        shapes = [(B, H, R), (B, H, P, N), (B, H, N), (B, H, P)]
+        for t, s, n in zip(init, shapes, ("theta", "ssm", "k", "v")):
+            _req(tuple(t.shape) == s, f"initial carry {n} must be {s}, got {tuple(t.shape)}")
+    if out.numel():
+        _launch(p, dims, chunk_size, out, init=init, fin=fin)
+    elif init is not None:
+        fin = tuple(t.clone() for t in init)
+    return out, fin
