@@ -1,0 +1,269 @@
+"""Benchmark: Mamba3 chunked scan throughput on one MI355X (+ roofline, CPU baseline).
+
+Headline workload: the bf16 chunked Mamba3 SISO scan
+forward at B=8, L=4096, H=32, P=64, N=128, R=32, chunk 64, with fp32 state and
+accumulation; synthetic inputs with the configuration's seeded distributions,
+generated on the device before timing (inputs resident in HBM).  A "step" is
+one scan call over the whole batch (one kernel launch).  ``value`` is tokens/s
+over the batch (B*L tokens per step, every head included).
+
+Also reported on the same JSON line:
+  roofline      for the scan kernel: algorithmic bytes per launch /
+                mean kernel time from HIP events on the launch stream
+  cpu_baseline  the numpy float32 restatement of the reference scan
+                (oracle/, the reference's own JAX is not installed) timed on
+                the host on a bounded sample (one of the 8 sequences)
+  secondary     decode state update (config 4, HBM GB/s) and the long-context
+                scan (config 3), each with its own roofline
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--no-secondary] [--mode scan|decode|copy]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sigma-0_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Mamba3 scan tokens/s + % of MFMA/HBM roofline, bf16 B=8 L=4096 H=32"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "scan_chunked_bf16_config2_traffic.json")
+
+
+def scan_bytes(B, L, H, N, P, R, s_io):
+    """Algorithmic HBM bytes of one prefill call: every input read once, Out
+    written once -- Q, K (N each), V, Z, Out (P each) at s_io bytes, ADT, DT,
+    Trap and R angle rates in f32 per token-head (biases negligible)."""
+    return B * L * H * ((2 * N + 3 * P) * s_io + 3 * 4 + R * 4)
+
+
+def scan_flops(B, L, H, N, P, CS):
+    """Dense-tile SSD FLOP count per call: 2*CS*N + 2*CS*P + 4*P*N per token-head."""
+    return B * L * H * (2 * CS * N + 2 * CS * P + 4 * P * N)
+
+
+def decode_bytes(B, H, N, P, R, s_in, s_out):
+    """Per decode step: f32 state, angle, k and v carries read and written,
+    step inputs (x, z, B, C at s_in; adt, dt, trap, R angles f32) and y."""
+    return B * H * (2 * P * N * 4 + 2 * R * 4 + 2 * N * 4 + 2 * P * 4 + (2 * P + 2 * N) * s_in
+                    + 3 * 4 + R * 4 + P * s_out)
+
+
+def make_scan_inputs(torch, B, L, H, N, P, R, seed, io_dtype, device="cuda"):
+    """Seeded synthetic scan inputs on the device (config distributions:
+    x, z ~ N(0,1); dt = softplus(N(-2,0.5)); A_h = -exp(U[0, ln 16]);
+    B, C ~ N(0,1)/sqrt(N); biases ~ N(0,1)/sqrt(N); D ~ N(0,1);
+    angles ~ U[-pi, pi]; trap ~ U(0,1))."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    f = dict(device=device, dtype=torch.float32, generator=g)
+    sN = 1.0 / math.sqrt(N)
+    Q = (torch.randn(B, L, H, N, **f) * sN).to(io_dtype)
+    K = (torch.randn(B, L, H, N, **f) * sN).to(io_dtype)
+    V = torch.randn(B, L, H, P, **f).to(io_dtype)
+    Z = torch.randn(B, L, H, P, **f).to(io_dtype)
+    DT = torch.nn.functional.softplus(torch.randn(B, H, L, **f) * 0.5 - 2.0)
+    A = -torch.exp(torch.rand(H, **f) * math.log(16.0))
+    ADT = (A[None, :, None] * DT).contiguous()
+    Trap = torch.rand(B, H, L, **f)
+    Ang = (torch.rand(B, L, H, R, **f) * 2 - 1) * math.pi
+    Qb = torch.randn(H, N, **f) * sN
+    Kb = torch.randn(H, N, **f) * sN
+    D = torch.randn(H, **f)
+    return (Q, K, V, ADT, DT, Trap, Qb, Kb, Ang, D, Z)
+
+
+def time_calls(torch, fn, steps, warmup):
+    """Warm up, then time `steps` calls: wall clock between synchronisations and
+    per-call HIP events on the current stream (where the kernels launch)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for s, e in ev:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    kern = sum(s.elapsed_time(e) for s, e in ev) / steps / 1e3
+    return wall, kern
+
+
+def bench_scan(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
+    from mamba3_rocm import mamba3_siso_hip
+    args = make_scan_inputs(torch, B, L, H, N, P, R, seed, torch.bfloat16)
+    fn = lambda: mamba3_siso_hip(*args, chunk_size=CS)  # noqa: E731
+    wall, kern = time_calls(torch, fn, steps, warmup)
+    nbytes = scan_bytes(B, L, H, N, P, R, 2)
+    return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, flops=scan_flops(B, L, H, N, P, CS),
+                achieved_gbs=nbytes / kern / 1e9)
+
+
+def bench_decode(torch, B, H, N, P, R, steps, warmup, seed):
+    """Config 4: `steps` consecutive decode steps in place on a B=512 carry."""
+    from mamba3_rocm import rnn_step_hip
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    f = dict(device="cuda", dtype=torch.float32, generator=g)
+    sN = 1.0 / math.sqrt(N)
+    carry = (torch.rand(B, H, R, **f) * 2 * math.pi, torch.randn(B, H, P, N, **f) * 0.1,
+             torch.randn(B, H, N, **f) * sN, torch.randn(B, H, P, **f))
+    T = steps + warmup
+    bf = torch.bfloat16
+    xs = torch.randn(T, B, H, P, **f).to(bf)
+    zs = torch.randn(T, B, H, P, **f).to(bf)
+    bs = (torch.randn(T, B, H, N, **f) * sN).to(bf)
+    cs = (torch.randn(T, B, H, N, **f) * sN).to(bf)
+    dts = torch.nn.functional.softplus(torch.randn(T, B, H, **f) * 0.5 - 2.0)
+    A = -torch.exp(torch.rand(H, **f) * math.log(16.0))
+    adts = A[None, None, :] * dts
+    traps = torch.sigmoid(torch.rand(T, B, H, **f))
+    angs = (torch.rand(T, B, H, R, **f) * 2 - 1) * math.pi
+    Bb, Cb, D = torch.randn(H, N, **f) * sN, torch.randn(H, N, **f) * sN, torch.randn(H, **f)
+    step = [0]
+
+    def fn():
+        i = step[0]
+        step[0] += 1
+        rnn_step_hip(carry, (xs[i], zs[i], bs[i], cs[i], adts[i], dts[i], traps[i], angs[i]),
+                     Bb, Cb, D, angle_mode="wrapped", diag_mode="current")
+
+    wall, kern = time_calls(torch, fn, steps, warmup)
+    nbytes = decode_bytes(B, H, N, P, R, 2, 4)
+    return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
+
+
+def bench_copy(torch, nbytes, steps, warmup):
+    """Plain device copy of a known size: calibration kernel for the PMC
+    FETCH_SIZE / WRITE_SIZE counters."""
+    n = nbytes // 2
+    x = torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_()
+    y = torch.empty_like(x)
+    wall, kern = time_calls(torch, lambda: y.copy_(x), steps, warmup)
+    return dict(kernel_s=kern, read_bytes=n * 2, write_bytes=n * 2,
+                achieved_gbs=2 * n * 2 / kern / 1e9)
+
+
+def cpu_baseline():
+    """Numpy float32 restatement of the reference scan (oracle/mamba3_ref.py,
+    following mamba3_jax.py:62-419 with the dense phase-5 state pass) on one
+    sequence of the headline workload: 4096 tokens x 32 heads."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import inputs as I
+    from oracle import mamba3_ref as M
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    B, L, H, N, P, R, CS = 1, 4096, 32, 128, 64, 32, 64
+    d = I.scan_inputs(B, L, H, N, P, R, seed=2, bf16=True)
+    args = (d["Q"], d["K"], d["V"], d["ADT"], d["DT"], d["Trap"], d["Angles"], d["Q_bias"],
+            d["K_bias"], d["D"], d["Z"])
+    t0 = time.perf_counter()
+    M.mamba3_ssd_chunked_batched(*args, chunk_size=CS, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    return {"value": round(B * L / dt, 1), "unit": "tokens/s", "cores": int(threads),
+            "kind": "port",
+            "sample": (f"numpy float32 restatement of mamba3_ssd_chunked_jax (reference JAX not "
+                       f"installed), 1 of 8 sequences of the headline workload (L=4096, H=32, "
+                       f"N=128, P=64, chunk 64), {dt:.1f} s, BLAS threads={threads}, "
+                       f"host={len(os.sched_getaffinity(0))} cores")}
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            return json.load(fh).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--mode", choices=("scan", "decode", "copy"), default="scan")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): "
+              "this build runs the scan on a single MI355X; the batch and head axes shard "
+              "across GPUs with no exchange.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+
+    if args.mode == "copy":
+        r = bench_copy(torch, 1 << 30, args.steps, args.warmup)
+        print(json.dumps({"mode": "copy", **r}), flush=True)
+        return
+    if args.mode == "decode":
+        r = bench_decode(torch, 512, 32, 128, 64, 32, args.steps, args.warmup, seed=4)
+        print(json.dumps({"mode": "decode", **r}), flush=True)
+        return
+
+    B, L, H, N, P, R, CS = 8, 4096, 32, 128, 64, 32, 64
+    r = bench_scan(torch, B, L, H, N, P, R, CS, args.steps, args.warmup, seed=2)
+    ms = r["wall_s"] * 1e3
+    out = {
+        "metric": METRIC,
+        "value": round(B * L / r["wall_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded, config distributions, generated on device)",
+        "config": {"workload": "mamba3 chunked scan forward, config 2", "B": B, "L": L, "H": H,
+                   "P": P, "N": N, "R": R, "chunk": CS, "io_dtype": "bf16",
+                   "state_dtype": "f32"},
+        "roofline": {"bound": "hbm", "achieved": round(r["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(), "algorithmic_bytes": r["bytes"],
+                     "kernel_ms": round(r["kernel_s"] * 1e3, 4),
+                     "mfma_tflops": round(r["flops"] / r["kernel_s"] / 1e12, 1)},
+    }
+    if not args.no_secondary:
+        dec = bench_decode(torch, 512, 32, 128, 64, 32, 256, 16, seed=4)
+        lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
+        out["secondary"] = {
+            "decode_config4": {"B": 512, "H": 32, "P": 64, "N": 128, "steps": 256,
+                               "us_per_step": round(dec["kernel_s"] * 1e6, 2),
+                               "tokens_per_s": round(512 / dec["wall_s"], 1),
+                               "achieved_gbs": round(dec["achieved_gbs"], 1),
+                               "frac_hbm": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "long_context_config3": {"B": 1, "L": 32768, "H": 32, "chunk": 128,
+                                     "kernel_ms": round(lc["kernel_s"] * 1e3, 4),
+                                     "tokens_per_s": round(32768 / lc["wall_s"], 1),
+                                     "achieved_gbs": round(lc["achieved_gbs"], 1),
+                                     "frac_hbm": round(lc["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+        }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -104,23 +104,42 @@ __device__ __forceinline__ void store8(float* p, const float f[8]) {
 }
 
 // ---------------------------------------------------------------- wave ops
-// Inclusive prefix sum over the 64 lanes of a wavefront.
+// DPP lane move: lanes whose source is outside the row, or whose row/bank is
+// masked off, receive 0.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp0(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, BANK_MASK, true));
+}
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// Inclusive prefix sum over the 64 lanes of a wavefront: Hillis-Steele inside
+// each row of 16 lanes (row_shr 1, 2, 4, 8), then the row totals are carried
+// with row_bcast:15 (into rows 1 and 3) and row_bcast:31 (into rows 2 and 3).
 __device__ __forceinline__ float wave_incl_scan(float v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    float o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
+  v += dpp0<kDppRowShr1>(v);
+  v += dpp0<kDppRowShr2>(v);
+  v += dpp0<kDppRowShr4>(v);
+  v += dpp0<kDppRowShr8>(v);
+  v += dpp0<kDppRowBcast15, 0xa>(v);
+  v += dpp0<kDppRowBcast31, 0xc>(v);
   return v;
 }
 
 // Sum over aligned groups of G consecutive lanes (G a power of two <= 64);
-// every lane of the group receives the group sum.
+// every lane of the group receives the group sum.  Groups up to 16 lanes stay
+// inside a DPP row; wider groups use cross-row shuffles.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int d = G / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  if (G >= 2) v += dpp0<kDppQuadXor1>(v);
+  if (G >= 4) v += dpp0<kDppQuadXor2>(v);
+  if (G >= 8) v += dpp0<kDppHalfMirror>(v);
+  if (G >= 16) v += dpp0<kDppMirror>(v);
+  if (G >= 32) v += __shfl_xor(v, 16, 64);
+  if (G >= 64) v += __shfl_xor(v, 32, 64);
   return v;
 }
 

@@ -113,31 +113,36 @@ template <> struct MF<float> {
 };
 
 // Compile-time geometry of one instantiation.
-template <typename T, int CS_, int N_, int P_, int NW_>
+template <typename T, int CS_, int N_, int P_, int R_, int NW_>
 struct Geo {
   static constexpr bool BF = std::is_same<T, bf16>::value;
-  static constexpr int CS = CS_, N = N_, P = P_, NW = NW_, NT = 64 * NW_;
+  static constexpr int CS = CS_, N = N_, P = P_, R = R_, NW = NW_, NT = 64 * NW_;
+  static constexpr int NWY = NW / 2;                        // waves on output tiles; the rest on state tiles
   static constexpr int KSTEP = MF<T>::KSTEP;
   static constexpr int LB = CS / 32, PB = P / 32, NB = N / 32;
-  static constexpr int LDQ = N + MF<T>::PAD;      // sQ, sK rows
-  static constexpr int LDV = CS + MF<T>::PAD;     // sVt, sVwT rows
-  static constexpr int LDH = N + MF<T>::PAD;      // sHB rows
-  static constexpr int LDY = P + 4;               // sY rows (fp32)
-  static constexpr int RMAX = N / 2;
-  static constexpr int LDA = RMAX + 1;            // angle tables rows (fp32)
-  static constexpr int QV = (CS * N / 8 + NT - 1) / NT;     // 8-wide Q/K vectors per thread
-  static constexpr int VV = (CS * P / 8 + NT - 1) / NT;     // 8-wide V/Z vectors per thread
-  static constexpr int AV = (CS * RMAX + NT - 1) / NT;      // angle scalars per thread (max R)
-  static constexpr int HT = (NB * PB + NW - 1) / NW;        // state tiles per wave
+  static constexpr int LDQ = N + MF<T>::PAD;                // sQ, sK rows (elements)
+  static constexpr int LDV = CS + MF<T>::PAD;               // sVt, sVwT rows
+  static constexpr int LDH = N + MF<T>::PAD;                // sHB rows
+  static constexpr int LDY = P + 4;                         // sY rows (fp32)
+  static constexpr int LDC = R + 2;                         // cos/sin table rows (float2)
+  static constexpr int QG = N / 8;                          // 8-wide vectors per Q/K row
+  static constexpr int QROWS = NT / QG;                     // Q/K rows covered per pass
+  static constexpr int QV = (CS + QROWS - 1) / QROWS;       // Q/K vectors per thread
+  static constexpr int VV = (CS * (P / 8) + NT - 1) / NT;   // V/Z vectors per thread
+  static constexpr int CPW = R / NW;                        // rotation columns per wave
+  static constexpr int YT = (LB * PB + NWY - 1) / NWY;      // output tiles per output wave
+  static constexpr int ST = (NB * PB + (NW - NWY) - 1) / (NW - NWY);  // state tiles per state wave
   static constexpr bool VWT = BF;                           // precomputed w-scaled V^T
   static constexpr int TS = BF ? 2 : 4;
-  static constexpr int YB = CS * LDY * 4, AB = 2 * CS * LDA * 4;
+  static constexpr int YB = CS * LDY * 4, CB = CS * LDC * 8;
   static constexpr int COMMON = 2 * CS * LDQ * TS + (VWT ? 2 : 1) * P * LDV * TS +
-                                (YB > AB ? YB : AB) + 7 * CS * 4 + 64;
+                                (YB > CB ? YB : CB) + 7 * CS * 4 + 64;
   static constexpr int HBB = P * LDH * TS;
   // two state-operand buffers (no barrier between the output and state-update
   // MFMAs) when they fit in the 160 KiB of LDS, else one
   static constexpr int NHB = (COMMON + 2 * HBB <= 160 * 1024 - 512) ? 2 : 1;
+  static_assert(R == 0 || (R % NW == 0 && R % 4 == 0 && 2 * R <= N), "rotation width");
+  static_assert(NT % QG == 0, "Q/K column groups");
 };
 
 template <typename G>
@@ -149,8 +154,8 @@ struct __attribute__((aligned(16))) Smem {
   T vwt[G::VWT ? G::P * G::LDV : 1];
   T hb[G::NHB][G::P * G::LDH];
   union __attribute__((aligned(16))) U {
-    float y[G::CS * G::LDY];
-    struct A { float c[G::CS * G::LDA]; float s[G::CS * G::LDA]; } ang;
+    float y[G::CS * G::LDY];          // output tile before the gate (phase 3 -> 4)
+    float2 cs[G::CS * G::LDC];        // cos/sin of the rotation angles (phase 1 -> 2)
   } u;
   float ac2[G::CS];    // A_cum * log2(e)
   float expa[G::CS];   // e^{A_cum}
@@ -159,13 +164,17 @@ struct __attribute__((aligned(16))) Smem {
   float scl[G::CS];
   float dtv[G::CS];
   float qk[G::CS];
+  float qb[G::N];      // Q_bias, K_bias of this head
+  float kb[G::N];
   float dec;
 };
 
-template <typename T, int CS, int N, int P, int NW>
+template <int CPW> struct AngRegs { float v[CPW > 0 ? CPW : 1]; };
+
+template <typename T, int CS, int N, int P, int R, int NW>
 __global__ __launch_bounds__(64 * NW, 1)
 void scan_chunked_kernel(ScanArgs a) {
-  typedef Geo<T, CS, N, P, NW> G;
+  typedef Geo<T, CS, N, P, R, NW> G;
   typedef MF<T> M;
   static_assert(sizeof(Smem<G>) <= 160 * 1024, "LDS budget");
   __shared__ Smem<G> sm;
@@ -176,7 +185,7 @@ void scan_chunked_kernel(ScanArgs a) {
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh % a.H;
   const int hq = h / (a.H / a.Hqk);
-  const int L = a.L, H = a.H, HQ = a.Hqk, R = a.R;
+  const int L = a.L, H = a.H, HQ = a.Hqk;
   const int nc = (L + CS - 1) / CS;
   const T* gQ = reinterpret_cast<const T*>(a.q);
   const T* gK = reinterpret_cast<const T*>(a.k);
@@ -188,31 +197,30 @@ void scan_chunked_kernel(ScanArgs a) {
   const float* gtr = a.trap + (long)bh * L;
   const float Dh = a.D ? a.D[h] : 0.0f;
   const bool has_z = gZ != nullptr;
-  const int rshift = R > 0 ? __builtin_ctz(R) : 0;  // R is 0 or a power of two
 
-  // ---- per-thread constants: column group of the Q/K vectors, biases
-  constexpr int QG = N / 8;
-  const int qg = tid % QG;
-  float qb[8], kb[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    qb[i] = a.qbias[(long)h * N + 8 * qg + i];
-    kb[i] = a.kbias[(long)h * N + 8 * qg + i];
+  // ---- fixed per-thread mappings
+  const int qg = tid % G::QG;            // Q/K column group (8 columns)
+  const int qrow0 = tid / G::QG;         // Q/K row of pass 0
+  for (int n = tid; n < N; n += G::NT) {
+    sm.qb[n] = a.qbias[(long)h * N + n];
+    sm.kb[n] = a.kbias[(long)h * N + n];
   }
+  const long qk_base = ((long)b * L * HQ + hq) * N + 8 * qg;   // + t * HQ * N
+  const long v_base = ((long)b * L * H + h) * P;                // + t * H * P + 8 * g8
+  const long a_base = ((long)b * L * H + h) * R + wave * G::CPW;  // + t * H * R
 
   // ---- raw input registers (next chunk) and the current chunk's V/Z
   Vec8<T> rq[G::QV], rk[G::QV], rv[G::VV], rz[G::VV], cv[G::VV], cz[G::VV];
-  float ra[G::AV];
+  AngRegs<G::CPW> ra;
   float s_adt = 0.f, s_dt = 0.f, s_tr = 0.f, s_dtn = 0.f, s_trn = 0.f;
 
   auto load_chunk = [&](int c) {
     const int t0 = c * CS;
 #pragma unroll
     for (int i = 0; i < G::QV; ++i) {
-      const int v = tid + i * G::NT;
-      const int t = v / QG;
-      if (v < CS * QG && t0 + t < L) {
-        const long off = (((long)b * L + t0 + t) * HQ + hq) * N + 8 * qg;
+      const int t = qrow0 + i * G::QROWS;
+      if (t < CS && t0 + t < L) {
+        const long off = qk_base + (long)(t0 + t) * HQ * N;
         rq[i].load(gQ + off);
         rk[i].load(gK + off);
       } else {
@@ -223,9 +231,9 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
     for (int i = 0; i < G::VV; ++i) {
       const int v = tid + i * G::NT;
-      const int t = v / (P / 8), g8 = v % (P / 8);
-      if (v < CS * (P / 8) && t0 + t < L) {
-        const long off = (((long)b * L + t0 + t) * H + h) * P + 8 * g8;
+      const int t = v % CS, g8 = v / CS;
+      if (g8 < P / 8 && t0 + t < L) {
+        const long off = v_base + (long)(t0 + t) * H * P + 8 * g8;
         rv[i].load(gV + off);
         if (has_z) rz[i].load(gZ + off); else rz[i].zero();
       } else {
@@ -233,12 +241,21 @@ void scan_chunked_kernel(ScanArgs a) {
         rz[i].zero();
       }
     }
-    const int na = CS * R;
+    if (G::CPW > 0) {
+      const bool ok = lane < CS && t0 + lane < L;
+      const float* src = a.ang + a_base + (long)(t0 + lane) * H * R;
 #pragma unroll
-    for (int i = 0; i < G::AV; ++i) {
-      const int e = tid + i * G::NT;
-      const int t = e >> rshift, r = e & (R - 1);
-      ra[i] = (e < na && t0 + t < L) ? a.ang[(((long)b * L + t0 + t) * H + h) * R + r] : 0.0f;
+      for (int j = 0; j < G::CPW; j += (G::CPW >= 4 ? 4 : G::CPW)) {
+        if (G::CPW >= 4) {
+          const float4 x = ok ? *reinterpret_cast<const float4*>(src + j) : make_float4(0, 0, 0, 0);
+          ra.v[j] = x.x; ra.v[j + 1] = x.y; ra.v[j + 2] = x.z; ra.v[j + 3] = x.w;
+        } else if (G::CPW == 2) {
+          const float2 x = ok ? *reinterpret_cast<const float2*>(src) : make_float2(0, 0);
+          ra.v[0] = x.x; ra.v[1] = x.y;
+        } else {
+          ra.v[0] = ok ? src[0] : 0.0f;
+        }
+      }
     }
     if (wave == 0) {
       const int t = t0 + lane;
@@ -256,11 +273,11 @@ void scan_chunked_kernel(ScanArgs a) {
   auto scalar_stage = [&]() {
     const float sig = sigmoid_fast(s_tr);
     const float gam = s_dt * sig;
-    const float u = s_dt * (1.0f - sig);            // dt (1 - sigmoid) of this token
-    float un = __shfl_down(u, 1, 64);               // ... of the next token
+    const float u = s_dt * (1.0f - sig);                            // dt (1 - sigmoid), this token
+    float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // wave_shl:1 -> next token
     if (lane == CS - 1) un = s_dtn * (1.0f - sigmoid_fast(s_trn));
     const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
-    const float aend = __shfl(acum, CS - 1, 64);
+    const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
     if (lane < CS) {
       sm.ac2[lane] = acum * kLog2e;
       sm.expa[lane] = exp2_fast(acum * kLog2e);
@@ -272,36 +289,34 @@ void scan_chunked_kernel(ScanArgs a) {
     if (lane == 0) sm.dec = exp2_fast(aend * kLog2e);
   };
 
-  // ---- state accumulators: tiles z = wave + NW*m of h^T (rows n, cols p)
-  f32x16 hacc[G::HT];
-  float carry[(G::RMAX + NW - 1) / NW];
+  // ---- state accumulators (state waves): tiles z = (wave - NWY) * ST + m of h^T
+  const bool ywave = wave < G::NWY;
+  const int zw = (wave - G::NWY) * G::ST;
+  f32x16 hacc[G::ST];
+  float carry[G::CPW > 0 ? G::CPW : 1];
 #pragma unroll
-  for (int m = 0; m < (G::RMAX + NW - 1) / NW; ++m) {
-    const int r = wave + NW * m;
-    carry[m] = (a.init_theta && r < R) ? a.init_theta[(long)bh * R + r] : 0.0f;
-  }
+  for (int j = 0; j < G::CPW; ++j)
+    carry[j] = a.init_theta ? a.init_theta[(long)bh * R + wave * G::CPW + j] : 0.0f;
   {
     // effective entering state: h0 + (1 - sigmoid(trap_0)) dt_0 (v0 (x) k0)
-    float cinit = 0.0f;
-    if (a.init_h && L > 0) cinit = (1.0f - sigmoid_fast(gtr[0])) * gdt[0];
+    const float cinit = (a.init_h && L > 0) ? (1.0f - sigmoid_fast(gtr[0])) * gdt[0] : 0.0f;
 #pragma unroll
-    for (int m = 0; m < G::HT; ++m) {
-      const int z = wave + NW * m;
+    for (int m = 0; m < G::ST; ++m) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) hacc[m][r] = 0.0f;
-      if (a.init_h && z < G::NB * G::PB) {
+      const int z = zw + m;
+      if (!ywave && z < G::NB * G::PB) {
         const int nb = z / G::PB, pb = z % G::PB;
         const int p = 32 * pb + (lane & 31);
-        const float v0 = a.init_v[(long)bh * P + p];
+        if (a.init_h) {
+          const float v0 = a.init_v[(long)bh * P + p];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int n = 32 * nb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          hacc[m][r] = a.init_h[((long)bh * P + p) * N + n] + cinit * v0 * a.init_k[(long)bh * N + n];
+          for (int r = 0; r < 16; ++r) {
+            const int n = 32 * nb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            hacc[m][r] = a.init_h[((long)bh * P + p) * N + n] + cinit * v0 * a.init_k[(long)bh * N + n];
+          }
         }
-      }
-      if (z < G::NB * G::PB) {
-        const int nb = z / G::PB, pb = z % G::PB;
-        M::store_ht(sm.hb[0], G::LDH, 32 * pb + (lane & 31), 32 * nb, hacc[m], lane);
+        M::store_ht(sm.hb[0], G::LDH, p, 32 * nb, hacc[m], lane);
       }
     }
   }
@@ -314,44 +329,44 @@ void scan_chunked_kernel(ScanArgs a) {
     const int t0 = c * CS;
     const int hcur = c % G::NHB, hnext = (c + 1) % G::NHB;
 
-    // ---- phase 1a: per-element rotation increments tanh(theta) pi dt -> angle table
-    {
-      const int na = CS * R;
+    // ---- phase 1: rotation angles. lane = token, CPW columns per wave:
+    // increments tanh(theta) pi dt, chunk prefix (DPP scan), carry, wrap, cos/sin
+    if (G::CPW > 0) {
+      const float dtl = lane < CS ? sm.dtv[lane] : 0.0f;
+      float2 csv[G::CPW > 0 ? G::CPW : 1];
 #pragma unroll
-      for (int i = 0; i < G::AV; ++i) {
-        const int e = tid + i * G::NT;
-        if (e < na) {
-          const int t = e >> rshift, r = e & (R - 1);
-          sm.u.ang.c[t * G::LDA + r] = tanh_fast(ra[i]) * kPi * sm.dtv[t];
+      for (int j = 0; j < G::CPW; ++j) {
+        const float d = tanh_fast(ra.v[j]) * kPi * dtl;
+        const float th = wrap_2pi(carry[j] + wave_incl_scan(d));
+        carry[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
+        sincos_wrapped(th, &csv[j].x, &csv[j].y);
+      }
+      if (lane < CS) {
+        float2* dst = &sm.u.cs[lane * G::LDC + wave * G::CPW];
+#pragma unroll
+        for (int j = 0; j < G::CPW; j += 2) {
+          if (G::CPW >= 2) {
+            *reinterpret_cast<float4*>(dst + j) = make_float4(csv[j].x, csv[j].y, csv[j + 1].x, csv[j + 1].y);
+          } else {
+            dst[0] = csv[0];
+          }
         }
       }
     }
     __syncthreads();
-    // ---- phase 1b: prefix over the chunk per rotation column, carry, wrap, cos/sin
-#pragma unroll
-    for (int m = 0; m < (G::RMAX + NW - 1) / NW; ++m) {
-      const int r = wave + NW * m;
-      if (r < R) {
-        const float d = lane < CS ? sm.u.ang.c[lane * G::LDA + r] : 0.0f;
-        const float th = wrap_2pi(carry[m] + wave_incl_scan(d));
-        carry[m] = __shfl(th, CS - 1, 64);
-        if (lane < CS) {
-          float cs, sn;
-          sincos_wrapped(th, &cs, &sn);
-          sm.u.ang.c[lane * G::LDA + r] = cs;
-          sm.u.ang.s[lane * G::LDA + r] = sn;
-        }
-      }
-    }
-    __syncthreads();
-    // ---- phase 1c: biases, QK skip, rope, key scale -> sQ, sK; V^T, (w V)^T
+
+    // ---- phase 2: biases, QK skip, rope, key scale -> sQ, sK; V^T, (w V)^T
 #pragma unroll
     for (int i = 0; i < G::QV; ++i) {
-      const int v = tid + i * G::NT;
-      const int t = v / QG;
+      const int t = qrow0 + i * G::QROWS;
       float qf[8], kf[8];
       rq[i].to_f(qf);
       rk[i].to_f(kf);
+      const float4* qbp = reinterpret_cast<const float4*>(&sm.qb[8 * qg]);
+      const float4* kbp = reinterpret_cast<const float4*>(&sm.kb[8 * qg]);
+      const float4 qb0 = qbp[0], qb1 = qbp[1], kb0 = kbp[0], kb1 = kbp[1];
+      const float qb[8] = {qb0.x, qb0.y, qb0.z, qb0.w, qb1.x, qb1.y, qb1.z, qb1.w};
+      const float kb[8] = {kb0.x, kb0.y, kb0.z, kb0.w, kb1.x, kb1.y, kb1.z, kb1.w};
       float dot = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -359,21 +374,23 @@ void scan_chunked_kernel(ScanArgs a) {
         kf[e] += kb[e];
         dot += qf[e] * kf[e];
       }
-      dot = group_sum<QG>(dot);
-      if (v < CS * QG) {
+      dot = group_sum<G::QG>(dot);
+      if (t < CS) {
         const bool real = t0 + t < L;
         if (qg == 0) sm.qk[t] = real ? dot * sm.gam[t] : 0.0f;
+        if (4 * qg < R) {
+          const float4* cp = reinterpret_cast<const float4*>(&sm.u.cs[t * G::LDC + 4 * qg]);
+          const float4 c01 = cp[0], c23 = cp[1];
+          const float cs4[4] = {c01.x, c01.z, c23.x, c23.z};
+          const float sn4[4] = {c01.y, c01.w, c23.y, c23.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int j = 4 * qg + q;
-          if (j < R) {
-            const float cs = sm.u.ang.c[t * G::LDA + j], sn = sm.u.ang.s[t * G::LDA + j];
+          for (int q = 0; q < 4; ++q) {
             const float q0 = qf[2 * q], q1 = qf[2 * q + 1];
-            qf[2 * q] = q0 * cs - q1 * sn;
-            qf[2 * q + 1] = q0 * sn + q1 * cs;
+            qf[2 * q] = q0 * cs4[q] - q1 * sn4[q];
+            qf[2 * q + 1] = q0 * sn4[q] + q1 * cs4[q];
             const float k0 = kf[2 * q], k1 = kf[2 * q + 1];
-            kf[2 * q] = k0 * cs - k1 * sn;
-            kf[2 * q + 1] = k0 * sn + k1 * cs;
+            kf[2 * q] = k0 * cs4[q] - k1 * sn4[q];
+            kf[2 * q + 1] = k0 * sn4[q] + k1 * cs4[q];
           }
         }
         if (a.fin_k && t0 + t == L - 1) {
@@ -393,10 +410,10 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
     for (int i = 0; i < G::VV; ++i) {
       const int v = tid + i * G::NT;
+      const int t = v % CS, g8 = v / CS;
       cv[i] = rv[i];
       cz[i] = rz[i];
-      if (v < CS * (P / 8)) {
-        const int t = v / (P / 8), g8 = v % (P / 8);
+      if (g8 < P / 8) {
         float vf[8];
         rv[i].to_f(vf);
         const float wt = sm.w[t];
@@ -412,61 +429,75 @@ void scan_chunked_kernel(ScanArgs a) {
     // ---- next chunk's inputs go in flight under the matrix work
     if (c + 1 < nc) load_chunk(c + 1);
 
-    // ---- phase 3 + 6: Y = mask(K_s Q_r^T)^T V + e^{A_cum} Q_r h^T  -> sY
-    for (int y = wave; y < G::LB * G::PB; y += NW) {
-      const int lb = y / G::PB, pb = y % G::PB;
-      f32x16 yd, yo;
+    if (ywave) {
+      // ---- phases 3 + 6: Y = mask(K_s Q_r^T)^T V + e^{A_cum} Q_r h^T -> sY
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { yd[r] = 0.0f; yo[r] = 0.0f; }
-      const int l = 32 * lb + (lane & 31);
-      const float al = sm.ac2[l];
-      for (int sb = 0; sb <= lb; ++sb) {
-        f32x16 st;
+      for (int m = 0; m < G::YT; ++m) {
+        const int y = wave + G::NWY * m;
+        if (y < G::LB * G::PB) {
+          const int lb = y / G::PB, pb = y % G::PB;
+          f32x16 st[G::LB], yd, yo;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[r] = 0.0f;
+          for (int r = 0; r < 16; ++r) {
+            yd[r] = 0.0f;
+            yo[r] = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < N / G::KSTEP; ++kk) {
-          st = M::mma(M::ld(sm.k, G::LDQ, 32 * sb, kk * G::KSTEP, lane),
-                      M::ld(sm.q, G::LDQ, 32 * lb, kk * G::KSTEP, lane), st);
+            for (int sb = 0; sb < G::LB; ++sb) st[sb][r] = 0.0f;
+          }
+#pragma unroll 2
+          for (int kk = 0; kk < N / G::KSTEP; ++kk) {
+            const typename M::frag qf = M::ld(sm.q, G::LDQ, 32 * lb, kk * G::KSTEP, lane);
+#pragma unroll
+            for (int sb = 0; sb < G::LB; ++sb)
+              st[sb] = M::mma(M::ld(sm.k, G::LDQ, 32 * sb, kk * G::KSTEP, lane), qf, st[sb]);
+            yo = M::mma(qf, M::ld(sm.hb[hcur], G::LDH, 32 * pb, kk * G::KSTEP, lane), yo);
+          }
+          const int l = 32 * lb + (lane & 31);
+          const float al = sm.ac2[l];
+#pragma unroll
+          for (int sb = 0; sb < G::LB; ++sb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int s = 32 * sb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+              st[sb][r] = s < l ? st[sb][r] * exp2_fast(al - sm.ac2[s]) : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 32 / G::KSTEP; ++j)
+              yd = M::mma(M::from_acc(st[sb], j), M::vperm(sm.vt, G::LDV, 32 * pb, 32 * sb, j, lane), yd);
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int lr = 32 * lb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            sm.u.y[lr * G::LDY + 32 * pb + (lane & 31)] = yd[r] + sm.expa[lr] * yo[r];
+          }
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int s = 32 * sb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          st[r] = s < l ? st[r] * exp2_fast(al - sm.ac2[s]) : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < 32 / G::KSTEP; ++j) {
-          yd = M::mma(M::from_acc(st, j), M::vperm(sm.vt, G::LDV, 32 * pb, 32 * sb, j, lane), yd);
-        }
-      }
-#pragma unroll
-      for (int kk = 0; kk < N / G::KSTEP; ++kk) {
-        yo = M::mma(M::ld(sm.q, G::LDQ, 32 * lb, kk * G::KSTEP, lane),
-                    M::ld(sm.hb[hcur], G::LDH, 32 * pb, kk * G::KSTEP, lane), yo);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lr = 32 * lb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        sm.u.y[lr * G::LDY + 32 * pb + (lane & 31)] = yd[r] + sm.expa[lr] * yo[r];
       }
     }
     if (G::NHB == 1) __syncthreads();  // single state buffer: all reads of hb done
-
-    // ---- phase 4-5: h <- e^{A_end} h + (K_s)^T (w V)
-    {
+    if (!ywave) {
+      // ---- phases 4-5: h <- e^{A_end} h + (K_s)^T (w V), state tiles interleaved
       const float dec = sm.dec;
 #pragma unroll
-      for (int m = 0; m < G::HT; ++m) {
-        const int z = wave + NW * m;
-        if (z < G::NB * G::PB) {
-          const int nb = z / G::PB, pb = z % G::PB;
+      for (int m = 0; m < G::ST; ++m)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) hacc[m][r] *= dec;
+        for (int r = 0; r < 16; ++r) hacc[m][r] *= dec;
 #pragma unroll
-          for (int j = 0; j < CS / G::KSTEP; ++j) {
+      for (int j = 0; j < CS / G::KSTEP; ++j) {
+#pragma unroll
+        for (int m = 0; m < G::ST; ++m) {
+          const int z = zw + m;
+          if (z < G::NB * G::PB) {
+            const int nb = z / G::PB, pb = z % G::PB;
             hacc[m] = M::mma(M::kt(sm.k, G::LDQ, 32 * nb, j * G::KSTEP, lane),
                              M::vw(sm.vwt, sm.vt, sm.w, G::LDV, 32 * pb, j * G::KSTEP, lane), hacc[m]);
           }
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < G::ST; ++m) {
+        const int z = zw + m;
+        if (z < G::NB * G::PB) {
+          const int nb = z / G::PB, pb = z % G::PB;
           M::store_ht(sm.hb[hnext], G::LDH, 32 * pb + (lane & 31), 32 * nb, hacc[m], lane);
         }
       }
@@ -477,8 +508,8 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
     for (int i = 0; i < G::VV; ++i) {
       const int v = tid + i * G::NT;
-      const int t = v / (P / 8), g8 = v % (P / 8);
-      if (v < CS * (P / 8) && t0 + t < L) {
+      const int t = v % CS, g8 = v / CS;
+      if (g8 < P / 8 && t0 + t < L) {
         float vf[8], zf[8], yv[8];
         cv[i].to_f(vf);
         cz[i].to_f(zf);
@@ -493,8 +524,7 @@ void scan_chunked_kernel(ScanArgs a) {
           if (has_z) o *= silu_fast(zf[q]);
           yv[q] = o;
         }
-        const long off = (((long)b * L + t0 + t) * H + h) * P + 8 * g8;
-        store8(gO + off, yv);
+        store8(gO + v_base + (long)(t0 + t) * H * P + 8 * g8, yv);
         if (a.fin_v && t0 + t == L - 1) {
 #pragma unroll
           for (int q = 0; q < 8; ++q) a.fin_v[(long)bh * P + 8 * g8 + q] = vf[q];
@@ -506,56 +536,56 @@ void scan_chunked_kernel(ScanArgs a) {
   }
 
   if (a.fin_h) {
+    if (!ywave) {
 #pragma unroll
-    for (int m = 0; m < G::HT; ++m) {
-      const int z = wave + NW * m;
-      if (z < G::NB * G::PB) {
-        const int nb = z / G::PB, pb = z % G::PB;
-        const int p = 32 * pb + (lane & 31);
+      for (int m = 0; m < G::ST; ++m) {
+        const int z = zw + m;
+        if (z < G::NB * G::PB) {
+          const int nb = z / G::PB, pb = z % G::PB;
+          const int p = 32 * pb + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int n = 32 * nb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          a.fin_h[((long)bh * P + p) * N + n] = hacc[m][r];
+          for (int r = 0; r < 16; ++r) {
+            const int n = 32 * nb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            a.fin_h[((long)bh * P + p) * N + n] = hacc[m][r];
+          }
         }
       }
     }
+    if (lane == 0) {
 #pragma unroll
-    for (int m = 0; m < (G::RMAX + NW - 1) / NW; ++m) {
-      const int r = wave + NW * m;
-      if (r < R && lane == 0) a.fin_theta[(long)bh * R + r] = carry[m];
+      for (int j = 0; j < G::CPW; ++j) a.fin_theta[(long)bh * R + wave * G::CPW + j] = carry[j];
     }
   }
 }
 
 // ------------------------------------------------------------------ dispatch
-template <typename T, int CS, int N, int P>
-static hipError_t launch_one(const ScanArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((scan_chunked_kernel<T, CS, N, P, 4>), dim3(a.B * a.H), dim3(256), 0, st, a);
-  return hipGetLastError();
-}
+// (dtype, chunk, d_state, headdim, rotation width) instantiations; R is the
+// model's rope_fraction 0.5 (R = N/4) or 1.0 (R = N/2) width, or 0.
+#define M3_CHUNK_SHAPES(X)                                                                         \
+  X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0)                        \
+  X(bf16, 64, 128, 32, 32) X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 64, 32) \
+  X(bf16, 64, 64, 32, 16) X(bf16, 64, 32, 32, 8) X(bf16, 64, 32, 64, 8)                            \
+  X(bf16, 32, 128, 64, 32) X(bf16, 32, 64, 64, 16) X(bf16, 32, 64, 32, 16) X(bf16, 32, 128, 32, 32) \
+  X(float, 64, 64, 64, 16) X(float, 64, 64, 64, 32) X(float, 64, 64, 32, 16) X(float, 32, 64, 64, 16) \
+  X(float, 32, 64, 32, 16) X(float, 64, 32, 32, 8) X(float, 64, 32, 64, 8)
 
-#define M3_CHUNK_SHAPES(X)                                                        \
-  X(bf16, 64, 128, 64) X(bf16, 64, 64, 64) X(bf16, 64, 128, 128) X(bf16, 64, 64, 32)  \
-  X(bf16, 64, 128, 32) X(bf16, 32, 128, 64) X(bf16, 32, 64, 64) X(bf16, 32, 64, 32)   \
-  X(bf16, 32, 128, 32) X(bf16, 64, 32, 32) X(bf16, 64, 32, 64) X(bf16, 32, 32, 32)     \
-  X(float, 64, 64, 64) X(float, 64, 64, 32) X(float, 32, 64, 64) X(float, 32, 64, 32)  \
-  X(float, 64, 32, 32) X(float, 64, 32, 64) X(float, 32, 32, 32)
-
-static bool r_ok(int N, int R) { return R == 0 || (R > 0 && 2 * R <= N && (R & (R - 1)) == 0); }
+constexpr int kChunkWaves = 8;
 
 bool scan_chunked_supported(bool bf16_io, int CS, int N, int P, int R) {
-  if (!r_ok(N, R)) return false;
-#define X(T, cs, n, p) \
-  if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && N == n && P == p) return true;
+#define X(T, cs, n, p, r) \
+  if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && N == n && P == p && R == r) return true;
   M3_CHUNK_SHAPES(X)
 #undef X
   return false;
 }
 
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
-#define X(T, cs, n, p)                                                                  \
-  if ((std::is_same<T, bf16>::value == bf16_io) && a.CS == cs && a.N == n && a.P == p) \
-    return launch_one<T, cs, n, p>(a, st);
+#define X(T, cs, n, p, r)                                                                            \
+  if ((std::is_same<T, bf16>::value == bf16_io) && a.CS == cs && a.N == n && a.P == p && a.R == r) { \
+    hipLaunchKernelGGL((scan_chunked_kernel<T, cs, n, p, r, kChunkWaves>), dim3(a.B * a.H),          \
+                       dim3(64 * kChunkWaves), 0, st, a);                                             \
+    return hipGetLastError();                                                                         \
+  }
   M3_CHUNK_SHAPES(X)
 #undef X
   return hipErrorInvalidValue;
