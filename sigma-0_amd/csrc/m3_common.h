@@ -41,8 +41,10 @@ __device__ __forceinline__ float sigmoid_fast(float x) { return rcp_fast(1.0f + 
 __device__ __forceinline__ float silu_fast(float x) { return x * rcp_fast(1.0f + exp_fast(-x)); }
 
 // theta - 2pi*floor(theta/2pi): the range reduction the reference applies to
-// the cumulative rotation angle (mamba3_jax.py:143, mamba3.py:509).
-__device__ __forceinline__ float wrap_2pi(float th) { return th - kTwoPi * floorf(th / kTwoPi); }
+// the cumulative rotation angle (mamba3_jax.py:143, mamba3.py:509); the
+// quotient is formed with the reciprocal (differs only within an ulp of a
+// multiple of 2pi, where both results are equivalent angles).
+__device__ __forceinline__ float wrap_2pi(float th) { return th - kTwoPi * floorf(th * kInvTwoPi); }
 
 // cos/sin of a wrapped angle in [0, 2pi) through the revolution-based units.
 __device__ __forceinline__ void sincos_wrapped(float th, float* c, float* s) {

@@ -112,6 +112,58 @@ template <> struct MF<float> {
   }
 };
 
+// 16x16 tiles for the output path: v_mfma_f32_16x16x32_bf16 (KPL = 8) and
+// v_mfma_f32_16x16x4_f32 (KPL = 1).  A: lane i holds row i%16, k = (i/16)*KPL + [0,KPL);
+// B: col i%16, same k; C: lane i, reg r holds col i%16, row 4*(i/16) + r.
+template <typename T> struct MF16;
+template <> struct MF16<bf16> {
+  static constexpr int KSTEP = 32;
+  typedef bf16x8 frag;
+  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag ld(const bf16* buf, int ldm, int row0, int k0, int lane) {
+    return *reinterpret_cast<const bf16x8*>(buf + (row0 + (lane & 15)) * ldm + k0 + (lane >> 4) * 8);
+  }
+  // steps over a pair of 16-row S^T tiles (32 values of s): slots 0..3 are the
+  // first tile's regs (s = 4(lane/16) + 0..3), slots 4..7 the second's (s + 16)
+  static constexpr int STEPS = 1;
+  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int) {
+    frag f;
+    f[0] = (bf16)c0[0]; f[1] = (bf16)c0[1]; f[2] = (bf16)c0[2]; f[3] = (bf16)c0[3];
+    f[4] = (bf16)c1[0]; f[5] = (bf16)c1[1]; f[6] = (bf16)c1[2]; f[7] = (bf16)c1[3];
+    return f;
+  }
+  __device__ __forceinline__ static frag vperm(const bf16* vt, int ldv, int p0, int s0, int, int lane) {
+    const bf16* r = vt + (p0 + (lane & 15)) * ldv + s0 + 4 * (lane >> 4);
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(r);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(r + 16);
+    frag f;
+    f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+    f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+    return f;
+  }
+};
+template <> struct MF16<float> {
+  static constexpr int KSTEP = 4;
+  typedef float frag;
+  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag ld(const float* buf, int ldm, int row0, int k0, int lane) {
+    return buf[(row0 + (lane & 15)) * ldm + k0 + (lane >> 4)];
+  }
+  // step j (0..7) over a pair of tiles: j < 4 uses the first tile's reg j
+  // (s = 4(lane/16) + j), j >= 4 the second's reg j-4 (s + 16)
+  static constexpr int STEPS = 8;
+  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int j) {
+    return j < 4 ? c0[j] : c1[j - 4];
+  }
+  __device__ __forceinline__ static frag vperm(const float* vt, int ldv, int p0, int s0, int j, int lane) {
+    return vt[(p0 + (lane & 15)) * ldv + s0 + 4 * (lane >> 4) + (j & 3) + (j >= 4 ? 16 : 0)];
+  }
+};
+
 // Compile-time geometry of one instantiation.
 template <typename T, int CS_, int N_, int P_, int R_, int NW_>
 struct Geo {
@@ -130,7 +182,7 @@ struct Geo {
   static constexpr int QV = (CS + QROWS - 1) / QROWS;       // Q/K vectors per thread
   static constexpr int VV = (CS * (P / 8) + NT - 1) / NT;   // V/Z vectors per thread
   static constexpr int CPW = R / NW;                        // rotation columns per wave
-  static constexpr int YT = (LB * PB + NWY - 1) / NWY;      // output tiles per output wave
+  static constexpr int LB16 = CS / 16, PT = P / 16;          // 16-row query blocks, 16-col value tiles
   static constexpr int ST = (NB * PB + (NW - NWY) - 1) / (NW - NWY);  // state tiles per state wave
   static constexpr bool VWT = BF;                           // precomputed w-scaled V^T
   static constexpr int TS = BF ? 2 : 4;
@@ -157,9 +209,10 @@ struct __attribute__((aligned(16))) Smem {
     float y[G::CS * G::LDY];          // output tile before the gate (phase 3 -> 4)
     float2 cs[G::CS * G::LDC];        // cos/sin of the rotation angles (phase 1 -> 2)
   } u;
-  float ac2[G::CS];    // A_cum * log2(e)
+  alignas(16) float ac2[G::CS];    // A_cum * log2(e)
   float expa[G::CS];   // e^{A_cum}
   float w[G::CS];      // e^{A_end - A_cum}
+  alignas(16) float g16[G::CS];  // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
   float gam[G::CS];
   float scl[G::CS];
   float dtv[G::CS];
@@ -278,10 +331,12 @@ void scan_chunked_kernel(ScanArgs a) {
     if (lane == CS - 1) un = s_dtn * (1.0f - sigmoid_fast(s_trn));
     const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
     const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
+    const float ablk = __shfl(acum, lane | 15, 64);
     if (lane < CS) {
       sm.ac2[lane] = acum * kLog2e;
       sm.expa[lane] = exp2_fast(acum * kLog2e);
       sm.w[lane] = exp2_fast((aend - acum) * kLog2e);
+      sm.g16[lane] = exp2_fast((ablk - acum) * kLog2e);
       sm.gam[lane] = gam;
       sm.scl[lane] = gam + un;
       sm.dtv[lane] = s_dt;
@@ -429,48 +484,75 @@ void scan_chunked_kernel(ScanArgs a) {
     // ---- next chunk's inputs go in flight under the matrix work
     if (c + 1 < nc) load_chunk(c + 1);
 
-    if (ywave) {
-      // ---- phases 3 + 6: Y = mask(K_s Q_r^T)^T V + e^{A_cum} Q_r h^T -> sY
+    if (wave < G::LB16 && wave < G::NWY) {
+      // ---- phases 3 + 6 for query rows l in [16 lb, 16 lb + 16), all value columns:
+      //   Y = mask(K_s Q_r^T)^T V + e^{A_cum} Q_r h^T -> sY
+      typedef MF16<T> W;
+      const int lb = wave;
+      const int l = 16 * lb + (lane & 15);
+      const float al = sm.ac2[l];
+      f32x4 yd[G::PT], yo[G::PT];
 #pragma unroll
-      for (int m = 0; m < G::YT; ++m) {
-        const int y = wave + G::NWY * m;
-        if (y < G::LB * G::PB) {
-          const int lb = y / G::PB, pb = y % G::PB;
-          f32x16 st[G::LB], yd, yo;
+      for (int pt = 0; pt < G::PT; ++pt)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            yd[r] = 0.0f;
-            yo[r] = 0.0f;
+        for (int r = 0; r < 4; ++r) { yd[pt][r] = 0.0f; yo[pt][r] = 0.0f; }
+      // Y_off: Q_r (16 x N) . h^T (N x P)
 #pragma unroll
-            for (int sb = 0; sb < G::LB; ++sb) st[sb][r] = 0.0f;
-          }
-#pragma unroll 2
-          for (int kk = 0; kk < N / G::KSTEP; ++kk) {
-            const typename M::frag qf = M::ld(sm.q, G::LDQ, 32 * lb, kk * G::KSTEP, lane);
+      for (int kk = 0; kk < N / W::KSTEP; ++kk) {
+        const typename W::frag qf = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, lane);
 #pragma unroll
-            for (int sb = 0; sb < G::LB; ++sb)
-              st[sb] = M::mma(M::ld(sm.k, G::LDQ, 32 * sb, kk * G::KSTEP, lane), qf, st[sb]);
-            yo = M::mma(qf, M::ld(sm.hb[hcur], G::LDH, 32 * pb, kk * G::KSTEP, lane), yo);
-          }
-          const int l = 32 * lb + (lane & 31);
-          const float al = sm.ac2[l];
+        for (int pt = 0; pt < G::PT; ++pt)
+          yo[pt] = W::mma(qf, W::ld(sm.hb[hcur], G::LDH, 16 * pt, kk * W::KSTEP, lane), yo[pt]);
+      }
+      // Y_diag over key blocks sb <= lb, two 16-row blocks per step
 #pragma unroll
-          for (int sb = 0; sb < G::LB; ++sb) {
+      for (int sp = 0; sp < G::LB16; sp += 2) {
+        if (sp <= lb) {
+          f32x4 st[2];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int s = 32 * sb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-              st[sb][r] = s < l ? st[sb][r] * exp2_fast(al - sm.ac2[s]) : 0.0f;
+          for (int u = 0; u < 2; ++u) {
+            const int sb = sp + u;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) st[u][r] = 0.0f;
+            if (sb <= lb) {
+#pragma unroll
+              for (int kk = 0; kk < N / W::KSTEP; ++kk)
+                st[u] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, lane),
+                               W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, lane), st[u]);
+              const int s0 = 16 * sb + 4 * (lane >> 4);
+              if (sb < lb) {
+                // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
+                const float f = exp2_fast(fminf(al - sm.ac2[16 * sb + 15], 0.0f));
+                const float4 g = *reinterpret_cast<const float4*>(&sm.g16[s0]);
+                st[u][0] *= f * g.x; st[u][1] *= f * g.y; st[u][2] *= f * g.z; st[u][3] *= f * g.w;
+              } else {
+                // diagonal block: causal mask and per-element decay
+                const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[s0]);
+                const float asv[4] = {as.x, as.y, as.z, as.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const float v = st[u][r] * exp2_fast(fminf(al - asv[r], 0.0f));
+                  st[u][r] = (s0 + r < l) ? v : 0.0f;
+                }
+              }
             }
-#pragma unroll
-            for (int j = 0; j < 32 / G::KSTEP; ++j)
-              yd = M::mma(M::from_acc(st[sb], j), M::vperm(sm.vt, G::LDV, 32 * pb, 32 * sb, j, lane), yd);
           }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int lr = 32 * lb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            sm.u.y[lr * G::LDY + 32 * pb + (lane & 31)] = yd[r] + sm.expa[lr] * yo[r];
+          for (int j = 0; j < W::STEPS; ++j) {
+            const typename W::frag mf = W::from_acc(st[0], st[1], j);
+#pragma unroll
+            for (int pt = 0; pt < G::PT; ++pt)
+              yd[pt] = W::mma(mf, W::vperm(sm.vt, G::LDV, 16 * pt, 16 * sp, j, lane), yd[pt]);
           }
         }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int lr = 16 * lb + 4 * (lane >> 4) + r;
+        const float ea = sm.expa[lr];
+#pragma unroll
+        for (int pt = 0; pt < G::PT; ++pt)
+          sm.u.y[lr * G::LDY + 16 * pt + (lane & 15)] = yd[pt][r] + ea * yo[pt][r];
       }
     }
     if (G::NHB == 1) __syncthreads();  // single state buffer: all reads of hb done
