@@ -1,0 +1,180 @@
+"""The C-ABI library and the host layer, without a GPU.
+
+The library must load, export every function include/mamba3_scan.h declares,
+select kernels as documented, and reject invalid calls with the documented
+error codes before any device work.  The torch-facing wrappers must refuse
+CPU tensors (there is no CPU fallback) and validate shapes with the
+reference's messages.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mamba3_scan.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mamba3_rocm import _lib
+    return _lib.load()
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(m3_\w+)\s*\(", text, re.M)))
+
+
+def _header_define(name):
+    m = re.search(rf"#define\s+{name}\s+(\d+)", open(HEADER).read())
+    return int(m.group(1))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = _header_functions()
+    assert names == sorted(["m3_abi_version", "m3_last_error", "m3_chunk_scan_impl",
+                            "m3_chunk_scan_fwd", "m3_chunk_scan_fwd_carry", "m3_decode_step"])
+    for n in names:
+        assert hasattr(lib, n), n
+    from mamba3_rocm import _lib
+    assert sorted(_lib.EXPORTS) == names
+
+
+def test_abi_version_and_constants(lib):
+    from mamba3_rocm import _lib
+    assert lib.m3_abi_version() == 100
+    assert _lib.DTYPE_F32 == _header_define("M3_DTYPE_F32")
+    assert _lib.DTYPE_BF16 == _header_define("M3_DTYPE_BF16")
+    assert _lib.IMPL_CHUNKED_MFMA == _header_define("M3_IMPL_CHUNKED_MFMA")
+    assert _lib.IMPL_GENERIC == _header_define("M3_IMPL_GENERIC")
+
+
+def test_kernel_selection(lib):
+    f = lib.m3_chunk_scan_impl
+    CH, GEN, NONE = 1, 2, 0
+    assert f(1, 128, 64, 32, 64) == CH          # headline bf16 shape
+    assert f(1, 128, 64, 64, 64) == CH          # rope_fraction 1.0
+    assert f(1, 128, 64, 32, 32) == CH          # chunk 32
+    assert f(0, 64, 64, 16, 64) == CH           # fp32, config 1
+    assert f(0, 128, 64, 32, 64) == GEN         # fp32 with d_state 128
+    assert f(1, 128, 64, 32, 128) == GEN        # chunk 128 (no MFMA instantiation yet)
+    assert f(1, 64, 16, 16, 16) == GEN          # headdim 16
+    assert f(0, 4, 4, 1, 4) == GEN              # tiny model shapes
+    assert f(1, 1024, 64, 0, 64) == NONE        # state too large for either kernel
+    assert f(7, 128, 64, 32, 64) == NONE        # unknown dtype
+
+
+def _scan_call(lib, **kw):
+    a = dict(Q=None, K=None, V=None, ADT=None, DT=None, Trap=None, Qb=None, Kb=None, Ang=None,
+             D=None, Z=None, Out=None, B=1, L=8, H=2, Hqk=2, N=64, P=64, R=16, CS=64, io=1)
+    a.update(kw)
+    return lib.m3_chunk_scan_fwd(a["Q"], a["K"], a["V"], a["ADT"], a["DT"], a["Trap"], a["Qb"],
+                                 a["Kb"], a["Ang"], a["D"], a["Z"], a["Out"], a["B"], a["L"], a["H"],
+                                 a["Hqk"], a["N"], a["P"], a["R"], a["CS"], a["io"], None)
+
+
+def test_validation_errors_before_any_launch(lib):
+    E_ARG, E_UNSUP = _header_define("M3_E_ARG"), _header_define("M3_E_UNSUPPORTED")
+    assert _scan_call(lib, io=5) == E_ARG
+    assert b"io_dtype" in lib.m3_last_error()
+    assert _scan_call(lib, H=3, Hqk=2) == E_ARG
+    assert b"divisible by nheads_qk" in lib.m3_last_error()
+    assert _scan_call(lib, R=40) == E_ARG
+    assert b"<= d_state/2" in lib.m3_last_error()
+    assert _scan_call(lib, N=0) == E_ARG
+    assert _scan_call(lib) == E_ARG                      # NULL required pointers
+    assert b"NULL" in lib.m3_last_error()
+    assert _scan_call(lib, B=0) == 0                     # empty batch is a no-op
+    assert _scan_call(lib, L=0) == 0
+    assert lib.m3_last_error() == b""
+    fake = ctypes.c_void_p(4096)                         # never dereferenced: rejected first
+    assert _scan_call(lib, Q=fake, K=fake, V=fake, ADT=fake, DT=fake, Trap=fake, Qb=fake, Kb=fake,
+                      Ang=fake, Out=fake, N=1024, P=64, R=0) == E_UNSUP
+
+
+def test_misaligned_pointer_rejected(lib):
+    E_ALIGN = _header_define("M3_E_ALIGN")
+    ok = ctypes.c_void_p(4096)
+    bad = ctypes.c_void_p(4098)
+    assert _scan_call(lib, Q=bad, K=ok, V=ok, ADT=ok, DT=ok, Trap=ok, Qb=ok, Kb=ok, Ang=ok,
+                      Out=ok) == E_ALIGN
+
+
+def test_carry_arguments_all_or_none(lib):
+    p = ctypes.c_void_p(4096)
+    rc = lib.m3_chunk_scan_fwd_carry(p, p, p, p, p, p, p, p, p, None, None, p,
+                                     p, None, None, None, None, None, None, None,
+                                     1, 8, 2, 2, 64, 64, 16, 64, 1, None)
+    assert rc == _header_define("M3_E_ARG")
+    assert b"initial carry" in lib.m3_last_error()
+
+
+def test_decode_validation(lib):
+    E_ARG, E_UNSUP = _header_define("M3_E_ARG"), _header_define("M3_E_UNSUPPORTED")
+    p = ctypes.c_void_p(4096)
+    args = [p] * 16
+
+    def call(**kw):
+        d = dict(B=2, H=2, N=64, P=32, R=16, ind=1, outd=0, am=1, dm=0)
+        d.update(kw)
+        return lib.m3_decode_step(*args, d["B"], d["H"], d["N"], d["P"], d["R"], d["ind"], d["outd"],
+                                  d["am"], d["dm"], None)
+    assert call(am=2) == E_ARG and b"angle_mode" in lib.m3_last_error()
+    assert call(dm=3) == E_ARG and b"diag_mode" in lib.m3_last_error()
+    assert call(R=33) == E_ARG
+    assert call(N=12, R=4) == E_UNSUP                   # d_state/4 not a power of two
+    assert call(B=0) == 0
+
+
+def test_wrappers_refuse_cpu_tensors():
+    import torch
+    from mamba3_rocm import mamba3_siso_hip, rnn_step_hip
+    L, H, N, P, R = 8, 2, 64, 32, 16
+    z = lambda *s: torch.zeros(*s)  # noqa: E731
+    with pytest.raises(ValueError, match="ROCm device tensor"):
+        mamba3_siso_hip(z(L, H, N), z(L, H, N), z(L, H, P), z(H, L), z(H, L), z(H, L), z(H, N),
+                        z(H, N), z(L, H, R), z(H), z(L, H, P), 64)
+    carry = (z(1, H, R), z(1, H, P, N), z(1, H, N), z(1, H, P))
+    tin = (z(1, H, P), z(1, H, P), z(1, H, N), z(1, H, N), z(1, H), z(1, H), z(1, H), z(1, H, R))
+    with pytest.raises(ValueError, match="ROCm device tensor"):
+        rnn_step_hip(carry, tin, z(H, N), z(H, N), z(H))
+
+
+def test_mode_knobs_match_reference(monkeypatch):
+    from mamba3_rocm import recurrent_angle_mode, recurrent_diagonal_mode
+    monkeypatch.delenv("MAMBA3_RECURRENT_DIAGONAL_MODE", raising=False)
+    monkeypatch.delenv("MAMBA3_RECURRENT_ANGLE_MODE", raising=False)
+    assert recurrent_diagonal_mode() == "current"
+    assert recurrent_angle_mode() == "wrapped"
+    monkeypatch.setenv("MAMBA3_RECURRENT_DIAGONAL_MODE", "legacy_double")
+    monkeypatch.setenv("MAMBA3_RECURRENT_ANGLE_MODE", "legacy_unbounded")
+    assert recurrent_diagonal_mode() == "legacy_double"
+    assert recurrent_angle_mode() == "legacy_unbounded"
+    monkeypatch.setenv("MAMBA3_RECURRENT_DIAGONAL_MODE", "x")
+    with pytest.raises(ValueError, match="MAMBA3_RECURRENT_DIAGONAL_MODE"):
+        recurrent_diagonal_mode()
+    monkeypatch.setenv("MAMBA3_RECURRENT_ANGLE_MODE", "x")
+    with pytest.raises(ValueError, match="MAMBA3_RECURRENT_ANGLE_MODE"):
+        recurrent_angle_mode()
+
+
+def test_bench_byte_and_flop_formulas():
+    """bench.py's algorithmic counts at config 2 and config 4."""
+    import bench
+    assert bench.scan_bytes(8, 4096, 32, 128, 64, 32, 2) == 8 * 4096 * 32 * 1036
+    assert bench.scan_flops(8, 4096, 32, 128, 64, 64) == 8 * 4096 * 32 * 57344
+    # f32 carry traffic + bf16 step inputs + f32 y (the reference returns y in f32)
+    assert bench.decode_bytes(512, 32, 128, 64, 32, 2, 4) == 512 * 32 * 68492
+    assert abs(bench.scan_bytes(8, 4096, 32, 128, 64, 32, 2) / 8e12 * 1e6 - 135.8) < 0.1
+
+
+def test_bf16_rounding_matches_torch():
+    import torch
+    from oracle import inputs as I
+    x = np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 10
+    ours = I.bf16_round(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours, theirs)
