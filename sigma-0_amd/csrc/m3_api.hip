@@ -96,6 +96,8 @@ int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
   if (impl == M3_IMPL_NONE)
     return fail(M3_E_UNSUPPORTED, "no kernel for d_state=%d headdim=%d R=%d (generic limits: N even <= 512, "
                 "P <= 512, P*N*4 <= 64 KiB)", N, P, R);
+  if (impl == M3_IMPL_CHUNKED_MFMA && !aligned16(Angles))
+    return fail(M3_E_ALIGN, "Angles must be 16-byte aligned");  // staged as 16-byte rows
   m3::ScanArgs a;
   a.q = Q; a.k = K; a.v = V; a.adt = ADT; a.dt = DT; a.trap = Trap;
   a.qbias = Q_bias; a.kbias = K_bias; a.ang = Angles; a.D = D; a.z = Z; a.out = Out;

@@ -70,6 +70,7 @@ template <> struct Vec8<bf16> {
   uint4 raw;
   __device__ __forceinline__ void zero() { raw = make_uint4(0, 0, 0, 0); }
   __device__ __forceinline__ void load(const bf16* p) { raw = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void raw_set(const uint4& r) { raw = r; }
   __device__ __forceinline__ void to_f(float f[8]) const {
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -85,6 +86,10 @@ template <> struct Vec8<float> {
   __device__ __forceinline__ void load(const float* p) {
     a = reinterpret_cast<const float4*>(p)[0];
     b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void raw_set2(const uint4& r0, const uint4& r1) {
+    a = make_float4(__uint_as_float(r0.x), __uint_as_float(r0.y), __uint_as_float(r0.z), __uint_as_float(r0.w));
+    b = make_float4(__uint_as_float(r1.x), __uint_as_float(r1.y), __uint_as_float(r1.z), __uint_as_float(r1.w));
   }
   __device__ __forceinline__ void to_f(float f[8]) const {
     f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;

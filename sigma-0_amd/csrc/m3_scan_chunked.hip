@@ -12,10 +12,11 @@
 //            (K_s w)^T V on MFMA, h kept in fp32 accumulators      (:177-233)
 //   phase 7  (Y_diag + Y_off + (D + QK) V) * silu(Z), 16-byte stores (:402-419)
 //
-// One workgroup (4 waves) per (batch, head) walks the chunks in order; the
+// One workgroup (8 waves) per (batch, head) walks the chunks in order; the
 // P x N fp32 state never leaves the CU.  While a chunk's matrix work runs,
-// the next chunk's inputs are already in flight into registers, so every
-// input byte is read from HBM exactly once and the output written once.
+// the next chunk's inputs stream into LDS with direct-to-LDS loads (whole
+// rows per instruction, stored XOR-swizzled), so every input byte is read
+// from HBM exactly once and the output written once.
 //
 // MFMA tile conventions (32x32, verified lane layouts):
 //   A (32 x K): lane i holds row i%32, k = (i/32)*KPL + [0, KPL)
@@ -59,17 +60,22 @@ template <> struct MF<bf16> {
     f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
     return f;
   }
-  // A operand K^T: row n = n0 + lane%32, k = s = s0 + 8(lane/32) + q, read from row-major K[s][n]
-  __device__ __forceinline__ static frag kt(const bf16* k, int ldk, int n0, int s0, int lane) {
-    const bf16* c = k + (s0 + 8 * (lane >> 5)) * ldk + n0 + (lane & 31);
+  // A operand (w K)^T: row n = n0 + lane%32, k = s = s0 + 8(lane/32) + q, read from
+  // row-major K[s][n] and scaled by w[s] (the decay from token s to the chunk end)
+  __device__ __forceinline__ static frag ktw(const bf16* k, const float* w, int ldk, int n0, int s0, int lane) {
+    const int sb = s0 + 8 * (lane >> 5);
+    const bf16* c = k + sb * ldk + n0 + (lane & 31);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + sb);
+    const float4 w1 = *reinterpret_cast<const float4*>(w + sb + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
     frag f;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) f[q] = c[q * ldk];
+    for (int q = 0; q < 8; ++q) f[q] = (bf16)((float)c[q * ldk] * wv[q]);
     return f;
   }
-  // B operand w-scaled V for the state update: precomputed V^T * w in vwt
-  __device__ __forceinline__ static frag vw(const bf16* vwt, const bf16*, const float*, int ldv, int p0, int s0, int lane) {
-    return ld(vwt, ldv, p0, s0, lane);
+  // B operand V[s][p]: row p of V^T, s = s0 + 8(lane/32) + q
+  __device__ __forceinline__ static frag vs(const bf16* vt, int ldv, int p0, int s0, int lane) {
+    return ld(vt, ldv, p0, s0, lane);
   }
   // write rows n0 + 8g + 4(lane/32) + 0..3 of column p of a C tile into hb[p][n]
   __device__ __forceinline__ static void store_ht(bf16* hb, int ldh, int p, int n0, const f32x16& c, int lane) {
@@ -96,12 +102,12 @@ template <> struct MF<float> {
   __device__ __forceinline__ static frag vperm(const float* vt, int ldv, int p0, int s0, int j, int lane) {
     return vt[(p0 + (lane & 31)) * ldv + s0 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)];
   }
-  __device__ __forceinline__ static frag kt(const float* k, int ldk, int n0, int s0, int lane) {
-    return k[(s0 + (lane >> 5)) * ldk + n0 + (lane & 31)];
+  __device__ __forceinline__ static frag ktw(const float* k, const float* w, int ldk, int n0, int s0, int lane) {
+    const int sv = s0 + (lane >> 5);
+    return k[sv * ldk + n0 + (lane & 31)] * w[sv];
   }
-  __device__ __forceinline__ static frag vw(const float*, const float* vt, const float* w, int ldv, int p0, int s0, int lane) {
-    const int s = s0 + (lane >> 5);
-    return vt[(p0 + (lane & 31)) * ldv + s] * w[s];
+  __device__ __forceinline__ static frag vs(const float* vt, int ldv, int p0, int s0, int lane) {
+    return vt[(p0 + (lane & 31)) * ldv + s0 + (lane >> 5)];
   }
   __device__ __forceinline__ static void store_ht(float* hb, int ldh, int p, int n0, const f32x16& c, int lane) {
 #pragma unroll
@@ -171,30 +177,28 @@ struct Geo {
   static constexpr int CS = CS_, N = N_, P = P_, R = R_, NW = NW_, NT = 64 * NW_;
   static constexpr int NWY = NW / 2;                        // waves on output tiles; the rest on state tiles
   static constexpr int KSTEP = MF<T>::KSTEP;
-  static constexpr int LB = CS / 32, PB = P / 32, NB = N / 32;
+  static constexpr int PB = P / 32, NB = N / 32;            // 32x32 state tiles
+  static constexpr int LB16 = CS / 16, PT = P / 16;         // 16-row query blocks, 16-col value tiles
+  static constexpr int TS = BF ? 2 : 4;
   static constexpr int LDQ = N + MF<T>::PAD;                // sQ, sK rows (elements)
-  static constexpr int LDV = CS + MF<T>::PAD;               // sVt, sVwT rows
+  static constexpr int LDV = CS + MF<T>::PAD;               // sVt rows
   static constexpr int LDH = N + MF<T>::PAD;                // sHB rows
   static constexpr int LDY = P + 4;                         // sY rows (fp32)
-  static constexpr int LDC = R + 2;                         // cos/sin table rows (float2)
-  static constexpr int QG = N / 8;                          // 8-wide vectors per Q/K row
-  static constexpr int QROWS = NT / QG;                     // Q/K rows covered per pass
-  static constexpr int QV = (CS + QROWS - 1) / QROWS;       // Q/K vectors per thread
-  static constexpr int VV = (CS * (P / 8) + NT - 1) / NT;   // V/Z vectors per thread
-  static constexpr int CPW = R / NW;                        // rotation columns per wave
-  static constexpr int LB16 = CS / 16, PT = P / 16;          // 16-row query blocks, 16-col value tiles
-  static constexpr int ST = (NB * PB + (NW - NWY) - 1) / (NW - NWY);  // state tiles per state wave
-  static constexpr bool VWT = BF;                           // precomputed w-scaled V^T
-  static constexpr int TS = BF ? 2 : 4;
-  static constexpr int YB = CS * LDY * 4, CB = CS * LDC * 8;
-  static constexpr int COMMON = 2 * CS * LDQ * TS + (VWT ? 2 : 1) * P * LDV * TS +
-                                (YB > CB ? YB : CB) + 7 * CS * 4 + 64;
+  static constexpr int QG = N / 8, QGW = (QG + NW - 1) / NW;  // Q/K 8-column groups, per wave
+  static constexpr int VG = P / 8, VGW = (VG + NW - 1) / NW;  // V/Z 8-column groups, per wave
+  static constexpr int HT = (NB * PB + (NW - NWY) - 1) / (NW - NWY);  // state tiles per state wave
+  // 16-byte staging slots per row: Q/K, V/Z, rotation rates
+  static constexpr int SQ = N * TS / 16, SV = P * TS / 16, SA = R / 4 > 0 ? R / 4 : 1;
+  static constexpr int GS = 8 * TS / 16;                    // slots per 8-element group (1 bf16, 2 f32)
+  static constexpr int STAGE = (2 * CS * SQ + 2 * CS * SV + CS * SA) * 16 + 3 * (CS + 4) * 4;
+  static constexpr int COMMON = 2 * CS * LDQ * TS + P * LDV * TS + CS * LDY * 4 + 8 * CS * 4 + 8 * N + 64 + STAGE;
   static constexpr int HBB = P * LDH * TS;
   // two state-operand buffers (no barrier between the output and state-update
   // MFMAs) when they fit in the 160 KiB of LDS, else one
   static constexpr int NHB = (COMMON + 2 * HBB <= 160 * 1024 - 512) ? 2 : 1;
-  static_assert(R == 0 || (R % NW == 0 && R % 4 == 0 && 2 * R <= N), "rotation width");
-  static_assert(NT % QG == 0, "Q/K column groups");
+  static_assert(CS <= 64, "one token per lane");
+  static_assert(R % 4 == 0 && 2 * R <= N, "rotation width: a multiple of 4, at most N/2");
+  static_assert((SQ & (SQ - 1)) == 0 && (SV & (SV - 1)) == 0 && (SA & (SA - 1)) == 0, "swizzle widths");
 };
 
 template <typename G>
@@ -203,26 +207,80 @@ struct __attribute__((aligned(16))) Smem {
   T q[G::CS * G::LDQ];
   T k[G::CS * G::LDQ];
   T vt[G::P * G::LDV];
-  T vwt[G::VWT ? G::P * G::LDV : 1];
   T hb[G::NHB][G::P * G::LDH];
-  union __attribute__((aligned(16))) U {
-    float y[G::CS * G::LDY];          // output tile before the gate (phase 3 -> 4)
-    float2 cs[G::CS * G::LDC];        // cos/sin of the rotation angles (phase 1 -> 2)
-  } u;
-  alignas(16) float ac2[G::CS];    // A_cum * log2(e)
-  float expa[G::CS];   // e^{A_cum}
-  float w[G::CS];      // e^{A_end - A_cum}
-  alignas(16) float g16[G::CS];  // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
-  float gam[G::CS];
-  float scl[G::CS];
-  float dtv[G::CS];
-  float qk[G::CS];
-  float qb[G::N];      // Q_bias, K_bias of this head
-  float kb[G::N];
-  float dec;
+  alignas(16) float y[G::CS * G::LDY];   // output tile before the gate (phase 3 -> 7)
+  // raw inputs staged by direct-to-LDS loads: 16-byte slots, row t slot s stored at
+  // t * S + (s ^ (t mod S)) so that a lane-per-row read is bank-conflict free
+  alignas(16) uint4 rq[G::CS * G::SQ];
+  alignas(16) uint4 rk[G::CS * G::SQ];
+  alignas(16) uint4 rv[G::CS * G::SV];
+  alignas(16) uint4 rz[G::CS * G::SV];
+  alignas(16) uint4 ra[G::CS * G::SA];
+  alignas(16) float rs[3][G::CS + 4];    // adt, dt, trap of the chunk; [CS] = the next token's
+  alignas(16) float qb[G::N];            // biases of this head
+  alignas(16) float kb[G::N];
+  alignas(16) float ac2[G::CS];          // A_cum * log2(e)
+  alignas(16) float g16[G::CS];          // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
+  alignas(16) float w[G::CS];            // e^{A_end - A_cum}
+  float expa[G::CS];                     // e^{A_cum}
+  float qk[2][G::CS];                    // QK skip term, accumulated over column groups (chunk parity)
+  float dec;                             // e^{A_end}
 };
 
-template <int CPW> struct AngRegs { float v[CPW > 0 ? CPW : 1]; };
+// Direct-to-LDS loads (global_load_lds): the LDS slot is the instruction's base plus
+// size * lane.  The LDS pointer is cast to the local address space here so that the
+// builtin sees a local pointer rather than a flat one.
+typedef __attribute__((address_space(3))) uint4 lds_uint4;
+typedef __attribute__((address_space(3))) float lds_float;
+__device__ __forceinline__ void lds_dma16(const void* g, lds_uint4* l) { __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0); }
+__device__ __forceinline__ void lds_dma4(const void* g, lds_float* l) { __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0); }
+
+// Direct-to-LDS staging of CS rows x S 16-byte slots.  Instruction j stages 64 slots:
+// lane -> (row, physical slot) = (64j/S + lane/S, lane%S), fetching logical slot
+// (lane%S) ^ (row%S), so each row is read whole (coalesced) and stored swizzled.  The
+// lane part of the global offset repeats every PER instructions (row%S repeats), so a
+// few 32-bit lane offsets plus a wave-uniform row base address every instruction.
+template <int CS, int S>
+__device__ __forceinline__ void stage_rows(lds_uint4* dst, const char* src, long stride, int rows_valid,
+                                           int lane) {
+  constexpr int RP = 64 / S;                               // rows per instruction
+  constexpr int NJ = CS * S / 64;                          // instructions
+  static_assert(CS * S % 64 == 0, "whole instructions");
+  constexpr int PER = S * S / 64 > 1 ? S * S / 64 : 1;     // period of the lane pattern
+  const int lrow = lane / S;
+  uint32_t off[PER];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const uint32_t row = p * RP + lrow;
+    off[p] = row * (uint32_t)stride + 16u * ((lane % S) ^ (row & (S - 1)));
+  }
+  // the row base is made opaque so that the compiler keeps one wave-uniform base per
+  // group of PER instructions instead of strength-reducing to 64-bit lane pointers
+  const char* base = src;
+  asm volatile("" : "+s"(base));
+  if (rows_valid >= CS) {
+#pragma unroll
+    for (int m = 0; m < NJ / PER; ++m) {
+      const char* bm = base + (long)m * (PER * RP) * stride;
+#pragma unroll
+      for (int p = 0; p < PER; ++p) lds_dma16(bm + off[p], dst + 64 * (m * PER + p));
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < NJ / PER; ++m) {
+      const char* bm = base + (long)m * (PER * RP) * stride;
+#pragma unroll
+      for (int p = 0; p < PER; ++p) {
+        const int j = m * PER + p;
+        if (j * RP + lrow < rows_valid) lds_dma16(bm + off[p], dst + 64 * j);
+      }
+    }
+  }
+}
+template <int S>
+__device__ __forceinline__ const uint4& staged(const uint4* buf, int row, int slot) {
+  return buf[row * S + (slot ^ (row & (S - 1)))];
+}
 
 template <typename T, int CS, int N, int P, int R, int NW>
 __global__ __launch_bounds__(64 * NW, 1)
@@ -235,128 +293,81 @@ void scan_chunked_kernel(ScanArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave >= 0 && wave < NW);
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh % a.H;
   const int hq = h / (a.H / a.Hqk);
   const int L = a.L, H = a.H, HQ = a.Hqk;
   const int nc = (L + CS - 1) / CS;
-  const T* gQ = reinterpret_cast<const T*>(a.q);
-  const T* gK = reinterpret_cast<const T*>(a.k);
-  const T* gV = reinterpret_cast<const T*>(a.v);
-  const T* gZ = reinterpret_cast<const T*>(a.z);
   T* gO = reinterpret_cast<T*>(a.out);
   const float* gadt = a.adt + (long)bh * L;
   const float* gdt = a.dt + (long)bh * L;
   const float* gtr = a.trap + (long)bh * L;
   const float Dh = a.D ? a.D[h] : 0.0f;
-  const bool has_z = gZ != nullptr;
+  const bool has_z = a.z != nullptr;
 
-  // ---- fixed per-thread mappings
-  const int qg = tid % G::QG;            // Q/K column group (8 columns)
-  const int qrow0 = tid / G::QG;         // Q/K row of pass 0
-  for (int n = tid; n < N; n += G::NT) {
-    sm.qb[n] = a.qbias[(long)h * N + n];
-    sm.kb[n] = a.kbias[(long)h * N + n];
+  // ---- element offsets of row (b, t=0, head) in each input; rows advance by the stride
+  const long qk_row = ((long)b * L * HQ + hq) * N, qk_stride = (long)HQ * N;
+  const long v_row = ((long)b * L * H + h) * P, v_stride = (long)H * P;
+  const long a_row = ((long)b * L * H + h) * R, a_stride = (long)H * R;
+  for (int i = tid; i < N; i += G::NT) {
+    sm.qb[i] = a.qbias[(long)h * N + i];
+    sm.kb[i] = a.kbias[(long)h * N + i];
   }
-  const long qk_base = ((long)b * L * HQ + hq) * N + 8 * qg;   // + t * HQ * N
-  const long v_base = ((long)b * L * H + h) * P;                // + t * H * P + 8 * g8
-  const long a_base = ((long)b * L * H + h) * R + wave * G::CPW;  // + t * H * R
 
-  // ---- raw input registers (next chunk) and the current chunk's V/Z
-  Vec8<T> rq[G::QV], rk[G::QV], rv[G::VV], rz[G::VV], cv[G::VV], cz[G::VV];
-  AngRegs<G::CPW> ra;
-  float s_adt = 0.f, s_dt = 0.f, s_tr = 0.f, s_dtn = 0.f, s_trn = 0.f;
-
-  auto load_chunk = [&](int c) {
+  // ---- staging: the state waves stream the next chunk's inputs into LDS
+  auto stage_main = [&](int c) {           // Q, K, V, rotation rates, scalars of chunk c
     const int t0 = c * CS;
-#pragma unroll
-    for (int i = 0; i < G::QV; ++i) {
-      const int t = qrow0 + i * G::QROWS;
-      if (t < CS && t0 + t < L) {
-        const long off = qk_base + (long)(t0 + t) * HQ * N;
-        rq[i].load(gQ + off);
-        rk[i].load(gK + off);
-      } else {
-        rq[i].zero();
-        rk[i].zero();
+    const int valid = L - t0;
+    const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
+    const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
+    const char* v0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + v_row + (long)t0 * v_stride);
+    if (wave == G::NWY) stage_rows<CS, G::SQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
+    if (wave == G::NWY + 1) stage_rows<CS, G::SQ>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
+    if (wave == G::NWY + 2) {
+      stage_rows<CS, G::SV>((lds_uint4*)sm.rv, v0, v_stride * G::TS, valid, lane);
+      if (R > 0) {
+        const char* a0 = reinterpret_cast<const char*>(a.ang + a_row + (long)t0 * a_stride);
+        stage_rows<CS, G::SA>((lds_uint4*)sm.ra, a0, a_stride * 4, valid, lane);
       }
     }
-#pragma unroll
-    for (int i = 0; i < G::VV; ++i) {
-      const int v = tid + i * G::NT;
-      const int t = v % CS, g8 = v / CS;
-      if (g8 < P / 8 && t0 + t < L) {
-        const long off = v_base + (long)(t0 + t) * H * P + 8 * g8;
-        rv[i].load(gV + off);
-        if (has_z) rz[i].load(gZ + off); else rz[i].zero();
-      } else {
-        rv[i].zero();
-        rz[i].zero();
+    if (wave == G::NWY + 3) {
+      if (lane < CS && lane < valid) {
+        lds_dma4(gadt + t0 + lane, (lds_float*)&sm.rs[0][0]);
+        lds_dma4(gdt + t0 + lane, (lds_float*)&sm.rs[1][0]);
+        lds_dma4(gtr + t0 + lane, (lds_float*)&sm.rs[2][0]);
+      }
+      if (lane == 0 && t0 + CS < L) {
+        lds_dma4(gdt + t0 + CS, (lds_float*)&sm.rs[1][CS]);
+        lds_dma4(gtr + t0 + CS, (lds_float*)&sm.rs[2][CS]);
       }
     }
-    if (G::CPW > 0) {
-      const bool ok = lane < CS && t0 + lane < L;
-      const float* src = a.ang + a_base + (long)(t0 + lane) * H * R;
-#pragma unroll
-      for (int j = 0; j < G::CPW; j += (G::CPW >= 4 ? 4 : G::CPW)) {
-        if (G::CPW >= 4) {
-          const float4 x = ok ? *reinterpret_cast<const float4*>(src + j) : make_float4(0, 0, 0, 0);
-          ra.v[j] = x.x; ra.v[j + 1] = x.y; ra.v[j + 2] = x.z; ra.v[j + 3] = x.w;
-        } else if (G::CPW == 2) {
-          const float2 x = ok ? *reinterpret_cast<const float2*>(src) : make_float2(0, 0);
-          ra.v[0] = x.x; ra.v[1] = x.y;
-        } else {
-          ra.v[0] = ok ? src[0] : 0.0f;
-        }
-      }
-    }
-    if (wave == 0) {
-      const int t = t0 + lane;
-      const bool ok = lane < CS && t < L;
-      s_adt = ok ? gadt[t] : 0.f;
-      s_dt = ok ? gdt[t] : 0.f;
-      s_tr = ok ? gtr[t] : 0.f;
-      const bool okn = lane == CS - 1 && t0 + CS < L;
-      s_dtn = okn ? gdt[t0 + CS] : 0.f;
-      s_trn = okn ? gtr[t0 + CS] : 0.f;
+  };
+  auto stage_z = [&](int c) {              // Z of chunk c
+    if (has_z && wave == G::NWY + 3) {
+      const int t0 = c * CS;
+      const char* z0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.z) + v_row + (long)t0 * v_stride);
+      stage_rows<CS, G::SV>((lds_uint4*)sm.rz, z0, v_stride * G::TS, L - t0, lane);
     }
   };
 
-  // wave 0: decay prefix, trapezoid weights for the chunk whose scalars are in s_*
-  auto scalar_stage = [&]() {
-    const float sig = sigmoid_fast(s_tr);
-    const float gam = s_dt * sig;
-    const float u = s_dt * (1.0f - sig);                            // dt (1 - sigmoid), this token
-    float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // wave_shl:1 -> next token
-    if (lane == CS - 1) un = s_dtn * (1.0f - sigmoid_fast(s_trn));
-    const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
-    const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
-    const float ablk = __shfl(acum, lane | 15, 64);
-    if (lane < CS) {
-      sm.ac2[lane] = acum * kLog2e;
-      sm.expa[lane] = exp2_fast(acum * kLog2e);
-      sm.w[lane] = exp2_fast((aend - acum) * kLog2e);
-      sm.g16[lane] = exp2_fast((ablk - acum) * kLog2e);
-      sm.gam[lane] = gam;
-      sm.scl[lane] = gam + un;
-      sm.dtv[lane] = s_dt;
-    }
-    if (lane == 0) sm.dec = exp2_fast(aend * kLog2e);
-  };
-
-  // ---- state accumulators (state waves): tiles z = (wave - NWY) * ST + m of h^T
+  // ---- state accumulators (state waves): tiles z = (wave - NWY) * HT + m of h^T
   const bool ywave = wave < G::NWY;
-  const int zw = (wave - G::NWY) * G::ST;
-  f32x16 hacc[G::ST];
-  float carry[G::CPW > 0 ? G::CPW : 1];
+  const int zw = (wave - G::NWY) * G::HT;
+  f32x16 hacc[G::HT];
+  float carry[G::QGW][4];
 #pragma unroll
-  for (int j = 0; j < G::CPW; ++j)
-    carry[j] = a.init_theta ? a.init_theta[(long)bh * R + wave * G::CPW + j] : 0.0f;
+  for (int k = 0; k < G::QGW; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 4 * (wave + NW * k) + j;
+      carry[k][j] = (a.init_theta && r < R) ? a.init_theta[(long)bh * R + r] : 0.0f;
+    }
   {
     // effective entering state: h0 + (1 - sigmoid(trap_0)) dt_0 (v0 (x) k0)
     const float cinit = (a.init_h && L > 0) ? (1.0f - sigmoid_fast(gtr[0])) * gdt[0] : 0.0f;
 #pragma unroll
-    for (int m = 0; m < G::ST; ++m) {
+    for (int m = 0; m < G::HT; ++m) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) hacc[m][r] = 0.0f;
       const int z = zw + m;
@@ -375,114 +386,139 @@ void scan_chunked_kernel(ScanArgs a) {
       }
     }
   }
-
-  load_chunk(0);
-  if (wave == 0) scalar_stage();
+  // staging never holds uninitialised bits: rows past the sequence end are not loaded
+  for (int i = tid; i < G::CS * G::SQ; i += G::NT) { sm.rq[i] = make_uint4(0, 0, 0, 0); sm.rk[i] = sm.rq[i]; }
+  for (int i = tid; i < G::CS * G::SV; i += G::NT) { sm.rv[i] = make_uint4(0, 0, 0, 0); sm.rz[i] = sm.rv[i]; }
+  for (int i = tid; i < G::CS * G::SA; i += G::NT) sm.ra[i] = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < 3 * (G::CS + 4); i += G::NT) ((lds_float*)&sm.rs[0][0])[i] = 0.0f;
+  if (tid < CS) sm.qk[0][tid] = 0.0f;
   __syncthreads();
+  stage_main(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  Vec8<T> cv[G::VGW];                      // this lane's V row slice, kept for the epilogue
 
   for (int c = 0; c < nc; ++c) {
     const int t0 = c * CS;
     const int hcur = c % G::NHB, hnext = (c + 1) % G::NHB;
+    const bool tail = t0 + CS > L;              // chunk holds padding rows
+    const bool tok = lane < CS && t0 + lane < L;
+    const int tl = lane < CS ? lane : 0;        // staging row of this lane
 
-    // ---- phase 1: rotation angles. lane = token, CPW columns per wave:
-    // increments tanh(theta) pi dt, chunk prefix (DPP scan), carry, wrap, cos/sin
-    if (G::CPW > 0) {
-      const float dtl = lane < CS ? sm.dtv[lane] : 0.0f;
-      float2 csv[G::CPW > 0 ? G::CPW : 1];
+    // ================= prep: lane = token =================
+    // per-token decay prefix and trapezoid weights (every wave, registers)
+    const float s_adt = tok ? sm.rs[0][tl] : 0.0f;
+    const float s_dt = tok ? sm.rs[1][tl] : 0.0f;
+    const float s_tr = tok ? sm.rs[2][tl] : 0.0f;
+    const float sig = sigmoid_fast(s_tr);
+    const float gam = s_dt * sig;
+    const float u = s_dt * (1.0f - sig);                                   // dt (1 - sigmoid), this token
+    float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // next token
+    if (lane == CS - 1) un = (t0 + CS < L) ? sm.rs[1][CS] * (1.0f - sigmoid_fast(sm.rs[2][CS])) : 0.0f;
+    const float scl = gam + un;
+    const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
+    const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
+    if (wave == 0 && lane < CS) {
+      const float ablk = __shfl(acum, lane | 15, 64);
+      sm.ac2[lane] = acum * kLog2e;
+      sm.expa[lane] = exp2_fast(acum * kLog2e);
+      sm.g16[lane] = exp2_fast((ablk - acum) * kLog2e);
+      sm.w[lane] = exp2_fast((aend - acum) * kLog2e);
+      if (lane == 0) sm.dec = exp2_fast(aend * kLog2e);
+    }
+    // Q/K column groups: rotation angles, biases, QK skip partial, rope, key scale
+    float dot = 0.0f;
 #pragma unroll
-      for (int j = 0; j < G::CPW; ++j) {
-        const float d = tanh_fast(ra.v[j]) * kPi * dtl;
-        const float th = wrap_2pi(carry[j] + wave_incl_scan(d));
-        carry[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
-        sincos_wrapped(th, &csv[j].x, &csv[j].y);
-      }
-      if (lane < CS) {
-        float2* dst = &sm.u.cs[lane * G::LDC + wave * G::CPW];
-#pragma unroll
-        for (int j = 0; j < G::CPW; j += 2) {
-          if (G::CPW >= 2) {
-            *reinterpret_cast<float4*>(dst + j) = make_float4(csv[j].x, csv[j].y, csv[j + 1].x, csv[j + 1].y);
+    for (int k = 0; k < G::QGW; ++k) {
+      const int g = wave + NW * k;
+      if (g < G::QG) {
+        float qf[8], kf[8];
+        {
+          Vec8<T> qv, kv;
+          if constexpr (G::BF) {
+            qv.raw_set(staged<G::SQ>(sm.rq, tl, g));
+            kv.raw_set(staged<G::SQ>(sm.rk, tl, g));
           } else {
-            dst[0] = csv[0];
+            qv.raw_set2(staged<G::SQ>(sm.rq, tl, 2 * g), staged<G::SQ>(sm.rq, tl, 2 * g + 1));
+            kv.raw_set2(staged<G::SQ>(sm.rk, tl, 2 * g), staged<G::SQ>(sm.rk, tl, 2 * g + 1));
           }
+          qv.to_f(qf);
+          kv.to_f(kf);
+        }
+        {
+          const float4* qb4 = reinterpret_cast<const float4*>(&sm.qb[8 * g]);
+          const float4* kb4 = reinterpret_cast<const float4*>(&sm.kb[8 * g]);
+          const float4 qa = qb4[0], qc = qb4[1], ka = kb4[0], kc = kb4[1];
+          const float qbv[8] = {qa.x, qa.y, qa.z, qa.w, qc.x, qc.y, qc.z, qc.w};
+          const float kbv[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            qf[e] += qbv[e];
+            kf[e] += kbv[e];
+            dot += qf[e] * kf[e];
+          }
+        }
+        if (4 * g < R) {
+          const uint4 rr = staged<G::SA>(sm.ra, tl, g);
+          const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
+                                __uint_as_float(rr.w)};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // theta = carry + prefix of tanh(rate) pi dt over the chunk, mod 2pi
+            const float d = tok ? tanh_fast(rav[j]) * kPi * s_dt : 0.0f;
+            const float th = wrap_2pi(carry[k][j] + wave_incl_scan(d));
+            carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
+            float cs, sn;
+            sincos_wrapped(th, &cs, &sn);
+            const float q0 = qf[2 * j], q1 = qf[2 * j + 1];
+            qf[2 * j] = q0 * cs - q1 * sn;
+            qf[2 * j + 1] = q0 * sn + q1 * cs;
+            const float k0 = kf[2 * j], k1 = kf[2 * j + 1];
+            kf[2 * j] = k0 * cs - k1 * sn;
+            kf[2 * j + 1] = k0 * sn + k1 * cs;
+          }
+        }
+        if (a.fin_k && t0 + lane == L - 1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a.fin_k[(long)bh * N + 8 * g + e] = kf[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] *= scl;
+        if (tail && !tok) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) { qf[e] = 0.0f; kf[e] = 0.0f; }
+        }
+        if (lane < CS) {
+          store8(&sm.q[lane * G::LDQ + 8 * g], qf);
+          store8(&sm.k[lane * G::LDQ + 8 * g], kf);
+        }
+      }
+    }
+    if (lane < CS) atomicAdd(&sm.qk[c & 1][lane], dot * gam);   // gam == 0 on padding rows
+    // V column groups: V^T (this lane's slice is kept for the epilogue)
+#pragma unroll
+    for (int k = 0; k < G::VGW; ++k) {
+      const int g = wave + NW * k;
+      if (g < G::VG) {
+        if constexpr (G::BF) cv[k].raw_set(staged<G::SV>(sm.rv, tl, g));
+        else cv[k].raw_set2(staged<G::SV>(sm.rv, tl, 2 * g), staged<G::SV>(sm.rv, tl, 2 * g + 1));
+        if (tail && !tok) cv[k].zero();
+        if (lane < CS) {
+          float vf[8];
+          cv[k].to_f(vf);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) sm.vt[(8 * g + q) * G::LDV + lane] = Elem<T>::from_f(vf[q]);
         }
       }
     }
     __syncthreads();
 
-    // ---- phase 2: biases, QK skip, rope, key scale -> sQ, sK; V^T, (w V)^T
-#pragma unroll
-    for (int i = 0; i < G::QV; ++i) {
-      const int t = qrow0 + i * G::QROWS;
-      float qf[8], kf[8];
-      rq[i].to_f(qf);
-      rk[i].to_f(kf);
-      const float4* qbp = reinterpret_cast<const float4*>(&sm.qb[8 * qg]);
-      const float4* kbp = reinterpret_cast<const float4*>(&sm.kb[8 * qg]);
-      const float4 qb0 = qbp[0], qb1 = qbp[1], kb0 = kbp[0], kb1 = kbp[1];
-      const float qb[8] = {qb0.x, qb0.y, qb0.z, qb0.w, qb1.x, qb1.y, qb1.z, qb1.w};
-      const float kb[8] = {kb0.x, kb0.y, kb0.z, kb0.w, kb1.x, kb1.y, kb1.z, kb1.w};
-      float dot = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qf[e] += qb[e];
-        kf[e] += kb[e];
-        dot += qf[e] * kf[e];
-      }
-      dot = group_sum<G::QG>(dot);
-      if (t < CS) {
-        const bool real = t0 + t < L;
-        if (qg == 0) sm.qk[t] = real ? dot * sm.gam[t] : 0.0f;
-        if (4 * qg < R) {
-          const float4* cp = reinterpret_cast<const float4*>(&sm.u.cs[t * G::LDC + 4 * qg]);
-          const float4 c01 = cp[0], c23 = cp[1];
-          const float cs4[4] = {c01.x, c01.z, c23.x, c23.z};
-          const float sn4[4] = {c01.y, c01.w, c23.y, c23.w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float q0 = qf[2 * q], q1 = qf[2 * q + 1];
-            qf[2 * q] = q0 * cs4[q] - q1 * sn4[q];
-            qf[2 * q + 1] = q0 * sn4[q] + q1 * cs4[q];
-            const float k0 = kf[2 * q], k1 = kf[2 * q + 1];
-            kf[2 * q] = k0 * cs4[q] - k1 * sn4[q];
-            kf[2 * q + 1] = k0 * sn4[q] + k1 * cs4[q];
-          }
-        }
-        if (a.fin_k && t0 + t == L - 1) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a.fin_k[(long)bh * N + 8 * qg + e] = kf[e];
-        }
-        const float sc = sm.scl[t];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          qf[e] = real ? qf[e] : 0.0f;
-          kf[e] = real ? kf[e] * sc : 0.0f;
-        }
-        store8(&sm.q[t * G::LDQ + 8 * qg], qf);
-        store8(&sm.k[t * G::LDQ + 8 * qg], kf);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < G::VV; ++i) {
-      const int v = tid + i * G::NT;
-      const int t = v % CS, g8 = v / CS;
-      cv[i] = rv[i];
-      cz[i] = rz[i];
-      if (g8 < P / 8) {
-        float vf[8];
-        rv[i].to_f(vf);
-        const float wt = sm.w[t];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          sm.vt[(8 * g8 + q) * G::LDV + t] = Elem<T>::from_f(vf[q]);
-          if (G::VWT) sm.vwt[(8 * g8 + q) * G::LDV + t] = Elem<T>::from_f(vf[q] * wt);
-        }
-      }
-    }
-    __syncthreads();
+    // ---- staging for the epilogue of this chunk and the inputs of the next one
+    stage_z(c);
+    if (c + 1 < nc) stage_main(c + 1);
 
-    // ---- next chunk's inputs go in flight under the matrix work
-    if (c + 1 < nc) load_chunk(c + 1);
+    if (wave == NW - 1 && lane < CS) sm.qk[(c + 1) & 1][lane] = 0.0f;   // read last by phase 7 of chunk c-1
 
     if (wave < G::LB16 && wave < G::NWY) {
       // ---- phases 3 + 6 for query rows l in [16 lb, 16 lb + 16), all value columns:
@@ -510,29 +546,29 @@ void scan_chunked_kernel(ScanArgs a) {
         if (sp <= lb) {
           f32x4 st[2];
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int sb = sp + u;
+          for (int u2 = 0; u2 < 2; ++u2) {
+            const int sb = sp + u2;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) st[u][r] = 0.0f;
+            for (int r = 0; r < 4; ++r) st[u2][r] = 0.0f;
             if (sb <= lb) {
 #pragma unroll
               for (int kk = 0; kk < N / W::KSTEP; ++kk)
-                st[u] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, lane),
-                               W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, lane), st[u]);
+                st[u2] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, lane),
+                                W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, lane), st[u2]);
               const int s0 = 16 * sb + 4 * (lane >> 4);
               if (sb < lb) {
                 // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
                 const float f = exp2_fast(fminf(al - sm.ac2[16 * sb + 15], 0.0f));
-                const float4 g = *reinterpret_cast<const float4*>(&sm.g16[s0]);
-                st[u][0] *= f * g.x; st[u][1] *= f * g.y; st[u][2] *= f * g.z; st[u][3] *= f * g.w;
+                const float4 g4 = *reinterpret_cast<const float4*>(&sm.g16[s0]);
+                st[u2][0] *= f * g4.x; st[u2][1] *= f * g4.y; st[u2][2] *= f * g4.z; st[u2][3] *= f * g4.w;
               } else {
                 // diagonal block: causal mask and per-element decay
                 const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[s0]);
                 const float asv[4] = {as.x, as.y, as.z, as.w};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                  const float v = st[u][r] * exp2_fast(fminf(al - asv[r], 0.0f));
-                  st[u][r] = (s0 + r < l) ? v : 0.0f;
+                  const float v = st[u2][r] * exp2_fast(fminf(al - asv[r], 0.0f));
+                  st[u2][r] = (s0 + r < l) ? v : 0.0f;
                 }
               }
             }
@@ -552,31 +588,31 @@ void scan_chunked_kernel(ScanArgs a) {
         const float ea = sm.expa[lr];
 #pragma unroll
         for (int pt = 0; pt < G::PT; ++pt)
-          sm.u.y[lr * G::LDY + 16 * pt + (lane & 15)] = yd[pt][r] + ea * yo[pt][r];
+          sm.y[lr * G::LDY + 16 * pt + (lane & 15)] = yd[pt][r] + ea * yo[pt][r];
       }
     }
     if (G::NHB == 1) __syncthreads();  // single state buffer: all reads of hb done
     if (!ywave) {
-      // ---- phases 4-5: h <- e^{A_end} h + (K_s)^T (w V), state tiles interleaved
+      // ---- phases 4-5: h <- e^{A_end} h + (w K_s)^T V, state tiles interleaved
       const float dec = sm.dec;
 #pragma unroll
-      for (int m = 0; m < G::ST; ++m)
+      for (int m = 0; m < G::HT; ++m)
 #pragma unroll
         for (int r = 0; r < 16; ++r) hacc[m][r] *= dec;
 #pragma unroll
       for (int j = 0; j < CS / G::KSTEP; ++j) {
 #pragma unroll
-        for (int m = 0; m < G::ST; ++m) {
+        for (int m = 0; m < G::HT; ++m) {
           const int z = zw + m;
           if (z < G::NB * G::PB) {
             const int nb = z / G::PB, pb = z % G::PB;
-            hacc[m] = M::mma(M::kt(sm.k, G::LDQ, 32 * nb, j * G::KSTEP, lane),
-                             M::vw(sm.vwt, sm.vt, sm.w, G::LDV, 32 * pb, j * G::KSTEP, lane), hacc[m]);
+            hacc[m] = M::mma(M::ktw(sm.k, sm.w, G::LDQ, 32 * nb, j * G::KSTEP, lane),
+                             M::vs(sm.vt, G::LDV, 32 * pb, j * G::KSTEP, lane), hacc[m]);
           }
         }
       }
 #pragma unroll
-      for (int m = 0; m < G::ST; ++m) {
+      for (int m = 0; m < G::HT; ++m) {
         const int z = zw + m;
         if (z < G::NB * G::PB) {
           const int nb = z / G::PB, pb = z % G::PB;
@@ -584,43 +620,46 @@ void scan_chunked_kernel(ScanArgs a) {
         }
       }
     }
+    __builtin_amdgcn_s_waitcnt(0);   // staged loads of this wave have landed in LDS
     __syncthreads();
 
-    // ---- phase 7: (Y + (D + QK) V) * silu(Z) -> out
+    // ================= phase 7: lane = token, (Y + (D + QK) V) * silu(Z) -> out =================
+    {
+      const float dq = Dh + (lane < CS ? sm.qk[c & 1][lane] : 0.0f);
 #pragma unroll
-    for (int i = 0; i < G::VV; ++i) {
-      const int v = tid + i * G::NT;
-      const int t = v % CS, g8 = v / CS;
-      if (g8 < P / 8 && t0 + t < L) {
-        float vf[8], zf[8], yv[8];
-        cv[i].to_f(vf);
-        cz[i].to_f(zf);
-        const float4 y0 = *reinterpret_cast<const float4*>(&sm.u.y[t * G::LDY + 8 * g8]);
-        const float4 y1 = *reinterpret_cast<const float4*>(&sm.u.y[t * G::LDY + 8 * g8 + 4]);
-        yv[0] = y0.x; yv[1] = y0.y; yv[2] = y0.z; yv[3] = y0.w;
-        yv[4] = y1.x; yv[5] = y1.y; yv[6] = y1.z; yv[7] = y1.w;
-        const float dq = Dh + sm.qk[t];
+      for (int k = 0; k < G::VGW; ++k) {
+        const int g = wave + NW * k;
+        if (g < G::VG && tok) {
+          float vf[8], zf[8], yv[8];
+          cv[k].to_f(vf);
+          Vec8<T> zv;
+          if constexpr (G::BF) zv.raw_set(staged<G::SV>(sm.rz, tl, g));
+          else zv.raw_set2(staged<G::SV>(sm.rz, tl, 2 * g), staged<G::SV>(sm.rz, tl, 2 * g + 1));
+          zv.to_f(zf);
+          const float4 y0 = *reinterpret_cast<const float4*>(&sm.y[lane * G::LDY + 8 * g]);
+          const float4 y1 = *reinterpret_cast<const float4*>(&sm.y[lane * G::LDY + 8 * g + 4]);
+          yv[0] = y0.x; yv[1] = y0.y; yv[2] = y0.z; yv[3] = y0.w;
+          yv[4] = y1.x; yv[5] = y1.y; yv[6] = y1.z; yv[7] = y1.w;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          float o = yv[q] + dq * vf[q];
-          if (has_z) o *= silu_fast(zf[q]);
-          yv[q] = o;
-        }
-        store8(gO + v_base + (long)(t0 + t) * H * P + 8 * g8, yv);
-        if (a.fin_v && t0 + t == L - 1) {
+          for (int q = 0; q < 8; ++q) {
+            float o = yv[q] + dq * vf[q];
+            if (has_z) o *= silu_fast(zf[q]);
+            yv[q] = o;
+          }
+          store8(gO + v_row + (long)(t0 + lane) * v_stride + 8 * g, yv);
+          if (a.fin_v && t0 + lane == L - 1) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) a.fin_v[(long)bh * P + 8 * g8 + q] = vf[q];
+            for (int q = 0; q < 8; ++q) a.fin_v[(long)bh * P + 8 * g + q] = vf[q];
+          }
         }
       }
     }
-    if (wave == 0 && c + 1 < nc) scalar_stage();
-    __syncthreads();
   }
 
   if (a.fin_h) {
     if (!ywave) {
 #pragma unroll
-      for (int m = 0; m < G::ST; ++m) {
+      for (int m = 0; m < G::HT; ++m) {
         const int z = zw + m;
         if (z < G::NB * G::PB) {
           const int nb = z / G::PB, pb = z % G::PB;
@@ -635,7 +674,12 @@ void scan_chunked_kernel(ScanArgs a) {
     }
     if (lane == 0) {
 #pragma unroll
-      for (int j = 0; j < G::CPW; ++j) a.fin_theta[(long)bh * R + wave * G::CPW + j] = carry[j];
+      for (int k = 0; k < G::QGW; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * (wave + NW * k) + j;
+          if (r < R) a.fin_theta[(long)bh * R + r] = carry[k][j];
+        }
     }
   }
 }
