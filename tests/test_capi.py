@@ -60,7 +60,8 @@ def test_kernel_selection(lib):
     assert f(1, 128, 64, 32, 32) == CH          # chunk 32
     assert f(0, 64, 64, 16, 64) == CH           # fp32, config 1
     assert f(0, 128, 64, 32, 64) == GEN         # fp32 with d_state 128
-    assert f(1, 128, 64, 32, 128) == GEN        # chunk 128 (no MFMA instantiation yet)
+    assert f(1, 128, 64, 32, 128) == CH         # chunk 128: 64-token sub-chunks
+    assert f(1, 128, 64, 32, 96) == GEN         # chunk 96: no instantiation
     assert f(1, 64, 16, 16, 16) == GEN          # headdim 16
     assert f(0, 4, 4, 1, 4) == GEN              # tiny model shapes
     assert f(1, 1024, 64, 0, 64) == NONE        # state too large for either kernel

@@ -48,6 +48,7 @@ F32_SHAPES = [
     (1, 1024, 4, 128, 64, 32, 64),    # reference GPU test shape (fp32, N=128)
     (2, 333, 4, 64, 32, 16, 32),
     (1, 97, 2, 32, 64, 8, 64),
+    (1, 300, 2, 64, 64, 16, 128),     # chunk 128: 64-token sub-chunks
 ]
 
 
@@ -69,6 +70,7 @@ BF16_SHAPES = [
     (1, 130, 2, 32, 32, 8, 64),
     (1, 77, 2, 128, 64, 64, 64),      # rope on every state pair (R = N/2)
     (1, 77, 2, 128, 64, 0, 64),       # no rope
+    (1, 700, 2, 128, 64, 32, 128),    # chunk 128 (config 3's): 64-token sub-chunks
 ]
 
 
