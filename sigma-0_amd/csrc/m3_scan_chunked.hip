@@ -117,8 +117,8 @@ struct Geo {
   static constexpr int VG = P / 8, VGW = (VG + NW - 1) / NW;  // V 8-column groups, per wave
   // 16-byte staging slots per row: Q/K, V, rotation rates
   static constexpr int SQ = N * TS / 16, SV = P * TS / 16, SA = R / 4 > 0 ? R / 4 : 1;
-  static constexpr int BASE = (2 * CS * LDQ + N * LDV + P * LDV) * TS + (2 * CS * SQ + CS * SV + CS * SA) * 16 +
-                              3 * (CS + 4) * 4 + 8 * N + 4 * CS * 4 + 64;
+  static constexpr int BASE = (2 * CS * LDQ + N * LDV + P * LDV) * TS + (2 * CS * SQ + CS * SV + 2 * CS * SA) * 16 +
+                              2 * 3 * (CS + 4) * 4 + 8 * N + 2 * 6 * CS * 4 + 64;
   // the gate of chunk c-1 overlaps chunk c's matrix phase when two pairs of Y tiles fit
   static constexpr bool OVL = BASE + 4 * CS * LDY * TS <= 160 * 1024 - 256;
   static constexpr int NY = OVL ? 2 : 1;
@@ -144,15 +144,21 @@ struct __attribute__((aligned(16))) Smem {
   alignas(16) uint4 rq[G::CS * G::SQ];
   alignas(16) uint4 rk[G::CS * G::SQ];
   alignas(16) uint4 rv[G::CS * G::SV];
-  alignas(16) uint4 ra[G::CS * G::SA];
-  alignas(16) float rs[3][G::CS + 4];    // adt, dt, trap of the chunk; [CS] = the next token's
+  // rotation rates and adt, dt, trap ([CS]: the next chunk's first token) of chunks
+  // c and c+1, by chunk parity: chunk c+1's angles and weights are computed during
+  // chunk c's matrix phase
+  alignas(16) uint4 ra[2][G::CS * G::SA];
+  alignas(16) float rs[2][3][G::CS + 4];
   alignas(16) float qb[G::N];            // biases of this head
   alignas(16) float kb[G::N];
-  alignas(16) float ac2[G::CS];          // A_cum * log2(e)
-  alignas(16) float g16[G::CS];          // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
-  alignas(16) float expa[G::CS];         // e^{A_cum}
-  alignas(16) float dg[G::CS];           // gamma / scale: turns the S diagonal into the QK skip weight
-  float dec;                             // e^{A_end}
+  // per-token chunk constants, by chunk parity
+  alignas(16) float ac2[2][G::CS];       // A_cum * log2(e)
+  alignas(16) float g16[2][G::CS];       // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
+  alignas(16) float expa[2][G::CS];      // e^{A_cum}
+  alignas(16) float dg[2][G::CS];        // gamma / scale: turns the S diagonal into the QK skip weight
+  alignas(16) float scl[2][G::CS];       // trapezoid key scale gamma_t + dt_{t+1} (1 - sigmoid_{t+1})
+  alignas(16) float wdec[2][G::CS];      // e^{A_end - A_cum}
+  float dec[2];                          // e^{A_end}
 };
 
 // Direct-to-LDS loads (global_load_lds): the LDS slot is M0 plus size * lane (the
@@ -264,32 +270,42 @@ void scan_chunked_kernel(ScanArgs a) {
     sm.kb[i] = a.kbias[(long)h * N + i];
   }
 
-  // ---- staging: the state waves stream a chunk's inputs into LDS
-  auto stage_main = [&](int c) {
+  // ---- staging, issued by the two lightest output waves:
+  // Q, K, V of chunk c; rotation rates and scalars of chunk c into parity c & 1
+  auto stage_qkv = [&](int c) {
     const int t0 = c * CS;
     const int valid = L - t0;
-    const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
-    const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
-    const char* v0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + v_row + (long)t0 * v_stride);
-    constexpr int JQ = CS * G::SQ / 64, JV = CS * G::SV / 64, JA = CS * G::SA / 64;
-    if (wave == G::NWY) stage_rows<CS, G::SQ, 0, JQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
-    if (wave == G::NWY + 1) stage_rows<CS, G::SQ, 0, JQ>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
-    if (wave == G::NWY + 2) {
+    constexpr int JQ = CS * G::SQ / 64, JV = CS * G::SV / 64;
+    if (wave == 0) {
+      const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
+      stage_rows<CS, G::SQ, 0, JQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
+    }
+    if (wave == 1) {
+      const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
+      stage_rows<CS, G::SQ, 0, JQ>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
+    }
+    if (wave == 0) {
+      const char* v0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + v_row + (long)t0 * v_stride);
       stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv, v0, v_stride * G::TS, valid, lane);
+    }
+  };
+  auto stage_ars = [&](int c) {
+    const int t0 = c * CS;
+    const int valid = L - t0;
+    constexpr int JA = CS * G::SA / 64;
+    if (wave == 1) {
       if (R > 0) {
         const char* a0 = reinterpret_cast<const char*>(a.ang + a_row + (long)t0 * a_stride);
-        stage_rows<CS, G::SA, 0, JA>((lds_uint4*)sm.ra, a0, a_stride * 4, valid, lane);
+        stage_rows<CS, G::SA, 0, JA>((lds_uint4*)sm.ra[c & 1], a0, a_stride * 4, valid, lane);
       }
-    }
-    if (wave == G::NWY + 3) {
       if (lane < CS && lane < valid) {
-        lds_dma4(gadt + t0 + lane, (lds_float*)&sm.rs[0][0]);
-        lds_dma4(gdt + t0 + lane, (lds_float*)&sm.rs[1][0]);
-        lds_dma4(gtr + t0 + lane, (lds_float*)&sm.rs[2][0]);
+        lds_dma4(gadt + t0 + lane, (lds_float*)&sm.rs[c & 1][0][0]);
+        lds_dma4(gdt + t0 + lane, (lds_float*)&sm.rs[c & 1][1][0]);
+        lds_dma4(gtr + t0 + lane, (lds_float*)&sm.rs[c & 1][2][0]);
       }
       if (lane == 0 && t0 + CS < L) {
-        lds_dma4(gdt + t0 + CS, (lds_float*)&sm.rs[1][CS]);
-        lds_dma4(gtr + t0 + CS, (lds_float*)&sm.rs[2][CS]);
+        lds_dma4(gdt + t0 + CS, (lds_float*)&sm.rs[c & 1][1][CS]);
+        lds_dma4(gtr + t0 + CS, (lds_float*)&sm.rs[c & 1][2][CS]);
       }
     }
   };
@@ -358,12 +374,68 @@ void scan_chunked_kernel(ScanArgs a) {
   // staging never holds uninitialised bits: rows past the sequence end are not loaded
   for (int i = tid; i < G::CS * G::SQ; i += G::NT) { sm.rq[i] = make_uint4(0, 0, 0, 0); sm.rk[i] = sm.rq[i]; }
   for (int i = tid; i < G::CS * G::SV; i += G::NT) sm.rv[i] = make_uint4(0, 0, 0, 0);
-  for (int i = tid; i < G::CS * G::SA; i += G::NT) sm.ra[i] = make_uint4(0, 0, 0, 0);
-  for (int i = tid; i < 3 * (G::CS + 4); i += G::NT) ((lds_float*)&sm.rs[0][0])[i] = 0.0f;
+  for (int i = tid; i < 2 * G::CS * G::SA; i += G::NT) (&sm.ra[0][0])[i] = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < 2 * 3 * (G::CS + 4); i += G::NT) (&sm.rs[0][0][0])[i] = 0.0f;
+
+  // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
+  // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
+  // the angles of its own rope pairs in registers.
+  constexpr int kScalarWave = 2;
+  float p_cs[G::QGW][4], p_sn[G::QGW][4];
+  auto pre = [&](int cc) {
+    const int t0 = cc * CS;
+    const int pb = cc & 1;
+    const bool tok = lane < CS && t0 + lane < L;
+    const int tl = lane < CS ? lane : 0;
+    const float s_dt = tok ? sm.rs[pb][1][tl] : 0.0f;
+    if (wave == kScalarWave) {
+      const float s_adt = tok ? sm.rs[pb][0][tl] : 0.0f;
+      const float s_tr = tok ? sm.rs[pb][2][tl] : 0.0f;
+      const float sig = sigmoid_fast(s_tr);
+      const float gam = s_dt * sig;
+      const float u = s_dt * (1.0f - sig);                                 // dt (1 - sigmoid), this token
+      float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // next token
+      if (lane == CS - 1) un = (t0 + CS < L) ? sm.rs[pb][1][CS] * (1.0f - sigmoid_fast(sm.rs[pb][2][CS])) : 0.0f;
+      const float scl = gam + un;
+      const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
+      const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
+      if (lane < CS) {
+        const float ablk = __shfl(acum, lane | 15, 64);
+        sm.scl[pb][lane] = scl;
+        sm.wdec[pb][lane] = exp2_fast((aend - acum) * kLog2e);
+        sm.ac2[pb][lane] = acum * kLog2e;
+        sm.expa[pb][lane] = exp2_fast(acum * kLog2e);
+        sm.g16[pb][lane] = exp2_fast((ablk - acum) * kLog2e);
+        sm.dg[pb][lane] = scl != 0.0f ? gam * rcp_fast(scl) : 0.0f;
+        if (lane == 0) sm.dec[pb] = exp2_fast(aend * kLog2e);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < G::QGW; ++k) {
+      const int g = wave + NW * k;
+      if (g < G::QG && 4 * g < R) {
+        const uint4 rr = staged<G::SA>(sm.ra[pb], tl, g);
+        const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
+                              __uint_as_float(rr.w)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // theta = carry + prefix of tanh(rate) pi dt over the chunk, mod 2pi
+          const float d = tok ? tanh_fast(rav[j]) * kPi * s_dt : 0.0f;
+          const float th = wrap_2pi(carry[k][j] + wave_incl_scan(d));
+          carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
+          sincos_wrapped(th, &p_cs[k][j], &p_sn[k][j]);
+        }
+      }
+    }
+  };
+
   __syncthreads();
-  stage_main(0);
+  stage_qkv(0);
+  stage_ars(0);
+  if (nc > 1) stage_ars(1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  pre(0);
 
   for (int c = 0; c < nc; ++c) {
     const int t0 = c * CS;
@@ -373,26 +445,7 @@ void scan_chunked_kernel(ScanArgs a) {
     // ================= preparation: lane = token =================
     // Rows past the sequence end hold stale (finite) inputs: their key scale is 0,
     // so they add nothing to S or h, and their outputs are never stored.
-    const float s_adt = tok ? sm.rs[0][tl] : 0.0f;
-    const float s_dt = tok ? sm.rs[1][tl] : 0.0f;
-    const float s_tr = tok ? sm.rs[2][tl] : 0.0f;
-    const float sig = sigmoid_fast(s_tr);
-    const float gam = s_dt * sig;
-    const float u = s_dt * (1.0f - sig);                                   // dt (1 - sigmoid), this token
-    float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // next token
-    if (lane == CS - 1) un = (t0 + CS < L) ? sm.rs[1][CS] * (1.0f - sigmoid_fast(sm.rs[2][CS])) : 0.0f;
-    const float scl = gam + un;
-    const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
-    const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
-    const float wdec = exp2_fast((aend - acum) * kLog2e);               // e^{A_end - A_cum}
-    if (wave == 0 && lane < CS) {
-      const float ablk = __shfl(acum, lane | 15, 64);
-      sm.ac2[lane] = acum * kLog2e;
-      sm.expa[lane] = exp2_fast(acum * kLog2e);
-      sm.g16[lane] = exp2_fast((ablk - acum) * kLog2e);
-      sm.dg[lane] = scl != 0.0f ? gam * rcp_fast(scl) : 0.0f;
-      if (lane == 0) sm.dec = exp2_fast(aend * kLog2e);
-    }
+    const float scl = sm.scl[c & 1][tl], wdec = sm.wdec[c & 1][tl];
     // Q/K column groups: rotation angles, biases, rope, key scale
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
@@ -424,17 +477,9 @@ void scan_chunked_kernel(ScanArgs a) {
           }
         }
         if (4 * g < R) {
-          const uint4 rr = staged<G::SA>(sm.ra, tl, g);
-          const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
-                                __uint_as_float(rr.w)};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            // theta = carry + prefix of tanh(rate) pi dt over the chunk, mod 2pi
-            const float d = tok ? tanh_fast(rav[j]) * kPi * s_dt : 0.0f;
-            const float th = wrap_2pi(carry[k][j] + wave_incl_scan(d));
-            carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
-            float cs, sn;
-            sincos_wrapped(th, &cs, &sn);
+            const float cs = p_cs[k][j], sn = p_sn[k][j];
             const float q0 = qf[2 * j], q1 = qf[2 * j + 1];
             qf[2 * j] = q0 * cs - q1 * sn;
             qf[2 * j + 1] = q0 * sn + q1 * cs;
@@ -485,11 +530,16 @@ void scan_chunked_kernel(ScanArgs a) {
     // Z of the chunk waiting for its gate has landed (it was loaded a chunk ago); this
     // wait keeps the compiler from waiting on the direct-to-LDS loads issued next
     if (G::OVL) __builtin_amdgcn_s_waitcnt(0);
-    // ---- inputs of the next chunk go in flight (this chunk's staging is consumed)
-    if (c + 1 < nc) stage_main(c + 1);
+    // ---- inputs of the next chunks go in flight (this chunk's Q/K/V staging is consumed)
+    if (c + 1 < nc) stage_qkv(c + 1);
+    if (c + 2 < nc) stage_ars(c + 2);
     // ---- gate of the previous chunk, under this chunk's matrix work
     if (G::OVL && c > 0) gate(c - 1);
+    // ---- next chunk's constants and rotations: state waves before their matrix work,
+    // output waves after it, so each SIMD pairs VALU work with matrix work
+    if (!ywave && c + 1 < nc) pre(c + 1);
 
+    const int pc = c & 1;
     T* ydst = sm.yd[c % G::NY];
     T* yodst = sm.yo[c % G::NY];
     if (ywave) {
@@ -498,8 +548,8 @@ void scan_chunked_kernel(ScanArgs a) {
         //   Y_diag = mask(K_s Q_r^T)^T V, the mask's diagonal carrying D + gamma QK
         const int lb = wave;
         const int l = 16 * lb + (lane & 15);
-        const float al = sm.ac2[l];
-        const float dgl = sm.dg[l];
+        const float al = sm.ac2[pc][l];
+        const float dgl = sm.dg[pc][l];
         f32x4 yd[G::PT];
 #pragma unroll
         for (int pt = 0; pt < G::PT; ++pt)
@@ -522,13 +572,13 @@ void scan_chunked_kernel(ScanArgs a) {
                 const int s0 = 16 * sb + g4;
                 if (sb < lb) {
                   // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
-                  const float f = exp2_fast(fminf(al - sm.ac2[16 * sb + 15], 0.0f));
-                  const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[s0]);
+                  const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
+                  const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
                   st[u2][0] *= f * gg.x; st[u2][1] *= f * gg.y; st[u2][2] *= f * gg.z; st[u2][3] *= f * gg.w;
                 } else {
                   // diagonal block: causal decay below the diagonal; on it, D plus the
                   // QK skip gamma_l (q_l . k_l) (the stored key carries the scale)
-                  const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[s0]);
+                  const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
                   const float asv[4] = {as.x, as.y, as.z, as.w};
 #pragma unroll
                   for (int r = 0; r < 4; ++r) {
@@ -573,13 +623,13 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) yo = W::mma(sm.q[l * G::LDQ + 16 * nb + g4 + r], hs[nb][r], yo);
         }
-        const float4 ea = *reinterpret_cast<const float4*>(&sm.expa[16 * lb + g4]);
+        const float4 ea = *reinterpret_cast<const float4*>(&sm.expa[pc][16 * lb + g4]);
         const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) yodst[(16 * lb + g4 + r) * G::LDY + pcol] = Elem<T>::from_f(eav[r] * yo[r]);
       }
       // ---- phases 4-5: h <- e^{A_end} h + (w K_s)^T V for my p-tile
-      const float dec = sm.dec;
+      const float dec = sm.dec[pc];
 #pragma unroll
       for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
@@ -592,6 +642,7 @@ void scan_chunked_kernel(ScanArgs a) {
           hs[nb] = W::mma(W::ld(sm.kwt, G::LDV, 16 * nb, ks * W::KSTEP, lane), vb, hs[nb]);
       }
     }
+    if (ywave && c + 1 < nc) pre(c + 1);
     __builtin_amdgcn_s_waitcnt(0);   // staged loads and gate stores of this wave are done
     if (G::OVL) load_z(c);           // Z for this chunk's gate, one chunk ahead
     __syncthreads();
@@ -624,21 +675,25 @@ void scan_chunked_kernel(ScanArgs a) {
 // model's rope_fraction 0.5 (R = N/4) or 1.0 (R = N/2) width, or 0.
 #define M3_CHUNK_SHAPES(X)                                                                         \
   X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0)                        \
-  X(bf16, 64, 128, 32, 32) X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 64, 32) \
+  X(bf16, 64, 128, 32, 32) X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 64, 32)                         \
   X(bf16, 64, 64, 32, 16) X(bf16, 64, 32, 32, 8) X(bf16, 64, 32, 64, 8)                            \
   X(bf16, 32, 128, 64, 32) X(bf16, 32, 64, 64, 16) X(bf16, 32, 64, 32, 16) X(bf16, 32, 128, 32, 32) \
-  X(float, 64, 64, 64, 16) X(float, 64, 64, 64, 32) X(float, 64, 64, 32, 16) X(float, 32, 64, 64, 16) \
-  X(float, 32, 64, 32, 16) X(float, 64, 32, 32, 8) X(float, 64, 32, 64, 8)
+  X(float, 32, 64, 64, 16) X(float, 32, 64, 64, 32) X(float, 32, 64, 32, 16) X(float, 32, 32, 32, 8) \
+  X(float, 32, 32, 64, 8)
 
 constexpr int kChunkWaves = 8;
 
-// Chunk sizes above 64 that are multiples of 64 run as 64-token sub-chunks: the
-// chunked form is an exact rewrite of the token recurrence for every chunk size, so
-// the blocking changes only the rounding, not the function computed.
-static int kernel_chunk(int CS) { return (CS > 64 && CS % 64 == 0) ? 64 : CS; }
+// The chunked form is an exact rewrite of the token recurrence for every chunk size,
+// so the kernel's blocking changes only the rounding, not the function computed:
+// bf16 runs chunk sizes that are multiples of 64 as 64-token sub-chunks, fp32 (twice
+// the LDS per token) multiples of 32 as 32-token sub-chunks.
+static int kernel_chunk(bool bf16_io, int CS) {
+  const int k = bf16_io ? 64 : 32;
+  return (CS > k && CS % k == 0) ? k : CS;
+}
 
 bool scan_chunked_supported(bool bf16_io, int CS_, int N, int P, int R) {
-  const int CS = kernel_chunk(CS_);
+  const int CS = kernel_chunk(bf16_io, CS_);
 #define X(T, cs, n, p, r) \
   if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && N == n && P == p && R == r) return true;
   M3_CHUNK_SHAPES(X)
@@ -647,7 +702,7 @@ bool scan_chunked_supported(bool bf16_io, int CS_, int N, int P, int R) {
 }
 
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
-  const int CS = kernel_chunk(a.CS);
+  const int CS = kernel_chunk(bf16_io, a.CS);
 #define X(T, cs, n, p, r)                                                                            \
   if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && a.N == n && a.P == p && a.R == r) {   \
     hipLaunchKernelGGL((scan_chunked_kernel<T, cs, n, p, r, kChunkWaves>), dim3(a.B * a.H),          \
