@@ -236,6 +236,18 @@ __device__ __forceinline__ void load4(const float* p, float* f) {
   f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
 }
 
+// Two values to two 16-bit (or 32-bit) slots: one packed conversion, then the low and
+// high halves written separately.
+__device__ __forceinline__ void store_pair(bf16* p0, bf16* p1, float a, float b) {
+  const bf16x2 v = {(bf16)a, (bf16)b};
+  *p0 = v[0];
+  *p1 = v[1];
+}
+__device__ __forceinline__ void store_pair(float* p0, float* p1, float a, float b) {
+  *p0 = a;
+  *p1 = b;
+}
+
 template <typename T, int CS, int N, int P, int R, int NW>
 __global__ __launch_bounds__(64 * NW, 1)
 void scan_chunked_kernel(ScanArgs a) {
@@ -369,7 +381,7 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = 4 * (wave + NW * k) + j;
-      carry[k][j] = (a.init_theta && r < R) ? a.init_theta[(long)bh * R + r] : 0.0f;
+      carry[k][j] = (a.init_theta && r < R) ? a.init_theta[(long)bh * R + r] * kInvTwoPi : 0.0f;  // revolutions
     }
   // staging never holds uninitialised bits: rows past the sequence end are not loaded
   for (int i = tid; i < G::CS * G::SQ; i += G::NT) { sm.rq[i] = make_uint4(0, 0, 0, 0); sm.rk[i] = sm.rq[i]; }
@@ -417,13 +429,18 @@ void scan_chunked_kernel(ScanArgs a) {
         const uint4 rr = staged<G::SA>(sm.ra[pb], tl, g);
         const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
                               __uint_as_float(rr.w)};
+        const float hdt = 0.5f * s_dt;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          // theta = carry + prefix of tanh(rate) pi dt over the chunk, mod 2pi
-          const float d = tok ? tanh_fast(rav[j]) * kPi * s_dt : 0.0f;
-          const float th = wrap_2pi(carry[k][j] + wave_incl_scan(d));
+          // angle in revolutions: carry + prefix of tanh(rate) pi dt / 2pi = tanh(rate) dt / 2,
+          // with tanh(x) = 1 - 2 / (1 + e^{2x}); the fractional part is the reference's
+          // mod-2pi wrap, and the hardware sin/cos take revolutions
+          const float rcp = rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j]));
+          const float d = tok ? fmaf(-s_dt, rcp, hdt) : 0.0f;
+          const float th = __builtin_amdgcn_fractf(carry[k][j] + wave_incl_scan(d));
           carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
-          sincos_wrapped(th, &p_cs[k][j], &p_sn[k][j]);
+          p_cs[k][j] = __builtin_amdgcn_cosf(th);
+          p_sn[k][j] = __builtin_amdgcn_sinf(th);
         }
       }
     }
@@ -500,7 +517,9 @@ void scan_chunked_kernel(ScanArgs a) {
           store4(&sm.k[lane * G::LDQ + W::qpos(8 * g)], kf);
           store4(&sm.k[lane * G::LDQ + W::qpos(8 * g + 4)], kf + 4);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sm.kwt[(8 * g + e) * G::LDV + lane] = Elem<T>::from_f(kf[e] * wdec);
+          for (int e = 0; e < 8; e += 2)
+            store_pair(&sm.kwt[(8 * g + e) * G::LDV + lane], &sm.kwt[(8 * g + e + 1) * G::LDV + lane], kf[e] * wdec,
+                       kf[e + 1] * wdec);
         }
       }
     }
@@ -516,7 +535,8 @@ void scan_chunked_kernel(ScanArgs a) {
         vv.to_f(vf);
         if (lane < CS) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) sm.vt[(8 * g + q) * G::LDV + lane] = Elem<T>::from_f(vf[q]);
+          for (int q = 0; q < 8; q += 2)
+            store_pair(&sm.vt[(8 * g + q) * G::LDV + lane], &sm.vt[(8 * g + q + 1) * G::LDV + lane], vf[q], vf[q + 1]);
         }
         if (a.fin_v && tok && t0 + lane == L - 1) {
 #pragma unroll
@@ -600,8 +620,9 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
         for (int pt = 0; pt < G::PT; ++pt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            ydst[(16 * lb + g4 + r) * G::LDY + 16 * pt + (lane & 15)] = Elem<T>::from_f(yd[pt][r]);
+          for (int r = 0; r < 4; r += 2)
+            store_pair(&ydst[(16 * lb + g4 + r) * G::LDY + 16 * pt + (lane & 15)],
+                       &ydst[(16 * lb + g4 + r + 1) * G::LDY + 16 * pt + (lane & 15)], yd[pt][r], yd[pt][r + 1]);
       }
     } else {
       // ---- phase 6: Y_off = e^{A_cum} Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
@@ -626,7 +647,9 @@ void scan_chunked_kernel(ScanArgs a) {
         const float4 ea = *reinterpret_cast<const float4*>(&sm.expa[pc][16 * lb + g4]);
         const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) yodst[(16 * lb + g4 + r) * G::LDY + pcol] = Elem<T>::from_f(eav[r] * yo[r]);
+        for (int r = 0; r < 4; r += 2)
+          store_pair(&yodst[(16 * lb + g4 + r) * G::LDY + pcol], &yodst[(16 * lb + g4 + r + 1) * G::LDY + pcol],
+                     eav[r] * yo[r], eav[r + 1] * yo[r + 1]);
       }
       // ---- phases 4-5: h <- e^{A_end} h + (w K_s)^T V for my p-tile
       const float dec = sm.dec[pc];
@@ -665,7 +688,7 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * (wave + NW * k) + j;
-        if (r < R) a.fin_theta[(long)bh * R + r] = carry[k][j];
+        if (r < R) a.fin_theta[(long)bh * R + r] = carry[k][j] * kTwoPi;
       }
   }
 }
