@@ -392,7 +392,7 @@ void scan_chunked_kernel(ScanArgs a) {
   // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
   // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
   // the angles of its own rope pairs in registers.
-  constexpr int kScalarWave = 2;
+  constexpr int kScalarWave = 0;
   float p_cs[G::QGW][4], p_sn[G::QGW][4];
   auto pre = [&](int cc) {
     const int t0 = cc * CS;
@@ -631,25 +631,43 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
         for (int q = 0; q < N / 32; ++q) hf[q] = W::hfrag(hs[2 * q], hs[2 * q + 1]);
       }
+      constexpr int NLB = G::LB16 / G::SPT;
+      f32x4 yo[NLB];
 #pragma unroll
-      for (int lb = part; lb < G::LB16; lb += G::SPT) {
-        f32x4 yo = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (G::BF) {
+      for (int i = 0; i < NLB; ++i)
 #pragma unroll
-          for (int q = 0; q < N / 32; ++q) yo = W::mma(W::ld(sm.q, G::LDQ, 16 * lb, 32 * q, lane), hf[q], yo);
-        } else {
-          const int l = 16 * lb + (lane & 15);
+        for (int r = 0; r < 4; ++r) yo[i][r] = 0.0f;
+      if constexpr (G::BF) {
+        // all query fragments first, then the query blocks' chains side by side
+        typename W::frag qa[NLB][N / 32];
 #pragma unroll
-          for (int nb = 0; nb < G::NB16; ++nb)
+        for (int i = 0; i < NLB; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) yo = W::mma(sm.q[l * G::LDQ + 16 * nb + g4 + r], hs[nb][r], yo);
-        }
+          for (int q = 0; q < N / 32; ++q) qa[i][q] = W::ld(sm.q, G::LDQ, 16 * (part + G::SPT * i), 32 * q, lane);
+#pragma unroll
+        for (int q = 0; q < N / 32; ++q)
+#pragma unroll
+          for (int i = 0; i < NLB; ++i) yo[i] = W::mma(qa[i][q], hf[q], yo[i]);
+      } else {
+#pragma unroll
+        for (int nb = 0; nb < G::NB16; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < NLB; ++i) {
+              const int l = 16 * (part + G::SPT * i) + (lane & 15);
+              yo[i] = W::mma(sm.q[l * G::LDQ + 16 * nb + g4 + r], hs[nb][r], yo[i]);
+            }
+      }
+#pragma unroll
+      for (int i = 0; i < NLB; ++i) {
+        const int lb = part + G::SPT * i;
         const float4 ea = *reinterpret_cast<const float4*>(&sm.expa[pc][16 * lb + g4]);
         const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
           store_pair(&yodst[(16 * lb + g4 + r) * G::LDY + pcol], &yodst[(16 * lb + g4 + r + 1) * G::LDY + pcol],
-                     eav[r] * yo[r], eav[r + 1] * yo[r + 1]);
+                     eav[r] * yo[i][r], eav[r + 1] * yo[i][r + 1]);
       }
       // ---- phases 4-5: h <- e^{A_end} h + (w K_s)^T V for my p-tile
       const float dec = sm.dec[pc];
