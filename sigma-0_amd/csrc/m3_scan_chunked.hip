@@ -562,67 +562,78 @@ void scan_chunked_kernel(ScanArgs a) {
     const int pc = c & 1;
     T* ydst = sm.yd[c % G::NY];
     T* yodst = sm.yo[c % G::NY];
-    if (ywave) {
-      if (wave < G::LB16) {
-        // ---- phase 3 for query rows l in [16 lb, 16 lb + 16), all p-tiles:
-        //   Y_diag = mask(K_s Q_r^T)^T V, the mask's diagonal carrying D + gamma QK
-        const int lb = wave;
-        const int l = 16 * lb + (lane & 15);
-        const float al = sm.ac2[pc][l];
-        const float dgl = sm.dg[pc][l];
-        f32x4 yd[G::PT];
+    // ---- phase 3 for query rows l in [16 lb, 16 lb + 16), all p-tiles (output wave lb):
+    //   Y_diag = mask(K_s Q_r^T)^T V, the mask's diagonal carrying D + gamma QK.
+    // Instantiated per query block so every loop over key blocks is static.
+    auto out_block = [&](auto lb_c) {
+      constexpr int lb = decltype(lb_c)::value;
+      const int l = 16 * lb + (lane & 15);
+      const float al = sm.ac2[pc][l];
+      const float dgl = sm.dg[pc][l];
+      constexpr int NK = N / W::KSTEP;
+      // query fragments first (B operand of every S^T block), then the key blocks'
+      // chains side by side
+      typename W::frag qf[NK];
 #pragma unroll
-        for (int pt = 0; pt < G::PT; ++pt)
+      for (int kk = 0; kk < NK; ++kk) qf[kk] = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, lane);
+      f32x4 st[lb + 2];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) yd[pt][r] = 0.0f;
+      for (int sb = 0; sb < lb + 2; ++sb)
 #pragma unroll
-        for (int sp = 0; sp < G::LB16; sp += 2) {
-          if (sp <= lb) {
-            f32x4 st[2];
+        for (int r = 0; r < 4; ++r) st[sb][r] = 0.0f;
 #pragma unroll
-            for (int u2 = 0; u2 < 2; ++u2) {
-              const int sb = sp + u2;
+      for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
-              for (int r = 0; r < 4; ++r) st[u2][r] = 0.0f;
-              if (sb <= lb) {
+        for (int sb = 0; sb <= lb; ++sb)
+          st[sb] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, lane), qf[kk], st[sb]);
 #pragma unroll
-                for (int kk = 0; kk < N / W::KSTEP; ++kk)
-                  st[u2] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, lane),
-                                  W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, lane), st[u2]);
-                const int s0 = 16 * sb + g4;
-                if (sb < lb) {
-                  // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
-                  const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
-                  const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
-                  st[u2][0] *= f * gg.x; st[u2][1] *= f * gg.y; st[u2][2] *= f * gg.z; st[u2][3] *= f * gg.w;
-                } else {
-                  // diagonal block: causal decay below the diagonal; on it, D plus the
-                  // QK skip gamma_l (q_l . k_l) (the stored key carries the scale)
-                  const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
-                  const float asv[4] = {as.x, as.y, as.z, as.w};
+      for (int sb = 0; sb <= lb; ++sb) {
+        const int s0 = 16 * sb + g4;
+        if (sb < lb) {
+          // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
+          const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
+          const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
+          st[sb][0] *= f * gg.x; st[sb][1] *= f * gg.y; st[sb][2] *= f * gg.z; st[sb][3] *= f * gg.w;
+        } else {
+          // diagonal block: causal decay below the diagonal; on it, D plus the
+          // QK skip gamma_l (q_l . k_l) (the stored key carries the scale)
+          const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
+          const float asv[4] = {as.x, as.y, as.z, as.w};
 #pragma unroll
-                  for (int r = 0; r < 4; ++r) {
-                    const float v = st[u2][r] * exp2_fast(fminf(al - asv[r], 0.0f));
-                    st[u2][r] = (s0 + r < l) ? v : (s0 + r == l ? Dh + st[u2][r] * dgl : 0.0f);
-                  }
-                }
-              }
-            }
-#pragma unroll
-            for (int j = 0; j < W::STEPS; ++j) {
-              const typename W::frag mf = W::from_acc(st[0], st[1], j);
-#pragma unroll
-              for (int pt = 0; pt < G::PT; ++pt)
-                yd[pt] = W::mma(mf, W::vperm(sm.vt, G::LDV, 16 * pt, 16 * sp, j, lane), yd[pt]);
-            }
+          for (int r = 0; r < 4; ++r) {
+            const float v = st[sb][r] * exp2_fast(fminf(al - asv[r], 0.0f));
+            st[sb][r] = (s0 + r < l) ? v : (s0 + r == l ? Dh + st[sb][r] * dgl : 0.0f);
           }
         }
+      }
+      f32x4 yd[G::PT];
 #pragma unroll
-        for (int pt = 0; pt < G::PT; ++pt)
+      for (int pt = 0; pt < G::PT; ++pt)
 #pragma unroll
-          for (int r = 0; r < 4; r += 2)
-            store_pair(&ydst[(16 * lb + g4 + r) * G::LDY + 16 * pt + (lane & 15)],
-                       &ydst[(16 * lb + g4 + r + 1) * G::LDY + 16 * pt + (lane & 15)], yd[pt][r], yd[pt][r + 1]);
+        for (int r = 0; r < 4; ++r) yd[pt][r] = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp <= lb; sp += 2) {
+#pragma unroll
+        for (int j = 0; j < W::STEPS; ++j) {
+          const typename W::frag mf = W::from_acc(st[sp], st[sp + 1], j);
+#pragma unroll
+          for (int pt = 0; pt < G::PT; ++pt)
+            yd[pt] = W::mma(mf, W::vperm(sm.vt, G::LDV, 16 * pt, 16 * sp, j, lane), yd[pt]);
+        }
+      }
+#pragma unroll
+      for (int pt = 0; pt < G::PT; ++pt)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2)
+          store_pair(&ydst[(16 * lb + g4 + r) * G::LDY + 16 * pt + (lane & 15)],
+                     &ydst[(16 * lb + g4 + r + 1) * G::LDY + 16 * pt + (lane & 15)], yd[pt][r], yd[pt][r + 1]);
+    };
+    if (ywave) {
+      if (wave == 0) out_block(std::integral_constant<int, 0>{});
+      if (wave == 1) out_block(std::integral_constant<int, 1>{});
+      if constexpr (G::LB16 > 2) {
+        if (wave == 2) out_block(std::integral_constant<int, 2>{});
+        if (wave == 3) out_block(std::integral_constant<int, 3>{});
       }
     } else {
       // ---- phase 6: Y_off = e^{A_cum} Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
