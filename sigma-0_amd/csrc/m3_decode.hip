@@ -14,11 +14,13 @@
 // input dtype, adt/dt/trap (B,H) f32 with trap post-sigmoid, angle (B,H,R) f32,
 // B_bias/C_bias (H,N) f32, D (H,) f32, y (B,H,P) in the output dtype.
 //
-// One 256-thread workgroup per (b, h).  The P*N fp32 state is streamed as
+// One 512-thread workgroup per (b, h).  The P*N fp32 state is streamed as
 // float4 with consecutive threads on consecutive 16-byte words, so each wave
-// reads and writes whole 1 KiB spans; those loads are issued before the small
-// per-head preamble (angles, rope, carries) so HBM latency overlaps it.  The
-// output dot C_rot . h reduces over the N/4 lanes holding one state row.
+// reads and writes whole 1 KiB spans, with non-temporal loads and stores (the
+// state is touched once per step and is larger than the caches); those loads are
+// issued before the small per-head preamble (angles, rope, carries) so HBM
+// latency overlaps it.  The output dot C_rot . h reduces over the N/4 lanes
+// holding one state row.
 #include "m3_scan.h"
 
 namespace m3 {
@@ -30,7 +32,7 @@ __device__ __forceinline__ float ld_f(const void* p, long i) {
   return Elem<T>::to_f(reinterpret_cast<const T*>(p)[i]);
 }
 
-constexpr int kDecThreads = 256;
+constexpr int kDecThreads = 512;
 constexpr int kDecMaxP = 256;
 constexpr int kDecMaxN = 256;
 
@@ -51,12 +53,12 @@ void decode_step_kernel(DecodeArgs a) {
   __shared__ float sQK;
 
   // 1. issue the state loads first
-  float4* hrow = reinterpret_cast<float4*>(a.h + (long)bh * P * N);
-  float4 hv[MAXV];
+  f32x4* hrow = reinterpret_cast<f32x4*>(a.h + (long)bh * P * N);
+  f32x4 hv[MAXV];
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     const int v = tid + i * kDecThreads;
-    if (v < nvec) hv[i] = hrow[v];
+    if (v < nvec) hv[i] = __builtin_nontemporal_load(hrow + v);
   }
 
   // 2. preamble: carries and step inputs into LDS, angle update
@@ -123,17 +125,16 @@ void decode_step_kernel(DecodeArgs a) {
       p = v / ROWL;
       const int n = (v % ROWL) * 4;
       const float vp = sVp[p], xp = sX[p];
-      float4 hn = hv[i];
-      float* hc = reinterpret_cast<float*>(&hn);
+      f32x4 hn = hv[i];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float t = dec * hc[q];
+        float t = dec * hn[q];
         t = t + c_prev * (vp * sKp[n + q]);
         t = t + c_cur * (xp * sB[n + q]);
-        hc[q] = t;
+        hn[q] = t;
         part += sC[n + q] * t;
       }
-      hrow[v] = hn;
+      __builtin_nontemporal_store(hn, hrow + v);
     }
     part = group_sum<ROWL>(part);
     if (v < nvec && (v % ROWL) == 0) sY[p] = part;
