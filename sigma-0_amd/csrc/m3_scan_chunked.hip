@@ -172,11 +172,12 @@ typedef __attribute__((address_space(3))) uint4 lds_uint4;
 typedef __attribute__((address_space(3))) float lds_float;
 __device__ __forceinline__ uint32_t lds_addr(const lds_uint4* p) { return (uint32_t)(uintptr_t)p; }
 __device__ __forceinline__ uint32_t lds_addr(const lds_float* p) { return (uint32_t)(uintptr_t)p; }
-__device__ __forceinline__ void lds_dma16(const void* g, lds_uint4* l) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds_addr(l)) : "memory");
+// Address = wave-uniform base (SGPRs) + 32-bit lane offset.
+__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, lds_uint4* l) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
 }
-__device__ __forceinline__ void lds_dma4(const void* g, lds_float* l) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(g), "{m0}"(lds_addr(l)) : "memory");
+__device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, lds_float* l) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
 }
 
 // Direct-to-LDS staging of instructions [J0, J1) of CS rows x S 16-byte slots.
@@ -205,12 +206,12 @@ __device__ __forceinline__ void stage_rows(lds_uint4* dst, const char* src, long
   if (rows_valid >= CS) {
 #pragma unroll
     for (int j = J0; j < J1; ++j)
-      lds_dma16(base + (long)(j / PER) * (PER * RP) * stride + off[j % PER], dst + 64 * j);
+      lds_dma16(base + (long)(j / PER) * (PER * RP) * stride, off[j % PER], dst + 64 * j);
   } else {
 #pragma unroll
     for (int j = J0; j < J1; ++j)
       if (j * RP + lrow < rows_valid)
-        lds_dma16(base + (long)(j / PER) * (PER * RP) * stride + off[j % PER], dst + 64 * j);
+        lds_dma16(base + (long)(j / PER) * (PER * RP) * stride, off[j % PER], dst + 64 * j);
   }
 }
 template <int S>
@@ -282,21 +283,20 @@ void scan_chunked_kernel(ScanArgs a) {
     sm.kb[i] = a.kbias[(long)h * N + i];
   }
 
-  // ---- staging, issued by the two lightest output waves:
+  // ---- staging, spread over the waves with the most slack in the matrix phase:
   // Q, K, V of chunk c; rotation rates and scalars of chunk c into parity c & 1
+  constexpr int kWQ0 = 2, kWQ1 = 4, kWK0 = 6, kWK1 = 7, kWV = 0, kWA = 5;
   auto stage_qkv = [&](int c) {
     const int t0 = c * CS;
     const int valid = L - t0;
     constexpr int JQ = CS * G::SQ / 64, JV = CS * G::SV / 64;
-    if (wave == 0) {
-      const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
-      stage_rows<CS, G::SQ, 0, JQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
-    }
-    if (wave == 1) {
-      const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
-      stage_rows<CS, G::SQ, 0, JQ>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
-    }
-    if (wave == 0) {
+    const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
+    const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
+    if (wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
+    if (wave == kWQ1) stage_rows<CS, G::SQ, JQ / 2, JQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
+    if (wave == kWK0) stage_rows<CS, G::SQ, 0, JQ / 2>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
+    if (wave == kWK1) stage_rows<CS, G::SQ, JQ / 2, JQ>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
+    if (wave == kWV) {
       const char* v0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + v_row + (long)t0 * v_stride);
       stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv, v0, v_stride * G::TS, valid, lane);
     }
@@ -305,19 +305,19 @@ void scan_chunked_kernel(ScanArgs a) {
     const int t0 = c * CS;
     const int valid = L - t0;
     constexpr int JA = CS * G::SA / 64;
-    if (wave == 1) {
+    if (wave == kWA) {
       if (R > 0) {
         const char* a0 = reinterpret_cast<const char*>(a.ang + a_row + (long)t0 * a_stride);
         stage_rows<CS, G::SA, 0, JA>((lds_uint4*)sm.ra[c & 1], a0, a_stride * 4, valid, lane);
       }
       if (lane < CS && lane < valid) {
-        lds_dma4(gadt + t0 + lane, (lds_float*)&sm.rs[c & 1][0][0]);
-        lds_dma4(gdt + t0 + lane, (lds_float*)&sm.rs[c & 1][1][0]);
-        lds_dma4(gtr + t0 + lane, (lds_float*)&sm.rs[c & 1][2][0]);
+        lds_dma4(gadt + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][0][0]);
+        lds_dma4(gdt + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][1][0]);
+        lds_dma4(gtr + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][2][0]);
       }
       if (lane == 0 && t0 + CS < L) {
-        lds_dma4(gdt + t0 + CS, (lds_float*)&sm.rs[c & 1][1][CS]);
-        lds_dma4(gtr + t0 + CS, (lds_float*)&sm.rs[c & 1][2][CS]);
+        lds_dma4(gdt + t0 + CS, 0u, (lds_float*)&sm.rs[c & 1][1][CS]);
+        lds_dma4(gtr + t0 + CS, 0u, (lds_float*)&sm.rs[c & 1][2][CS]);
       }
     }
   };
@@ -436,7 +436,7 @@ void scan_chunked_kernel(ScanArgs a) {
           // with tanh(x) = 1 - 2 / (1 + e^{2x}); the fractional part is the reference's
           // mod-2pi wrap, and the hardware sin/cos take revolutions
           const float rcp = rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j]));
-          const float d = tok ? fmaf(-s_dt, rcp, hdt) : 0.0f;
+          const float d = fmaf(-s_dt, rcp, hdt);        // s_dt = 0 past the sequence end
           const float th = __builtin_amdgcn_fractf(carry[k][j] + wave_incl_scan(d));
           carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
           p_cs[k][j] = __builtin_amdgcn_cosf(th);
@@ -531,14 +531,25 @@ void scan_chunked_kernel(ScanArgs a) {
         Vec8<T> vv;
         if constexpr (G::BF) vv.raw_set(staged<G::SV>(sm.rv, tl, g));
         else vv.raw_set2(staged<G::SV>(sm.rv, tl, 2 * g), staged<G::SV>(sm.rv, tl, 2 * g + 1));
-        float vf[8];
-        vv.to_f(vf);
         if (lane < CS) {
+          if constexpr (G::BF) {
+            // V^T straight from the stored 16-bit values: low and high halves of each word
+            const uint32_t w4[4] = {vv.raw.x, vv.raw.y, vv.raw.z, vv.raw.w};
 #pragma unroll
-          for (int q = 0; q < 8; q += 2)
-            store_pair(&sm.vt[(8 * g + q) * G::LDV + lane], &sm.vt[(8 * g + q + 1) * G::LDV + lane], vf[q], vf[q + 1]);
+            for (int q = 0; q < 4; ++q) {
+              reinterpret_cast<uint16_t*>(sm.vt)[(8 * g + 2 * q) * G::LDV + lane] = (uint16_t)(w4[q] & 0xffffu);
+              reinterpret_cast<uint16_t*>(sm.vt)[(8 * g + 2 * q + 1) * G::LDV + lane] = (uint16_t)(w4[q] >> 16);
+            }
+          } else {
+            float vf[8];
+            vv.to_f(vf);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) sm.vt[(8 * g + q) * G::LDV + lane] = vf[q];
+          }
         }
         if (a.fin_v && tok && t0 + lane == L - 1) {
+          float vf[8];
+          vv.to_f(vf);
 #pragma unroll
           for (int q = 0; q < 8; ++q) a.fin_v[(long)bh * P + 8 * g + q] = vf[q];
         }
