@@ -103,18 +103,20 @@ template <typename T, int CS_, int N_, int P_, int R_, int NW_>
 struct Geo {
   static constexpr bool BF = std::is_same<T, bf16>::value;
   static constexpr int CS = CS_, N = N_, P = P_, R = R_, NW = NW_, NT = 64 * NW_;
-  static constexpr int NWY = NW / 2;                        // output waves; the rest hold the state
+  static constexpr int NWY = 4;                             // output waves 0..3
+  static constexpr int NST = 4;                             // state waves 4..7
+  static constexpr int NAUX = NW - NWY - NST;               // auxiliary waves (rope angles, staging)
   static constexpr int KSTEP = MF16<T>::KSTEP;
   static constexpr int LB16 = CS / 16, PT = P / 16;         // 16-row query blocks, 16-col p-tiles
   static constexpr int NB16 = N / 16;                       // 16-row state tiles per p-tile
-  static constexpr int SPT = (NW - NWY) / PT;               // state waves per p-tile
+  static constexpr int SPT = NST / PT;                      // state waves per p-tile
   static constexpr int TS = BF ? 2 : 4;
   static constexpr int PAD = BF ? 8 : 4;
   static constexpr int LDQ = N + PAD;                       // sQ, sK rows (elements)
   static constexpr int LDV = CS + PAD;                      // sVt, sKwT rows
   static constexpr int LDY = P + (BF ? 8 : 2);              // sY rows (io precision)
-  static constexpr int QG = N / 8, QGW = (QG + NW - 1) / NW;  // Q/K 8-column groups, per wave
-  static constexpr int VG = P / 8, VGW = (VG + NW - 1) / NW;  // V 8-column groups, per wave
+  static constexpr int QG = N / 8, QGW = 2;                // Q/K 8-column groups, at most 2 per wave
+  static constexpr int VG = P / 8, VGW = 1;                // V 8-column groups, one per wave
   // 16-byte staging slots per row: Q/K, V, rotation rates
   static constexpr int SQ = N * TS / 16, SV = P * TS / 16, SA = R / 4 > 0 ? R / 4 : 1;
   static constexpr int BASE = (2 * CS * LDQ + N * LDV + P * LDV) * TS + (2 * CS * SQ + CS * SV + 2 * CS * SA) * 16 +
@@ -123,7 +125,26 @@ struct Geo {
   static constexpr bool OVL = BASE + 4 * CS * LDY * TS <= 160 * 1024 - 256;
   static constexpr int NY = OVL ? 2 : 1;
   static_assert(CS <= 64 && LB16 <= NWY, "one token per lane, one query block per output wave");
-  static_assert(SPT >= 1 && (NW - NWY) % PT == 0 && LB16 % SPT == 0, "state-wave split");
+  static_assert(SPT >= 1 && NST % PT == 0 && LB16 % SPT == 0, "state-wave split");
+  static_assert(NAUX == 0 || NAUX == 4, "8 or 12 waves");
+  static_assert(QG <= 2 * NW && VG <= (NAUX ? NWY + NST : NW), "column groups per wave");
+  // Q/K 8-column group k (< QGW) of a wave, or QG for none.  With auxiliary waves they
+  // take the first groups (the rope columns), two each, so the rope angle work stays
+  // off the matrix waves; the remaining groups go one per matrix wave.
+  __device__ static int qgroup(int wave, int k) {
+    if (NAUX == 0) {
+      const int g = wave + NW * k;
+      return g < QG ? g : QG;
+    }
+    if (wave >= NWY + NST) {
+      const int g = 2 * (wave - NWY - NST) + k;
+      return g < QG ? g : QG;
+    }
+    const int g = 2 * NAUX + wave + (NWY + NST) * k;
+    return g < QG ? g : QG;
+  }
+  // V 8-column group of a wave, or VG for none (matrix waves when auxiliary waves exist)
+  __device__ static int vgroup(int wave) { return (NAUX == 0 || wave < NWY + NST) && wave < VG ? wave : VG; }
   static_assert(R % 4 == 0 && 2 * R <= N, "rotation width: a multiple of 4, at most N/2");
   static_assert((SQ & (SQ - 1)) == 0 && (SV & (SV - 1)) == 0 && (SA & (SA - 1)) == 0, "swizzle widths");
 };
@@ -192,12 +213,16 @@ __device__ __forceinline__ void stage_rows(lds_uint4* dst, const char* src, long
   constexpr int RP = 64 / S;                               // rows per instruction
   constexpr int PER = S * S / 64 > 1 ? S * S / 64 : 1;     // period of the lane pattern
   static_assert(CS * S % 64 == 0 && J1 <= CS * S / 64, "whole instructions");
-  const int lrow = lane / S;
+  // the lane offsets are recomputed per call (a few VALU on the staging waves) rather
+  // than kept live across the chunk loop
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  const int lrow = ln / S;
   uint32_t off[PER];
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
     const uint32_t row = p * RP + lrow;
-    off[p] = row * (uint32_t)stride + 16u * ((lane % S) ^ (row & (S - 1)));
+    off[p] = row * (uint32_t)stride + 16u * ((ln % S) ^ (row & (S - 1)));
   }
   // the row base is made opaque so that the compiler keeps one wave-uniform base per
   // group of PER instructions instead of strength-reducing to 64-bit lane pointers
@@ -285,7 +310,8 @@ void scan_chunked_kernel(ScanArgs a) {
 
   // ---- staging, spread over the waves with the most slack in the matrix phase:
   // Q, K, V of chunk c; rotation rates and scalars of chunk c into parity c & 1
-  constexpr int kWQ0 = 2, kWQ1 = 4, kWK0 = 6, kWK1 = 7, kWV = 0, kWA = 5;
+  constexpr int kWQ0 = G::NAUX ? 8 : 2, kWQ1 = G::NAUX ? 9 : 4, kWK0 = G::NAUX ? 10 : 6, kWK1 = G::NAUX ? 11 : 7;
+  constexpr int kWV = G::NAUX ? 8 : 0, kWA = G::NAUX ? 9 : 5;
   auto stage_qkv = [&](int c) {
     const int t0 = c * CS;
     const int valid = L - t0;
@@ -356,21 +382,22 @@ void scan_chunked_kernel(ScanArgs a) {
   // p-tile pr (h^T[:, 16 pr + lane%16], all N rows, as 16x16 accumulators) and the
   // query blocks lb = part (mod SPT) of Y_off
   const bool ywave = wave < G::NWY;
+  const bool swave = wave >= G::NWY && wave < G::NWY + G::NST;   // the rest are auxiliary
   const int sw = wave - G::NWY;
-  const int pr = ywave ? 0 : sw % G::PT, part = ywave ? 0 : sw / G::PT;
+  const int pr = swave ? sw % G::PT : 0, part = swave ? sw / G::PT : 0;
   const int pcol = 16 * pr + (lane & 15);
   const int g4 = 4 * (lane >> 4);              // C-tile row offset of this lane
   f32x4 hs[G::NB16];
   {
     // effective entering state: h0 + (1 - sigmoid(trap_0)) dt_0 (v0 (x) k0)
     const float cinit = (a.init_h && L > 0) ? (1.0f - sigmoid_fast(gtr[0])) * gdt[0] : 0.0f;
-    const float v0 = (a.init_h && !ywave) ? a.init_v[(long)bh * P + pcol] : 0.0f;
+    const float v0 = (a.init_h && swave) ? a.init_v[(long)bh * P + pcol] : 0.0f;
 #pragma unroll
     for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = 16 * nb + g4 + r;
-        hs[nb][r] = (a.init_h && !ywave)
+        hs[nb][r] = (a.init_h && swave)
                         ? a.init_h[((long)bh * P + pcol) * N + n] + cinit * v0 * a.init_k[(long)bh * N + n]
                         : 0.0f;
       }
@@ -380,7 +407,7 @@ void scan_chunked_kernel(ScanArgs a) {
   for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int r = 4 * (wave + NW * k) + j;
+      const int r = 4 * G::qgroup(wave, k) + j;
       carry[k][j] = (a.init_theta && r < R) ? a.init_theta[(long)bh * R + r] * kInvTwoPi : 0.0f;  // revolutions
     }
   // staging never holds uninitialised bits: rows past the sequence end are not loaded
@@ -392,7 +419,7 @@ void scan_chunked_kernel(ScanArgs a) {
   // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
   // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
   // the angles of its own rope pairs in registers.
-  constexpr int kScalarWave = 0;
+  constexpr int kScalarWave = G::NAUX ? NW - 1 : 0;
   float p_cs[G::QGW][4], p_sn[G::QGW][4];
   auto pre = [&](int cc) {
     const int t0 = cc * CS;
@@ -424,7 +451,7 @@ void scan_chunked_kernel(ScanArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
-      const int g = wave + NW * k;
+      const int g = G::qgroup(wave, k);
       if (g < G::QG && 4 * g < R) {
         const uint4 rr = staged<G::SA>(sm.ra[pb], tl, g);
         const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
@@ -466,7 +493,7 @@ void scan_chunked_kernel(ScanArgs a) {
     // Q/K column groups: rotation angles, biases, rope, key scale
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
-      const int g = wave + NW * k;
+      const int g = G::qgroup(wave, k);
       if (g < G::QG) {
         float qf[8], kf[8];
         {
@@ -524,9 +551,8 @@ void scan_chunked_kernel(ScanArgs a) {
       }
     }
     // V column groups: V^T
-#pragma unroll
-    for (int k = 0; k < G::VGW; ++k) {
-      const int g = wave + NW * k;
+    {
+      const int g = G::vgroup(wave);
       if (g < G::VG) {
         Vec8<T> vv;
         if constexpr (G::BF) vv.raw_set(staged<G::SV>(sm.rv, tl, g));
@@ -568,7 +594,7 @@ void scan_chunked_kernel(ScanArgs a) {
     if (G::OVL && c > 0) gate(c - 1);
     // ---- next chunk's constants and rotations: state waves before their matrix work,
     // output waves after it, so each SIMD pairs VALU work with matrix work
-    if (!ywave && c + 1 < nc) pre(c + 1);
+    if (G::NAUX == 0 && swave && c + 1 < nc) pre(c + 1);
 
     const int pc = c & 1;
     T* ydst = sm.yd[c % G::NY];
@@ -578,7 +604,11 @@ void scan_chunked_kernel(ScanArgs a) {
     // Instantiated per query block so every loop over key blocks is static.
     auto out_block = [&](auto lb_c) {
       constexpr int lb = decltype(lb_c)::value;
-      const int l = 16 * lb + (lane & 15);
+      // lane-derived addresses are recomputed here, not kept live across the loop
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int g4l = 4 * (ln >> 4);
+      const int l = 16 * lb + (ln & 15);
       const float al = sm.ac2[pc][l];
       const float dgl = sm.dg[pc][l];
       constexpr int NK = N / W::KSTEP;
@@ -586,7 +616,7 @@ void scan_chunked_kernel(ScanArgs a) {
       // chains side by side
       typename W::frag qf[NK];
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) qf[kk] = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, lane);
+      for (int kk = 0; kk < NK; ++kk) qf[kk] = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, ln);
       f32x4 st[lb + 2];
 #pragma unroll
       for (int sb = 0; sb < lb + 2; ++sb)
@@ -596,10 +626,10 @@ void scan_chunked_kernel(ScanArgs a) {
       for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
         for (int sb = 0; sb <= lb; ++sb)
-          st[sb] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, lane), qf[kk], st[sb]);
+          st[sb] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, ln), qf[kk], st[sb]);
 #pragma unroll
       for (int sb = 0; sb <= lb; ++sb) {
-        const int s0 = 16 * sb + g4;
+        const int s0 = 16 * sb + g4l;
         if (sb < lb) {
           // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
           const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
@@ -629,15 +659,15 @@ void scan_chunked_kernel(ScanArgs a) {
           const typename W::frag mf = W::from_acc(st[sp], st[sp + 1], j);
 #pragma unroll
           for (int pt = 0; pt < G::PT; ++pt)
-            yd[pt] = W::mma(mf, W::vperm(sm.vt, G::LDV, 16 * pt, 16 * sp, j, lane), yd[pt]);
+            yd[pt] = W::mma(mf, W::vperm(sm.vt, G::LDV, 16 * pt, 16 * sp, j, ln), yd[pt]);
         }
       }
 #pragma unroll
       for (int pt = 0; pt < G::PT; ++pt)
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
-          store_pair(&ydst[(16 * lb + g4 + r) * G::LDY + 16 * pt + (lane & 15)],
-                     &ydst[(16 * lb + g4 + r + 1) * G::LDY + 16 * pt + (lane & 15)], yd[pt][r], yd[pt][r + 1]);
+          store_pair(&ydst[(16 * lb + g4l + r) * G::LDY + 16 * pt + (ln & 15)],
+                     &ydst[(16 * lb + g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
     };
     if (ywave) {
       if (wave == 0) out_block(std::integral_constant<int, 0>{});
@@ -646,7 +676,7 @@ void scan_chunked_kernel(ScanArgs a) {
         if (wave == 2) out_block(std::integral_constant<int, 2>{});
         if (wave == 3) out_block(std::integral_constant<int, 3>{});
       }
-    } else {
+    } else if (swave) {
       // ---- phase 6: Y_off = e^{A_cum} Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
       typename W::frag hf[G::BF ? N / 32 : 1];
       if constexpr (G::BF) {
@@ -660,16 +690,15 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) yo[i][r] = 0.0f;
       if constexpr (G::BF) {
-        // all query fragments first, then the query blocks' chains side by side
-        typename W::frag qa[NLB][N / 32];
+        // per k-step the query blocks' fragments, then their chains side by side
 #pragma unroll
-        for (int i = 0; i < NLB; ++i)
+        for (int q = 0; q < N / 32; ++q) {
+          typename W::frag qa[NLB];
 #pragma unroll
-          for (int q = 0; q < N / 32; ++q) qa[i][q] = W::ld(sm.q, G::LDQ, 16 * (part + G::SPT * i), 32 * q, lane);
+          for (int i = 0; i < NLB; ++i) qa[i] = W::ld(sm.q, G::LDQ, 16 * (part + G::SPT * i), 32 * q, lane);
 #pragma unroll
-        for (int q = 0; q < N / 32; ++q)
-#pragma unroll
-          for (int i = 0; i < NLB; ++i) yo[i] = W::mma(qa[i][q], hf[q], yo[i]);
+          for (int i = 0; i < NLB; ++i) yo[i] = W::mma(qa[i], hf[q], yo[i]);
+        }
       } else {
 #pragma unroll
         for (int nb = 0; nb < G::NB16; ++nb)
@@ -705,7 +734,7 @@ void scan_chunked_kernel(ScanArgs a) {
           hs[nb] = W::mma(W::ld(sm.kwt, G::LDV, 16 * nb, ks * W::KSTEP, lane), vb, hs[nb]);
       }
     }
-    if (ywave && c + 1 < nc) pre(c + 1);
+    if ((G::NAUX > 0 || !swave) && c + 1 < nc) pre(c + 1);
     __builtin_amdgcn_s_waitcnt(0);   // staged loads and gate stores of this wave are done
     if (G::OVL) load_z(c);           // Z for this chunk's gate, one chunk ahead
     __syncthreads();
@@ -716,7 +745,7 @@ void scan_chunked_kernel(ScanArgs a) {
   }
   if (G::OVL && nc > 0) gate(nc - 1);
 
-  if (a.fin_h && !ywave && part == 0) {
+  if (a.fin_h && swave && part == 0) {
 #pragma unroll
     for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
@@ -727,7 +756,7 @@ void scan_chunked_kernel(ScanArgs a) {
     for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r = 4 * (wave + NW * k) + j;
+        const int r = 4 * G::qgroup(wave, k) + j;
         if (r < R) a.fin_theta[(long)bh * R + r] = carry[k][j] * kTwoPi;
       }
   }
@@ -744,7 +773,7 @@ void scan_chunked_kernel(ScanArgs a) {
   X(float, 32, 64, 64, 16) X(float, 32, 64, 64, 32) X(float, 32, 64, 32, 16) X(float, 32, 32, 32, 8) \
   X(float, 32, 32, 64, 8)
 
-constexpr int kChunkWaves = 8;
+constexpr int kChunkWaves = 12;
 
 // The chunked form is an exact rewrite of the token recurrence for every chunk size,
 // so the kernel's blocking changes only the rounding, not the function computed:
