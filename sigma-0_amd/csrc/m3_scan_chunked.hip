@@ -310,7 +310,7 @@ void scan_chunked_kernel(ScanArgs a) {
 
   // ---- staging, spread over the waves with the most slack in the matrix phase:
   // Q, K, V of chunk c; rotation rates and scalars of chunk c into parity c & 1
-  constexpr int kWQ0 = G::NAUX ? 8 : 2, kWQ1 = G::NAUX ? 9 : 4, kWK0 = G::NAUX ? 10 : 6, kWK1 = G::NAUX ? 11 : 7;
+  constexpr int kWQ0 = G::NAUX ? 0 : 2, kWQ1 = G::NAUX ? 0 : 4, kWK0 = G::NAUX ? 1 : 6, kWK1 = G::NAUX ? 1 : 7;
   constexpr int kWV = G::NAUX ? 8 : 0, kWA = G::NAUX ? 9 : 5;
   auto stage_qkv = [&](int c) {
     const int t0 = c * CS;
@@ -480,6 +480,7 @@ void scan_chunked_kernel(ScanArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   pre(0);
+  __syncthreads();   // chunk 0's per-token constants (one wave writes them) before its preparation
 
   for (int c = 0; c < nc; ++c) {
     const int t0 = c * CS;
@@ -582,6 +583,9 @@ void scan_chunked_kernel(ScanArgs a) {
       }
     }
     if (!G::OVL) load_z(c);
+    // ---- gate of the previous chunk: with auxiliary waves, the matrix waves run it
+    // while the auxiliary waves finish their larger preparation share
+    if (G::OVL && G::NAUX > 0 && c > 0) gate(c - 1);
     __syncthreads();
 
     // Z of the chunk waiting for its gate has landed (it was loaded a chunk ago); this
@@ -590,8 +594,8 @@ void scan_chunked_kernel(ScanArgs a) {
     // ---- inputs of the next chunks go in flight (this chunk's Q/K/V staging is consumed)
     if (c + 1 < nc) stage_qkv(c + 1);
     if (c + 2 < nc) stage_ars(c + 2);
-    // ---- gate of the previous chunk, under this chunk's matrix work
-    if (G::OVL && c > 0) gate(c - 1);
+    // ---- without auxiliary waves: gate of the previous chunk, under this chunk's matrix work
+    if (G::OVL && G::NAUX == 0 && c > 0) gate(c - 1);
     // ---- next chunk's constants and rotations: state waves before their matrix work,
     // output waves after it, so each SIMD pairs VALU work with matrix work
     if (G::NAUX == 0 && swave && c + 1 < nc) pre(c + 1);
