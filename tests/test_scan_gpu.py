@@ -141,6 +141,20 @@ def test_headline_config_subset_and_chunk_invariance():
 
 
 @pytest.mark.parametrize("bf16", [False, True])
+def test_repeat_calls_bitwise_identical(bf16):
+    """The kernels use no atomics and no cross-workgroup communication, so repeated
+    calls must give bitwise-identical outputs; a race between waves (for example
+    a read of per-chunk constants before the wave that writes them) shows up here."""
+    torch = _torch()
+    B, L, H, N, P, R = (2, 2048, 16, 128, 64, 32) if bf16 else (2, 1024, 8, 64, 64, 16)
+    d = I.scan_inputs(B, L, H, N, P, R, seed=11, bf16=bf16)
+    t = to_dev(d, torch.bfloat16 if bf16 else torch.float32)
+    first = hip_scan(t, 64)
+    for _ in range(4):
+        assert torch.equal(hip_scan(t, 64), first)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
 def test_carry_split_equals_full(bf16):
     """Prefill [0, L1) with the carry out, then [L1, L) with it as the carry in,
     equals one prefill over [0, L) -- pins initial/final carry semantics."""
