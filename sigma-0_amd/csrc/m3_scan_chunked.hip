@@ -26,77 +26,9 @@
 // barriers per chunk: after the preparation phase and after the matrix phase.
 #include <type_traits>
 
-#include "m3_scan.h"
+#include "m3_chunk_common.h"
 
 namespace m3 {
-
-// 16x16 MFMA tiles: v_mfma_f32_16x16x32_bf16 (KPL = 8) and v_mfma_f32_16x16x4_f32
-// (KPL = 1).  A: lane i holds row i%16, k = (i/16)*KPL + [0,KPL); B: col i%16, same k;
-// C: lane i, reg r holds col i%16, row 4*(i/16) + r (verified lane layouts).
-template <typename T> struct MF16;
-template <> struct MF16<bf16> {
-  static constexpr int KSTEP = 32;
-  typedef bf16x8 frag;
-  // Q and K rows are stored with the columns of each 32-block permuted so that the
-  // k-slice a lane reads for Q h^T (8 contiguous elements) holds logical columns
-  // 4g + [0,4) and 16 + 4g + [0,4), g = lane/16: exactly the state rows a lane's
-  // two 16x16 h^T accumulator tiles hold.  S = K Q^T contracts over the same
-  // permuted order on both sides, so it is unaffected.
-  __host__ __device__ static constexpr int qpos(int n) {
-    return (n & ~31) + 8 * ((n & 15) >> 2) + ((n & 16) ? 4 : 0) + (n & 3);
-  }
-  // B operand of Q h^T for state rows [32q, 32q + 32): the lane's regs of tiles 2q, 2q+1
-  __device__ __forceinline__ static frag hfrag(const f32x4& a, const f32x4& b) {
-    frag f;
-    f[0] = (bf16)a[0]; f[1] = (bf16)a[1]; f[2] = (bf16)a[2]; f[3] = (bf16)a[3];
-    f[4] = (bf16)b[0]; f[5] = (bf16)b[1]; f[6] = (bf16)b[2]; f[7] = (bf16)b[3];
-    return f;
-  }
-  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static frag ld(const bf16* buf, int ldm, int row0, int k0, int lane) {
-    return *reinterpret_cast<const bf16x8*>(buf + (row0 + (lane & 15)) * ldm + k0 + (lane >> 4) * 8);
-  }
-  // steps over a pair of 16-row S^T tiles (32 values of s): slots 0..3 are the
-  // first tile's regs (s = 4(lane/16) + 0..3), slots 4..7 the second's (s + 16)
-  static constexpr int STEPS = 1;
-  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int) {
-    frag f;
-    f[0] = (bf16)c0[0]; f[1] = (bf16)c0[1]; f[2] = (bf16)c0[2]; f[3] = (bf16)c0[3];
-    f[4] = (bf16)c1[0]; f[5] = (bf16)c1[1]; f[6] = (bf16)c1[2]; f[7] = (bf16)c1[3];
-    return f;
-  }
-  __device__ __forceinline__ static frag vperm(const bf16* vt, int ldv, int p0, int s0, int, int lane) {
-    const bf16* r = vt + (p0 + (lane & 15)) * ldv + s0 + 4 * (lane >> 4);
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(r);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(r + 16);
-    frag f;
-    f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
-    f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
-    return f;
-  }
-};
-template <> struct MF16<float> {
-  static constexpr int KSTEP = 4;
-  typedef float frag;
-  __host__ __device__ static constexpr int qpos(int n) { return n; }
-  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static frag ld(const float* buf, int ldm, int row0, int k0, int lane) {
-    return buf[(row0 + (lane & 15)) * ldm + k0 + (lane >> 4)];
-  }
-  // step j (0..7) over a pair of tiles: j < 4 uses the first tile's reg j
-  // (s = 4(lane/16) + j), j >= 4 the second's reg j-4 (s + 16)
-  static constexpr int STEPS = 8;
-  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int j) {
-    return j < 4 ? c0[j] : c1[j - 4];
-  }
-  __device__ __forceinline__ static frag vperm(const float* vt, int ldv, int p0, int s0, int j, int lane) {
-    return vt[(p0 + (lane & 15)) * ldv + s0 + 4 * (lane >> 4) + (j & 3) + (j >= 4 ? 16 : 0)];
-  }
-};
 
 // Compile-time geometry of one instantiation.
 template <typename T, int CS_, int N_, int P_, int R_, int NW_>
@@ -181,98 +113,6 @@ struct __attribute__((aligned(16))) Smem {
   alignas(16) float wdec[2][G::CS];      // e^{A_end - A_cum}
   float dec[2];                          // e^{A_end}
 };
-
-// Direct-to-LDS loads (global_load_lds): the LDS slot is M0 plus size * lane (the
-// s_nop covers the M0-write hazard).  They
-// are issued from inline assembly so that the compiler does not treat every later
-// LDS access as possibly overlapping the in-flight writes (it would wait for all
-// outstanding vector memory before the first LDS read of the matrix phase).  The
-// kernel orders them itself: an s_waitcnt vmcnt(0) and a barrier separate each
-// batch from the first reads of the staged rows.
-typedef __attribute__((address_space(3))) uint4 lds_uint4;
-typedef __attribute__((address_space(3))) float lds_float;
-__device__ __forceinline__ uint32_t lds_addr(const lds_uint4* p) { return (uint32_t)(uintptr_t)p; }
-__device__ __forceinline__ uint32_t lds_addr(const lds_float* p) { return (uint32_t)(uintptr_t)p; }
-// Address = wave-uniform base (SGPRs) + 32-bit lane offset.
-__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, lds_uint4* l) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
-}
-__device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, lds_float* l) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
-}
-
-// Direct-to-LDS staging of instructions [J0, J1) of CS rows x S 16-byte slots.
-// Instruction j stages 64 slots: lane -> (row, physical slot) = (64j/S + lane/S,
-// lane%S), fetching logical slot (lane%S) ^ (row%S), so each row is read whole
-// (coalesced) and stored swizzled.  The lane part of the global offset repeats every
-// PER instructions (row%S repeats), so a few 32-bit lane offsets plus a wave-uniform
-// row base address every instruction.
-template <int CS, int S, int J0, int J1>
-__device__ __forceinline__ void stage_rows(lds_uint4* dst, const char* src, long stride, int rows_valid,
-                                           int lane) {
-  constexpr int RP = 64 / S;                               // rows per instruction
-  constexpr int PER = S * S / 64 > 1 ? S * S / 64 : 1;     // period of the lane pattern
-  static_assert(CS * S % 64 == 0 && J1 <= CS * S / 64, "whole instructions");
-  // the lane offsets are recomputed per call (a few VALU on the staging waves) rather
-  // than kept live across the chunk loop
-  int ln = lane;
-  asm volatile("" : "+v"(ln));
-  const int lrow = ln / S;
-  uint32_t off[PER];
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const uint32_t row = p * RP + lrow;
-    off[p] = row * (uint32_t)stride + 16u * ((ln % S) ^ (row & (S - 1)));
-  }
-  // the row base is made opaque so that the compiler keeps one wave-uniform base per
-  // group of PER instructions instead of strength-reducing to 64-bit lane pointers
-  const char* base = src;
-  asm volatile("" : "+s"(base));
-  if (rows_valid >= CS) {
-#pragma unroll
-    for (int j = J0; j < J1; ++j)
-      lds_dma16(base + (long)(j / PER) * (PER * RP) * stride, off[j % PER], dst + 64 * j);
-  } else {
-#pragma unroll
-    for (int j = J0; j < J1; ++j)
-      if (j * RP + lrow < rows_valid)
-        lds_dma16(base + (long)(j / PER) * (PER * RP) * stride, off[j % PER], dst + 64 * j);
-  }
-}
-template <int S>
-__device__ __forceinline__ const uint4& staged(const uint4* buf, int row, int slot) {
-  return buf[row * S + (slot ^ (row & (S - 1)))];
-}
-
-// Store 4 consecutive elements (8 bytes bf16, 16 bytes f32).
-__device__ __forceinline__ void store4(bf16* p, const float* f) {
-  bf16x4 v;
-  v[0] = (bf16)f[0]; v[1] = (bf16)f[1]; v[2] = (bf16)f[2]; v[3] = (bf16)f[3];
-  *reinterpret_cast<bf16x4*>(p) = v;
-}
-__device__ __forceinline__ void store4(float* p, const float* f) {
-  *reinterpret_cast<float4*>(p) = make_float4(f[0], f[1], f[2], f[3]);
-}
-__device__ __forceinline__ void load4(const bf16* p, float* f) {
-  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
-  f[0] = (float)v[0]; f[1] = (float)v[1]; f[2] = (float)v[2]; f[3] = (float)v[3];
-}
-__device__ __forceinline__ void load4(const float* p, float* f) {
-  const float4 v = *reinterpret_cast<const float4*>(p);
-  f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
-}
-
-// Two values to two 16-bit (or 32-bit) slots: one packed conversion, then the low and
-// high halves written separately.
-__device__ __forceinline__ void store_pair(bf16* p0, bf16* p1, float a, float b) {
-  const bf16x2 v = {(bf16)a, (bf16)b};
-  *p0 = v[0];
-  *p1 = v[1];
-}
-__device__ __forceinline__ void store_pair(float* p0, float* p1, float a, float b) {
-  *p0 = a;
-  *p1 = b;
-}
 
 template <typename T, int CS, int N, int P, int R, int NW>
 __global__ __launch_bounds__(64 * NW, 1)
