@@ -74,23 +74,27 @@ template <> struct MF16<float> {
   }
 };
 
-// Direct-to-LDS loads (global_load_lds): the LDS slot is M0 plus size * lane (the
-// s_nop covers the M0-write hazard).  They
+// Direct-to-LDS loads (global_load_lds): the LDS slot is M0 plus size * lane.  They
 // are issued from inline assembly so that the compiler does not treat every later
 // LDS access as possibly overlapping the in-flight writes (it would wait for all
 // outstanding vector memory before the first LDS read of the matrix phase).  The
 // kernel orders them itself: an s_waitcnt vmcnt(0) and a barrier separate each
 // batch from the first reads of the staged rows.
+// The compiler inserts no hazard wait states for instructions inside inline asm, so
+// the asm carries its own: a vector memory instruction that reads an SGPR written by
+// a VALU instruction needs 5 wait states (the compiler reloads spilled address SGPRs
+// with v_readlane right before the asm), and the M0 write needs 1.  s_nop 4 gives 5.
+// With fewer, the load can form its address from a stale SGPR half.
 typedef __attribute__((address_space(3))) uint4 lds_uint4;
 typedef __attribute__((address_space(3))) float lds_float;
 __device__ __forceinline__ uint32_t lds_addr(const lds_uint4* p) { return (uint32_t)(uintptr_t)p; }
 __device__ __forceinline__ uint32_t lds_addr(const lds_float* p) { return (uint32_t)(uintptr_t)p; }
 // Address = wave-uniform base (SGPRs) + 32-bit lane offset.
 __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, lds_uint4* l) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
 }
 __device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, lds_float* l) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
 }
 
 // Direct-to-LDS staging of instructions [J0, J1) of CS rows x S 16-byte slots.
