@@ -3,8 +3,9 @@
  *
  * Plain pointers and sizes only.  Every device pointer is a HIP device
  * address; `stream` is a hipStream_t passed as void* (NULL = default stream).
- * All calls are asynchronous on `stream`, allocate nothing, keep no per-call
- * state and may be issued concurrently from several host threads.  Return
+ * All calls are asynchronous on `stream`, allocate nothing (a split prefill
+ * takes a caller-owned workspace), keep no per-call state and may be issued
+ * concurrently from several host threads.  Return
  * value: 0 on success, else an M3_E* code; m3_last_error() then describes it
  * (thread-local string).
  *
@@ -22,6 +23,8 @@
  */
 #ifndef MAMBA3_SCAN_H_
 #define MAMBA3_SCAN_H_
+
+#include <stddef.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -85,6 +88,34 @@ int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
                             float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
                             int B, int L, int H, int Hqk, int N, int P, int R,
                             int chunk_size, int io_dtype, void* stream);
+
+/*
+ * Device workspace (bytes) that m3_chunk_scan_fwd_ws uses to split each sequence
+ * into segments running on separate compute units; 0 when the shape runs as one
+ * pass.  The split pays off when B*H is well below the compute-unit count
+ * (single-sequence prefill, long context).  Hqk does not matter.
+ */
+size_t m3_chunk_scan_ws_bytes(int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype);
+
+/*
+ * m3_chunk_scan_fwd_carry with a caller-owned device workspace of ws_bytes
+ * (>= m3_chunk_scan_ws_bytes of the shape, 16-byte aligned).  With ws NULL or a
+ * zero requirement it is exactly m3_chunk_scan_fwd_carry.  Otherwise it runs three
+ * kernels on `stream`: every segment from a zero carry (state only), a combine of
+ * the segments' exit carries into entering carries, and every segment's full scan
+ * from its entering carry: the carry algebra of the reference's sequence-parallel
+ * path (src/base_model/models/mamba3_seqpar.py:67-110) across the compute units of
+ * one GPU.  The workspace is scratch for the call only.
+ */
+int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
+                         const float* ADT, const float* DT, const float* Trap,
+                         const float* Q_bias, const float* K_bias, const float* Angles,
+                         const float* D, const void* Z, void* Out,
+                         const float* init_theta, const float* init_ssm,
+                         const float* init_k, const float* init_v,
+                         float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                         int B, int L, int H, int Hqk, int N, int P, int R,
+                         int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * One decode step for a batch, in place on the carry.  Replaces the body of

@@ -60,15 +60,21 @@ int m3_chunk_scan_impl(int io_dtype, int N, int P, int R, int chunk_size) {
   return impl_for(io_dtype, N, P, R, chunk_size);
 }
 
-int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
-                            const float* ADT, const float* DT, const float* Trap,
-                            const float* Q_bias, const float* K_bias, const float* Angles,
-                            const float* D, const void* Z, void* Out,
-                            const float* init_theta, const float* init_ssm,
-                            const float* init_k, const float* init_v,
-                            float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
-                            int B, int L, int H, int Hqk, int N, int P, int R,
-                            int chunk_size, int io_dtype, void* stream) {
+size_t m3_chunk_scan_ws_bytes(int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype) {
+  if ((io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16) || B <= 0 || L <= 0 || H <= 0 || chunk_size <= 0)
+    return 0;
+  return m3::scan_split_ws_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, N, P, R, chunk_size);
+}
+
+int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
+                         const float* ADT, const float* DT, const float* Trap,
+                         const float* Q_bias, const float* K_bias, const float* Angles,
+                         const float* D, const void* Z, void* Out,
+                         const float* init_theta, const float* init_ssm,
+                         const float* init_k, const float* init_v,
+                         float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                         int B, int L, int H, int Hqk, int N, int P, int R,
+                         int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
@@ -106,8 +112,31 @@ int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
   a.B = B; a.L = L; a.H = H; a.Hqk = Hqk; a.N = N; a.P = P; a.R = R; a.CS = chunk_size;
   const bool bf = io_dtype == M3_DTYPE_BF16;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (impl == M3_IMPL_CHUNKED_MFMA) return check_launch(m3::scan_chunked_launch(a, bf, st), "chunk scan");
+  if (impl == M3_IMPL_CHUNKED_MFMA) {
+    const size_t need = ws ? m3::scan_split_ws_bytes(bf, B, L, H, N, P, R, chunk_size) : 0;
+    if (need > 0) {
+      if (ws_bytes < need)
+        return fail(M3_E_ARG, "workspace of %zu bytes, the split needs %zu (m3_chunk_scan_ws_bytes)", ws_bytes, need);
+      if (!aligned16(ws)) return fail(M3_E_ALIGN, "workspace must be 16-byte aligned");
+      return check_launch(m3::scan_split_launch(a, bf, ws, st), "split chunk scan");
+    }
+    return check_launch(m3::scan_chunked_launch(a, bf, st), "chunk scan");
+  }
   return check_launch(m3::scan_generic_launch(a, bf, st), "generic scan");
+}
+
+int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
+                            const float* ADT, const float* DT, const float* Trap,
+                            const float* Q_bias, const float* K_bias, const float* Angles,
+                            const float* D, const void* Z, void* Out,
+                            const float* init_theta, const float* init_ssm,
+                            const float* init_k, const float* init_v,
+                            float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                            int B, int L, int H, int Hqk, int N, int P, int R,
+                            int chunk_size, int io_dtype, void* stream) {
+  return m3_chunk_scan_fwd_ws(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, init_theta, init_ssm,
+                              init_k, init_v, fin_theta, fin_ssm, fin_k, fin_v, B, L, H, Hqk, N, P, R, chunk_size,
+                              io_dtype, nullptr, 0, stream);
 }
 
 int m3_chunk_scan_fwd(const void* Q, const void* K, const void* V,

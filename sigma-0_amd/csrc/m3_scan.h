@@ -20,6 +20,12 @@ struct ScanArgs {
   const float* init_theta; const float* init_h; const float* init_k; const float* init_v;
   float* fin_theta; float* fin_h; float* fin_k; float* fin_v;
   int B, L, H, Hqk, N, P, R, CS;
+  // Sequence segments (chunked kernel only): with seg_len > 0 the grid's y index
+  // is the segment and block (bh, seg) covers tokens [seg * seg_len,
+  // min(L, (seg + 1) * seg_len)); seg_len is a multiple of 128.  Carries are one per
+  // (b, h) (init used by segment 0, fin written by the last segment) or, with
+  // init_per_seg / fin_per_seg, one per (b, h, segment) at index bh * nseg + seg.
+  int seg_len = 0, init_per_seg = 0, fin_per_seg = 0;
 };
 
 bool scan_generic_supported(int N, int P, int R);
@@ -28,6 +34,14 @@ hipError_t scan_generic_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
 // Chunked MFMA kernel: returns true when (dtype, CS, N, P, R) has an instantiation.
 bool scan_chunked_supported(bool bf16_io, int CS, int N, int P, int R);
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
+
+// State-only pass of the chunked kernel (sequence split, pass 1).
+bool scan_state_supported(bool bf16_io, int N, int P, int R);
+hipError_t scan_state_launch(const ScanArgs& a, hipStream_t st);
+
+// Sequence split across compute units: workspace bytes (0 = no split) and launch.
+size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS);
+hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStream_t st);
 
 // Arguments of one decode step (layouts in m3_decode.hip).
 struct DecodeArgs {

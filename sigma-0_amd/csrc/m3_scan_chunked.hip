@@ -114,7 +114,9 @@ struct __attribute__((aligned(16))) Smem {
   float dec[2];                          // e^{A_end}
 };
 
-template <typename T, int CS, int N, int P, int R, int NW>
+// SO (state only): the pass that produces each segment's exit carry from a zero
+// entering carry; it skips Q, Y_diag, Y_off, the gate and the output.
+template <typename T, int CS, int N, int P, int R, int NW, bool SO>
 __global__ __launch_bounds__(64 * NW, 1)
 void scan_chunked_kernel(ScanArgs a) {
   typedef Geo<T, CS, N, P, R, NW> G;
@@ -129,20 +131,32 @@ void scan_chunked_kernel(ScanArgs a) {
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh % a.H;
   const int hq = h / (a.H / a.Hqk);
-  const int L = a.L, H = a.H, HQ = a.Hqk;
+  const int Lg = a.L, H = a.H, HQ = a.Hqk;
+  // this block's tokens [tb, tb + L); Lnx counts the tokens from tb to the sequence
+  // end (the trapezoid weight of a segment's last token reads the next one)
+  const int seg = blockIdx.y, nseg = gridDim.y;
+  const int tb = a.seg_len > 0 ? seg * a.seg_len : 0;
+  const int L = a.seg_len > 0 ? min(Lg - tb, a.seg_len) : Lg;
+  const int Lnx = Lg - tb;
   const int nc = (L + CS - 1) / CS;
+  // carry slots: per (b, h) or per (b, h, segment)
+  const int ci_in = a.init_per_seg ? bh * nseg + seg : bh;
+  const int ci_out = a.fin_per_seg ? bh * nseg + seg : bh;
+  const bool has_init = a.init_per_seg || seg == 0;
+  const bool fin_here = a.fin_per_seg || seg == nseg - 1;
   T* gO = reinterpret_cast<T*>(a.out);
   const T* gZ = reinterpret_cast<const T*>(a.z);
-  const float* gadt = a.adt + (long)bh * L;
-  const float* gdt = a.dt + (long)bh * L;
-  const float* gtr = a.trap + (long)bh * L;
+  const float* gadt = a.adt + (long)bh * Lg + tb;
+  const float* gdt = a.dt + (long)bh * Lg + tb;
+  const float* gtr = a.trap + (long)bh * Lg + tb;
   const float Dh = a.D ? a.D[h] : 0.0f;
   const bool has_z = a.z != nullptr;
 
   // ---- element offsets of row (b, t=0, head) in each input; rows advance by the stride
-  const long qk_row = ((long)b * L * HQ + hq) * N, qk_stride = (long)HQ * N;
-  const long v_row = ((long)b * L * H + h) * P, v_stride = (long)H * P;
-  const long a_row = ((long)b * L * H + h) * R, a_stride = (long)H * R;
+  const long qk_stride = (long)HQ * N, v_stride = (long)H * P, a_stride = (long)H * R;
+  const long qk_row = ((long)b * Lg * HQ + hq) * N + tb * qk_stride;
+  const long v_row = ((long)b * Lg * H + h) * P + tb * v_stride;
+  const long a_row = ((long)b * Lg * H + h) * R + tb * a_stride;
   for (int i = tid; i < N; i += G::NT) {
     sm.qb[i] = a.qbias[(long)h * N + i];
     sm.kb[i] = a.kbias[(long)h * N + i];
@@ -158,8 +172,8 @@ void scan_chunked_kernel(ScanArgs a) {
     constexpr int JQ = CS * G::SQ / 64, JV = CS * G::SV / 64;
     const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
     const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
-    if (wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
-    if (wave == kWQ1) stage_rows<CS, G::SQ, JQ / 2, JQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
+    if (!SO && wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
+    if (!SO && wave == kWQ1) stage_rows<CS, G::SQ, JQ / 2, JQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
     if (wave == kWK0) stage_rows<CS, G::SQ, 0, JQ / 2>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
     if (wave == kWK1) stage_rows<CS, G::SQ, JQ / 2, JQ>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
     if (wave == kWV) {
@@ -181,7 +195,7 @@ void scan_chunked_kernel(ScanArgs a) {
         lds_dma4(gdt + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][1][0]);
         lds_dma4(gtr + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][2][0]);
       }
-      if (lane == 0 && t0 + CS < L) {
+      if (lane == 0 && t0 + CS < Lnx) {
         lds_dma4(gdt + t0 + CS, 0u, (lds_float*)&sm.rs[c & 1][1][CS]);
         lds_dma4(gtr + t0 + CS, 0u, (lds_float*)&sm.rs[c & 1][2][CS]);
       }
@@ -230,15 +244,15 @@ void scan_chunked_kernel(ScanArgs a) {
   f32x4 hs[G::NB16];
   {
     // effective entering state: h0 + (1 - sigmoid(trap_0)) dt_0 (v0 (x) k0)
-    const float cinit = (a.init_h && L > 0) ? (1.0f - sigmoid_fast(gtr[0])) * gdt[0] : 0.0f;
-    const float v0 = (a.init_h && swave) ? a.init_v[(long)bh * P + pcol] : 0.0f;
+    const bool own = a.init_h && has_init && swave;
+    const float cinit = own ? (1.0f - sigmoid_fast(gtr[0])) * gdt[0] : 0.0f;
+    const float v0 = own ? a.init_v[(long)ci_in * P + pcol] : 0.0f;
 #pragma unroll
     for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = 16 * nb + g4 + r;
-        hs[nb][r] = (a.init_h && swave)
-                        ? a.init_h[((long)bh * P + pcol) * N + n] + cinit * v0 * a.init_k[(long)bh * N + n]
+        hs[nb][r] = own ? a.init_h[((long)ci_in * P + pcol) * N + n] + cinit * v0 * a.init_k[(long)ci_in * N + n]
                         : 0.0f;
       }
   }
@@ -248,7 +262,7 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = 4 * G::qgroup(wave, k) + j;
-      carry[k][j] = (a.init_theta && r < R) ? a.init_theta[(long)bh * R + r] * kInvTwoPi : 0.0f;  // revolutions
+      carry[k][j] = (a.init_theta && has_init && r < R) ? a.init_theta[(long)ci_in * R + r] * kInvTwoPi : 0.0f;  // revolutions
     }
   // staging never holds uninitialised bits: rows past the sequence end are not loaded
   for (int i = tid; i < G::CS * G::SQ; i += G::NT) { sm.rq[i] = make_uint4(0, 0, 0, 0); sm.rk[i] = sm.rq[i]; }
@@ -274,7 +288,7 @@ void scan_chunked_kernel(ScanArgs a) {
       const float gam = s_dt * sig;
       const float u = s_dt * (1.0f - sig);                                 // dt (1 - sigmoid), this token
       float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // next token
-      if (lane == CS - 1) un = (t0 + CS < L) ? sm.rs[pb][1][CS] * (1.0f - sigmoid_fast(sm.rs[pb][2][CS])) : 0.0f;
+      if (lane == CS - 1) un = (t0 + CS < Lnx) ? sm.rs[pb][1][CS] * (1.0f - sigmoid_fast(sm.rs[pb][2][CS])) : 0.0f;
       const float scl = gam + un;
       const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
       const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
@@ -373,15 +387,17 @@ void scan_chunked_kernel(ScanArgs a) {
             kf[2 * j + 1] = k0 * sn + k1 * cs;
           }
         }
-        if (a.fin_k && tok && t0 + lane == L - 1) {
+        if (a.fin_k && fin_here && tok && t0 + lane == L - 1) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a.fin_k[(long)bh * N + 8 * g + e] = kf[e];
+          for (int e = 0; e < 8; ++e) a.fin_k[(long)ci_out * N + 8 * g + e] = kf[e];
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) kf[e] *= scl;
         if (lane < CS) {
-          store4(&sm.q[lane * G::LDQ + W::qpos(8 * g)], qf);
-          store4(&sm.q[lane * G::LDQ + W::qpos(8 * g + 4)], qf + 4);
+          if constexpr (!SO) {
+            store4(&sm.q[lane * G::LDQ + W::qpos(8 * g)], qf);
+            store4(&sm.q[lane * G::LDQ + W::qpos(8 * g + 4)], qf + 4);
+          }
           store4(&sm.k[lane * G::LDQ + W::qpos(8 * g)], kf);
           store4(&sm.k[lane * G::LDQ + W::qpos(8 * g + 4)], kf + 4);
 #pragma unroll
@@ -414,18 +430,18 @@ void scan_chunked_kernel(ScanArgs a) {
             for (int q = 0; q < 8; ++q) sm.vt[(8 * g + q) * G::LDV + lane] = vf[q];
           }
         }
-        if (a.fin_v && tok && t0 + lane == L - 1) {
+        if (a.fin_v && fin_here && tok && t0 + lane == L - 1) {
           float vf[8];
           vv.to_f(vf);
 #pragma unroll
-          for (int q = 0; q < 8; ++q) a.fin_v[(long)bh * P + 8 * g + q] = vf[q];
+          for (int q = 0; q < 8; ++q) a.fin_v[(long)ci_out * P + 8 * g + q] = vf[q];
         }
       }
     }
-    if (!G::OVL) load_z(c);
+    if (!SO && !G::OVL) load_z(c);
     // ---- gate of the previous chunk: with auxiliary waves, the matrix waves run it
     // while the auxiliary waves finish their larger preparation share
-    if (G::OVL && G::NAUX > 0 && c > 0) gate(c - 1);
+    if (!SO && G::OVL && G::NAUX > 0 && c > 0) gate(c - 1);
     __syncthreads();
 
     // Z of the chunk waiting for its gate has landed (it was loaded a chunk ago); this
@@ -435,7 +451,7 @@ void scan_chunked_kernel(ScanArgs a) {
     if (c + 1 < nc) stage_qkv(c + 1);
     if (c + 2 < nc) stage_ars(c + 2);
     // ---- without auxiliary waves: gate of the previous chunk, under this chunk's matrix work
-    if (G::OVL && G::NAUX == 0 && c > 0) gate(c - 1);
+    if (!SO && G::OVL && G::NAUX == 0 && c > 0) gate(c - 1);
     // ---- next chunk's constants and rotations: state waves before their matrix work,
     // output waves after it, so each SIMD pairs VALU work with matrix work
     if (G::NAUX == 0 && swave && c + 1 < nc) pre(c + 1);
@@ -513,7 +529,7 @@ void scan_chunked_kernel(ScanArgs a) {
           store_pair(&ydst[(16 * lb + g4l + r) * G::LDY + 16 * pt + (ln & 15)],
                      &ydst[(16 * lb + g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
     };
-    if (ywave) {
+    if (!SO && ywave) {                 // the state-only pass has no Y_diag
       if (wave == 0) out_block(std::integral_constant<int, 0>{});
       if (wave == 1) out_block(std::integral_constant<int, 1>{});
       if constexpr (G::LB16 > 2) {
@@ -522,6 +538,7 @@ void scan_chunked_kernel(ScanArgs a) {
       }
     } else if (swave) {
       // ---- phase 6: Y_off = e^{A_cum} Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
+      if constexpr (!SO) {
       typename W::frag hf[G::BF ? N / 32 : 1];
       if constexpr (G::BF) {
 #pragma unroll
@@ -564,6 +581,7 @@ void scan_chunked_kernel(ScanArgs a) {
           store_pair(&yodst[(16 * lb + g4 + r) * G::LDY + pcol], &yodst[(16 * lb + g4 + r + 1) * G::LDY + pcol],
                      eav[r] * yo[i][r], eav[r + 1] * yo[i][r + 1]);
       }
+      }  // !SO
       // ---- phases 4-5: h <- e^{A_end} h + (w K_s)^T V for my p-tile
       const float dec = sm.dec[pc];
 #pragma unroll
@@ -580,28 +598,28 @@ void scan_chunked_kernel(ScanArgs a) {
     }
     if ((G::NAUX > 0 || !swave) && c + 1 < nc) pre(c + 1);
     __builtin_amdgcn_s_waitcnt(0);   // staged loads and gate stores of this wave are done
-    if (G::OVL) load_z(c);           // Z for this chunk's gate, one chunk ahead
+    if (!SO && G::OVL) load_z(c);    // Z for this chunk's gate, one chunk ahead
     __syncthreads();
-    if (!G::OVL) {
+    if (!SO && !G::OVL) {
       gate(c);
       // the next chunk writes the single pair of Y tiles after its preparation barrier
     }
   }
-  if (G::OVL && nc > 0) gate(nc - 1);
+  if (!SO && G::OVL && nc > 0) gate(nc - 1);
 
-  if (a.fin_h && swave && part == 0) {
+  if (a.fin_h && fin_here && swave && part == 0) {
 #pragma unroll
     for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a.fin_h[((long)bh * P + pcol) * N + 16 * nb + g4 + r] = hs[nb][r];
+      for (int r = 0; r < 4; ++r) a.fin_h[((long)ci_out * P + pcol) * N + 16 * nb + g4 + r] = hs[nb][r];
   }
-  if (a.fin_theta && lane == 0) {
+  if (a.fin_theta && fin_here && lane == 0) {
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * G::qgroup(wave, k) + j;
-        if (r < R) a.fin_theta[(long)bh * R + r] = carry[k][j] * kTwoPi;
+        if (r < R) a.fin_theta[(long)ci_out * R + r] = carry[k][j] * kTwoPi;
       }
   }
 }
@@ -639,13 +657,40 @@ bool scan_chunked_supported(bool bf16_io, int CS_, int N, int P, int R) {
 
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
   const int CS = kernel_chunk(bf16_io, a.CS);
+  const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
 #define X(T, cs, n, p, r)                                                                            \
   if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && a.N == n && a.P == p && a.R == r) {   \
-    hipLaunchKernelGGL((scan_chunked_kernel<T, cs, n, p, r, kChunkWaves>), dim3(a.B * a.H),          \
+    hipLaunchKernelGGL((scan_chunked_kernel<T, cs, n, p, r, kChunkWaves, false>), dim3(a.B * a.H, nseg), \
                        dim3(64 * kChunkWaves), 0, st, a);                                             \
     return hipGetLastError();                                                                         \
   }
   M3_CHUNK_SHAPES(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+// The state-only pass of the sequence split (bf16, d_state 128, headdim 64: the
+// model's shapes), with its rotation widths.
+#define M3_STATE_SHAPES(X) X(128, 64, 32) X(128, 64, 64) X(128, 64, 0)
+
+bool scan_state_supported(bool bf16_io, int N, int P, int R) {
+  if (!bf16_io) return false;
+#define X(n, p, r) \
+  if (N == n && P == p && R == r) return true;
+  M3_STATE_SHAPES(X)
+#undef X
+  return false;
+}
+
+hipError_t scan_state_launch(const ScanArgs& a, hipStream_t st) {
+  const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
+#define X(n, p, r)                                                                                     \
+  if (a.N == n && a.P == p && a.R == r) {                                                              \
+    hipLaunchKernelGGL((scan_chunked_kernel<bf16, 64, n, p, r, kChunkWaves, true>), dim3(a.B * a.H, nseg), \
+                       dim3(64 * kChunkWaves), 0, st, a);                                               \
+    return hipGetLastError();                                                                           \
+  }
+  M3_STATE_SHAPES(X)
 #undef X
   return hipErrorInvalidValue;
 }

@@ -86,37 +86,45 @@ def _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z):
     return prepared, (B, L, H, HQ, N, P, R), unbatched
 
 
-def _launch(p, dims, chunk_size, out, init=None, fin=None):
+def _launch(p, dims, chunk_size, out, init=None, fin=None, seq_split=True):
     B, L, H, HQ, N, P, R = dims
     lib = _lib.load()
     io = _IO[p["V"].dtype]
     common = (_ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]),
               _ptr(p["Trap"]), _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]),
               _ptr(p["D"]), _ptr(p["Z"]), _ptr(out))
-    tail = (B, L, H, HQ, N, P, R, int(chunk_size), io, _stream(p["V"]))
-    if init is None and fin is None:
-        rc = lib.m3_chunk_scan_fwd(*common, *tail)
+    tail = (B, L, H, HQ, N, P, R, int(chunk_size), io)
+    ip = tuple(_ptr(t) for t in init) if init is not None else (None,) * 4
+    fp = tuple(_ptr(t) for t in fin) if fin is not None else (None,) * 4
+    ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, H, N, P, R, int(chunk_size), io) if seq_split else 0
+    if ws_bytes:
+        # few (batch, head) pairs: the sequence is split across compute units; the
+        # workspace lives for this call only (torch's caching allocator, same stream)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=p["V"].device)
+        rc = lib.m3_chunk_scan_fwd_ws(*common, *ip, *fp, *tail, ws.data_ptr(), ws_bytes, _stream(p["V"]))
+    elif init is None and fin is None:
+        rc = lib.m3_chunk_scan_fwd(*common, *tail, _stream(p["V"]))
     else:
-        ip = tuple(_ptr(t) for t in init) if init is not None else (None,) * 4
-        fp = tuple(_ptr(t) for t in fin) if fin is not None else (None,) * 4
-        rc = lib.m3_chunk_scan_fwd_carry(*common, *ip, *fp, *tail)
+        rc = lib.m3_chunk_scan_fwd_carry(*common, *ip, *fp, *tail, _stream(p["V"]))
     _lib.check(rc, "m3_chunk_scan_fwd")
 
 
 def mamba3_siso_hip(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
-                    chunk_size: int = 64) -> torch.Tensor:
+                    chunk_size: int = 64, seq_split: bool = True) -> torch.Tensor:
     """Mamba3 SISO chunked scan forward on gfx950.
 
     Same arguments as the reference's mamba3_siso_triton (mamba3_ops.py:1116):
     Q, K (L, Hqk, N); V, Z (L, H, P); ADT, DT, Trap (H, L) with Trap the
     pre-sigmoid logits; Q_bias, K_bias (H, N); Angles (L, H, R) raw rates;
     D (H,) or None; Z or None; or all of them with a leading batch dim.
-    Returns Out with V's shape and dtype.
+    Returns Out with V's shape and dtype.  ``seq_split`` lets a launch with few
+    (batch, head) pairs split each sequence across compute units (same result up
+    to rounding); False forces one pass.
     """
     p, dims, unbatched = _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z)
     out = torch.empty_like(p["V"])
     if out.numel():
-        _launch(p, dims, chunk_size, out)
+        _launch(p, dims, chunk_size, out, seq_split=seq_split)
     return out[0] if unbatched else out
 
 
@@ -137,7 +145,7 @@ def new_carry(B: int, H: int, N: int, P: int, R: int, device) -> Tuple[torch.Ten
 
 
 def mamba3_siso_hip_carry(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
-                          chunk_size: int = 64, initial_carry=None):
+                          chunk_size: int = 64, initial_carry=None, seq_split: bool = True):
     """Prefill that also consumes and returns the recurrent carry, so decode can
     continue where prefill stopped (the Triton kernel's HAS_INITIAL_STATES /
     RETURN_FINAL_STATES, siso_fwd.py:76-77).  Batched inputs only.
@@ -154,7 +162,7 @@ def mamba3_siso_hip_carry(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None
         for t, s, n in zip(init, shapes, ("theta", "ssm", "k", "v")):
             _req(tuple(t.shape) == s, f"initial carry {n} must be {s}, got {tuple(t.shape)}")
     if out.numel():
-        _launch(p, dims, chunk_size, out, init=init, fin=fin)
+        _launch(p, dims, chunk_size, out, init=init, fin=fin, seq_split=seq_split)
     elif init is not None:
         fin = tuple(t.clone() for t in init)
     return out, fin

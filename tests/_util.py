@@ -36,11 +36,11 @@ def to_dev(d, io_dtype, device="cuda"):
     return out
 
 
-def hip_scan(t, chunk_size, no_d=False, no_z=False):
+def hip_scan(t, chunk_size, no_d=False, no_z=False, seq_split=True):
     from mamba3_rocm import mamba3_siso_hip
     return mamba3_siso_hip(t["Q"], t["K"], t["V"], t["ADT"], t["DT"], t["Trap"], t["Q_bias"],
                            t["K_bias"], t["Angles"], None if no_d else t["D"],
-                           None if no_z else t["Z"], chunk_size)
+                           None if no_z else t["Z"], chunk_size, seq_split=seq_split)
 
 
 __all__ = ["I", "M", "rel", "oracle_scan", "to_dev", "hip_scan", "ARG_ORDER"]

@@ -25,7 +25,7 @@ def lib():
 
 def _header_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(m3_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(m3_\w+)\s*\(", text, re.M)))
 
 
 def _header_define(name):
@@ -36,7 +36,8 @@ def _header_define(name):
 def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
     assert names == sorted(["m3_abi_version", "m3_last_error", "m3_chunk_scan_impl",
-                            "m3_chunk_scan_fwd", "m3_chunk_scan_fwd_carry", "m3_decode_step"])
+                            "m3_chunk_scan_fwd", "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes",
+                            "m3_chunk_scan_fwd_ws", "m3_decode_step"])
     for n in names:
         assert hasattr(lib, n), n
     from mamba3_rocm import _lib
@@ -66,6 +67,24 @@ def test_kernel_selection(lib):
     assert f(0, 4, 4, 1, 4) == GEN              # tiny model shapes
     assert f(1, 1024, 64, 0, 64) == NONE        # state too large for either kernel
     assert f(7, 128, 64, 32, 64) == NONE        # unknown dtype
+
+
+def test_split_workspace_sizes(lib):
+    """Workspace for the sequence split: per (b, h, segment) two carries (P x N state,
+    N key, P value, R angles, each array 256-byte aligned); none when B*H already
+    fills the chip, for short sequences, fp32, or shapes without the state-only pass."""
+    f = lib.m3_chunk_scan_ws_bytes
+    bf, f32 = 1, 0
+    al = lambda n: (n * 4 + 255) // 256 * 256  # noqa: E731
+    # config 3: B*H = 32 -> 8 segments of 4096 tokens
+    bhs = 32 * 8
+    assert f(1, 32768, 32, 128, 64, 32, 128, bf) == 2 * (al(bhs * 64 * 128) + al(bhs * 128) + al(bhs * 64) + al(bhs * 32))
+    assert f(8, 4096, 32, 128, 64, 32, 64, bf) == 0          # config 2: 256 (b, h) pairs
+    assert f(1, 400, 2, 128, 64, 32, 64, bf) == 0            # too short to split
+    assert f(1, 4096, 2, 128, 64, 32, 64, f32) == 0          # fp32: one pass
+    assert f(1, 4096, 2, 64, 64, 16, 64, bf) == 0            # no state-only pass for d_state 64
+    assert f(1, 4096, 2, 128, 64, 32, 48, bf) == 0           # chunk 48: generic kernel
+    assert f(1, 1061, 3, 128, 64, 32, 64, bf) > 0
 
 
 def _scan_call(lib, **kw):

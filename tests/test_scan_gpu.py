@@ -187,6 +187,65 @@ def test_carry_split_equals_full(bf16):
         assert rel(a.cpu().numpy(), b.cpu().numpy()) <= (1e-2 if bf16 else 1e-4)
 
 
+# (B, L, H, Hqk, R, CS): shapes whose few (batch, head) pairs split the sequence
+SPLIT_SHAPES = [
+    (1, 1061, 3, 3, 32, 64),     # ragged last segment
+    (2, 700, 2, 1, 64, 128),     # GQA (one Q/K head), full-width rope, chunk 128
+    (1, 600, 2, 2, 0, 64),       # no rope
+    (1, 640, 2, 2, 32, 32),      # chunk 32: the full pass runs other chunks than the state pass
+]
+
+
+@pytest.mark.parametrize("B,L,H,Hqk,R,CS", SPLIT_SHAPES)
+def test_sequence_split_matches_oracle_and_single_pass(B, L, H, Hqk, R, CS):
+    """bf16 launches with B*H far below the CU count split each sequence into
+    segments (state-only pass, carry combine, full pass); the result matches the
+    oracle and the one-pass kernel up to rounding."""
+    torch = _torch()
+    from mamba3_rocm import _lib
+    N, P = 128, 64
+    assert _lib.load().m3_chunk_scan_ws_bytes(B, L, H, N, P, R, CS, _lib.DTYPE_BF16) > 0
+    d = I.scan_inputs(B, L, H, N, P, R, seed=21, Hqk=Hqk, bf16=True)
+    t = to_dev(d, torch.bfloat16)
+    split = hip_scan(t, CS).float().cpu().numpy()
+    single = hip_scan(t, CS, seq_split=False).float().cpu().numpy()
+    ref = oracle_scan(d, CS)
+    print(f"split {(B, L, H, Hqk, R, CS)} rel={rel(split, ref):.3e} vs single {rel(split, single):.3e}")
+    assert np.isfinite(split).all()
+    assert rel(split, ref) <= BF16_TOL
+    assert rel(split, single) <= BF16_TOL
+
+
+def test_sequence_split_carry_in_and_out():
+    """The split path consumes an initial carry (segment 0) and returns the last
+    segment's exit carry, like the one-pass kernel."""
+    torch = _torch()
+    from mamba3_rocm import mamba3_siso_hip_carry
+    B, L, H, N, P, R = 1, 900, 2, 128, 64, 32
+    L1 = 100
+    d = I.scan_inputs(B, L1 + L, H, N, P, R, seed=22, bf16=True)
+    t = to_dev(d, torch.bfloat16)
+
+    def part(lo, hi, carry, split):
+        s = {k: (v[:, lo:hi] if k in ("Q", "K", "V", "Z", "Angles") else
+                 v[:, :, lo:hi] if k in ("ADT", "DT", "Trap") else v) for k, v in t.items()}
+        return mamba3_siso_hip_carry(s["Q"], s["K"], s["V"], s["ADT"], s["DT"], s["Trap"],
+                                     s["Q_bias"], s["K_bias"], s["Angles"], s["D"], s["Z"], 64,
+                                     initial_carry=carry, seq_split=split)
+
+    _, c1 = part(0, L1, None, False)
+    y_split, c_split = part(L1, L1 + L, c1, True)
+    y_one, c_one = part(L1, L1 + L, c1, False)
+    torch.cuda.synchronize()
+    ref = oracle_scan(d, 64)[:, L1:]
+    assert rel(y_split.float().cpu().numpy(), ref) <= BF16_TOL
+    assert rel(y_split.float().cpu().numpy(), y_one.float().cpu().numpy()) <= BF16_TOL
+    th_a, th_b = c_split[0].cpu().numpy(), c_one[0].cpu().numpy()
+    assert rel(np.cos(th_a), np.cos(th_b)) <= 1e-4 and rel(np.sin(th_a), np.sin(th_b)) <= 1e-4
+    for a, b in zip(c_split[1:], c_one[1:]):
+        assert rel(a.cpu().numpy(), b.cpu().numpy()) <= 1e-2
+
+
 def test_only_one_hip_runtime_loaded():
     """The library binds to torch's HIP runtime (one libamdhip64 in the process)."""
     import os
