@@ -199,7 +199,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=("scan", "decode", "copy"), default="scan")
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "copy"), default="scan")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -223,6 +223,15 @@ def main():
     if args.mode == "decode":
         r = bench_decode(torch, 512, 32, 128, 64, 32, args.steps, args.warmup, seed=4)
         print(json.dumps({"mode": "decode", **r}), flush=True)
+        return
+
+    if args.mode == "long":
+        # config 3 alone (B*H = 32: the sequence split runs), for profiling
+        r = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3)
+        print(json.dumps({"mode": "long", "kernel_ms": round(r["kernel_s"] * 1e3, 4),
+                          "tokens_per_s": round(32768 / r["wall_s"], 1),
+                          "achieved_gbs": round(r["achieved_gbs"], 1),
+                          "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
 
     B, L, H, N, P, R, CS = 8, 4096, 32, 128, 64, 32, 64

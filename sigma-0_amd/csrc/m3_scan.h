@@ -26,6 +26,8 @@ struct ScanArgs {
   // (b, h) (init used by segment 0, fin written by the last segment) or, with
   // init_per_seg / fin_per_seg, one per (b, h, segment) at index bh * nseg + seg.
   int seg_len = 0, init_per_seg = 0, fin_per_seg = 0;
+  // State-only pass: the segment's total log-decay (sum of adt), one float per carry slot.
+  float* fin_logdec = nullptr;
 };
 
 bool scan_generic_supported(int N, int P, int R);

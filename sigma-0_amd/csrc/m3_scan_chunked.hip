@@ -275,6 +275,7 @@ void scan_chunked_kernel(ScanArgs a) {
   // the angles of its own rope pairs in registers.
   constexpr int kScalarWave = G::NAUX ? NW - 1 : 0;
   float p_cs[G::QGW][4], p_sn[G::QGW][4];
+  float logdec = 0.0f;                     // state-only pass: sum of the chunks' log-decays
   auto pre = [&](int cc) {
     const int t0 = cc * CS;
     const int pb = cc & 1;
@@ -301,6 +302,7 @@ void scan_chunked_kernel(ScanArgs a) {
         sm.g16[pb][lane] = exp2_fast((ablk - acum) * kLog2e);
         sm.dg[pb][lane] = scl != 0.0f ? gam * rcp_fast(scl) : 0.0f;
         if (lane == 0) sm.dec[pb] = exp2_fast(aend * kLog2e);
+        if constexpr (SO) logdec += aend;
       }
     }
 #pragma unroll
@@ -612,6 +614,9 @@ void scan_chunked_kernel(ScanArgs a) {
     for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) a.fin_h[((long)ci_out * P + pcol) * N + 16 * nb + g4 + r] = hs[nb][r];
+  }
+  if constexpr (SO) {
+    if (a.fin_logdec && fin_here && wave == kScalarWave && lane == 0) a.fin_logdec[ci_out] = logdec;
   }
   if (a.fin_theta && fin_here && lane == 0) {
 #pragma unroll

@@ -5,11 +5,11 @@
 // sequence can be cut into S segments that run side by side:
 //
 //   pass 1  the state-only kernel runs every segment from a zero carry and leaves
-//           its exit state h_i^0 and rope angle advance Δθ_i, with keys rotated by
-//           the segment's own angles (starting from zero).  A segment's last
+//           its exit state h_i^0, rope angle advance Δθ_i and total log-decay ΣA_i,
+//           with keys rotated by the segment's own angles (starting from zero).  A segment's last
 //           token already carries the trapezoid's cross term with the next token
 //           (its key scale reads the next token), so h_i^0 is complete;
-//   pass 2  one block per (b, h) chains the segments: the state entering segment
+//   pass 2  the combine chains the segments, one thread per state element: the state entering segment
 //           i+1 is  h' = e^{ΣA_i} h + h_i^0 rot(θ)^T  and  θ' = θ + Δθ_i (mod 2π),
 //           where rot(θ) turns the rope pairs (2r, 2r+1) of the state's d_state axis
 //           by the entering angles (a rotation by θ + φ is rotation by φ, then θ).
@@ -30,7 +30,6 @@ namespace {
 constexpr int kCombineThreads = 256;
 constexpr int kTargetBlocks = 256;     // MI355X compute units
 constexpr int kMinSegment = 256;       // tokens
-constexpr int kMaxRope = 64;           // rope pairs: R <= d_state / 2 <= 64 for the split shapes
 
 // Segment length for a (B, H, L) launch, or 0 for no split.  Segments are whole
 // multiples of 128 tokens, so every interior segment ends on a kernel chunk.
@@ -48,6 +47,7 @@ struct Carries {
   float* k;   // (BH, S, N)   last rope'd key (pass 1 writes it; the combine does not need it)
   float* v;   // (BH, S, P)
   float* th;  // (BH, S, R)
+  float* ld;  // (BH, S)      pass 1: the segment's total log-decay
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -61,67 +61,74 @@ size_t carve(char* base, long bhs, int N, int P, int R, Carries* loc, Carries* i
     return p;
   };
   Carries* sets[2] = {loc, in};
-  for (Carries* c : sets) {
+  for (int set = 0; set < 2; ++set) {
+    Carries* c = sets[set];
     Carries t;
     t.h = take((size_t)bhs * P * N);
     t.k = take((size_t)bhs * N);
     t.v = take((size_t)bhs * P);
     t.th = take((size_t)bhs * (R > 0 ? R : 1));
+    t.ld = set == 0 ? take((size_t)bhs) : nullptr;
     if (c) *c = t;
   }
   return off;
 }
 
+// Grid (P*N / kCombineThreads, B*H): thread -> state element (p, n) of one (b, h),
+// walking the segments in order.  Block x == 0 also writes the small carry parts
+// (angles, zero k and v of segments 1..).
 __global__ __launch_bounds__(kCombineThreads)
 void seg_combine_kernel(ScanArgs a, int nseg, Carries loc, Carries in) {
-  __shared__ float red[kCombineThreads];
-  __shared__ float cs_[kMaxRope], sn_[kMaxRope];
-  const int bh = blockIdx.x, tid = threadIdx.x;
-  const int N = a.N, P = a.P, R = a.R, L = a.L, len = a.seg_len;
+  const int bh = blockIdx.y, tid = threadIdx.x;
+  const int N = a.N, P = a.P, R = a.R;
   const long c0 = (long)bh * nseg;                 // carry slot of segment 0
-  // segment 0 enters with the caller's carry, or zero
-  for (int e = tid; e < P * N; e += kCombineThreads) in.h[c0 * P * N + e] = a.init_h ? a.init_h[(long)bh * P * N + e] : 0.0f;
-  for (int n = tid; n < N; n += kCombineThreads) in.k[c0 * N + n] = a.init_k ? a.init_k[(long)bh * N + n] : 0.0f;
-  for (int p = tid; p < P; p += kCombineThreads) in.v[c0 * P + p] = a.init_v ? a.init_v[(long)bh * P + p] : 0.0f;
-  for (int r = tid; r < R; r += kCombineThreads) in.th[c0 * R + r] = a.init_theta ? a.init_theta[(long)bh * R + r] : 0.0f;
-  __syncthreads();
-  const float* adt = a.adt + (long)bh * L;
-  for (int i = 0; i + 1 < nseg; ++i) {
-    const long ci = c0 + i, cn = ci + 1;
-    const int t0 = i * len, t1 = min(L, t0 + len);
-    // e^{sum of A dt over the segment}
-    float sum = 0.0f;
-    for (int t = t0 + tid; t < t1; t += kCombineThreads) sum += adt[t];
-    red[tid] = sum;
-    __syncthreads();
-    for (int w = kCombineThreads / 2; w > 0; w >>= 1) {
-      if (tid < w) red[tid] += red[tid + w];
-      __syncthreads();
+  const int e = blockIdx.x * kCombineThreads + tid;
+  if (blockIdx.x == 0) {
+    for (int n = tid; n < N; n += kCombineThreads) {
+      in.k[c0 * N + n] = a.init_k ? a.init_k[(long)bh * N + n] : 0.0f;
+      for (int i = 1; i < nseg; ++i) in.k[(c0 + i) * N + n] = 0.0f;
     }
-    const float dec = expf(red[0]);
-    // cross term of the first token with the previous one: only for the caller's
-    // carry (segment 0); later carries hold zero k and v
-    const float dt0 = a.dt[(long)bh * L + t0], tr0 = a.trap[(long)bh * L + t0];
-    const float cross = i == 0 ? (1.0f - 1.0f / (1.0f + expf(-tr0))) * dt0 : 0.0f;
-    for (int r = tid; r < R; r += kCombineThreads) sincosf(in.th[ci * R + r], &sn_[r], &cs_[r]);
-    __syncthreads();
-    const float* lh = loc.h + ci * P * N;
-    for (int e = tid; e < P * N; e += kCombineThreads) {
-      const int p = e / N, n = e % N, r = n >> 1;
-      float own = lh[e];
-      if (r < R) {                       // segment-local key frame -> entering frame
-        const float h0 = lh[p * N + 2 * r], h1 = lh[p * N + 2 * r + 1];
-        own = (n & 1) ? h0 * sn_[r] + h1 * cs_[r] : h0 * cs_[r] - h1 * sn_[r];
-      }
-      in.h[cn * P * N + e] = dec * (in.h[ci * P * N + e] + cross * in.v[ci * P + p] * in.k[ci * N + n]) + own;
+    for (int p = tid; p < P; p += kCombineThreads) {
+      in.v[c0 * P + p] = a.init_v ? a.init_v[(long)bh * P + p] : 0.0f;
+      for (int i = 1; i < nseg; ++i) in.v[(c0 + i) * P + p] = 0.0f;
     }
-    for (int p = tid; p < P; p += kCombineThreads) in.v[cn * P + p] = 0.0f;
-    for (int n = tid; n < N; n += kCombineThreads) in.k[cn * N + n] = 0.0f;
     for (int r = tid; r < R; r += kCombineThreads) {
-      const float x = in.th[ci * R + r] + loc.th[ci * R + r];
-      in.th[cn * R + r] = x - kTwoPi * floorf(x * kInvTwoPi);
+      float th = a.init_theta ? a.init_theta[(long)bh * R + r] : 0.0f;
+      in.th[c0 * R + r] = th;
+      for (int i = 0; i + 1 < nseg; ++i) {
+        const float x = th + loc.th[(c0 + i) * R + r];
+        th = x - kTwoPi * floorf(x * kInvTwoPi);
+        in.th[(c0 + i + 1) * R + r] = th;
+      }
     }
-    __syncthreads();
+  }
+  if (e >= P * N) return;
+  const int p = e / N, n = e % N, r = n >> 1;
+  const bool rope = r < R;
+  // segment 0 enters with the caller's carry, or zero; its cross term with the
+  // previous token (c = (1 - sigmoid(trap_0)) dt_0) is added here, as the kernel
+  // adds it to an entering carry
+  float h = a.init_h ? a.init_h[(long)bh * P * N + e] : 0.0f;
+  in.h[c0 * P * N + e] = h;
+  if (a.init_h) {
+    const float dt0 = a.dt[(long)bh * a.L], tr0 = a.trap[(long)bh * a.L];
+    h += (1.0f - 1.0f / (1.0f + expf(-tr0))) * dt0 * a.init_v[(long)bh * P + p] * a.init_k[(long)bh * N + n];
+  }
+  float th = rope && a.init_theta ? a.init_theta[(long)bh * R + r] : 0.0f;
+  for (int i = 0; i + 1 < nseg; ++i) {
+    const long ci = c0 + i;
+    const float* lh = loc.h + ci * P * N;
+    float own = lh[e];
+    if (rope) {                          // segment-local key frame -> entering frame
+      float sn, cs;
+      sincosf(th, &sn, &cs);
+      const float h0 = lh[p * N + 2 * r], h1 = lh[p * N + 2 * r + 1];
+      own = (n & 1) ? h0 * sn + h1 * cs : h0 * cs - h1 * sn;
+      const float x = th + loc.th[ci * R + r];
+      th = x - kTwoPi * floorf(x * kInvTwoPi);
+    }
+    h = expf(loc.ld[ci]) * h + own;
+    in.h[(ci + 1) * P * N + e] = h;
   }
 }
 
@@ -129,7 +136,7 @@ void seg_combine_kernel(ScanArgs a, int nseg, Carries loc, Carries in) {
 
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS) {
   const int len = seg_len_for(B, H, L);
-  if (len == 0 || R > kMaxRope || !scan_state_supported(bf16_io, N, P, R) || !scan_chunked_supported(bf16_io, CS, N, P, R))
+  if (len == 0 || !scan_state_supported(bf16_io, N, P, R) || !scan_chunked_supported(bf16_io, CS, N, P, R))
     return 0;
   const long bhs = (long)B * H * ((L + len - 1) / len);
   return carve(nullptr, bhs, N, P, R, nullptr, nullptr);
@@ -146,13 +153,15 @@ hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStrea
   p1.seg_len = len;
   p1.init_theta = p1.init_h = p1.init_k = p1.init_v = nullptr;
   p1.fin_h = loc.h; p1.fin_k = loc.k; p1.fin_v = loc.v; p1.fin_theta = a.R > 0 ? loc.th : nullptr;
+  p1.fin_logdec = loc.ld;
   p1.fin_per_seg = 1;
   hipError_t e = scan_state_launch(p1, st);
   if (e != hipSuccess) return e;
 
   ScanArgs p2 = a;                                   // pass 2: entering carries
   p2.seg_len = len;
-  hipLaunchKernelGGL(seg_combine_kernel, dim3(a.B * a.H), dim3(kCombineThreads), 0, st, p2, nseg, loc, in);
+  hipLaunchKernelGGL(seg_combine_kernel, dim3((a.P * a.N + kCombineThreads - 1) / kCombineThreads, a.B * a.H),
+                     dim3(kCombineThreads), 0, st, p2, nseg, loc, in);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
 

@@ -71,14 +71,16 @@ def test_kernel_selection(lib):
 
 def test_split_workspace_sizes(lib):
     """Workspace for the sequence split: per (b, h, segment) two carries (P x N state,
-    N key, P value, R angles, each array 256-byte aligned); none when B*H already
-    fills the chip, for short sequences, fp32, or shapes without the state-only pass."""
+    N key, P value, R angles, each array 256-byte aligned) and one log-decay; none
+    when B*H already fills the chip, for short sequences, fp32, or shapes without the
+    state-only pass."""
     f = lib.m3_chunk_scan_ws_bytes
     bf, f32 = 1, 0
     al = lambda n: (n * 4 + 255) // 256 * 256  # noqa: E731
     # config 3: B*H = 32 -> 8 segments of 4096 tokens
     bhs = 32 * 8
-    assert f(1, 32768, 32, 128, 64, 32, 128, bf) == 2 * (al(bhs * 64 * 128) + al(bhs * 128) + al(bhs * 64) + al(bhs * 32))
+    assert f(1, 32768, 32, 128, 64, 32, 128, bf) == (2 * (al(bhs * 64 * 128) + al(bhs * 128) + al(bhs * 64) + al(bhs * 32))
+                                                     + al(bhs))
     assert f(8, 4096, 32, 128, 64, 32, 64, bf) == 0          # config 2: 256 (b, h) pairs
     assert f(1, 400, 2, 128, 64, 32, 64, bf) == 0            # too short to split
     assert f(1, 4096, 2, 128, 64, 32, 64, f32) == 0          # fp32: one pass
