@@ -118,6 +118,37 @@ int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
                          int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Device workspace (bytes) that m3_chunk_scan_bwd needs for a shape; 0 when the
+ * backward has no kernel for (io_dtype, N, P, R).  About 2 * B*H*L*P*N/CS * the
+ * element size (the state entering and the adjoint state after each chunk).
+ */
+size_t m3_chunk_scan_bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
+                                  int io_dtype);
+
+/*
+ * Backward of m3_chunk_scan_fwd: the reference's custom_vjp backward of
+ * mamba3_siso_triton (src/base_model/models/mamba3_ops.py:821-902, gradients in
+ * the forward's argument order).  Inputs are the forward's inputs and dOut (like
+ * V); outputs, written whole:
+ *   dQ, dK (B,L,Hqk,N) and dV (B,L,H,P) in io_dtype (with Hqk < H, dQ and dK sum
+ *   the value heads that share a Q/K head); dZ like Z (NULL when Z is NULL);
+ *   dADT, dDT, dTrap (B,H,L), dAngles (B,L,H,R) float32 (dAngles may be NULL
+ *   when R = 0); dQ_bias, dK_bias (H,N) and dD (H,) float32 (dD NULL when D is
+ *   NULL), summed over the batch.
+ * The chunk size does not change the gradients (the chunked form is exact).  The
+ * workspace (>= m3_chunk_scan_bwd_ws_bytes, 16-byte aligned) is scratch for the
+ * call.  Deterministic: no atomics, fixed summation order.
+ */
+int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
+                      const float* ADT, const float* DT, const float* Trap,
+                      const float* Q_bias, const float* K_bias, const float* Angles,
+                      const float* D, const void* Z, const void* dOut,
+                      void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                      float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                      int B, int L, int H, int Hqk, int N, int P, int R,
+                      int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * One decode step for a batch, in place on the carry.  Replaces the body of
  * rnn_step inside Mamba3SSM.__call_rnn__ (src/base_model/models/mamba3.py:498-562)
  * vmapped over batch (lob_seq_model.py:747-751):

@@ -150,6 +150,61 @@ int m3_chunk_scan_fwd(const void* Q, const void* K, const void* V,
                                  B, L, H, Hqk, N, P, R, chunk_size, io_dtype, stream);
 }
 
+size_t m3_chunk_scan_bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
+                                  int io_dtype) {
+  if ((io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16) || B <= 0 || L <= 0 || H <= 0 || Hqk <= 0 ||
+      H % Hqk != 0 || chunk_size <= 0)
+    return 0;
+  return m3::scan_bwd_ws_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, Hqk, N, P, R);
+}
+
+int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
+                      const float* ADT, const float* DT, const float* Trap,
+                      const float* Q_bias, const float* K_bias, const float* Angles,
+                      const float* D, const void* Z, const void* dOut,
+                      void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                      float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                      int B, int L, int H, int Hqk, int N, int P, int R,
+                      int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
+    return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d H=%d Hqk=%d N=%d P=%d R=%d chunk=%d)",
+                B, L, H, Hqk, N, P, R, chunk_size);
+  if (H % Hqk != 0) return fail(M3_E_ARG, "nheads (%d) must be divisible by nheads_qk (%d)", H, Hqk);
+  if (2 * R > N) return fail(M3_E_ARG, "num rope angles R=%d must be <= d_state/2 = %d", R, N / 2);
+  const bool bf = io_dtype == M3_DTYPE_BF16;
+  if (!m3::scan_bwd_supported(bf, N, P, R))
+    return fail(M3_E_UNSUPPORTED, "no backward kernel for io_dtype=%d d_state=%d headdim=%d R=%d", io_dtype, N, P, R);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!Q || !K || !V || !ADT || !DT || !Trap || !Q_bias || !K_bias || (R > 0 && !Angles) || !dOut || !dQ || !dK ||
+      !dV || !dADT || !dDT || !dTrap || !dQ_bias || !dK_bias || (R > 0 && !dAngles))
+    return fail(M3_E_ARG, "NULL required pointer");
+  if ((Z == nullptr) != (dZ == nullptr)) return fail(M3_E_ARG, "pass dZ exactly when Z is given");
+  const void* vec_ptrs[] = {Q, K, V, Z, dOut, dQ, dK, dV, dZ};
+  for (const void* p : vec_ptrs)
+    if (!aligned16(p)) return fail(M3_E_ALIGN, "Q, K, V, Z, dOut and their gradients must be 16-byte aligned");
+  const size_t need = m3::scan_bwd_ws_bytes(bf, B, L, H, Hqk, N, P, R);
+  if (ws == nullptr || ws_bytes < need)
+    return fail(M3_E_ARG, "workspace of %zu bytes, the backward needs %zu (m3_chunk_scan_bwd_ws_bytes)", ws_bytes, need);
+  if (!aligned16(ws)) return fail(M3_E_ALIGN, "workspace must be 16-byte aligned");
+  m3::ScanBwd g;
+  m3::ScanArgs& a = g.fwd;
+  a.q = Q; a.k = K; a.v = V; a.adt = ADT; a.dt = DT; a.trap = Trap;
+  a.qbias = Q_bias; a.kbias = K_bias; a.ang = Angles; a.D = D; a.z = Z; a.out = nullptr;
+  a.init_theta = a.init_h = a.init_k = a.init_v = nullptr;
+  a.fin_theta = a.fin_h = a.fin_k = a.fin_v = nullptr;
+  a.B = B; a.L = L; a.H = H; a.Hqk = Hqk; a.N = N; a.P = P; a.R = R; a.CS = chunk_size;
+  g.dout = dOut;
+  g.dq = dQ; g.dk = dK; g.dv = dV; g.dz = dZ;
+  g.dadt = dADT; g.ddt = dDT; g.dtrap = dTrap; g.dang = dAngles;
+  g.dqb = dQ_bias; g.dkb = dK_bias; g.dD = D ? dD : nullptr;
+  return check_launch(m3::scan_bwd_launch(g, bf, ws, reinterpret_cast<hipStream_t>(stream)), "scan backward");
+}
+
 int m3_decode_step(float* theta, float* ssm, float* k, float* v,
                    const void* x, const void* z, const void* Bt, const void* Ct,
                    const float* adt, const float* dt, const float* trap, const float* angle,

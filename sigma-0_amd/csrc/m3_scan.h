@@ -28,6 +28,11 @@ struct ScanArgs {
   int seg_len = 0, init_per_seg = 0, fin_per_seg = 0;
   // State-only pass: the segment's total log-decay (sum of adt), one float per carry slot.
   float* fin_logdec = nullptr;
+  // State-only pass for the backward: the state entering every chunk, [bh][chunk][P][N]
+  // in the I/O type, and the rope angle entering every chunk, [bh][chunk][R], in
+  // revolutions.
+  void* chunk_h = nullptr;
+  float* chunk_th = nullptr;
 };
 
 bool scan_generic_supported(int N, int P, int R);
@@ -37,9 +42,21 @@ hipError_t scan_generic_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
 bool scan_chunked_supported(bool bf16_io, int CS, int N, int P, int R);
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
 
-// State-only pass of the chunked kernel (sequence split, pass 1).
-bool scan_state_supported(bool bf16_io, int N, int P, int R);
-hipError_t scan_state_launch(const ScanArgs& a, hipStream_t st);
+// State-only pass of the chunked kernel (sequence split pass 1, backward chunk states).
+bool scan_state_supported(bool bf16_io, int CS, int N, int P, int R);
+hipError_t scan_state_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
+
+// Backward: gradients of every input for a forward call described by fwd.
+struct ScanBwd {
+  ScanArgs fwd;
+  const void* dout;                                    // like V, io dtype
+  void* dq; void* dk; void* dv; void* dz;              // io dtype; dz null without Z
+  float* dadt; float* ddt; float* dtrap; float* dang;  // like ADT, DT, Trap, Angles
+  float* dqb; float* dkb; float* dD;                   // (H, N), (H, N), (H,) or null
+};
+bool scan_bwd_supported(bool bf16_io, int N, int P, int R);
+size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R);
+hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st);
 
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS);

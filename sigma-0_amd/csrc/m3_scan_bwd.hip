@@ -1,0 +1,808 @@
+// Backward of the chunked Mamba3 SISO scan on CDNA4 matrix cores.
+//
+// Gradients of every input of mamba3_siso_triton (the reference's custom_vjp,
+// src/base_model/models/mamba3_ops.py:821-902, output order (dQ, dK, dV, dADT, dDT,
+// dTrap, dQ_bias, dK_bias, dAngles, dD, dZ)).  With q~ = rot(q + qb), k~ = scale
+// rot(k + kb), A the running sum of adt and dy = dOut silu(z):
+//
+//   y_t   = sum_{s<t} (q~_t . k~_s) e^{A_t - A_s} v_s + (D + gamma_t (q^.k^)_t) v_t
+//   dv_s  = sum_{t>s} (q~_t . k~_s) e^{A_t - A_s} dy_t + (D + QK_s) dy_s
+//   dq~_t = sum_{s<t} e^{A_t - A_s} (dy_t . v_s) k~_s
+//   dk~_s = sum_{t>s} e^{A_t - A_s} (dy_t . v_s) q~_t
+//   dA_t  = q~_t . dq~_t - k~_t . dk~_t,   dadt = reverse cumsum of dA
+//
+// and the chain through rope, bias, trapezoid weights and the angle cumsum.  Four
+// launches per call:
+//   1. the chunked kernel's state-only pass saves the state entering every chunk
+//      h_c and the rope angle entering it (scan_state_launch with chunk_h/chunk_th);
+//   2. scan_adjoint_kernel walks each (b, h) backwards and saves the adjoint state
+//      G_c = sum_{t after chunk c} e^{A_t - A_end(c)} dy_t (x) q~_t of every chunk;
+//   3. scan_bwd_chunk_kernel, one workgroup per (chunk, b, h), computes the chunk's
+//      terms from h_c and G_c on MFMA: dZ, dV, dQ, dK, and per token dA, d(theta),
+//      d(scale), d(gamma) (kept in the dADT, dAngles, dTrap, dDT outputs);
+//   4. scan_bwd_finish_kernel turns those into dADT, dAngles, dDT, dTrap (reverse
+//      cumsums over the sequence, the trapezoid and angle chains), and
+//      scan_bwd_reduce_kernel sums the bias and D gradients over batch and chunks.
+// Every sum runs in a fixed order, so the gradients are deterministic.
+#include <type_traits>
+
+#include "m3_chunk_common.h"
+
+namespace m3 {
+namespace {
+
+constexpr int kBwdWaves = 8;
+constexpr int kBwdThreads = 64 * kBwdWaves;
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// MFMA operand whose 16 rows (A) or columns (B) are columns c0.. of a row-major
+// [k][col] LDS matrix: the transpose of what MF16::ld reads.  bf16: two
+// ds_read_b64_tr_b16, each giving lane l the column c0 + l%16 of a 4 x 16 block
+// (lane 4j+q addresses row j, columns 4q..4q+3).
+__device__ __forceinline__ bf16x8 ld_tr(const bf16* buf, int ld, int k0, int c0, int lane) {
+  const int g = lane >> 4, l = lane & 15;
+  const bf16* p = buf + (k0 + 8 * g + (l >> 2)) * ld + c0 + 4 * (l & 3);
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * ld));
+  bf16x8 f;
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+  f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+  return f;
+}
+__device__ __forceinline__ float ld_tr(const float* buf, int ld, int k0, int c0, int lane) {
+  return buf[(k0 + (lane >> 4)) * ld + c0 + (lane & 15)];
+}
+
+// Angle increment of a token in revolutions, tanh(rate) pi dt / 2pi, with the same
+// arithmetic as the forward kernel (so the saved chunk angles continue exactly).
+__device__ __forceinline__ float angle_step(float rate, float dt) {
+  const float rcp = rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rate));
+  return fmaf(-dt, rcp, 0.5f * dt);
+}
+
+// Rotate the four rope pairs of 8-column group g by the token's angles th4 (inverse
+// rotation with sgn = -1); pairs r >= R pass through.
+template <int R>
+__device__ __forceinline__ void rope8(float x[8], const float th4[4], int g, float sgn) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * g + j;
+    if (r < R) {
+      const float c = __builtin_amdgcn_cosf(th4[j]), s = sgn * __builtin_amdgcn_sinf(th4[j]);
+      const float x0 = x[2 * j], x1 = x[2 * j + 1];
+      x[2 * j] = x0 * c - x1 * s;
+      x[2 * j + 1] = x0 * s + x1 * c;
+    }
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+// Reverse inclusive scan over the 64 lanes (lane i gets the sum over lanes >= i).
+__device__ __forceinline__ float wave_rev_scan(float v, int lane) {
+  v = __shfl(v, 63 - lane, 64);
+  v = wave_incl_scan(v);
+  return __shfl(v, 63 - lane, 64);
+}
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float f[8]) {
+  Vec8<T> v;
+  v.load(p);
+  v.to_f(f);
+}
+
+struct BwdArgs {
+  ScanArgs s;                  // forward inputs and dims (s.CS: the kernel chunk)
+  const void* dout;
+  void* dq; void* dk; void* dv; void* dz;
+  float* dadt; float* ddt; float* dtrap; float* dang; float* dqb; float* dkb; float* dD;
+  const void* hs;              // [bh][nc][P][N] T: state entering each chunk
+  void* gs;                    // [bh][nc][N][P] T: adjoint state after each chunk
+  const float* th0;            // [bh][nc][R] revolutions: angle entering each chunk
+  float* pqb; float* pkb;      // [bh][nc][N] partial bias gradients
+  float* pd;                   // [bh][nc] partial D gradient
+  float* dqh; float* dkh;      // GQA: per-head dQ, dK (B, L, H, N) f32, else null
+  int nc;
+};
+
+// Per-chunk token constants shared by the adjoint and gradient kernels: lane = token.
+template <int CS>
+__device__ __forceinline__ void chunk_scalars(const BwdArgs& a, int bh, int t0, int lane, float* ac, float* gam,
+                                              float* scl, float* dtv, float* aend) {
+  const int L = a.s.L;
+  const bool tok = lane < CS && t0 + lane < L;
+  const long base = (long)bh * L + t0;
+  const float adt = tok ? a.s.adt[base + lane] : 0.0f;
+  const float dt = tok ? a.s.dt[base + lane] : 0.0f;
+  const float tr = tok ? a.s.trap[base + lane] : 0.0f;
+  const float sg = 1.0f / (1.0f + expf(-tr));
+  const float gm = dt * sg;
+  float un = __shfl_down(dt * (1.0f - sg), 1, 64);                  // next token's dt (1 - sigmoid)
+  if (lane == CS - 1) {
+    const bool nxt = t0 + CS < L;
+    const float dtn = nxt ? a.s.dt[base + CS] : 0.0f, trn = nxt ? a.s.trap[base + CS] : 0.0f;
+    un = dtn * (1.0f - 1.0f / (1.0f + expf(-trn)));
+  }
+  const float acum = wave_incl_scan(lane < CS ? adt : 0.0f);
+  const float ae = __shfl(acum, CS - 1, 64);
+  if (lane < CS) {
+    ac[lane] = acum;
+    gam[lane] = gm;
+    scl[lane] = tok ? gm + un : 0.0f;
+    dtv[lane] = dt;
+  }
+  if (lane == 0) *aend = ae;
+}
+
+// Rope angles (revolutions) of this lane's token for the pairs 4g..4g+3 of column
+// group g: the angle entering the chunk plus a wave scan of the increments.  Call
+// with the whole wave (g uniform).
+template <int CS, int R>
+__device__ __forceinline__ void group_theta(const BwdArgs& a, int b, int h, int bh, int c, int t0, int g, int lane,
+                                            float th4[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) th4[j] = 0.0f;
+  if constexpr (R > 0) {
+    if (4 * g >= R) return;
+    const int L = a.s.L, H = a.s.H;
+    const bool tok = lane < CS && t0 + lane < L;
+    const float dt = tok ? a.s.dt[(long)bh * L + t0 + lane] : 0.0f;
+    float4 rt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (tok) rt = *reinterpret_cast<const float4*>(a.s.ang + (((long)b * L + t0 + lane) * H + h) * R + 4 * g);
+    const float rv[4] = {rt.x, rt.y, rt.z, rt.w};
+    const float* t0c = a.th0 + ((long)bh * a.nc + c) * R + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * g + j < R) th4[j] = __builtin_amdgcn_fractf(t0c[j] + wave_incl_scan(angle_step(rv[j], dt)));
+  }
+}
+
+// ------------------------------------------------------------------ adjoint pass
+template <typename T, int CS, int N, int P, int R>
+struct AdjSmem {
+  static constexpr int PAD = std::is_same<T, bf16>::value ? 8 : 4;
+  alignas(16) T qt[CS][N + PAD];      // q~ of the chunk
+  alignas(16) T dye[CS][P + PAD];     // e^{A_cum} dy
+  float ac[CS], gam[CS], scl[CS], dtv[CS];
+  float aend;
+};
+
+template <typename T, int CS, int N, int P, int R>
+__global__ __launch_bounds__(kBwdThreads, 1)
+void scan_adjoint_kernel(BwdArgs a) {
+  typedef MF16<T> W;
+  typedef AdjSmem<T, CS, N, P, R> S;
+  __shared__ S sm;
+  constexpr int PAD = S::PAD, KS = W::KSTEP;
+  constexpr int NTILE = (P / 16) * (N / 16), TPW = (NTILE + kBwdWaves - 1) / kBwdWaves;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh = blockIdx.x, b = bh / a.s.H, h = bh % a.s.H;
+  const int hq = h / (a.s.H / a.s.Hqk);
+  const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
+  const T* gq = reinterpret_cast<const T*>(a.s.q);
+  const T* gdo = reinterpret_cast<const T*>(a.dout);
+  const T* gz = reinterpret_cast<const T*>(a.s.z);
+  T* gs = reinterpret_cast<T*>(a.gs);
+
+  f32x4 G[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) G[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int c = nc - 1; c >= 0; --c) {
+    const int t0 = c * CS;
+    // adjoint state beyond chunk c, [n][p]
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = wave + kBwdWaves * i;
+      if (tile < NTILE) {
+        const int pt = tile / (N / 16), nt = tile % (N / 16);
+        const int n = 16 * nt + (lane & 15), p = 16 * pt + 4 * (lane >> 4);
+        const float gv[4] = {G[i][0], G[i][1], G[i][2], G[i][3]};
+        store4(gs + (((long)bh * nc + c) * N + n) * P + p, gv);
+      }
+    }
+    if (wave == 0) chunk_scalars<CS>(a, bh, t0, lane, sm.ac, sm.gam, sm.scl, sm.dtv, &sm.aend);
+    __syncthreads();
+    const bool tok = lane < CS && t0 + lane < L;
+    for (int g = wave; g < N / 8; g += kBwdWaves) {
+      float q[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th4[4];
+      group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
+      if (tok) {
+        load8(gq + (((long)b * L + t0 + lane) * HQ + hq) * N + 8 * g, q);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] += a.s.qbias[(long)h * N + 8 * g + e];
+        rope8<R>(q, th4, g, 1.0f);
+      }
+      if (lane < CS) store8(&sm.qt[lane][8 * g], q);
+    }
+    for (int g = wave; g < P / 8; g += kBwdWaves) {
+      float dy[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (tok) {
+        const long row = (((long)b * L + t0 + lane) * H + h) * P + 8 * g;
+        load8(gdo + row, dy);
+        if (gz) {
+          float z[8];
+          load8(gz + row, z);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[e] *= z[e] / (1.0f + expf(-z[e]));
+        }
+        const float ea = expf(sm.ac[lane]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dy[e] *= ea;
+      }
+      if (lane < CS) store8(&sm.dye[lane][8 * g], dy);
+    }
+    __syncthreads();
+    // G <- e^{A_end} G + sum_t e^{A_cum,t} dy_t (x) q~_t
+    const float dec = expf(sm.aend);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = wave + kBwdWaves * i;
+      if (tile < NTILE) {
+        const int pt = tile / (N / 16), nt = tile % (N / 16);
+        f32x4 acc = G[i] * dec;
+#pragma unroll
+        for (int k0 = 0; k0 < CS; k0 += KS)
+          acc = W::mma(ld_tr(&sm.dye[0][0], P + PAD, k0, 16 * pt, lane), ld_tr(&sm.qt[0][0], N + PAD, k0, 16 * nt, lane),
+                       acc);
+        G[i] = acc;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------ per-chunk gradients
+template <typename T, int CS, int N, int P, int R>
+struct GradSmem {
+  static constexpr int PAD = std::is_same<T, bf16>::value ? 8 : 4;
+  static constexpr int NH = N / 2;     // dq~ / dk~ are formed half the columns at a time
+  alignas(16) T qt[CS][N + PAD];       // q~
+  alignas(16) T kt[CS][N + PAD];       // k~
+  alignas(16) T v[CS][P + PAD];
+  alignas(16) T dy[CS][P + PAD];
+  alignas(16) T h[P][N + PAD];         // state entering the chunk
+  alignas(16) T gt[N][P + PAD];        // adjoint state after the chunk, [n][p]
+  alignas(16) T sm[CS][CS + PAD];      // S masked and decayed
+  alignas(16) T dpm[CS][CS + PAD];     // dP masked and decayed
+  alignas(16) float res[CS][NH + 4];   // dq~ or dk~ of half the columns
+  // bf16: what q~ (k~) lost to rounding, for half the columns: dq~ and dk~ take
+  // their q~ / k~ operand as hi + lo (the angle gradient cancels to a small sum)
+  alignas(16) T lo[CS][NH + PAD];
+  float ac[CS], gam[CS], scl[CS], dtv[CS], qk[CS], dqk[CS];
+  float pq[N / 8][CS];                 // per column group: q^.k^, then q~.dq~ - k~.dk~
+  float ps[N / 8][CS];                 // per column group: dk~ . rot(k^)
+  float pv[P / 8][CS];                 // per value group: dy.v
+  float aend;
+};
+
+template <typename T, int CS, int N, int P, int R>
+__global__ __launch_bounds__(kBwdThreads, 1)
+void scan_bwd_chunk_kernel(BwdArgs a) {
+  typedef MF16<T> W;
+  typedef GradSmem<T, CS, N, P, R> S;
+  static_assert(sizeof(S) <= 160 * 1024, "LDS budget");
+  __shared__ S sm;
+  constexpr int PAD = S::PAD, KS = W::KSTEP, NH = S::NH;
+  constexpr int TB = CS / 16;                          // 16-token blocks
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = blockIdx.x, bh = blockIdx.y, b = bh / a.s.H, h = bh % a.s.H;
+  const int hq = h / (a.s.H / a.s.Hqk);
+  const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
+  const int t0 = c * CS;
+  const T* gq = reinterpret_cast<const T*>(a.s.q);
+  const T* gk = reinterpret_cast<const T*>(a.s.k);
+  const T* gv = reinterpret_cast<const T*>(a.s.v);
+  const T* gdo = reinterpret_cast<const T*>(a.dout);
+  const T* gz = reinterpret_cast<const T*>(a.s.z);
+  const float Dh = a.s.D ? a.s.D[h] : 0.0f;
+  const bool tok = lane < CS && t0 + lane < L;
+  const long qrow = (((long)b * L + t0 + lane) * HQ + hq) * N;   // this lane's token
+  const long vrow = (((long)b * L + t0 + lane) * H + h) * P;
+
+  // ---- token constants, angles, and the two saved states
+  if (wave == 0) chunk_scalars<CS>(a, bh, t0, lane, sm.ac, sm.gam, sm.scl, sm.dtv, &sm.aend);
+  {
+    const T* hsrc = reinterpret_cast<const T*>(a.hs) + ((long)bh * nc + c) * P * N;
+    const T* gsrc = reinterpret_cast<const T*>(a.gs) + ((long)bh * nc + c) * N * P;
+    for (int i = tid; i < P * N / 8; i += kBwdThreads) {
+      const int p = i / (N / 8), n8 = i % (N / 8);
+      *reinterpret_cast<Vec8<T>*>(&sm.h[p][8 * n8]) = *reinterpret_cast<const Vec8<T>*>(hsrc + p * N + 8 * n8);
+    }
+    for (int i = tid; i < N * P / 8; i += kBwdThreads) {
+      const int n = i / (P / 8), p8 = i % (P / 8);
+      *reinterpret_cast<Vec8<T>*>(&sm.gt[n][8 * p8]) = *reinterpret_cast<const Vec8<T>*>(gsrc + n * P + 8 * p8);
+    }
+  }
+  __syncthreads();
+
+  // ---- preparation, lane = token: q~, k~, v, dy and the row dot products
+  for (int g = wave; g < N / 8; g += kBwdWaves) {
+    float q[8] = {0, 0, 0, 0, 0, 0, 0, 0}, k[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th4[4];
+    float dot = 0.0f;
+    group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
+    if (tok) {
+      load8(gq + qrow + 8 * g, q);
+      load8(gk + qrow + 8 * g, k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        q[e] += a.s.qbias[(long)h * N + 8 * g + e];
+        k[e] += a.s.kbias[(long)h * N + 8 * g + e];
+        dot += q[e] * k[e];
+      }
+      rope8<R>(q, th4, g, 1.0f);
+      rope8<R>(k, th4, g, 1.0f);
+      const float sc = sm.scl[lane];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) k[e] *= sc;
+    }
+    if (lane < CS) {
+      store8(&sm.qt[lane][8 * g], q);
+      store8(&sm.kt[lane][8 * g], k);
+      sm.pq[g][lane] = dot;
+    }
+  }
+  for (int g = wave; g < P / 8; g += kBwdWaves) {
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dy[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float dot = 0.0f;
+    if (tok) {
+      load8(gv + vrow + 8 * g, v);
+      load8(gdo + vrow + 8 * g, dy);
+      if (gz) {
+        float z[8];
+        load8(gz + vrow + 8 * g, z);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dy[e] *= z[e] / (1.0f + expf(-z[e]));
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot += dy[e] * v[e];
+    }
+    if (lane < CS) {
+      store8(&sm.v[lane][8 * g], v);
+      store8(&sm.dy[lane][8 * g], dy);
+      sm.pv[g][lane] = dot;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float qk = 0.0f, dqk = 0.0f;
+    if (lane < CS) {
+      for (int g = 0; g < N / 8; ++g) qk += sm.pq[g][lane];
+      for (int g = 0; g < P / 8; ++g) dqk += sm.pv[g][lane];
+      sm.qk[lane] = qk;
+      sm.dqk[lane] = dqk;
+    }
+    const float tot = wave_sum(dqk);               // padding tokens hold dy = 0
+    if (lane == 0 && a.pd) a.pd[(long)bh * nc + c] = tot;
+  }
+
+  // ---- S = q~ k~^T and dP = dy v^T, masked (s < t) and decayed e^{A_t - A_s}
+  for (int i = wave; i < 2 * TB * TB; i += kBwdWaves) {
+    const int which = i / (TB * TB), tt = (i % (TB * TB)) / TB, st = (i % (TB * TB)) % TB;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (st <= tt) {
+      if (which == 0) {
+        for (int k0 = 0; k0 < N; k0 += KS)
+          acc = W::mma(W::ld(&sm.qt[0][0], N + PAD, 16 * tt, k0, lane), W::ld(&sm.kt[0][0], N + PAD, 16 * st, k0, lane),
+                       acc);
+      } else {
+        for (int k0 = 0; k0 < P; k0 += KS)
+          acc = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * tt, k0, lane), W::ld(&sm.v[0][0], P + PAD, 16 * st, k0, lane),
+                       acc);
+      }
+    }
+    const int s = 16 * st + (lane & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * tt + 4 * (lane >> 4) + r;
+      const float val = s < t ? acc[r] * expf(sm.ac[t] - sm.ac[s]) : 0.0f;
+      if (which == 0) sm.sm[t][s] = (T)val;
+      else sm.dpm[t][s] = (T)val;
+    }
+  }
+  __syncthreads();
+
+  // ---- y (for dZ) and dV, per 16 x 16 tile of (token, value column)
+  const float aend = sm.aend;
+  for (int i = wave; i < 2 * TB * (P / 16); i += kBwdWaves) {
+    const int which = i / (TB * (P / 16)), rt = (i % (TB * (P / 16))) / (P / 16), pt = i % (P / 16);
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (which == 0) {
+      if (!gz || !a.dz) continue;
+      // y_t = sum_s Sm[t][s] v_s + e^{A_t} q~_t . h + (D + QK_t) v_t
+      for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS)
+        acc = W::mma(W::ld(&sm.sm[0][0], CS + PAD, 16 * rt, k0, lane), ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane),
+                     acc);
+      for (int k0 = 0; k0 < N; k0 += KS)
+        acc2 = W::mma(W::ld(&sm.qt[0][0], N + PAD, 16 * rt, k0, lane), W::ld(&sm.h[0][0], N + PAD, 16 * pt, k0, lane),
+                      acc2);
+      const int p = 16 * pt + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * rt + 4 * (lane >> 4) + r;
+        if (t0 + t < L) {
+          const long o = (((long)b * L + t0 + t) * H + h) * P + p;
+          const float y = acc[r] + expf(sm.ac[t]) * acc2[r] + (Dh + sm.gam[t] * sm.qk[t]) * (float)sm.v[t][p];
+          const float z = (float)gz[o], sz = 1.0f / (1.0f + expf(-z));
+          reinterpret_cast<T*>(a.dz)[o] = (T)((float)gdo[o] * y * sz * (1.0f + z * (1.0f - sz)));
+        }
+      }
+    } else {
+      // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G k~_s + (D + QK_s) dy_s
+      for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS)
+        acc = W::mma(ld_tr(&sm.sm[0][0], CS + PAD, k0, 16 * rt, lane), ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane),
+                     acc);
+      for (int k0 = 0; k0 < N; k0 += KS)
+        acc2 = W::mma(W::ld(&sm.kt[0][0], N + PAD, 16 * rt, k0, lane), ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane),
+                      acc2);
+      const int p = 16 * pt + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s = 16 * rt + 4 * (lane >> 4) + r;
+        if (t0 + s < L) {
+          const float dv = acc[r] + expf(aend - sm.ac[s]) * acc2[r] + (Dh + sm.gam[s] * sm.qk[s]) * (float)sm.dy[s][p];
+          reinterpret_cast<T*>(a.dv)[(((long)b * L + t0 + s) * H + h) * P + p] = (T)dv;
+        }
+      }
+    }
+  }
+
+  // ---- dq~ then dk~, half the columns at a time, each followed by its chain rule
+  constexpr bool BF = std::is_same<T, bf16>::value;
+  for (int pass = 0; pass < 4; ++pass) {
+    const bool isq = pass < 2;
+    const int n0 = (pass & 1) * NH;
+    if constexpr (BF) {
+      // rounding residual of the operand this pass multiplies: k~ (dq~) or q~ (dk~)
+      if (wave < NH / 8) {
+        const int g = n0 / 8 + wave;
+        float x[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th4[4];
+        group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
+        if (tok) {
+          load8((isq ? gk : gq) + qrow + 8 * g, x);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] += (isq ? a.s.kbias : a.s.qbias)[(long)h * N + 8 * g + e];
+          rope8<R>(x, th4, g, 1.0f);
+          if (isq) {
+            const float sc = sm.scl[lane];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] *= sc;
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] -= (float)(bf16)x[e];
+        }
+        if (lane < CS) store8(&sm.lo[lane][8 * wave], x);
+      }
+      __syncthreads();
+    }
+    for (int i = wave; i < TB * (NH / 16); i += kBwdWaves) {
+      const int rt = i / (NH / 16), nt = i % (NH / 16);
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (isq) {
+        // dq~_t = sum_s dPm[t][s] k~_s + e^{A_t} dy_t h
+        for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS) {
+          const typename W::frag fa = W::ld(&sm.dpm[0][0], CS + PAD, 16 * rt, k0, lane);
+          acc = W::mma(fa, ld_tr(&sm.kt[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc);
+          if constexpr (BF) acc = W::mma(fa, ld_tr(&sm.lo[0][0], NH + PAD, k0, 16 * nt, lane), acc);
+        }
+        for (int k0 = 0; k0 < P; k0 += KS)
+          acc2 = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * rt, k0, lane),
+                        ld_tr(&sm.h[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc2);
+      } else {
+        // dk~_s = sum_t dPm[t][s] q~_t + e^{A_end - A_s} v_s G
+        for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS) {
+          const typename W::frag fa = ld_tr(&sm.dpm[0][0], CS + PAD, k0, 16 * rt, lane);
+          acc = W::mma(fa, ld_tr(&sm.qt[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc);
+          if constexpr (BF) acc = W::mma(fa, ld_tr(&sm.lo[0][0], NH + PAD, k0, 16 * nt, lane), acc);
+        }
+        for (int k0 = 0; k0 < P; k0 += KS)
+          acc2 = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * rt, k0, lane),
+                        W::ld(&sm.gt[0][0], P + PAD, n0 + 16 * nt, k0, lane), acc2);
+      }
+      const int nl = 16 * nt + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * rt + 4 * (lane >> 4) + r;
+        const float w = isq ? expf(sm.ac[t]) : expf(aend - sm.ac[t]);
+        sm.res[t][nl] = acc[r] + w * acc2[r];
+      }
+    }
+    __syncthreads();
+    // chain rule, lane = token, one 8-column group per wave
+    const int g = n0 / 8 + wave;
+    if (wave < NH / 8) {
+      float dx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, out[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th[4];
+      float dot = 0.0f, dsc = 0.0f;
+      group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th);
+      if (tok) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dx[e] = sm.res[lane][8 * (g - n0 / 8) + e];
+        float q[8], k[8];
+        load8(gq + qrow + 8 * g, q);
+        load8(gk + qrow + 8 * g, k);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          q[e] += a.s.qbias[(long)h * N + 8 * g + e];
+          k[e] += a.s.kbias[(long)h * N + 8 * g + e];
+        }
+        const float sc = sm.scl[lane], gqk = sm.dqk[lane] * sm.gam[lane];
+        float xr[8];                                      // q~ (pass Q) or rot(k^) (pass K)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xr[e] = isq ? q[e] : k[e];
+        rope8<R>(xr, th, g, 1.0f);
+        const float f = isq ? 1.0f : sc;                  // k~ = scale rot(k^)
+        float dth[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dot += f * xr[e] * dx[e];
+          dsc += xr[e] * dx[e];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dth[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
+        // d(q^) = rot^T dq~ + dQK gamma k^;  d(k^) = scale rot^T dk~ + dQK gamma q^
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = f * dx[e];
+        rope8<R>(out, th, g, -1.0f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] += gqk * (isq ? k[e] : q[e]);
+        // angle gradient of the pairs of this group (finished by the finish kernel)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * g + j;
+          if (r < R) {
+            float* dst = a.dang + (((long)b * L + t0 + lane) * H + h) * R + r;
+            *dst = isq ? dth[j] : *dst + dth[j];
+          }
+        }
+        // dQ / dK rows
+        if (a.dqh) {
+          float* dst = (isq ? a.dqh : a.dkh) + (((long)b * L + t0 + lane) * H + h) * N + 8 * g;
+          store8(dst, out);
+        } else {
+          T* dst = reinterpret_cast<T*>(isq ? a.dq : a.dk) + qrow + 8 * g;
+          store8(dst, out);
+        }
+      }
+      if (lane < CS) {
+        if (isq) sm.pq[g][lane] = dot;   // the same thread subtracts k~.dk~ in pass K
+        else {
+          sm.pq[g][lane] -= dot;
+          sm.ps[g][lane] = dsc;
+        }
+      }
+      // bias gradient partials: column sums over the chunk's tokens
+      float* pb = (isq ? a.pqb : a.pkb) + ((long)bh * nc + c) * N + 8 * g;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float s = wave_sum(out[e]);
+        if (lane == 0) pb[e] = s;
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- per token: dA, d(scale), d(gamma) into the dADT, dTrap, dDT outputs
+  if (wave == 0 && tok) {
+    float da = 0.0f, ds = 0.0f;
+    for (int g = 0; g < N / 8; ++g) {
+      da += sm.pq[g][lane];
+      ds += sm.ps[g][lane];
+    }
+    const long o = (long)bh * L + t0 + lane;
+    a.dadt[o] = da;
+    a.dtrap[o] = ds;
+    a.ddt[o] = sm.dqk[lane] * sm.qk[lane] + ds;
+  }
+}
+
+// --------------------------------------------------------------- finishing scans
+// Per (b, h), blocks of 64 tokens from the end: dadt = reverse cumsum of dA;
+// dPhi = reverse cumsum of d(theta), dAngles = dPhi pi dt (1 - tanh^2), the angle
+// part of dDT = pi sum_r dPhi tanh; du_t = d(scale)_{t-1}; dDT = dgamma sigmoid +
+// du (1 - sigmoid) + angle part; dTrap = (dgamma - du) dt sigmoid (1 - sigmoid).
+constexpr int kFinWaves = 4;
+__global__ __launch_bounds__(64 * kFinWaves)
+void scan_bwd_finish_kernel(BwdArgs a) {
+  __shared__ float part[kFinWaves][64];
+  __shared__ float carry_th[64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.x, b = bh / a.s.H, h = bh % a.s.H;
+  const int L = a.s.L, H = a.s.H, R = a.s.R;
+  const float kPi = 3.14159265358979323846f;
+  for (int r = tid; r < R; r += 64 * kFinWaves) carry_th[r] = 0.0f;
+  float carry_a = 0.0f;
+  __syncthreads();
+  const int nblk = (L + 63) / 64;
+  for (int j = nblk - 1; j >= 0; --j) {
+    const int t = 64 * j + lane;
+    const bool tok = t < L;
+    const long o = (long)bh * L + t;
+    const float dt = tok ? a.s.dt[o] : 0.0f;
+    float angp = 0.0f;
+    // rope pair r belongs to one wave, which alone reads and updates carry_th[r]
+    for (int r = wave; r < R; r += kFinWaves) {
+      float* dp = a.dang + (((long)b * L + t) * H + h) * R + r;
+      const float d = tok ? *dp : 0.0f;
+      const float sum = wave_rev_scan(d, lane) + carry_th[r];
+      const float tot = __shfl(sum, 0, 64);
+      if (tok) {
+        const float tn = tanhf(a.s.ang[(((long)b * L + t) * H + h) * R + r]);
+        *dp = sum * kPi * dt * (1.0f - tn * tn);
+        angp += sum * tn * kPi;
+      }
+      if (lane == 0) carry_th[r] = tot;
+    }
+    part[wave][lane] = angp;
+    __syncthreads();
+    if (wave == 0) {
+      const float dA = tok ? a.dadt[o] : 0.0f;
+      const float sum = wave_rev_scan(dA, lane) + carry_a;
+      carry_a = __shfl(sum, 0, 64);
+      float angd = 0.0f;
+      for (int w = 0; w < kFinWaves; ++w) angd += part[w][lane];
+      const float dsc = tok ? a.dtrap[o] : 0.0f;
+      float du = __shfl_up(dsc, 1, 64);
+      if (lane == 0) du = (t > 0) ? a.dtrap[o - 1] : 0.0f;
+      const float dg = tok ? a.ddt[o] : 0.0f;
+      if (tok) {
+        const float sg = 1.0f / (1.0f + expf(-a.s.trap[o]));
+        a.dadt[o] = sum;
+        a.ddt[o] = dg * sg + du * (1.0f - sg) + angd;
+        a.dtrap[o] = (dg - du) * dt * sg * (1.0f - sg);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Bias and D gradients: sums over batch and chunks of the per-chunk partials.
+__global__ void scan_bwd_reduce_kernel(BwdArgs a) {
+  const int h = blockIdx.x, N = a.s.N, H = a.s.H, B = a.s.B, nc = a.nc;
+  for (int n = threadIdx.x; n < N; n += blockDim.x) {
+    float sq = 0.0f, sk = 0.0f;
+    for (int b = 0; b < B; ++b)
+      for (int c = 0; c < nc; ++c) {
+        const long i = (((long)b * H + h) * nc + c) * N + n;
+        sq += a.pqb[i];
+        sk += a.pkb[i];
+      }
+    a.dqb[(long)h * N + n] = sq;
+    a.dkb[(long)h * N + n] = sk;
+  }
+  if (a.dD && threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int b = 0; b < B; ++b)
+      for (int c = 0; c < nc; ++c) s += a.pd[((long)b * H + h) * nc + c];
+    a.dD[h] = s;
+  }
+}
+
+// GQA: dQ, dK of a Q/K head = sum over the value heads that share it.
+template <typename T>
+__global__ void scan_bwd_gqa_kernel(BwdArgs a) {
+  const int B = a.s.B, L = a.s.L, H = a.s.H, HQ = a.s.Hqk, N = a.s.N, rep = H / HQ;
+  const long total = (long)B * L * HQ * N;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const int n = i % N;
+    const long row = i / N;                      // (b, t, hq)
+    const int hq = row % HQ;
+    const long bt = row / HQ;
+    float sq = 0.0f, sk = 0.0f;
+    for (int j = 0; j < rep; ++j) {
+      const long src = (bt * H + hq * rep + j) * N + n;
+      sq += a.dqh[src];
+      sk += a.dkh[src];
+    }
+    reinterpret_cast<T*>(a.dq)[i] = (T)sq;
+    reinterpret_cast<T*>(a.dk)[i] = (T)sk;
+  }
+}
+
+size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct BwdWs {
+  size_t hs, gs, th, pqb, pkb, pd, dqh, dkh, total;
+};
+
+BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R) {
+  const int CS = bf16_io ? 64 : 32;
+  const long nc = (L + CS - 1) / CS, bhc = (long)B * H * nc;
+  const size_t ts = bf16_io ? 2 : 4;
+  BwdWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
+  w.hs = take(bhc * P * N * ts);
+  w.gs = take(bhc * P * N * ts);
+  w.th = take(bhc * (R > 0 ? R : 1) * 4);
+  w.pqb = take(bhc * N * 4);
+  w.pkb = take(bhc * N * 4);
+  w.pd = take(bhc * 4);
+  const bool gqa = Hqk < H;
+  w.dqh = gqa ? take((size_t)B * L * H * N * 4) : 0;
+  w.dkh = gqa ? take((size_t)B * L * H * N * 4) : 0;
+  w.total = off;
+  return w;
+}
+
+}  // namespace
+
+// (dtype, kernel chunk, d_state, headdim, rotation width) of the backward
+#define M3_BWD_SHAPES(X)                                                                    \
+  X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0)                 \
+  X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 32, 16) X(float, 32, 64, 64, 16) X(float, 32, 64, 32, 16)
+
+bool scan_bwd_supported(bool bf16_io, int N, int P, int R) {
+#define X(T, cs, n, p, r) \
+  if ((std::is_same<T, bf16>::value == bf16_io) && N == n && P == p && R == r) return true;
+  M3_BWD_SHAPES(X)
+#undef X
+  return false;
+}
+
+size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R) {
+  if (!scan_bwd_supported(bf16_io, N, P, R) || B <= 0 || L <= 0) return 0;
+  return bwd_layout(bf16_io, B, L, H, Hqk, N, P, R).total;
+}
+
+hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st) {
+  const ScanArgs& s = g.fwd;
+  const int CS = bf16_io ? 64 : 32;
+  const BwdWs w = bwd_layout(bf16_io, s.B, s.L, s.H, s.Hqk, s.N, s.P, s.R);
+  char* base = reinterpret_cast<char*>(ws);
+  BwdArgs a;
+  a.s = s;
+  a.s.CS = CS;
+  a.dout = g.dout;
+  a.dq = g.dq; a.dk = g.dk; a.dv = g.dv; a.dz = g.dz;
+  a.dadt = g.dadt; a.ddt = g.ddt; a.dtrap = g.dtrap; a.dang = g.dang;
+  a.dqb = g.dqb; a.dkb = g.dkb; a.dD = g.dD;
+  a.hs = base + w.hs;
+  a.gs = base + w.gs;
+  a.th0 = reinterpret_cast<float*>(base + w.th);
+  a.pqb = reinterpret_cast<float*>(base + w.pqb);
+  a.pkb = reinterpret_cast<float*>(base + w.pkb);
+  a.pd = reinterpret_cast<float*>(base + w.pd);
+  a.dqh = w.dqh ? reinterpret_cast<float*>(base + w.dqh) : nullptr;
+  a.dkh = w.dkh ? reinterpret_cast<float*>(base + w.dkh) : nullptr;
+  a.nc = (s.L + CS - 1) / CS;
+
+  // 1. chunk states and angles (the forward's state-only pass)
+  ScanArgs p1 = s;
+  p1.CS = CS;
+  p1.seg_len = 0; p1.init_per_seg = 0; p1.fin_per_seg = 0;
+  p1.init_theta = p1.init_h = p1.init_k = p1.init_v = nullptr;
+  p1.fin_theta = p1.fin_h = p1.fin_k = p1.fin_v = nullptr;
+  p1.fin_logdec = nullptr;
+  p1.chunk_h = base + w.hs;
+  p1.chunk_th = s.R > 0 ? reinterpret_cast<float*>(base + w.th) : nullptr;
+  hipError_t e = scan_state_launch(p1, bf16_io, st);
+  if (e != hipSuccess) return e;
+
+  const dim3 grid_bh(s.B * s.H), grid_c(a.nc, s.B * s.H);
+  bool found = false;
+#define X(T, cs, n, p, r)                                                                                  \
+  if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
+    found = true;                                                                                          \
+    hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r>), grid_bh, dim3(kBwdThreads), 0, st, a);       \
+    if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
+    hipLaunchKernelGGL((scan_bwd_chunk_kernel<T, cs, n, p, r>), grid_c, dim3(kBwdThreads), 0, st, a);      \
+    if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
+    if (a.dqh) {                                                                                           \
+      hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \
+      if ((e = hipGetLastError()) != hipSuccess) return e;                                                 \
+    }                                                                                                      \
+  }
+  M3_BWD_SHAPES(X)
+#undef X
+  if (!found) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(scan_bwd_finish_kernel, grid_bh, dim3(64 * kFinWaves), 0, st, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(scan_bwd_reduce_kernel, dim3(s.H), dim3(128), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace m3

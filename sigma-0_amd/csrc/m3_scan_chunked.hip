@@ -321,6 +321,9 @@ void scan_chunked_kernel(ScanArgs a) {
           const float rcp = rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j]));
           const float d = fmaf(-s_dt, rcp, hdt);        // s_dt = 0 past the sequence end
           const float th = __builtin_amdgcn_fractf(carry[k][j] + wave_incl_scan(d));
+          if constexpr (SO) {            // backward: the angle entering chunk cc (revolutions)
+            if (a.chunk_th && lane == 0) a.chunk_th[((long)bh * nc + cc) * R + 4 * g + j] = carry[k][j];
+          }
           carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
           p_cs[k][j] = __builtin_amdgcn_cosf(th);
           p_sn[k][j] = __builtin_amdgcn_sinf(th);
@@ -585,6 +588,16 @@ void scan_chunked_kernel(ScanArgs a) {
       }
       }  // !SO
       // ---- phases 4-5: h <- e^{A_end} h + (w K_s)^T V for my p-tile
+      if constexpr (SO) {                // backward: the state entering chunk c, [p][n]
+        if (a.chunk_h && part == 0) {
+          T* dst = reinterpret_cast<T*>(a.chunk_h) + ((long)(bh * nc + c) * P + pcol) * N + g4;
+#pragma unroll
+          for (int nb = 0; nb < G::NB16; ++nb) {
+            const float hv[4] = {hs[nb][0], hs[nb][1], hs[nb][2], hs[nb][3]};
+            store4(dst + 16 * nb, hv);
+          }
+        }
+      }
       const float dec = sm.dec[pc];
 #pragma unroll
       for (int nb = 0; nb < G::NB16; ++nb)
@@ -674,26 +687,29 @@ hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) 
   return hipErrorInvalidValue;
 }
 
-// The state-only pass of the sequence split (bf16, d_state 128, headdim 64: the
-// model's shapes), with its rotation widths.
-#define M3_STATE_SHAPES(X) X(128, 64, 32) X(128, 64, 64) X(128, 64, 0)
+// The state-only pass: the sequence split's first pass (bf16, d_state 128, headdim
+// 64) and the backward's chunk states (the backward's shapes).
+#define M3_STATE_SHAPES(X)                                                                  \
+  X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0)                 \
+  X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 32, 16) X(float, 32, 64, 64, 16) X(float, 32, 64, 32, 16)
 
-bool scan_state_supported(bool bf16_io, int N, int P, int R) {
-  if (!bf16_io) return false;
-#define X(n, p, r) \
-  if (N == n && P == p && R == r) return true;
+bool scan_state_supported(bool bf16_io, int CS_, int N, int P, int R) {
+  const int CS = kernel_chunk(bf16_io, CS_);
+#define X(T, cs, n, p, r) \
+  if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && N == n && P == p && R == r) return true;
   M3_STATE_SHAPES(X)
 #undef X
   return false;
 }
 
-hipError_t scan_state_launch(const ScanArgs& a, hipStream_t st) {
+hipError_t scan_state_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
+  const int CS = kernel_chunk(bf16_io, a.CS);
   const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
-#define X(n, p, r)                                                                                     \
-  if (a.N == n && a.P == p && a.R == r) {                                                              \
-    hipLaunchKernelGGL((scan_chunked_kernel<bf16, 64, n, p, r, kChunkWaves, true>), dim3(a.B * a.H, nseg), \
-                       dim3(64 * kChunkWaves), 0, st, a);                                               \
-    return hipGetLastError();                                                                           \
+#define X(T, cs, n, p, r)                                                                           \
+  if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && a.N == n && a.P == p && a.R == r) {  \
+    hipLaunchKernelGGL((scan_chunked_kernel<T, cs, n, p, r, kChunkWaves, true>), dim3(a.B * a.H, nseg), \
+                       dim3(64 * kChunkWaves), 0, st, a);                                            \
+    return hipGetLastError();                                                                        \
   }
   M3_STATE_SHAPES(X)
 #undef X

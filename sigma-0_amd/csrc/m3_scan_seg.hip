@@ -136,7 +136,9 @@ void seg_combine_kernel(ScanArgs a, int nseg, Carries loc, Carries in) {
 
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS) {
   const int len = seg_len_for(B, H, L);
-  if (len == 0 || !scan_state_supported(bf16_io, N, P, R) || !scan_chunked_supported(bf16_io, CS, N, P, R))
+  // the model's shapes (bf16, d_state 128, headdim 64); others run one pass
+  if (len == 0 || !bf16_io || N != 128 || P != 64 || !scan_state_supported(bf16_io, 64, N, P, R) ||
+      !scan_chunked_supported(bf16_io, CS, N, P, R))
     return 0;
   const long bhs = (long)B * H * ((L + len - 1) / len);
   return carve(nullptr, bhs, N, P, R, nullptr, nullptr);
@@ -155,7 +157,8 @@ hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStrea
   p1.fin_h = loc.h; p1.fin_k = loc.k; p1.fin_v = loc.v; p1.fin_theta = a.R > 0 ? loc.th : nullptr;
   p1.fin_logdec = loc.ld;
   p1.fin_per_seg = 1;
-  hipError_t e = scan_state_launch(p1, st);
+  p1.CS = 64;
+  hipError_t e = scan_state_launch(p1, bf16_io, st);
   if (e != hipSuccess) return e;
 
   ScanArgs p2 = a;                                   // pass 2: entering carries

@@ -121,11 +121,83 @@ def mamba3_siso_hip(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=No
     (batch, head) pairs split each sequence across compute units (same result up
     to rounding); False forces one pass.
     """
-    p, dims, unbatched = _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z)
+    args = (Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z)
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in args):
+        return _Mamba3Siso.apply(int(chunk_size), bool(seq_split), *args)
+    return _forward(args, chunk_size, seq_split)
+
+
+def _forward(args, chunk_size, seq_split):
+    p, dims, unbatched = _prep(*args)
     out = torch.empty_like(p["V"])
     if out.numel():
         _launch(p, dims, chunk_size, out, seq_split=seq_split)
     return out[0] if unbatched else out
+
+
+def mamba3_siso_hip_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dOut,
+                        chunk_size: int = 64):
+    """Gradients of mamba3_siso_hip's output against every input, given dOut (the
+    output cotangent, V's shape).  The reference's backward (mamba3_siso_bwd,
+    mamba3_ops.py:821-902) returns the same tuple:
+    (dQ, dK, dV, dADT, dDT, dTrap, dQ_bias, dK_bias, dAngles, dD, dZ), each in its
+    input's shape; dD and dZ are None when D and Z are.  The forward is recomputed
+    from the inputs (no saved state)."""
+    p, (B, L, H, HQ, N, P, R), unbatched = _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z)
+    io = _IO[p["V"].dtype]
+    dO = (dOut[None] if unbatched else dOut).to(p["V"].dtype).contiguous()
+    _req(tuple(dO.shape) == (B, L, H, P), f"dOut must be {(B, L, H, P)}, got {tuple(dOut.shape)}")
+    dev, dt = p["V"].device, p["V"].dtype
+    f32 = dict(device=dev, dtype=torch.float32)
+    g = dict(Q=torch.empty_like(p["Q"]), K=torch.empty_like(p["K"]), V=torch.empty_like(p["V"]),
+             ADT=torch.empty(B, H, L, **f32), DT=torch.empty(B, H, L, **f32),
+             Trap=torch.empty(B, H, L, **f32), Q_bias=torch.empty(H, N, **f32),
+             K_bias=torch.empty(H, N, **f32), Angles=torch.empty(B, L, H, R, **f32),
+             D=None if p["D"] is None else torch.empty(H, **f32),
+             Z=None if p["Z"] is None else torch.empty_like(p["Z"]))
+    if B and L:
+        lib = _lib.load()
+        ws_bytes = lib.m3_chunk_scan_bwd_ws_bytes(B, L, H, HQ, N, P, R, int(chunk_size), io)
+        if ws_bytes == 0:
+            raise _lib.Mamba3LibraryError(
+                f"no backward kernel for dtype={dt} d_state={N} headdim={P} rope angles={R}")
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        rc = lib.m3_chunk_scan_bwd(
+            _ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
+            _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(dO),
+            _ptr(g["Q"]), _ptr(g["K"]), _ptr(g["V"]), _ptr(g["ADT"]), _ptr(g["DT"]), _ptr(g["Trap"]),
+            _ptr(g["Q_bias"]), _ptr(g["K_bias"]), _ptr(g["Angles"]), _ptr(g["D"]), _ptr(g["Z"]),
+            B, L, H, HQ, N, P, R, int(chunk_size), io, ws.data_ptr(), ws_bytes, _stream(p["V"]))
+        _lib.check(rc, "m3_chunk_scan_bwd")
+    else:
+        for t in g.values():
+            if t is not None:
+                t.zero_()
+    order = ("Q", "K", "V", "ADT", "DT", "Trap", "Q_bias", "K_bias", "Angles", "D", "Z")
+    if unbatched:
+        return tuple(None if g[k] is None else (g[k] if k in ("Q_bias", "K_bias", "D") else g[k][0])
+                     for k in order)
+    return tuple(g[k] for k in order)
+
+
+class _Mamba3Siso(torch.autograd.Function):
+    """mamba3_siso_hip with its backward: the reference's custom_vjp pair
+    (mamba3_ops.py:909-1045).  Saves the inputs only; the backward recomputes."""
+
+    @staticmethod
+    def forward(ctx, chunk_size, seq_split, *args):
+        ctx.chunk_size = chunk_size
+        ctx.save_for_backward(*(t if isinstance(t, torch.Tensor) else None for t in args))
+        return _forward(args, chunk_size, seq_split)
+
+    @staticmethod
+    def backward(ctx, dout):
+        args = ctx.saved_tensors
+        grads = mamba3_siso_hip_bwd(*args, dout, chunk_size=ctx.chunk_size)
+        out = []
+        for t, gr in zip(args, grads):
+            out.append(None if t is None or gr is None else gr.to(t.dtype))
+        return (None, None, *out)
 
 
 def mamba3_ssd_chunked_hip(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z,

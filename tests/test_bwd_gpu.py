@@ -1,0 +1,112 @@
+"""Backward of the prefill scan on the GPU vs the gradient oracle (parity gate).
+
+Every one of the eleven input gradients is compared with torch autograd of the
+float64 restatement (oracle/mamba3_vjp.py, the counterpart of the reference's
+jax.grad pin, test_mamba3_pallas_ssd.py:108-128) on the same inputs and output
+cotangent.  Metric: the reference's _rel (max abs error / max abs reference).
+Bars: 2e-5 for float32 I/O (the reference's gradient bar); 3e-2 for bf16 I/O
+(bf16 MFMA operands, float32 accumulation; the reference's bf16-I/O class).
+"""
+import numpy as np
+import pytest
+
+from _util import I, rel, to_dev
+from oracle import mamba3_vjp as V
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 2e-5
+BF16_TOL = 3e-2
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _grads(d, cot, torch_dtype, no_d=False, no_z=False, chunk=64):
+    torch = _torch()
+    from mamba3_rocm import mamba3_siso_hip_bwd
+    t = to_dev(d, torch_dtype)
+    dout = torch.from_numpy(np.ascontiguousarray(cot)).to("cuda").to(torch_dtype)
+    g = mamba3_siso_hip_bwd(t["Q"], t["K"], t["V"], t["ADT"], t["DT"], t["Trap"], t["Q_bias"],
+                            t["K_bias"], t["Angles"], None if no_d else t["D"],
+                            None if no_z else t["Z"], dout, chunk_size=chunk)
+    torch.cuda.synchronize()
+    return [None if x is None else x.float().cpu().numpy() for x in g]
+
+
+def _check(B, L, H, Hqk, N, P, R, bf16, seed, no_d=False, no_z=False, chunk=64):
+    torch = _torch()
+    d = I.scan_inputs(B, L, H, N, P, R, seed=seed, Hqk=Hqk, bf16=bf16)
+    cot = V.cotangent(B, L, H, P, seed=seed + 100)
+    if bf16:
+        cot = I.bf16_round(cot)
+    print(f"case bwd {(B, L, H, Hqk, N, P, R)} bf16={bf16} no_d={no_d} no_z={no_z}", flush=True)
+    got = _grads(d, cot, torch.bfloat16 if bf16 else torch.float32, no_d, no_z, chunk)
+    _, ref = V.vjp(d, cot, 16, no_d=no_d, no_z=no_z)
+    tol = BF16_TOL if bf16 else F32_TOL
+    errs = {}
+    for name, a, b in zip(V.NAMES, got, ref):
+        if b is None:
+            assert a is None, name
+            continue
+        assert a.shape == b.shape, (name, a.shape, b.shape)
+        if b.size == 0:
+            continue
+        assert np.isfinite(a).all(), f"d{name} has non-finite entries"
+        errs[name] = rel(a, b)
+    print("  " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+    bad = {k: v for k, v in errs.items() if v > tol}
+    assert not bad, f"gradients above {tol}: {bad}"
+
+
+BF16_SHAPES = [
+    (1, 200, 2, 2, 128, 64, 32),     # model geometry, ragged L (several chunks)
+    (2, 130, 4, 2, 128, 64, 32),     # GQA
+    (1, 150, 2, 2, 128, 64, 64),     # rope on every state pair
+    (1, 100, 2, 2, 128, 64, 0),      # no rope
+    (1, 160, 2, 2, 64, 32, 16),
+]
+
+
+@pytest.mark.parametrize("B,L,H,Hqk,N,P,R", BF16_SHAPES)
+def test_bf16_gradients_match_oracle(B, L, H, Hqk, N, P, R):
+    _check(B, L, H, Hqk, N, P, R, bf16=True, seed=31)
+
+
+F32_SHAPES = [
+    (1, 150, 2, 2, 64, 32, 16),
+    (2, 70, 4, 1, 64, 64, 16),       # GQA, L below two chunks
+]
+
+
+@pytest.mark.parametrize("B,L,H,Hqk,N,P,R", F32_SHAPES)
+def test_f32_gradients_match_oracle(B, L, H, Hqk, N, P, R):
+    _check(B, L, H, Hqk, N, P, R, bf16=False, seed=32)
+
+
+def test_gradients_without_d_and_z():
+    _check(1, 120, 2, 2, 128, 64, 32, bf16=True, seed=33, no_d=True, no_z=True)
+    _check(1, 90, 2, 2, 64, 32, 16, bf16=False, seed=34, no_d=True, no_z=True)
+
+
+def test_autograd_matches_functional_backward_and_is_deterministic():
+    """mamba3_siso_hip under torch autograd (the custom_vjp) gives the functional
+    backward's gradients, bitwise, on repeated calls."""
+    torch = _torch()
+    from mamba3_rocm import mamba3_siso_hip, mamba3_siso_hip_bwd
+    B, L, H, N, P, R = 1, 140, 2, 128, 64, 32
+    d = I.scan_inputs(B, L, H, N, P, R, seed=35, bf16=True)
+    t = to_dev(d, torch.bfloat16)
+    cot = torch.from_numpy(I.bf16_round(V.cotangent(B, L, H, P, seed=36))).to("cuda").to(torch.bfloat16)
+    names = V.NAMES
+    leaves = {k: t[k].clone().requires_grad_(True) for k in names}
+    y = mamba3_siso_hip(*(leaves[k] for k in names), chunk_size=64)
+    y.backward(cot)
+    g1 = mamba3_siso_hip_bwd(*(t[k] for k in names), cot, chunk_size=64)
+    g2 = mamba3_siso_hip_bwd(*(t[k] for k in names), cot, chunk_size=64)
+    torch.cuda.synchronize()
+    for k, a, b in zip(names, g1, g2):
+        assert torch.equal(a, b), f"d{k} differs between two calls"
+        assert torch.equal(leaves[k].grad.to(a.dtype), a), f"autograd d{k} differs"

@@ -37,7 +37,8 @@ def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
     assert names == sorted(["m3_abi_version", "m3_last_error", "m3_chunk_scan_impl",
                             "m3_chunk_scan_fwd", "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes",
-                            "m3_chunk_scan_fwd_ws", "m3_decode_step"])
+                            "m3_chunk_scan_fwd_ws", "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd",
+                            "m3_decode_step"])
     for n in names:
         assert hasattr(lib, n), n
     from mamba3_rocm import _lib
@@ -87,6 +88,47 @@ def test_split_workspace_sizes(lib):
     assert f(1, 4096, 2, 64, 64, 16, 64, bf) == 0            # no state-only pass for d_state 64
     assert f(1, 4096, 2, 128, 64, 32, 48, bf) == 0           # chunk 48: generic kernel
     assert f(1, 1061, 3, 128, 64, 32, 64, bf) > 0
+
+
+def test_backward_workspace_sizes(lib):
+    """Backward workspace: chunk-entering states and adjoint states (B*H*nc*P*N in
+    the I/O type each, 64-token chunks for bf16, 32 for fp32), chunk angles, bias and
+    D partials, and per-head dQ/dK (float32) when Hqk < H; 0 without a kernel."""
+    f = lib.m3_chunk_scan_bwd_ws_bytes
+    bf, f32 = 1, 0
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+
+    def expect(B, L, H, Hqk, N, P, R, io):
+        cs = 64 if io == bf else 32
+        bhc = B * H * ((L + cs - 1) // cs)
+        ts = 2 if io == bf else 4
+        n = 2 * al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4) + 2 * al(bhc * N * 4) + al(bhc * 4)
+        if Hqk < H:
+            n += 2 * al(B * L * H * N * 4)
+        return n
+    assert f(8, 4096, 32, 32, 128, 64, 32, 64, bf) == expect(8, 4096, 32, 32, 128, 64, 32, bf)
+    assert f(2, 300, 4, 2, 64, 32, 16, 64, f32) == expect(2, 300, 4, 2, 64, 32, 16, f32)
+    assert f(1, 100, 2, 2, 64, 16, 16, 64, bf) == 0        # headdim 16: no backward kernel
+    assert f(1, 100, 2, 2, 128, 64, 32, 64, 7) == 0        # unknown dtype
+    assert f(1, 100, 3, 2, 128, 64, 32, 64, bf) == 0       # H not a multiple of Hqk
+
+
+def test_backward_validation(lib):
+    E_ARG, E_UNSUP = _header_define("M3_E_ARG"), _header_define("M3_E_UNSUPPORTED")
+    p = ctypes.c_void_p(4096)
+
+    def call(Z=p, dZ=p, N=128, P=64, R=32, ws=p, wsb=1 << 40, **kw):
+        d = dict(B=1, L=8, H=2, Hqk=2, io=1)
+        d.update(kw)
+        return lib.m3_chunk_scan_bwd(p, p, p, p, p, p, p, p, p, p, Z, p,
+                                     p, p, p, p, p, p, p, p, p, p, dZ,
+                                     d["B"], d["L"], d["H"], d["Hqk"], N, P, R, 64, d["io"], ws, wsb, None)
+    assert call(P=16) == E_UNSUP and b"no backward kernel" in lib.m3_last_error()
+    assert call(Z=None) == E_ARG and b"dZ" in lib.m3_last_error()
+    assert call(ws=None) == E_ARG and b"workspace" in lib.m3_last_error()
+    assert call(wsb=16) == E_ARG
+    assert call(H=3) == E_ARG
+    assert call(B=0) == 0
 
 
 def _scan_call(lib, **kw):
