@@ -48,6 +48,14 @@ def scan_flops(B, L, H, N, P, CS):
     return B * L * H * (2 * CS * N + 2 * CS * P + 4 * P * N)
 
 
+def bwd_bytes(B, L, H, N, P, R, s_io):
+    """Algorithmic HBM bytes of one backward call: the forward's inputs and dOut read
+    once (Q, K; V, Z, dOut at s_io; ADT, DT, Trap, angles f32), every gradient
+    written once (dQ, dK; dV, dZ at s_io; dADT, dDT, dTrap, dAngles f32), per
+    token-head.  The chunk states it keeps in its workspace are not counted."""
+    return B * L * H * ((2 * N + 3 * P) * s_io + 3 * 4 + R * 4 + (2 * N + 2 * P) * s_io + 3 * 4 + R * 4)
+
+
 def decode_bytes(B, H, N, P, R, s_in, s_out):
     """Per decode step: f32 state, angle, k and v carries read and written,
     step inputs (x, z, B, C at s_in; adt, dt, trap, R angles f32) and y."""
@@ -106,6 +114,20 @@ def bench_scan(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
     nbytes = scan_bytes(B, L, H, N, P, R, 2)
     return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, flops=scan_flops(B, L, H, N, P, CS),
                 achieved_gbs=nbytes / kern / 1e9)
+
+
+def bench_bwd(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
+    """Backward of the scan (all eleven input gradients) on the config's inputs and a
+    N(0, 1) output cotangent."""
+    from mamba3_rocm import mamba3_siso_hip_bwd
+    args = make_scan_inputs(torch, B, L, H, N, P, R, seed, torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1000)
+    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(torch.bfloat16)
+    fn = lambda: mamba3_siso_hip_bwd(*args, dout, chunk_size=CS)  # noqa: E731
+    wall, kern = time_calls(torch, fn, steps, warmup)
+    nbytes = bwd_bytes(B, L, H, N, P, R, 2)
+    return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
 
 
 def bench_decode(torch, B, H, N, P, R, steps, warmup, seed):
@@ -199,7 +221,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "copy"), default="scan")
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "copy"), default="scan")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -225,6 +247,14 @@ def main():
         print(json.dumps({"mode": "decode", **r}), flush=True)
         return
 
+    if args.mode == "bwd":
+        # backward at config 2 alone, for profiling
+        r = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)
+        print(json.dumps({"mode": "bwd", "ms": round(r["kernel_s"] * 1e3, 4),
+                          "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
+                          "achieved_gbs": round(r["achieved_gbs"], 1),
+                          "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        return
     if args.mode == "long":
         # config 3 alone (B*H = 32: the sequence split runs), for profiling
         r = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3)
@@ -262,6 +292,7 @@ def main():
     if not args.no_secondary:
         dec = bench_decode(torch, 512, 32, 128, 64, 32, 256, 16, seed=4)
         lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
+        bw = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         out["secondary"] = {
             "decode_config4": {"B": 512, "H": 32, "P": 64, "N": 128, "steps": 256,
                                "us_per_step": round(dec["kernel_s"] * 1e6, 2),
@@ -273,6 +304,11 @@ def main():
                                      "tokens_per_s": round(32768 / lc["wall_s"], 1),
                                      "achieved_gbs": round(lc["achieved_gbs"], 1),
                                      "frac_hbm": round(lc["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
+                                 "ms": round(bw["kernel_s"] * 1e3, 4),
+                                 "tokens_per_s": round(8 * 4096 / bw["wall_s"], 1),
+                                 "achieved_gbs": round(bw["achieved_gbs"], 1),
+                                 "frac_hbm": round(bw["achieved_gbs"] / HBM_PEAK_GBS, 4)},
         }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

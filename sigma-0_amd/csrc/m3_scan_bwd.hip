@@ -77,6 +77,20 @@ __device__ __forceinline__ void rope8(float x[8], const float th4[4], int g, flo
   }
 }
 
+// The same rotation with the pairs' cosines and sines given.
+template <int R>
+__device__ __forceinline__ void rot8(float x[8], const float cs[4], const float sn[4], int g, float sgn) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (4 * g + j < R) {
+      const float c = cs[j], s = sgn * sn[j];
+      const float x0 = x[2 * j], x1 = x[2 * j + 1];
+      x[2 * j] = x0 * c - x1 * s;
+      x[2 * j + 1] = x0 * s + x1 * c;
+    }
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
 // Reverse inclusive scan over the 64 lanes (lane i gets the sum over lanes >= i).
@@ -104,6 +118,8 @@ struct BwdArgs {
   float* pqb; float* pkb;      // [bh][nc][N] partial bias gradients
   float* pd;                   // [bh][nc] partial D gradient
   float* dqh; float* dkh;      // GQA: per-head dQ, dK (B, L, H, N) f32, else null
+  float* dsc;                  // [bh][L] d(scale) per token
+  float* ctot;                 // [bh][nc][1 + R] chunk sums of dA and of d(theta) per pair
   int nc;
 };
 
@@ -264,6 +280,7 @@ struct GradSmem {
   alignas(16) T kt[CS][N + PAD];       // k~
   alignas(16) T v[CS][P + PAD];
   alignas(16) T dy[CS][P + PAD];
+  alignas(16) T fz[CS][P + PAD];       // dOut sigmoid(z) (1 + z (1 - sigmoid(z))): dZ = y fz
   alignas(16) T h[P][N + PAD];         // state entering the chunk
   alignas(16) T gt[N][P + PAD];        // adjoint state after the chunk, [n][p]
   alignas(16) T sm[CS][CS + PAD];      // S masked and decayed
@@ -320,34 +337,65 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
   }
   __syncthreads();
 
+  // ---- this thread's two column groups, one per half of the state columns (waves
+  // < GH): q^ = q + qb, k^ = k + kb and the rope cos/sin of their pairs stay in
+  // registers for every phase below.  Padding tokens hold zeros.
+  constexpr int GH = NH / 8;
+  const bool qkw = wave < GH;
+  float qh[2][8], kh[2][8], cs[2][4], sn[2][4];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int g = hh * GH + wave;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qh[hh][e] = kh[hh][e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cs[hh][j] = 1.0f, sn[hh][j] = 0.0f;
+    if (qkw) {
+      float th4[4];
+      group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cs[hh][j] = __builtin_amdgcn_cosf(th4[j]);
+        sn[hh][j] = __builtin_amdgcn_sinf(th4[j]);
+      }
+      if (tok) {
+        load8(gq + qrow + 8 * g, qh[hh]);
+        load8(gk + qrow + 8 * g, kh[hh]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          qh[hh][e] += a.s.qbias[(long)h * N + 8 * g + e];
+          kh[hh][e] += a.s.kbias[(long)h * N + 8 * g + e];
+        }
+      }
+    }
+  }
+
   // ---- preparation, lane = token: q~, k~, v, dy and the row dot products
-  for (int g = wave; g < N / 8; g += kBwdWaves) {
-    float q[8] = {0, 0, 0, 0, 0, 0, 0, 0}, k[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th4[4];
-    float dot = 0.0f;
-    group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
-    if (tok) {
-      load8(gq + qrow + 8 * g, q);
-      load8(gk + qrow + 8 * g, k);
+  if (qkw) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int g = hh * GH + wave;
+      float q[8], k[8], dot = 0.0f;
+      const float sc = tok ? sm.scl[lane] : 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        q[e] += a.s.qbias[(long)h * N + 8 * g + e];
-        k[e] += a.s.kbias[(long)h * N + 8 * g + e];
+        q[e] = qh[hh][e];
+        k[e] = kh[hh][e];
         dot += q[e] * k[e];
       }
-      rope8<R>(q, th4, g, 1.0f);
-      rope8<R>(k, th4, g, 1.0f);
-      const float sc = sm.scl[lane];
+      rot8<R>(q, cs[hh], sn[hh], g, 1.0f);
+      rot8<R>(k, cs[hh], sn[hh], g, 1.0f);
 #pragma unroll
       for (int e = 0; e < 8; ++e) k[e] *= sc;
-    }
-    if (lane < CS) {
-      store8(&sm.qt[lane][8 * g], q);
-      store8(&sm.kt[lane][8 * g], k);
-      sm.pq[g][lane] = dot;
+      if (lane < CS) {
+        store8(&sm.qt[lane][8 * g], q);
+        store8(&sm.kt[lane][8 * g], k);
+        sm.pq[g][lane] = dot;
+      }
     }
   }
   for (int g = wave; g < P / 8; g += kBwdWaves) {
-    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dy[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dy[8] = {0, 0, 0, 0, 0, 0, 0, 0}, fz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float dot = 0.0f;
     if (tok) {
       load8(gv + vrow + 8 * g, v);
@@ -356,7 +404,11 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
         float z[8];
         load8(gz + vrow + 8 * g, z);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dy[e] *= z[e] / (1.0f + expf(-z[e]));
+        for (int e = 0; e < 8; ++e) {
+          const float sz = 1.0f / (1.0f + expf(-z[e]));
+          fz[e] = dy[e] * sz * (1.0f + z[e] * (1.0f - sz));
+          dy[e] *= z[e] * sz;
+        }
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) dot += dy[e] * v[e];
@@ -364,6 +416,7 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
     if (lane < CS) {
       store8(&sm.v[lane][8 * g], v);
       store8(&sm.dy[lane][8 * g], dy);
+      store8(&sm.fz[lane][8 * g], fz);
       sm.pv[g][lane] = dot;
     }
   }
@@ -399,7 +452,7 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * tt + 4 * (lane >> 4) + r;
-      const float val = s < t ? acc[r] * expf(sm.ac[t] - sm.ac[s]) : 0.0f;
+      const float val = s < t ? acc[r] * exp2_fast((sm.ac[t] - sm.ac[s]) * kLog2e) : 0.0f;
       if (which == 0) sm.sm[t][s] = (T)val;
       else sm.dpm[t][s] = (T)val;
     }
@@ -426,9 +479,9 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
         const int t = 16 * rt + 4 * (lane >> 4) + r;
         if (t0 + t < L) {
           const long o = (((long)b * L + t0 + t) * H + h) * P + p;
-          const float y = acc[r] + expf(sm.ac[t]) * acc2[r] + (Dh + sm.gam[t] * sm.qk[t]) * (float)sm.v[t][p];
-          const float z = (float)gz[o], sz = 1.0f / (1.0f + expf(-z));
-          reinterpret_cast<T*>(a.dz)[o] = (T)((float)gdo[o] * y * sz * (1.0f + z * (1.0f - sz)));
+          const float y = acc[r] + exp2_fast(sm.ac[t] * kLog2e) * acc2[r] +
+                          (Dh + sm.gam[t] * sm.qk[t]) * (float)sm.v[t][p];
+          reinterpret_cast<T*>(a.dz)[o] = (T)(y * (float)sm.fz[t][p]);
         }
       }
     } else {
@@ -444,7 +497,8 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int s = 16 * rt + 4 * (lane >> 4) + r;
         if (t0 + s < L) {
-          const float dv = acc[r] + expf(aend - sm.ac[s]) * acc2[r] + (Dh + sm.gam[s] * sm.qk[s]) * (float)sm.dy[s][p];
+          const float dv = acc[r] + exp2_fast((aend - sm.ac[s]) * kLog2e) * acc2[r] +
+                           (Dh + sm.gam[s] * sm.qk[s]) * (float)sm.dy[s][p];
           reinterpret_cast<T*>(a.dv)[(((long)b * L + t0 + s) * H + h) * P + p] = (T)dv;
         }
       }
@@ -453,27 +507,37 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
 
   // ---- dq~ then dk~, half the columns at a time, each followed by its chain rule
   constexpr bool BF = std::is_same<T, bf16>::value;
+  // unrolled: the register arrays above are indexed with compile-time halves only
+#pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const bool isq = pass < 2;
     const int n0 = (pass & 1) * NH;
+    const int hh = pass & 1;
+    // this thread's group of the half: raw values and rope by value selection
+    float gq8[8], gk8[8], gcs[4], gsn[4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gq8[e] = hh ? qh[1][e] : qh[0][e];
+      gk8[e] = hh ? kh[1][e] : kh[0][e];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      gcs[j] = hh ? cs[1][j] : cs[0][j];
+      gsn[j] = hh ? sn[1][j] : sn[0][j];
+    }
     if constexpr (BF) {
       // rounding residual of the operand this pass multiplies: k~ (dq~) or q~ (dk~)
-      if (wave < NH / 8) {
+      if (qkw) {
         const int g = n0 / 8 + wave;
-        float x[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th4[4];
-        group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
-        if (tok) {
-          load8((isq ? gk : gq) + qrow + 8 * g, x);
+        float x[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] += (isq ? a.s.kbias : a.s.qbias)[(long)h * N + 8 * g + e];
-          rope8<R>(x, th4, g, 1.0f);
-          if (isq) {
-            const float sc = sm.scl[lane];
+        for (int e = 0; e < 8; ++e) x[e] = isq ? gk8[e] : gq8[e];
+        rot8<R>(x, gcs, gsn, g, 1.0f);
+        const float sc = isq && tok ? sm.scl[lane] : 1.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] *= sc;
-          }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] -= (float)(bf16)x[e];
+        for (int e = 0; e < 8; ++e) {
+          x[e] *= sc;
+          x[e] -= (float)(bf16)x[e];
         }
         if (lane < CS) store8(&sm.lo[lane][8 * wave], x);
       }
@@ -507,33 +571,24 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * rt + 4 * (lane >> 4) + r;
-        const float w = isq ? expf(sm.ac[t]) : expf(aend - sm.ac[t]);
+        const float w = exp2_fast((isq ? sm.ac[t] : aend - sm.ac[t]) * kLog2e);
         sm.res[t][nl] = acc[r] + w * acc2[r];
       }
     }
     __syncthreads();
     // chain rule, lane = token, one 8-column group per wave
     const int g = n0 / 8 + wave;
-    if (wave < NH / 8) {
-      float dx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, out[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th[4];
-      float dot = 0.0f, dsc = 0.0f;
-      group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th);
+    if (qkw) {
+      float dx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, out[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      float dot = 0.0f, dsc = 0.0f, dthf[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (tok) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) dx[e] = sm.res[lane][8 * (g - n0 / 8) + e];
-        float q[8], k[8];
-        load8(gq + qrow + 8 * g, q);
-        load8(gk + qrow + 8 * g, k);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          q[e] += a.s.qbias[(long)h * N + 8 * g + e];
-          k[e] += a.s.kbias[(long)h * N + 8 * g + e];
-        }
         const float sc = sm.scl[lane], gqk = sm.dqk[lane] * sm.gam[lane];
         float xr[8];                                      // q~ (pass Q) or rot(k^) (pass K)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xr[e] = isq ? q[e] : k[e];
-        rope8<R>(xr, th, g, 1.0f);
+        for (int e = 0; e < 8; ++e) xr[e] = isq ? gq8[e] : gk8[e];
+        rot8<R>(xr, gcs, gsn, g, 1.0f);
         const float f = isq ? 1.0f : sc;                  // k~ = scale rot(k^)
         float dth[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -546,16 +601,17 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
         // d(q^) = rot^T dq~ + dQK gamma k^;  d(k^) = scale rot^T dk~ + dQK gamma q^
 #pragma unroll
         for (int e = 0; e < 8; ++e) out[e] = f * dx[e];
-        rope8<R>(out, th, g, -1.0f);
+        rot8<R>(out, gcs, gsn, g, -1.0f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] += gqk * (isq ? k[e] : q[e]);
+        for (int e = 0; e < 8; ++e) out[e] += gqk * (isq ? gk8[e] : gq8[e]);
         // angle gradient of the pairs of this group (finished by the finish kernel)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * g + j;
           if (r < R) {
             float* dst = a.dang + (((long)b * L + t0 + lane) * H + h) * R + r;
-            *dst = isq ? dth[j] : *dst + dth[j];
+            dthf[j] = isq ? dth[j] : *dst + dth[j];
+            *dst = dthf[j];
           }
         }
         // dQ / dK rows
@@ -574,6 +630,16 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
           sm.ps[g][lane] = dsc;
         }
       }
+      // chunk sums of the finished angle gradient, for the reverse cumsum over chunks
+      if (!isq) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (4 * g + j < R) {
+            const float s = wave_sum(dthf[j]);
+            if (lane == 0) a.ctot[((long)bh * nc + c) * (R + 1) + 1 + 4 * g + j] = s;
+          }
+        }
+      }
       // bias gradient partials: column sums over the chunk's tokens
       float* pb = (isq ? a.pqb : a.pkb) + ((long)bh * nc + c) * N + 8 * g;
 #pragma unroll
@@ -585,99 +651,136 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
     __syncthreads();
   }
 
-  // ---- per token: dA, d(scale), d(gamma) into the dADT, dTrap, dDT outputs
-  if (wave == 0 && tok) {
+  // ---- per token: dA and d(gamma) into the dADT and dDT outputs, d(scale) into the
+  // workspace, and the chunk sum of dA
+  if (wave == 0) {
     float da = 0.0f, ds = 0.0f;
-    for (int g = 0; g < N / 8; ++g) {
-      da += sm.pq[g][lane];
-      ds += sm.ps[g][lane];
+    if (tok) {
+      for (int g = 0; g < N / 8; ++g) {
+        da += sm.pq[g][lane];
+        ds += sm.ps[g][lane];
+      }
+      const long o = (long)bh * L + t0 + lane;
+      a.dadt[o] = da;
+      a.dsc[o] = ds;
+      a.ddt[o] = sm.dqk[lane] * sm.qk[lane] + ds;
     }
-    const long o = (long)bh * L + t0 + lane;
-    a.dadt[o] = da;
-    a.dtrap[o] = ds;
-    a.ddt[o] = sm.dqk[lane] * sm.qk[lane] + ds;
+    const float tot = wave_sum(da);
+    if (lane == 0) a.ctot[((long)bh * nc + c) * (a.s.R + 1)] = tot;
   }
 }
 
 // --------------------------------------------------------------- finishing scans
-// Per (b, h), blocks of 64 tokens from the end: dadt = reverse cumsum of dA;
-// dPhi = reverse cumsum of d(theta), dAngles = dPhi pi dt (1 - tanh^2), the angle
-// part of dDT = pi sum_r dPhi tanh; du_t = d(scale)_{t-1}; dDT = dgamma sigmoid +
-// du (1 - sigmoid) + angle part; dTrap = (dgamma - du) dt sigmoid (1 - sigmoid).
+// One workgroup per (chunk, b, h), lane = token: dadt = reverse cumsum of dA; dPhi =
+// reverse cumsum of d(theta), dAngles = dPhi pi dt (1 - tanh^2), the angle part of
+// dDT = pi sum_r dPhi tanh; du_t = d(scale)_{t-1}; dDT = dgamma sigmoid + du
+// (1 - sigmoid) + angle part; dTrap = (dgamma - du) dt sigmoid (1 - sigmoid).  The
+// sums over later chunks come from the chunk totals.  The chunk's d(theta) and angle
+// rate rows pass through LDS so that the (token, pair) tiles move coalesced.
 constexpr int kFinWaves = 4;
+template <int CS>
 __global__ __launch_bounds__(64 * kFinWaves)
 void scan_bwd_finish_kernel(BwdArgs a) {
   __shared__ float part[kFinWaves][64];
-  __shared__ float carry_th[64];
+  __shared__ float carry[65];                // [0]: dA of the later chunks, [1 + r]: d(theta)
+  __shared__ float tdth[CS][65];             // d(theta), then dAngles, of (token, pair)
+  __shared__ float tang[CS][65];             // angle rates
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int bh = blockIdx.x, b = bh / a.s.H, h = bh % a.s.H;
-  const int L = a.s.L, H = a.s.H, R = a.s.R;
+  const int c = blockIdx.x, bh = blockIdx.y, b = bh / a.s.H, h = bh % a.s.H;
+  const int L = a.s.L, H = a.s.H, R = a.s.R, nc = a.nc;
   const float kPi = 3.14159265358979323846f;
-  for (int r = tid; r < R; r += 64 * kFinWaves) carry_th[r] = 0.0f;
-  float carry_a = 0.0f;
+  // suffix sums of the chunk totals over chunks c+1.., one value per wave pass
+  for (int v = wave; v <= R; v += kFinWaves) {
+    float s = 0.0f;
+    for (int cc = c + 1 + lane; cc < nc; cc += 64) s += a.ctot[((long)bh * nc + cc) * (R + 1) + v];
+    s = wave_sum(s);
+    if (lane == 0) carry[v] = s;
+  }
   __syncthreads();
-  const int nblk = (L + 63) / 64;
-  for (int j = nblk - 1; j >= 0; --j) {
-    const int t = 64 * j + lane;
-    const bool tok = t < L;
-    const long o = (long)bh * L + t;
-    const float dt = tok ? a.s.dt[o] : 0.0f;
-    float angp = 0.0f;
-    // rope pair r belongs to one wave, which alone reads and updates carry_th[r]
-    for (int r = wave; r < R; r += kFinWaves) {
-      float* dp = a.dang + (((long)b * L + t) * H + h) * R + r;
-      const float d = tok ? *dp : 0.0f;
-      const float sum = wave_rev_scan(d, lane) + carry_th[r];
-      const float tot = __shfl(sum, 0, 64);
-      if (tok) {
-        const float tn = tanhf(a.s.ang[(((long)b * L + t) * H + h) * R + r]);
-        *dp = sum * kPi * dt * (1.0f - tn * tn);
-        angp += sum * tn * kPi;
-      }
-      if (lane == 0) carry_th[r] = tot;
+  const int t = c * CS + lane;
+  const bool tok = lane < CS && t < L;
+  const long o = (long)bh * L + t;
+  const float dt = tok ? a.s.dt[o] : 0.0f;
+  const int nt = min(CS, L - c * CS);                                // tokens of this chunk
+  const long row0 = (((long)b * L + c * CS) * H + h) * R;           // (token 0, pair 0)
+  for (int i = tid; i < nt * R; i += 64 * kFinWaves) {
+    const int tt = i / R, r = i % R;
+    tdth[tt][r] = a.dang[row0 + (long)tt * H * R + r];
+    tang[tt][r] = a.s.ang[row0 + (long)tt * H * R + r];
+  }
+  __syncthreads();
+  float angp = 0.0f;
+  for (int r = wave; r < R; r += kFinWaves) {
+    const float d = tok ? tdth[lane][r] : 0.0f;
+    const float sum = wave_rev_scan(d, lane) + carry[1 + r];
+    if (tok) {
+      const float tn = tanhf(tang[lane][r]);
+      tdth[lane][r] = sum * kPi * dt * (1.0f - tn * tn);
+      angp += sum * tn * kPi;
     }
-    part[wave][lane] = angp;
-    __syncthreads();
-    if (wave == 0) {
-      const float dA = tok ? a.dadt[o] : 0.0f;
-      const float sum = wave_rev_scan(dA, lane) + carry_a;
-      carry_a = __shfl(sum, 0, 64);
-      float angd = 0.0f;
-      for (int w = 0; w < kFinWaves; ++w) angd += part[w][lane];
-      const float dsc = tok ? a.dtrap[o] : 0.0f;
-      float du = __shfl_up(dsc, 1, 64);
-      if (lane == 0) du = (t > 0) ? a.dtrap[o - 1] : 0.0f;
-      const float dg = tok ? a.ddt[o] : 0.0f;
-      if (tok) {
-        const float sg = 1.0f / (1.0f + expf(-a.s.trap[o]));
-        a.dadt[o] = sum;
-        a.ddt[o] = dg * sg + du * (1.0f - sg) + angd;
-        a.dtrap[o] = (dg - du) * dt * sg * (1.0f - sg);
-      }
+  }
+  part[wave][lane] = angp;
+  __syncthreads();
+  for (int i = tid; i < nt * R; i += 64 * kFinWaves) {
+    const int tt = i / R, r = i % R;
+    a.dang[row0 + (long)tt * H * R + r] = tdth[tt][r];
+  }
+  if (wave == 0) {
+    const float dA = tok ? a.dadt[o] : 0.0f;
+    const float sum = wave_rev_scan(dA, lane) + carry[0];
+    float angd = 0.0f;
+    for (int w = 0; w < kFinWaves; ++w) angd += part[w][lane];
+    if (tok) {
+      const float du = t > 0 ? a.dsc[o - 1] : 0.0f;
+      const float dg = a.ddt[o];
+      const float sg = 1.0f / (1.0f + expf(-a.s.trap[o]));
+      a.dadt[o] = sum;
+      a.ddt[o] = dg * sg + du * (1.0f - sg) + angd;
+      a.dtrap[o] = (dg - du) * dt * sg * (1.0f - sg);
     }
-    __syncthreads();
   }
 }
 
-// Bias and D gradients: sums over batch and chunks of the per-chunk partials.
-__global__ void scan_bwd_reduce_kernel(BwdArgs a) {
-  const int h = blockIdx.x, N = a.s.N, H = a.s.H, B = a.s.B, nc = a.nc;
-  for (int n = threadIdx.x; n < N; n += blockDim.x) {
-    float sq = 0.0f, sk = 0.0f;
-    for (int b = 0; b < B; ++b)
-      for (int c = 0; c < nc; ++c) {
-        const long i = (((long)b * H + h) * nc + c) * N + n;
-        sq += a.pqb[i];
-        sk += a.pkb[i];
-      }
-    a.dqb[(long)h * N + n] = sq;
-    a.dkb[(long)h * N + n] = sk;
+// Bias and D gradients: sums over batch and chunks of the per-chunk partials.  Block
+// (h, column block of 16): 16 partial sums per column in a fixed order, then a tree.
+__global__ __launch_bounds__(256)
+void scan_bwd_reduce_kernel(BwdArgs a) {
+  __shared__ float red[2][256];
+  const int h = blockIdx.x, tid = threadIdx.x, N = a.s.N, H = a.s.H, B = a.s.B, nc = a.nc;
+  const int n = blockIdx.y * 16 + (tid & 15), part = tid >> 4;
+  const int J = B * nc;
+  float sq = 0.0f, sk = 0.0f;
+  if (n < N)
+    for (int j = part; j < J; j += 16) {
+      const long i = (((long)(j / nc) * H + h) * nc + j % nc) * N + n;
+      sq += a.pqb[i];
+      sk += a.pkb[i];
+    }
+  red[0][tid] = sq;
+  red[1][tid] = sk;
+  __syncthreads();
+  for (int w = 128; w >= 16; w >>= 1) {
+    if (tid < w) {
+      red[0][tid] += red[0][tid + w];
+      red[1][tid] += red[1][tid + w];
+    }
+    __syncthreads();
   }
-  if (a.dD && threadIdx.x == 0) {
+  if (tid < 16 && n < N) {
+    a.dqb[(long)h * N + n] = red[0][tid];
+    a.dkb[(long)h * N + n] = red[1][tid];
+  }
+  if (a.dD && blockIdx.y == 0) {
+    __syncthreads();
     float s = 0.0f;
-    for (int b = 0; b < B; ++b)
-      for (int c = 0; c < nc; ++c) s += a.pd[((long)b * H + h) * nc + c];
-    a.dD[h] = s;
+    for (int j = tid; j < J; j += 256) s += a.pd[((long)(j / nc) * H + h) * nc + j % nc];
+    red[0][tid] = s;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+      if (tid < w) red[0][tid] += red[0][tid + w];
+      __syncthreads();
+    }
+    if (tid == 0) a.dD[h] = red[0][0];
   }
 }
 
@@ -705,7 +808,7 @@ __global__ void scan_bwd_gqa_kernel(BwdArgs a) {
 size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct BwdWs {
-  size_t hs, gs, th, pqb, pkb, pd, dqh, dkh, total;
+  size_t hs, gs, th, pqb, pkb, pd, dsc, ctot, dqh, dkh, total;
 };
 
 BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R) {
@@ -721,6 +824,8 @@ BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R
   w.pqb = take(bhc * N * 4);
   w.pkb = take(bhc * N * 4);
   w.pd = take(bhc * 4);
+  w.dsc = take((size_t)B * H * L * 4);
+  w.ctot = take(bhc * (R + 1) * 4);
   const bool gqa = Hqk < H;
   w.dqh = gqa ? take((size_t)B * L * H * N * 4) : 0;
   w.dkh = gqa ? take((size_t)B * L * H * N * 4) : 0;
@@ -768,6 +873,8 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.pd = reinterpret_cast<float*>(base + w.pd);
   a.dqh = w.dqh ? reinterpret_cast<float*>(base + w.dqh) : nullptr;
   a.dkh = w.dkh ? reinterpret_cast<float*>(base + w.dkh) : nullptr;
+  a.dsc = reinterpret_cast<float*>(base + w.dsc);
+  a.ctot = reinterpret_cast<float*>(base + w.ctot);
   a.nc = (s.L + CS - 1) / CS;
 
   // 1. chunk states and angles (the forward's state-only pass)
@@ -799,9 +906,10 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   M3_BWD_SHAPES(X)
 #undef X
   if (!found) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(scan_bwd_finish_kernel, grid_bh, dim3(64 * kFinWaves), 0, st, a);
+  if (CS == 64) hipLaunchKernelGGL(scan_bwd_finish_kernel<64>, grid_c, dim3(64 * kFinWaves), 0, st, a);
+  else hipLaunchKernelGGL(scan_bwd_finish_kernel<32>, grid_c, dim3(64 * kFinWaves), 0, st, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(scan_bwd_reduce_kernel, dim3(s.H), dim3(128), 0, st, a);
+  hipLaunchKernelGGL(scan_bwd_reduce_kernel, dim3(s.H, (s.N + 15) / 16), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -93,7 +93,8 @@ def test_split_workspace_sizes(lib):
 def test_backward_workspace_sizes(lib):
     """Backward workspace: chunk-entering states and adjoint states (B*H*nc*P*N in
     the I/O type each, 64-token chunks for bf16, 32 for fp32), chunk angles, bias and
-    D partials, and per-head dQ/dK (float32) when Hqk < H; 0 without a kernel."""
+    D partials, per-token d(scale), chunk sums of dA and d(theta), and per-head dQ/dK
+    (float32) when Hqk < H; 0 without a kernel."""
     f = lib.m3_chunk_scan_bwd_ws_bytes
     bf, f32 = 1, 0
     al = lambda n: (n + 255) // 256 * 256  # noqa: E731
@@ -102,7 +103,8 @@ def test_backward_workspace_sizes(lib):
         cs = 64 if io == bf else 32
         bhc = B * H * ((L + cs - 1) // cs)
         ts = 2 if io == bf else 4
-        n = 2 * al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4) + 2 * al(bhc * N * 4) + al(bhc * 4)
+        n = (2 * al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4) + 2 * al(bhc * N * 4) + al(bhc * 4)
+             + al(B * H * L * 4) + al(bhc * (R + 1) * 4))
         if Hqk < H:
             n += 2 * al(B * L * H * N * 4)
         return n
