@@ -48,6 +48,13 @@ def scan_flops(B, L, H, N, P, CS):
     return B * L * H * (2 * CS * N + 2 * CS * P + 4 * P * N)
 
 
+def shared_bytes(B, L, H, N, P, R, s_io):
+    """Algorithmic HBM bytes of one call of the fused path's contract: Q, K and the
+    angle rates read once per token (shared over heads), V, Z, Out and ADT, DT,
+    Trap per token-head."""
+    return B * L * (2 * N * s_io + R * 4) + B * L * H * (3 * P * s_io + 3 * 4)
+
+
 def bwd_bytes(B, L, H, N, P, R, s_io):
     """Algorithmic HBM bytes of one backward call: the forward's inputs and dOut read
     once (Q, K; V, Z, dOut at s_io; ADT, DT, Trap, angles f32), every gradient
@@ -127,6 +134,18 @@ def bench_bwd(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
     fn = lambda: mamba3_siso_hip_bwd(*args, dout, chunk_size=CS)  # noqa: E731
     wall, kern = time_calls(torch, fn, steps, warmup)
     nbytes = bwd_bytes(B, L, H, N, P, R, 2)
+    return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
+
+
+def bench_shared(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
+    """Config 2 with B, C and the angle rates shared over heads (the fused path)."""
+    from mamba3_rocm import mamba3_ssd_chunked_shared_hip
+    Q, K, V, ADT, DT, Trap, Qb, Kb, Ang, D, Z = make_scan_inputs(torch, B, L, H, N, P, R, seed, torch.bfloat16)
+    Qs, Ks, Angs = Q[:, :, 0].contiguous(), K[:, :, 0].contiguous(), Ang[:, :, 0].contiguous()
+    fn = lambda: mamba3_ssd_chunked_shared_hip(Qs, Ks, V, ADT, DT, Trap, Angs, Qb, Kb, D, Z,  # noqa: E731
+                                               chunk_size=CS)
+    wall, kern = time_calls(torch, fn, steps, warmup)
+    nbytes = shared_bytes(B, L, H, N, P, R, 2)
     return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
 
 
@@ -221,7 +240,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "copy"), default="scan")
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "shared", "copy"), default="scan")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -251,6 +270,13 @@ def main():
         # backward at config 2 alone, for profiling
         r = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)
         print(json.dumps({"mode": "bwd", "ms": round(r["kernel_s"] * 1e3, 4),
+                          "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
+                          "achieved_gbs": round(r["achieved_gbs"], 1),
+                          "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        return
+    if args.mode == "shared":
+        r = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)
+        print(json.dumps({"mode": "shared", "kernel_ms": round(r["kernel_s"] * 1e3, 4),
                           "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
                           "achieved_gbs": round(r["achieved_gbs"], 1),
                           "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
@@ -293,6 +319,7 @@ def main():
         dec = bench_decode(torch, 512, 32, 128, 64, 32, 256, 16, seed=4)
         lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
         bw = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
+        sh = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         out["secondary"] = {
             "decode_config4": {"B": 512, "H": 32, "P": 64, "N": 128, "steps": 256,
                                "us_per_step": round(dec["kernel_s"] * 1e6, 2),
@@ -304,6 +331,11 @@ def main():
                                      "tokens_per_s": round(32768 / lc["wall_s"], 1),
                                      "achieved_gbs": round(lc["achieved_gbs"], 1),
                                      "frac_hbm": round(lc["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "shared_bc_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
+                                  "kernel_ms": round(sh["kernel_s"] * 1e3, 4),
+                                  "tokens_per_s": round(8 * 4096 / sh["wall_s"], 1),
+                                  "achieved_gbs": round(sh["achieved_gbs"], 1),
+                                  "frac_hbm": round(sh["achieved_gbs"] / HBM_PEAK_GBS, 4)},
             "backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
                                  "ms": round(bw["kernel_s"] * 1e3, 4),
                                  "tokens_per_s": round(8 * 4096 / bw["wall_s"], 1),

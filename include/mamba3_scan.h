@@ -149,6 +149,38 @@ int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
                       int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The fused front end's contract: Q, K (B,L,N) and the angle rates (B,L,R) shared
+ * over the H heads, the rest per head as in m3_chunk_scan_fwd.  Replaces the
+ * reference's mamba3_ssd_chunked_pallas (src/base_model/models/mamba3_pallas.py:
+ * 813-849, the model's shared_bc path, mamba3.py:356).  Same result as
+ * m3_chunk_scan_fwd with Q, K and the angle rates repeated over heads.  The
+ * workspace is as for m3_chunk_scan_fwd_ws (m3_chunk_scan_ws_bytes; NULL runs one
+ * pass).  Blocks of heads that share a Q/K row are placed on one XCD so that its
+ * L2 serves the sharing.
+ */
+int m3_chunk_scan_fwd_shared(const void* Q, const void* K, const void* V,
+                             const float* ADT, const float* DT, const float* Trap,
+                             const float* Q_bias, const float* K_bias, const float* Angles,
+                             const float* D, const void* Z, void* Out,
+                             int B, int L, int H, int N, int P, int R,
+                             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Backward of m3_chunk_scan_fwd_shared (the fused path's custom VJPs,
+ * mamba3_pallas.py:292-410): dQ, dK (B,L,N) and dAngles (B,L,R) are summed over
+ * heads; the rest as in m3_chunk_scan_bwd.
+ */
+size_t m3_chunk_scan_bwd_shared_ws_bytes(int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype);
+int m3_chunk_scan_bwd_shared(const void* Q, const void* K, const void* V,
+                             const float* ADT, const float* DT, const float* Trap,
+                             const float* Q_bias, const float* K_bias, const float* Angles,
+                             const float* D, const void* Z, const void* dOut,
+                             void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                             float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                             int B, int L, int H, int N, int P, int R,
+                             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * One decode step for a batch, in place on the carry.  Replaces the body of
  * rnn_step inside Mamba3SSM.__call_rnn__ (src/base_model/models/mamba3.py:498-562)
  * vmapped over batch (lob_seq_model.py:747-751):

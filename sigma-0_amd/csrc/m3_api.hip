@@ -66,15 +66,16 @@ size_t m3_chunk_scan_ws_bytes(int B, int L, int H, int N, int P, int R, int chun
   return m3::scan_split_ws_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, N, P, R, chunk_size);
 }
 
-int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
-                         const float* ADT, const float* DT, const float* Trap,
-                         const float* Q_bias, const float* K_bias, const float* Angles,
-                         const float* D, const void* Z, void* Out,
-                         const float* init_theta, const float* init_ssm,
-                         const float* init_k, const float* init_v,
-                         float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
-                         int B, int L, int H, int Hqk, int N, int P, int R,
-                         int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+namespace {
+int scan_fwd(const void* Q, const void* K, const void* V,
+             const float* ADT, const float* DT, const float* Trap,
+             const float* Q_bias, const float* K_bias, const float* Angles,
+             const float* D, const void* Z, void* Out,
+             const float* init_theta, const float* init_ssm,
+             const float* init_k, const float* init_v,
+             float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+             int B, int L, int H, int Hqk, int N, int P, int R,
+             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
@@ -110,6 +111,7 @@ int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
   a.init_theta = init_theta; a.init_h = init_ssm; a.init_k = init_k; a.init_v = init_v;
   a.fin_theta = fin_theta; a.fin_h = fin_ssm; a.fin_k = fin_k; a.fin_v = fin_v;
   a.B = B; a.L = L; a.H = H; a.Hqk = Hqk; a.N = N; a.P = P; a.R = R; a.CS = chunk_size;
+  a.ang_shared = ang_shared ? 1 : 0;
   const bool bf = io_dtype == M3_DTYPE_BF16;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (impl == M3_IMPL_CHUNKED_MFMA) {
@@ -123,6 +125,32 @@ int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
     return check_launch(m3::scan_chunked_launch(a, bf, st), "chunk scan");
   }
   return check_launch(m3::scan_generic_launch(a, bf, st), "generic scan");
+}
+}  // namespace
+
+int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
+                         const float* ADT, const float* DT, const float* Trap,
+                         const float* Q_bias, const float* K_bias, const float* Angles,
+                         const float* D, const void* Z, void* Out,
+                         const float* init_theta, const float* init_ssm,
+                         const float* init_k, const float* init_v,
+                         float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                         int B, int L, int H, int Hqk, int N, int P, int R,
+                         int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+  return scan_fwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, init_theta, init_ssm, init_k, init_v,
+                  fin_theta, fin_ssm, fin_k, fin_v, B, L, H, Hqk, N, P, R, chunk_size, io_dtype, ws, ws_bytes, stream,
+                  false);
+}
+
+int m3_chunk_scan_fwd_shared(const void* Q, const void* K, const void* V,
+                             const float* ADT, const float* DT, const float* Trap,
+                             const float* Q_bias, const float* K_bias, const float* Angles,
+                             const float* D, const void* Z, void* Out,
+                             int B, int L, int H, int N, int P, int R,
+                             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+  return scan_fwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, nullptr, nullptr, nullptr, nullptr,
+                  nullptr, nullptr, nullptr, nullptr, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes, stream,
+                  true);
 }
 
 int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
@@ -150,22 +178,23 @@ int m3_chunk_scan_fwd(const void* Q, const void* K, const void* V,
                                  B, L, H, Hqk, N, P, R, chunk_size, io_dtype, stream);
 }
 
-size_t m3_chunk_scan_bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
-                                  int io_dtype) {
+namespace {
+size_t bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size, int io_dtype,
+                    bool ang_shared) {
   if ((io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16) || B <= 0 || L <= 0 || H <= 0 || Hqk <= 0 ||
       H % Hqk != 0 || chunk_size <= 0)
     return 0;
-  return m3::scan_bwd_ws_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, Hqk, N, P, R);
+  return m3::scan_bwd_ws_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, Hqk, N, P, R, ang_shared);
 }
 
-int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
-                      const float* ADT, const float* DT, const float* Trap,
-                      const float* Q_bias, const float* K_bias, const float* Angles,
-                      const float* D, const void* Z, const void* dOut,
-                      void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
-                      float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
-                      int B, int L, int H, int Hqk, int N, int P, int R,
-                      int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+int scan_bwd(const void* Q, const void* K, const void* V,
+             const float* ADT, const float* DT, const float* Trap,
+             const float* Q_bias, const float* K_bias, const float* Angles,
+             const float* D, const void* Z, const void* dOut,
+             void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+             float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+             int B, int L, int H, int Hqk, int N, int P, int R,
+             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
@@ -187,7 +216,7 @@ int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
   const void* vec_ptrs[] = {Q, K, V, Z, dOut, dQ, dK, dV, dZ};
   for (const void* p : vec_ptrs)
     if (!aligned16(p)) return fail(M3_E_ALIGN, "Q, K, V, Z, dOut and their gradients must be 16-byte aligned");
-  const size_t need = m3::scan_bwd_ws_bytes(bf, B, L, H, Hqk, N, P, R);
+  const size_t need = m3::scan_bwd_ws_bytes(bf, B, L, H, Hqk, N, P, R, ang_shared);
   if (ws == nullptr || ws_bytes < need)
     return fail(M3_E_ARG, "workspace of %zu bytes, the backward needs %zu (m3_chunk_scan_bwd_ws_bytes)", ws_bytes, need);
   if (!aligned16(ws)) return fail(M3_E_ALIGN, "workspace must be 16-byte aligned");
@@ -198,11 +227,48 @@ int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
   a.init_theta = a.init_h = a.init_k = a.init_v = nullptr;
   a.fin_theta = a.fin_h = a.fin_k = a.fin_v = nullptr;
   a.B = B; a.L = L; a.H = H; a.Hqk = Hqk; a.N = N; a.P = P; a.R = R; a.CS = chunk_size;
+  a.ang_shared = ang_shared ? 1 : 0;
   g.dout = dOut;
   g.dq = dQ; g.dk = dK; g.dv = dV; g.dz = dZ;
   g.dadt = dADT; g.ddt = dDT; g.dtrap = dTrap; g.dang = dAngles;
   g.dqb = dQ_bias; g.dkb = dK_bias; g.dD = D ? dD : nullptr;
   return check_launch(m3::scan_bwd_launch(g, bf, ws, reinterpret_cast<hipStream_t>(stream)), "scan backward");
+}
+}  // namespace
+
+size_t m3_chunk_scan_bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
+                                  int io_dtype) {
+  return bwd_ws_bytes(B, L, H, Hqk, N, P, R, chunk_size, io_dtype, false);
+}
+
+int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
+                      const float* ADT, const float* DT, const float* Trap,
+                      const float* Q_bias, const float* K_bias, const float* Angles,
+                      const float* D, const void* Z, const void* dOut,
+                      void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                      float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                      int B, int L, int H, int Hqk, int N, int P, int R,
+                      int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+  return scan_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dOut, dQ, dK, dV, dADT, dDT, dTrap,
+                  dQ_bias, dK_bias, dAngles, dD, dZ, B, L, H, Hqk, N, P, R, chunk_size, io_dtype, ws, ws_bytes,
+                  stream, false);
+}
+
+size_t m3_chunk_scan_bwd_shared_ws_bytes(int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype) {
+  return bwd_ws_bytes(B, L, H, 1, N, P, R, chunk_size, io_dtype, true);
+}
+
+int m3_chunk_scan_bwd_shared(const void* Q, const void* K, const void* V,
+                             const float* ADT, const float* DT, const float* Trap,
+                             const float* Q_bias, const float* K_bias, const float* Angles,
+                             const float* D, const void* Z, const void* dOut,
+                             void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                             float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                             int B, int L, int H, int N, int P, int R,
+                             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+  return scan_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dOut, dQ, dK, dV, dADT, dDT, dTrap,
+                  dQ_bias, dK_bias, dAngles, dD, dZ, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes,
+                  stream, true);
 }
 
 int m3_decode_step(float* theta, float* ssm, float* k, float* v,

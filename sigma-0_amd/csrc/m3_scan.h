@@ -33,7 +33,17 @@ struct ScanArgs {
   // revolutions.
   void* chunk_h = nullptr;
   float* chunk_th = nullptr;
+  // Angle rates shared over heads, (B, L, R), instead of (B, L, H, R): the fused
+  // front end's layout (Q and K then come with Hqk = 1).
+  int ang_shared = 0;
 };
+
+// Block order for launches whose heads share Q/K rows: blocks are handed to the 8
+// XCDs round-robin, so block i runs (b, h) = (i % 8) * (G / 8) + i / 8 and the heads
+// of one batch row share one XCD's L2.  Identity when nothing is shared.
+__device__ __forceinline__ int xcd_bh(int i, int G, int Hqk, int H) {
+  return (Hqk < H && G % 8 == 0) ? (i % 8) * (G / 8) + i / 8 : i;
+}
 
 bool scan_generic_supported(int N, int P, int R);
 hipError_t scan_generic_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
@@ -55,7 +65,7 @@ struct ScanBwd {
   float* dqb; float* dkb; float* dD;                   // (H, N), (H, N), (H,) or null
 };
 bool scan_bwd_supported(bool bf16_io, int N, int P, int R);
-size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R);
+size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared);
 hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st);
 
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.

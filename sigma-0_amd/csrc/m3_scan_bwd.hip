@@ -166,7 +166,8 @@ __device__ __forceinline__ void group_theta(const BwdArgs& a, int b, int h, int 
     const bool tok = lane < CS && t0 + lane < L;
     const float dt = tok ? a.s.dt[(long)bh * L + t0 + lane] : 0.0f;
     float4 rt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (tok) rt = *reinterpret_cast<const float4*>(a.s.ang + (((long)b * L + t0 + lane) * H + h) * R + 4 * g);
+    const long arow = a.s.ang_shared ? (long)b * L + t0 + lane : ((long)b * L + t0 + lane) * H + h;
+    if (tok) rt = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * g);
     const float rv[4] = {rt.x, rt.y, rt.z, rt.w};
     const float* t0c = a.th0 + ((long)bh * a.nc + c) * R + 4 * g;
 #pragma unroll
@@ -703,10 +704,12 @@ void scan_bwd_finish_kernel(BwdArgs a) {
   const float dt = tok ? a.s.dt[o] : 0.0f;
   const int nt = min(CS, L - c * CS);                                // tokens of this chunk
   const long row0 = (((long)b * L + c * CS) * H + h) * R;           // (token 0, pair 0)
+  const int AH = a.s.ang_shared ? 1 : H;                             // angle-rate rows per token
+  const long arow0 = (((long)b * L + c * CS) * AH + (a.s.ang_shared ? 0 : h)) * R;
   for (int i = tid; i < nt * R; i += 64 * kFinWaves) {
     const int tt = i / R, r = i % R;
     tdth[tt][r] = a.dang[row0 + (long)tt * H * R + r];
-    tang[tt][r] = a.s.ang[row0 + (long)tt * H * R + r];
+    tang[tt][r] = a.s.ang[arow0 + (long)tt * AH * R + r];
   }
   __syncthreads();
   float angp = 0.0f;
@@ -784,6 +787,19 @@ void scan_bwd_reduce_kernel(BwdArgs a) {
   }
 }
 
+// Shared angle rates: dAngles (B, L, R) = sum over heads of the per-head gradients.
+__global__ void scan_bwd_angle_heads_kernel(BwdArgs a, float* dang_out) {
+  const int H = a.s.H, R = a.s.R;
+  const long total = (long)a.s.B * a.s.L * R;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const int r = i % R;
+    const long bt = i / R;
+    float s = 0.0f;
+    for (int h = 0; h < H; ++h) s += a.dang[(bt * H + h) * R + r];
+    dang_out[i] = s;
+  }
+}
+
 // GQA: dQ, dK of a Q/K head = sum over the value heads that share it.
 template <typename T>
 __global__ void scan_bwd_gqa_kernel(BwdArgs a) {
@@ -808,10 +824,10 @@ __global__ void scan_bwd_gqa_kernel(BwdArgs a) {
 size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct BwdWs {
-  size_t hs, gs, th, pqb, pkb, pd, dsc, ctot, dqh, dkh, total;
+  size_t hs, gs, th, pqb, pkb, pd, dsc, ctot, dqh, dkh, dangh, total;
 };
 
-BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R) {
+BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared) {
   const int CS = bf16_io ? 64 : 32;
   const long nc = (L + CS - 1) / CS, bhc = (long)B * H * nc;
   const size_t ts = bf16_io ? 2 : 4;
@@ -829,6 +845,7 @@ BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R
   const bool gqa = Hqk < H;
   w.dqh = gqa ? take((size_t)B * L * H * N * 4) : 0;
   w.dkh = gqa ? take((size_t)B * L * H * N * 4) : 0;
+  w.dangh = ang_shared && R > 0 ? take((size_t)B * L * H * R * 4) : 0;      // per-head dAngles
   w.total = off;
   return w;
 }
@@ -848,22 +865,23 @@ bool scan_bwd_supported(bool bf16_io, int N, int P, int R) {
   return false;
 }
 
-size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R) {
+size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared) {
   if (!scan_bwd_supported(bf16_io, N, P, R) || B <= 0 || L <= 0) return 0;
-  return bwd_layout(bf16_io, B, L, H, Hqk, N, P, R).total;
+  return bwd_layout(bf16_io, B, L, H, Hqk, N, P, R, ang_shared).total;
 }
 
 hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st) {
   const ScanArgs& s = g.fwd;
   const int CS = bf16_io ? 64 : 32;
-  const BwdWs w = bwd_layout(bf16_io, s.B, s.L, s.H, s.Hqk, s.N, s.P, s.R);
+  const BwdWs w = bwd_layout(bf16_io, s.B, s.L, s.H, s.Hqk, s.N, s.P, s.R, s.ang_shared != 0);
   char* base = reinterpret_cast<char*>(ws);
   BwdArgs a;
   a.s = s;
   a.s.CS = CS;
   a.dout = g.dout;
   a.dq = g.dq; a.dk = g.dk; a.dv = g.dv; a.dz = g.dz;
-  a.dadt = g.dadt; a.ddt = g.ddt; a.dtrap = g.dtrap; a.dang = g.dang;
+  a.dadt = g.dadt; a.ddt = g.ddt; a.dtrap = g.dtrap;
+  a.dang = w.dangh ? reinterpret_cast<float*>(base + w.dangh) : g.dang;   // per head, then summed
   a.dqb = g.dqb; a.dkb = g.dkb; a.dD = g.dD;
   a.hs = base + w.hs;
   a.gs = base + w.gs;
@@ -909,6 +927,10 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   if (CS == 64) hipLaunchKernelGGL(scan_bwd_finish_kernel<64>, grid_c, dim3(64 * kFinWaves), 0, st, a);
   else hipLaunchKernelGGL(scan_bwd_finish_kernel<32>, grid_c, dim3(64 * kFinWaves), 0, st, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (w.dangh) {
+    hipLaunchKernelGGL(scan_bwd_angle_heads_kernel, dim3(1024), dim3(256), 0, st, a, g.dang);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(scan_bwd_reduce_kernel, dim3(s.H, (s.N + 15) / 16), dim3(256), 0, st, a);
   return hipGetLastError();
 }

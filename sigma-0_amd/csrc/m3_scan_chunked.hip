@@ -128,7 +128,7 @@ void scan_chunked_kernel(ScanArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __builtin_assume(wave >= 0 && wave < NW);
-  const int bh = blockIdx.x;
+  const int bh = xcd_bh(blockIdx.x, gridDim.x, a.Hqk, a.H);
   const int b = bh / a.H, h = bh % a.H;
   const int hq = h / (a.H / a.Hqk);
   const int Lg = a.L, H = a.H, HQ = a.Hqk;
@@ -153,10 +153,11 @@ void scan_chunked_kernel(ScanArgs a) {
   const bool has_z = a.z != nullptr;
 
   // ---- element offsets of row (b, t=0, head) in each input; rows advance by the stride
-  const long qk_stride = (long)HQ * N, v_stride = (long)H * P, a_stride = (long)H * R;
+  const int AH = a.ang_shared ? 1 : H;                 // angle rows per token
+  const long qk_stride = (long)HQ * N, v_stride = (long)H * P, a_stride = (long)AH * R;
   const long qk_row = ((long)b * Lg * HQ + hq) * N + tb * qk_stride;
   const long v_row = ((long)b * Lg * H + h) * P + tb * v_stride;
-  const long a_row = ((long)b * Lg * H + h) * R + tb * a_stride;
+  const long a_row = ((long)b * Lg * AH + (a.ang_shared ? 0 : h)) * R + tb * a_stride;
   for (int i = tid; i < N; i += G::NT) {
     sm.qb[i] = a.qbias[(long)h * N + i];
     sm.kb[i] = a.kbias[(long)h * N + i];

@@ -65,7 +65,8 @@ void scan_generic_kernel(ScanArgs a) {
     const long tok = (long)b * L + t;
     // A: angle update, biased q/k, x
     for (int r = tid; r < R; r += kGenThreads) {
-      const float th = wrap_2pi(sTh[r] + tanh_fast(a.ang[(tok * H + h) * R + r]) * kPi * dtv);
+      const long arow = a.ang_shared ? tok : tok * H + h;      // shared rates: (B, L, R)
+      const float th = wrap_2pi(sTh[r] + tanh_fast(a.ang[arow * R + r]) * kPi * dtv);
       sTh[r] = th;
       sincos_wrapped(th, &sCos[r], &sSin[r]);
     }

@@ -2,7 +2,9 @@
 
 Prefill: ``mamba3_siso_hip`` (the reference's mamba3_siso_triton signature),
 ``mamba3_ssd_chunked_hip`` (the pure-JAX oracle's signature) and
-``mamba3_siso_hip_carry`` (prefill with the recurrent carry in and out).
+``mamba3_siso_hip_carry`` (prefill with the recurrent carry in and out) and
+``mamba3_ssd_chunked_shared_hip`` (the fused path's contract: B and C shared over
+heads).
 Backward: ``mamba3_siso_hip`` is differentiable (torch autograd, the reference's
 custom_vjp); ``mamba3_siso_hip_bwd`` returns all eleven input gradients directly.
 Decode: ``rnn_step_hip`` (the reference's rnn_step contract, batched).
@@ -12,8 +14,10 @@ nothing here computes on the CPU.
 from ._lib import Mamba3LibraryError, load  # noqa: F401
 from .decode import recurrent_angle_mode, recurrent_diagonal_mode, rnn_step_hip  # noqa: F401
 from .ops import (mamba3_siso_hip, mamba3_siso_hip_bwd, mamba3_siso_hip_carry,  # noqa: F401
-                  mamba3_ssd_chunked_hip, new_carry)
+                  mamba3_ssd_chunked_hip, mamba3_ssd_chunked_shared_hip,
+                  mamba3_ssd_chunked_shared_hip_bwd, new_carry)
 
-__all__ = ["mamba3_siso_hip", "mamba3_siso_hip_bwd", "mamba3_ssd_chunked_hip", "mamba3_siso_hip_carry", "new_carry",
+__all__ = ["mamba3_siso_hip", "mamba3_siso_hip_bwd", "mamba3_ssd_chunked_hip",
+           "mamba3_ssd_chunked_shared_hip", "mamba3_ssd_chunked_shared_hip_bwd", "mamba3_siso_hip_carry", "new_carry",
            "rnn_step_hip", "recurrent_angle_mode", "recurrent_diagonal_mode", "load",
            "Mamba3LibraryError"]

@@ -238,3 +238,139 @@ def mamba3_siso_hip_carry(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None
     elif init is not None:
         fin = tuple(t.clone() for t in init)
     return out, fin
+
+
+# ----------------------------------------------------------------- shared B/C
+def _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z):
+    """Validate and normalise the fused path's layout: Q, K (B, L, N) and angle
+    rates (B, L, R), shared over the H heads of V (B, L, H, P)."""
+    unbatched = V.dim() == 3
+    if unbatched:
+        Q, K, V, ADT, DT, Trap, angles = Q[None], K[None], V[None], ADT[None], DT[None], Trap[None], angles[None]
+        if Z is not None and Z.dim() == 3:
+            Z = Z[None]
+    if angles.dim() == 4:
+        angles = angles[:, :, 0]
+    _req(Q.dim() == 3 and tuple(Q.shape) == tuple(K.shape),
+         "the fused path takes Q and K as (L, d_state), shared over heads")
+    B, L, N = Q.shape
+    _req(V.dim() == 4 and tuple(V.shape[:2]) == (B, L), f"V must be {(B, L, '<H>', '<P>')}, got {tuple(V.shape)}")
+    H, P = V.shape[2], V.shape[3]
+    for name, t in (("Q", Q), ("K", K), ("V", V)):
+        _dev(t, name)
+    for name, t in (("ADT", ADT), ("DT", DT), ("Trap", Trap)):
+        _req(tuple(t.shape) == (B, H, L), f"{name} must be {(B, H, L)}, got {tuple(t.shape)}")
+    for name, t in (("Q_bias", Q_bias), ("K_bias", K_bias)):
+        _req(tuple(t.shape) == (H, N), f"{name} must be {(H, N)}, got {tuple(t.shape)}")
+    _req(angles.dim() == 3 and tuple(angles.shape[:2]) == (B, L),
+         f"angles must be (L, R) or (L, 1, R), got {tuple(angles.shape)}")
+    R = angles.shape[-1]
+    _req(R <= N // 2, f"headdim_angles ({R}) must be <= headdim_qk // 2 ({N // 2})")
+    if D is not None:
+        _req(tuple(D.shape) == (H,), f"D must be {(H,)}, got {tuple(D.shape)}")
+    if Z is not None:
+        _req(tuple(Z.shape) == (B, L, H, P), f"Z must be {(B, L, H, P)}, got {tuple(Z.shape)}")
+    dt = V.dtype
+    _req(dt in _IO, f"V dtype must be float32 or bfloat16, got {dt}")
+    p = dict(Q=Q.to(dt).contiguous(), K=K.to(dt).contiguous(), V=V.contiguous(), ADT=_f32(ADT), DT=_f32(DT),
+             Trap=_f32(Trap), Q_bias=_f32(Q_bias), K_bias=_f32(K_bias), Angles=_f32(angles),
+             D=None if D is None else _f32(D), Z=None if Z is None else Z.to(dt).contiguous())
+    return p, (B, L, H, N, P, R), unbatched
+
+
+def _shared_forward(args, chunk_size, seq_split):
+    p, (B, L, H, N, P, R), unbatched = _prep_shared(*args)
+    out = torch.empty_like(p["V"])
+    if out.numel():
+        lib = _lib.load()
+        io = _IO[p["V"].dtype]
+        ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, H, N, P, R, int(chunk_size), io) if seq_split else 0
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=p["V"].device)
+        rc = lib.m3_chunk_scan_fwd_shared(
+            _ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
+            _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(out),
+            B, L, H, N, P, R, int(chunk_size), io, ws.data_ptr() if ws_bytes else None, ws_bytes,
+            _stream(p["V"]))
+        _lib.check(rc, "m3_chunk_scan_fwd_shared")
+    return out[0] if unbatched else out
+
+
+def mamba3_ssd_chunked_shared_hip_bwd(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z, dOut,
+                                      chunk_size: int = 64):
+    """All eleven input gradients of mamba3_ssd_chunked_shared_hip, in its argument
+    order (Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z); dQ, dK and dangles
+    are summed over heads (shaped like the shared inputs); dD, dZ None when absent."""
+    ang_in = angles
+    p, (B, L, H, N, P, R), unbatched = _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z)
+    io = _IO[p["V"].dtype]
+    dO = (dOut[None] if unbatched else dOut).to(p["V"].dtype).contiguous()
+    _req(tuple(dO.shape) == (B, L, H, P), f"dOut must be {(B, L, H, P)}, got {tuple(dOut.shape)}")
+    dev = p["V"].device
+    f32 = dict(device=dev, dtype=torch.float32)
+    g = dict(Q=torch.empty_like(p["Q"]), K=torch.empty_like(p["K"]), V=torch.empty_like(p["V"]),
+             ADT=torch.empty(B, H, L, **f32), DT=torch.empty(B, H, L, **f32), Trap=torch.empty(B, H, L, **f32),
+             Angles=torch.empty(B, L, R, **f32), Q_bias=torch.empty(H, N, **f32), K_bias=torch.empty(H, N, **f32),
+             D=None if p["D"] is None else torch.empty(H, **f32),
+             Z=None if p["Z"] is None else torch.empty_like(p["Z"]))
+    if B and L:
+        lib = _lib.load()
+        ws_bytes = lib.m3_chunk_scan_bwd_shared_ws_bytes(B, L, H, N, P, R, int(chunk_size), io)
+        if ws_bytes == 0:
+            raise _lib.Mamba3LibraryError(
+                f"no backward kernel for dtype={p['V'].dtype} d_state={N} headdim={P} rope angles={R}")
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        rc = lib.m3_chunk_scan_bwd_shared(
+            _ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
+            _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(dO),
+            _ptr(g["Q"]), _ptr(g["K"]), _ptr(g["V"]), _ptr(g["ADT"]), _ptr(g["DT"]), _ptr(g["Trap"]),
+            _ptr(g["Q_bias"]), _ptr(g["K_bias"]), _ptr(g["Angles"]), _ptr(g["D"]), _ptr(g["Z"]),
+            B, L, H, N, P, R, int(chunk_size), io, ws.data_ptr(), ws_bytes, _stream(p["V"]))
+        _lib.check(rc, "m3_chunk_scan_bwd_shared")
+    else:
+        for t in g.values():
+            if t is not None:
+                t.zero_()
+    dang = g["Angles"].reshape(ang_in.shape if not unbatched else (1,) + tuple(ang_in.shape))
+    out = dict(g, Angles=dang)
+    order = ("Q", "K", "V", "ADT", "DT", "Trap", "Angles", "Q_bias", "K_bias", "D", "Z")
+    if unbatched:
+        return tuple(None if out[k] is None else (out[k] if k in ("Q_bias", "K_bias", "D") else out[k][0])
+                     for k in order)
+    return tuple(out[k] for k in order)
+
+
+class _Mamba3Shared(torch.autograd.Function):
+    """mamba3_ssd_chunked_shared_hip with its backward (the fused path is
+    differentiable, mamba3_pallas.py:824-830)."""
+
+    @staticmethod
+    def forward(ctx, chunk_size, seq_split, *args):
+        ctx.chunk_size = chunk_size
+        ctx.save_for_backward(*(t if isinstance(t, torch.Tensor) else None for t in args))
+        return _shared_forward(args, chunk_size, seq_split)
+
+    @staticmethod
+    def backward(ctx, dout):
+        args = ctx.saved_tensors
+        grads = mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=ctx.chunk_size)
+        return (None, None, *(None if t is None or gr is None else gr.to(t.dtype) for t, gr in zip(args, grads)))
+
+
+def mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D=None, Z=None,
+                                  chunk_size: int = 64, seq_split: bool = True) -> torch.Tensor:
+    """The reference's fused-path entry with B and C shared over heads,
+    mamba3_ssd_chunked_pallas(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z,
+    chunk_size) (src/base_model/models/mamba3_pallas.py:813-849): Q, K (L, N) shared
+    over heads; angles (L, R), (L, 1, R) or (L, nh, R); V, Z (L, nh, P); ADT, DT, Trap
+    (nh, L); Q_bias, K_bias (nh, N); D (nh,); optionally a leading batch dim on
+    every per-sequence input.  Same result as the per-head scan with Q, K and angles
+    repeated over heads.  Differentiable (torch autograd)."""
+    per_head = angles.dim() == (4 if V.dim() == 4 else 3) and angles.shape[-2] > 1
+    if per_head:
+        # angle rates per head: the per-head path with one shared Q/K head (Hqk = 1)
+        return mamba3_siso_hip(Q.unsqueeze(-2), K.unsqueeze(-2), V, ADT, DT, Trap, Q_bias, K_bias, angles,
+                               D, Z, chunk_size=chunk_size, seq_split=seq_split)
+    args = (Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z)
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in args):
+        return _Mamba3Shared.apply(int(chunk_size), bool(seq_split), *args)
+    return _shared_forward(args, chunk_size, seq_split)
