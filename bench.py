@@ -149,6 +149,21 @@ def bench_shared(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
     return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
 
 
+def bench_layer(torch, B, L, d_model, steps, warmup, seed):
+    """One Mamba3 mixer layer forward (config 5's layer: d_model 768, 24 heads of 64,
+    d_state 128, bf16 compute) on a (B, L, d_model) float32 input."""
+    from mamba3_rocm import Mamba3Layer
+    from mamba3_rocm.layer import init_params
+    params = init_params(d_model, seed, "cuda")
+    layer = Mamba3Layer(params, d_model, dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    x = torch.randn(B, L, d_model, device="cuda", generator=g)
+    wall, kern = time_calls(torch, lambda: layer(x), steps, warmup)
+    gemm_flops = 2 * B * L * d_model * (layer.d_in_proj + layer.d_inner)
+    return dict(wall_s=wall, kernel_s=kern, gemm_flops=gemm_flops)
+
+
 def bench_decode(torch, B, H, N, P, R, steps, warmup, seed):
     """Config 4: `steps` consecutive decode steps in place on a B=512 carry."""
     from mamba3_rocm import rnn_step_hip
@@ -240,7 +255,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "shared", "copy"), default="scan")
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "shared", "layer", "copy"), default="scan")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -273,6 +288,12 @@ def main():
                           "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
                           "achieved_gbs": round(r["achieved_gbs"], 1),
                           "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        return
+    if args.mode == "layer":
+        r = bench_layer(torch, 4, 12288, 768, args.steps, args.warmup, seed=5)
+        print(json.dumps({"mode": "layer", "ms": round(r["kernel_s"] * 1e3, 4),
+                          "tokens_per_s": round(4 * 12288 / r["wall_s"], 1),
+                          "gemm_tflop": round(r["gemm_flops"] / 1e12, 4)}), flush=True)
         return
     if args.mode == "shared":
         r = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)

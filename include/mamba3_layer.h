@@ -1,0 +1,48 @@
+/*
+ * C ABI of the Mamba3 mixer layer's fused elementwise kernels (libmamba3_rocm.so).
+ *
+ * The layer (Mamba3SSM, src/base_model/models/mamba3.py) is
+ *   proj = x @ in_proj                                  (library GEMM)
+ *   m3_layer_pre: split, BCNorm, decay, trapezoid, angle rates
+ *   m3_chunk_scan_fwd_shared (mamba3_scan.h): the scan, B/C shared over heads
+ *   m3_layer_post: output RMSNorm
+ *   out = m3_layer_post(...) @ out_proj                 (library GEMM)
+ * Same conventions as mamba3_scan.h: device pointers, io_dtype M3_DTYPE_F32 or
+ * M3_DTYPE_BF16, asynchronous on `stream`, 0 or an M3_E* code (m3_last_error).
+ */
+#ifndef MAMBA3_LAYER_H
+#define MAMBA3_LAYER_H
+
+#include "mamba3_scan.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Replaces the JAX operations of Mamba3SSM._preprocess with shared_bc=True
+ * (mamba3.py:203-268).  proj (B, L, 2HP + 2N + 3H + R) in io_dtype holds
+ * [z, x, B, C, dd_dt, dd_A, trap, angles] per token.  Writes Q = RMSNorm(C)
+ * and K = RMSNorm(B) (B, L, N) in io_dtype (statistics in float32, scales
+ * C_norm_scale / B_norm_scale (N,), eps), V = x and Z = z (B, L, H, P) in io_dtype,
+ * DT = softplus(dd_dt + dt_bias), ADT = min(-softplus(dd_A), -A_floor) * DT and
+ * Trap = trap as float32 (B, H, L), and the angle rates as float32 (B, L, R).
+ */
+int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_scale, const float* C_norm_scale,
+                 void* Q, void* K, void* V, void* Z, float* ADT, float* DT, float* Trap, float* Angles,
+                 int B, int L, int H, int P, int N, int R, float A_floor, float eps, int io_dtype, void* stream);
+
+/*
+ * Replaces the RMSNorm of Mamba3SSM._post_norm_and_project (mamba3.py:281-312,
+ * one device): out = (y * rsqrt(mean(y^2) + eps)) * scale over the last axis D,
+ * with the reference's rounding (the rsqrt in y's dtype, the product in the
+ * out-projection's dtype).  y, out (B, L, D) in io_dtype; scale (D,) float32.
+ */
+int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, int D, float eps, int io_dtype,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA3_LAYER_H */

@@ -9,7 +9,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "../../include/mamba3_scan.h"
+#include "../../include/mamba3_layer.h"
 #include "m3_scan.h"
 
 namespace {
@@ -308,6 +308,48 @@ int m3_decode_step(float* theta, float* ssm, float* k, float* v,
   return check_launch(m3::decode_step_launch(a, in_dtype == M3_DTYPE_BF16, out_dtype == M3_DTYPE_BF16,
                                              reinterpret_cast<hipStream_t>(stream)),
                       "decode step");
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_scale, const float* C_norm_scale,
+                 void* Q, void* K, void* V, void* Z, float* ADT, float* DT, float* Trap, float* Angles,
+                 int B, int L, int H, int P, int N, int R, float A_floor, float eps, int io_dtype, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || H <= 0 || P <= 0 || N <= 0 || R < 0)
+    return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d H=%d P=%d N=%d R=%d)", B, L, H, P, N, R);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!proj || !dt_bias || !B_norm_scale || !C_norm_scale || !Q || !K || !V || !Z || !ADT || !DT || !Trap ||
+      (R > 0 && !Angles))
+    return fail(M3_E_ARG, "NULL required pointer");
+  m3::LayerPreArgs a;
+  a.proj = proj; a.dt_bias = dt_bias; a.b_scale = B_norm_scale; a.c_scale = C_norm_scale;
+  a.q = Q; a.k = K; a.v = V; a.z = Z; a.adt = ADT; a.dt = DT; a.trap = Trap; a.ang = Angles;
+  a.B = B; a.L = L; a.H = H; a.P = P; a.N = N; a.R = R; a.A_floor = A_floor; a.eps = eps;
+  return check_launch(m3::layer_pre_launch(a, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "layer pre");
+}
+
+int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, int D, float eps, int io_dtype,
+                  void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!y || !scale || !out) return fail(M3_E_ARG, "NULL required pointer");
+  m3::LayerPostArgs a;
+  a.y = y; a.scale = scale; a.out = out; a.B = B; a.L = L; a.D = D; a.eps = eps;
+  return check_launch(m3::layer_post_launch(a, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "layer post");
 }
 
 }  // extern "C"

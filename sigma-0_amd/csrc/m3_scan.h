@@ -68,6 +68,25 @@ bool scan_bwd_supported(bool bf16_io, int N, int P, int R);
 size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared);
 hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st);
 
+// Mamba3 mixer layer: the elementwise work around the scan.
+struct LayerPreArgs {
+  const void* proj;                        // (B, L, 2HP + 2N + 3H + R), io dtype
+  const float* dt_bias; const float* b_scale; const float* c_scale;   // (H,), (N,), (N,)
+  void* q; void* k;                        // (B, L, N) io dtype: normalised C and B
+  void* v; void* z;                        // (B, L, H, P) io dtype
+  float* adt; float* dt; float* trap;      // (B, H, L)
+  float* ang;                              // (B, L, R)
+  int B, L, H, P, N, R;
+  float A_floor, eps;
+};
+struct LayerPostArgs {
+  const void* y; const float* scale; void* out;   // (B, L, D), (D,), (B, L, D)
+  int B, L, D;
+  float eps;
+};
+hipError_t layer_pre_launch(const LayerPreArgs& a, bool bf16_io, hipStream_t st);
+hipError_t layer_post_launch(const LayerPostArgs& a, bool bf16_io, hipStream_t st);
+
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS);
 hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStream_t st);

@@ -36,7 +36,8 @@ constexpr int kMinSegment = 256;       // tokens
 int seg_len_for(int B, int H, int L) {
   const int bh = B * H;
   if (bh <= 0 || bh * 2 > kTargetBlocks || L < 2 * kMinSegment) return 0;
-  const int s = min((kTargetBlocks + bh - 1) / bh, L / kMinSegment);
+  // whole waves of blocks only: a partly filled second wave costs a full segment time
+  const int s = min(kTargetBlocks / bh, L / kMinSegment);
   if (s < 2) return 0;
   const int len = ((L + s - 1) / s + 127) / 128 * 128;
   return (L + len - 1) / len >= 2 ? len : 0;

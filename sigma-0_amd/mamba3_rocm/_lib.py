@@ -22,7 +22,8 @@ IMPL_NONE, IMPL_CHUNKED_MFMA, IMPL_GENERIC = 0, 1, 2
 EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_scan_fwd",
            "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes", "m3_chunk_scan_fwd_ws",
            "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd", "m3_chunk_scan_fwd_shared",
-           "m3_chunk_scan_bwd_shared_ws_bytes", "m3_chunk_scan_bwd_shared", "m3_decode_step")
+           "m3_chunk_scan_bwd_shared_ws_bytes", "m3_chunk_scan_bwd_shared", "m3_decode_step",
+           "m3_layer_pre", "m3_layer_post")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -39,6 +40,8 @@ _SIGS = {
     "m3_chunk_scan_fwd_shared": ([_P] * 12 + [_I] * 8 + [_P, ctypes.c_size_t, _P], _I),
     "m3_chunk_scan_bwd_shared_ws_bytes": ([_I] * 8, ctypes.c_size_t),
     "m3_chunk_scan_bwd_shared": ([_P] * 23 + [_I] * 8 + [_P, ctypes.c_size_t, _P], _I),
+    "m3_layer_pre": ([_P] * 12 + [_I] * 6 + [ctypes.c_float, ctypes.c_float, _I, _P], _I),
+    "m3_layer_post": ([_P] * 3 + [_I] * 3 + [ctypes.c_float, _I, _P], _I),
     "m3_decode_step": ([_P] * 16 + [_I] * 9 + [_P], _I),
 }
 

@@ -1,0 +1,115 @@
+"""The Mamba3 mixer layer on gfx950: Mamba3SSM's forward
+(src/base_model/models/mamba3.py:191-331, the fused path with B and C shared over
+heads).
+
+    proj = x @ in_proj                      library GEMM in the compute dtype
+    m3_layer_pre                            split, BCNorm, decay, trapezoid, rates
+    m3_chunk_scan_fwd_shared                the scan
+    m3_layer_post                           output RMSNorm
+    out = ... @ out_proj                    library GEMM
+
+Parameters keep the reference's names and layouts (flax Dense kernels are
+(in, out)) and stay float32; ``dtype`` is the compute dtype of the projections
+and the scan's operands (the reference's ``dtype`` field, mamba3.py:103-110).
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict
+
+import torch
+
+from . import _lib
+from .ops import _IO, _ptr, _stream, mamba3_ssd_chunked_shared_hip
+
+PARAM_NAMES = ("in_proj", "dt_bias", "B_bias", "C_bias", "B_norm", "C_norm", "D", "out_norm", "out_proj")
+
+
+class Mamba3Layer:
+    """Forward of one Mamba3SSM layer (d_model -> d_model) on a ROCm device."""
+
+    def __init__(self, params: Dict[str, torch.Tensor], d_model: int, d_state: int = 128, expand: int = 2,
+                 headdim: int = 64, chunk_size: int = 64, rope_fraction: float = 0.5, A_floor: float = 1e-4,
+                 dtype: torch.dtype = torch.bfloat16, eps: float = 1e-6):
+        d_inner_target = expand * d_model
+        self.hd = min(headdim, d_inner_target)
+        self.nh = max(1, d_inner_target // self.hd)
+        split = int(d_state * rope_fraction)
+        split -= split % 2
+        self.R = split // 2
+        self.N, self.d_model, self.chunk_size = d_state, d_model, chunk_size
+        self.A_floor, self.eps, self.dtype = float(A_floor), float(eps), dtype
+        self.d_inner = self.nh * self.hd
+        self.d_in_proj = 2 * self.d_inner + 2 * d_state + 3 * self.nh + self.R
+        if dtype not in _IO:
+            raise ValueError(f"dtype must be float32 or bfloat16, got {dtype}")
+        p = {k: params[k] for k in PARAM_NAMES}
+        if not p["in_proj"].is_cuda:
+            raise ValueError("Mamba3Layer parameters must be ROCm device tensors (no CPU path)")
+        expect = dict(in_proj=(d_model, self.d_in_proj), dt_bias=(self.nh,), B_bias=(self.nh, d_state),
+                      C_bias=(self.nh, d_state), B_norm=(d_state,), C_norm=(d_state,), D=(self.nh,),
+                      out_norm=(self.d_inner,), out_proj=(self.d_inner, d_model))
+        for k, shape in expect.items():
+            if tuple(p[k].shape) != shape:
+                raise ValueError(f"{k} must be {shape}, got {tuple(p[k].shape)}")
+        self.params = {k: v.to(torch.float32).contiguous() for k, v in p.items()}
+        # the projections' operands in the compute dtype (nn.Dense(dtype=...) casts them)
+        self.w_in = self.params["in_proj"].to(dtype).contiguous()
+        self.w_out = self.params["out_proj"].to(dtype).contiguous()
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """x (B, L, d_model) or (L, d_model) -> the same shape, in the compute dtype."""
+        unbatched = x.dim() == 2
+        if unbatched:
+            x = x[None]
+        B, L, _ = x.shape
+        dt, dev = self.dtype, x.device
+        nh, hd, N, R = self.nh, self.hd, self.N, self.R
+        proj = torch.matmul(x.to(dt), self.w_in)                      # (B, L, d_in_proj)
+        Q = torch.empty(B, L, N, device=dev, dtype=dt)
+        K = torch.empty_like(Q)
+        V = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
+        Z = torch.empty_like(V)
+        f32 = dict(device=dev, dtype=torch.float32)
+        ADT, DT, Trap = (torch.empty(B, nh, L, **f32) for _ in range(3))
+        Ang = torch.empty(B, L, R, **f32)
+        lib = _lib.load()
+        io = _IO[dt]
+        pp = self.params
+        _lib.check(lib.m3_layer_pre(_ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]),
+                                    _ptr(Q), _ptr(K), _ptr(V), _ptr(Z), _ptr(ADT), _ptr(DT), _ptr(Trap), _ptr(Ang),
+                                    B, L, nh, hd, N, R, self.A_floor, self.eps, io, _stream(proj)),
+                   "m3_layer_pre")
+        y = mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, Ang, pp["C_bias"], pp["B_bias"], pp["D"], Z,
+                                          chunk_size=self.chunk_size)   # Q = C, K = B (mamba3.py:382-388)
+        yn = torch.empty(B, L, self.d_inner, device=dev, dtype=dt)
+        _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), B, L, self.d_inner, self.eps, io,
+                                     _stream(y)), "m3_layer_post")
+        out = torch.matmul(yn, self.w_out)
+        return out[0] if unbatched else out
+
+    __call__ = forward
+
+
+def init_params(d_model: int, seed: int, device, d_state: int = 128, expand: int = 2, headdim: int = 64,
+                rope_fraction: float = 0.5, dt_min: float = 0.001, dt_max: float = 0.1) -> Dict[str, torch.Tensor]:
+    """Random float32 parameters with the reference's initialisers (mamba3.py:145-183),
+    generated on the device."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    d_inner_target = expand * d_model
+    hd = min(headdim, d_inner_target)
+    nh = max(1, d_inner_target // hd)
+    split = int(d_state * rope_fraction)
+    split -= split % 2
+    R = split // 2
+    di = nh * hd
+    dproj = 2 * di + 2 * d_state + 3 * nh + R
+    f = dict(device=device, dtype=torch.float32)
+    u = torch.rand(nh, generator=g, **f)
+    dt = torch.exp(u * (math.log(dt_max) - math.log(dt_min)) + math.log(dt_min)).clamp_min(1e-4)
+    return dict(in_proj=torch.randn(d_model, dproj, generator=g, **f) / math.sqrt(d_model),
+                dt_bias=dt + torch.log(-torch.expm1(-dt)), B_bias=torch.ones(nh, d_state, **f),
+                C_bias=torch.ones(nh, d_state, **f), B_norm=torch.ones(d_state, **f), C_norm=torch.ones(d_state, **f),
+                D=torch.ones(nh, **f), out_norm=torch.ones(di, **f),
+                out_proj=torch.randn(di, d_model, generator=g, **f) / math.sqrt(di))

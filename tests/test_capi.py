@@ -15,6 +15,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mamba3_scan.h")
+HEADERS = [HEADER, os.path.join(ROOT, "include", "mamba3_layer.h")]
 
 
 @pytest.fixture(scope="module")
@@ -24,7 +25,7 @@ def lib():
 
 
 def _header_functions():
-    text = open(HEADER).read()
+    text = "\n".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(m3_\w+)\s*\(", text, re.M)))
 
 
@@ -39,7 +40,8 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd", "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes",
                             "m3_chunk_scan_fwd_ws", "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd",
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
-                            "m3_chunk_scan_bwd_shared", "m3_decode_step"])
+                            "m3_chunk_scan_bwd_shared", "m3_decode_step", "m3_layer_pre",
+                            "m3_layer_post"])
     for n in names:
         assert hasattr(lib, n), n
     from mamba3_rocm import _lib

@@ -1,0 +1,75 @@
+"""Pins of the mixer-layer oracle (oracle/mamba3_layer.py), CPU only.
+
+The layer composes the pinned scan oracle with simple maps; these checks fix
+the composition: the shared-B/C path equals the per-head path the reference
+also takes (B and C repeated over heads before BCNorm, mamba3.py:236-242 and
+265-268), RMSNorm and softplus identities, the decay floor, and linearity of the
+output projection.
+"""
+import numpy as np
+
+from oracle import mamba3_layer as ML
+from oracle import mamba3_ref as M
+
+
+def _case(seed=0, B=2, L=70, d_model=32, N=16, headdim=16):
+    p = ML.init_params(d_model, seed, d_state=N, headdim=headdim)
+    x = np.random.default_rng(seed + 1).standard_normal((B, L, d_model)).astype(np.float32)
+    return p, x
+
+
+def _per_head_path(p, x, N, headdim, chunk):
+    """The reference's non-shared preprocessing: B, C and angles repeated over heads
+    (mamba3.py:236-238, 265-268), BCNorm per head row, per-head scan."""
+    B, L, d_model = x.shape
+    nh, hd, R, _ = ML.dims(d_model, N, 2, headdim)
+    di = nh * hd
+    proj = x.astype(np.float64) @ p["in_proj"].astype(np.float64)
+    cut = np.cumsum([di, di, N, N, nh, nh, nh])
+    z, xv, Bm, Cm, dd_dt, dd_A, trap, ang = np.split(proj, cut, axis=-1)
+    Brep = np.repeat(Bm[:, :, None, :], nh, axis=2)
+    Crep = np.repeat(Cm[:, :, None, :], nh, axis=2)
+    Bn, Cn = ML.rmsnorm(Brep, p["B_norm"]), ML.rmsnorm(Crep, p["C_norm"])
+    A = np.minimum(-ML.softplus(dd_A), -1e-4)
+    DT = ML.softplus(dd_dt + p["dt_bias"])
+    y = M.mamba3_ssd_chunked_batched(
+        Cn, Bn, xv.reshape(B, L, nh, hd), np.transpose(A * DT, (0, 2, 1)), np.transpose(DT, (0, 2, 1)),
+        np.transpose(trap, (0, 2, 1)), np.repeat(ang[:, :, None, :], nh, axis=2), p["C_bias"], p["B_bias"],
+        p["D"], z.reshape(B, L, nh, hd), chunk_size=chunk).reshape(B, L, di)
+    y = y / np.sqrt(np.mean(y * y, axis=-1, keepdims=True) + ML.EPS) * p["out_norm"]
+    return y @ p["out_proj"].astype(np.float64)
+
+
+def test_shared_path_equals_per_head_path():
+    p, x = _case()
+    a = ML.layer_forward(p, x, d_state=16, headdim=16, chunk_size=16)
+    b = _per_head_path(p, x, 16, 16, 16)
+    assert np.abs(a - b).max() <= 1e-12 * np.abs(b).max()
+
+
+def test_rmsnorm_and_softplus_identities():
+    x = np.random.default_rng(3).standard_normal((5, 40)) * 7
+    y = ML.rmsnorm(x, np.ones(40))
+    assert np.allclose(np.sqrt(np.mean(y * y, axis=-1)), 1.0, atol=1e-6)
+    s = np.random.default_rng(4).standard_normal(40)
+    assert np.allclose(ML.rmsnorm(x, s), y * s)
+    t = np.linspace(-30, 30, 101)
+    assert np.allclose(ML.softplus(t) - ML.softplus(-t), t, atol=1e-12)
+    assert np.all(np.minimum(-ML.softplus(t), -1e-4) <= -1e-4)
+
+
+def test_output_projection_is_linear_and_chunk_invariant():
+    p, x = _case(seed=5)
+    base = ML.layer_forward(p, x, d_state=16, headdim=16, chunk_size=16)
+    q = dict(p, out_proj=p["out_proj"] * 2)
+    assert np.allclose(ML.layer_forward(q, x, d_state=16, headdim=16, chunk_size=16), 2 * base, rtol=1e-12,
+                       atol=1e-12)
+    assert np.allclose(ML.layer_forward(p, x, d_state=16, headdim=16, chunk_size=8), base, rtol=1e-9,
+                       atol=1e-12)
+
+
+def test_dims_follow_setup():
+    # model geometry: d_model 768, expand 2 -> 24 heads of 64, 32 rope pairs
+    nh, hd, R, dproj = ML.dims(768)
+    assert (nh, hd, R) == (24, 64, 32)
+    assert dproj == 2 * 1536 + 2 * 128 + 3 * 24 + 32
