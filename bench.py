@@ -13,11 +13,14 @@ Also reported on the same JSON line:
   cpu_baseline  the numpy float32 restatement of the reference scan
                 (oracle/, the reference's own JAX is not installed) timed on
                 the host on a bounded sample (one of the 8 sequences)
-  secondary     decode state update (config 4, HBM GB/s) and the long-context
-                scan (config 3), each with its own roofline
+  secondary     decode state update (config 4, HBM GB/s), the long-context
+                scan (config 3), the shared-B/C scan and the scan backward at
+                config 2, each with its own roofline, and the 12-layer backbone
+                prefill with its log-probabilities (config 5)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--no-secondary] [--mode scan|decode|copy]
+                       [--no-secondary]
+                       [--mode scan|decode|long|bwd|shared|layer|stack|copy]
 """
 from __future__ import annotations
 
@@ -164,6 +167,23 @@ def bench_layer(torch, B, L, d_model, steps, warmup, seed):
     return dict(wall_s=wall, kernel_s=kern, gemm_flops=gemm_flops)
 
 
+def bench_stack(torch, B, L, d_model, n_layers, vocab, steps, warmup, seed):
+    """Config 5: the Mamba3 backbone prefill (embedding, n_layers SequenceLayer blocks
+    with half_glu1 and prenorm around the mixer, decoder and log_softmax) on token ids
+    drawn uniformly from the vocabulary; bf16 compute, random-init parameters."""
+    from mamba3_rocm import Mamba3Stack
+    from mamba3_rocm.stack import init_params
+    params = init_params(vocab, d_model, n_layers, seed, "cuda")
+    stack = Mamba3Stack(params, d_model, activation="half_glu1", prenorm=True, dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    ids = torch.randint(0, vocab, (B, L), device="cuda", generator=g)
+    wall, kern = time_calls(torch, lambda: stack.logits(ids), steps, warmup)
+    layer = stack.blocks[0]["mixer"]
+    gemm_flops = 2 * B * L * d_model * (n_layers * (layer.d_in_proj + layer.d_inner + d_model) + vocab)
+    return dict(wall_s=wall, kernel_s=kern, gemm_flops=gemm_flops)
+
+
 def bench_decode(torch, B, H, N, P, R, steps, warmup, seed):
     """Config 4: `steps` consecutive decode steps in place on a B=512 carry."""
     from mamba3_rocm import rnn_step_hip
@@ -255,7 +275,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "shared", "layer", "copy"), default="scan")
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "shared", "layer", "stack", "copy"),
+                    default="scan")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     args = ap.parse_args()
@@ -292,6 +313,12 @@ def main():
     if args.mode == "layer":
         r = bench_layer(torch, 4, 12288, 768, args.steps, args.warmup, seed=5)
         print(json.dumps({"mode": "layer", "ms": round(r["kernel_s"] * 1e3, 4),
+                          "tokens_per_s": round(4 * 12288 / r["wall_s"], 1),
+                          "gemm_tflop": round(r["gemm_flops"] / 1e12, 4)}), flush=True)
+        return
+    if args.mode == "stack":
+        r = bench_stack(torch, 4, 12288, 768, 12, 2112, args.steps, args.warmup, seed=5)
+        print(json.dumps({"mode": "stack", "ms": round(r["kernel_s"] * 1e3, 4),
                           "tokens_per_s": round(4 * 12288 / r["wall_s"], 1),
                           "gemm_tflop": round(r["gemm_flops"] / 1e12, 4)}), flush=True)
         return
@@ -341,6 +368,7 @@ def main():
         lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
         bw = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         sh = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
+        bb = bench_stack(torch, 4, 12288, 768, 12, 2112, 5, 2, seed=5)
         out["secondary"] = {
             "decode_config4": {"B": 512, "H": 32, "P": 64, "N": 128, "steps": 256,
                                "us_per_step": round(dec["kernel_s"] * 1e6, 2),
@@ -362,6 +390,11 @@ def main():
                                  "tokens_per_s": round(8 * 4096 / bw["wall_s"], 1),
                                  "achieved_gbs": round(bw["achieved_gbs"], 1),
                                  "frac_hbm": round(bw["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "backbone_prefill_config5": {"B": 4, "L": 12288, "layers": 12, "d_model": 768, "vocab": 2112,
+                                         "activation": "half_glu1", "prenorm": True, "dtype": "bf16",
+                                         "ms": round(bb["kernel_s"] * 1e3, 4),
+                                         "tokens_per_s": round(4 * 12288 / bb["wall_s"], 1),
+                                         "gemm_tflops": round(bb["gemm_flops"] / bb["kernel_s"] / 1e12, 1)},
         }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

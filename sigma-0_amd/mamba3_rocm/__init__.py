@@ -9,18 +9,19 @@ Backward: ``mamba3_siso_hip`` is differentiable (torch autograd, the reference's
 custom_vjp); ``mamba3_siso_hip_bwd`` returns all eleven input gradients directly.
 Decode: ``rnn_step_hip`` (the reference's rnn_step contract, batched).
 Layer: ``Mamba3Layer`` (Mamba3SSM's forward: projections, BCNorm, decay, scan,
-output norm).
+output norm); ``Mamba3Stack`` (the embedding and SequenceLayer blocks around it).
 All run hand-written HIP kernels through the C ABI of include/mamba3_scan.h;
 nothing here computes on the CPU.
 """
 from ._lib import Mamba3LibraryError, load  # noqa: F401
 from .decode import recurrent_angle_mode, recurrent_diagonal_mode, rnn_step_hip  # noqa: F401
 from .layer import Mamba3Layer  # noqa: F401
+from .stack import Mamba3Stack  # noqa: F401
 from .ops import (mamba3_siso_hip, mamba3_siso_hip_bwd, mamba3_siso_hip_carry,  # noqa: F401
                   mamba3_ssd_chunked_hip, mamba3_ssd_chunked_shared_hip,
                   mamba3_ssd_chunked_shared_hip_bwd, new_carry)
 
 __all__ = ["mamba3_siso_hip", "mamba3_siso_hip_bwd", "mamba3_ssd_chunked_hip",
            "mamba3_ssd_chunked_shared_hip", "mamba3_ssd_chunked_shared_hip_bwd", "mamba3_siso_hip_carry", "new_carry",
-           "rnn_step_hip", "Mamba3Layer", "recurrent_angle_mode", "recurrent_diagonal_mode", "load",
+           "rnn_step_hip", "Mamba3Layer", "Mamba3Stack", "recurrent_angle_mode", "recurrent_diagonal_mode", "load",
            "Mamba3LibraryError"]

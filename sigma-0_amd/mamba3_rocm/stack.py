@@ -1,0 +1,104 @@
+"""The Mamba3 backbone around the mixer on gfx950: StackedEncoderModel
+(src/base_model/models/seq_model.py:47-118, use_embed_layer=True) of
+SequenceLayer blocks (layers.py:108-160) with the Mamba3 mixer (Mamba3Layer).
+
+A block is skip = x; LayerNorm if prenorm; mixer; activation (gelu, full_glu,
+half_glu1, half_glu2, with the block's out1/out2 Dense layers in the compute
+dtype); x = skip + x; LayerNorm if postnorm.  flax defaults: LayerNorm eps 1e-6,
+gelu with the tanh approximation.  The mixer runs the hand-written kernels; the
+norms, the gate and the embedding lookup are the host framework's (torch) ops.
+``logits`` adds the LOB models' per-token head (mode "none"): the decoder Dense
+on the float32 features, then log_softmax in float32 (lob_seq_model.py:530-542).
+Inference only (dropout is the identity).
+"""
+from __future__ import annotations
+
+from typing import Dict, List
+
+import torch
+import torch.nn.functional as F
+
+from .layer import Mamba3Layer
+
+ACTIVATIONS = ("gelu", "full_glu", "half_glu1", "half_glu2")
+
+
+class Mamba3Stack:
+    """Token ids (B, L) -> features (B, L, d_model), float32 residual stream."""
+
+    def __init__(self, params: Dict, d_model: int, activation: str = "half_glu1", prenorm: bool = True,
+                 d_state: int = 128, headdim: int = 64, chunk_size: int = 64, dtype: torch.dtype = torch.bfloat16):
+        if activation not in ACTIVATIONS:
+            raise ValueError(f"activation must be one of {ACTIVATIONS}, got {activation!r}")
+        self.activation, self.prenorm, self.dtype, self.d_model = activation, prenorm, dtype, d_model
+        self.embed = params["embed"].to(torch.float32).contiguous()
+        self.blocks: List[Dict] = []
+        for lp in params["layers"]:
+            b = dict(mixer=Mamba3Layer(lp["mixer"], d_model, d_state=d_state, headdim=headdim,
+                                       chunk_size=chunk_size, dtype=dtype),
+                     ln_scale=lp["ln_scale"].float(), ln_bias=lp["ln_bias"].float())
+            for n in ("out1", "out2"):
+                b[n + "_w"] = lp[n + "_w"].to(dtype).t().contiguous()     # flax (in, out) -> F.linear (out, in)
+                b[n + "_b"] = lp[n + "_b"].to(dtype)
+            self.blocks.append(b)
+        self.decoder_w = self.decoder_b = None
+        if "decoder_w" in params:
+            self.decoder_w = params["decoder_w"].float().t().contiguous()
+            self.decoder_b = params["decoder_b"].float().contiguous()
+
+    def _block(self, b, x):
+        skip = x
+        if self.prenorm:
+            x = F.layer_norm(x, (self.d_model,), b["ln_scale"], b["ln_bias"], eps=1e-6)
+        x = b["mixer"](x)                                   # compute dtype
+        dense = lambda a, n: F.linear(a, b[n + "_w"], b[n + "_b"])   # noqa: E731
+        if self.activation == "gelu":
+            x = F.gelu(x, approximate="tanh")
+        else:
+            g = F.gelu(x, approximate="tanh")
+            if self.activation == "full_glu":
+                x = dense(g, "out1") * torch.sigmoid(dense(g, "out2"))
+            elif self.activation == "half_glu1":
+                x = g * torch.sigmoid(dense(g, "out2"))
+            else:
+                x = x * torch.sigmoid(dense(g, "out2"))
+        x = skip + x.float()
+        if not self.prenorm:
+            x = F.layer_norm(x, (self.d_model,), b["ln_scale"], b["ln_bias"], eps=1e-6)
+        return x
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        x = self.embed[ids]
+        for b in self.blocks:
+            x = self._block(b, x)
+        return x
+
+    __call__ = forward
+
+    def logits(self, ids: torch.Tensor) -> torch.Tensor:
+        """Per-token log-probabilities (B, L, vocab), float32."""
+        if self.decoder_w is None:
+            raise ValueError("logits needs decoder_w and decoder_b in the parameters")
+        return torch.log_softmax(F.linear(self.forward(ids), self.decoder_w, self.decoder_b), dim=-1)
+
+
+def init_params(vocab: int, d_model: int, n_layers: int, seed: int, device, d_state: int = 128,
+                headdim: int = 64) -> Dict:
+    """Random float32 parameters on the device (the mixer's with its reference
+    initialisers, LayerNorm ones/zeros, Dense kernels N(0, 1/fan_in), the decoder
+    Dense to ``vocab``)."""
+    from .layer import init_params as mixer_params
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    f = dict(device=device, dtype=torch.float32)
+    p = dict(embed=torch.randn(vocab, d_model, generator=g, **f), layers=[])
+    for i in range(n_layers):
+        lp = dict(mixer=mixer_params(d_model, seed * 1000 + i, device, d_state=d_state, headdim=headdim),
+                  ln_scale=torch.ones(d_model, **f), ln_bias=torch.zeros(d_model, **f))
+        for n in ("out1", "out2"):
+            lp[n + "_w"] = torch.randn(d_model, d_model, generator=g, **f) / d_model ** 0.5
+            lp[n + "_b"] = torch.zeros(d_model, **f)
+        p["layers"].append(lp)
+    p["decoder_w"] = torch.randn(d_model, vocab, generator=g, **f) / d_model ** 0.5
+    p["decoder_b"] = torch.zeros(vocab, **f)
+    return p

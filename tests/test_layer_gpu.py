@@ -33,3 +33,52 @@ def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16):
     print(f"layer {(B, L, d_model, N, headdim)} bf16={bf16} rel={err:.3e}", flush=True)
     assert np.isfinite(y).all()
     assert err <= (2e-2 if bf16 else 1e-4)
+
+
+@pytest.mark.parametrize("activation,prenorm,bf16", [
+    ("half_glu1", True, True), ("full_glu", False, True), ("half_glu2", True, False), ("gelu", False, False),
+])
+def test_stack_matches_oracle(activation, prenorm, bf16):
+    """Embedding + two SequenceLayer blocks with the Mamba3 mixer vs the stack oracle."""
+    import torch
+    from mamba3_rocm import Mamba3Stack
+    from oracle import mamba3_stack as MS
+    N, hd = (128, 64) if bf16 else (64, 32)
+    p = MS.init_params(vocab=37, d_model=64, n_layers=2, seed=61, d_state=N, headdim=hd)
+    ids = np.random.default_rng(62).integers(0, 37, size=(2, 260))
+    tp = dict(embed=torch.from_numpy(p["embed"]).cuda(), decoder_w=torch.from_numpy(p["decoder_w"]).cuda(),
+              decoder_b=torch.from_numpy(p["decoder_b"]).cuda(), layers=[{k: ({kk: torch.from_numpy(vv).cuda() for kk, vv in v.items()} if k == "mixer"
+                           else torch.from_numpy(v).cuda()) for k, v in lp.items()} for lp in p["layers"]])
+    stack = Mamba3Stack(tp, 64, activation=activation, prenorm=prenorm, d_state=N, headdim=hd,
+                        dtype=torch.bfloat16 if bf16 else torch.float32)
+    y = stack(torch.from_numpy(ids).cuda()).float().cpu().numpy()
+    ref = MS.stack_forward(p, ids, activation=activation, prenorm=prenorm, d_state=N, headdim=hd, bf16=bf16)
+    err = rel(y, ref)
+    print(f"stack {activation} prenorm={prenorm} bf16={bf16} rel={err:.3e}", flush=True)
+    assert err <= (2e-2 if bf16 else 1e-4)
+
+
+def _torch_params(p):
+    import torch
+    t = lambda a: torch.from_numpy(a).cuda()   # noqa: E731
+    return dict(embed=t(p["embed"]), decoder_w=t(p["decoder_w"]), decoder_b=t(p["decoder_b"]),
+                layers=[{k: ({kk: t(vv) for kk, vv in v.items()} if k == "mixer" else t(v))
+                         for k, v in lp.items()} for lp in p["layers"]])
+
+
+def test_backbone_logits_config5_geometry():
+    """Config 5's model geometry (d_model 768, 24 heads of 64, d_state 128, vocab 2112,
+    half_glu1, prenorm, bf16) with 2 of its 12 layers on a short sequence: per-token
+    log-probabilities vs the oracle backbone, max-rel-err within 2e-2."""
+    import torch
+    from mamba3_rocm import Mamba3Stack
+    from oracle import mamba3_stack as MS
+    p = MS.init_params(vocab=2112, d_model=768, n_layers=2, seed=5)
+    ids = np.random.default_rng(55).integers(0, 2112, size=(1, 200))
+    stack = Mamba3Stack(_torch_params(p), 768, dtype=torch.bfloat16)
+    lp = stack.logits(torch.from_numpy(ids).cuda()).cpu().numpy()
+    ref = MS.lm_forward(p, ids, bf16=True)
+    err = rel(lp, ref)
+    agree = float(np.mean(np.argmax(lp, -1) == np.argmax(ref, -1)))
+    print(f"stack logits config5 geometry rel={err:.3e} argmax agreement={agree:.4f}", flush=True)
+    assert lp.dtype == np.float32 and err <= 2e-2

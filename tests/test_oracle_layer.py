@@ -73,3 +73,42 @@ def test_dims_follow_setup():
     nh, hd, R, dproj = ML.dims(768)
     assert (nh, hd, R) == (24, 64, 32)
     assert dproj == 2 * 1536 + 2 * 128 + 3 * 24 + 32
+
+
+def test_stack_oracle_identities():
+    """LayerNorm and gelu identities, and a block whose mixer outputs zero is the
+    identity (prenorm) or LayerNorm of its input (postnorm), for every activation."""
+    from oracle import mamba3_stack as MS
+    x = np.random.default_rng(6).standard_normal((3, 50)) * 4 + 2
+    y = MS.layernorm(x, np.ones(50), np.zeros(50))
+    assert np.allclose(y.mean(-1), 0, atol=1e-12) and np.allclose(y.std(-1), 1, atol=1e-5)
+    t = np.linspace(-6, 6, 61)
+    assert np.allclose(MS.gelu(t) - MS.gelu(-t), t, atol=1e-12) and MS.gelu(0.0) == 0.0
+    p = MS.init_params(vocab=11, d_model=32, n_layers=1, seed=7, d_state=16, headdim=16)
+    lp = p["layers"][0]
+    lp["mixer"]["out_proj"] = np.zeros_like(lp["mixer"]["out_proj"])
+    ids = np.random.default_rng(8).integers(0, 11, size=(2, 20))
+    emb = p["embed"][ids].astype(np.float64)
+    for act in MS.ACTIVATIONS:
+        if act == "full_glu":       # out1(0) + bias, gated: not zero by construction
+            continue
+        out = MS.stack_forward(p, ids, activation=act, prenorm=True, d_state=16, headdim=16)
+        assert np.allclose(out, emb, atol=1e-12), act
+        out = MS.stack_forward(p, ids, activation=act, prenorm=False, d_state=16, headdim=16)
+        assert np.allclose(out, MS.layernorm(emb, lp["ln_scale"], lp["ln_bias"]), atol=1e-12), act
+
+
+def test_lm_head_is_normalised_and_shift_invariant():
+    """Each token's log-probabilities sum to one in probability, and a constant added
+    to every decoder bias leaves them unchanged."""
+    from oracle import mamba3_stack as MS
+    p = MS.init_params(vocab=13, d_model=32, n_layers=1, seed=9, d_state=16, headdim=16)
+    ids = np.random.default_rng(10).integers(0, 13, size=(2, 24))
+    lp = MS.lm_forward(p, ids, d_state=16, headdim=16)
+    assert lp.shape == (2, 24, 13)
+    assert np.allclose(np.exp(lp).sum(-1), 1.0, atol=1e-12)
+    q = dict(p, decoder_b=p["decoder_b"] + 3.5)
+    assert np.allclose(MS.lm_forward(q, ids, d_state=16, headdim=16), lp, atol=1e-12)
+    feats = MS.stack_forward(p, ids, d_state=16, headdim=16)
+    z = feats @ p["decoder_w"].astype(np.float64) + p["decoder_b"]
+    assert np.allclose(np.argmax(lp, -1), np.argmax(z, -1))
