@@ -274,7 +274,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "shared", "layer", "stack", "copy"),
                     default="scan")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -6,74 +6,6 @@
 
 namespace m3 {
 
-// 16x16 MFMA tiles: v_mfma_f32_16x16x32_bf16 (KPL = 8) and v_mfma_f32_16x16x4_f32
-// (KPL = 1).  A: lane i holds row i%16, k = (i/16)*KPL + [0,KPL); B: col i%16, same k;
-// C: lane i, reg r holds col i%16, row 4*(i/16) + r (verified lane layouts).
-template <typename T> struct MF16;
-template <> struct MF16<bf16> {
-  static constexpr int KSTEP = 32;
-  typedef bf16x8 frag;
-  // Q and K rows are stored with the columns of each 32-block permuted so that the
-  // k-slice a lane reads for Q h^T (8 contiguous elements) holds logical columns
-  // 4g + [0,4) and 16 + 4g + [0,4), g = lane/16: exactly the state rows a lane's
-  // two 16x16 h^T accumulator tiles hold.  S = K Q^T contracts over the same
-  // permuted order on both sides, so it is unaffected.
-  __host__ __device__ static constexpr int qpos(int n) {
-    return (n & ~31) + 8 * ((n & 15) >> 2) + ((n & 16) ? 4 : 0) + (n & 3);
-  }
-  // B operand of Q h^T for state rows [32q, 32q + 32): the lane's regs of tiles 2q, 2q+1
-  __device__ __forceinline__ static frag hfrag(const f32x4& a, const f32x4& b) {
-    frag f;
-    f[0] = (bf16)a[0]; f[1] = (bf16)a[1]; f[2] = (bf16)a[2]; f[3] = (bf16)a[3];
-    f[4] = (bf16)b[0]; f[5] = (bf16)b[1]; f[6] = (bf16)b[2]; f[7] = (bf16)b[3];
-    return f;
-  }
-  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static frag ld(const bf16* buf, int ldm, int row0, int k0, int lane) {
-    return *reinterpret_cast<const bf16x8*>(buf + (row0 + (lane & 15)) * ldm + k0 + (lane >> 4) * 8);
-  }
-  // steps over a pair of 16-row S^T tiles (32 values of s): slots 0..3 are the
-  // first tile's regs (s = 4(lane/16) + 0..3), slots 4..7 the second's (s + 16)
-  static constexpr int STEPS = 1;
-  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int) {
-    frag f;
-    f[0] = (bf16)c0[0]; f[1] = (bf16)c0[1]; f[2] = (bf16)c0[2]; f[3] = (bf16)c0[3];
-    f[4] = (bf16)c1[0]; f[5] = (bf16)c1[1]; f[6] = (bf16)c1[2]; f[7] = (bf16)c1[3];
-    return f;
-  }
-  __device__ __forceinline__ static frag vperm(const bf16* vt, int ldv, int p0, int s0, int, int lane) {
-    const bf16* r = vt + (p0 + (lane & 15)) * ldv + s0 + 4 * (lane >> 4);
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(r);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(r + 16);
-    frag f;
-    f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
-    f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
-    return f;
-  }
-};
-template <> struct MF16<float> {
-  static constexpr int KSTEP = 4;
-  typedef float frag;
-  __host__ __device__ static constexpr int qpos(int n) { return n; }
-  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static frag ld(const float* buf, int ldm, int row0, int k0, int lane) {
-    return buf[(row0 + (lane & 15)) * ldm + k0 + (lane >> 4)];
-  }
-  // step j (0..7) over a pair of tiles: j < 4 uses the first tile's reg j
-  // (s = 4(lane/16) + j), j >= 4 the second's reg j-4 (s + 16)
-  static constexpr int STEPS = 8;
-  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int j) {
-    return j < 4 ? c0[j] : c1[j - 4];
-  }
-  __device__ __forceinline__ static frag vperm(const float* vt, int ldv, int p0, int s0, int j, int lane) {
-    return vt[(p0 + (lane & 15)) * ldv + s0 + 4 * (lane >> 4) + (j & 3) + (j >= 4 ? 16 : 0)];
-  }
-};
-
 // Direct-to-LDS loads (global_load_lds): the LDS slot is M0 plus size * lane.  They
 // are issued from inline assembly so that the compiler does not treat every later
 // LDS access as possibly overlapping the in-flight writes (it would wait for all
@@ -139,6 +71,46 @@ template <int S>
 __device__ __forceinline__ const uint4& staged(const uint4* buf, int row, int slot) {
   return buf[row * S + (slot ^ (row & (S - 1)))];
 }
+// Element (row, col) of a tile staged as above (rows of S 16-byte slots, swizzled).
+template <int S, typename T>
+__device__ __forceinline__ const T* staged_elem(const uint4* buf, int row, int col) {
+  constexpr int E = 16 / (int)sizeof(T);
+  return reinterpret_cast<const T*>(&buf[row * S + ((col / E) ^ (row & (S - 1)))]) + col % E;
+}
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// MFMA operand whose 16 rows (A) or columns (B) are columns c0.. of a row-major
+// [k][col] LDS matrix: the transpose of what MF16::ld reads.  bf16: two
+// ds_read_b64_tr_b16, each giving lane l the column c0 + l%16 of a 4 x 16 block
+// (lane 4j+q addresses row j, columns 4q..4q+3).
+__device__ __forceinline__ bf16x8 ld_tr(const bf16* buf, int ld, int k0, int c0, int lane) {
+  const int g = lane >> 4, l = lane & 15;
+  const bf16* p = buf + (k0 + 8 * g + (l >> 2)) * ld + c0 + 4 * (l & 3);
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * ld));
+  bf16x8 f;
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+  f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+  return f;
+}
+__device__ __forceinline__ float ld_tr(const float* buf, int ld, int k0, int c0, int lane) {
+  return buf[(k0 + (lane >> 4)) * ld + c0 + (lane & 15)];
+}
+// ld_tr from a staged (swizzled) [k][col] bf16 tile, with the rows chosen per lane
+// group: lane l gets column c0 + l%16, k-slots 0..3 from rows r_lo + 0..3 and 4..7
+// from rows r_hi + 0..3.
+template <int S>
+__device__ __forceinline__ bf16x8 staged_tr(const uint4* buf, int r_lo, int r_hi, int c0, int lane) {
+  const int l = lane & 15;
+  const int col = c0 + 4 * (l & 3);
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)staged_elem<S, bf16>(buf, r_lo + (l >> 2), col));
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)staged_elem<S, bf16>(buf, r_hi + (l >> 2), col));
+  bf16x8 f;
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+  f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+  return f;
+}
 
 // Store 4 consecutive elements (8 bytes bf16, 16 bytes f32).
 __device__ __forceinline__ void store4(bf16* p, const float* f) {
@@ -169,5 +141,113 @@ __device__ __forceinline__ void store_pair(float* p0, float* p1, float a, float 
   *p0 = a;
   *p1 = b;
 }
+
+// 16x16 MFMA tiles: v_mfma_f32_16x16x32_bf16 (KPL = 8) and v_mfma_f32_16x16x4_f32
+// (KPL = 1).  A: lane i holds row i%16, k = (i/16)*KPL + [0,KPL); B: col i%16, same k;
+// C: lane i, reg r holds col i%16, row 4*(i/16) + r (verified lane layouts).
+template <typename T> struct MF16;
+// Operand access for the chunk kernel's MFMAs.  Q and K rows are stored in natural
+// column order; V stays in its staged (swizzled) [token][p] rows and is read with
+// transposed LDS reads, as is K for the state update, so no transposed copy is built.
+template <> struct MF16<bf16> {
+  static constexpr int KSTEP = 32;
+  typedef bf16x8 frag;
+  // B operand of Q h^T for state rows [32q, 32q + 32): the lane's regs of tiles 2q, 2q+1
+  // (rows 32q + 4g + r and 32q + 16 + 4g + r, g = lane/16)
+  __device__ __forceinline__ static frag hfrag(const f32x4& a, const f32x4& b) {
+    frag f;
+    f[0] = (bf16)a[0]; f[1] = (bf16)a[1]; f[2] = (bf16)a[2]; f[3] = (bf16)a[3];
+    f[4] = (bf16)b[0]; f[5] = (bf16)b[1]; f[6] = (bf16)b[2]; f[7] = (bf16)b[3];
+    return f;
+  }
+  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag ld(const bf16* buf, int ldm, int row0, int k0, int lane) {
+    return *reinterpret_cast<const bf16x8*>(buf + (row0 + (lane & 15)) * ldm + k0 + (lane >> 4) * 8);
+  }
+  // A operand of Q h^T: row row0 + lane%16, the columns matching hfrag's state rows
+  __device__ __forceinline__ static frag qoff(const bf16* buf, int ldm, int row0, int k0, int lane) {
+    const bf16* r = buf + (row0 + (lane & 15)) * ldm + k0 + 4 * (lane >> 4);
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(r);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(r + 16);
+    frag f;
+    f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+    f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+    return f;
+  }
+  // steps over a pair of 16-row S^T tiles (32 values of s): slots 0..3 are the
+  // first tile's regs (s = 4(lane/16) + 0..3), slots 4..7 the second's (s + 16)
+  static constexpr int STEPS = 1;
+  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int) {
+    frag f;
+    f[0] = (bf16)c0[0]; f[1] = (bf16)c0[1]; f[2] = (bf16)c0[2]; f[3] = (bf16)c0[3];
+    f[4] = (bf16)c1[0]; f[5] = (bf16)c1[1]; f[6] = (bf16)c1[2]; f[7] = (bf16)c1[3];
+    return f;
+  }
+  // B operand of M V (k = token, matching from_acc's slots), column p0 + lane%16
+  template <int S>
+  __device__ __forceinline__ static frag vdiag(const uint4* rv, int p0, int s0, int, int lane) {
+    const int g4 = 4 * (lane >> 4);
+    return staged_tr<S>(rv, s0 + g4, s0 + 16 + g4, p0, lane);
+  }
+  // B operand of K^T V (k = token t0 + 8(lane/16) + 0..7), column p0 + lane%16
+  template <int S>
+  __device__ __forceinline__ static frag vstate(const uint4* rv, int p0, int t0, int lane) {
+    const int t = t0 + 8 * (lane >> 4);
+    return staged_tr<S>(rv, t, t + 4, p0, lane);
+  }
+  // A operand of K^T V: rows n0 + lane%16 of K^T from the [token][n] rows
+  __device__ __forceinline__ static frag kstate(const bf16* k, int ldq, int t0, int n0, int lane) {
+    return ld_tr(k, ldq, t0, n0, lane);
+  }
+  // the per-token weights of vstate's k-slots (WN per lane, tokens from ktok), and
+  // the scaling of a fragment by them
+  static constexpr int WN = 8;
+  __device__ __forceinline__ static int ktok(int t0, int lane) { return t0 + 8 * (lane >> 4); }
+  __device__ __forceinline__ static void load_w(const float* w, float out[WN]) {
+    const float4 a = *reinterpret_cast<const float4*>(w);
+    const float4 b = *reinterpret_cast<const float4*>(w + 4);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  }
+  __device__ __forceinline__ static frag scale(frag v, const float w[WN]) {
+    frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = (bf16)((float)v[j] * w[j]);
+    return f;
+  }
+};
+template <> struct MF16<float> {
+  static constexpr int KSTEP = 4;
+  typedef float frag;
+  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag ld(const float* buf, int ldm, int row0, int k0, int lane) {
+    return buf[(row0 + (lane & 15)) * ldm + k0 + (lane >> 4)];
+  }
+  // step j (0..7) over a pair of tiles: j < 4 uses the first tile's reg j
+  // (s = 4(lane/16) + j), j >= 4 the second's reg j-4 (s + 16)
+  static constexpr int STEPS = 8;
+  __device__ __forceinline__ static frag from_acc(const f32x4& c0, const f32x4& c1, int j) {
+    return j < 4 ? c0[j] : c1[j - 4];
+  }
+  template <int S>
+  __device__ __forceinline__ static frag vdiag(const uint4* rv, int p0, int s0, int j, int lane) {
+    return *staged_elem<S, float>(rv, s0 + 4 * (lane >> 4) + (j & 3) + (j >= 4 ? 16 : 0), p0 + (lane & 15));
+  }
+  template <int S>
+  __device__ __forceinline__ static frag vstate(const uint4* rv, int p0, int t0, int lane) {
+    return *staged_elem<S, float>(rv, t0 + (lane >> 4), p0 + (lane & 15));
+  }
+  __device__ __forceinline__ static frag kstate(const float* k, int ldq, int t0, int n0, int lane) {
+    return ld_tr(k, ldq, t0, n0, lane);
+  }
+  static constexpr int WN = 1;
+  __device__ __forceinline__ static int ktok(int t0, int lane) { return t0 + (lane >> 4); }
+  __device__ __forceinline__ static void load_w(const float* w, float out[WN]) { out[0] = w[0]; }
+  __device__ __forceinline__ static frag scale(frag v, const float w[WN]) { return v * w[0]; }
+};
 
 }  // namespace m3

@@ -34,26 +34,6 @@ namespace {
 constexpr int kBwdWaves = 8;
 constexpr int kBwdThreads = 64 * kBwdWaves;
 
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-
-// MFMA operand whose 16 rows (A) or columns (B) are columns c0.. of a row-major
-// [k][col] LDS matrix: the transpose of what MF16::ld reads.  bf16: two
-// ds_read_b64_tr_b16, each giving lane l the column c0 + l%16 of a 4 x 16 block
-// (lane 4j+q addresses row j, columns 4q..4q+3).
-__device__ __forceinline__ bf16x8 ld_tr(const bf16* buf, int ld, int k0, int c0, int lane) {
-  const int g = lane >> 4, l = lane & 15;
-  const bf16* p = buf + (k0 + 8 * g + (l >> 2)) * ld + c0 + 4 * (l & 3);
-  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * ld));
-  bf16x8 f;
-  f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
-  f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
-  return f;
-}
-__device__ __forceinline__ float ld_tr(const float* buf, int ld, int k0, int c0, int lane) {
-  return buf[(k0 + (lane >> 4)) * ld + c0 + (lane & 15)];
-}
-
 // Angle increment of a token in revolutions, tanh(rate) pi dt / 2pi, with the same
 // arithmetic as the forward kernel (so the saved chunk angles continue exactly).
 __device__ __forceinline__ float angle_step(float rate, float dt) {

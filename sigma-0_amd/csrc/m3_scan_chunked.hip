@@ -9,21 +9,27 @@
 //   phase 3  S^T = K_s Q_r^T on MFMA, causal decay mask in registers, then
 //            Y_diag = M V on MFMA straight from the S^T accumulators (:371-393)
 //   phase 4-6 Y_off = e^{A_cum} (Q_r h^T) on MFMA with h taken straight from
-//            the fp32 state accumulators; h <- e^{A_end} h + (w K_s)^T V (:177-233)
-//   phase 7  (Y_diag + Y_off + (D + QK) V) * silu(Z), fused into the matrix
-//            phase                                               (:402-419)
+//            the fp32 state accumulators (the row scale applied by the gate);
+//            h <- e^{A_end} h + K_s^T (w V) (:177-233)
+//   phase 7  (Y_diag + Y_off + (D + QK) V) * silu(Z), fused into the
+//            preparation phase of the next chunk                 (:402-419)
 //
-// One workgroup (8 waves) per (batch, head) walks the chunks in order; the
-// P x N fp32 state never leaves the registers.  Each wave owns 16 columns of
-// the value dimension (a p-tile) and a share of the chunk's query rows: it
-// keeps h^T[:, p-tile] (all N rows) as 16x16 accumulators, computes Y for its
-// (rows, p-tile) and applies the output gate and store itself.  Two waves share
-// each p-tile (so its state update runs twice, which is cheaper than a
-// barrier), and query blocks are paired {0,3}, {1,2} so both do equal work.
-// While a chunk's matrix work runs, the next chunk's inputs stream into LDS with
-// direct-to-LDS loads (whole rows per instruction, stored XOR-swizzled), so
-// every input byte is read from HBM once and the output written once.  Two
-// barriers per chunk: after the preparation phase and after the matrix phase.
+// One workgroup of 12 waves per (batch, head) walks the chunks in order; the P x N
+// fp32 state never leaves the registers.  Output waves 0-3 each own a 16-row query
+// block of Y_diag (all p-tiles).  State waves 4-7 each own 16 columns of the value
+// dimension (a p-tile): h^T[:, p-tile] (all N rows) as 16x16 accumulators, Y_off of
+// that p-tile and its state update.  Auxiliary waves 8-11 take the larger share of
+// the preparation (the rope'd columns) and compute the next chunk's rotation angles
+// while the others run the matrix work.  A chunk is two phases with a barrier after
+// each:
+//   preparation  lane = token: biases, rope and key scale into the Q/K tiles; the gate
+//                and store of the previous chunk's Y; the direct-to-LDS loads of the
+//                next chunk's Q and K
+//   matrix       the loads of the next chunk's V and of the rates and scalars of the
+//                chunk after, then the MFMA work, with V read straight from its
+//                staged rows and K^T from the K tile by transposed LDS reads
+// The staged inputs are double-buffered by chunk parity, so every load has a whole
+// chunk to land; every input byte is read from HBM once and the output written once.
 #include <type_traits>
 
 #include "m3_chunk_common.h"
@@ -37,7 +43,7 @@ struct Geo {
   static constexpr int CS = CS_, N = N_, P = P_, R = R_, NW = NW_, NT = 64 * NW_;
   static constexpr int NWY = 4;                             // output waves 0..3
   static constexpr int NST = 4;                             // state waves 4..7
-  static constexpr int NAUX = NW - NWY - NST;               // auxiliary waves (rope angles, staging)
+  static constexpr int NAUX = NW - NWY - NST;               // auxiliary waves 8..11
   static constexpr int KSTEP = MF16<T>::KSTEP;
   static constexpr int LB16 = CS / 16, PT = P / 16;         // 16-row query blocks, 16-col p-tiles
   static constexpr int NB16 = N / 16;                       // 16-row state tiles per p-tile
@@ -45,29 +51,25 @@ struct Geo {
   static constexpr int TS = BF ? 2 : 4;
   static constexpr int PAD = BF ? 8 : 4;
   static constexpr int LDQ = N + PAD;                       // sQ, sK rows (elements)
-  static constexpr int LDV = CS + PAD;                      // sVt, sKwT rows
   static constexpr int LDY = P + (BF ? 8 : 2);              // sY rows (io precision)
   static constexpr int QG = N / 8, QGW = 2;                // Q/K 8-column groups, at most 2 per wave
-  static constexpr int VG = P / 8, VGW = 1;                // V 8-column groups, one per wave
   // 16-byte staging slots per row: Q/K, V, rotation rates
   static constexpr int SQ = N * TS / 16, SV = P * TS / 16, SA = R / 4 > 0 ? R / 4 : 1;
-  static constexpr int BASE = (2 * CS * LDQ + N * LDV + P * LDV) * TS + (2 * CS * SQ + CS * SV + 2 * CS * SA) * 16 +
-                              2 * 3 * (CS + 4) * 4 + 8 * N + 2 * 6 * CS * 4 + 64;
-  // the gate of chunk c-1 overlaps chunk c's matrix phase when two pairs of Y tiles fit
-  static constexpr bool OVL = BASE + 4 * CS * LDY * TS <= 160 * 1024 - 256;
-  static constexpr int NY = OVL ? 2 : 1;
+  // LDS bytes besides the Q/K staging.  The Q/K staging is double-buffered where it
+  // fits; otherwise (rotation width N/2 at d_state 128) it is single-buffered and its
+  // loads wait until the preparation phase has consumed it.
+  static constexpr int FIXED = 2 * CS * LDQ * TS + 2 * CS * LDY * TS + (2 * CS * SV + 2 * CS * SA) * 16 +
+                               2 * 3 * (CS + 4) * 4 + 8 * N + 2 * 6 * CS * 4 + 64;
+  static constexpr bool DBQK = FIXED + 4 * CS * SQ * 16 <= 160 * 1024 - 512;
+  static constexpr int NQK = DBQK ? 2 : 1;
   static_assert(CS <= 64 && LB16 <= NWY, "one token per lane, one query block per output wave");
   static_assert(SPT >= 1 && NST % PT == 0 && LB16 % SPT == 0, "state-wave split");
-  static_assert(NAUX == 0 || NAUX == 4, "8 or 12 waves");
-  static_assert(QG <= 2 * NW && VG <= (NAUX ? NWY + NST : NW), "column groups per wave");
-  // Q/K 8-column group k (< QGW) of a wave, or QG for none.  With auxiliary waves they
-  // take the first groups (the rope columns), two each, so the rope angle work stays
-  // off the matrix waves; the remaining groups go one per matrix wave.
+  static_assert(NAUX == 4, "12 waves");
+  static_assert(QG <= 2 * NAUX + NWY + NST, "column groups per wave");
+  // Q/K 8-column group k (< QGW) of a wave, or QG for none: the auxiliary waves take the
+  // first groups (the rope columns), two each, so the rope angle work stays off the
+  // matrix waves; the remaining groups go one per matrix wave.
   __device__ static int qgroup(int wave, int k) {
-    if (NAUX == 0) {
-      const int g = wave + NW * k;
-      return g < QG ? g : QG;
-    }
     if (wave >= NWY + NST) {
       const int g = 2 * (wave - NWY - NST) + k;
       return g < QG ? g : QG;
@@ -75,8 +77,6 @@ struct Geo {
     const int g = 2 * NAUX + wave + (NWY + NST) * k;
     return g < QG ? g : QG;
   }
-  // V 8-column group of a wave, or VG for none (matrix waves when auxiliary waves exist)
-  __device__ static int vgroup(int wave) { return (NAUX == 0 || wave < NWY + NST) && wave < VG ? wave : VG; }
   static_assert(R % 4 == 0 && 2 * R <= N, "rotation width: a multiple of 4, at most N/2");
   static_assert((SQ & (SQ - 1)) == 0 && (SV & (SV - 1)) == 0 && (SA & (SA - 1)) == 0, "swizzle widths");
 };
@@ -84,22 +84,20 @@ struct Geo {
 template <typename G>
 struct __attribute__((aligned(16))) Smem {
   typedef typename std::conditional<G::BF, bf16, float>::type T;
-  T q[G::CS * G::LDQ];                   // rope'd Q rows (columns in MF16::qpos order)
-  T k[G::CS * G::LDQ];                   // rope'd, trapezoid-scaled K rows (same order)
-  T kwt[G::N * G::LDV];                  // (w K)^T: the state update's A operand
-  T vt[G::P * G::LDV];                   // V^T
+  T q[G::CS * G::LDQ];                   // rope'd Q rows
+  T k[G::CS * G::LDQ];                   // rope'd, trapezoid-scaled K rows
   // Y before the gate, in two parts written by plain stores: the intra-chunk part
-  // (output waves, by query block) and e^{A_cum} Q h^T (state waves, by p-tile)
-  alignas(16) T yd[G::NY][G::CS * G::LDY];
-  alignas(16) T yo[G::NY][G::CS * G::LDY];
-  // raw inputs staged by direct-to-LDS loads: 16-byte slots, row t slot s stored at
-  // t * S + (s ^ (t mod S)) so that a lane-per-row read is bank-conflict free
-  alignas(16) uint4 rq[G::CS * G::SQ];
-  alignas(16) uint4 rk[G::CS * G::SQ];
-  alignas(16) uint4 rv[G::CS * G::SV];
-  // rotation rates and adt, dt, trap ([CS]: the next chunk's first token) of chunks
-  // c and c+1, by chunk parity: chunk c+1's angles and weights are computed during
-  // chunk c's matrix phase
+  // (output waves, by query block) and Q h^T (state waves, by p-tile; the gate applies
+  // its e^{A_cum} row scale)
+  alignas(16) T yd[G::CS * G::LDY];
+  alignas(16) T yo[G::CS * G::LDY];
+  // raw inputs staged by direct-to-LDS loads, by chunk parity: 16-byte slots, row t slot
+  // s stored at t * S + (s ^ (t mod S)) so that a lane-per-row read is bank-conflict free
+  alignas(16) uint4 rq[G::NQK][G::CS * G::SQ];
+  alignas(16) uint4 rk[G::NQK][G::CS * G::SQ];
+  alignas(16) uint4 rv[2][G::CS * G::SV];
+  // rotation rates and adt, dt, trap ([CS]: the next chunk's first token), by chunk
+  // parity: chunk c+1's angles and weights are computed during chunk c's matrix phase
   alignas(16) uint4 ra[2][G::CS * G::SA];
   alignas(16) float rs[2][3][G::CS + 4];
   alignas(16) float qb[G::N];            // biases of this head
@@ -107,7 +105,7 @@ struct __attribute__((aligned(16))) Smem {
   // per-token chunk constants, by chunk parity
   alignas(16) float ac2[2][G::CS];       // A_cum * log2(e)
   alignas(16) float g16[2][G::CS];       // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
-  alignas(16) float expa[2][G::CS];      // e^{A_cum}
+  alignas(16) float expa[2][G::CS];      // e^{A_cum} (read by the gate, a chunk later)
   alignas(16) float dg[2][G::CS];        // gamma / scale: turns the S diagonal into the QK skip weight
   alignas(16) float scl[2][G::CS];       // trapezoid key scale gamma_t + dt_{t+1} (1 - sigmoid_{t+1})
   alignas(16) float wdec[2][G::CS];      // e^{A_end - A_cum}
@@ -163,23 +161,33 @@ void scan_chunked_kernel(ScanArgs a) {
     sm.kb[i] = a.kbias[(long)h * N + i];
   }
 
-  // ---- staging, spread over the waves with the most slack in the matrix phase:
-  // Q, K, V of chunk c; rotation rates and scalars of chunk c into parity c & 1
-  constexpr int kWQ0 = G::NAUX ? 0 : 2, kWQ1 = G::NAUX ? 0 : 4, kWK0 = G::NAUX ? 1 : 6, kWK1 = G::NAUX ? 1 : 7;
-  constexpr int kWV = G::NAUX ? 8 : 0, kWA = G::NAUX ? 9 : 5;
-  auto stage_qkv = [&](int c) {
+  // ---- staging.  Q/K of chunk c into buffer c % NQK, V into parity c & 1, rotation
+  // rates and scalars into parity c & 1.  A wave waits while the CU's load path drains
+  // the loads queued ahead of its own, so they go to waves with slack: Q/K to the
+  // output waves at the end of their preparation share (single-buffered Q/K: the
+  // auxiliary waves, after the preparation barrier); V, rates and scalars to output
+  // waves 0 and 1 (the two lightest query blocks) at the start of the matrix phase.
+  constexpr int kWQ0 = G::DBQK ? 0 : 8, kWQ1 = G::DBQK ? 1 : 9, kWK0 = G::DBQK ? 2 : 10, kWK1 = G::DBQK ? 3 : 11;
+  constexpr int kWV = 0, kWA = 1;
+  auto stage_qk = [&](int c) {
     const int t0 = c * CS;
     const int valid = L - t0;
-    constexpr int JQ = CS * G::SQ / 64, JV = CS * G::SV / 64;
+    constexpr int JQ = CS * G::SQ / 64;
     const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
     const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
-    if (!SO && wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
-    if (!SO && wave == kWQ1) stage_rows<CS, G::SQ, JQ / 2, JQ>((lds_uint4*)sm.rq, q0, qk_stride * G::TS, valid, lane);
-    if (wave == kWK0) stage_rows<CS, G::SQ, 0, JQ / 2>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
-    if (wave == kWK1) stage_rows<CS, G::SQ, JQ / 2, JQ>((lds_uint4*)sm.rk, k0, qk_stride * G::TS, valid, lane);
+    lds_uint4* dq = (lds_uint4*)sm.rq[c % G::NQK];
+    lds_uint4* dk = (lds_uint4*)sm.rk[c % G::NQK];
+    if (!SO && wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>(dq, q0, qk_stride * G::TS, valid, lane);
+    if (!SO && wave == kWQ1) stage_rows<CS, G::SQ, JQ / 2, JQ>(dq, q0, qk_stride * G::TS, valid, lane);
+    if (wave == kWK0) stage_rows<CS, G::SQ, 0, JQ / 2>(dk, k0, qk_stride * G::TS, valid, lane);
+    if (wave == kWK1) stage_rows<CS, G::SQ, JQ / 2, JQ>(dk, k0, qk_stride * G::TS, valid, lane);
+  };
+  auto stage_v = [&](int c) {
+    const int t0 = c * CS;
+    constexpr int JV = CS * G::SV / 64;
     if (wave == kWV) {
       const char* v0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + v_row + (long)t0 * v_stride);
-      stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv, v0, v_stride * G::TS, valid, lane);
+      stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv[c & 1], v0, v_stride * G::TS, L - t0, lane);
     }
   };
   auto stage_ars = [&](int c) {
@@ -212,17 +220,18 @@ void scan_chunked_kernel(ScanArgs a) {
   auto load_z = [&](int c) {
     if (has_z && eact && c * CS + erow < L) zr.load(gZ + v_row + (long)(c * CS + erow) * v_stride + 8 * egrp);
   };
-  auto gate = [&](int c) {                 // Y of chunk c (tiles c % NY) -> out
+  auto gate = [&](int c) {                 // Y of chunk c -> out
     if (eact && c * CS + erow < L) {
       const int off = erow * G::LDY + 8 * egrp;
       Vec8<T> ya, yb;
-      ya.load(&sm.yd[c % G::NY][off]);
-      yb.load(&sm.yo[c % G::NY][off]);
+      ya.load(&sm.yd[off]);
+      yb.load(&sm.yo[off]);
+      const float ea = sm.expa[c & 1][erow];   // the e^{A_cum} row scale of Q h^T
       float o[8], ob[8];
       ya.to_f(o);
       yb.to_f(ob);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] += ob[q];
+      for (int q = 0; q < 8; ++q) o[q] = fmaf(ob[q], ea, o[q]);
       if (has_z) {
         float zf[8];
         zr.to_f(zf);
@@ -266,15 +275,19 @@ void scan_chunked_kernel(ScanArgs a) {
       carry[k][j] = (a.init_theta && has_init && r < R) ? a.init_theta[(long)ci_in * R + r] * kInvTwoPi : 0.0f;  // revolutions
     }
   // staging never holds uninitialised bits: rows past the sequence end are not loaded
-  for (int i = tid; i < G::CS * G::SQ; i += G::NT) { sm.rq[i] = make_uint4(0, 0, 0, 0); sm.rk[i] = sm.rq[i]; }
-  for (int i = tid; i < G::CS * G::SV; i += G::NT) sm.rv[i] = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < G::NQK * G::CS * G::SQ; i += G::NT) {
+    (&sm.rq[0][0])[i] = make_uint4(0, 0, 0, 0);
+    (&sm.rk[0][0])[i] = make_uint4(0, 0, 0, 0);
+  }
+  for (int i = tid; i < 2 * G::CS * G::SV; i += G::NT) (&sm.rv[0][0])[i] = make_uint4(0, 0, 0, 0);
   for (int i = tid; i < 2 * G::CS * G::SA; i += G::NT) (&sm.ra[0][0])[i] = make_uint4(0, 0, 0, 0);
   for (int i = tid; i < 2 * 3 * (G::CS + 4); i += G::NT) (&sm.rs[0][0][0])[i] = 0.0f;
 
   // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
   // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
   // the angles of its own rope pairs in registers.
-  constexpr int kScalarWave = G::NAUX ? NW - 1 : 0;
+  // (wave 8 shares a SIMD with the lightest output wave)
+  constexpr int kScalarWave = G::NWY + G::NST;
   float p_cs[G::QGW][4], p_sn[G::QGW][4];
   float logdec = 0.0f;                     // state-only pass: sum of the chunks' log-decays
   auto pre = [&](int cc) {
@@ -334,7 +347,8 @@ void scan_chunked_kernel(ScanArgs a) {
   };
 
   __syncthreads();
-  stage_qkv(0);
+  stage_qk(0);
+  stage_v(0);
   stage_ars(0);
   if (nc > 1) stage_ars(1);
   __builtin_amdgcn_s_waitcnt(0);
@@ -346,11 +360,15 @@ void scan_chunked_kernel(ScanArgs a) {
     const int t0 = c * CS;
     const bool tok = lane < CS && t0 + lane < L;
     const int tl = lane < CS ? lane : 0;        // staging row of this lane
+    const int pc = c & 1;
+    const uint4* sq = sm.rq[c % G::NQK];
+    const uint4* sk = sm.rk[c % G::NQK];
+    const uint4* sv = sm.rv[pc];
 
     // ================= preparation: lane = token =================
     // Rows past the sequence end hold stale (finite) inputs: their key scale is 0,
     // so they add nothing to S or h, and their outputs are never stored.
-    const float scl = sm.scl[c & 1][tl], wdec = sm.wdec[c & 1][tl];
+    const float scl = sm.scl[pc][tl];
     // Q/K column groups: rotation angles, biases, rope, key scale
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
@@ -360,11 +378,11 @@ void scan_chunked_kernel(ScanArgs a) {
         {
           Vec8<T> qv, kv;
           if constexpr (G::BF) {
-            qv.raw_set(staged<G::SQ>(sm.rq, tl, g));
-            kv.raw_set(staged<G::SQ>(sm.rk, tl, g));
+            qv.raw_set(staged<G::SQ>(sq, tl, g));
+            kv.raw_set(staged<G::SQ>(sk, tl, g));
           } else {
-            qv.raw_set2(staged<G::SQ>(sm.rq, tl, 2 * g), staged<G::SQ>(sm.rq, tl, 2 * g + 1));
-            kv.raw_set2(staged<G::SQ>(sm.rk, tl, 2 * g), staged<G::SQ>(sm.rk, tl, 2 * g + 1));
+            qv.raw_set2(staged<G::SQ>(sq, tl, 2 * g), staged<G::SQ>(sq, tl, 2 * g + 1));
+            kv.raw_set2(staged<G::SQ>(sk, tl, 2 * g), staged<G::SQ>(sk, tl, 2 * g + 1));
           }
           qv.to_f(qf);
           kv.to_f(kf);
@@ -400,71 +418,27 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) kf[e] *= scl;
         if (lane < CS) {
-          if constexpr (!SO) {
-            store4(&sm.q[lane * G::LDQ + W::qpos(8 * g)], qf);
-            store4(&sm.q[lane * G::LDQ + W::qpos(8 * g + 4)], qf + 4);
-          }
-          store4(&sm.k[lane * G::LDQ + W::qpos(8 * g)], kf);
-          store4(&sm.k[lane * G::LDQ + W::qpos(8 * g + 4)], kf + 4);
-#pragma unroll
-          for (int e = 0; e < 8; e += 2)
-            store_pair(&sm.kwt[(8 * g + e) * G::LDV + lane], &sm.kwt[(8 * g + e + 1) * G::LDV + lane], kf[e] * wdec,
-                       kf[e + 1] * wdec);
+          if constexpr (!SO) store8(&sm.q[lane * G::LDQ + 8 * g], qf);
+          store8(&sm.k[lane * G::LDQ + 8 * g], kf);
         }
       }
     }
-    // V column groups: V^T
-    {
-      const int g = G::vgroup(wave);
-      if (g < G::VG) {
-        Vec8<T> vv;
-        if constexpr (G::BF) vv.raw_set(staged<G::SV>(sm.rv, tl, g));
-        else vv.raw_set2(staged<G::SV>(sm.rv, tl, 2 * g), staged<G::SV>(sm.rv, tl, 2 * g + 1));
-        if (lane < CS) {
-          if constexpr (G::BF) {
-            // V^T straight from the stored 16-bit values: low and high halves of each word
-            const uint32_t w4[4] = {vv.raw.x, vv.raw.y, vv.raw.z, vv.raw.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              reinterpret_cast<uint16_t*>(sm.vt)[(8 * g + 2 * q) * G::LDV + lane] = (uint16_t)(w4[q] & 0xffffu);
-              reinterpret_cast<uint16_t*>(sm.vt)[(8 * g + 2 * q + 1) * G::LDV + lane] = (uint16_t)(w4[q] >> 16);
-            }
-          } else {
-            float vf[8];
-            vv.to_f(vf);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) sm.vt[(8 * g + q) * G::LDV + lane] = vf[q];
-          }
-        }
-        if (a.fin_v && fin_here && tok && t0 + lane == L - 1) {
-          float vf[8];
-          vv.to_f(vf);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) a.fin_v[(long)ci_out * P + 8 * g + q] = vf[q];
-        }
-      }
-    }
-    if (!SO && !G::OVL) load_z(c);
-    // ---- gate of the previous chunk: with auxiliary waves, the matrix waves run it
-    // while the auxiliary waves finish their larger preparation share
-    if (!SO && G::OVL && G::NAUX > 0 && c > 0) gate(c - 1);
+    // final carry's V: the segment's last token, straight from the staged row
+    if (a.fin_v && fin_here && c == nc - 1 && wave == 6 && lane < P)
+      a.fin_v[(long)ci_out * P + lane] = Elem<T>::to_f(*staged_elem<G::SV, T>(sv, L - 1 - t0, lane));
+    // gate of the previous chunk (its Y tiles were written before the last barrier),
+    // then Z for this chunk's gate, then the loads of the next chunks: the gate's wait
+    // for Z comes before any of them is in flight
+    if (!SO && c > 0) gate(c - 1);
+    if (!SO) load_z(c);
+    if (G::DBQK && c + 1 < nc) stage_qk(c + 1);
     __syncthreads();
 
-    // Z of the chunk waiting for its gate has landed (it was loaded a chunk ago); this
-    // wait keeps the compiler from waiting on the direct-to-LDS loads issued next
-    if (G::OVL) __builtin_amdgcn_s_waitcnt(0);
-    // ---- inputs of the next chunks go in flight (this chunk's Q/K/V staging is consumed)
-    if (c + 1 < nc) stage_qkv(c + 1);
+    // single-buffered Q/K staging: every wave has read this chunk's rows
+    if (!G::DBQK && c + 1 < nc) stage_qk(c + 1);
+    if (c + 1 < nc) stage_v(c + 1);
     if (c + 2 < nc) stage_ars(c + 2);
-    // ---- without auxiliary waves: gate of the previous chunk, under this chunk's matrix work
-    if (!SO && G::OVL && G::NAUX == 0 && c > 0) gate(c - 1);
-    // ---- next chunk's constants and rotations: state waves before their matrix work,
-    // output waves after it, so each SIMD pairs VALU work with matrix work
-    if (G::NAUX == 0 && swave && c + 1 < nc) pre(c + 1);
 
-    const int pc = c & 1;
-    T* ydst = sm.yd[c % G::NY];
-    T* yodst = sm.yo[c % G::NY];
     // ---- phase 3 for query rows l in [16 lb, 16 lb + 16), all p-tiles (output wave lb):
     //   Y_diag = mask(K_s Q_r^T)^T V, the mask's diagonal carrying D + gamma QK.
     // Instantiated per query block so every loop over key blocks is static.
@@ -525,15 +499,15 @@ void scan_chunked_kernel(ScanArgs a) {
           const typename W::frag mf = W::from_acc(st[sp], st[sp + 1], j);
 #pragma unroll
           for (int pt = 0; pt < G::PT; ++pt)
-            yd[pt] = W::mma(mf, W::vperm(sm.vt, G::LDV, 16 * pt, 16 * sp, j, ln), yd[pt]);
+            yd[pt] = W::mma(mf, W::template vdiag<G::SV>(sv, 16 * pt, 16 * sp, j, ln), yd[pt]);
         }
       }
 #pragma unroll
       for (int pt = 0; pt < G::PT; ++pt)
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
-          store_pair(&ydst[(16 * lb + g4l + r) * G::LDY + 16 * pt + (ln & 15)],
-                     &ydst[(16 * lb + g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
+          store_pair(&sm.yd[(16 * lb + g4l + r) * G::LDY + 16 * pt + (ln & 15)],
+                     &sm.yd[(16 * lb + g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
     };
     if (!SO && ywave) {                 // the state-only pass has no Y_diag
       if (wave == 0) out_block(std::integral_constant<int, 0>{});
@@ -543,7 +517,15 @@ void scan_chunked_kernel(ScanArgs a) {
         if (wave == 3) out_block(std::integral_constant<int, 3>{});
       }
     } else if (swave) {
-      // ---- phase 6: Y_off = e^{A_cum} Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
+      // the state update's decay and per-token weights are read before this wave's
+      // stores (a read issued after them would wait for them too)
+      const float dec = sm.dec[pc];
+      float wv[CS / W::KSTEP][W::WN];
+      auto load_wv = [&]() {
+#pragma unroll
+        for (int ks = 0; ks < CS / W::KSTEP; ++ks) W::load_w(&sm.wdec[pc][W::ktok(ks * W::KSTEP, lane)], wv[ks]);
+      };
+      // ---- phase 6: Y_off = Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
       if constexpr (!SO) {
       typename W::frag hf[G::BF ? N / 32 : 1];
       if constexpr (G::BF) {
@@ -562,7 +544,7 @@ void scan_chunked_kernel(ScanArgs a) {
         for (int q = 0; q < N / 32; ++q) {
           typename W::frag qa[NLB];
 #pragma unroll
-          for (int i = 0; i < NLB; ++i) qa[i] = W::ld(sm.q, G::LDQ, 16 * (part + G::SPT * i), 32 * q, lane);
+          for (int i = 0; i < NLB; ++i) qa[i] = W::qoff(sm.q, G::LDQ, 16 * (part + G::SPT * i), 32 * q, lane);
 #pragma unroll
           for (int i = 0; i < NLB; ++i) yo[i] = W::mma(qa[i], hf[q], yo[i]);
         }
@@ -577,18 +559,19 @@ void scan_chunked_kernel(ScanArgs a) {
               yo[i] = W::mma(sm.q[l * G::LDQ + 16 * nb + g4 + r], hs[nb][r], yo[i]);
             }
       }
+      load_wv();
 #pragma unroll
       for (int i = 0; i < NLB; ++i) {
         const int lb = part + G::SPT * i;
-        const float4 ea = *reinterpret_cast<const float4*>(&sm.expa[pc][16 * lb + g4]);
-        const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
-          store_pair(&yodst[(16 * lb + g4 + r) * G::LDY + pcol], &yodst[(16 * lb + g4 + r + 1) * G::LDY + pcol],
-                     eav[r] * yo[i][r], eav[r + 1] * yo[i][r + 1]);
+          store_pair(&sm.yo[(16 * lb + g4 + r) * G::LDY + pcol], &sm.yo[(16 * lb + g4 + r + 1) * G::LDY + pcol],
+                     yo[i][r], yo[i][r + 1]);
       }
-      }  // !SO
-      // ---- phases 4-5: h <- e^{A_end} h + (w K_s)^T V for my p-tile
+      } else {
+        load_wv();
+      }
+      // ---- phases 4-5: h <- e^{A_end} h + K_s^T (w V) for my p-tile
       if constexpr (SO) {                // backward: the state entering chunk c, [p][n]
         if (a.chunk_h && part == 0) {
           T* dst = reinterpret_cast<T*>(a.chunk_h) + ((long)(bh * nc + c) * P + pcol) * N + g4;
@@ -599,29 +582,23 @@ void scan_chunked_kernel(ScanArgs a) {
           }
         }
       }
-      const float dec = sm.dec[pc];
 #pragma unroll
       for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) hs[nb][r] *= dec;
 #pragma unroll
       for (int ks = 0; ks < CS / W::KSTEP; ++ks) {
-        const typename W::frag vb = W::ld(sm.vt, G::LDV, 16 * pr, ks * W::KSTEP, lane);
+        const typename W::frag vb = W::scale(W::template vstate<G::SV>(sv, 16 * pr, ks * W::KSTEP, lane), wv[ks]);
 #pragma unroll
         for (int nb = 0; nb < G::NB16; ++nb)
-          hs[nb] = W::mma(W::ld(sm.kwt, G::LDV, 16 * nb, ks * W::KSTEP, lane), vb, hs[nb]);
+          hs[nb] = W::mma(W::kstate(sm.k, G::LDQ, ks * W::KSTEP, 16 * nb, lane), vb, hs[nb]);
       }
     }
-    if ((G::NAUX > 0 || !swave) && c + 1 < nc) pre(c + 1);
-    __builtin_amdgcn_s_waitcnt(0);   // staged loads and gate stores of this wave are done
-    if (!SO && G::OVL) load_z(c);    // Z for this chunk's gate, one chunk ahead
+    if (c + 1 < nc) pre(c + 1);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's staged loads and gate stores are done
     __syncthreads();
-    if (!SO && !G::OVL) {
-      gate(c);
-      // the next chunk writes the single pair of Y tiles after its preparation barrier
-    }
   }
-  if (!SO && G::OVL && nc > 0) gate(nc - 1);
+  if (!SO && nc > 0) gate(nc - 1);
 
   if (a.fin_h && fin_here && swave && part == 0) {
 #pragma unroll
