@@ -137,6 +137,24 @@ __device__ __forceinline__ float wave_incl_scan(float v) {
   return v;
 }
 
+// Four independent inclusive scans (the same operations as wave_incl_scan on each
+// value), advanced step by step so that each value's DPP step fills the others' wait
+// states instead of four chains running one after another.
+__device__ __forceinline__ void wave_incl_scan4(float v[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp0<kDppRowShr1>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp0<kDppRowShr2>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp0<kDppRowShr4>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp0<kDppRowShr8>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp0<kDppRowBcast15, 0xa>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp0<kDppRowBcast31, 0xc>(v[j]);
+}
+
 // Sum over aligned groups of G consecutive lanes (G a power of two <= 64);
 // every lane of the group receives the group sum.  Groups up to 16 lanes stay
 // inside a DPP row; wider groups use cross-row shuffles.

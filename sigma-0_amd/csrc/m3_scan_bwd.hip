@@ -24,6 +24,8 @@
 //      cumsums over the sequence, the trapezoid and angle chains), and
 //      scan_bwd_reduce_kernel sums the bias and D gradients over batch and chunks.
 // Every sum runs in a fixed order, so the gradients are deterministic.
+#include <algorithm>
+#include <cstddef>
 #include <type_traits>
 
 #include "m3_chunk_common.h"
@@ -133,21 +135,30 @@ __device__ __forceinline__ void chunk_scalars(const BwdArgs& a, int bh, int t0, 
 }
 
 // Rope angles (revolutions) of this lane's token for the pairs 4g..4g+3 of column
-// group g: the angle entering the chunk plus a wave scan of the increments.  Call
-// with the whole wave (g uniform).
+// group g: the angle entering the chunk plus a wave scan of the increments.  The
+// rates are requested first (group_rates) and used later, so that their load latency
+// overlaps the other loads of the kernel.  Call with the whole wave (g uniform).
+// Lanes past the sequence end read the last token's row (a valid address), so the
+// load is unconditional and nothing waits on it until its use; their dt is 0, which
+// makes their angle increments 0.
 template <int CS, int R>
-__device__ __forceinline__ void group_theta(const BwdArgs& a, int b, int h, int bh, int c, int t0, int g, int lane,
+__device__ __forceinline__ float4 group_rates(const BwdArgs& a, int b, int h, int t0, int g, int lane) {
+  float4 rt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if constexpr (R > 0) {
+    const int L = a.s.L, H = a.s.H;
+    const int t = min(t0 + lane, L - 1);
+    const long arow = a.s.ang_shared ? (long)b * L + t : ((long)b * L + t) * H + h;
+    if (4 * g < R) rt = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * g);
+  }
+  return rt;
+}
+template <int CS, int R>
+__device__ __forceinline__ void group_theta(const BwdArgs& a, int bh, int c, int g, float4 rt, float dt,
                                             float th4[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) th4[j] = 0.0f;
   if constexpr (R > 0) {
     if (4 * g >= R) return;
-    const int L = a.s.L, H = a.s.H;
-    const bool tok = lane < CS && t0 + lane < L;
-    const float dt = tok ? a.s.dt[(long)bh * L + t0 + lane] : 0.0f;
-    float4 rt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const long arow = a.s.ang_shared ? (long)b * L + t0 + lane : ((long)b * L + t0 + lane) * H + h;
-    if (tok) rt = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * g);
     const float rv[4] = {rt.x, rt.y, rt.z, rt.w};
     const float* t0c = a.th0 + ((long)bh * a.nc + c) * R + 4 * g;
 #pragma unroll
@@ -204,9 +215,10 @@ void scan_adjoint_kernel(BwdArgs a) {
     if (wave == 0) chunk_scalars<CS>(a, bh, t0, lane, sm.ac, sm.gam, sm.scl, sm.dtv, &sm.aend);
     __syncthreads();
     const bool tok = lane < CS && t0 + lane < L;
+    const float dtl = tok ? a.s.dt[(long)bh * L + t0 + lane] : 0.0f;
     for (int g = wave; g < N / 8; g += kBwdWaves) {
       float q[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th4[4];
-      group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
+      group_theta<CS, R>(a, bh, c, g, group_rates<CS, R>(a, b, h, t0, g, lane), dtl, th4);
       if (tok) {
         load8(gq + (((long)b * L + t0 + lane) * HQ + hq) * N + 8 * g, q);
 #pragma unroll
@@ -275,54 +287,168 @@ struct GradSmem {
   float ps[N / 8][CS];                 // per column group: dk~ . rot(k^)
   float pv[P / 8][CS];                 // per value group: dy.v
   float aend;
+  alignas(16) float sink[64];          // destination of the L2 prefetch loads (never read)
 };
 
+// The global inputs of one (chunk, b, h) item of the chunk-gradient kernel, loaded into
+// registers: the two saved states, this thread's Q/K rows (two column groups) and
+// V/dOut/Z rows (one value group), the rates of its rope pairs and dt.  Every load is
+// unconditional, from a clamped valid address where a lane or wave has nothing to load
+// (past the sequence end, beyond the column groups), so the compiler never waits on one
+// before its use; the unused values are zeroed or ignored there.
+template <typename T, int CS, int N, int P, int R>
+struct ItemLoads {
+  static constexpr int GH = N / 16;                                       // column groups per half
+  static constexpr int HP = (P * N / 8 + kBwdThreads - 1) / kBwdThreads;  // 8-element state pieces per thread
+  static constexpr int VGW = (P / 8 + kBwdWaves - 1) / kBwdWaves;         // value groups per wave
+  Vec8<T> hpc[HP], gpc[HP], qraw[2], kraw[2], vraw[VGW], dyraw[VGW], zraw[VGW];
+  float4 rates[2];
+  float dtraw;
+  __device__ __forceinline__ void issue(const BwdArgs& a, int c, int bh, int tid, int wave, int lane) {
+    const int b = bh / a.s.H, h = bh % a.s.H, hq = h / (a.s.H / a.s.Hqk);
+    const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc, t0 = c * CS;
+    const int tcl = min(t0 + lane, L - 1);
+    const long qrow = (((long)b * L + tcl) * HQ + hq) * N;
+    const long vrow = (((long)b * L + tcl) * H + h) * P;
+    const T* hsrc = reinterpret_cast<const T*>(a.hs) + ((long)bh * nc + c) * P * N;
+    const T* gsrc = reinterpret_cast<const T*>(a.gs) + ((long)bh * nc + c) * N * P;
+#pragma unroll
+    for (int k = 0; k < HP; ++k) {
+      const int i = min(tid + k * kBwdThreads, P * N / 8 - 1);
+      hpc[k].load(hsrc + 8 * i);
+      gpc[k].load(gsrc + 8 * i);
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int g = min(hh * GH + wave, N / 8 - 1);
+      qraw[hh].load(reinterpret_cast<const T*>(a.s.q) + qrow + 8 * g);
+      kraw[hh].load(reinterpret_cast<const T*>(a.s.k) + qrow + 8 * g);
+      rates[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (R > 0) {
+        const long arow = a.s.ang_shared ? (long)b * L + tcl : ((long)b * L + tcl) * H + h;
+        rates[hh] = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * min(g, R / 4 - 1));
+      }
+    }
+    dtraw = a.s.dt[(long)bh * L + tcl];
+    const T* gv = reinterpret_cast<const T*>(a.s.v);
+    const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) : gv;
+#pragma unroll
+    for (int k = 0; k < VGW; ++k) {
+      const int g = min(wave + k * kBwdWaves, P / 8 - 1);
+      vraw[k].load(gv + vrow + 8 * g);
+      dyraw[k].load(reinterpret_cast<const T*>(a.dout) + vrow + 8 * g);
+      zraw[k].load(gz + vrow + 8 * g);
+    }
+  }
+};
+
+// Requests every input line of an item into L2: one direct-to-LDS dword load per
+// 128-byte line (lane = line, or lane = token for the row tensors), all written to a
+// 256-byte LDS sink that nothing reads.  The saved states, Q, K, V, dOut, Z, the
+// rates, and adt, dt, trap of the item's tokens.  Lanes past the sequence end request
+// the last token's rows.
+template <typename T, int CS, int N, int P, int R>
+__device__ __forceinline__ void prefetch_item(const BwdArgs& a, int c, int bh, int wave, int lane,
+                                              uint32_t sink) {
+  constexpr int TS = sizeof(T);
+  constexpr int SL = P * N * TS / 128;                 // lines per saved state
+  constexpr int SJ = (SL + 63) / 64;
+  constexpr int QJ = N * TS / 128 > 0 ? N * TS / 128 : 1;
+  constexpr int VJ = P * TS / 128 > 0 ? P * TS / 128 : 1;
+  constexpr int AJ = R * 4 / 128 > 0 ? R * 4 / 128 : (R > 0 ? 1 : 0);
+  constexpr int NJ = 2 * SJ + 2 * QJ + 3 * VJ + AJ + 3;
+  const int b = bh / a.s.H, h = bh % a.s.H, hq = h / (a.s.H / a.s.Hqk);
+  const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, t0 = c * CS;
+  const uint32_t dt = (uint32_t)(min(t0 + lane, L - 1) - t0);      // this lane's token in the item
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j % kBwdWaves != wave) continue;
+    const char* base;
+    uint32_t off;
+    if (j < 2 * SJ) {
+      base = reinterpret_cast<const char*>(j < SJ ? a.hs : a.gs) + ((long)bh * a.nc + c) * P * N * TS;
+      off = 128u * (uint32_t)min((j % SJ) * 64 + lane, SL - 1);
+    } else if (j < 2 * SJ + 2 * QJ) {
+      const int k = j - 2 * SJ;
+      base = reinterpret_cast<const char*>(k < QJ ? a.s.q : a.s.k) + (((long)b * L + t0) * HQ + hq) * N * TS;
+      off = dt * (uint32_t)(HQ * N * TS) + 128u * (uint32_t)(k % QJ);
+    } else if (j < 2 * SJ + 2 * QJ + 3 * VJ) {
+      const int k = j - 2 * SJ - 2 * QJ, which = k / VJ;
+      const void* src = which == 0 ? a.s.v : which == 1 ? a.dout : (a.s.z ? a.s.z : a.s.v);
+      base = reinterpret_cast<const char*>(src) + (((long)b * L + t0) * H + h) * P * TS;
+      off = dt * (uint32_t)(H * P * TS) + 128u * (uint32_t)(k % VJ);
+    } else if (j < NJ - 3) {
+      const long arow = a.s.ang_shared ? (long)b * L + t0 : ((long)b * L + t0) * H + h;
+      base = reinterpret_cast<const char*>(a.s.ang + arow * R);
+      off = dt * (uint32_t)((a.s.ang_shared ? 1 : H) * R * 4) + 128u * (uint32_t)(j - (NJ - 3 - AJ));
+    } else {
+      const int k = j - (NJ - 3);
+      const float* src = k == 0 ? a.s.adt : k == 1 ? a.s.dt : a.s.trap;
+      base = reinterpret_cast<const char*>(src + (long)bh * L + t0);
+      off = 4u * dt;
+    }
+    // the base is wave-uniform; it is moved to scalar registers explicitly (readfirstlane
+    // returns a signed int: each half is taken as uint32_t before widening, or a low half
+    // with bit 31 set would sign-extend over the high half)
+    const uint64_t bv = reinterpret_cast<uint64_t>(base);
+    const uint32_t bhi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bv >> 32));
+    const uint32_t blo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bv);
+    const uint64_t bs = ((uint64_t)bhi << 32) | (uint64_t)blo;
+    lds_dma4_at(reinterpret_cast<const void*>(bs), off, sink);
+  }
+}
+
+// Persistent: one workgroup per compute unit walks the (chunk, b, h) items.  Once an
+// item's inputs are in LDS and registers, the next item's input lines are requested
+// into L2, so they arrive during this item's matrix work instead of in a burst of
+// every compute unit at every workgroup start.
 template <typename T, int CS, int N, int P, int R>
 __global__ __launch_bounds__(kBwdThreads, 1)
 void scan_bwd_chunk_kernel(BwdArgs a) {
   typedef MF16<T> W;
   typedef GradSmem<T, CS, N, P, R> S;
+  typedef ItemLoads<T, CS, N, P, R> Loads;
   static_assert(sizeof(S) <= 160 * 1024, "LDS budget");
   __shared__ S sm;
   constexpr int PAD = S::PAD, KS = W::KSTEP, NH = S::NH;
   constexpr int TB = CS / 16;                          // 16-token blocks
+  constexpr int GH = NH / 8, HP = Loads::HP, VGW = Loads::VGW;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = blockIdx.x, bh = blockIdx.y, b = bh / a.s.H, h = bh % a.s.H;
-  const int hq = h / (a.s.H / a.s.Hqk);
+  __builtin_assume(wave >= 0 && wave < kBwdWaves);
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
+  const int nitems = nc * a.s.B * H;
+  const bool qkw = wave < GH;
+  // LDS byte address of the prefetch sink: the object's base (its first field) plus the
+  // field offset (an address-space cast of the sink's own address miscompiles here)
+  const uint32_t sink = lds_addr((lds_float*)&sm.qt[0][0]) + (uint32_t)offsetof(S, sink);
+
+  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+  const int c = item % nc, bh = item / nc, b = bh / H, h = bh % H;
+  Loads cur;
+  cur.issue(a, c, bh, tid, wave, lane);
+  const int hq = h / (H / HQ);
   const int t0 = c * CS;
-  const T* gq = reinterpret_cast<const T*>(a.s.q);
-  const T* gk = reinterpret_cast<const T*>(a.s.k);
-  const T* gv = reinterpret_cast<const T*>(a.s.v);
-  const T* gdo = reinterpret_cast<const T*>(a.dout);
   const T* gz = reinterpret_cast<const T*>(a.s.z);
   const float Dh = a.s.D ? a.s.D[h] : 0.0f;
   const bool tok = lane < CS && t0 + lane < L;
-  const long qrow = (((long)b * L + t0 + lane) * HQ + hq) * N;   // this lane's token
-  const long vrow = (((long)b * L + t0 + lane) * H + h) * P;
+  const long qrow = (((long)b * L + t0 + lane) * HQ + hq) * N;   // this lane's token (stores)
+  const float dtl = tok ? cur.dtraw : 0.0f;
 
-  // ---- token constants, angles, and the two saved states
+  // ---- token constants and the two saved states into LDS
   if (wave == 0) chunk_scalars<CS>(a, bh, t0, lane, sm.ac, sm.gam, sm.scl, sm.dtv, &sm.aend);
-  {
-    const T* hsrc = reinterpret_cast<const T*>(a.hs) + ((long)bh * nc + c) * P * N;
-    const T* gsrc = reinterpret_cast<const T*>(a.gs) + ((long)bh * nc + c) * N * P;
-    for (int i = tid; i < P * N / 8; i += kBwdThreads) {
-      const int p = i / (N / 8), n8 = i % (N / 8);
-      *reinterpret_cast<Vec8<T>*>(&sm.h[p][8 * n8]) = *reinterpret_cast<const Vec8<T>*>(hsrc + p * N + 8 * n8);
-    }
-    for (int i = tid; i < N * P / 8; i += kBwdThreads) {
-      const int n = i / (P / 8), p8 = i % (P / 8);
-      *reinterpret_cast<Vec8<T>*>(&sm.gt[n][8 * p8]) = *reinterpret_cast<const Vec8<T>*>(gsrc + n * P + 8 * p8);
+#pragma unroll
+  for (int k = 0; k < HP; ++k) {
+    const int i = tid + k * kBwdThreads;
+    if (i < P * N / 8) {
+      *reinterpret_cast<Vec8<T>*>(&sm.h[i / (N / 8)][8 * (i % (N / 8))]) = cur.hpc[k];
+      *reinterpret_cast<Vec8<T>*>(&sm.gt[i / (P / 8)][8 * (i % (P / 8))]) = cur.gpc[k];
     }
   }
-  __syncthreads();
 
   // ---- this thread's two column groups, one per half of the state columns (waves
   // < GH): q^ = q + qb, k^ = k + kb and the rope cos/sin of their pairs stay in
   // registers for every phase below.  Padding tokens hold zeros.
-  constexpr int GH = NH / 8;
-  const bool qkw = wave < GH;
   float qh[2][8], kh[2][8], cs[2][4], sn[2][4];
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
@@ -333,15 +459,15 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
     for (int j = 0; j < 4; ++j) cs[hh][j] = 1.0f, sn[hh][j] = 0.0f;
     if (qkw) {
       float th4[4];
-      group_theta<CS, R>(a, b, h, bh, c, t0, g, lane, th4);
+      group_theta<CS, R>(a, bh, c, g, cur.rates[hh], dtl, th4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         cs[hh][j] = __builtin_amdgcn_cosf(th4[j]);
         sn[hh][j] = __builtin_amdgcn_sinf(th4[j]);
       }
       if (tok) {
-        load8(gq + qrow + 8 * g, qh[hh]);
-        load8(gk + qrow + 8 * g, kh[hh]);
+        cur.qraw[hh].to_f(qh[hh]);
+        cur.kraw[hh].to_f(kh[hh]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           qh[hh][e] += a.s.qbias[(long)h * N + 8 * g + e];
@@ -349,6 +475,13 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
         }
       }
     }
+  }
+  __syncthreads();   // the token constants (key scale below) and the saved states
+
+  // ---- the next item's inputs are requested into L2
+  if (item + (int)gridDim.x < nitems) {
+    const int in = item + gridDim.x;
+    prefetch_item<T, CS, N, P, R>(a, in % nc, in / nc, wave, lane, sink);
   }
 
   // ---- preparation, lane = token: q~, k~, v, dy and the row dot products
@@ -375,18 +508,21 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
       }
     }
   }
-  for (int g = wave; g < P / 8; g += kBwdWaves) {
+#pragma unroll
+  for (int k = 0; k < VGW; ++k) {
+    const int g = wave + k * kBwdWaves;
+    if (g >= P / 8) continue;
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dy[8] = {0, 0, 0, 0, 0, 0, 0, 0}, fz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float dot = 0.0f;
     if (tok) {
-      load8(gv + vrow + 8 * g, v);
-      load8(gdo + vrow + 8 * g, dy);
+      cur.vraw[k].to_f(v);
+      cur.dyraw[k].to_f(dy);
       if (gz) {
         float z[8];
-        load8(gz + vrow + 8 * g, z);
+        cur.zraw[k].to_f(z);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float sz = 1.0f / (1.0f + expf(-z[e]));
+          const float sz = sigmoid_fast(z[e]);
           fz[e] = dy[e] * sz * (1.0f + z[e] * (1.0f - sz));
           dy[e] *= z[e] * sz;
         }
@@ -649,6 +785,9 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
     const float tot = wave_sum(da);
     if (lane == 0) a.ctot[((long)bh * nc + c) * (a.s.R + 1)] = tot;
   }
+  __syncthreads();   // the next item rewrites the LDS tiles
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // no prefetch load is in flight when the workgroup ends
 }
 
 // --------------------------------------------------------------- finishing scans
@@ -888,13 +1027,19 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   if (e != hipSuccess) return e;
 
   const dim3 grid_bh(s.B * s.H), grid_c(a.nc, s.B * s.H);
+  // the chunk-gradient kernel is persistent: one workgroup per compute unit (its LDS
+  // tiles allow one), each walking its share of the (chunk, b, h) items
+  int dev = 0, ncu = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+    ncu = 256;
+  const dim3 grid_p((unsigned)std::min<long>((long)a.nc * s.B * s.H, ncu));
   bool found = false;
 #define X(T, cs, n, p, r)                                                                                  \
   if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
     found = true;                                                                                          \
     hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r>), grid_bh, dim3(kBwdThreads), 0, st, a);       \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
-    hipLaunchKernelGGL((scan_bwd_chunk_kernel<T, cs, n, p, r>), grid_c, dim3(kBwdThreads), 0, st, a);      \
+    hipLaunchKernelGGL((scan_bwd_chunk_kernel<T, cs, n, p, r>), grid_p, dim3(kBwdThreads), 0, st, a);      \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
     if (a.dqh) {                                                                                           \
       hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \

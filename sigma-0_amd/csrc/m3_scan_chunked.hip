@@ -327,14 +327,17 @@ void scan_chunked_kernel(ScanArgs a) {
         const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
                               __uint_as_float(rr.w)};
         const float hdt = 0.5f * s_dt;
+        // angle in revolutions: carry + prefix of tanh(rate) pi dt / 2pi = tanh(rate) dt / 2,
+        // with tanh(x) = 1 - 2 / (1 + e^{2x}); the fractional part is the reference's
+        // mod-2pi wrap, and the hardware sin/cos take revolutions
+        float d[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          d[j] = fmaf(-s_dt, rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j])), hdt);   // s_dt = 0 past the end
+        wave_incl_scan4(d);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          // angle in revolutions: carry + prefix of tanh(rate) pi dt / 2pi = tanh(rate) dt / 2,
-          // with tanh(x) = 1 - 2 / (1 + e^{2x}); the fractional part is the reference's
-          // mod-2pi wrap, and the hardware sin/cos take revolutions
-          const float rcp = rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j]));
-          const float d = fmaf(-s_dt, rcp, hdt);        // s_dt = 0 past the sequence end
-          const float th = __builtin_amdgcn_fractf(carry[k][j] + wave_incl_scan(d));
+          const float th = __builtin_amdgcn_fractf(carry[k][j] + d[j]);
           if constexpr (SO) {            // backward: the angle entering chunk cc (revolutions)
             if (a.chunk_th && lane == 0) a.chunk_th[((long)bh * nc + cc) * R + 4 * g + j] = carry[k][j];
           }

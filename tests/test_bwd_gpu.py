@@ -110,3 +110,15 @@ def test_autograd_matches_functional_backward_and_is_deterministic():
     for k, a, b in zip(names, g1, g2):
         assert torch.equal(a, b), f"d{k} differs between two calls"
         assert torch.equal(leaves[k].grad.to(a.dtype), a), f"autograd d{k} differs"
+
+
+@pytest.mark.parametrize("B,L,H,Hqk,N,P,R,bf16", [
+    (1, 1280, 16, 16, 128, 64, 32, True),   # 20 chunks x 16 heads = 320 items
+    (1, 2600, 4, 4, 64, 32, 16, False),     # 82 chunks (of 32) x 4 heads = 328 items
+])
+def test_gradients_with_more_items_than_compute_units(B, L, H, Hqk, N, P, R, bf16):
+    """The chunk-gradient kernel is persistent (one workgroup per compute unit walking
+    the (chunk, b, h) items): with more items than compute units, workgroups process
+    several items and prefetch the next one's inputs, which the short cases above
+    never do."""
+    _check(B, L, H, Hqk, N, P, R, bf16=bf16, seed=37)
