@@ -41,7 +41,7 @@ __device__ __forceinline__ void lds_dma4_at(const void* sbase, uint32_t voff, ui
 // PER instructions (row%S repeats), so a few 32-bit lane offsets plus a wave-uniform
 // row base address every instruction.
 template <int CS, int S, int J0, int J1>
-__device__ __forceinline__ void stage_rows(lds_uint4* dst, const char* src, long stride, int rows_valid,
+__device__ __forceinline__ void stage_rows(lds_uint4* dst, const char* src, int stride, int rows_valid,
                                            int lane) {
   constexpr int RP = 64 / S;                               // rows per instruction
   constexpr int PER = S * S / 64 > 1 ? S * S / 64 : 1;     // period of the lane pattern
@@ -58,18 +58,22 @@ __device__ __forceinline__ void stage_rows(lds_uint4* dst, const char* src, long
     off[p] = row * (uint32_t)stride + 16u * ((ln % S) ^ (row & (S - 1)));
   }
   // the row base is made opaque so that the compiler keeps one wave-uniform base per
-  // group of PER instructions instead of strength-reducing to 64-bit lane pointers
+  // group of PER instructions instead of strength-reducing to 64-bit lane pointers; the
+  // stride too, so that the per-group offsets are formed here (a few scalar operations)
+  // instead of being hoisted out of the caller's loop and spilled
   const char* base = src;
   asm volatile("" : "+s"(base));
+  int sstride = stride;
+  asm volatile("" : "+s"(sstride));
   if (rows_valid >= CS) {
 #pragma unroll
     for (int j = J0; j < J1; ++j)
-      lds_dma16(base + (long)(j / PER) * (PER * RP) * stride, off[j % PER], dst + 64 * j);
+      lds_dma16(base + (long)((j / PER) * (PER * RP)) * sstride, off[j % PER], dst + 64 * j);
   } else {
 #pragma unroll
     for (int j = J0; j < J1; ++j)
       if (j * RP + lrow < rows_valid)
-        lds_dma16(base + (long)(j / PER) * (PER * RP) * stride, off[j % PER], dst + 64 * j);
+        lds_dma16(base + (long)((j / PER) * (PER * RP)) * sstride, off[j % PER], dst + 64 * j);
   }
 }
 template <int S>

@@ -110,6 +110,7 @@ struct __attribute__((aligned(16))) Smem {
   alignas(16) float scl[2][G::CS];       // trapezoid key scale gamma_t + dt_{t+1} (1 - sigmoid_{t+1})
   alignas(16) float wdec[2][G::CS];      // e^{A_end - A_cum}
   float dec[2];                          // e^{A_end}
+  alignas(16) float fink[G::N];          // the last token's rope'd key (final carry), unscaled
 };
 
 // SO (state only): the pass that produces each segment's exit carry from a zero
@@ -152,10 +153,16 @@ void scan_chunked_kernel(ScanArgs a) {
 
   // ---- element offsets of row (b, t=0, head) in each input; rows advance by the stride
   const int AH = a.ang_shared ? 1 : H;                 // angle rows per token
-  const long qk_stride = (long)HQ * N, v_stride = (long)H * P, a_stride = (long)AH * R;
-  const long qk_row = ((long)b * Lg * HQ + hq) * N + tb * qk_stride;
-  const long v_row = ((long)b * Lg * H + h) * P + tb * v_stride;
-  const long a_row = ((long)b * Lg * AH + (a.ang_shared ? 0 : h)) * R + tb * a_stride;
+  // row strides (elements) are 32-bit; offsets along the sequence are formed in 64 bits
+  const int qk_stride = HQ * N, v_stride = H * P, a_stride = AH * R;
+  // this block's first row of each input (and of the output); the loop only adds t * stride
+  const T* q_base = reinterpret_cast<const T*>(a.q) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
+  const T* k_base = reinterpret_cast<const T*>(a.k) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
+  const long v_row = ((long)b * Lg * H + h) * P + (long)tb * v_stride;
+  const T* v_base = reinterpret_cast<const T*>(a.v) + v_row;
+  const T* z_base = gZ + v_row;
+  T* o_base = gO + v_row;
+  const float* ang_base = a.ang + ((long)b * Lg * AH + (a.ang_shared ? 0 : h)) * R + (long)tb * a_stride;
   for (int i = tid; i < N; i += G::NT) {
     sm.qb[i] = a.qbias[(long)h * N + i];
     sm.kb[i] = a.kbias[(long)h * N + i];
@@ -173,8 +180,8 @@ void scan_chunked_kernel(ScanArgs a) {
     const int t0 = c * CS;
     const int valid = L - t0;
     constexpr int JQ = CS * G::SQ / 64;
-    const char* q0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.q) + qk_row + (long)t0 * qk_stride);
-    const char* k0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + qk_row + (long)t0 * qk_stride);
+    const char* q0 = reinterpret_cast<const char*>(q_base + (long)t0 * qk_stride);
+    const char* k0 = reinterpret_cast<const char*>(k_base + (long)t0 * qk_stride);
     lds_uint4* dq = (lds_uint4*)sm.rq[c % G::NQK];
     lds_uint4* dk = (lds_uint4*)sm.rk[c % G::NQK];
     if (!SO && wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>(dq, q0, qk_stride * G::TS, valid, lane);
@@ -186,7 +193,7 @@ void scan_chunked_kernel(ScanArgs a) {
     const int t0 = c * CS;
     constexpr int JV = CS * G::SV / 64;
     if (wave == kWV) {
-      const char* v0 = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + v_row + (long)t0 * v_stride);
+      const char* v0 = reinterpret_cast<const char*>(v_base + (long)t0 * v_stride);
       stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv[c & 1], v0, v_stride * G::TS, L - t0, lane);
     }
   };
@@ -196,17 +203,23 @@ void scan_chunked_kernel(ScanArgs a) {
     constexpr int JA = CS * G::SA / 64;
     if (wave == kWA) {
       if (R > 0) {
-        const char* a0 = reinterpret_cast<const char*>(a.ang + a_row + (long)t0 * a_stride);
+        const char* a0 = reinterpret_cast<const char*>(ang_base + (long)t0 * a_stride);
         stage_rows<CS, G::SA, 0, JA>((lds_uint4*)sm.ra[c & 1], a0, a_stride * 4, valid, lane);
       }
+      // the bases are made opaque here so that no derived pointer is hoisted out of the
+      // chunk loop (and spilled)
+      const float* pa = gadt + t0;
+      const float* pd = gdt + t0;
+      const float* pt = gtr + t0;
+      asm volatile("" : "+s"(pa), "+s"(pd), "+s"(pt));
       if (lane < CS && lane < valid) {
-        lds_dma4(gadt + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][0][0]);
-        lds_dma4(gdt + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][1][0]);
-        lds_dma4(gtr + t0, 4u * lane, (lds_float*)&sm.rs[c & 1][2][0]);
+        lds_dma4(pa, 4u * lane, (lds_float*)&sm.rs[c & 1][0][0]);
+        lds_dma4(pd, 4u * lane, (lds_float*)&sm.rs[c & 1][1][0]);
+        lds_dma4(pt, 4u * lane, (lds_float*)&sm.rs[c & 1][2][0]);
       }
       if (lane == 0 && t0 + CS < Lnx) {
-        lds_dma4(gdt + t0 + CS, 0u, (lds_float*)&sm.rs[c & 1][1][CS]);
-        lds_dma4(gtr + t0 + CS, 0u, (lds_float*)&sm.rs[c & 1][2][CS]);
+        lds_dma4(pd, 4u * CS, (lds_float*)&sm.rs[c & 1][1][CS]);
+        lds_dma4(pt, 4u * CS, (lds_float*)&sm.rs[c & 1][2][CS]);
       }
     }
   };
@@ -218,7 +231,7 @@ void scan_chunked_kernel(ScanArgs a) {
   Vec8<T> zr;                              // Z of the chunk waiting for its gate
   zr.zero();
   auto load_z = [&](int c) {
-    if (has_z && eact && c * CS + erow < L) zr.load(gZ + v_row + (long)(c * CS + erow) * v_stride + 8 * egrp);
+    if (has_z && eact && c * CS + erow < L) zr.load(z_base + (long)(c * CS + erow) * v_stride + 8 * egrp);
   };
   auto gate = [&](int c) {                 // Y of chunk c -> out
     if (eact && c * CS + erow < L) {
@@ -238,7 +251,7 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) o[q] *= silu_fast(zf[q]);
       }
-      store8(gO + v_row + (long)(c * CS + erow) * v_stride + 8 * egrp, o);
+      store8(o_base + (long)(c * CS + erow) * v_stride + 8 * egrp, o);
     }
   };
 
@@ -414,10 +427,7 @@ void scan_chunked_kernel(ScanArgs a) {
             kf[2 * j + 1] = k0 * sn + k1 * cs;
           }
         }
-        if (a.fin_k && fin_here && tok && t0 + lane == L - 1) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a.fin_k[(long)ci_out * N + 8 * g + e] = kf[e];
-        }
+        if (tok && t0 + lane == L - 1) store8(&sm.fink[8 * g], kf);   // the final carry's key, written after the loop
 #pragma unroll
         for (int e = 0; e < 8; ++e) kf[e] *= scl;
         if (lane < CS) {
@@ -426,9 +436,6 @@ void scan_chunked_kernel(ScanArgs a) {
         }
       }
     }
-    // final carry's V: the segment's last token, straight from the staged row
-    if (a.fin_v && fin_here && c == nc - 1 && wave == 6 && lane < P)
-      a.fin_v[(long)ci_out * P + lane] = Elem<T>::to_f(*staged_elem<G::SV, T>(sv, L - 1 - t0, lane));
     // gate of the previous chunk (its Y tiles were written before the last barrier),
     // then Z for this chunk's gate, then the loads of the next chunks: the gate's wait
     // for Z comes before any of them is in flight
@@ -603,6 +610,14 @@ void scan_chunked_kernel(ScanArgs a) {
   }
   if (!SO && nc > 0) gate(nc - 1);
 
+  // final carry: k of the last token (kept in LDS by its preparation) and its v (still
+  // in the last chunk's staged rows)
+  if (a.fin_k && fin_here && nc > 0) {
+    for (int i = tid; i < N; i += G::NT) a.fin_k[(long)ci_out * N + i] = sm.fink[i];
+    for (int i = tid; i < P; i += G::NT)
+      a.fin_v[(long)ci_out * P + i] =
+          Elem<T>::to_f(*staged_elem<G::SV, T>(sm.rv[(nc - 1) & 1], L - 1 - (nc - 1) * CS, i));
+  }
   if (a.fin_h && fin_here && swave && part == 0) {
 #pragma unroll
     for (int nb = 0; nb < G::NB16; ++nb)
