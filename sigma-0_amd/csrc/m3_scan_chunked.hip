@@ -66,15 +66,23 @@ struct Geo {
   static_assert(SPT >= 1 && NST % PT == 0 && LB16 % SPT == 0, "state-wave split");
   static_assert(NAUX == 4, "12 waves");
   static_assert(QG <= 2 * NAUX + NWY + NST, "column groups per wave");
-  // Q/K 8-column group k (< QGW) of a wave, or QG for none: the auxiliary waves take the
-  // first groups (the rope columns), two each, so the rope angle work stays off the
-  // matrix waves; the remaining groups go one per matrix wave.
+  // Q/K 8-column group k (< QGW) of a wave, or QG for none.  The first groups are the
+  // rope columns, and their owner also computes their angles for the next chunk.  Full
+  // pass: the auxiliary waves take the first groups, two each, so the angle work stays
+  // off the matrix waves; the remaining groups go one per matrix wave.  State-only pass
+  // (no Q and no Y, so the output waves have no matrix work): the output waves and then
+  // the auxiliary waves take the first groups, one each, and the state waves two each
+  // of the rest, which halves the angle work per wave.
+  template <bool SO>
   __device__ static int qgroup(int wave, int k) {
-    if (wave >= NWY + NST) {
-      const int g = 2 * (wave - NWY - NST) + k;
-      return g < QG ? g : QG;
+    int g;
+    if constexpr (SO) {
+      if (wave < NWY) g = k == 0 ? wave : QG;
+      else if (wave >= NWY + NST) g = k == 0 ? NWY + (wave - NWY - NST) : QG;
+      else g = NWY + NAUX + 2 * (wave - NWY) + k;
+    } else {
+      g = wave >= NWY + NST ? 2 * (wave - NWY - NST) + k : 2 * NAUX + wave + (NWY + NST) * k;
     }
-    const int g = 2 * NAUX + wave + (NWY + NST) * k;
     return g < QG ? g : QG;
   }
   static_assert(R % 4 == 0 && 2 * R <= N, "rotation width: a multiple of 4, at most N/2");
@@ -284,7 +292,7 @@ void scan_chunked_kernel(ScanArgs a) {
   for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int r = 4 * G::qgroup(wave, k) + j;
+      const int r = 4 * G::template qgroup<SO>(wave, k) + j;
       carry[k][j] = (a.init_theta && has_init && r < R) ? a.init_theta[(long)ci_in * R + r] * kInvTwoPi : 0.0f;  // revolutions
     }
   // staging never holds uninitialised bits: rows past the sequence end are not loaded
@@ -334,7 +342,7 @@ void scan_chunked_kernel(ScanArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
-      const int g = G::qgroup(wave, k);
+      const int g = G::template qgroup<SO>(wave, k);
       if (g < G::QG && 4 * g < R) {
         const uint4 rr = staged<G::SA>(sm.ra[pb], tl, g);
         const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
@@ -388,7 +396,7 @@ void scan_chunked_kernel(ScanArgs a) {
     // Q/K column groups: rotation angles, biases, rope, key scale
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
-      const int g = G::qgroup(wave, k);
+      const int g = G::template qgroup<SO>(wave, k);
       if (g < G::QG) {
         float qf[8], kf[8];
         {
@@ -632,7 +640,7 @@ void scan_chunked_kernel(ScanArgs a) {
     for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r = 4 * G::qgroup(wave, k) + j;
+        const int r = 4 * G::template qgroup<SO>(wave, k) + j;
         if (r < R) a.fin_theta[(long)ci_out * R + r] = carry[k][j] * kTwoPi;
       }
   }
