@@ -28,11 +28,6 @@ __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, lds_
 __device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, lds_float* l) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_addr(l)) : "memory");
 }
-// The same with the LDS byte address given as a number (base of a __shared__ object
-// plus a field offset).
-__device__ __forceinline__ void lds_dma4_at(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
-  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_byte_addr) : "memory");
-}
 
 // Direct-to-LDS staging of instructions [J0, J1) of CS rows x S 16-byte slots.
 // Instruction j stages 64 slots: lane -> (row, physical slot) = (64j/S + lane/S,

@@ -24,8 +24,6 @@
 //      cumsums over the sequence, the trapezoid and angle chains), and
 //      scan_bwd_reduce_kernel sums the bias and D gradients over batch and chunks.
 // Every sum runs in a fixed order, so the gradients are deterministic.
-#include <algorithm>
-#include <cstddef>
 #include <type_traits>
 
 #include "m3_chunk_common.h"
@@ -287,7 +285,6 @@ struct GradSmem {
   float ps[N / 8][CS];                 // per column group: dk~ . rot(k^)
   float pv[P / 8][CS];                 // per value group: dy.v
   float aend;
-  alignas(16) float sink[64];          // destination of the L2 prefetch loads (never read)
 };
 
 // The global inputs of one (chunk, b, h) item of the chunk-gradient kernel, loaded into
@@ -342,66 +339,7 @@ struct ItemLoads {
   }
 };
 
-// Requests every input line of an item into L2: one direct-to-LDS dword load per
-// 128-byte line (lane = line, or lane = token for the row tensors), all written to a
-// 256-byte LDS sink that nothing reads.  The saved states, Q, K, V, dOut, Z, the
-// rates, and adt, dt, trap of the item's tokens.  Lanes past the sequence end request
-// the last token's rows.
-template <typename T, int CS, int N, int P, int R>
-__device__ __forceinline__ void prefetch_item(const BwdArgs& a, int c, int bh, int wave, int lane,
-                                              uint32_t sink) {
-  constexpr int TS = sizeof(T);
-  constexpr int SL = P * N * TS / 128;                 // lines per saved state
-  constexpr int SJ = (SL + 63) / 64;
-  constexpr int QJ = N * TS / 128 > 0 ? N * TS / 128 : 1;
-  constexpr int VJ = P * TS / 128 > 0 ? P * TS / 128 : 1;
-  constexpr int AJ = R * 4 / 128 > 0 ? R * 4 / 128 : (R > 0 ? 1 : 0);
-  constexpr int NJ = 2 * SJ + 2 * QJ + 3 * VJ + AJ + 3;
-  const int b = bh / a.s.H, h = bh % a.s.H, hq = h / (a.s.H / a.s.Hqk);
-  const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, t0 = c * CS;
-  const uint32_t dt = (uint32_t)(min(t0 + lane, L - 1) - t0);      // this lane's token in the item
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    if (j % kBwdWaves != wave) continue;
-    const char* base;
-    uint32_t off;
-    if (j < 2 * SJ) {
-      base = reinterpret_cast<const char*>(j < SJ ? a.hs : a.gs) + ((long)bh * a.nc + c) * P * N * TS;
-      off = 128u * (uint32_t)min((j % SJ) * 64 + lane, SL - 1);
-    } else if (j < 2 * SJ + 2 * QJ) {
-      const int k = j - 2 * SJ;
-      base = reinterpret_cast<const char*>(k < QJ ? a.s.q : a.s.k) + (((long)b * L + t0) * HQ + hq) * N * TS;
-      off = dt * (uint32_t)(HQ * N * TS) + 128u * (uint32_t)(k % QJ);
-    } else if (j < 2 * SJ + 2 * QJ + 3 * VJ) {
-      const int k = j - 2 * SJ - 2 * QJ, which = k / VJ;
-      const void* src = which == 0 ? a.s.v : which == 1 ? a.dout : (a.s.z ? a.s.z : a.s.v);
-      base = reinterpret_cast<const char*>(src) + (((long)b * L + t0) * H + h) * P * TS;
-      off = dt * (uint32_t)(H * P * TS) + 128u * (uint32_t)(k % VJ);
-    } else if (j < NJ - 3) {
-      const long arow = a.s.ang_shared ? (long)b * L + t0 : ((long)b * L + t0) * H + h;
-      base = reinterpret_cast<const char*>(a.s.ang + arow * R);
-      off = dt * (uint32_t)((a.s.ang_shared ? 1 : H) * R * 4) + 128u * (uint32_t)(j - (NJ - 3 - AJ));
-    } else {
-      const int k = j - (NJ - 3);
-      const float* src = k == 0 ? a.s.adt : k == 1 ? a.s.dt : a.s.trap;
-      base = reinterpret_cast<const char*>(src + (long)bh * L + t0);
-      off = 4u * dt;
-    }
-    // the base is wave-uniform; it is moved to scalar registers explicitly (readfirstlane
-    // returns a signed int: each half is taken as uint32_t before widening, or a low half
-    // with bit 31 set would sign-extend over the high half)
-    const uint64_t bv = reinterpret_cast<uint64_t>(base);
-    const uint32_t bhi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bv >> 32));
-    const uint32_t blo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bv);
-    const uint64_t bs = ((uint64_t)bhi << 32) | (uint64_t)blo;
-    lds_dma4_at(reinterpret_cast<const void*>(bs), off, sink);
-  }
-}
-
-// Persistent: one workgroup per compute unit walks the (chunk, b, h) items.  Once an
-// item's inputs are in LDS and registers, the next item's input lines are requested
-// into L2, so they arrive during this item's matrix work instead of in a burst of
-// every compute unit at every workgroup start.
+// One workgroup per (chunk, b, h) item.
 template <typename T, int CS, int N, int P, int R>
 __global__ __launch_bounds__(kBwdThreads, 1)
 void scan_bwd_chunk_kernel(BwdArgs a) {
@@ -417,14 +355,8 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __builtin_assume(wave >= 0 && wave < kBwdWaves);
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
-  const int nitems = nc * a.s.B * H;
   const bool qkw = wave < GH;
-  // LDS byte address of the prefetch sink: the object's base (its first field) plus the
-  // field offset (an address-space cast of the sink's own address miscompiles here)
-  const uint32_t sink = lds_addr((lds_float*)&sm.qt[0][0]) + (uint32_t)offsetof(S, sink);
-
-  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
-  const int c = item % nc, bh = item / nc, b = bh / H, h = bh % H;
+  const int c = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   Loads cur;
   cur.issue(a, c, bh, tid, wave, lane);
   const int hq = h / (H / HQ);
@@ -478,11 +410,6 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
   }
   __syncthreads();   // the token constants (key scale below) and the saved states
 
-  // ---- the next item's inputs are requested into L2
-  if (item + (int)gridDim.x < nitems) {
-    const int in = item + gridDim.x;
-    prefetch_item<T, CS, N, P, R>(a, in % nc, in / nc, wave, lane, sink);
-  }
 
   // ---- preparation, lane = token: q~, k~, v, dy and the row dot products
   if (qkw) {
@@ -785,9 +712,6 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
     const float tot = wave_sum(da);
     if (lane == 0) a.ctot[((long)bh * nc + c) * (a.s.R + 1)] = tot;
   }
-  __syncthreads();   // the next item rewrites the LDS tiles
-  }
-  __builtin_amdgcn_s_waitcnt(0);   // no prefetch load is in flight when the workgroup ends
 }
 
 // --------------------------------------------------------------- finishing scans
@@ -1027,19 +951,13 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   if (e != hipSuccess) return e;
 
   const dim3 grid_bh(s.B * s.H), grid_c(a.nc, s.B * s.H);
-  // the chunk-gradient kernel is persistent: one workgroup per compute unit (its LDS
-  // tiles allow one), each walking its share of the (chunk, b, h) items
-  int dev = 0, ncu = 256;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
-    ncu = 256;
-  const dim3 grid_p((unsigned)std::min<long>((long)a.nc * s.B * s.H, ncu));
   bool found = false;
 #define X(T, cs, n, p, r)                                                                                  \
   if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
     found = true;                                                                                          \
     hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r>), grid_bh, dim3(kBwdThreads), 0, st, a);       \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
-    hipLaunchKernelGGL((scan_bwd_chunk_kernel<T, cs, n, p, r>), grid_p, dim3(kBwdThreads), 0, st, a);      \
+    hipLaunchKernelGGL((scan_bwd_chunk_kernel<T, cs, n, p, r>), grid_c, dim3(kBwdThreads), 0, st, a);      \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
     if (a.dqh) {                                                                                           \
       hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \

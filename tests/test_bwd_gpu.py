@@ -117,8 +117,6 @@ def test_autograd_matches_functional_backward_and_is_deterministic():
     (1, 2600, 4, 4, 64, 32, 16, False),     # 82 chunks (of 32) x 4 heads = 328 items
 ])
 def test_gradients_with_more_items_than_compute_units(B, L, H, Hqk, N, P, R, bf16):
-    """The chunk-gradient kernel is persistent (one workgroup per compute unit walking
-    the (chunk, b, h) items): with more items than compute units, workgroups process
-    several items and prefetch the next one's inputs, which the short cases above
-    never do."""
+    """More (chunk, b, h) items than compute units (longer sequences and more heads
+    than the cases above): several waves of chunk-gradient workgroups per launch."""
     _check(B, L, H, Hqk, N, P, R, bf16=bf16, seed=37)
