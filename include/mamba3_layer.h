@@ -4,7 +4,8 @@
  * The layer (Mamba3SSM, src/base_model/models/mamba3.py) is
  *   proj = x @ in_proj                                  (library GEMM)
  *   m3_layer_pre: split, BCNorm, decay, trapezoid, angle rates
- *   m3_chunk_scan_fwd_shared (mamba3_scan.h): the scan, B/C shared over heads
+ *   m3_layer_scan: the scan, B/C shared over heads, x and z read in place from
+ *                  proj (or m3_chunk_scan_fwd_shared of mamba3_scan.h on copies)
  *   m3_layer_post: output RMSNorm
  *   out = m3_layer_post(...) @ out_proj                 (library GEMM)
  * Same conventions as mamba3_scan.h: device pointers, io_dtype M3_DTYPE_F32 or
@@ -24,13 +25,33 @@ extern "C" {
  * (mamba3.py:203-268).  proj (B, L, 2HP + 2N + 3H + R) in io_dtype holds
  * [z, x, B, C, dd_dt, dd_A, trap, angles] per token.  Writes Q = RMSNorm(C)
  * and K = RMSNorm(B) (B, L, N) in io_dtype (statistics in float32, scales
- * C_norm_scale / B_norm_scale (N,), eps), V = x and Z = z (B, L, H, P) in io_dtype,
- * DT = softplus(dd_dt + dt_bias), ADT = min(-softplus(dd_A), -A_floor) * DT and
- * Trap = trap as float32 (B, H, L), and the angle rates as float32 (B, L, R).
+ * C_norm_scale / B_norm_scale (N,), eps), V = x and Z = z (B, L, H, P) in io_dtype
+ * (both null: not copied, for m3_layer_scan), DT = softplus(dd_dt + dt_bias),
+ * ADT = min(-softplus(dd_A), -A_floor) * DT and Trap = trap as float32 (B, H, L),
+ * and the angle rates as float32 (B, L, R).
  */
 int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_scale, const float* C_norm_scale,
                  void* Q, void* K, void* V, void* Z, float* ADT, float* DT, float* Trap, float* Angles,
                  int B, int L, int H, int P, int N, int R, float A_floor, float eps, int io_dtype, void* stream);
+
+/*
+ * The layer's scan (_forward_pallas, mamba3.py:369-370, 413-425: Q = C and K = B (B, L, N),
+ * angle rates (B, L, R)) reading x (V) and z (Z) in place from the projection
+ * proj (B, L, d_in_proj), columns [HP, 2HP) and [0, HP), instead of from copies.
+ * Otherwise the arguments and result of m3_chunk_scan_fwd_shared (Out (B, L, H, P)
+ * contiguous, the same workspace size from m3_chunk_scan_ws_bytes).  The rows and
+ * the offset of x (H*P elements) must be multiples of 16 bytes (M3_E_ALIGN
+ * otherwise; bf16: d_in_proj and H*P multiples of 8) and the shape must have a
+ * chunked kernel (M3_E_UNSUPPORTED otherwise); the caller then copies x and z with
+ * m3_layer_pre and uses m3_chunk_scan_fwd_shared.  The reference's layer slices x
+ * and z out of the projection as views before its scan call (mamba3.py:212-219);
+ * this entry point is that call without the copies a contiguous C ABI would need.
+ */
+int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
+                  const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                  const float* Q_bias, const float* K_bias, const float* D, void* Out,
+                  int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                  void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Replaces the RMSNorm of Mamba3SSM._post_norm_and_project (mamba3.py:281-312,

@@ -75,7 +75,8 @@ int scan_fwd(const void* Q, const void* K, const void* V,
              const float* init_k, const float* init_v,
              float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
              int B, int L, int H, int Hqk, int N, int P, int R,
-             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared) {
+             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared,
+             long vz_tok = 0, long vz_bat = 0) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
@@ -105,6 +106,8 @@ int scan_fwd(const void* Q, const void* K, const void* V,
                 "P <= 512, P*N*4 <= 64 KiB)", N, P, R);
   if (impl == M3_IMPL_CHUNKED_MFMA && !aligned16(Angles))
     return fail(M3_E_ALIGN, "Angles must be 16-byte aligned");  // staged as 16-byte rows
+  if (vz_tok != 0 && impl != M3_IMPL_CHUNKED_MFMA)
+    return fail(M3_E_UNSUPPORTED, "V and Z read in place (token stride %ld) need the chunked kernel", vz_tok);
   m3::ScanArgs a;
   a.q = Q; a.k = K; a.v = V; a.adt = ADT; a.dt = DT; a.trap = Trap;
   a.qbias = Q_bias; a.kbias = K_bias; a.ang = Angles; a.D = D; a.z = Z; a.out = Out;
@@ -112,6 +115,7 @@ int scan_fwd(const void* Q, const void* K, const void* V,
   a.fin_theta = fin_theta; a.fin_h = fin_ssm; a.fin_k = fin_k; a.fin_v = fin_v;
   a.B = B; a.L = L; a.H = H; a.Hqk = Hqk; a.N = N; a.P = P; a.R = R; a.CS = chunk_size;
   a.ang_shared = ang_shared ? 1 : 0;
+  a.vz_tok = vz_tok; a.vz_bat = vz_bat;
   const bool bf = io_dtype == M3_DTYPE_BF16;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (impl == M3_IMPL_CHUNKED_MFMA) {
@@ -325,15 +329,40 @@ int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_sca
     g_err[0] = '\0';
     return M3_OK;
   }
-  if (!proj || !dt_bias || !B_norm_scale || !C_norm_scale || !Q || !K || !V || !Z || !ADT || !DT || !Trap ||
+  if (!proj || !dt_bias || !B_norm_scale || !C_norm_scale || !Q || !K || !ADT || !DT || !Trap ||
       (R > 0 && !Angles))
     return fail(M3_E_ARG, "NULL required pointer");
+  if ((V == nullptr) != (Z == nullptr)) return fail(M3_E_ARG, "V and Z: pass both or neither");
   m3::LayerPreArgs a;
   a.proj = proj; a.dt_bias = dt_bias; a.b_scale = B_norm_scale; a.c_scale = C_norm_scale;
   a.q = Q; a.k = K; a.v = V; a.z = Z; a.adt = ADT; a.dt = DT; a.trap = Trap; a.ang = Angles;
   a.B = B; a.L = L; a.H = H; a.P = P; a.N = N; a.R = R; a.A_floor = A_floor; a.eps = eps;
   return check_launch(m3::layer_pre_launch(a, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
                       "layer pre");
+}
+
+int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
+                  const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                  const float* Q_bias, const float* K_bias, const float* D, void* Out,
+                  int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                  void* ws, size_t ws_bytes, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (H <= 0 || P <= 0 || N <= 0 || R < 0)
+    return fail(M3_E_ARG, "non-positive dimension (H=%d N=%d P=%d R=%d)", H, N, P, R);
+  if ((long)d_in_proj < 2L * H * P + 2L * N + 3L * H + R)
+    return fail(M3_E_ARG, "d_in_proj=%d is smaller than the projection's fields (2HP + 2N + 3H + R = %ld)", d_in_proj,
+                2L * H * P + 2L * N + 3L * H + R);
+  const long es = io_dtype == M3_DTYPE_BF16 ? 2 : 4;
+  if (((long)d_in_proj * es) % 16 != 0)
+    return fail(M3_E_ALIGN, "projection rows of %ld bytes: the in-place read of x and z needs a multiple of 16",
+                (long)d_in_proj * es);
+  if (!proj) return fail(M3_E_ARG, "NULL required pointer");
+  const char* pz = reinterpret_cast<const char*>(proj);          // z: columns [0, HP)
+  const char* pv = pz + (long)H * P * es;                          // x: columns [HP, 2HP)
+  return scan_fwd(Q, K, pv, ADT, DT, Trap, Q_bias, K_bias, Angles, D, pz, Out, nullptr, nullptr, nullptr, nullptr,
+                  nullptr, nullptr, nullptr, nullptr, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes, stream,
+                  true, d_in_proj, (long)L * d_in_proj);
 }
 
 int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, int D, float eps, int io_dtype,

@@ -63,8 +63,10 @@ void layer_pre_kernel(LayerPreArgs a) {
   for (int j = wave; j < nt; j += kLayerThreads / 64) {
     const long tok = (long)b * a.L + l0 + j;
     const T* row = proj + tok * dproj;
-    wave_copy(reinterpret_cast<T*>(a.z) + tok * DI, row, DI, lane);
-    wave_copy(reinterpret_cast<T*>(a.v) + tok * DI, row + DI, DI, lane);
+    if (a.v) {   // null when the scan reads x and z in place from the projection
+      wave_copy(reinterpret_cast<T*>(a.z) + tok * DI, row, DI, lane);
+      wave_copy(reinterpret_cast<T*>(a.v) + tok * DI, row + DI, DI, lane);
+    }
     // BCNorm over d_state (one scale per matrix, shared over heads)
     float ssb = 0.0f, ssc = 0.0f;
     for (int n = lane; n < N; n += 64) {

@@ -36,6 +36,10 @@ struct ScanArgs {
   // Angle rates shared over heads, (B, L, R), instead of (B, L, H, R): the fused
   // front end's layout (Q and K then come with Hqk = 1).
   int ang_shared = 0;
+  // Token and batch strides (elements) of V and Z when they are read in place from
+  // wider rows (the mixer layer's input projection); 0: the contiguous (B, L, H, P)
+  // layout.  Honoured by the chunked kernel only; the output stays contiguous.
+  long vz_tok = 0, vz_bat = 0;
 };
 
 // Block order for launches whose heads share Q/K rows: blocks are handed to the 8

@@ -163,13 +163,16 @@ void scan_chunked_kernel(ScanArgs a) {
   const int AH = a.ang_shared ? 1 : H;                 // angle rows per token
   // row strides (elements) are 32-bit; offsets along the sequence are formed in 64 bits
   const int qk_stride = HQ * N, v_stride = H * P, a_stride = AH * R;
+  // V and Z rows: contiguous (B, L, H, P), or in place in wider rows
+  const int vz_stride = a.vz_tok ? (int)a.vz_tok : v_stride;
+  const long vz_batch = a.vz_bat ? a.vz_bat : (long)Lg * v_stride;
   // this block's first row of each input (and of the output); the loop only adds t * stride
   const T* q_base = reinterpret_cast<const T*>(a.q) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
   const T* k_base = reinterpret_cast<const T*>(a.k) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
-  const long v_row = ((long)b * Lg * H + h) * P + (long)tb * v_stride;
-  const T* v_base = reinterpret_cast<const T*>(a.v) + v_row;
-  const T* z_base = gZ + v_row;
-  T* o_base = gO + v_row;
+  const long vz_row = (long)b * vz_batch + (long)h * P + (long)tb * vz_stride;
+  const T* v_base = reinterpret_cast<const T*>(a.v) + vz_row;
+  const T* z_base = gZ + vz_row;
+  T* o_base = gO + ((long)b * Lg * H + h) * P + (long)tb * v_stride;
   const float* ang_base = a.ang + ((long)b * Lg * AH + (a.ang_shared ? 0 : h)) * R + (long)tb * a_stride;
   for (int i = tid; i < N; i += G::NT) {
     sm.qb[i] = a.qbias[(long)h * N + i];
@@ -201,8 +204,8 @@ void scan_chunked_kernel(ScanArgs a) {
     const int t0 = c * CS;
     constexpr int JV = CS * G::SV / 64;
     if (wave == kWV) {
-      const char* v0 = reinterpret_cast<const char*>(v_base + (long)t0 * v_stride);
-      stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv[c & 1], v0, v_stride * G::TS, L - t0, lane);
+      const char* v0 = reinterpret_cast<const char*>(v_base + (long)t0 * vz_stride);
+      stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv[c & 1], v0, vz_stride * G::TS, L - t0, lane);
     }
   };
   auto stage_ars = [&](int c) {
@@ -239,7 +242,7 @@ void scan_chunked_kernel(ScanArgs a) {
   Vec8<T> zr;                              // Z of the chunk waiting for its gate
   zr.zero();
   auto load_z = [&](int c) {
-    if (has_z && eact && c * CS + erow < L) zr.load(z_base + (long)(c * CS + erow) * v_stride + 8 * egrp);
+    if (has_z && eact && c * CS + erow < L) zr.load(z_base + (long)(c * CS + erow) * vz_stride + 8 * egrp);
   };
   auto gate = [&](int c) {                 // Y of chunk c -> out
     if (eact && c * CS + erow < L) {

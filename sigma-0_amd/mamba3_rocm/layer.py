@@ -3,10 +3,13 @@
 heads).
 
     proj = x @ in_proj                      library GEMM in the compute dtype
-    m3_layer_pre                            split, BCNorm, decay, trapezoid, rates
-    m3_chunk_scan_fwd_shared                the scan
+    m3_layer_pre                            BCNorm, decay, trapezoid, rates
+    m3_layer_scan                           the scan, x and z read in place from proj
     m3_layer_post                           output RMSNorm
     out = ... @ out_proj                    library GEMM
+
+Where the projection rows are not a multiple of 16 bytes, m3_layer_pre also copies
+x and z out of proj and the scan is m3_chunk_scan_fwd_shared on the copies.
 
 Parameters keep the reference's names and layouts (flax Dense kernels are
 (in, out)) and stay float32; ``dtype`` is the compute dtype of the projections
@@ -56,6 +59,7 @@ class Mamba3Layer:
         # the projections' operands in the compute dtype (nn.Dense(dtype=...) casts them)
         self.w_in = self.params["in_proj"].to(dtype).contiguous()
         self.w_out = self.params["out_proj"].to(dtype).contiguous()
+        self.last_scan = None      # "in_place" or "copies": how the last forward fed x and z to the scan
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """x (B, L, d_model) or (L, d_model) -> the same shape, in the compute dtype."""
@@ -65,23 +69,43 @@ class Mamba3Layer:
         B, L, _ = x.shape
         dt, dev = self.dtype, x.device
         nh, hd, N, R = self.nh, self.hd, self.N, self.R
-        proj = torch.matmul(x.to(dt), self.w_in)                      # (B, L, d_in_proj)
+        proj = torch.matmul(x.to(dt), self.w_in).contiguous()         # (B, L, d_in_proj)
         Q = torch.empty(B, L, N, device=dev, dtype=dt)
         K = torch.empty_like(Q)
-        V = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
-        Z = torch.empty_like(V)
         f32 = dict(device=dev, dtype=torch.float32)
         ADT, DT, Trap = (torch.empty(B, nh, L, **f32) for _ in range(3))
         Ang = torch.empty(B, L, R, **f32)
         lib = _lib.load()
         io = _IO[dt]
         pp = self.params
-        _lib.check(lib.m3_layer_pre(_ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]),
-                                    _ptr(Q), _ptr(K), _ptr(V), _ptr(Z), _ptr(ADT), _ptr(DT), _ptr(Trap), _ptr(Ang),
-                                    B, L, nh, hd, N, R, self.A_floor, self.eps, io, _stream(proj)),
-                   "m3_layer_pre")
-        y = mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, Ang, pp["C_bias"], pp["B_bias"], pp["D"], Z,
-                                          chunk_size=self.chunk_size)   # Q = C, K = B (mamba3.py:382-388)
+        st = _stream(proj)
+
+        def pre(V, Z):
+            _lib.check(lib.m3_layer_pre(_ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]),
+                                        _ptr(Q), _ptr(K), _ptr(V), _ptr(Z), _ptr(ADT), _ptr(DT), _ptr(Trap),
+                                        _ptr(Ang), B, L, nh, hd, N, R, self.A_floor, self.eps, io, st),
+                       "m3_layer_pre")
+
+        # Q = C, K = B (_forward_pallas, mamba3.py:413-425); x and z read in place from proj
+        pre(None, None)
+        y = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
+        ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, nh, N, hd, R, self.chunk_size, io)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        rc = lib.m3_layer_scan(_ptr(Q), _ptr(K), _ptr(proj), self.d_in_proj, _ptr(ADT), _ptr(DT), _ptr(Trap),
+                               _ptr(Ang), _ptr(pp["C_bias"]), _ptr(pp["B_bias"]), _ptr(pp["D"]), _ptr(y),
+                               B, L, nh, N, hd, R, self.chunk_size, io, ws.data_ptr() if ws_bytes else None,
+                               ws_bytes, st)
+        self.last_scan = "in_place"
+        if rc in (_lib.M3_E_UNSUPPORTED, _lib.M3_E_ALIGN):
+            self.last_scan = "copies"
+            # rows not 16-byte multiples, or no chunked kernel: copy x and z, scan the copies
+            V = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
+            Z = torch.empty_like(V)
+            pre(V, Z)
+            y = mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, Ang, pp["C_bias"], pp["B_bias"], pp["D"], Z,
+                                              chunk_size=self.chunk_size)
+        else:
+            _lib.check(rc, "m3_layer_scan")
         yn = torch.empty(B, L, self.d_inner, device=dev, dtype=dt)
         _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), B, L, self.d_inner, self.eps, io,
                                      _stream(y)), "m3_layer_post")

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_ws", "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd",
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
                             "m3_chunk_scan_bwd_shared", "m3_decode_step", "m3_layer_pre",
-                            "m3_layer_post"])
+                            "m3_layer_scan", "m3_layer_post"])
     for n in names:
         assert hasattr(lib, n), n
     from mamba3_rocm import _lib
@@ -55,6 +55,8 @@ def test_abi_version_and_constants(lib):
     assert _lib.DTYPE_BF16 == _header_define("M3_DTYPE_BF16")
     assert _lib.IMPL_CHUNKED_MFMA == _header_define("M3_IMPL_CHUNKED_MFMA")
     assert _lib.IMPL_GENERIC == _header_define("M3_IMPL_GENERIC")
+    for name in ("M3_OK", "M3_E_ARG", "M3_E_ALIGN", "M3_E_UNSUPPORTED", "M3_E_LAUNCH"):
+        assert getattr(_lib, name) == _header_define(name), name
 
 
 def test_kernel_selection(lib):
@@ -247,3 +249,24 @@ def test_bf16_rounding_matches_torch():
     ours = I.bf16_round(x)
     theirs = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     assert np.array_equal(ours, theirs)
+
+
+def test_layer_scan_validation(lib):
+    """m3_layer_scan (x and z read in place from the projection) rejects bad
+    arguments before any launch: dtype, a projection narrower than its fields, rows
+    that are not a multiple of 16 bytes, NULL; m3_layer_pre takes V and Z together."""
+    from mamba3_rocm import _lib
+    fake = 1 << 20                      # never dereferenced: every call fails validation first
+    H, N, P, R = 4, 128, 64, 32
+    full = 2 * H * P + 2 * N + 3 * H + R      # 812 elements: 1624 bytes in bf16, not a multiple of 16
+
+    def scan(proj, d_in_proj, io=_lib.DTYPE_BF16):
+        return lib.m3_layer_scan(fake, fake, proj, d_in_proj, fake, fake, fake, fake, fake, fake, fake, fake,
+                                 2, 64, H, N, P, R, 64, io, None, 0, None)
+    assert scan(fake, full + 4, io=7) == _lib.M3_E_ARG
+    assert scan(fake, full - 1) == _lib.M3_E_ARG
+    assert scan(fake, full) == _lib.M3_E_ALIGN
+    assert b"16" in lib.m3_last_error()
+    assert scan(None, full + 4) == _lib.M3_E_ARG
+    assert lib.m3_layer_pre(fake, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, fake,
+                            2, 64, H, P, N, R, 1e-4, 1e-6, _lib.DTYPE_BF16, None) == _lib.M3_E_ARG

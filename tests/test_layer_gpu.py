@@ -14,12 +14,13 @@ from oracle import mamba3_layer as ML
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("B,L,d_model,N,headdim,bf16", [
-    (2, 200, 128, 128, 64, True),      # model geometry per head (d_state 128, headdim 64, 4 heads)
-    (1, 1100, 64, 128, 64, True),      # B*H small: the scan's sequence split
-    (2, 150, 64, 64, 32, False),       # fp32: chunked kernel shapes
+@pytest.mark.parametrize("B,L,d_model,N,headdim,bf16,path", [
+    (2, 200, 128, 128, 64, True, "copies"),     # model geometry per head; 812-wide rows: x, z copied
+    (2, 330, 256, 128, 64, True, "in_place"),   # 1336-wide bf16 rows (16-byte multiple): read in place
+    (1, 1100, 64, 128, 64, True, "copies"),     # B*H small: the scan's sequence split
+    (2, 150, 64, 64, 32, False, "in_place"),    # fp32: chunked kernel shapes, 412-wide rows in place
 ])
-def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16):
+def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16, path):
     import torch
     from mamba3_rocm import Mamba3Layer
     p = ML.init_params(d_model, seed=51, d_state=N, headdim=headdim)
@@ -30,7 +31,8 @@ def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16):
     y = layer(torch.from_numpy(x).cuda()).float().cpu().numpy()
     ref = ML.layer_forward(p, x, d_state=N, headdim=headdim, bf16=bf16)
     err = rel(y, ref)
-    print(f"layer {(B, L, d_model, N, headdim)} bf16={bf16} rel={err:.3e}", flush=True)
+    print(f"layer {(B, L, d_model, N, headdim)} bf16={bf16} {layer.last_scan} rel={err:.3e}", flush=True)
+    assert layer.last_scan == path
     assert np.isfinite(y).all()
     assert err <= (2e-2 if bf16 else 1e-4)
 
