@@ -62,6 +62,49 @@ int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
 int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, int D, float eps, int io_dtype,
                   void* stream);
 
+/*
+ * The backbone block around the mixer: SequenceLayer.__call__
+ * (src/base_model/models/layers.py:108-160).  A block on the float32 residual
+ * stream x is
+ *   prenorm:  y = mixer(m3_block_norm(x) -> compute dtype)
+ *   postnorm: y = mixer(x)
+ *   gelu:                 x = m3_block_act(y, -, -, skip = x)
+ *   full_glu / half_glu*: g = m3_block_gelu(y); h1 = out1(g), h2 = out2(g) (GEMMs);
+ *                         x = m3_block_act(y, h1, h2, skip = x)
+ *   postnorm: x = m3_block_norm(x) -> float32
+ */
+#define M3_ACT_GELU 0      /* gelu(y)                    layers.py:139-140 */
+#define M3_ACT_FULL_GLU 1  /* h1 * sigmoid(h2)           layers.py:126-129 */
+#define M3_ACT_HALF_GLU1 2 /* gelu(y) * sigmoid(h2)      layers.py:130-133 */
+#define M3_ACT_HALF_GLU2 3 /* y * sigmoid(h2)            layers.py:134-138 */
+
+/*
+ * flax nn.LayerNorm of the block (self.norm, layers.py:121-122 and 150-151): x
+ * (B, L, D) float32 -> out (B, L, D) in out_dtype (M3_DTYPE_BF16 for the mixer's
+ * input, M3_DTYPE_F32 for the postnorm residual; out may be x then).  Mean and
+ * biased variance in float32, (x - mean) * rsqrt(var + eps) * scale + bias, scale
+ * and bias (D,) float32.
+ */
+int m3_block_norm(const float* x, const float* scale, const float* bias, void* out, int B, int L, int D, float eps,
+                  int out_dtype, void* stream);
+
+/*
+ * nn.gelu (approximate=True, the tanh form) of the mixer output, elementwise in
+ * io_dtype: the GLU Dense layers' input (layers.py:127, 131, 136).  out may be x.
+ */
+int m3_block_gelu(const void* x, void* out, int B, int L, int D, int io_dtype, void* stream);
+
+/*
+ * The activation epilogue and the residual add (layers.py:126-148):
+ * out = skip + act, float32, with act per `activation` (M3_ACT_*) from the mixer
+ * output y and the Dense outputs h1 = out1(gelu(y)) (full_glu only) and
+ * h2 = out2(gelu(y)) (all GLU forms), all in io_dtype; the sigmoid and the
+ * products are rounded to io_dtype as a layer computing in it rounds them.
+ * out may be skip.
+ */
+int m3_block_act(const void* y, const void* h1, const void* h2, const float* skip, float* out, int B, int L, int D,
+                 int activation, int io_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -381,4 +381,55 @@ int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, in
                       "layer post");
 }
 
+int m3_block_norm(const float* x, const float* scale, const float* bias, void* out, int B, int L, int D, float eps,
+                  int out_dtype, void* stream) {
+  if (out_dtype != M3_DTYPE_F32 && out_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "out_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", out_dtype);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!x || !scale || !bias || !out) return fail(M3_E_ARG, "NULL required pointer");
+  m3::BlockNormArgs a;
+  a.x = x; a.scale = scale; a.bias = bias; a.out = out; a.rows = (long)B * L; a.D = D; a.eps = eps; a.vec = 0;
+  return check_launch(m3::block_norm_launch(a, out_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "block norm");
+}
+
+int m3_block_gelu(const void* x, void* out, int B, int L, int D, int io_dtype, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!x || !out) return fail(M3_E_ARG, "NULL required pointer");
+  m3::BlockEltArgs a{};
+  a.y = x; a.out = out; a.n = (long)B * L * D; a.act = M3_ACT_GELU;
+  return check_launch(m3::block_elt_launch(a, true, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "block gelu");
+}
+
+int m3_block_act(const void* y, const void* h1, const void* h2, const float* skip, float* out, int B, int L, int D,
+                 int activation, int io_dtype, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (activation < M3_ACT_GELU || activation > M3_ACT_HALF_GLU2)
+    return fail(M3_E_ARG, "activation must be one of M3_ACT_GELU..M3_ACT_HALF_GLU2, got %d", activation);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!y || !skip || !out) return fail(M3_E_ARG, "NULL required pointer");
+  if (activation == M3_ACT_FULL_GLU && !h1) return fail(M3_E_ARG, "full_glu needs h1 (the out1 Dense output)");
+  if (activation != M3_ACT_GELU && !h2) return fail(M3_E_ARG, "the GLU activations need h2 (the out2 Dense output)");
+  m3::BlockEltArgs a{};
+  a.y = y; a.h1 = h1; a.h2 = h2; a.skip = skip; a.out = out; a.n = (long)B * L * D; a.act = activation;
+  return check_launch(m3::block_elt_launch(a, false, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "block activation");
+}
+
 }  // extern "C"

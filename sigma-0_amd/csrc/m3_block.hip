@@ -1,0 +1,205 @@
+// The backbone block's elementwise work around the mixer on gfx950:
+// SequenceLayer.__call__ (src/base_model/models/layers.py:108-160).
+//   block_norm_kernel  flax nn.LayerNorm over d_model (layers.py:121-122, 150-151):
+//                      mean and biased variance in float32, (x - mean) *
+//                      rsqrt(var + eps) * scale + bias, from the float32 residual
+//                      stream to the compute dtype (prenorm: the mixer's input) or
+//                      to float32 (postnorm: the residual stream itself).
+//   block_gelu_kernel  nn.gelu (tanh form) in the compute dtype: the GLU Dense's
+//                      input (layers.py:127-137).
+//   block_act_kernel   the activation epilogue and the residual add
+//                      (layers.py:126-148): gelu, full_glu, half_glu1 or
+//                      half_glu2 from the mixer output y and the Dense outputs,
+//                      each product rounded to the compute dtype as a bf16
+//                      layer rounds it, then out = skip + that, in float32.
+// All three read and write each element once: HBM-bound, one wave per row for
+// the norm (its statistics), eight elements per lane for the elementwise pair.
+#include "../../include/mamba3_layer.h"
+#include "m3_scan.h"
+
+namespace m3 {
+namespace {
+
+constexpr int kBlockThreads = 256;
+
+// 0.5 x (1 + tanh(u)) == x * sigmoid(2u): the tanh gelu with one exponential.
+// u = sqrt(2/pi) (x + 0.044715 x^3); exp(-2u) -> inf for large negative x gives
+// x * rcp(inf) = -0, the gelu's limit.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float u2 = 1.5957691216057308f * fmaf(0.044715f * x * x, x, x);   // 2 sqrt(2/pi) (x + k x^3)
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-u2));
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+template <typename T>
+__device__ __forceinline__ float rnd(float x) { return Elem<T>::to_f(Elem<T>::from_f(x)); }
+
+// One wave per row.  The vector path holds the row in registers (D a multiple of 4,
+// D <= 64 * 4 * kNormVec, 16-byte rows): one read, two register passes for the
+// statistics, one write.  Otherwise the row is read from memory three times.
+constexpr int kNormVec = 8;
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float o[4]);
+template <>
+__device__ __forceinline__ void store4<float>(float* p, const float o[4]) {
+  *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
+}
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* p, const float o[4]) {
+  bf16x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = (bf16)o[i];
+  *reinterpret_cast<bf16x4*>(p) = v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlockThreads)
+void block_norm_kernel(BlockNormArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long row = (long)blockIdx.x * (kBlockThreads / 64) + wave;
+  if (row >= a.rows) return;                           // whole waves only: no barrier below
+  const int D = a.D;
+  const float* x = a.x + row * D;
+  T* out = reinterpret_cast<T*>(a.out) + row * D;
+  const float inv_d = 1.0f / (float)D;
+  if (a.vec) {
+    const int n4 = D / 4;
+    float4 v[kNormVec];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+      const int i = lane + 64 * k;
+      v[k] = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0, 0, 0, 0);
+      s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    }
+    const float mean = group_sum<64>(s) * inv_d;
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+      if (lane + 64 * k < n4) {
+        const float dx = v[k].x - mean, dy = v[k].y - mean, dz = v[k].z - mean, dw = v[k].w - mean;
+        ss += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
+    }
+    const float rs = rsqrtf(group_sum<64>(ss) * inv_d + a.eps);
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+      const int i = lane + 64 * k;
+      if (i < n4) {
+        const float4 sc = reinterpret_cast<const float4*>(a.scale)[i];
+        const float4 bi = reinterpret_cast<const float4*>(a.bias)[i];
+        const float o[4] = {fmaf((v[k].x - mean) * rs, sc.x, bi.x), fmaf((v[k].y - mean) * rs, sc.y, bi.y),
+                            fmaf((v[k].z - mean) * rs, sc.z, bi.z), fmaf((v[k].w - mean) * rs, sc.w, bi.w)};
+        store4<T>(out + 4 * i, o);
+      }
+    }
+  } else {
+    float s = 0.0f;
+    for (int i = lane; i < D; i += 64) s += x[i];
+    const float mean = group_sum<64>(s) * inv_d;
+    float ss = 0.0f;
+    for (int i = lane; i < D; i += 64) ss += (x[i] - mean) * (x[i] - mean);
+    const float rs = rsqrtf(group_sum<64>(ss) * inv_d + a.eps);
+    for (int i = lane; i < D; i += 64) out[i] = Elem<T>::from_f(fmaf((x[i] - mean) * rs, a.scale[i], a.bias[i]));
+  }
+}
+
+// Eight elements per lane when n is a multiple of 8 and the arrays are 16-byte
+// aligned (a.vec), else one.
+template <typename T>
+__global__ __launch_bounds__(kBlockThreads)
+void block_gelu_kernel(BlockEltArgs a) {
+  const long i = (long)blockIdx.x * kBlockThreads + threadIdx.x;
+  const T* x = reinterpret_cast<const T*>(a.y);
+  T* out = reinterpret_cast<T*>(a.out);
+  if (a.vec) {
+    if (8 * i >= a.n) return;
+    float f[8], o[8];
+    Vec8<T> v;
+    v.load(x + 8 * i);
+    v.to_f(f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = gelu_tanh(f[e]);
+    store8(out + 8 * i, o);
+  } else if (i < a.n) {
+    out[i] = Elem<T>::from_f(gelu_tanh(Elem<T>::to_f(x[i])));
+  }
+}
+
+// v = the activation's output rounded to T; out = skip + v (out may be skip).
+template <typename T>
+__device__ __forceinline__ float block_act(int act, float y, float h1, float h2) {
+  switch (act) {
+    case M3_ACT_GELU: return rnd<T>(gelu_tanh(y));
+    case M3_ACT_FULL_GLU: return rnd<T>(h1 * rnd<T>(sigmoid_f(h2)));
+    case M3_ACT_HALF_GLU1: return rnd<T>(rnd<T>(gelu_tanh(y)) * rnd<T>(sigmoid_f(h2)));
+    default: return rnd<T>(y * rnd<T>(sigmoid_f(h2)));         // M3_ACT_HALF_GLU2
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlockThreads)
+void block_act_kernel(BlockEltArgs a) {
+  const long i = (long)blockIdx.x * kBlockThreads + threadIdx.x;
+  const T* y = reinterpret_cast<const T*>(a.y);
+  const T* h1 = reinterpret_cast<const T*>(a.h1);
+  const T* h2 = reinterpret_cast<const T*>(a.h2);
+  float* out = reinterpret_cast<float*>(a.out);
+  const int act = a.act;
+  if (a.vec) {
+    if (8 * i >= a.n) return;
+    float fy[8], f1[8] = {}, f2[8] = {}, sk[8], o[8];
+    Vec8<T> v;
+    v.load(y + 8 * i);
+    v.to_f(fy);
+    if (act == M3_ACT_FULL_GLU) {
+      v.load(h1 + 8 * i);
+      v.to_f(f1);
+    }
+    if (act != M3_ACT_GELU) {
+      v.load(h2 + 8 * i);
+      v.to_f(f2);
+    }
+    Vec8<float> s;
+    s.load(a.skip + 8 * i);
+    s.to_f(sk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = sk[e] + block_act<T>(act, fy[e], f1[e], f2[e]);
+    store8(out + 8 * i, o);
+  } else if (i < a.n) {
+    const float f1 = act == M3_ACT_FULL_GLU ? Elem<T>::to_f(h1[i]) : 0.0f;
+    const float f2 = act != M3_ACT_GELU ? Elem<T>::to_f(h2[i]) : 0.0f;
+    out[i] = a.skip[i] + block_act<T>(act, Elem<T>::to_f(y[i]), f1, f2);
+  }
+}
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+hipError_t block_norm_launch(BlockNormArgs a, bool bf16_out, hipStream_t st) {
+  a.vec = a.D % 4 == 0 && a.D <= 64 * 4 * kNormVec && al16(a.x) && al16(a.out) && al16(a.scale) && al16(a.bias);
+  const dim3 grid((unsigned)((a.rows + kBlockThreads / 64 - 1) / (kBlockThreads / 64)));
+  if (bf16_out) hipLaunchKernelGGL(block_norm_kernel<bf16>, grid, dim3(kBlockThreads), 0, st, a);
+  else hipLaunchKernelGGL(block_norm_kernel<float>, grid, dim3(kBlockThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t block_elt_launch(BlockEltArgs a, bool gelu_only, bool bf16_io, hipStream_t st) {
+  a.vec = a.n % 8 == 0 && al16(a.y) && al16(a.out) && (!a.h1 || al16(a.h1)) && (!a.h2 || al16(a.h2)) &&
+          (!a.skip || al16(a.skip));
+  const long lanes = a.vec ? a.n / 8 : a.n;
+  const dim3 grid((unsigned)((lanes + kBlockThreads - 1) / kBlockThreads));
+  if (gelu_only) {
+    if (bf16_io) hipLaunchKernelGGL(block_gelu_kernel<bf16>, grid, dim3(kBlockThreads), 0, st, a);
+    else hipLaunchKernelGGL(block_gelu_kernel<float>, grid, dim3(kBlockThreads), 0, st, a);
+  } else {
+    if (bf16_io) hipLaunchKernelGGL(block_act_kernel<bf16>, grid, dim3(kBlockThreads), 0, st, a);
+    else hipLaunchKernelGGL(block_act_kernel<float>, grid, dim3(kBlockThreads), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace m3

@@ -91,6 +91,23 @@ struct LayerPostArgs {
 hipError_t layer_pre_launch(const LayerPreArgs& a, bool bf16_io, hipStream_t st);
 hipError_t layer_post_launch(const LayerPostArgs& a, bool bf16_io, hipStream_t st);
 
+// The backbone block's norm and elementwise kernels (m3_block.hip).  `vec` is set by
+// the launchers (16-byte paths).
+struct BlockNormArgs {
+  const float* x; const float* scale; const float* bias; void* out;   // (rows, D), (D,), (D,), (rows, D)
+  long rows; int D;
+  float eps;
+  int vec;
+};
+struct BlockEltArgs {
+  const void* y; const void* h1; const void* h2; const float* skip; void* out;   // n elements each
+  long n;
+  int act;   // M3_ACT_*
+  int vec;
+};
+hipError_t block_norm_launch(BlockNormArgs a, bool bf16_out, hipStream_t st);
+hipError_t block_elt_launch(BlockEltArgs a, bool gelu_only, bool bf16_io, hipStream_t st);
+
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS);
 hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStream_t st);

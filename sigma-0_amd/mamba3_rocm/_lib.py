@@ -16,6 +16,8 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmamba3_rocm.so")
 # return codes of the C ABI (include/mamba3_scan.h)
 M3_OK, M3_E_ARG, M3_E_ALIGN, M3_E_UNSUPPORTED, M3_E_LAUNCH = 0, 1, 2, 3, 4
+# activations of m3_block_act (include/mamba3_layer.h)
+M3_ACT_GELU, M3_ACT_FULL_GLU, M3_ACT_HALF_GLU1, M3_ACT_HALF_GLU2 = 0, 1, 2, 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -25,7 +27,7 @@ EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_sc
            "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes", "m3_chunk_scan_fwd_ws",
            "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd", "m3_chunk_scan_fwd_shared",
            "m3_chunk_scan_bwd_shared_ws_bytes", "m3_chunk_scan_bwd_shared", "m3_decode_step",
-           "m3_layer_pre", "m3_layer_scan", "m3_layer_post")
+           "m3_layer_pre", "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu", "m3_block_act")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -45,6 +47,9 @@ _SIGS = {
     "m3_layer_pre": ([_P] * 12 + [_I] * 6 + [ctypes.c_float, ctypes.c_float, _I, _P], _I),
     "m3_layer_scan": ([_P] * 3 + [_I] + [_P] * 8 + [_I] * 8 + [_P, ctypes.c_size_t, _P], _I),
     "m3_layer_post": ([_P] * 3 + [_I] * 3 + [ctypes.c_float, _I, _P], _I),
+    "m3_block_norm": ([_P] * 4 + [_I] * 3 + [ctypes.c_float, _I, _P], _I),
+    "m3_block_gelu": ([_P] * 2 + [_I] * 4 + [_P], _I),
+    "m3_block_act": ([_P] * 5 + [_I] * 5 + [_P], _I),
     "m3_decode_step": ([_P] * 16 + [_I] * 9 + [_P], _I),
 }
 

@@ -5,8 +5,11 @@ SequenceLayer blocks (layers.py:108-160) with the Mamba3 mixer (Mamba3Layer).
 A block is skip = x; LayerNorm if prenorm; mixer; activation (gelu, full_glu,
 half_glu1, half_glu2, with the block's out1/out2 Dense layers in the compute
 dtype); x = skip + x; LayerNorm if postnorm.  flax defaults: LayerNorm eps 1e-6,
-gelu with the tanh approximation.  The mixer runs the hand-written kernels; the
-norms, the gate and the embedding lookup are the host framework's (torch) ops.
+gelu with the tanh approximation.  The mixer and the block's elementwise work run
+the hand-written kernels: m3_block_norm (LayerNorm from the float32 residual
+straight to the mixer's dtype), m3_block_gelu (the Dense layers' input) and
+m3_block_act (the gate and the residual add in one pass).  The Dense layers are
+library GEMMs; the embedding lookup is torch's gather.
 ``logits`` adds the LOB models' per-token head (mode "none"): the decoder Dense
 on the float32 features, then log_softmax in float32 (lob_seq_model.py:530-542).
 Inference only (dropout is the identity).
@@ -18,9 +21,13 @@ from typing import Dict, List
 import torch
 import torch.nn.functional as F
 
+from . import _lib
 from .layer import Mamba3Layer
+from .ops import _IO, _ptr, _stream
 
 ACTIVATIONS = ("gelu", "full_glu", "half_glu1", "half_glu2")
+_ACT = dict(gelu=_lib.M3_ACT_GELU, full_glu=_lib.M3_ACT_FULL_GLU, half_glu1=_lib.M3_ACT_HALF_GLU1,
+            half_glu2=_lib.M3_ACT_HALF_GLU2)
 
 
 class Mamba3Stack:
@@ -36,7 +43,7 @@ class Mamba3Stack:
         for lp in params["layers"]:
             b = dict(mixer=Mamba3Layer(lp["mixer"], d_model, d_state=d_state, headdim=headdim,
                                        chunk_size=chunk_size, dtype=dtype),
-                     ln_scale=lp["ln_scale"].float(), ln_bias=lp["ln_bias"].float())
+                     ln_scale=lp["ln_scale"].float().contiguous(), ln_bias=lp["ln_bias"].float().contiguous())
             for n in ("out1", "out2"):
                 b[n + "_w"] = lp[n + "_w"].to(dtype).t().contiguous()     # flax (in, out) -> F.linear (out, in)
                 b[n + "_b"] = lp[n + "_b"].to(dtype)
@@ -47,28 +54,37 @@ class Mamba3Stack:
             self.decoder_b = params["decoder_b"].float().contiguous()
 
     def _block(self, b, x):
+        """SequenceLayer.__call__ (layers.py:108-160) on the float32 residual x (B, L, D)."""
+        lib, io, st = _lib.load(), _IO[self.dtype], _stream(x)
+        Bn, L, D = x.shape
+
+        def norm(src, out, dtype):
+            _lib.check(lib.m3_block_norm(_ptr(src), _ptr(b["ln_scale"]), _ptr(b["ln_bias"]), _ptr(out), Bn, L, D,
+                                         1e-6, dtype, st), "m3_block_norm")
+
         skip = x
         if self.prenorm:
-            x = F.layer_norm(x, (self.d_model,), b["ln_scale"], b["ln_bias"], eps=1e-6)
-        x = b["mixer"](x)                                   # compute dtype
-        dense = lambda a, n: F.linear(a, b[n + "_w"], b[n + "_b"])   # noqa: E731
-        if self.activation == "gelu":
-            x = F.gelu(x, approximate="tanh")
+            xin = torch.empty(Bn, L, D, device=x.device, dtype=self.dtype)
+            norm(x, xin, io)
         else:
-            g = F.gelu(x, approximate="tanh")
+            xin = x
+        y = b["mixer"](xin).contiguous()                    # compute dtype
+        h1 = h2 = None
+        if self.activation != "gelu":
+            g = torch.empty_like(y)
+            _lib.check(lib.m3_block_gelu(_ptr(y), _ptr(g), Bn, L, D, io, st), "m3_block_gelu")
+            h2 = F.linear(g, b["out2_w"], b["out2_b"])
             if self.activation == "full_glu":
-                x = dense(g, "out1") * torch.sigmoid(dense(g, "out2"))
-            elif self.activation == "half_glu1":
-                x = g * torch.sigmoid(dense(g, "out2"))
-            else:
-                x = x * torch.sigmoid(dense(g, "out2"))
-        x = skip + x.float()
+                h1 = F.linear(g, b["out1_w"], b["out1_b"])
+        out = torch.empty_like(x)
+        _lib.check(lib.m3_block_act(_ptr(y), _ptr(h1), _ptr(h2), _ptr(skip), _ptr(out), Bn, L, D,
+                                    _ACT[self.activation], io, st), "m3_block_act")
         if not self.prenorm:
-            x = F.layer_norm(x, (self.d_model,), b["ln_scale"], b["ln_bias"], eps=1e-6)
-        return x
+            norm(out, out, _lib.DTYPE_F32)
+        return out
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
-        x = self.embed[ids]
+        x = self.embed[ids].contiguous()
         for b in self.blocks:
             x = self._block(b, x)
         return x

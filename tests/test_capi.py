@@ -41,7 +41,8 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_ws", "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd",
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
                             "m3_chunk_scan_bwd_shared", "m3_decode_step", "m3_layer_pre",
-                            "m3_layer_scan", "m3_layer_post"])
+                            "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu",
+                            "m3_block_act"])
     for n in names:
         assert hasattr(lib, n), n
     from mamba3_rocm import _lib
@@ -270,3 +271,26 @@ def test_layer_scan_validation(lib):
     assert scan(None, full + 4) == _lib.M3_E_ARG
     assert lib.m3_layer_pre(fake, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, fake,
                             2, 64, H, P, N, R, 1e-4, 1e-6, _lib.DTYPE_BF16, None) == _lib.M3_E_ARG
+
+
+def test_block_entry_points_validate(lib):
+    """The backbone block's C entry points (LayerNorm, gelu, activation epilogue)
+    reject bad dtypes, activations and missing Dense outputs before any launch, and
+    an empty batch is a no-op; the activation codes match the header."""
+    from mamba3_rocm import _lib
+    text = open(os.path.join(ROOT, "include", "mamba3_layer.h")).read()
+    for name in ("M3_ACT_GELU", "M3_ACT_FULL_GLU", "M3_ACT_HALF_GLU1", "M3_ACT_HALF_GLU2"):
+        assert getattr(_lib, name) == int(re.search(rf"#define\s+{name}\s+(\d+)", text).group(1)), name
+    fake = 1 << 20                      # never dereferenced: every call fails validation or is empty
+    bf = _lib.DTYPE_BF16
+    assert lib.m3_block_norm(fake, fake, fake, fake, 2, 8, 64, 1e-6, 5, None) == _lib.M3_E_ARG
+    assert lib.m3_block_norm(fake, None, fake, fake, 2, 8, 64, 1e-6, bf, None) == _lib.M3_E_ARG
+    assert lib.m3_block_norm(fake, fake, fake, fake, 0, 8, 64, 1e-6, bf, None) == _lib.M3_OK
+    assert lib.m3_block_gelu(fake, fake, 2, 8, 0, bf, None) == _lib.M3_E_ARG
+    assert lib.m3_block_gelu(fake, fake, 2, 8, 64, 9, None) == _lib.M3_E_ARG
+    assert lib.m3_block_act(fake, None, fake, fake, fake, 2, 8, 64, 4, bf, None) == _lib.M3_E_ARG
+    assert lib.m3_block_act(fake, None, fake, fake, fake, 2, 8, 64, _lib.M3_ACT_FULL_GLU, bf, None) == _lib.M3_E_ARG
+    assert b"h1" in lib.m3_last_error()
+    assert lib.m3_block_act(fake, None, None, fake, fake, 2, 8, 64, _lib.M3_ACT_HALF_GLU2, bf, None) == _lib.M3_E_ARG
+    assert lib.m3_block_act(fake, None, None, None, fake, 2, 8, 64, _lib.M3_ACT_GELU, bf, None) == _lib.M3_E_ARG
+    assert lib.m3_block_act(fake, None, None, fake, fake, 0, 8, 64, _lib.M3_ACT_GELU, bf, None) == _lib.M3_OK

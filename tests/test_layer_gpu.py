@@ -5,6 +5,8 @@ bf16 2e-2 (the scan's bf16 bar; the oracle rounds to bf16 where the reference's
 bf16 layer does).  The reference's own bf16-vs-f32 layer bound is 5e-2
 (test_mamba3_mixed_precision.py:86-104).
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -84,3 +86,82 @@ def test_backbone_logits_config5_geometry():
     agree = float(np.mean(np.argmax(lp, -1) == np.argmax(ref, -1)))
     print(f"stack logits config5 geometry rel={err:.3e} argmax agreement={agree:.4f}", flush=True)
     assert lp.dtype == np.float32 and err <= 2e-2
+
+
+@pytest.mark.parametrize("B,L,D,bf16", [
+    (2, 37, 768, True),     # config 5's width: the register path
+    (1, 9, 100, False),     # fp32, D % 8 != 0: 16-byte norm rows, scalar elementwise path
+    (1, 5, 2050, True),     # D > 2048 and D % 4 != 0: the norm's scalar path
+])
+def test_block_kernels_match_torch_fp32(B, L, D, bf16):
+    """m3_block_norm / m3_block_gelu / m3_block_act against torch restatements of
+    LayerNorm (float32, eps 1e-6), the tanh gelu and the four activation epilogues
+    (float64, the oracle's precision, with the same rounding points).  fp32: 2e-6
+    relative to the largest element; bf16: within 2^-7 relative per element (a last-bit
+    difference in float32 can flip one rounding).  The gelu reference is float64
+    is x * sigmoid(2u) in float64, equal to 0.5 x (1 + tanh(u)) (checked to 1e-12 where
+    the latter is accurate): 1 + tanh(u) cancels for x below about -4.5 in float32 and
+    about -7 in float64."""
+    import torch
+    import torch.nn.functional as F
+    from mamba3_rocm import _lib
+    from mamba3_rocm.ops import _stream
+    lib = _lib.load()
+    g = torch.Generator(device="cuda").manual_seed(71)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    io = _lib.DTYPE_BF16 if bf16 else _lib.DTYPE_F32
+    x = torch.randn(B, L, D, device="cuda", generator=g) * 3 + 0.5
+    sc = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+    bi = 0.1 * torch.randn(D, device="cuda", generator=g)
+    st = _stream(x)
+    r = (lambda t: t.to(dt).double())         # noqa: E731
+
+    def close(got, want, what):
+        got, want = got.double(), want.double()
+        if bf16:
+            # absolute floor: below x = -10.7 exp(-2u) overflows float32 and the kernel's gelu
+            # is -0 where the exact value is under 1e-38
+            tol = want.abs() * 2 ** -7 * 1.01 + 1e-30
+            bad = ((got - want).abs() > tol).sum().item()
+            assert bad == 0, f"{what}: {bad} elements outside 2^-7 relative"
+        else:
+            err = ((got - want).abs().max() / want.abs().max()).item()
+            assert err <= 2e-6, f"{what}: rel {err:.2e}"
+
+    ln_ref = F.layer_norm(x, (D,), sc, bi, eps=1e-6)
+    out = torch.empty(B, L, D, device="cuda", dtype=dt)
+    _lib.check(lib.m3_block_norm(x.data_ptr(), sc.data_ptr(), bi.data_ptr(), out.data_ptr(), B, L, D, 1e-6, io, st),
+               "m3_block_norm")
+    close(out, r(ln_ref), "norm")
+    o32 = x.clone()
+    _lib.check(lib.m3_block_norm(o32.data_ptr(), sc.data_ptr(), bi.data_ptr(), o32.data_ptr(), B, L, D, 1e-6,
+                                 _lib.DTYPE_F32, st), "m3_block_norm f32 in place")
+    assert ((o32 - ln_ref).abs().max() / ln_ref.abs().max()).item() <= 2e-6
+
+    y = r(x).to(dt).contiguous()
+    gl = torch.empty_like(y)
+    _lib.check(lib.m3_block_gelu(y.data_ptr(), gl.data_ptr(), B, L, D, io, st), "m3_block_gelu")
+    yd = y.double()
+    gelu_ref = yd * torch.sigmoid(2 * math.sqrt(2 / math.pi) * (yd + 0.044715 * yd ** 3))
+    ok = yd > -4                               # where the tanh form has no cancellation in float64
+    tanh_form = F.gelu(yd, approximate="tanh")
+    assert ((gelu_ref - tanh_form)[ok].abs() <= 1e-12 * (1 + tanh_form[ok].abs())).all()
+    close(gl, r(gelu_ref), "gelu")
+
+    h1 = (torch.randn(B, L, D, device="cuda", generator=g) * 2).to(dt)
+    h2 = (torch.randn(B, L, D, device="cuda", generator=g) * 2).to(dt)
+    skip = torch.randn(B, L, D, device="cuda", generator=g)
+    yf, f1, f2 = y.double(), h1.double(), h2.double()
+    want = {_lib.M3_ACT_GELU: r(gelu_ref),
+            _lib.M3_ACT_FULL_GLU: r(f1 * r(torch.sigmoid(f2))),
+            _lib.M3_ACT_HALF_GLU1: r(r(gelu_ref) * r(torch.sigmoid(f2))),
+            _lib.M3_ACT_HALF_GLU2: r(yf * r(torch.sigmoid(f2)))}
+    for act, v in want.items():
+        out = torch.empty_like(skip)
+        _lib.check(lib.m3_block_act(y.data_ptr(), h1.data_ptr(), h2.data_ptr(), skip.data_ptr(), out.data_ptr(),
+                                    B, L, D, act, io, st), "m3_block_act")
+        # out = float32(skip + v): v may differ by its own tolerance, the add by one float32 rounding
+        want_out = (skip.double() + v).float().double()
+        tol = v.abs() * (2 ** -7 * 1.01 if bf16 else 2e-6) + want_out.abs() * 2 ** -23 + 1e-30
+        bad = ((out.double() - want_out).abs() > tol).sum().item()
+        assert bad == 0, f"act {act}: {bad} elements outside tolerance"
