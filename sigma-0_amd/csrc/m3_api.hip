@@ -333,7 +333,11 @@ int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_sca
       (R > 0 && !Angles))
     return fail(M3_E_ARG, "NULL required pointer");
   if ((V == nullptr) != (Z == nullptr)) return fail(M3_E_ARG, "V and Z: pass both or neither");
-  m3::LayerPreArgs a;
+  const size_t es = io_dtype == M3_DTYPE_BF16 ? 2 : 4;
+  if (m3::layer_pre_lds_bytes(1, 2 * N + 3 * H + R, N, es) > (size_t)m3::kLayerPreLds)
+    return fail(M3_E_UNSUPPORTED, "one token's B, C, per-head and angle fields (%zu bytes) exceed the %d-byte staging",
+                (size_t)(2 * N + 3 * H + R) * es, m3::kLayerPreLds);
+  m3::LayerPreArgs a{};
   a.proj = proj; a.dt_bias = dt_bias; a.b_scale = B_norm_scale; a.c_scale = C_norm_scale;
   a.q = Q; a.k = K; a.v = V; a.z = Z; a.adt = ADT; a.dt = DT; a.trap = Trap; a.ang = Angles;
   a.B = B; a.L = L; a.H = H; a.P = P; a.N = N; a.R = R; a.A_floor = A_floor; a.eps = eps;

@@ -45,32 +45,76 @@ __device__ __forceinline__ void wave_copy(T* dst, const T* src, int n, int lane)
   }
 }
 
-// A tile of kTileTok consecutive tokens of one batch row per workgroup: the row work
-// (copies, BCNorm, angle rates) one wave per token, the per-head values with lanes
-// along the tokens so that the (B, H, L) outputs are stored in whole rows.
-constexpr int kTileTok = 64;
+// A tile of up to 64 consecutive tokens of one batch row per workgroup (a.tile, a
+// power of two chosen so the staging fits in LDS).  The workgroup first stages the
+// tile's [B, C, dd_dt, dd_A, trap, angles] segments and the two norm scales into LDS,
+// with every load issued before any is used (16-byte chunks when the rows allow).
+// Then one wave per token normalises B and C and stores the angle rates, and lanes
+// along the tokens compute the per-head decay, so that the (B, H, L) outputs are
+// stored in whole rows.  Only the copies of z and x (the fallback route) read proj
+// directly.
+constexpr int kStageUnroll = 12;
 
 template <typename T>
 __global__ __launch_bounds__(kLayerThreads)
 void layer_pre_kernel(LayerPreArgs a) {
+  extern __shared__ __align__(16) unsigned char pre_smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tiles = (a.L + kTileTok - 1) / kTileTok;
-  const int b = blockIdx.x / tiles, l0 = (blockIdx.x % tiles) * kTileTok;
-  const int nt = min(kTileTok, a.L - l0);
+  const int TT = a.tile;
+  const int tiles = (a.L + TT - 1) / TT;
+  const int b = blockIdx.x / tiles, l0 = (blockIdx.x % tiles) * TT;
+  const int nt = min(TT, a.L - l0);
   const int DI = a.H * a.P, N = a.N, H = a.H, R = a.R;
-  const int dproj = 2 * DI + 2 * N + 3 * H + R;
+  const int seg = 2 * N + 3 * H + R;                   // staged elements per token
+  const int dproj = 2 * DI + seg;
   const T* proj = reinterpret_cast<const T*>(a.proj);
+  const long tok0 = (long)b * a.L + l0;
+  const T* src0 = proj + tok0 * dproj + 2 * DI;         // the tile's first segment
+  T* sseg = reinterpret_cast<T*>(pre_smem);             // [TT][seg]
+  float* sscale = reinterpret_cast<float*>(pre_smem + (((size_t)TT * seg * sizeof(T) + 15) & ~(size_t)15));  // [2][N]
+
+  if (a.vec) {    // rows, the segment offset and its length are multiples of 16 bytes
+    constexpr int E = 16 / sizeof(T);
+    const int cpt = seg / E, total = nt * cpt;
+    for (int i0 = tid; i0 < total; i0 += kLayerThreads * kStageUnroll) {
+      uint4 r[kStageUnroll];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int i = i0 + u * kLayerThreads;
+        const int j = i / cpt, c = i - j * cpt;
+        r[u] = i < total ? *reinterpret_cast<const uint4*>(src0 + (long)j * dproj + c * E) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int i = i0 + u * kLayerThreads;
+        if (i < total) reinterpret_cast<uint4*>(sseg)[i] = r[u];      // element j * seg + c * E
+      }
+    }
+  } else {
+    const int total = nt * seg;
+    for (int i = tid; i < total; i += kLayerThreads) {
+      const int j = i / seg, e = i - j * seg;
+      sseg[i] = src0[(long)j * dproj + e];
+    }
+  }
+  for (int n = tid; n < N; n += kLayerThreads) {
+    sscale[n] = a.b_scale[n];
+    sscale[N + n] = a.c_scale[n];
+  }
+  __syncthreads();
+
   for (int j = wave; j < nt; j += kLayerThreads / 64) {
-    const long tok = (long)b * a.L + l0 + j;
-    const T* row = proj + tok * dproj;
+    const long tok = tok0 + j;
     if (a.v) {   // null when the scan reads x and z in place from the projection
+      const T* row = proj + tok * dproj;
       wave_copy(reinterpret_cast<T*>(a.z) + tok * DI, row, DI, lane);
       wave_copy(reinterpret_cast<T*>(a.v) + tok * DI, row + DI, DI, lane);
     }
+    const T* s = sseg + j * seg;
     // BCNorm over d_state (one scale per matrix, shared over heads)
     float ssb = 0.0f, ssc = 0.0f;
     for (int n = lane; n < N; n += 64) {
-      const float xb = Elem<T>::to_f(row[2 * DI + n]), xc = Elem<T>::to_f(row[2 * DI + N + n]);
+      const float xb = Elem<T>::to_f(s[n]), xc = Elem<T>::to_f(s[N + n]);
       ssb += xb * xb;
       ssc += xc * xc;
     }
@@ -80,17 +124,16 @@ void layer_pre_kernel(LayerPreArgs a) {
     T* kq = reinterpret_cast<T*>(a.k) + tok * N;
     T* qq = reinterpret_cast<T*>(a.q) + tok * N;
     for (int n = lane; n < N; n += 64) {
-      kq[n] = Elem<T>::from_f(Elem<T>::to_f(row[2 * DI + n]) * rb * a.b_scale[n]);
-      qq[n] = Elem<T>::from_f(Elem<T>::to_f(row[2 * DI + N + n]) * rc * a.c_scale[n]);
+      kq[n] = Elem<T>::from_f(Elem<T>::to_f(s[n]) * rb * sscale[n]);
+      qq[n] = Elem<T>::from_f(Elem<T>::to_f(s[N + n]) * rc * sscale[N + n]);
     }
-    const T* ar = row + 2 * DI + 2 * N + 3 * H;
-    for (int r = lane; r < R; r += 64) a.ang[tok * R + r] = Elem<T>::to_f(ar[r]);
+    for (int r = lane; r < R; r += 64) a.ang[tok * R + r] = Elem<T>::to_f(s[2 * N + 3 * H + r]);
   }
   // per-head decay and trapezoid inputs, float32, (B, H, L): lanes along the tokens
-  for (int i = tid; i < H * kTileTok; i += kLayerThreads) {
-    const int h = i / kTileTok, j = i % kTileTok;
+  for (int i = tid; i < H * TT; i += kLayerThreads) {
+    const int h = i / TT, j = i % TT;
     if (j < nt) {
-      const T* hd = proj + ((long)b * a.L + l0 + j) * dproj + 2 * DI + 2 * N;
+      const T* hd = sseg + j * seg + 2 * N;
       const float dt = softplus(Elem<T>::to_f(hd[h]) + a.dt_bias[h]);
       const float A = fminf(-softplus(Elem<T>::to_f(hd[H + h])), -a.A_floor);
       const long o = ((long)b * H + h) * a.L + l0 + j;
@@ -151,10 +194,24 @@ void layer_post_kernel(LayerPostArgs a) {
 
 }  // namespace
 
-hipError_t layer_pre_launch(const LayerPreArgs& a, bool bf16_io, hipStream_t st) {
-  const dim3 grid((unsigned)((long)a.B * ((a.L + kTileTok - 1) / kTileTok)));
-  if (bf16_io) hipLaunchKernelGGL(layer_pre_kernel<bf16>, grid, dim3(kLayerThreads), 0, st, a);
-  else hipLaunchKernelGGL(layer_pre_kernel<float>, grid, dim3(kLayerThreads), 0, st, a);
+// LDS bytes of a tile of `tile` tokens (the layout of layer_pre_kernel).
+size_t layer_pre_lds_bytes(int tile, int seg, int N, size_t es) {
+  return (((size_t)tile * seg * es + 15) & ~(size_t)15) + 2 * (size_t)N * sizeof(float);
+}
+
+hipError_t layer_pre_launch(LayerPreArgs a, bool bf16_io, hipStream_t st) {
+  const size_t es = bf16_io ? 2 : 4;
+  const int seg = 2 * a.N + 3 * a.H + a.R;
+  const long dproj = 2L * a.H * a.P + seg;
+  a.tile = 64;
+  while (a.tile > 1 && layer_pre_lds_bytes(a.tile, seg, a.N, es) > (size_t)kLayerPreLds) a.tile /= 2;
+  if (layer_pre_lds_bytes(a.tile, seg, a.N, es) > (size_t)kLayerPreLds) return hipErrorInvalidValue;
+  a.vec = (dproj * es) % 16 == 0 && (2L * a.H * a.P * es) % 16 == 0 && (seg * es) % 16 == 0 &&
+          (reinterpret_cast<uintptr_t>(a.proj) & 15) == 0;
+  const dim3 grid((unsigned)((long)a.B * ((a.L + a.tile - 1) / a.tile)));
+  const size_t lds = layer_pre_lds_bytes(a.tile, seg, a.N, es);
+  if (bf16_io) hipLaunchKernelGGL(layer_pre_kernel<bf16>, grid, dim3(kLayerThreads), lds, st, a);
+  else hipLaunchKernelGGL(layer_pre_kernel<float>, grid, dim3(kLayerThreads), lds, st, a);
   return hipGetLastError();
 }
 

@@ -82,13 +82,18 @@ struct LayerPreArgs {
   float* ang;                              // (B, L, R)
   int B, L, H, P, N, R;
   float A_floor, eps;
+  int tile, vec;                           // set by layer_pre_launch: tokens per workgroup, 16-byte staging
 };
+// Largest LDS staging of one token's [B, C, dd_dt, dd_A, trap, angles] plus the norm
+// scales that layer_pre supports (bytes).
+constexpr int kLayerPreLds = 64 * 1024;
 struct LayerPostArgs {
   const void* y; const float* scale; void* out;   // (B, L, D), (D,), (B, L, D)
   int B, L, D;
   float eps;
 };
-hipError_t layer_pre_launch(const LayerPreArgs& a, bool bf16_io, hipStream_t st);
+hipError_t layer_pre_launch(LayerPreArgs a, bool bf16_io, hipStream_t st);
+size_t layer_pre_lds_bytes(int tile, int seg, int N, size_t es);
 hipError_t layer_post_launch(const LayerPostArgs& a, bool bf16_io, hipStream_t st);
 
 // The backbone block's norm and elementwise kernels (m3_block.hip).  `vec` is set by
