@@ -86,26 +86,29 @@ class Mamba3Layer:
                                         _ptr(Ang), B, L, nh, hd, N, R, self.A_floor, self.eps, io, st),
                        "m3_layer_pre")
 
-        # Q = C, K = B (_forward_pallas, mamba3.py:413-425); x and z read in place from proj
-        pre(None, None)
-        y = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
-        ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, nh, N, hd, R, self.chunk_size, io)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        rc = lib.m3_layer_scan(_ptr(Q), _ptr(K), _ptr(proj), self.d_in_proj, _ptr(ADT), _ptr(DT), _ptr(Trap),
-                               _ptr(Ang), _ptr(pp["C_bias"]), _ptr(pp["B_bias"]), _ptr(pp["D"]), _ptr(y),
-                               B, L, nh, N, hd, R, self.chunk_size, io, ws.data_ptr() if ws_bytes else None,
-                               ws_bytes, st)
-        self.last_scan = "in_place"
-        if rc in (_lib.M3_E_UNSUPPORTED, _lib.M3_E_ALIGN):
-            self.last_scan = "copies"
-            # rows not 16-byte multiples, or no chunked kernel: copy x and z, scan the copies
+        # Q = C, K = B (_forward_pallas, mamba3.py:413-425).  x and z are read in place
+        # from proj when its rows and the x block are 16-byte aligned and the shape has
+        # the chunked kernel (m3_layer_scan's conditions); otherwise they are copied.
+        es = proj.element_size()
+        in_place = ((self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
+                    and proj.data_ptr() % 16 == 0
+                    and lib.m3_chunk_scan_impl(io, N, hd, R, self.chunk_size) == _lib.IMPL_CHUNKED_MFMA)
+        self.last_scan = "in_place" if in_place else "copies"
+        if in_place:
+            pre(None, None)
+            y = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
+            ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, nh, N, hd, R, self.chunk_size, io)
+            ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+            _lib.check(lib.m3_layer_scan(_ptr(Q), _ptr(K), _ptr(proj), self.d_in_proj, _ptr(ADT), _ptr(DT),
+                                         _ptr(Trap), _ptr(Ang), _ptr(pp["C_bias"]), _ptr(pp["B_bias"]),
+                                         _ptr(pp["D"]), _ptr(y), B, L, nh, N, hd, R, self.chunk_size, io,
+                                         ws.data_ptr() if ws_bytes else None, ws_bytes, st), "m3_layer_scan")
+        else:
             V = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
             Z = torch.empty_like(V)
             pre(V, Z)
             y = mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, Ang, pp["C_bias"], pp["B_bias"], pp["D"], Z,
                                               chunk_size=self.chunk_size)
-        else:
-            _lib.check(rc, "m3_layer_scan")
         yn = torch.empty(B, L, self.d_inner, device=dev, dtype=dt)
         _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), B, L, self.d_inner, self.eps, io,
                                      _stream(y)), "m3_layer_post")

@@ -21,6 +21,7 @@ pytestmark = pytest.mark.gpu
     (2, 330, 256, 128, 64, True, "in_place"),   # 1336-wide bf16 rows (16-byte multiple): read in place
     (1, 1100, 64, 128, 64, True, "copies"),     # B*H small: the scan's sequence split
     (2, 150, 64, 64, 32, False, "in_place"),    # fp32: chunked kernel shapes, 412-wide rows in place
+    (1, 100, 1024, 256, 64, True, "copies"),    # d_state 256: generic scan; layer_pre tiles of 32 tokens
 ])
 def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16, path):
     import torch
