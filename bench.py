@@ -259,7 +259,40 @@ def cpu_baseline(min_seconds=10.0):
             "sample": (f"numpy float32 restatement of mamba3_ssd_chunked_jax (reference JAX not "
                        f"installed), {nseq} of the 8 sequences of the headline workload (L=4096, "
                        f"H=32, N=128, P=64, chunk 64), {spent:.1f} s of compute, "
-                       f"BLAS threads={threads}, host={len(os.sched_getaffinity(0))} cores")}
+                       f"BLAS threads={threads}, host={len(os.sched_getaffinity(0))} cores"),
+            "other": cpu_baseline_other()}
+
+
+def cpu_baseline_other(decode_seconds=4.0):
+    """The other CPU baselines of the measurement plan, on the same host: config 1
+    whole (B=2, L=1024, H=8, N=P=64, R=16, chunk 64, float32) through the scan
+    restatement, and decode config 4 through the numpy float32 rnn_step restatement
+    (mamba3.py:498-562) on 64 of its 512 batch rows, steps until decode_seconds."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import inputs as I
+    from oracle import mamba3_ref as M
+    d = I.scan_inputs(2, 1024, 8, 64, 64, 16, seed=1)
+    t0 = time.perf_counter()
+    M.mamba3_ssd_chunked_batched(d["Q"], d["K"], d["V"], d["ADT"], d["DT"], d["Trap"], d["Angles"],
+                                 d["Q_bias"], d["K_bias"], d["D"], d["Z"], chunk_size=64, dtype=np.float32)
+    c1 = time.perf_counter() - t0
+    rows, max_steps = 64, 256
+    e = I.decode_inputs(rows, 32, 128, 64, 32, 32, seed=4)
+    carry = (e["theta"], e["h"], e["k_prev"], e["v_prev"])
+    spent, steps = 0.0, 0
+    while steps < max_steps and spent < decode_seconds:
+        t = steps % 32
+        step_in = tuple(e[k][t] for k in ("x", "z", "Bt", "Ct", "adt", "dt", "trap", "ang"))
+        t0 = time.perf_counter()
+        carry, _ = M.rnn_step(carry, step_in, e["B_bias"], e["C_bias"], e["D"], dtype=np.float32)
+        spent += time.perf_counter() - t0
+        steps += 1
+    return {"config1_scan": {"value": round(2 * 1024 / c1, 1), "unit": "tokens/s",
+                             "sample": f"config 1 whole (2 x 1024 tokens, 8 heads), {c1:.2f} s"},
+            "decode_config4": {"value": round(rows * steps / spent, 1), "unit": "tokens/s",
+                               "sample": (f"{rows} of the 512 batch rows, {steps} steps of rnn_step "
+                                          f"(32 heads, N=128, P=64), {spent:.1f} s")}}
 
 
 def load_traffic():
