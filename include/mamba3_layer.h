@@ -105,6 +105,20 @@ int m3_block_gelu(const void* x, void* out, int B, int L, int D, int io_dtype, v
 int m3_block_act(const void* y, const void* h1, const void* h2, const float* skip, float* out, int B, int L, int D,
                  int activation, int io_dtype, void* stream);
 
+/*
+ * m3_block_act followed by a LayerNorm of its result, in one pass over each row:
+ * s = skip + act (stored to `out` (float32) when out is not NULL), then
+ * ln_out = LayerNorm(s; scale, bias, eps) in ln_dtype.  Two uses:
+ *   prenorm:  out = the next residual, ln_out = the next block's normalised mixer
+ *             input (its scale and bias, ln_dtype the compute dtype);
+ *   postnorm: out = NULL, ln_out = this block's LayerNorm of the sum in float32,
+ *             the residual stream itself (layers.py:149-151).
+ * ln_out must not alias skip or out; out may be skip.
+ */
+int m3_block_act_norm(const void* y, const void* h1, const void* h2, const float* skip, float* out,
+                      const float* scale, const float* bias, void* ln_out, int B, int L, int D, float eps,
+                      int activation, int io_dtype, int ln_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

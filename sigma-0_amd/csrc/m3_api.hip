@@ -401,6 +401,33 @@ int m3_block_norm(const float* x, const float* scale, const float* bias, void* o
                       "block norm");
 }
 
+int m3_block_act_norm(const void* y, const void* h1, const void* h2, const float* skip, float* out,
+                      const float* scale, const float* bias, void* ln_out, int B, int L, int D, float eps,
+                      int activation, int io_dtype, int ln_dtype, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (ln_dtype != M3_DTYPE_F32 && ln_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "ln_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", ln_dtype);
+  if (activation < M3_ACT_GELU || activation > M3_ACT_HALF_GLU2)
+    return fail(M3_E_ARG, "activation must be one of M3_ACT_GELU..M3_ACT_HALF_GLU2, got %d", activation);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!y || !skip || !scale || !bias || !ln_out) return fail(M3_E_ARG, "NULL required pointer");
+  if (activation == M3_ACT_FULL_GLU && !h1) return fail(M3_E_ARG, "full_glu needs h1 (the out1 Dense output)");
+  if (activation != M3_ACT_GELU && !h2) return fail(M3_E_ARG, "the GLU activations need h2 (the out2 Dense output)");
+  if (ln_out == (const void*)skip || (out && ln_out == (void*)out))
+    return fail(M3_E_ARG, "ln_out must not alias skip or out");
+  m3::BlockActNormArgs a{};
+  a.y = y; a.h1 = h1; a.h2 = h2; a.skip = skip; a.out = out; a.scale = scale; a.bias = bias; a.ln_out = ln_out;
+  a.rows = (long)B * L; a.D = D; a.eps = eps; a.act = activation;
+  return check_launch(m3::block_act_norm_launch(a, io_dtype == M3_DTYPE_BF16, ln_dtype == M3_DTYPE_BF16,
+                                                reinterpret_cast<hipStream_t>(stream)),
+                      "block activation + norm");
+}
+
 int m3_block_gelu(const void* x, void* out, int B, int L, int D, int io_dtype, void* stream) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);

@@ -41,6 +41,20 @@ __device__ __forceinline__ float rnd(float x) { return Elem<T>::to_f(Elem<T>::fr
 constexpr int kNormVec = 8;
 
 template <typename T>
+__device__ __forceinline__ void load4(const T* p, float f[4]);
+template <>
+__device__ __forceinline__ void load4<float>(const float* p, float f[4]) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void load4<bf16>(const bf16* p, float f[4]) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f[i] = (float)v[i];
+}
+
+template <typename T>
 __device__ __forceinline__ void store4(T* p, const float o[4]);
 template <>
 __device__ __forceinline__ void store4<float>(float* p, const float o[4]) {
@@ -175,6 +189,90 @@ void block_act_kernel(BlockEltArgs a) {
   }
 }
 
+// The epilogue and a LayerNorm of its result in one pass, one wave per row:
+// s = skip + act (float32, stored to `out` when given), then LayerNorm(s) with
+// (scale, bias) to `ln_out` in U.  The vector path (a.vec: D a multiple of 4, at most
+// 64 * 4 * kNormVec, 16-byte rows) keeps the row in registers; the scalar path
+// recomputes s in each of its three passes, so it needs no scratch.
+template <typename T, typename U>
+__global__ __launch_bounds__(kBlockThreads)
+void block_act_norm_kernel(BlockActNormArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long row = (long)blockIdx.x * (kBlockThreads / 64) + wave;
+  if (row >= a.rows) return;                           // whole waves only: no barrier below
+  const int D = a.D, act = a.act;
+  const long base = row * D;
+  const T* y = reinterpret_cast<const T*>(a.y) + base;
+  const T* h1 = a.h1 ? reinterpret_cast<const T*>(a.h1) + base : nullptr;
+  const T* h2 = a.h2 ? reinterpret_cast<const T*>(a.h2) + base : nullptr;
+  const float* skip = a.skip + base;
+  float* out = a.out ? a.out + base : nullptr;
+  U* lo = reinterpret_cast<U*>(a.ln_out) + base;
+  const float inv_d = 1.0f / (float)D;
+  auto value = [&](int i) {
+    const float f1 = act == M3_ACT_FULL_GLU ? Elem<T>::to_f(h1[i]) : 0.0f;
+    const float f2 = act != M3_ACT_GELU ? Elem<T>::to_f(h2[i]) : 0.0f;
+    return skip[i] + block_act<T>(act, Elem<T>::to_f(y[i]), f1, f2);
+  };
+  if (a.vec) {
+    const int n4 = D / 4;
+    float4 v[kNormVec];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+      const int i = lane + 64 * k;
+      v[k] = make_float4(0, 0, 0, 0);
+      if (i < n4) {
+        const float4 sk = reinterpret_cast<const float4*>(skip)[i];
+        float fy[4], f1[4] = {}, f2[4] = {};
+        load4(y + 4 * i, fy);
+        if (act == M3_ACT_FULL_GLU) load4(h1 + 4 * i, f1);
+        if (act != M3_ACT_GELU) load4(h2 + 4 * i, f2);
+        v[k] = make_float4(sk.x + block_act<T>(act, fy[0], f1[0], f2[0]), sk.y + block_act<T>(act, fy[1], f1[1], f2[1]),
+                           sk.z + block_act<T>(act, fy[2], f1[2], f2[2]), sk.w + block_act<T>(act, fy[3], f1[3], f2[3]));
+        if (out) reinterpret_cast<float4*>(out)[i] = v[k];
+      }
+      s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    }
+    const float mean = group_sum<64>(s) * inv_d;
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+      if (lane + 64 * k < n4) {
+        const float dx = v[k].x - mean, dy = v[k].y - mean, dz = v[k].z - mean, dw = v[k].w - mean;
+        ss += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
+    }
+    const float rs = rsqrtf(group_sum<64>(ss) * inv_d + a.eps);
+#pragma unroll
+    for (int k = 0; k < kNormVec; ++k) {
+      const int i = lane + 64 * k;
+      if (i < n4) {
+        const float4 sc = reinterpret_cast<const float4*>(a.scale)[i];
+        const float4 bi = reinterpret_cast<const float4*>(a.bias)[i];
+        const float o[4] = {fmaf((v[k].x - mean) * rs, sc.x, bi.x), fmaf((v[k].y - mean) * rs, sc.y, bi.y),
+                            fmaf((v[k].z - mean) * rs, sc.z, bi.z), fmaf((v[k].w - mean) * rs, sc.w, bi.w)};
+        store4<U>(lo + 4 * i, o);
+      }
+    }
+  } else {     // three passes over the row, each recomputing s (no scratch)
+    float s = 0.0f;
+    for (int i = lane; i < D; i += 64) {
+      const float x = value(i);
+      if (out) out[i] = x;
+      s += x;
+    }
+    const float mean = group_sum<64>(s) * inv_d;
+    float ss = 0.0f;
+    for (int i = lane; i < D; i += 64) {
+      const float dx = value(i) - mean;
+      ss += dx * dx;
+    }
+    const float rs = rsqrtf(group_sum<64>(ss) * inv_d + a.eps);
+    for (int i = lane; i < D; i += 64) lo[i] = Elem<U>::from_f(fmaf((value(i) - mean) * rs, a.scale[i], a.bias[i]));
+  }
+}
+
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -184,6 +282,19 @@ hipError_t block_norm_launch(BlockNormArgs a, bool bf16_out, hipStream_t st) {
   const dim3 grid((unsigned)((a.rows + kBlockThreads / 64 - 1) / (kBlockThreads / 64)));
   if (bf16_out) hipLaunchKernelGGL(block_norm_kernel<bf16>, grid, dim3(kBlockThreads), 0, st, a);
   else hipLaunchKernelGGL(block_norm_kernel<float>, grid, dim3(kBlockThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t block_act_norm_launch(BlockActNormArgs a, bool bf16_io, bool bf16_ln, hipStream_t st) {
+  const size_t es = bf16_io ? 2 : 4;
+  a.vec = a.D % 4 == 0 && a.D <= 64 * 4 * kNormVec && (a.D * es) % 8 == 0 && al16(a.skip) && al16(a.scale) &&
+          al16(a.bias) && (!a.out || al16(a.out)) && al16(a.ln_out) && al16(a.y) && (!a.h1 || al16(a.h1)) &&
+          (!a.h2 || al16(a.h2));
+  const dim3 grid((unsigned)((a.rows + kBlockThreads / 64 - 1) / (kBlockThreads / 64)));
+  if (bf16_io && bf16_ln) hipLaunchKernelGGL((block_act_norm_kernel<bf16, bf16>), grid, dim3(kBlockThreads), 0, st, a);
+  else if (bf16_io) hipLaunchKernelGGL((block_act_norm_kernel<bf16, float>), grid, dim3(kBlockThreads), 0, st, a);
+  else if (bf16_ln) hipLaunchKernelGGL((block_act_norm_kernel<float, bf16>), grid, dim3(kBlockThreads), 0, st, a);
+  else hipLaunchKernelGGL((block_act_norm_kernel<float, float>), grid, dim3(kBlockThreads), 0, st, a);
   return hipGetLastError();
 }
 

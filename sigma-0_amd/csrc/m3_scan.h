@@ -110,7 +110,17 @@ struct BlockEltArgs {
   int act;   // M3_ACT_*
   int vec;
 };
+struct BlockActNormArgs {
+  const void* y; const void* h1; const void* h2; const float* skip;   // (rows, D)
+  float* out;                                                         // (rows, D) float32 or null
+  const float* scale; const float* bias; void* ln_out;                // (D,), (D,), (rows, D)
+  long rows; int D;
+  float eps;
+  int act;   // M3_ACT_*
+  int vec;
+};
 hipError_t block_norm_launch(BlockNormArgs a, bool bf16_out, hipStream_t st);
+hipError_t block_act_norm_launch(BlockActNormArgs a, bool bf16_io, bool bf16_ln, hipStream_t st);
 hipError_t block_elt_launch(BlockEltArgs a, bool gelu_only, bool bf16_io, hipStream_t st);
 
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.

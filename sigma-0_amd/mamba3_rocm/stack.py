@@ -7,8 +7,9 @@ half_glu1, half_glu2, with the block's out1/out2 Dense layers in the compute
 dtype); x = skip + x; LayerNorm if postnorm.  flax defaults: LayerNorm eps 1e-6,
 gelu with the tanh approximation.  The mixer and the block's elementwise work run
 the hand-written kernels: m3_block_norm (LayerNorm from the float32 residual
-straight to the mixer's dtype), m3_block_gelu (the Dense layers' input) and
-m3_block_act (the gate and the residual add in one pass).  The Dense layers are
+straight to the mixer's dtype, for the first block), m3_block_gelu (the Dense
+layers' input) and m3_block_act_norm (the gate, the residual add and the next
+block's LayerNorm in one pass; postnorm: this block's).  The Dense layers are
 library GEMMs; the embedding lookup is torch's gather.
 ``logits`` adds the LOB models' per-token head (mode "none"): the decoder Dense
 on the float32 features, then log_softmax in float32 (lob_seq_model.py:530-542).
@@ -53,22 +54,14 @@ class Mamba3Stack:
             self.decoder_w = params["decoder_w"].float().t().contiguous()
             self.decoder_b = params["decoder_b"].float().contiguous()
 
-    def _block(self, b, x):
-        """SequenceLayer.__call__ (layers.py:108-160) on the float32 residual x (B, L, D)."""
+    def _block(self, b, x, xin, nxt):
+        """SequenceLayer.__call__ (layers.py:108-160) on the float32 residual x (B, L, D).
+        Prenorm: xin is this block's normalised input, made by the previous block's
+        epilogue (or by m3_block_norm for the first block), and the epilogue makes the
+        next block's (nxt) the same way.  Returns (residual, next block's input)."""
         lib, io, st = _lib.load(), _IO[self.dtype], _stream(x)
         Bn, L, D = x.shape
-
-        def norm(src, out, dtype):
-            _lib.check(lib.m3_block_norm(_ptr(src), _ptr(b["ln_scale"]), _ptr(b["ln_bias"]), _ptr(out), Bn, L, D,
-                                         1e-6, dtype, st), "m3_block_norm")
-
-        skip = x
-        if self.prenorm:
-            xin = torch.empty(Bn, L, D, device=x.device, dtype=self.dtype)
-            norm(x, xin, io)
-        else:
-            xin = x
-        y = b["mixer"](xin).contiguous()                    # compute dtype
+        y = b["mixer"](xin if self.prenorm else x).contiguous()     # compute dtype
         h1 = h2 = None
         if self.activation != "gelu":
             g = torch.empty_like(y)
@@ -76,17 +69,36 @@ class Mamba3Stack:
             h2 = F.linear(g, b["out2_w"], b["out2_b"])
             if self.activation == "full_glu":
                 h1 = F.linear(g, b["out1_w"], b["out1_b"])
+        act = _ACT[self.activation]
         out = torch.empty_like(x)
-        _lib.check(lib.m3_block_act(_ptr(y), _ptr(h1), _ptr(h2), _ptr(skip), _ptr(out), Bn, L, D,
-                                    _ACT[self.activation], io, st), "m3_block_act")
-        if not self.prenorm:
-            norm(out, out, _lib.DTYPE_F32)
-        return out
+        if self.prenorm and nxt is None:
+            _lib.check(lib.m3_block_act(_ptr(y), _ptr(h1), _ptr(h2), _ptr(x), _ptr(out), Bn, L, D, act, io, st),
+                       "m3_block_act")
+            return out, None
+        if self.prenorm:         # residual and the next block's LayerNorm in one pass
+            xn = torch.empty(Bn, L, D, device=x.device, dtype=self.dtype)
+            _lib.check(lib.m3_block_act_norm(_ptr(y), _ptr(h1), _ptr(h2), _ptr(x), _ptr(out), _ptr(nxt["ln_scale"]),
+                                             _ptr(nxt["ln_bias"]), _ptr(xn), Bn, L, D, 1e-6, act, io, io, st),
+                       "m3_block_act_norm")
+            return out, xn
+        # postnorm: the LayerNorm of skip + act is the residual itself
+        _lib.check(lib.m3_block_act_norm(_ptr(y), _ptr(h1), _ptr(h2), _ptr(x), None, _ptr(b["ln_scale"]),
+                                         _ptr(b["ln_bias"]), _ptr(out), Bn, L, D, 1e-6, act, io, _lib.DTYPE_F32, st),
+                   "m3_block_act_norm")
+        return out, None
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
         x = self.embed[ids].contiguous()
-        for b in self.blocks:
-            x = self._block(b, x)
+        xin = None
+        if self.prenorm and self.blocks:
+            b0 = self.blocks[0]
+            xin = torch.empty(*x.shape, device=x.device, dtype=self.dtype)
+            _lib.check(_lib.load().m3_block_norm(_ptr(x), _ptr(b0["ln_scale"]), _ptr(b0["ln_bias"]), _ptr(xin),
+                                                 x.shape[0], x.shape[1], x.shape[2], 1e-6, _IO[self.dtype],
+                                                 _stream(x)), "m3_block_norm")
+        for i, b in enumerate(self.blocks):
+            nxt = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
+            x, xin = self._block(b, x, xin, nxt)
         return x
 
     __call__ = forward

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
                             "m3_chunk_scan_bwd_shared", "m3_decode_step", "m3_layer_pre",
                             "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu",
-                            "m3_block_act"])
+                            "m3_block_act", "m3_block_act_norm"])
     for n in names:
         assert hasattr(lib, n), n
     from mamba3_rocm import _lib
@@ -294,3 +294,9 @@ def test_block_entry_points_validate(lib):
     assert lib.m3_block_act(fake, None, None, fake, fake, 2, 8, 64, _lib.M3_ACT_HALF_GLU2, bf, None) == _lib.M3_E_ARG
     assert lib.m3_block_act(fake, None, None, None, fake, 2, 8, 64, _lib.M3_ACT_GELU, bf, None) == _lib.M3_E_ARG
     assert lib.m3_block_act(fake, None, None, fake, fake, 0, 8, 64, _lib.M3_ACT_GELU, bf, None) == _lib.M3_OK
+    an = lambda *a: lib.m3_block_act_norm(*a)   # noqa: E731
+    assert an(fake, None, fake, fake, fake, fake, fake, fake, 2, 8, 64, 1e-6, 2, bf, 7, None) == _lib.M3_E_ARG
+    assert an(fake, None, fake, fake, fake, None, fake, fake, 2, 8, 64, 1e-6, 2, bf, bf, None) == _lib.M3_E_ARG
+    assert an(fake, None, fake, 4096, None, fake, fake, 4096, 2, 8, 64, 1e-6, 2, bf, bf, None) == _lib.M3_E_ARG
+    assert b"alias" in lib.m3_last_error()
+    assert an(fake, None, fake, fake, None, fake, fake, 4096, 0, 8, 64, 1e-6, 2, bf, bf, None) == _lib.M3_OK

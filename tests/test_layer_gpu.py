@@ -166,3 +166,28 @@ def test_block_kernels_match_torch_fp32(B, L, D, bf16):
         tol = v.abs() * (2 ** -7 * 1.01 if bf16 else 2e-6) + want_out.abs() * 2 ** -23 + 1e-30
         bad = ((out.double() - want_out).abs() > tol).sum().item()
         assert bad == 0, f"act {act}: {bad} elements outside tolerance"
+        # the fused epilogue + LayerNorm: the same sum, bit for bit, then the norm of it
+        # (prenorm: sum kept, norm in the compute dtype; postnorm: only the float32 norm)
+        ln_want = F.layer_norm(out.double(), (D,), sc.double(), bi.double(), eps=1e-6)
+        out2 = torch.empty_like(skip)
+        lno = torch.empty(B, L, D, device="cuda", dtype=dt)
+        _lib.check(lib.m3_block_act_norm(y.data_ptr(), h1.data_ptr(), h2.data_ptr(), skip.data_ptr(), out2.data_ptr(),
+                                         sc.data_ptr(), bi.data_ptr(), lno.data_ptr(), B, L, D, 1e-6, act, io, io,
+                                         st), "m3_block_act_norm")
+        if bf16:   # the rounding to bf16 before the add leaves one way to evaluate the sum
+            assert torch.equal(out2, out), f"act {act}: fused sum differs from m3_block_act"
+        else:      # float32: the compiler may fuse skip + x * rcp(..) into one FMA on one path; the
+            # difference is the product's rounding, half an ulp of |act| <= |out| + |skip|
+            tol = (2 * out.abs() + skip.abs()) * 2 ** -23 + 1e-30
+            assert ((out2 - out).abs() <= tol).all(), f"act {act}: fused sum"
+        got = lno.double()
+        if bf16:   # near-zero normalised values carry the float32 mean's rounding: 1e-6 absolute floor
+            bad = ((got - r(ln_want)).abs() > r(ln_want).abs() * 2 ** -7 * 1.01 + 1e-6).sum().item()
+            assert bad == 0, f"act {act}: {bad} normalised elements outside tolerance"
+        else:
+            assert ((got - ln_want).abs().max() / ln_want.abs().max()).item() <= 2e-6
+        lnf = torch.empty_like(skip)
+        _lib.check(lib.m3_block_act_norm(y.data_ptr(), h1.data_ptr(), h2.data_ptr(), skip.data_ptr(), None,
+                                         sc.data_ptr(), bi.data_ptr(), lnf.data_ptr(), B, L, D, 1e-6, act, io,
+                                         _lib.DTYPE_F32, st), "m3_block_act_norm postnorm")
+        assert ((lnf.double() - ln_want).abs().max() / ln_want.abs().max()).item() <= 2e-6
