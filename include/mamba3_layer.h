@@ -119,6 +119,13 @@ int m3_block_act_norm(const void* y, const void* h1, const void* h2, const float
                       const float* scale, const float* bias, void* ln_out, int B, int L, int D, float eps,
                       int activation, int io_dtype, int ln_dtype, void* stream);
 
+/*
+ * The per-token head's nn.log_softmax over the vocabulary, float32
+ * (lob_seq_model.py:542): out = x - max - log(sum(exp(x - max))) per row of
+ * x (B, L, V).  out may be x.
+ */
+int m3_log_softmax(const float* x, float* out, int B, int L, int V, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

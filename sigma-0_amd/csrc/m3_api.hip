@@ -428,6 +428,17 @@ int m3_block_act_norm(const void* y, const void* h1, const void* h2, const float
                       "block activation + norm");
 }
 
+int m3_log_softmax(const float* x, float* out, int B, int L, int V, void* stream) {
+  if (B < 0 || L < 0 || V <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d V=%d)", B, L, V);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!x || !out) return fail(M3_E_ARG, "NULL required pointer");
+  return check_launch(m3::log_softmax_launch(x, out, (long)B * L, V, reinterpret_cast<hipStream_t>(stream)),
+                      "log_softmax");
+}
+
 int m3_block_gelu(const void* x, void* out, int B, int L, int D, int io_dtype, void* stream) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);

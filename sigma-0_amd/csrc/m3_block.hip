@@ -273,6 +273,55 @@ void block_act_norm_kernel(BlockActNormArgs a) {
   }
 }
 
+// log_softmax over each row of V float32 logits, one wave per row: x - max -
+// log(sum(exp(x - max))).  The vector path (V a multiple of 4, at most 64 * 4 *
+// kSoftmaxVec, 16-byte rows) reads the row once into registers; otherwise three
+// passes over memory.  out may be x.
+constexpr int kSoftmaxVec = 16;
+
+__global__ __launch_bounds__(kBlockThreads)
+void log_softmax_kernel(const float* x, float* out, long rows, int V, int vec) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long row = (long)blockIdx.x * (kBlockThreads / 64) + wave;
+  if (row >= rows) return;                             // whole waves only: no barrier below
+  const float* xr = x + row * V;
+  float* orow = out + row * V;
+  auto wave_max = [](float m) {
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    return m;
+  };
+  if (vec) {
+    const int n4 = V / 4;
+    float4 v[kSoftmaxVec];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kSoftmaxVec; ++k) {
+      const int i = lane + 64 * k;
+      v[k] = i < n4 ? reinterpret_cast<const float4*>(xr)[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kSoftmaxVec; ++k)
+      if (lane + 64 * k < n4) s += (expf(v[k].x - m) + expf(v[k].y - m)) + (expf(v[k].z - m) + expf(v[k].w - m));
+    const float lse = m + logf(group_sum<64>(s));
+#pragma unroll
+    for (int k = 0; k < kSoftmaxVec; ++k) {
+      const int i = lane + 64 * k;
+      if (i < n4) reinterpret_cast<float4*>(orow)[i] = make_float4(v[k].x - lse, v[k].y - lse, v[k].z - lse, v[k].w - lse);
+    }
+  } else {
+    float m = -INFINITY;
+    for (int i = lane; i < V; i += 64) m = fmaxf(m, xr[i]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int i = lane; i < V; i += 64) s += expf(xr[i] - m);
+    const float lse = m + logf(group_sum<64>(s));
+    for (int i = lane; i < V; i += 64) orow[i] = xr[i] - lse;
+  }
+}
+
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -295,6 +344,13 @@ hipError_t block_act_norm_launch(BlockActNormArgs a, bool bf16_io, bool bf16_ln,
   else if (bf16_io) hipLaunchKernelGGL((block_act_norm_kernel<bf16, float>), grid, dim3(kBlockThreads), 0, st, a);
   else if (bf16_ln) hipLaunchKernelGGL((block_act_norm_kernel<float, bf16>), grid, dim3(kBlockThreads), 0, st, a);
   else hipLaunchKernelGGL((block_act_norm_kernel<float, float>), grid, dim3(kBlockThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t log_softmax_launch(const float* x, float* out, long rows, int V, hipStream_t st) {
+  const int vec = V % 4 == 0 && V <= 64 * 4 * kSoftmaxVec && al16(x) && al16(out);
+  const dim3 grid((unsigned)((rows + kBlockThreads / 64 - 1) / (kBlockThreads / 64)));
+  hipLaunchKernelGGL(log_softmax_kernel, grid, dim3(kBlockThreads), 0, st, x, out, rows, V, vec);
   return hipGetLastError();
 }
 

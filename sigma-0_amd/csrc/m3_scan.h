@@ -121,6 +121,7 @@ struct BlockActNormArgs {
 };
 hipError_t block_norm_launch(BlockNormArgs a, bool bf16_out, hipStream_t st);
 hipError_t block_act_norm_launch(BlockActNormArgs a, bool bf16_io, bool bf16_ln, hipStream_t st);
+hipError_t log_softmax_launch(const float* x, float* out, long rows, int V, hipStream_t st);
 hipError_t block_elt_launch(BlockEltArgs a, bool gelu_only, bool bf16_io, hipStream_t st);
 
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.

@@ -27,7 +27,8 @@ EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_sc
            "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes", "m3_chunk_scan_fwd_ws",
            "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd", "m3_chunk_scan_fwd_shared",
            "m3_chunk_scan_bwd_shared_ws_bytes", "m3_chunk_scan_bwd_shared", "m3_decode_step",
-           "m3_layer_pre", "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu", "m3_block_act", "m3_block_act_norm")
+           "m3_layer_pre", "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu", "m3_block_act", "m3_block_act_norm",
+           "m3_log_softmax")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -51,6 +52,7 @@ _SIGS = {
     "m3_block_gelu": ([_P] * 2 + [_I] * 4 + [_P], _I),
     "m3_block_act": ([_P] * 5 + [_I] * 5 + [_P], _I),
     "m3_block_act_norm": ([_P] * 8 + [_I] * 3 + [ctypes.c_float] + [_I] * 3 + [_P], _I),
+    "m3_log_softmax": ([_P] * 2 + [_I] * 3 + [_P], _I),
     "m3_decode_step": ([_P] * 16 + [_I] * 9 + [_P], _I),
 }
 

@@ -12,7 +12,8 @@ layers' input) and m3_block_act_norm (the gate, the residual add and the next
 block's LayerNorm in one pass; postnorm: this block's).  The Dense layers are
 library GEMMs; the embedding lookup is torch's gather.
 ``logits`` adds the LOB models' per-token head (mode "none"): the decoder Dense
-on the float32 features, then log_softmax in float32 (lob_seq_model.py:530-542).
+on the float32 features (a library GEMM), then log_softmax in float32 with
+m3_log_softmax (lob_seq_model.py:530-542).
 Inference only (dropout is the identity).
 """
 from __future__ import annotations
@@ -107,7 +108,10 @@ class Mamba3Stack:
         """Per-token log-probabilities (B, L, vocab), float32."""
         if self.decoder_w is None:
             raise ValueError("logits needs decoder_w and decoder_b in the parameters")
-        return torch.log_softmax(F.linear(self.forward(ids), self.decoder_w, self.decoder_b), dim=-1)
+        z = F.linear(self.forward(ids), self.decoder_w, self.decoder_b).contiguous()
+        _lib.check(_lib.load().m3_log_softmax(_ptr(z), _ptr(z), z.shape[0], z.shape[1], z.shape[2], _stream(z)),
+                   "m3_log_softmax")
+        return z
 
 
 def init_params(vocab: int, d_model: int, n_layers: int, seed: int, device, d_state: int = 128,

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
                             "m3_chunk_scan_bwd_shared", "m3_decode_step", "m3_layer_pre",
                             "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu",
-                            "m3_block_act", "m3_block_act_norm"])
+                            "m3_block_act", "m3_block_act_norm", "m3_log_softmax"])
     for n in names:
         assert hasattr(lib, n), n
     from mamba3_rocm import _lib

@@ -191,3 +191,9 @@ def test_block_kernels_match_torch_fp32(B, L, D, bf16):
                                          sc.data_ptr(), bi.data_ptr(), lnf.data_ptr(), B, L, D, 1e-6, act, io,
                                          _lib.DTYPE_F32, st), "m3_block_act_norm postnorm")
         assert ((lnf.double() - ln_want).abs().max() / ln_want.abs().max()).item() <= 2e-6
+
+    # the head's log_softmax over rows of width D (in place), against float64
+    logits = torch.randn(B, L, D, device="cuda", generator=g) * 4
+    want = torch.log_softmax(logits.double(), dim=-1)
+    _lib.check(lib.m3_log_softmax(logits.data_ptr(), logits.data_ptr(), B, L, D, st), "m3_log_softmax")
+    assert ((logits.double() - want).abs() <= 1e-6 * (1 + want.abs())).all(), "log_softmax"
