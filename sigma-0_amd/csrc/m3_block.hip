@@ -193,7 +193,7 @@ void block_act_kernel(BlockEltArgs a) {
 // s = skip + act (float32, stored to `out` when given), then LayerNorm(s) with
 // (scale, bias) to `ln_out` in U.  The vector path (a.vec: D a multiple of 4, at most
 // 64 * 4 * kNormVec, 16-byte rows) keeps the row in registers; the scalar path
-// recomputes s in each of its three passes, so it needs no scratch.
+// re-reads s from out, or recomputes it when out is null, so it needs no scratch.
 template <typename T, typename U>
 __global__ __launch_bounds__(kBlockThreads)
 void block_act_norm_kernel(BlockActNormArgs a) {
@@ -255,7 +255,9 @@ void block_act_norm_kernel(BlockActNormArgs a) {
         store4<U>(lo + 4 * i, o);
       }
     }
-  } else {     // three passes over the row, each recomputing s (no scratch)
+  } else {     // three passes over the row: s is stored to out when given (each lane
+               // re-reads only its own elements, also when out is skip), else recomputed
+    auto sum_at = [&](int i) { return out ? out[i] : value(i); };
     float s = 0.0f;
     for (int i = lane; i < D; i += 64) {
       const float x = value(i);
@@ -265,11 +267,11 @@ void block_act_norm_kernel(BlockActNormArgs a) {
     const float mean = group_sum<64>(s) * inv_d;
     float ss = 0.0f;
     for (int i = lane; i < D; i += 64) {
-      const float dx = value(i) - mean;
+      const float dx = sum_at(i) - mean;
       ss += dx * dx;
     }
     const float rs = rsqrtf(group_sum<64>(ss) * inv_d + a.eps);
-    for (int i = lane; i < D; i += 64) lo[i] = Elem<U>::from_f(fmaf((value(i) - mean) * rs, a.scale[i], a.bias[i]));
+    for (int i = lane; i < D; i += 64) lo[i] = Elem<U>::from_f(fmaf((sum_at(i) - mean) * rs, a.scale[i], a.bias[i]));
   }
 }
 

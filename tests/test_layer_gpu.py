@@ -186,6 +186,12 @@ def test_block_kernels_match_torch_fp32(B, L, D, bf16):
             assert bad == 0, f"act {act}: {bad} normalised elements outside tolerance"
         else:
             assert ((got - ln_want).abs().max() / ln_want.abs().max()).item() <= 2e-6
+        # in place on the residual (out = skip), as the header allows
+        sk2, ln2 = skip.clone(), torch.empty_like(lno)
+        _lib.check(lib.m3_block_act_norm(y.data_ptr(), h1.data_ptr(), h2.data_ptr(), sk2.data_ptr(), sk2.data_ptr(),
+                                         sc.data_ptr(), bi.data_ptr(), ln2.data_ptr(), B, L, D, 1e-6, act, io, io,
+                                         st), "m3_block_act_norm in place")
+        assert torch.equal(sk2, out2) and torch.equal(ln2, lno), f"act {act}: in-place act_norm"
         lnf = torch.empty_like(skip)
         _lib.check(lib.m3_block_act_norm(y.data_ptr(), h1.data_ptr(), h2.data_ptr(), skip.data_ptr(), None,
                                          sc.data_ptr(), bi.data_ptr(), lnf.data_ptr(), B, L, D, 1e-6, act, io,
