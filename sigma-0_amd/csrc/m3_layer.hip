@@ -76,12 +76,17 @@ void layer_pre_kernel(LayerPreArgs a) {
   if (a.vec) {    // rows, the segment offset and its length are multiples of 16 bytes
     constexpr int E = 16 / sizeof(T);
     const int cpt = seg / E, total = nt * cpt;
+    const float rcpt = 1.0f / (float)cpt;
     for (int i0 = tid; i0 < total; i0 += kLayerThreads * kStageUnroll) {
       uint4 r[kStageUnroll];
 #pragma unroll
       for (int u = 0; u < kStageUnroll; ++u) {
         const int i = i0 + u * kLayerThreads;
-        const int j = i / cpt, c = i - j * cpt;
+        // j = i / cpt without an integer division: i < 2^24, so the float quotient is
+        // off by at most one, and the remainder's sign or size corrects it
+        int j = (int)((float)i * rcpt), c = i - j * cpt;
+        if (c < 0) { --j; c += cpt; }
+        else if (c >= cpt) { ++j; c -= cpt; }
         r[u] = i < total ? *reinterpret_cast<const uint4*>(src0 + (long)j * dproj + c * E) : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
@@ -130,8 +135,9 @@ void layer_pre_kernel(LayerPreArgs a) {
     for (int r = lane; r < R; r += 64) a.ang[tok * R + r] = Elem<T>::to_f(s[2 * N + 3 * H + r]);
   }
   // per-head decay and trapezoid inputs, float32, (B, H, L): lanes along the tokens
+  const int tt_shift = __builtin_ctz(TT);               // TT is a power of two
   for (int i = tid; i < H * TT; i += kLayerThreads) {
-    const int h = i / TT, j = i % TT;
+    const int h = i >> tt_shift, j = i & (TT - 1);
     if (j < nt) {
       const T* hd = sseg + j * seg + 2 * N;
       const float dt = softplus(Elem<T>::to_f(hd[h]) + a.dt_bias[h]);
