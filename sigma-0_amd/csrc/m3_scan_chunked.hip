@@ -4,30 +4,34 @@
 // src/base_model/models/mamba3_jax.py:327-419) in one kernel:
 //   phase 1  per-chunk decay prefix (wave64 scan), rotation-angle prefix
 //            (wave64 scans over the chunk, carried across chunks and range
-//            reduced mod 2pi), trapezoid weights, biases, QK-dot skip, rope,
-//            key scaling                                        (:236-324)
-//   phase 3  S^T = K_s Q_r^T on MFMA, causal decay mask in registers, then
-//            Y_diag = M V on MFMA straight from the S^T accumulators (:371-393)
-//   phase 4-6 Y_off = e^{A_cum} (Q_r h^T) on MFMA with h taken straight from
-//            the fp32 state accumulators (the row scale applied by the gate);
-//            h <- e^{A_end} h + K_s^T (w V) (:177-233)
-//   phase 7  (Y_diag + Y_off + (D + QK) V) * silu(Z), fused into the
-//            preparation phase of the next chunk                 (:402-419)
+//            reduced mod 2pi), trapezoid weights, biases, QK-dot skip, rope
+//                                                                (:236-324)
+//   phase 3  S^T = K Q_r^T on MFMA, causal decay mask (with the keys' trapezoid
+//            scale) in registers, then Y_diag^T = V^T M^T on MFMA straight from
+//            the S^T accumulators                                 (:371-393)
+//   phase 6  Y_off^T = h Q_r^T on MFMA from the state kept in LDS  (:224-233)
+//   phase 4-5 h <- e^{A_end} h + K^T (w V) on MFMA, h in fp32 accumulators
+//                                                                (:177-222)
+//   phase 7  (Y_diag + e^{A_cum} Y_off + (D + QK) V) * silu(Z), in the registers of
+//            the wave that formed Y                               (:402-419)
 //
 // One workgroup of 12 waves per (batch, head) walks the chunks in order; the P x N
-// fp32 state never leaves the registers.  Output waves 0-3 each own a 16-row query
-// block of Y_diag (all p-tiles).  State waves 4-7 each own 16 columns of the value
-// dimension (a p-tile): h^T[:, p-tile] (all N rows) as 16x16 accumulators, Y_off of
-// that p-tile and its state update.  Auxiliary waves 8-11 take the larger share of
+// fp32 state never leaves the registers of the state waves.  Output waves 0-3 each
+// own a 16-row query block: its S^T, Y_diag, Y_off, the gate and the output store.
+// State waves 4-7 each own 16 columns of the value dimension (a p-tile):
+// h^T[:, p-tile] (all N rows) as 16x16 accumulators and its update; in the
+// preparation phase they copy the state entering the chunk into LDS (io type), where
+// the output waves read it for Y_off.  Auxiliary waves 8-11 take the larger share of
 // the preparation (the rope'd columns) and compute the next chunk's rotation angles
 // while the others run the matrix work.  A chunk is two phases with a barrier after
 // each:
-//   preparation  lane = token: biases, rope and key scale into the Q/K tiles; the gate
-//                and store of the previous chunk's Y; the direct-to-LDS loads of the
+//   preparation  lane = token: biases and rope into the Q/K tiles; the state into
+//                LDS; Z of the chunk into registers; the direct-to-LDS loads of the
 //                next chunk's Q and K
 //   matrix       the loads of the next chunk's V and of the rates and scalars of the
 //                chunk after, then the MFMA work, with V read straight from its
-//                staged rows and K^T from the K tile by transposed LDS reads
+//                staged rows and K^T from the K tile by transposed LDS reads; the
+//                gate and the output store
 // The staged inputs are double-buffered by chunk parity, so every load has a whole
 // chunk to land; every input byte is read from HBM once and the output written once.
 #include <type_traits>
@@ -50,20 +54,19 @@ struct Geo {
   static constexpr int SPT = NST / PT;                      // state waves per p-tile
   static constexpr int TS = BF ? 2 : 4;
   static constexpr int PAD = BF ? 8 : 4;
-  static constexpr int LDQ = N + PAD;                       // sQ, sK rows (elements)
-  static constexpr int LDY = P + (BF ? 8 : 2);              // sY rows (io precision)
+  static constexpr int LDQ = N + PAD;                       // sQ, sK and sH rows (elements)
   static constexpr int QG = N / 8, QGW = 2;                // Q/K 8-column groups, at most 2 per wave
   // 16-byte staging slots per row: Q/K, V, rotation rates
   static constexpr int SQ = N * TS / 16, SV = P * TS / 16, SA = R / 4 > 0 ? R / 4 : 1;
   // LDS bytes besides the Q/K staging.  The Q/K staging is double-buffered where it
   // fits; otherwise (rotation width N/2 at d_state 128) it is single-buffered and its
   // loads wait until the preparation phase has consumed it.
-  static constexpr int FIXED = 2 * CS * LDQ * TS + 2 * CS * LDY * TS + (2 * CS * SV + 2 * CS * SA) * 16 +
-                               2 * 3 * (CS + 4) * 4 + 8 * N + 2 * 6 * CS * 4 + 64;
+  static constexpr int FIXED = (2 * CS + P) * LDQ * TS + (2 * CS * SV + 2 * CS * SA) * 16 + 2 * 3 * (CS + 4) * 4 +
+                               12 * N + 2 * 6 * CS * 4 + 64;
   static constexpr bool DBQK = FIXED + 4 * CS * SQ * 16 <= 160 * 1024 - 512;
   static constexpr int NQK = DBQK ? 2 : 1;
   static_assert(CS <= 64 && LB16 <= NWY, "one token per lane, one query block per output wave");
-  static_assert(SPT >= 1 && NST % PT == 0 && LB16 % SPT == 0, "state-wave split");
+  static_assert(SPT >= 1 && NST % PT == 0, "state-wave split");
   static_assert(NAUX == 4, "12 waves");
   static_assert(QG <= 2 * NAUX + NWY + NST, "column groups per wave");
   // Q/K 8-column group k (< QGW) of a wave, or QG for none.  The first groups are the
@@ -93,12 +96,8 @@ template <typename G>
 struct __attribute__((aligned(16))) Smem {
   typedef typename std::conditional<G::BF, bf16, float>::type T;
   T q[G::CS * G::LDQ];                   // rope'd Q rows
-  T k[G::CS * G::LDQ];                   // rope'd, trapezoid-scaled K rows
-  // Y before the gate, in two parts written by plain stores: the intra-chunk part
-  // (output waves, by query block) and Q h^T (state waves, by p-tile; the gate applies
-  // its e^{A_cum} row scale)
-  alignas(16) T yd[G::CS * G::LDY];
-  alignas(16) T yo[G::CS * G::LDY];
+  T k[G::CS * G::LDQ];                   // rope'd K rows (without the trapezoid scale)
+  T h[G::P * G::LDQ];                    // the state entering the chunk, h[p][n]
   // raw inputs staged by direct-to-LDS loads, by chunk parity: 16-byte slots, row t slot
   // s stored at t * S + (s ^ (t mod S)) so that a lane-per-row read is bank-conflict free
   alignas(16) uint4 rq[G::NQK][G::CS * G::SQ];
@@ -110,16 +109,27 @@ struct __attribute__((aligned(16))) Smem {
   alignas(16) float rs[2][3][G::CS + 4];
   alignas(16) float qb[G::N];            // biases of this head
   alignas(16) float kb[G::N];
-  // per-token chunk constants, by chunk parity
+  // per-token chunk constants, by chunk parity.  The K tile holds the keys without
+  // their trapezoid scale: the scale of key s is a factor of every term key s adds (to
+  // S and to the state), so it is folded into that key's decay factors below.
   alignas(16) float ac2[2][G::CS];       // A_cum * log2(e)
-  alignas(16) float g16[2][G::CS];       // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
-  alignas(16) float expa[2][G::CS];      // e^{A_cum} (read by the gate, a chunk later)
-  alignas(16) float dg[2][G::CS];        // gamma / scale: turns the S diagonal into the QK skip weight
+  alignas(16) float g16[2][G::CS];       // scale_s e^{A_e - A_cum}, A_e = A_cum at the end of the key's 16-block
+  alignas(16) float expa[2][G::CS];      // e^{A_cum}: the row scale of Y_off
+  alignas(16) float gam[2][G::CS];       // gamma_l: the weight of the QK skip term on the S diagonal
   alignas(16) float scl[2][G::CS];       // trapezoid key scale gamma_t + dt_{t+1} (1 - sigmoid_{t+1})
-  alignas(16) float wdec[2][G::CS];      // e^{A_end - A_cum}
+  alignas(16) float wdec[2][G::CS];      // scale_s e^{A_end - A_cum}
   float dec[2];                          // e^{A_end}
   alignas(16) float fink[G::N];          // the last token's rope'd key (final carry), unscaled
 };
+
+// Four elements held as raw bits (bf16: 8 bytes, f32: 16 bytes) as floats.
+__device__ __forceinline__ void raw4_to_f(const uint2& r, float f[4]) {
+  f[0] = __uint_as_float(r.x << 16); f[1] = __uint_as_float(r.x & 0xffff0000u);
+  f[2] = __uint_as_float(r.y << 16); f[3] = __uint_as_float(r.y & 0xffff0000u);
+}
+__device__ __forceinline__ void raw4_to_f(const uint4& r, float f[4]) {
+  f[0] = __uint_as_float(r.x); f[1] = __uint_as_float(r.y); f[2] = __uint_as_float(r.z); f[3] = __uint_as_float(r.w);
+}
 
 // SO (state only): the pass that produces each segment's exit carry from a zero
 // entering carry; it skips Q, Y_diag, Y_off, the gate and the output.
@@ -183,10 +193,11 @@ void scan_chunked_kernel(ScanArgs a) {
   // rates and scalars into parity c & 1.  A wave waits while the CU's load path drains
   // the loads queued ahead of its own, so they go to waves with slack: Q/K to the
   // output waves at the end of their preparation share (single-buffered Q/K: the
-  // auxiliary waves, after the preparation barrier); V, rates and scalars to output
-  // waves 0 and 1 (the two lightest query blocks) at the start of the matrix phase.
+  // auxiliary waves, after the preparation barrier); V, rates and scalars to two state
+  // waves at the start of the matrix phase.  Every issuing wave waits for its loads
+  // before the chunk's closing barrier (the output waves before their gate).
   constexpr int kWQ0 = G::DBQK ? 0 : 8, kWQ1 = G::DBQK ? 1 : 9, kWK0 = G::DBQK ? 2 : 10, kWK1 = G::DBQK ? 3 : 11;
-  constexpr int kWV = 0, kWA = 1;
+  constexpr int kWV = 6, kWA = 7;
   auto stage_qk = [&](int c) {
     const int t0 = c * CS;
     const int valid = L - t0;
@@ -235,40 +246,8 @@ void scan_chunked_kernel(ScanArgs a) {
     }
   };
 
-  // ---- gate (phase 7): thread -> (row, 8-column group) of a chunk's Y tile
-  constexpr int GROUPS = CS * (P / 8);
-  const int erow = tid / (P / 8), egrp = tid % (P / 8);
-  const bool eact = tid < GROUPS;
-  Vec8<T> zr;                              // Z of the chunk waiting for its gate
-  zr.zero();
-  auto load_z = [&](int c) {
-    if (has_z && eact && c * CS + erow < L) zr.load(z_base + (long)(c * CS + erow) * vz_stride + 8 * egrp);
-  };
-  auto gate = [&](int c) {                 // Y of chunk c -> out
-    if (eact && c * CS + erow < L) {
-      const int off = erow * G::LDY + 8 * egrp;
-      Vec8<T> ya, yb;
-      ya.load(&sm.yd[off]);
-      yb.load(&sm.yo[off]);
-      const float ea = sm.expa[c & 1][erow];   // the e^{A_cum} row scale of Q h^T
-      float o[8], ob[8];
-      ya.to_f(o);
-      yb.to_f(ob);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] = fmaf(ob[q], ea, o[q]);
-      if (has_z) {
-        float zf[8];
-        zr.to_f(zf);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) o[q] *= silu_fast(zf[q]);
-      }
-      store8(o_base + (long)(c * CS + erow) * v_stride + 8 * egrp, o);
-    }
-  };
-
   // ---- roles: output waves own query block lb = wave (all p-tiles); state waves own
-  // p-tile pr (h^T[:, 16 pr + lane%16], all N rows, as 16x16 accumulators) and the
-  // query blocks lb = part (mod SPT) of Y_off
+  // p-tile pr (h^T[:, 16 pr + lane%16], all N rows, as 16x16 accumulators)
   const bool ywave = wave < G::NWY;
   const bool swave = wave >= G::NWY && wave < G::NWY + G::NST;   // the rest are auxiliary
   const int sw = wave - G::NWY;
@@ -307,6 +286,19 @@ void scan_chunked_kernel(ScanArgs a) {
   for (int i = tid; i < 2 * G::CS * G::SA; i += G::NT) (&sm.ra[0][0])[i] = make_uint4(0, 0, 0, 0);
   for (int i = tid; i < 2 * 3 * (G::CS + 4); i += G::NT) (&sm.rs[0][0][0])[i] = 0.0f;
 
+  // ---- Z of the chunk in the layout of an output wave's Y^T tiles: lane -> query row
+  // 16 wave + lane%16 and, per p-tile, the 4 columns 16 pt + 4 (lane/16) + 0..3
+  typedef typename std::conditional<G::BF, uint2, uint4>::type Z4;
+  Z4 zr[G::PT];
+  auto load_z = [&](int c) {
+    const int l = 16 * wave + (lane & 15);
+    if (has_z && ywave && 16 * wave < CS && c * CS + l < L) {
+      const T* zp = z_base + (long)(c * CS + l) * vz_stride + g4;
+#pragma unroll
+      for (int pt = 0; pt < G::PT; ++pt) zr[pt] = *reinterpret_cast<const Z4*>(zp + 16 * pt);
+    }
+  };
+
   // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
   // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
   // the angles of its own rope pairs in registers.
@@ -334,11 +326,11 @@ void scan_chunked_kernel(ScanArgs a) {
       if (lane < CS) {
         const float ablk = __shfl(acum, lane | 15, 64);
         sm.scl[pb][lane] = scl;
-        sm.wdec[pb][lane] = exp2_fast((aend - acum) * kLog2e);
+        sm.wdec[pb][lane] = exp2_fast((aend - acum) * kLog2e) * scl;
         sm.ac2[pb][lane] = acum * kLog2e;
         sm.expa[pb][lane] = exp2_fast(acum * kLog2e);
-        sm.g16[pb][lane] = exp2_fast((ablk - acum) * kLog2e);
-        sm.dg[pb][lane] = scl != 0.0f ? gam * rcp_fast(scl) : 0.0f;
+        sm.g16[pb][lane] = exp2_fast((ablk - acum) * kLog2e) * scl;
+        sm.gam[pb][lane] = gam;
         if (lane == 0) sm.dec[pb] = exp2_fast(aend * kLog2e);
         if constexpr (SO) logdec += aend;
       }
@@ -383,20 +375,16 @@ void scan_chunked_kernel(ScanArgs a) {
   pre(0);
   __syncthreads();   // chunk 0's per-token constants (one wave writes them) before its preparation
 
-  for (int c = 0; c < nc; ++c) {
+  // ================= preparation, lane = token: this wave's Q/K column groups =========
+  // (biases and rope into the Q/K tiles).  Rows past the sequence end hold stale
+  // (finite) inputs: their key scale is 0, so they add nothing to S or h, and their
+  // outputs are never stored.
+  auto prep_groups = [&](int c) {
     const int t0 = c * CS;
     const bool tok = lane < CS && t0 + lane < L;
     const int tl = lane < CS ? lane : 0;        // staging row of this lane
-    const int pc = c & 1;
     const uint4* sq = sm.rq[c % G::NQK];
     const uint4* sk = sm.rk[c % G::NQK];
-    const uint4* sv = sm.rv[pc];
-
-    // ================= preparation: lane = token =================
-    // Rows past the sequence end hold stale (finite) inputs: their key scale is 0,
-    // so they add nothing to S or h, and their outputs are never stored.
-    const float scl = sm.scl[pc][tl];
-    // Q/K column groups: rotation angles, biases, rope, key scale
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
       const int g = G::template qgroup<SO>(wave, k);
@@ -439,187 +427,243 @@ void scan_chunked_kernel(ScanArgs a) {
           }
         }
         if (tok && t0 + lane == L - 1) store8(&sm.fink[8 * g], kf);   // the final carry's key, written after the loop
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] *= scl;
         if (lane < CS) {
           if constexpr (!SO) store8(&sm.q[lane * G::LDQ + 8 * g], qf);
           store8(&sm.k[lane * G::LDQ + 8 * g], kf);
         }
       }
     }
-    // gate of the previous chunk (its Y tiles were written before the last barrier),
-    // then Z for this chunk's gate, then the loads of the next chunks: the gate's wait
-    // for Z comes before any of them is in flight
-    if (!SO && c > 0) gate(c - 1);
-    if (!SO) load_z(c);
-    if (G::DBQK && c + 1 < nc) stage_qk(c + 1);
-    __syncthreads();
+  };
 
-    // single-buffered Q/K staging: every wave has read this chunk's rows
-    if (!G::DBQK && c + 1 < nc) stage_qk(c + 1);
-    if (c + 1 < nc) stage_v(c + 1);
-    if (c + 2 < nc) stage_ars(c + 2);
-
-    // ---- phase 3 for query rows l in [16 lb, 16 lb + 16), all p-tiles (output wave lb):
-    //   Y_diag = mask(K_s Q_r^T)^T V, the mask's diagonal carrying D + gamma QK.
-    // Instantiated per query block so every loop over key blocks is static.
-    auto out_block = [&](auto lb_c) {
-      constexpr int lb = decltype(lb_c)::value;
-      // lane-derived addresses are recomputed here, not kept live across the loop
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-      const int g4l = 4 * (ln >> 4);
-      const int l = 16 * lb + (ln & 15);
-      const float al = sm.ac2[pc][l];
-      const float dgl = sm.dg[pc][l];
-      constexpr int NK = N / W::KSTEP;
+  // ---- query rows l in [16 lb, 16 lb + 16), all p-tiles (output wave lb).  The
+  // products are formed transposed (Y^T = V^T M^T and h Q_r^T), so each lane holds 4
+  // consecutive p of one query row: the gate and the store need no exchange.
+  //   phase 3  Y_diag^T = V^T mask(K Q_r^T), the mask's diagonal carrying D + gamma QK
+  //   phase 6  Y_off^T = h Q_r^T, scaled by the row's e^{A_cum}
+  //   phase 7  (Y_diag + Y_off) silu(Z), stored
+  // Instantiated per query block so every loop over key blocks is static.
+  auto out_block = [&](auto lb_c, int c) {
+    constexpr int lb = decltype(lb_c)::value;
+    const int t0 = c * CS;
+    const int pc = c & 1;
+    const uint4* sv = sm.rv[pc];
+    // lane-derived addresses are recomputed here, not kept live across the loop
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int g4l = 4 * (ln >> 4);
+    const int l = 16 * lb + (ln & 15);
+    const float al = sm.ac2[pc][l];
+    const float gl = sm.gam[pc][l];
+    constexpr int NK = N / W::KSTEP;
+    f32x4 st[lb + 2];
+#pragma unroll
+    for (int sb = 0; sb < lb + 2; ++sb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st[sb][r] = 0.0f;
+    {
       // query fragments first (B operand of every S^T block), then the key blocks'
       // chains side by side
       typename W::frag qf[NK];
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) qf[kk] = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, ln);
-      f32x4 st[lb + 2];
-#pragma unroll
-      for (int sb = 0; sb < lb + 2; ++sb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) st[sb][r] = 0.0f;
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
         for (int sb = 0; sb <= lb; ++sb)
           st[sb] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, ln), qf[kk], st[sb]);
+    }
+    // the V operands, requested before the mask arithmetic so that it covers their latency
+    constexpr int NSP = lb / 2 + 1;
+    typename W::frag vf[NSP][W::STEPS][G::PT];
 #pragma unroll
-      for (int sb = 0; sb <= lb; ++sb) {
-        const int s0 = 16 * sb + g4l;
-        if (sb < lb) {
-          // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
-          const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
-          const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
-          st[sb][0] *= f * gg.x; st[sb][1] *= f * gg.y; st[sb][2] *= f * gg.z; st[sb][3] *= f * gg.w;
-        } else {
-          // diagonal block: causal decay below the diagonal; on it, D plus the
-          // QK skip gamma_l (q_l . k_l) (the stored key carries the scale)
-          const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
-          const float asv[4] = {as.x, as.y, as.z, as.w};
+    for (int i = 0; i < NSP; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float v = st[sb][r] * exp2_fast(fminf(al - asv[r], 0.0f));
-            st[sb][r] = (s0 + r < l) ? v : (s0 + r == l ? Dh + st[sb][r] * dgl : 0.0f);
+      for (int j = 0; j < W::STEPS; ++j)
+#pragma unroll
+        for (int pt = 0; pt < G::PT; ++pt) vf[i][j][pt] = W::template vdiag<G::SV>(sv, 16 * pt, 32 * i, j, ln);
+#pragma unroll
+    for (int sb = 0; sb <= lb; ++sb) {
+      const int s0 = 16 * sb + g4l;
+      if (sb < lb) {
+        // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1 (the
+        // second carries the key scale)
+        const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
+        const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
+        st[sb][0] *= f * gg.x; st[sb][1] *= f * gg.y; st[sb][2] *= f * gg.z; st[sb][3] *= f * gg.w;
+      } else {
+        // diagonal block: causal decay times the key scale below the diagonal; on it,
+        // D plus the QK skip gamma_l (q_l . k_l)
+        const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
+        const float4 sc = *reinterpret_cast<const float4*>(&sm.scl[pc][s0]);
+        const float asv[4] = {as.x, as.y, as.z, as.w};
+        const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = st[sb][r] * exp2_fast(fminf(al - asv[r], 0.0f)) * scv[r];
+          st[sb][r] = (s0 + r < l) ? v : (s0 + r == l ? Dh + st[sb][r] * gl : 0.0f);
+        }
+      }
+    }
+    f32x4 yd[G::PT];
+#pragma unroll
+    for (int pt = 0; pt < G::PT; ++pt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yd[pt][r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NSP; ++i) {
+#pragma unroll
+      for (int j = 0; j < W::STEPS; ++j) {
+        const typename W::frag mf = W::from_acc(st[2 * i], st[2 * i + 1], j);
+#pragma unroll
+        for (int pt = 0; pt < G::PT; ++pt) yd[pt] = W::mma(vf[i][j][pt], mf, yd[pt]);
+      }
+    }
+    // Y_off^T = h Q_r^T: the query fragments again (B), the state rows (A)
+    f32x4 yo[G::PT];
+#pragma unroll
+    for (int pt = 0; pt < G::PT; ++pt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yo[pt][r] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      const typename W::frag qk = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, ln);
+#pragma unroll
+      for (int pt = 0; pt < G::PT; ++pt) yo[pt] = W::mma(W::ld(sm.h, G::LDQ, 16 * pt, kk * W::KSTEP, ln), qk, yo[pt]);
+    }
+    const float ea = sm.expa[pc][l];
+    // this wave's staged loads (issued in the preparation phase) and Z have landed
+    __builtin_amdgcn_s_waitcnt(0);
+    if (t0 + l < L) {
+      T* op = o_base + (long)(t0 + l) * v_stride + g4l;
+#pragma unroll
+      for (int pt = 0; pt < G::PT; ++pt) {
+        float y4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y4[r] = fmaf(yo[pt][r], ea, yd[pt][r]);
+        if (has_z) {
+          float z4[4];
+          raw4_to_f(zr[pt], z4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y4[r] *= silu_fast(z4[r]);
+        }
+        store4(op + 16 * pt, y4);
+      }
+    }
+  };
+
+  // final carry, the parts held in registers: this wave's rope angles (and, for the
+  // state-only pass's scalar wave, the total log-decay)
+  auto fin_regs = [&]() {
+    if (a.fin_theta && fin_here && lane == 0) {
+#pragma unroll
+      for (int k = 0; k < G::QGW; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * G::template qgroup<SO>(wave, k) + j;
+          if (r < R) a.fin_theta[(long)ci_out * R + r] = carry[k][j] * kTwoPi;
+        }
+    }
+    if constexpr (SO) {
+      if (a.fin_logdec && fin_here && wave == kScalarWave && lane == 0) a.fin_logdec[ci_out] = logdec;
+    }
+  };
+
+  // ---- the chunk loop, one per role: the roles share no loop-carried registers
+  // (the state accumulators live only in the state waves' loop), and every loop passes
+  // the same two barriers per chunk.
+  if (ywave) {
+    for (int c = 0; c < nc; ++c) {
+      prep_groups(c);
+      // Z for this chunk's gate, then the loads of the next chunk's Q/K
+      if (!SO) load_z(c);
+      if (G::DBQK && c + 1 < nc) stage_qk(c + 1);
+      __syncthreads();
+      if constexpr (!SO) {
+        if (wave == 0) out_block(std::integral_constant<int, 0>{}, c);
+        if (wave == 1) out_block(std::integral_constant<int, 1>{}, c);
+        if constexpr (G::LB16 > 2) {
+          if (wave == 2) out_block(std::integral_constant<int, 2>{}, c);
+          if (wave == 3) out_block(std::integral_constant<int, 3>{}, c);
+        }
+      }
+      if (c + 1 < nc) pre(c + 1);
+      // staged loads have landed before the barrier (a wave with a query block waited
+      // before its gate, so that the gate's stores are not waited for)
+      if (SO || 16 * wave >= CS) __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    fin_regs();
+  } else if (swave) {
+    for (int c = 0; c < nc; ++c) {
+      const int pc = c & 1;
+      prep_groups(c);
+      // the state entering this chunk, h[p][n] in the io type, for the output waves'
+      // Y_off (the state waves of a p-tile hold it alike; the first writes it)
+      if (!SO && part == 0) {
+#pragma unroll
+        for (int nb = 0; nb < G::NB16; ++nb) {
+          const float hv[4] = {hs[nb][0], hs[nb][1], hs[nb][2], hs[nb][3]};
+          store4(&sm.h[pcol * G::LDQ + 16 * nb + g4], hv);
+        }
+      }
+      __syncthreads();
+      if (c + 1 < nc) stage_v(c + 1);
+      if (c + 2 < nc) stage_ars(c + 2);
+      {
+        // lane-derived addresses are recomputed here, not kept live across the loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const uint4* sv = sm.rv[pc];
+        const float dec = sm.dec[pc];
+        float wv[CS / W::KSTEP][W::WN];
+#pragma unroll
+        for (int ks = 0; ks < CS / W::KSTEP; ++ks) W::load_w(&sm.wdec[pc][W::ktok(ks * W::KSTEP, ln)], wv[ks]);
+        // ---- phases 4-5: h <- e^{A_end} h + K^T (w V) for my p-tile
+        if constexpr (SO) {                // backward: the state entering chunk c, [p][n]
+          if (a.chunk_h && part == 0) {
+            T* dst = reinterpret_cast<T*>(a.chunk_h) + ((long)(bh * nc + c) * P + pcol) * N + g4;
+#pragma unroll
+            for (int nb = 0; nb < G::NB16; ++nb) {
+              const float hv[4] = {hs[nb][0], hs[nb][1], hs[nb][2], hs[nb][3]};
+              store4(dst + 16 * nb, hv);
+            }
           }
         }
-      }
-      f32x4 yd[G::PT];
-#pragma unroll
-      for (int pt = 0; pt < G::PT; ++pt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) yd[pt][r] = 0.0f;
-#pragma unroll
-      for (int sp = 0; sp <= lb; sp += 2) {
-#pragma unroll
-        for (int j = 0; j < W::STEPS; ++j) {
-          const typename W::frag mf = W::from_acc(st[sp], st[sp + 1], j);
-#pragma unroll
-          for (int pt = 0; pt < G::PT; ++pt)
-            yd[pt] = W::mma(mf, W::template vdiag<G::SV>(sv, 16 * pt, 16 * sp, j, ln), yd[pt]);
-        }
-      }
-#pragma unroll
-      for (int pt = 0; pt < G::PT; ++pt)
-#pragma unroll
-        for (int r = 0; r < 4; r += 2)
-          store_pair(&sm.yd[(16 * lb + g4l + r) * G::LDY + 16 * pt + (ln & 15)],
-                     &sm.yd[(16 * lb + g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
-    };
-    if (!SO && ywave) {                 // the state-only pass has no Y_diag
-      if (wave == 0) out_block(std::integral_constant<int, 0>{});
-      if (wave == 1) out_block(std::integral_constant<int, 1>{});
-      if constexpr (G::LB16 > 2) {
-        if (wave == 2) out_block(std::integral_constant<int, 2>{});
-        if (wave == 3) out_block(std::integral_constant<int, 3>{});
-      }
-    } else if (swave) {
-      // the state update's decay and per-token weights are read before this wave's
-      // stores (a read issued after them would wait for them too)
-      const float dec = sm.dec[pc];
-      float wv[CS / W::KSTEP][W::WN];
-      auto load_wv = [&]() {
-#pragma unroll
-        for (int ks = 0; ks < CS / W::KSTEP; ++ks) W::load_w(&sm.wdec[pc][W::ktok(ks * W::KSTEP, lane)], wv[ks]);
-      };
-      // ---- phase 6: Y_off = Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
-      if constexpr (!SO) {
-      typename W::frag hf[G::BF ? N / 32 : 1];
-      if constexpr (G::BF) {
-#pragma unroll
-        for (int q = 0; q < N / 32; ++q) hf[q] = W::hfrag(hs[2 * q], hs[2 * q + 1]);
-      }
-      constexpr int NLB = G::LB16 / G::SPT;
-      f32x4 yo[NLB];
-#pragma unroll
-      for (int i = 0; i < NLB; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) yo[i][r] = 0.0f;
-      if constexpr (G::BF) {
-        // per k-step the query blocks' fragments, then their chains side by side
-#pragma unroll
-        for (int q = 0; q < N / 32; ++q) {
-          typename W::frag qa[NLB];
-#pragma unroll
-          for (int i = 0; i < NLB; ++i) qa[i] = W::qoff(sm.q, G::LDQ, 16 * (part + G::SPT * i), 32 * q, lane);
-#pragma unroll
-          for (int i = 0; i < NLB; ++i) yo[i] = W::mma(qa[i], hf[q], yo[i]);
-        }
-      } else {
 #pragma unroll
         for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
+          for (int r = 0; r < 4; ++r) hs[nb][r] *= dec;
 #pragma unroll
-            for (int i = 0; i < NLB; ++i) {
-              const int l = 16 * (part + G::SPT * i) + (lane & 15);
-              yo[i] = W::mma(sm.q[l * G::LDQ + 16 * nb + g4 + r], hs[nb][r], yo[i]);
-            }
-      }
-      load_wv();
+        for (int ks = 0; ks < CS / W::KSTEP; ++ks) {
+          const typename W::frag vb = W::scale(W::template vstate<G::SV>(sv, 16 * pr, ks * W::KSTEP, ln), wv[ks]);
 #pragma unroll
-      for (int i = 0; i < NLB; ++i) {
-        const int lb = part + G::SPT * i;
-#pragma unroll
-        for (int r = 0; r < 4; r += 2)
-          store_pair(&sm.yo[(16 * lb + g4 + r) * G::LDY + pcol], &sm.yo[(16 * lb + g4 + r + 1) * G::LDY + pcol],
-                     yo[i][r], yo[i][r + 1]);
-      }
-      } else {
-        load_wv();
-      }
-      // ---- phases 4-5: h <- e^{A_end} h + K_s^T (w V) for my p-tile
-      if constexpr (SO) {                // backward: the state entering chunk c, [p][n]
-        if (a.chunk_h && part == 0) {
-          T* dst = reinterpret_cast<T*>(a.chunk_h) + ((long)(bh * nc + c) * P + pcol) * N + g4;
-#pragma unroll
-          for (int nb = 0; nb < G::NB16; ++nb) {
-            const float hv[4] = {hs[nb][0], hs[nb][1], hs[nb][2], hs[nb][3]};
-            store4(dst + 16 * nb, hv);
-          }
+          for (int nb = 0; nb < G::NB16; ++nb)
+            hs[nb] = W::mma(W::kstate(sm.k, G::LDQ, ks * W::KSTEP, 16 * nb, ln), vb, hs[nb]);
         }
       }
+      if (c + 1 < nc) pre(c + 1);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    fin_regs();
+    if (a.fin_h && fin_here && part == 0) {
 #pragma unroll
       for (int nb = 0; nb < G::NB16; ++nb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) hs[nb][r] *= dec;
-#pragma unroll
-      for (int ks = 0; ks < CS / W::KSTEP; ++ks) {
-        const typename W::frag vb = W::scale(W::template vstate<G::SV>(sv, 16 * pr, ks * W::KSTEP, lane), wv[ks]);
-#pragma unroll
-        for (int nb = 0; nb < G::NB16; ++nb)
-          hs[nb] = W::mma(W::kstate(sm.k, G::LDQ, ks * W::KSTEP, 16 * nb, lane), vb, hs[nb]);
-      }
+        for (int r = 0; r < 4; ++r) a.fin_h[((long)ci_out * P + pcol) * N + 16 * nb + g4 + r] = hs[nb][r];
     }
-    if (c + 1 < nc) pre(c + 1);
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's staged loads and gate stores are done
-    __syncthreads();
+  } else {
+    for (int c = 0; c < nc; ++c) {
+      prep_groups(c);
+      __syncthreads();
+      // single-buffered Q/K staging: every wave has read this chunk's rows
+      if (!G::DBQK && c + 1 < nc) stage_qk(c + 1);
+      if (c + 1 < nc) pre(c + 1);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    fin_regs();
   }
-  if (!SO && nc > 0) gate(nc - 1);
 
   // final carry: k of the last token (kept in LDS by its preparation) and its v (still
   // in the last chunk's staged rows)
@@ -628,24 +672,6 @@ void scan_chunked_kernel(ScanArgs a) {
     for (int i = tid; i < P; i += G::NT)
       a.fin_v[(long)ci_out * P + i] =
           Elem<T>::to_f(*staged_elem<G::SV, T>(sm.rv[(nc - 1) & 1], L - 1 - (nc - 1) * CS, i));
-  }
-  if (a.fin_h && fin_here && swave && part == 0) {
-#pragma unroll
-    for (int nb = 0; nb < G::NB16; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) a.fin_h[((long)ci_out * P + pcol) * N + 16 * nb + g4 + r] = hs[nb][r];
-  }
-  if constexpr (SO) {
-    if (a.fin_logdec && fin_here && wave == kScalarWave && lane == 0) a.fin_logdec[ci_out] = logdec;
-  }
-  if (a.fin_theta && fin_here && lane == 0) {
-#pragma unroll
-    for (int k = 0; k < G::QGW; ++k)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * G::template qgroup<SO>(wave, k) + j;
-        if (r < R) a.fin_theta[(long)ci_out * R + r] = carry[k][j] * kTwoPi;
-      }
   }
 }
 
