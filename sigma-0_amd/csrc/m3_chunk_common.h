@@ -82,23 +82,6 @@ __device__ __forceinline__ const T* staged_elem(const uint4* buf, int row, int c
   return reinterpret_cast<const T*>(&buf[row * S + ((col / E) ^ (row & (S - 1)))]) + col % E;
 }
 
-// Eight values as the elements of 8-column group g of staged row `row`, in the slots a
-// lane-per-row read of that group uses: one 16-byte slot in bf16, two in f32.
-template <int S, typename T>
-__device__ __forceinline__ void store_staged8(uint4* buf, int row, int g, const float f[8]) {
-  if constexpr (sizeof(T) == 2) {
-    bf16x8 v;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (bf16)f[i];
-    buf[row * S + (g ^ (row & (S - 1)))] = __builtin_bit_cast(uint4, v);
-  } else {
-    buf[row * S + ((2 * g) ^ (row & (S - 1)))] =
-        make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
-    buf[row * S + ((2 * g + 1) ^ (row & (S - 1)))] =
-        make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7]));
-  }
-}
-
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 // MFMA operand whose 16 rows (A) or columns (B) are columns c0.. of a row-major
@@ -222,28 +205,6 @@ template <> struct MF16<bf16> {
   __device__ __forceinline__ static frag kstate(const bf16* k, int ldq, int t0, int n0, int lane) {
     return ld_tr(k, ldq, t0, n0, lane);
   }
-  // The same operands from Q/K rows kept in the staged (swizzled) layout of
-  // stage_rows (S 16-byte slots per row): ld, qoff and kstate.
-  template <int S>
-  __device__ __forceinline__ static frag ld_st(const uint4* buf, int row0, int k0, int lane) {
-    const uint4 v = staged<S>(buf, row0 + (lane & 15), k0 / 8 + (lane >> 4));
-    return __builtin_bit_cast(frag, v);
-  }
-  template <int S>
-  __device__ __forceinline__ static frag qoff_st(const uint4* buf, int row0, int k0, int lane) {
-    const int row = row0 + (lane & 15), c = k0 + 4 * (lane >> 4);
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(staged_elem<S, bf16>(buf, row, c));
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(staged_elem<S, bf16>(buf, row, c + 16));
-    frag f;
-    f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
-    f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
-    return f;
-  }
-  template <int S>
-  __device__ __forceinline__ static frag kstate_st(const uint4* buf, int t0, int n0, int lane) {
-    const int t = t0 + 8 * (lane >> 4);
-    return staged_tr<S>(buf, t, t + 4, n0, lane);
-  }
   // the per-token weights of vstate's k-slots (WN per lane, tokens from ktok), and
   // the scaling of a fragment by them
   static constexpr int WN = 8;
@@ -286,14 +247,6 @@ template <> struct MF16<float> {
   }
   __device__ __forceinline__ static frag kstate(const float* k, int ldq, int t0, int n0, int lane) {
     return ld_tr(k, ldq, t0, n0, lane);
-  }
-  template <int S>
-  __device__ __forceinline__ static frag ld_st(const uint4* buf, int row0, int k0, int lane) {
-    return *staged_elem<S, float>(buf, row0 + (lane & 15), k0 + (lane >> 4));
-  }
-  template <int S>
-  __device__ __forceinline__ static frag kstate_st(const uint4* buf, int t0, int n0, int lane) {
-    return *staged_elem<S, float>(buf, t0 + (lane >> 4), n0 + (lane & 15));
   }
   static constexpr int WN = 1;
   __device__ __forceinline__ static int ktok(int t0, int lane) { return t0 + (lane >> 4); }

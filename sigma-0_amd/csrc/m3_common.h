@@ -1,8 +1,8 @@
 // Shared device helpers for the Mamba3 SISO scan kernels (gfx950 / CDNA4).
 //
 // Wave64 everywhere: prefix scans and reductions are written for 64-lane
-// wavefronts, MFMA tiles are 32x32 (v_mfma_f32_32x32x16_bf16 and
-// v_mfma_f32_32x32x2_f32).  Transcendentals use the hardware units:
+// wavefronts, MFMA tiles are 16x16 (v_mfma_f32_16x16x32_bf16 and
+// v_mfma_f32_16x16x4_f32).  Transcendentals use the hardware units:
 // v_exp_f32 (2^x), v_rcp_f32, and v_sin_f32 / v_cos_f32, which take their
 // argument in revolutions (sin(2*pi*u)); angles are range-reduced to [0, 2pi)
 // before use, so u lies in [0, 1).
