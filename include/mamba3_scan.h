@@ -4,8 +4,9 @@
  * Plain pointers and sizes only.  Every device pointer is a HIP device
  * address; `stream` is a hipStream_t passed as void* (NULL = default stream).
  * All calls are asynchronous on `stream`, allocate nothing (a split prefill
- * takes a caller-owned workspace), keep no per-call state and may be issued
- * concurrently from several host threads.  Return
+ * takes a caller-owned workspace, or the library's own scratch array in
+ * m3_chunk_scan_fwd_noalloc), keep no per-call state and may be issued
+ * concurrently from several host threads (m3_chunk_scan_fwd_noalloc: see there).  Return
  * value: 0 on success, else an M3_E* code; m3_last_error() then describes it
  * (thread-local string).
  *
@@ -116,6 +117,29 @@ int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
                          float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
                          int B, int L, int H, int Hqk, int N, int P, int R,
                          int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * m3_chunk_scan_fwd_ws without the workspace argument: the split's scratch is a
+ * device array of 17 MiB that the library holds for the life of the process, one
+ * copy per GPU (its address is looked up on the first call on each device).  No
+ * counterpart in the reference: this entry point is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It allocates nothing and calls no allocating routine.  Shapes whose
+ * split would need more than the 17 MiB (m3_chunk_scan_ws_bytes) are rejected with
+ * M3_E_ARG; shapes that run as one pass need no scratch.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.  Nothing in the array needs
+ * to start at zero.
+ */
+int m3_chunk_scan_fwd_noalloc(const void* Q, const void* K, const void* V,
+                              const float* ADT, const float* DT, const float* Trap,
+                              const float* Q_bias, const float* K_bias, const float* Angles,
+                              const float* D, const void* Z, void* Out,
+                              const float* init_theta, const float* init_ssm,
+                              const float* init_k, const float* init_v,
+                              float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                              int B, int L, int H, int Hqk, int N, int P, int R,
+                              int chunk_size, int io_dtype, void* stream);
 
 /*
  * Device workspace (bytes) that m3_chunk_scan_bwd needs for a shape; 0 when the

@@ -9,6 +9,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/mamba3_layer.h"
 #include "m3_scan.h"
 
@@ -155,6 +157,69 @@ int m3_chunk_scan_fwd_shared(const void* Q, const void* K, const void* V,
   return scan_fwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, nullptr, nullptr, nullptr, nullptr,
                   nullptr, nullptr, nullptr, nullptr, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes, stream,
                   true);
+}
+
+}  // extern "C"
+
+// ---- the allocation-free split prefill (m3_chunk_scan_fwd_noalloc)
+// The sequence split's carry workspace lives in a device array that the library
+// holds for the process, one copy per GPU, instead of memory from the caller.  Every
+// split shape needs at most 256 (batch, head, segment) carry slots (the split targets
+// one wave of 256 blocks), which at d_state 128, headdim 64 and R <= 64 is at most
+// 16.5 MB; the array holds 17 MiB.  Nothing in it needs to start at zero: the first
+// kernel of a split call writes every carry slot that the later ones read.
+namespace m3 {
+constexpr size_t kNoallocScratchBytes = size_t(17) << 20;
+__device__ __align__(256) char scratch[kNoallocScratchBytes];
+}  // namespace m3
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// The array's device address on the current device, looked up once per device with
+// that device current (each GPU holds its own copy at its own address).
+int scratch_on_current_device(void** ptr) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(M3_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(M3_E_ARG, "device %d beyond the %d supported", dev, kMaxDevices);
+  std::call_once(g_scratch_once[dev], [dev] {
+    g_scratch_err[dev] = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(m3::scratch));
+  });
+  if (g_scratch_err[dev] != hipSuccess)
+    return fail(M3_E_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(g_scratch_err[dev]));
+  *ptr = g_scratch_ptr[dev];
+  return M3_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int m3_chunk_scan_fwd_noalloc(const void* Q, const void* K, const void* V,
+                              const float* ADT, const float* DT, const float* Trap,
+                              const float* Q_bias, const float* K_bias, const float* Angles,
+                              const float* D, const void* Z, void* Out,
+                              const float* init_theta, const float* init_ssm,
+                              const float* init_k, const float* init_v,
+                              float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                              int B, int L, int H, int Hqk, int N, int P, int R,
+                              int chunk_size, int io_dtype, void* stream) {
+  const size_t need = m3_chunk_scan_ws_bytes(B, L, H, N, P, R, chunk_size, io_dtype);
+  if (need > m3::kNoallocScratchBytes)
+    return fail(M3_E_ARG, "the split needs %zu bytes of scratch, the library holds %zu (m3_chunk_scan_fwd_ws "
+                "takes a workspace of any size)", need, m3::kNoallocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_on_current_device(&ws);
+    if (rc != M3_OK) return rc;
+  }
+  return scan_fwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, init_theta, init_ssm, init_k, init_v,
+                  fin_theta, fin_ssm, fin_k, fin_v, B, L, H, Hqk, N, P, R, chunk_size, io_dtype, ws, need, stream,
+                  false);
 }
 
 int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,

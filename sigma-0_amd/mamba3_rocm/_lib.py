@@ -25,6 +25,7 @@ IMPL_NONE, IMPL_CHUNKED_MFMA, IMPL_GENERIC = 0, 1, 2
 
 EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_scan_fwd",
            "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes", "m3_chunk_scan_fwd_ws",
+           "m3_chunk_scan_fwd_noalloc",
            "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd", "m3_chunk_scan_fwd_shared",
            "m3_chunk_scan_bwd_shared_ws_bytes", "m3_chunk_scan_bwd_shared", "m3_decode_step",
            "m3_layer_pre", "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu", "m3_block_act", "m3_block_act_norm",
@@ -40,6 +41,7 @@ _SIGS = {
     "m3_chunk_scan_fwd_carry": ([_P] * 20 + [_I] * 9 + [_P], _I),
     "m3_chunk_scan_ws_bytes": ([_I] * 8, ctypes.c_size_t),
     "m3_chunk_scan_fwd_ws": ([_P] * 20 + [_I] * 9 + [_P, ctypes.c_size_t, _P], _I),
+    "m3_chunk_scan_fwd_noalloc": ([_P] * 20 + [_I] * 9 + [_P], _I),
     "m3_chunk_scan_bwd_ws_bytes": ([_I] * 9, ctypes.c_size_t),
     "m3_chunk_scan_bwd": ([_P] * 23 + [_I] * 9 + [_P, ctypes.c_size_t, _P], _I),
     "m3_chunk_scan_fwd_shared": ([_P] * 12 + [_I] * 8 + [_P, ctypes.c_size_t, _P], _I),

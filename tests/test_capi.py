@@ -38,7 +38,8 @@ def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
     assert names == sorted(["m3_abi_version", "m3_last_error", "m3_chunk_scan_impl",
                             "m3_chunk_scan_fwd", "m3_chunk_scan_fwd_carry", "m3_chunk_scan_ws_bytes",
-                            "m3_chunk_scan_fwd_ws", "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd",
+                            "m3_chunk_scan_fwd_ws", "m3_chunk_scan_fwd_noalloc",
+                            "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd",
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
                             "m3_chunk_scan_bwd_shared", "m3_decode_step", "m3_layer_pre",
                             "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu",
