@@ -45,6 +45,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "sigma-0_amd"))
 
 HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense float32 matrix
 METRIC = "Mamba3 scan tokens/s + % of MFMA/HBM roofline, bf16 B=8 L=4096 H=32"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "scan_chunked_bf16_config2_traffic.json")
 SCAN_KERNEL = "scan_chunked_kernelIDF16bLi64ELi128ELi64ELi32ELi12ELb0E"
@@ -454,6 +455,16 @@ def main():
                           "achieved_gbs": round(r["achieved_gbs"], 1),
                           "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
+    if args.mode == "fp32":
+        # config 2's shape with float32 I/O (what the model hands the scan), for profiling
+        r = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2,
+                       io_dtype=torch.float32)
+        print(json.dumps({"mode": "fp32", "kernel_ms": round(r["kernel_s"] * 1e3, 4),
+                          "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
+                          "tflops": round(r["flops"] / r["kernel_s"] / 1e12, 1),
+                          "frac_mfma_fp32": round(r["flops"] / r["kernel_s"] / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+                          "achieved_gbs": round(r["achieved_gbs"], 1)}), flush=True)
+        return
     if args.mode == "long":
         # config 3 alone (B*H = 32: the sequence split runs), for profiling
         r = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3)
@@ -496,6 +507,8 @@ def main():
         lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
         bw = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         sh = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
+        f32 = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2,
+                         io_dtype=torch.float32)
         bb = bench_stack(torch, 4, 12288, 768, 12, 2112, 5, 2, seed=5)
         out["secondary"] = {
             "decode_config4": {"B": 512, "H": 32, "P": 64, "N": 128, "steps": 256,
@@ -513,6 +526,13 @@ def main():
                                   "tokens_per_s": round(8 * 4096 / sh["wall_s"], 1),
                                   "achieved_gbs": round(sh["achieved_gbs"], 1),
                                   "frac_hbm": round(sh["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",
+                                "kernel_ms": round(f32["kernel_s"] * 1e3, 4),
+                                "tokens_per_s": round(8 * 4096 / f32["wall_s"], 1),
+                                "bound": "mfma_fp32", "tflops": round(f32["flops"] / f32["kernel_s"] / 1e12, 1),
+                                "frac_mfma_fp32": round(f32["flops"] / f32["kernel_s"] / 1e12
+                                                        / FP32_MFMA_PEAK_TFLOPS, 4),
+                                "achieved_gbs": round(f32["achieved_gbs"], 1)},
             "backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
                                  "ms": round(bw["kernel_s"] * 1e3, 4),
                                  "tokens_per_s": round(8 * 4096 / bw["wall_s"], 1),

@@ -38,6 +38,8 @@ int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_sca
  * The layer's scan (_forward_pallas, mamba3.py:369-370, 413-425: Q = C and K = B (B, L, N),
  * angle rates (B, L, R)) reading x (V) and z (Z) in place from the projection
  * proj (B, L, d_in_proj), columns [HP, 2HP) and [0, HP), instead of from copies.
+ * d_in_proj must be the projection's width 2HP + 2N + 3H + R, the layout m3_layer_pre
+ * reads (M3_E_ARG otherwise).
  * Otherwise the arguments and result of m3_chunk_scan_fwd_shared (Out (B, L, H, P)
  * contiguous, the same workspace size from m3_chunk_scan_ws_bytes).  The rows and
  * the offset of x (H*P elements) must be multiples of 16 bytes (M3_E_ALIGN

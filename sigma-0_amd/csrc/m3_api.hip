@@ -419,8 +419,9 @@ int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (H <= 0 || P <= 0 || N <= 0 || R < 0)
     return fail(M3_E_ARG, "non-positive dimension (H=%d N=%d P=%d R=%d)", H, N, P, R);
-  if ((long)d_in_proj < 2L * H * P + 2L * N + 3L * H + R)
-    return fail(M3_E_ARG, "d_in_proj=%d is smaller than the projection's fields (2HP + 2N + 3H + R = %ld)", d_in_proj,
+  // the projection layout that m3_layer_pre reads too: no padded rows
+  if ((long)d_in_proj != 2L * H * P + 2L * N + 3L * H + R)
+    return fail(M3_E_ARG, "d_in_proj=%d is not the projection's width (2HP + 2N + 3H + R = %ld)", d_in_proj,
                 2L * H * P + 2L * N + 3L * H + R);
   const long es = io_dtype == M3_DTYPE_BF16 ? 2 : 4;
   if (((long)d_in_proj * es) % 16 != 0)

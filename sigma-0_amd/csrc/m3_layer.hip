@@ -162,7 +162,7 @@ void layer_post_kernel(LayerPostArgs a) {
   const T* y = reinterpret_cast<const T*>(a.y) + tok * D;
   T* out = reinterpret_cast<T*>(a.out) + tok * D;
   const bool vec = D % V == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.scale) & 15) == 0;
   float ss = 0.0f;
   if (vec && sizeof(T) == 2) {
     for (int i = lane; i < D / 8; i += 64) {

@@ -55,6 +55,9 @@ hipError_t scan_generic_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
 // Chunked MFMA kernel: returns true when (dtype, CS, N, P, R) has an instantiation.
 bool scan_chunked_supported(bool bf16_io, int CS, int N, int P, int R);
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
+// Its float32-I/O kernel (m3_scan_chunked_f32.hip), reached through the two above.
+bool scan_chunked_f32_supported(int CS, int N, int P, int R);
+hipError_t scan_chunked_f32_launch(const ScanArgs& a, hipStream_t st);
 
 // State-only pass of the chunked kernel (sequence split pass 1, backward chunk states).
 bool scan_state_supported(bool bf16_io, int CS, int N, int P, int R);

@@ -678,13 +678,12 @@ void scan_chunked_kernel(ScanArgs a) {
 // ------------------------------------------------------------------ dispatch
 // (dtype, chunk, d_state, headdim, rotation width) instantiations; R is the
 // model's rope_fraction 0.5 (R = N/4) or 1.0 (R = N/2) width, or 0.
+// float32 I/O has its own kernel (m3_scan_chunked_f32.hip).
 #define M3_CHUNK_SHAPES(X)                                                                         \
   X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0)                        \
   X(bf16, 64, 128, 32, 32) X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 64, 32)                         \
   X(bf16, 64, 64, 32, 16) X(bf16, 64, 32, 32, 8) X(bf16, 64, 32, 64, 8)                            \
-  X(bf16, 32, 128, 64, 32) X(bf16, 32, 64, 64, 16) X(bf16, 32, 64, 32, 16) X(bf16, 32, 128, 32, 32) \
-  X(float, 32, 64, 64, 16) X(float, 32, 64, 64, 32) X(float, 32, 64, 32, 16) X(float, 32, 32, 32, 8) \
-  X(float, 32, 32, 64, 8)
+  X(bf16, 32, 128, 64, 32) X(bf16, 32, 64, 64, 16) X(bf16, 32, 64, 32, 16) X(bf16, 32, 128, 32, 32)
 
 constexpr int kChunkWaves = 12;
 
@@ -698,6 +697,7 @@ static int kernel_chunk(bool bf16_io, int CS) {
 }
 
 bool scan_chunked_supported(bool bf16_io, int CS_, int N, int P, int R) {
+  if (!bf16_io) return scan_chunked_f32_supported(CS_, N, P, R);
   const int CS = kernel_chunk(bf16_io, CS_);
 #define X(T, cs, n, p, r) \
   if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && N == n && P == p && R == r) return true;
@@ -707,6 +707,7 @@ bool scan_chunked_supported(bool bf16_io, int CS_, int N, int P, int R) {
 }
 
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
+  if (!bf16_io) return scan_chunked_f32_launch(a, st);
   const int CS = kernel_chunk(bf16_io, a.CS);
   const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
 #define X(T, cs, n, p, r)                                                                            \

@@ -1,0 +1,683 @@
+// Chunked Mamba3 SISO prefill scan with float32 I/O on CDNA4 matrix cores.
+//
+// The same operator as m3_scan_chunked.hip (the reference's mamba3_ssd_chunked_jax,
+// phases 1-7, src/base_model/models/mamba3_jax.py:327-419), for the float32
+// inputs the model hands its scan (mamba3.py:363-367 casts x, z, B and C to float32
+// before mamba3_siso_triton), with float32 MFMA operands (v_mfma_f32_16x16x4_f32,
+// float32 accumulation: exact float32 contractions) and 32-token chunks.
+//
+// The work is split differently from the bf16 kernel because a float32 MFMA costs
+// 16 times a bf16 one per FLOP, so the matrix work must be spread over every SIMD:
+// one workgroup of 12 waves per (batch, head) walks the chunks in order.  Output
+// waves 0-1 each own a 16-row query block of Y_diag (S^T, the causal mask, M V).
+// State waves 4-7 each own 16 columns of the value dimension (a p-tile): h^T[:, p-tile]
+// (all N rows) as 16x16 accumulators, that p-tile's Y_off = Q_r h^T and its state
+// update.  Auxiliary waves 8-11 take the larger share of the preparation (the rope'd
+// columns) and compute the next chunk's rotation angles while the others run the
+// matrix work.  A chunk is two phases with a barrier after each:
+//   preparation  lane = token: biases, rope and key scale into the Q/K tiles; the gate
+//                and store of the previous chunk's Y; the direct-to-LDS loads of the
+//                next chunk's Q and K
+//   matrix       the loads of the next chunk's V and of the rates and scalars of the
+//                chunk after, then the MFMA work
+// The staged inputs are double-buffered by chunk parity; every input byte is read
+// from HBM once and the output written once.
+#include <type_traits>
+
+#include "m3_chunk_common.h"
+
+namespace m3 {
+namespace chunked_f32 {
+
+// Compile-time geometry of one instantiation.
+template <typename T, int CS_, int N_, int P_, int R_, int NW_>
+struct Geo {
+  static constexpr bool BF = std::is_same<T, bf16>::value;
+  static constexpr int CS = CS_, N = N_, P = P_, R = R_, NW = NW_, NT = 64 * NW_;
+  static constexpr int NWY = 4;                             // output waves 0..3
+  static constexpr int NST = 4;                             // state waves 4..7
+  static constexpr int NAUX = NW - NWY - NST;               // auxiliary waves 8..11
+  static constexpr int KSTEP = MF16<T>::KSTEP;
+  static constexpr int LB16 = CS / 16, PT = P / 16;         // 16-row query blocks, 16-col p-tiles
+  static constexpr int NB16 = N / 16;                       // 16-row state tiles per p-tile
+  static constexpr int SPT = NST / PT;                      // state waves per p-tile
+  static constexpr int TS = BF ? 2 : 4;
+  static constexpr int PAD = BF ? 8 : 4;
+  static constexpr int LDQ = N + PAD;                       // sQ, sK rows (elements)
+  static constexpr int LDY = P + (BF ? 8 : 2);              // sY rows (io precision)
+  static constexpr int QG = N / 8, QGW = 2;                // Q/K 8-column groups, at most 2 per wave
+  // 16-byte staging slots per row: Q/K, V, rotation rates
+  static constexpr int SQ = N * TS / 16, SV = P * TS / 16, SA = R / 4 > 0 ? R / 4 : 1;
+  // LDS bytes besides the Q/K staging.  The Q/K staging is double-buffered where it
+  // fits; otherwise (rotation width N/2 at d_state 128) it is single-buffered and its
+  // loads wait until the preparation phase has consumed it.
+  static constexpr int FIXED = 2 * CS * LDQ * TS + 2 * CS * LDY * TS + (2 * CS * SV + 2 * CS * SA) * 16 +
+                               2 * 3 * (CS + 4) * 4 + 8 * N + 2 * 6 * CS * 4 + 64;
+  static constexpr bool DBQK = FIXED + 4 * CS * SQ * 16 <= 160 * 1024 - 512;
+  static constexpr int NQK = DBQK ? 2 : 1;
+  static_assert(CS <= 64 && LB16 <= NWY, "one token per lane, one query block per output wave");
+  static_assert(SPT >= 1 && NST % PT == 0 && LB16 % SPT == 0, "state-wave split");
+  static_assert(NAUX == 4, "12 waves");
+  static_assert(QG <= 2 * NAUX + NWY + NST, "column groups per wave");
+  // Q/K 8-column group k (< QGW) of a wave, or QG for none.  The first groups are the
+  // rope columns, and their owner also computes their angles for the next chunk.  Full
+  // pass: the auxiliary waves take the first groups, two each, so the angle work stays
+  // off the matrix waves; the remaining groups go one per matrix wave.  State-only pass
+  // (no Q and no Y, so the output waves have no matrix work): the output waves and then
+  // the auxiliary waves take the first groups, one each, and the state waves two each
+  // of the rest, which halves the angle work per wave.
+  template <bool SO>
+  __device__ static int qgroup(int wave, int k) {
+    int g;
+    if constexpr (SO) {
+      if (wave < NWY) g = k == 0 ? wave : QG;
+      else if (wave >= NWY + NST) g = k == 0 ? NWY + (wave - NWY - NST) : QG;
+      else g = NWY + NAUX + 2 * (wave - NWY) + k;
+    } else {
+      g = wave >= NWY + NST ? 2 * (wave - NWY - NST) + k : 2 * NAUX + wave + (NWY + NST) * k;
+    }
+    return g < QG ? g : QG;
+  }
+  static_assert(R % 4 == 0 && 2 * R <= N, "rotation width: a multiple of 4, at most N/2");
+  static_assert((SQ & (SQ - 1)) == 0 && (SV & (SV - 1)) == 0 && (SA & (SA - 1)) == 0, "swizzle widths");
+};
+
+template <typename G>
+struct __attribute__((aligned(16))) Smem {
+  typedef typename std::conditional<G::BF, bf16, float>::type T;
+  T q[G::CS * G::LDQ];                   // rope'd Q rows
+  T k[G::CS * G::LDQ];                   // rope'd, trapezoid-scaled K rows
+  // Y before the gate, in two parts written by plain stores: the intra-chunk part
+  // (output waves, by query block) and Q h^T (state waves, by p-tile; the gate applies
+  // its e^{A_cum} row scale)
+  alignas(16) T yd[G::CS * G::LDY];
+  alignas(16) T yo[G::CS * G::LDY];
+  // raw inputs staged by direct-to-LDS loads, by chunk parity: 16-byte slots, row t slot
+  // s stored at t * S + (s ^ (t mod S)) so that a lane-per-row read is bank-conflict free
+  alignas(16) uint4 rq[G::NQK][G::CS * G::SQ];
+  alignas(16) uint4 rk[G::NQK][G::CS * G::SQ];
+  alignas(16) uint4 rv[2][G::CS * G::SV];
+  // rotation rates and adt, dt, trap ([CS]: the next chunk's first token), by chunk
+  // parity: chunk c+1's angles and weights are computed during chunk c's matrix phase
+  alignas(16) uint4 ra[2][G::CS * G::SA];
+  alignas(16) float rs[2][3][G::CS + 4];
+  alignas(16) float qb[G::N];            // biases of this head
+  alignas(16) float kb[G::N];
+  // per-token chunk constants, by chunk parity
+  alignas(16) float ac2[2][G::CS];       // A_cum * log2(e)
+  alignas(16) float g16[2][G::CS];       // e^{A_e - A_cum}, A_e = A_cum at the end of the token's 16-block
+  alignas(16) float expa[2][G::CS];      // e^{A_cum} (read by the gate, a chunk later)
+  alignas(16) float dg[2][G::CS];        // gamma / scale: turns the S diagonal into the QK skip weight
+  alignas(16) float scl[2][G::CS];       // trapezoid key scale gamma_t + dt_{t+1} (1 - sigmoid_{t+1})
+  alignas(16) float wdec[2][G::CS];      // e^{A_end - A_cum}
+  float dec[2];                          // e^{A_end}
+  alignas(16) float fink[G::N];          // the last token's rope'd key (final carry), unscaled
+};
+
+// SO (state only): the pass that produces each segment's exit carry from a zero
+// entering carry; it skips Q, Y_diag, Y_off, the gate and the output.
+template <typename T, int CS, int N, int P, int R, int NW, bool SO>
+__global__ __launch_bounds__(64 * NW, 1)
+void scan_chunked_f32_kernel(ScanArgs a) {
+  typedef Geo<T, CS, N, P, R, NW> G;
+  typedef MF16<T> W;
+  static_assert(sizeof(Smem<G>) <= 160 * 1024, "LDS budget");
+  __shared__ Smem<G> sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave >= 0 && wave < NW);
+  const int bh = xcd_bh(blockIdx.x, gridDim.x, a.Hqk, a.H);
+  const int b = bh / a.H, h = bh % a.H;
+  const int hq = h / (a.H / a.Hqk);
+  const int Lg = a.L, H = a.H, HQ = a.Hqk;
+  // this block's tokens [tb, tb + L); Lnx counts the tokens from tb to the sequence
+  // end (the trapezoid weight of a segment's last token reads the next one)
+  const int seg = blockIdx.y, nseg = gridDim.y;
+  const int tb = a.seg_len > 0 ? seg * a.seg_len : 0;
+  const int L = a.seg_len > 0 ? min(Lg - tb, a.seg_len) : Lg;
+  const int Lnx = Lg - tb;
+  const int nc = (L + CS - 1) / CS;
+  // carry slots: per (b, h) or per (b, h, segment)
+  const int ci_in = a.init_per_seg ? bh * nseg + seg : bh;
+  const int ci_out = a.fin_per_seg ? bh * nseg + seg : bh;
+  const bool has_init = a.init_per_seg || seg == 0;
+  const bool fin_here = a.fin_per_seg || seg == nseg - 1;
+  T* gO = reinterpret_cast<T*>(a.out);
+  const T* gZ = reinterpret_cast<const T*>(a.z);
+  const float* gadt = a.adt + (long)bh * Lg + tb;
+  const float* gdt = a.dt + (long)bh * Lg + tb;
+  const float* gtr = a.trap + (long)bh * Lg + tb;
+  const float Dh = a.D ? a.D[h] : 0.0f;
+  const bool has_z = a.z != nullptr;
+
+  // ---- element offsets of row (b, t=0, head) in each input; rows advance by the stride
+  const int AH = a.ang_shared ? 1 : H;                 // angle rows per token
+  // row strides (elements) are 32-bit; offsets along the sequence are formed in 64 bits
+  const int qk_stride = HQ * N, v_stride = H * P, a_stride = AH * R;
+  // V and Z rows: contiguous (B, L, H, P), or in place in wider rows
+  const int vz_stride = a.vz_tok ? (int)a.vz_tok : v_stride;
+  const long vz_batch = a.vz_bat ? a.vz_bat : (long)Lg * v_stride;
+  // this block's first row of each input (and of the output); the loop only adds t * stride
+  const T* q_base = reinterpret_cast<const T*>(a.q) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
+  const T* k_base = reinterpret_cast<const T*>(a.k) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
+  const long vz_row = (long)b * vz_batch + (long)h * P + (long)tb * vz_stride;
+  const T* v_base = reinterpret_cast<const T*>(a.v) + vz_row;
+  const T* z_base = gZ + vz_row;
+  T* o_base = gO + ((long)b * Lg * H + h) * P + (long)tb * v_stride;
+  const float* ang_base = a.ang + ((long)b * Lg * AH + (a.ang_shared ? 0 : h)) * R + (long)tb * a_stride;
+  for (int i = tid; i < N; i += G::NT) {
+    sm.qb[i] = a.qbias[(long)h * N + i];
+    sm.kb[i] = a.kbias[(long)h * N + i];
+  }
+
+  // ---- staging.  Q/K of chunk c into buffer c % NQK, V into parity c & 1, rotation
+  // rates and scalars into parity c & 1.  A wave waits while the CU's load path drains
+  // the loads queued ahead of its own, so they go to waves with slack: Q/K to the
+  // output waves at the end of their preparation share (single-buffered Q/K: the
+  // auxiliary waves, after the preparation barrier); V, rates and scalars to output
+  // waves 0 and 1 (the two lightest query blocks) at the start of the matrix phase.
+  constexpr int kWQ0 = G::DBQK ? 0 : 8, kWQ1 = G::DBQK ? 1 : 9, kWK0 = G::DBQK ? 2 : 10, kWK1 = G::DBQK ? 3 : 11;
+  constexpr int kWV = 0, kWA = 1;
+  auto stage_qk = [&](int c) {
+    const int t0 = c * CS;
+    const int valid = L - t0;
+    constexpr int JQ = CS * G::SQ / 64;
+    const char* q0 = reinterpret_cast<const char*>(q_base + (long)t0 * qk_stride);
+    const char* k0 = reinterpret_cast<const char*>(k_base + (long)t0 * qk_stride);
+    lds_uint4* dq = (lds_uint4*)sm.rq[c % G::NQK];
+    lds_uint4* dk = (lds_uint4*)sm.rk[c % G::NQK];
+    if (!SO && wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>(dq, q0, qk_stride * G::TS, valid, lane);
+    if (!SO && wave == kWQ1) stage_rows<CS, G::SQ, JQ / 2, JQ>(dq, q0, qk_stride * G::TS, valid, lane);
+    if (wave == kWK0) stage_rows<CS, G::SQ, 0, JQ / 2>(dk, k0, qk_stride * G::TS, valid, lane);
+    if (wave == kWK1) stage_rows<CS, G::SQ, JQ / 2, JQ>(dk, k0, qk_stride * G::TS, valid, lane);
+  };
+  auto stage_v = [&](int c) {
+    const int t0 = c * CS;
+    constexpr int JV = CS * G::SV / 64;
+    if (wave == kWV) {
+      const char* v0 = reinterpret_cast<const char*>(v_base + (long)t0 * vz_stride);
+      stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv[c & 1], v0, vz_stride * G::TS, L - t0, lane);
+    }
+  };
+  auto stage_ars = [&](int c) {
+    const int t0 = c * CS;
+    const int valid = L - t0;
+    constexpr int JA = CS * G::SA / 64;
+    if (wave == kWA) {
+      if (R > 0) {
+        const char* a0 = reinterpret_cast<const char*>(ang_base + (long)t0 * a_stride);
+        stage_rows<CS, G::SA, 0, JA>((lds_uint4*)sm.ra[c & 1], a0, a_stride * 4, valid, lane);
+      }
+      // the bases are made opaque here so that no derived pointer is hoisted out of the
+      // chunk loop (and spilled)
+      const float* pa = gadt + t0;
+      const float* pd = gdt + t0;
+      const float* pt = gtr + t0;
+      asm volatile("" : "+s"(pa), "+s"(pd), "+s"(pt));
+      if (lane < CS && lane < valid) {
+        lds_dma4(pa, 4u * lane, (lds_float*)&sm.rs[c & 1][0][0]);
+        lds_dma4(pd, 4u * lane, (lds_float*)&sm.rs[c & 1][1][0]);
+        lds_dma4(pt, 4u * lane, (lds_float*)&sm.rs[c & 1][2][0]);
+      }
+      if (lane == 0 && t0 + CS < Lnx) {
+        lds_dma4(pd, 4u * CS, (lds_float*)&sm.rs[c & 1][1][CS]);
+        lds_dma4(pt, 4u * CS, (lds_float*)&sm.rs[c & 1][2][CS]);
+      }
+    }
+  };
+
+  // ---- gate (phase 7): thread -> (row, 8-column group) of a chunk's Y tile
+  constexpr int GROUPS = CS * (P / 8);
+  const int erow = tid / (P / 8), egrp = tid % (P / 8);
+  const bool eact = tid < GROUPS;
+  Vec8<T> zr;                              // Z of the chunk waiting for its gate
+  zr.zero();
+  auto load_z = [&](int c) {
+    if (has_z && eact && c * CS + erow < L) zr.load(z_base + (long)(c * CS + erow) * vz_stride + 8 * egrp);
+  };
+  auto gate = [&](int c) {                 // Y of chunk c -> out
+    if (eact && c * CS + erow < L) {
+      const int off = erow * G::LDY + 8 * egrp;
+      Vec8<T> ya, yb;
+      ya.load(&sm.yd[off]);
+      yb.load(&sm.yo[off]);
+      const float ea = sm.expa[c & 1][erow];   // the e^{A_cum} row scale of Q h^T
+      float o[8], ob[8];
+      ya.to_f(o);
+      yb.to_f(ob);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = fmaf(ob[q], ea, o[q]);
+      if (has_z) {
+        float zf[8];
+        zr.to_f(zf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q] *= silu_fast(zf[q]);
+      }
+      store8(o_base + (long)(c * CS + erow) * v_stride + 8 * egrp, o);
+    }
+  };
+
+  // ---- roles: output waves own query block lb = wave (all p-tiles); state waves own
+  // p-tile pr (h^T[:, 16 pr + lane%16], all N rows, as 16x16 accumulators) and the
+  // query blocks lb = part (mod SPT) of Y_off
+  const bool ywave = wave < G::NWY;
+  const bool swave = wave >= G::NWY && wave < G::NWY + G::NST;   // the rest are auxiliary
+  const int sw = wave - G::NWY;
+  const int pr = swave ? sw % G::PT : 0, part = swave ? sw / G::PT : 0;
+  const int pcol = 16 * pr + (lane & 15);
+  const int g4 = 4 * (lane >> 4);              // C-tile row offset of this lane
+  f32x4 hs[G::NB16];
+  {
+    // effective entering state: h0 + (1 - sigmoid(trap_0)) dt_0 (v0 (x) k0)
+    const bool own = a.init_h && has_init && swave;
+    const float cinit = own ? (1.0f - sigmoid_fast(gtr[0])) * gdt[0] : 0.0f;
+    const float v0 = own ? a.init_v[(long)ci_in * P + pcol] : 0.0f;
+#pragma unroll
+    for (int nb = 0; nb < G::NB16; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = 16 * nb + g4 + r;
+        hs[nb][r] = own ? a.init_h[((long)ci_in * P + pcol) * N + n] + cinit * v0 * a.init_k[(long)ci_in * N + n]
+                        : 0.0f;
+      }
+  }
+  float carry[G::QGW][4];
+#pragma unroll
+  for (int k = 0; k < G::QGW; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 4 * G::template qgroup<SO>(wave, k) + j;
+      carry[k][j] = (a.init_theta && has_init && r < R) ? a.init_theta[(long)ci_in * R + r] * kInvTwoPi : 0.0f;  // revolutions
+    }
+  // staging never holds uninitialised bits: rows past the sequence end are not loaded
+  for (int i = tid; i < G::NQK * G::CS * G::SQ; i += G::NT) {
+    (&sm.rq[0][0])[i] = make_uint4(0, 0, 0, 0);
+    (&sm.rk[0][0])[i] = make_uint4(0, 0, 0, 0);
+  }
+  for (int i = tid; i < 2 * G::CS * G::SV; i += G::NT) (&sm.rv[0][0])[i] = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < 2 * G::CS * G::SA; i += G::NT) (&sm.ra[0][0])[i] = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < 2 * 3 * (G::CS + 4); i += G::NT) (&sm.rs[0][0][0])[i] = 0.0f;
+
+  // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
+  // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
+  // the angles of its own rope pairs in registers.
+  // (wave 8 shares a SIMD with the lightest output wave)
+  constexpr int kScalarWave = G::NWY + G::NST;
+  float p_cs[G::QGW][4], p_sn[G::QGW][4];
+  float logdec = 0.0f;                     // state-only pass: sum of the chunks' log-decays
+  auto pre = [&](int cc) {
+    const int t0 = cc * CS;
+    const int pb = cc & 1;
+    const bool tok = lane < CS && t0 + lane < L;
+    const int tl = lane < CS ? lane : 0;
+    const float s_dt = tok ? sm.rs[pb][1][tl] : 0.0f;
+    if (wave == kScalarWave) {
+      const float s_adt = tok ? sm.rs[pb][0][tl] : 0.0f;
+      const float s_tr = tok ? sm.rs[pb][2][tl] : 0.0f;
+      const float sig = sigmoid_fast(s_tr);
+      const float gam = s_dt * sig;
+      const float u = s_dt * (1.0f - sig);                                 // dt (1 - sigmoid), this token
+      float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // next token
+      if (lane == CS - 1) un = (t0 + CS < Lnx) ? sm.rs[pb][1][CS] * (1.0f - sigmoid_fast(sm.rs[pb][2][CS])) : 0.0f;
+      const float scl = gam + un;
+      const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
+      const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
+      if (lane < CS) {
+        const float ablk = __shfl(acum, lane | 15, 64);
+        sm.scl[pb][lane] = scl;
+        sm.wdec[pb][lane] = exp2_fast((aend - acum) * kLog2e);
+        sm.ac2[pb][lane] = acum * kLog2e;
+        sm.expa[pb][lane] = exp2_fast(acum * kLog2e);
+        sm.g16[pb][lane] = exp2_fast((ablk - acum) * kLog2e);
+        sm.dg[pb][lane] = scl != 0.0f ? gam * rcp_fast(scl) : 0.0f;
+        if (lane == 0) sm.dec[pb] = exp2_fast(aend * kLog2e);
+        if constexpr (SO) logdec += aend;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < G::QGW; ++k) {
+      const int g = G::template qgroup<SO>(wave, k);
+      if (g < G::QG && 4 * g < R) {
+        const uint4 rr = staged<G::SA>(sm.ra[pb], tl, g);
+        const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
+                              __uint_as_float(rr.w)};
+        const float hdt = 0.5f * s_dt;
+        // angle in revolutions: carry + prefix of tanh(rate) pi dt / 2pi = tanh(rate) dt / 2,
+        // with tanh(x) = 1 - 2 / (1 + e^{2x}); the fractional part is the reference's
+        // mod-2pi wrap, and the hardware sin/cos take revolutions
+        float d[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          d[j] = fmaf(-s_dt, rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j])), hdt);   // s_dt = 0 past the end
+        wave_incl_scan4(d);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float th = __builtin_amdgcn_fractf(carry[k][j] + d[j]);
+          if constexpr (SO) {            // backward: the angle entering chunk cc (revolutions)
+            if (a.chunk_th && lane == 0) a.chunk_th[((long)bh * nc + cc) * R + 4 * g + j] = carry[k][j];
+          }
+          carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
+          p_cs[k][j] = __builtin_amdgcn_cosf(th);
+          p_sn[k][j] = __builtin_amdgcn_sinf(th);
+        }
+      }
+    }
+  };
+
+  __syncthreads();
+  stage_qk(0);
+  stage_v(0);
+  stage_ars(0);
+  if (nc > 1) stage_ars(1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  pre(0);
+  __syncthreads();   // chunk 0's per-token constants (one wave writes them) before its preparation
+
+  for (int c = 0; c < nc; ++c) {
+    const int t0 = c * CS;
+    const bool tok = lane < CS && t0 + lane < L;
+    const int tl = lane < CS ? lane : 0;        // staging row of this lane
+    const int pc = c & 1;
+    const uint4* sq = sm.rq[c % G::NQK];
+    const uint4* sk = sm.rk[c % G::NQK];
+    const uint4* sv = sm.rv[pc];
+
+    // ================= preparation: lane = token =================
+    // Rows past the sequence end hold stale (finite) inputs: their key scale is 0,
+    // so they add nothing to S or h, and their outputs are never stored.
+    const float scl = sm.scl[pc][tl];
+    // Q/K column groups: rotation angles, biases, rope, key scale
+#pragma unroll
+    for (int k = 0; k < G::QGW; ++k) {
+      const int g = G::template qgroup<SO>(wave, k);
+      if (g < G::QG) {
+        float qf[8], kf[8];
+        {
+          Vec8<T> qv, kv;
+          if constexpr (G::BF) {
+            qv.raw_set(staged<G::SQ>(sq, tl, g));
+            kv.raw_set(staged<G::SQ>(sk, tl, g));
+          } else {
+            qv.raw_set2(staged<G::SQ>(sq, tl, 2 * g), staged<G::SQ>(sq, tl, 2 * g + 1));
+            kv.raw_set2(staged<G::SQ>(sk, tl, 2 * g), staged<G::SQ>(sk, tl, 2 * g + 1));
+          }
+          qv.to_f(qf);
+          kv.to_f(kf);
+        }
+        {
+          const float4* qb4 = reinterpret_cast<const float4*>(&sm.qb[8 * g]);
+          const float4* kb4 = reinterpret_cast<const float4*>(&sm.kb[8 * g]);
+          const float4 qa = qb4[0], qc = qb4[1], ka = kb4[0], kc = kb4[1];
+          const float qbv[8] = {qa.x, qa.y, qa.z, qa.w, qc.x, qc.y, qc.z, qc.w};
+          const float kbv[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            qf[e] += qbv[e];
+            kf[e] += kbv[e];
+          }
+        }
+        if (4 * g < R) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float cs = p_cs[k][j], sn = p_sn[k][j];
+            const float q0 = qf[2 * j], q1 = qf[2 * j + 1];
+            qf[2 * j] = q0 * cs - q1 * sn;
+            qf[2 * j + 1] = q0 * sn + q1 * cs;
+            const float k0 = kf[2 * j], k1 = kf[2 * j + 1];
+            kf[2 * j] = k0 * cs - k1 * sn;
+            kf[2 * j + 1] = k0 * sn + k1 * cs;
+          }
+        }
+        if (tok && t0 + lane == L - 1) store8(&sm.fink[8 * g], kf);   // the final carry's key, written after the loop
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] *= scl;
+        if (lane < CS) {
+          if constexpr (!SO) store8(&sm.q[lane * G::LDQ + 8 * g], qf);
+          store8(&sm.k[lane * G::LDQ + 8 * g], kf);
+        }
+      }
+    }
+    // gate of the previous chunk (its Y tiles were written before the last barrier),
+    // then Z for this chunk's gate, then the loads of the next chunks: the gate's wait
+    // for Z comes before any of them is in flight
+    if (!SO && c > 0) gate(c - 1);
+    if (!SO) load_z(c);
+    if (G::DBQK && c + 1 < nc) stage_qk(c + 1);
+    __syncthreads();
+
+    // single-buffered Q/K staging: every wave has read this chunk's rows
+    if (!G::DBQK && c + 1 < nc) stage_qk(c + 1);
+    if (c + 1 < nc) stage_v(c + 1);
+    if (c + 2 < nc) stage_ars(c + 2);
+
+    // ---- phase 3 for query rows l in [16 lb, 16 lb + 16), all p-tiles (output wave lb):
+    //   Y_diag = mask(K_s Q_r^T)^T V, the mask's diagonal carrying D + gamma QK.
+    // Instantiated per query block so every loop over key blocks is static.
+    auto out_block = [&](auto lb_c) {
+      constexpr int lb = decltype(lb_c)::value;
+      // lane-derived addresses are recomputed here, not kept live across the loop
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int g4l = 4 * (ln >> 4);
+      const int l = 16 * lb + (ln & 15);
+      const float al = sm.ac2[pc][l];
+      const float dgl = sm.dg[pc][l];
+      constexpr int NK = N / W::KSTEP;
+      // query fragments first (B operand of every S^T block), then the key blocks'
+      // chains side by side
+      typename W::frag qf[NK];
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) qf[kk] = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, ln);
+      f32x4 st[lb + 2];
+#pragma unroll
+      for (int sb = 0; sb < lb + 2; ++sb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st[sb][r] = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+        for (int sb = 0; sb <= lb; ++sb)
+          st[sb] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, ln), qf[kk], st[sb]);
+#pragma unroll
+      for (int sb = 0; sb <= lb; ++sb) {
+        const int s0 = 16 * sb + g4l;
+        if (sb < lb) {
+          // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
+          const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
+          const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
+          st[sb][0] *= f * gg.x; st[sb][1] *= f * gg.y; st[sb][2] *= f * gg.z; st[sb][3] *= f * gg.w;
+        } else {
+          // diagonal block: causal decay below the diagonal; on it, D plus the
+          // QK skip gamma_l (q_l . k_l) (the stored key carries the scale)
+          const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
+          const float asv[4] = {as.x, as.y, as.z, as.w};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float v = st[sb][r] * exp2_fast(fminf(al - asv[r], 0.0f));
+            st[sb][r] = (s0 + r < l) ? v : (s0 + r == l ? Dh + st[sb][r] * dgl : 0.0f);
+          }
+        }
+      }
+      f32x4 yd[G::PT];
+#pragma unroll
+      for (int pt = 0; pt < G::PT; ++pt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yd[pt][r] = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp <= lb; sp += 2) {
+#pragma unroll
+        for (int j = 0; j < W::STEPS; ++j) {
+          const typename W::frag mf = W::from_acc(st[sp], st[sp + 1], j);
+#pragma unroll
+          for (int pt = 0; pt < G::PT; ++pt)
+            yd[pt] = W::mma(mf, W::template vdiag<G::SV>(sv, 16 * pt, 16 * sp, j, ln), yd[pt]);
+        }
+      }
+#pragma unroll
+      for (int pt = 0; pt < G::PT; ++pt)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2)
+          store_pair(&sm.yd[(16 * lb + g4l + r) * G::LDY + 16 * pt + (ln & 15)],
+                     &sm.yd[(16 * lb + g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
+    };
+    if (!SO && ywave) {                 // the state-only pass has no Y_diag
+      if (wave == 0) out_block(std::integral_constant<int, 0>{});
+      if (wave == 1) out_block(std::integral_constant<int, 1>{});
+      if constexpr (G::LB16 > 2) {
+        if (wave == 2) out_block(std::integral_constant<int, 2>{});
+        if (wave == 3) out_block(std::integral_constant<int, 3>{});
+      }
+    } else if (swave) {
+      // the state update's decay and per-token weights are read before this wave's
+      // stores (a read issued after them would wait for them too)
+      const float dec = sm.dec[pc];
+      float wv[CS / W::KSTEP][W::WN];
+      auto load_wv = [&]() {
+#pragma unroll
+        for (int ks = 0; ks < CS / W::KSTEP; ++ks) W::load_w(&sm.wdec[pc][W::ktok(ks * W::KSTEP, lane)], wv[ks]);
+      };
+      // ---- phase 6: Y_off = Q_r h^T for my p-tile, query blocks lb = part (mod SPT)
+      if constexpr (!SO) {
+      typename W::frag hf[G::BF ? N / 32 : 1];
+      if constexpr (G::BF) {
+#pragma unroll
+        for (int q = 0; q < N / 32; ++q) hf[q] = W::hfrag(hs[2 * q], hs[2 * q + 1]);
+      }
+      constexpr int NLB = G::LB16 / G::SPT;
+      f32x4 yo[NLB];
+#pragma unroll
+      for (int i = 0; i < NLB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yo[i][r] = 0.0f;
+      if constexpr (G::BF) {
+        // per k-step the query blocks' fragments, then their chains side by side
+#pragma unroll
+        for (int q = 0; q < N / 32; ++q) {
+          typename W::frag qa[NLB];
+#pragma unroll
+          for (int i = 0; i < NLB; ++i) qa[i] = W::qoff(sm.q, G::LDQ, 16 * (part + G::SPT * i), 32 * q, lane);
+#pragma unroll
+          for (int i = 0; i < NLB; ++i) yo[i] = W::mma(qa[i], hf[q], yo[i]);
+        }
+      } else {
+#pragma unroll
+        for (int nb = 0; nb < G::NB16; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < NLB; ++i) {
+              const int l = 16 * (part + G::SPT * i) + (lane & 15);
+              yo[i] = W::mma(sm.q[l * G::LDQ + 16 * nb + g4 + r], hs[nb][r], yo[i]);
+            }
+      }
+      load_wv();
+#pragma unroll
+      for (int i = 0; i < NLB; ++i) {
+        const int lb = part + G::SPT * i;
+#pragma unroll
+        for (int r = 0; r < 4; r += 2)
+          store_pair(&sm.yo[(16 * lb + g4 + r) * G::LDY + pcol], &sm.yo[(16 * lb + g4 + r + 1) * G::LDY + pcol],
+                     yo[i][r], yo[i][r + 1]);
+      }
+      } else {
+        load_wv();
+      }
+      // ---- phases 4-5: h <- e^{A_end} h + K_s^T (w V) for my p-tile
+      if constexpr (SO) {                // backward: the state entering chunk c, [p][n]
+        if (a.chunk_h && part == 0) {
+          T* dst = reinterpret_cast<T*>(a.chunk_h) + ((long)(bh * nc + c) * P + pcol) * N + g4;
+#pragma unroll
+          for (int nb = 0; nb < G::NB16; ++nb) {
+            const float hv[4] = {hs[nb][0], hs[nb][1], hs[nb][2], hs[nb][3]};
+            store4(dst + 16 * nb, hv);
+          }
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < G::NB16; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hs[nb][r] *= dec;
+#pragma unroll
+      for (int ks = 0; ks < CS / W::KSTEP; ++ks) {
+        const typename W::frag vb = W::scale(W::template vstate<G::SV>(sv, 16 * pr, ks * W::KSTEP, lane), wv[ks]);
+#pragma unroll
+        for (int nb = 0; nb < G::NB16; ++nb)
+          hs[nb] = W::mma(W::kstate(sm.k, G::LDQ, ks * W::KSTEP, 16 * nb, lane), vb, hs[nb]);
+      }
+    }
+    if (c + 1 < nc) pre(c + 1);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's staged loads and gate stores are done
+    __syncthreads();
+  }
+  if (!SO && nc > 0) gate(nc - 1);
+
+  // final carry: k of the last token (kept in LDS by its preparation) and its v (still
+  // in the last chunk's staged rows)
+  if (a.fin_k && fin_here && nc > 0) {
+    for (int i = tid; i < N; i += G::NT) a.fin_k[(long)ci_out * N + i] = sm.fink[i];
+    for (int i = tid; i < P; i += G::NT)
+      a.fin_v[(long)ci_out * P + i] =
+          Elem<T>::to_f(*staged_elem<G::SV, T>(sm.rv[(nc - 1) & 1], L - 1 - (nc - 1) * CS, i));
+  }
+  if (a.fin_h && fin_here && swave && part == 0) {
+#pragma unroll
+    for (int nb = 0; nb < G::NB16; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a.fin_h[((long)ci_out * P + pcol) * N + 16 * nb + g4 + r] = hs[nb][r];
+  }
+  if constexpr (SO) {
+    if (a.fin_logdec && fin_here && wave == kScalarWave && lane == 0) a.fin_logdec[ci_out] = logdec;
+  }
+  if (a.fin_theta && fin_here && lane == 0) {
+#pragma unroll
+    for (int k = 0; k < G::QGW; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * G::template qgroup<SO>(wave, k) + j;
+        if (r < R) a.fin_theta[(long)ci_out * R + r] = carry[k][j] * kTwoPi;
+      }
+  }
+}
+
+}  // namespace chunked_f32
+
+// ------------------------------------------------------------------ dispatch
+// (chunk, d_state, headdim, rotation width) instantiations with float32 I/O; R is the
+// model's rope_fraction 0.5 (R = N/4) or 1.0 (R = N/2) width.  Chunk sizes that are
+// multiples of 32 run as 32-token sub-chunks (the chunked form is an exact rewrite of
+// the token recurrence for every chunk size: only the rounding differs).
+#define M3_F32_SHAPES(X)                                                                       \
+  X(32, 128, 64, 32) X(32, 128, 64, 64) X(32, 64, 64, 16) X(32, 64, 64, 32) X(32, 64, 32, 16) \
+  X(32, 32, 32, 8) X(32, 32, 64, 8)
+
+constexpr int kF32Waves = 12;
+
+static int f32_kernel_chunk(int CS) { return (CS > 32 && CS % 32 == 0) ? 32 : CS; }
+
+bool scan_chunked_f32_supported(int CS_, int N, int P, int R) {
+  const int CS = f32_kernel_chunk(CS_);
+#define X(cs, n, p, r) \
+  if (CS == cs && N == n && P == p && R == r) return true;
+  M3_F32_SHAPES(X)
+#undef X
+  return false;
+}
+
+hipError_t scan_chunked_f32_launch(const ScanArgs& a, hipStream_t st) {
+  const int CS = f32_kernel_chunk(a.CS);
+  const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
+#define X(cs, n, p, r)                                                                                 \
+  if (CS == cs && a.N == n && a.P == p && a.R == r) {                                                  \
+    hipLaunchKernelGGL((chunked_f32::scan_chunked_f32_kernel<float, cs, n, p, r, kF32Waves, false>),   \
+                       dim3(a.B * a.H, nseg), dim3(64 * kF32Waves), 0, st, a);                         \
+    return hipGetLastError();                                                                          \
+  }
+  M3_F32_SHAPES(X)
+#undef X
+  return hipErrorInvalidValue;
+}
+
+}  // namespace m3

@@ -51,6 +51,8 @@ def rnn_step_hip(carry: Sequence[torch.Tensor], t_inputs: Sequence[torch.Tensor]
     x, z, Bt, Ct, adt, dt, trap, ang = t_inputs
     angle_mode = angle_mode or recurrent_angle_mode()
     diag_mode = diag_mode or recurrent_diagonal_mode()
+    from .ops import mamba3_contraction_precision_mode
+    mamba3_contraction_precision_mode()     # the reference's decode reads it too (mamba3.py:545)
     _req(angle_mode in ("wrapped", "legacy_unbounded"), "angle_mode must be wrapped or legacy_unbounded")
     _req(diag_mode in ("current", "legacy_double"), "diag_mode must be current or legacy_double")
     B, H, P, N = ssm.shape

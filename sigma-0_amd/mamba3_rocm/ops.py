@@ -13,6 +13,7 @@ returned in ``V.dtype`` (mamba3_ops.py:273).
 """
 from __future__ import annotations
 
+import os
 from typing import Optional, Tuple
 
 import torch
@@ -20,6 +21,27 @@ import torch
 from . import _lib
 
 _IO = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def mamba3_contraction_precision_mode() -> str:
+    """The reference's contraction-precision contract
+    (src/base_model/models/mamba3_jax.py:44-52): MAMBA3_CONTRACTION_PRECISION is
+    "highest" (the default; an empty value means the default) or "default", anything
+    else raises ValueError with the reference's message.  Read on every call, as there.
+
+    "highest" asks for exact float32 contractions, which is what every kernel here
+    computes with float32 I/O (float32 MFMA operands, or float32 arithmetic in the
+    token-recurrent kernel, with float32 accumulation).
+    "default" lets the reference's XLA path use TF32 on its GPUs; gfx950 has no
+    TF32-class matrix instruction and bf16 operands would be coarser than TF32, so it
+    runs the same exact float32 contractions, which satisfy a mode that permits less.
+    With bf16 I/O the operands are bf16 under either mode, with float32 accumulation
+    (the reference's Triton kernel dots in the input dtype, siso_fwd.py:333-345).
+    """
+    mode = os.environ.get("MAMBA3_CONTRACTION_PRECISION") or "highest"
+    if mode not in {"highest", "default"}:
+        raise ValueError("MAMBA3_CONTRACTION_PRECISION must be highest or default")
+    return mode
 
 
 def _req(cond: bool, msg: str) -> None:
@@ -47,6 +69,7 @@ def _stream(t: torch.Tensor) -> int:
 
 def _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z):
     """Validate and normalise to the batched contiguous layout of the C ABI."""
+    mamba3_contraction_precision_mode()
     unbatched = V.dim() == 3
     if unbatched:
         Q, K, V = Q[None], K[None], V[None]
@@ -244,6 +267,7 @@ def mamba3_siso_hip_carry(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None
 def _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z):
     """Validate and normalise the fused path's layout: Q, K (B, L, N) and angle
     rates (B, L, R), shared over the H heads of V (B, L, H, P)."""
+    mamba3_contraction_precision_mode()
     unbatched = V.dim() == 3
     if unbatched:
         Q, K, V, ADT, DT, Trap, angles = Q[None], K[None], V[None], ADT[None], DT[None], Trap[None], angles[None]

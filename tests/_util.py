@@ -43,4 +43,40 @@ def hip_scan(t, chunk_size, no_d=False, no_z=False, seq_split=True):
                            None if no_z else t["Z"], chunk_size, seq_split=seq_split)
 
 
-__all__ = ["I", "M", "rel", "oracle_scan", "to_dev", "hip_scan", "ARG_ORDER"]
+def device_scan_inputs(B, L, H, N, P, R, seed, io_dtype):
+    """Seeded scan inputs generated on the device (for sizes where numpy generation
+    is slow), with the configurations' distributions: x, z ~ N(0,1);
+    dt = softplus(N(-2, 0.5)); A_h = -exp(U[0, ln 16]); B, C and the biases
+    ~ N(0,1)/sqrt(N); D ~ N(0,1); angles ~ U[-pi, pi]; trap ~ U(0,1).  Q, K, V, Z
+    in io_dtype, the rest float32."""
+    import math
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    f = dict(device="cuda", dtype=torch.float32, generator=g)
+    sN = 1.0 / math.sqrt(N)
+    t = dict(Q=(torch.randn(B, L, H, N, **f) * sN).to(io_dtype), K=(torch.randn(B, L, H, N, **f) * sN).to(io_dtype),
+             V=torch.randn(B, L, H, P, **f).to(io_dtype), Z=torch.randn(B, L, H, P, **f).to(io_dtype))
+    t["DT"] = torch.nn.functional.softplus(torch.randn(B, H, L, **f) * 0.5 - 2.0)
+    A = -torch.exp(torch.rand(H, **f) * math.log(16.0))
+    t["ADT"] = (A[None, :, None] * t["DT"]).contiguous()
+    t["Trap"] = torch.rand(B, H, L, **f)
+    t["Angles"] = (torch.rand(B, L, H, R, **f) * 2 - 1) * math.pi
+    t["Q_bias"] = torch.randn(H, N, **f) * sN
+    t["K_bias"] = torch.randn(H, N, **f) * sN
+    t["D"] = torch.randn(H, **f)
+    return t
+
+
+def heads_to_numpy(t, heads):
+    """The inputs of a subset of heads as a standalone float32 numpy problem (the scan
+    is independent per (batch, head)), for the oracle."""
+    import torch
+    idx = torch.as_tensor(heads, device="cuda")
+    sel = dict(Q=(2, "Q"), K=(2, "K"), V=(2, "V"), Z=(2, "Z"), Angles=(2, "Angles"), ADT=(1, "ADT"),
+               DT=(1, "DT"), Trap=(1, "Trap"), Q_bias=(0, "Q_bias"), K_bias=(0, "K_bias"), D=(0, "D"))
+    return {k: t[name].index_select(dim, idx).float().cpu().numpy() for k, (dim, name) in sel.items()}
+
+
+__all__ = ["I", "M", "rel", "oracle_scan", "to_dev", "hip_scan", "ARG_ORDER", "device_scan_inputs",
+           "heads_to_numpy"]

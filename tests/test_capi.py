@@ -68,7 +68,8 @@ def test_kernel_selection(lib):
     assert f(1, 128, 64, 64, 64) == CH          # rope_fraction 1.0
     assert f(1, 128, 64, 32, 32) == CH          # chunk 32
     assert f(0, 64, 64, 16, 64) == CH           # fp32, config 1
-    assert f(0, 128, 64, 32, 64) == GEN         # fp32 with d_state 128
+    assert f(0, 128, 64, 32, 64) == CH          # fp32 at the model's geometry (d_state 128, headdim 64)
+    assert f(0, 128, 64, 0, 64) == GEN          # fp32, d_state 128 without rope
     assert f(1, 128, 64, 32, 128) == CH         # chunk 128: 64-token sub-chunks
     assert f(1, 128, 64, 32, 96) == GEN         # chunk 96: no instantiation
     assert f(1, 64, 16, 16, 16) == GEN          # headdim 16
@@ -255,21 +256,25 @@ def test_bf16_rounding_matches_torch():
 
 def test_layer_scan_validation(lib):
     """m3_layer_scan (x and z read in place from the projection) rejects bad
-    arguments before any launch: dtype, a projection narrower than its fields, rows
-    that are not a multiple of 16 bytes, NULL; m3_layer_pre takes V and Z together."""
+    arguments before any launch: dtype, a projection row that is not exactly its
+    fields' width (the layout m3_layer_pre reads), rows that are not a multiple of 16
+    bytes, NULL; m3_layer_pre takes V and Z together."""
     from mamba3_rocm import _lib
     fake = 1 << 20                      # never dereferenced: every call fails validation first
     H, N, P, R = 4, 128, 64, 32
     full = 2 * H * P + 2 * N + 3 * H + R      # 812 elements: 1624 bytes in bf16, not a multiple of 16
 
-    def scan(proj, d_in_proj, io=_lib.DTYPE_BF16):
+    def scan(proj, d_in_proj, io=_lib.DTYPE_BF16, heads=H):
         return lib.m3_layer_scan(fake, fake, proj, d_in_proj, fake, fake, fake, fake, fake, fake, fake, fake,
-                                 2, 64, H, N, P, R, 64, io, None, 0, None)
-    assert scan(fake, full + 4, io=7) == _lib.M3_E_ARG
+                                 2, 64, heads, N, P, R, 64, io, None, 0, None)
+    assert scan(fake, full, io=7) == _lib.M3_E_ARG
     assert scan(fake, full - 1) == _lib.M3_E_ARG
+    assert scan(fake, full + 4) == _lib.M3_E_ARG          # padded rows: m3_layer_pre reads the exact width
+    assert b"width" in lib.m3_last_error()
     assert scan(fake, full) == _lib.M3_E_ALIGN
     assert b"16" in lib.m3_last_error()
-    assert scan(None, full + 4) == _lib.M3_E_ARG
+    full8 = 2 * 8 * P + 2 * N + 3 * 8 + R     # 1336 elements: 16-byte rows in bf16
+    assert scan(None, full8, heads=8) == _lib.M3_E_ARG
     assert lib.m3_layer_pre(fake, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, fake,
                             2, 64, H, P, N, R, 1e-4, 1e-6, _lib.DTYPE_BF16, None) == _lib.M3_E_ARG
 
@@ -301,3 +306,27 @@ def test_block_entry_points_validate(lib):
     assert an(fake, None, fake, 4096, None, fake, fake, 4096, 2, 8, 64, 1e-6, 2, bf, bf, None) == _lib.M3_E_ARG
     assert b"alias" in lib.m3_last_error()
     assert an(fake, None, fake, fake, None, fake, fake, 4096, 0, 8, 64, 1e-6, 2, bf, bf, None) == _lib.M3_OK
+
+
+def test_contraction_precision_knob(monkeypatch):
+    """MAMBA3_CONTRACTION_PRECISION follows the reference's contract
+    (mamba3_jax.py:44-52): highest by default (also when empty), default accepted,
+    anything else raises its ValueError -- at the entry points too, before any
+    device work."""
+    import torch
+    from mamba3_rocm import mamba3_contraction_precision_mode, mamba3_siso_hip, rnn_step_hip
+    monkeypatch.delenv("MAMBA3_CONTRACTION_PRECISION", raising=False)
+    assert mamba3_contraction_precision_mode() == "highest"
+    monkeypatch.setenv("MAMBA3_CONTRACTION_PRECISION", "")
+    assert mamba3_contraction_precision_mode() == "highest"
+    monkeypatch.setenv("MAMBA3_CONTRACTION_PRECISION", "default")
+    assert mamba3_contraction_precision_mode() == "default"
+    for bad in ("tf32", "HIGHEST", "high"):
+        monkeypatch.setenv("MAMBA3_CONTRACTION_PRECISION", bad)
+        with pytest.raises(ValueError, match="MAMBA3_CONTRACTION_PRECISION must be highest or default"):
+            mamba3_contraction_precision_mode()
+        t = torch.zeros(1)
+        with pytest.raises(ValueError, match="MAMBA3_CONTRACTION_PRECISION must be highest or default"):
+            mamba3_siso_hip(t, t, torch.zeros(4, 2, 8), t, t, t, t, t, t)
+        with pytest.raises(ValueError, match="MAMBA3_CONTRACTION_PRECISION must be highest or default"):
+            rnn_step_hip((t, t, t, t), (t,) * 8, t, t, t)

@@ -16,16 +16,21 @@ from oracle import mamba3_layer as ML
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("B,L,d_model,N,headdim,bf16,path", [
-    (2, 200, 128, 128, 64, True, "copies"),     # model geometry per head; 812-wide rows: x, z copied
-    (2, 330, 256, 128, 64, True, "in_place"),   # 1336-wide bf16 rows (16-byte multiple): read in place
-    (1, 1100, 64, 128, 64, True, "copies"),     # B*H small: the scan's sequence split
-    (2, 150, 64, 64, 32, False, "in_place"),    # fp32: chunked kernel shapes, 412-wide rows in place
-    (1, 100, 1024, 256, 64, True, "copies"),    # d_state 256: generic scan; layer_pre tiles of 32 tokens
+@pytest.mark.parametrize("B,L,d_model,N,headdim,bf16,path,split", [
+    (2, 200, 128, 128, 64, True, "copies", False),    # model geometry per head; 812-wide rows: x, z copied
+    (2, 330, 256, 128, 64, True, "in_place", False),  # 1336-wide bf16 rows (16-byte multiple): read in place
+    (1, 1100, 64, 128, 64, True, "copies", True),     # B*H small: the scan's sequence split
+    (1, 1100, 256, 128, 64, True, "in_place", True),  # in place and split (config 5's route: strided V/Z
+                                                      # offsets in the state-only and per-segment passes)
+    (2, 150, 64, 64, 32, False, "in_place", False),   # fp32: chunked kernel shapes, 412-wide rows in place
+    (1, 100, 1024, 256, 64, True, "copies", False),   # d_state 256: generic scan; layer_pre tiles of 32 tokens
 ])
-def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16, path):
+def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16, path, split):
     import torch
-    from mamba3_rocm import Mamba3Layer
+    from mamba3_rocm import Mamba3Layer, _lib
+    H, R = 2 * d_model // headdim, N // 4
+    io = _lib.DTYPE_BF16 if bf16 else _lib.DTYPE_F32
+    assert (_lib.load().m3_chunk_scan_ws_bytes(B, L, H, N, headdim, R, 64, io) > 0) == split
     p = ML.init_params(d_model, seed=51, d_state=N, headdim=headdim)
     x = np.random.default_rng(52).standard_normal((B, L, d_model)).astype(np.float32)
     dt = torch.bfloat16 if bf16 else torch.float32
@@ -203,3 +208,31 @@ def test_block_kernels_match_torch_fp32(B, L, D, bf16):
     want = torch.log_softmax(logits.double(), dim=-1)
     _lib.check(lib.m3_log_softmax(logits.data_ptr(), logits.data_ptr(), B, L, D, st), "m3_log_softmax")
     assert ((logits.double() - want).abs() <= 1e-6 * (1 + want.abs())).all(), "log_softmax"
+
+
+def test_layer_post_with_a_scale_that_is_not_16_byte_aligned():
+    """m3_layer_post's 16-byte path reads the norm scale eight at a time; a scale
+    pointer that is only 4-byte aligned takes the element path, with the same result."""
+    import torch
+    from mamba3_rocm import _lib
+    lib = _lib.load()
+    B, L, D = 2, 37, 768
+    g = torch.Generator(device="cuda")
+    g.manual_seed(71)
+    y = torch.randn(B, L, D, device="cuda", generator=g).to(torch.bfloat16)
+    buf = torch.empty(D + 1, device="cuda")
+    buf[1:] = 1.0 + 0.1 * torch.randn(D, device="cuda", generator=g)
+    offset = buf[1:]                                    # 4 bytes past a 16-byte boundary
+    aligned = offset.clone()
+    assert offset.data_ptr() % 16 == 4 and aligned.data_ptr() % 16 == 0
+    outs = []
+    for scale in (aligned, offset):
+        out = torch.empty_like(y)
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = lib.m3_layer_post(y.data_ptr(), scale.data_ptr(), out.data_ptr(), B, L, D, 1e-6, _lib.DTYPE_BF16,
+                               stream)
+        assert rc == 0, lib.m3_last_error()
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0].float()).all()
+    assert torch.equal(outs[0], outs[1])

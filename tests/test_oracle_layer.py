@@ -112,3 +112,42 @@ def test_lm_head_is_normalised_and_shift_invariant():
     feats = MS.stack_forward(p, ids, d_state=16, headdim=16)
     z = feats @ p["decoder_w"].astype(np.float64) + p["decoder_b"]
     assert np.allclose(np.argmax(lp, -1), np.argmax(z, -1))
+
+
+def test_stack_oracle_glu_variants_closed_forms():
+    """The GLU activations of layers.py:126-141 with m the mixer output and g = gelu(m):
+    full_glu = out1(g) sigmoid(out2(g)), half_glu1 = g sigmoid(out2(g)),
+    half_glu2 = m sigmoid(out2(g)).  Two special cases fix the wiring:
+    (1) out2's kernel zero and bias b: the gate is the constant sigmoid(b), so the
+        gated tensor shows (g, m, or out1(g));
+    (2) out2 = alpha I without bias and out1 = I: the gate is sigmoid(alpha g), so a
+        gate fed m instead of g, or out1 and out2 swapped, fails."""
+    from oracle import mamba3_stack as MS
+    D = 32
+    p = MS.init_params(vocab=11, d_model=D, n_layers=1, seed=12, d_state=16, headdim=16)
+    lp = p["layers"][0]
+    ids = np.random.default_rng(13).integers(0, 11, size=(2, 20))
+    emb = p["embed"][ids].astype(np.float64)
+    m = ML.layer_forward(lp["mixer"], MS.layernorm(emb, lp["ln_scale"], lp["ln_bias"]), d_state=16, headdim=16)
+    g = MS.gelu(m)
+    assert np.abs(m).max() > 0.1 and np.abs(g - m).max() > 0.1, "the mixer output must be non-trivial"
+
+    def block(act):   # prenorm: x + act(mixer(LN(x)))
+        return MS.stack_forward(p, ids, activation=act, prenorm=True, d_state=16, headdim=16) - emb
+
+    b = np.random.default_rng(14).standard_normal(D)
+    lp["out2_w"], lp["out2_b"] = np.zeros((D, D), np.float32), b.astype(np.float32)
+    s = MS.sigmoid(b.astype(np.float32).astype(np.float64))
+    out1 = g @ lp["out1_w"].astype(np.float64) + lp["out1_b"]
+    assert np.allclose(block("half_glu1"), g * s, atol=1e-10)
+    assert np.allclose(block("half_glu2"), m * s, atol=1e-10)
+    assert np.allclose(block("full_glu"), out1 * s, atol=1e-10)
+
+    alpha = 3.0
+    lp["out2_w"], lp["out2_b"] = (alpha * np.eye(D)).astype(np.float32), np.zeros(D, np.float32)
+    lp["out1_w"], lp["out1_b"] = np.eye(D, dtype=np.float32), np.zeros(D, np.float32)
+    gate = MS.sigmoid(alpha * g)
+    assert np.allclose(block("half_glu1"), g * gate, atol=1e-10)
+    assert np.allclose(block("half_glu2"), m * gate, atol=1e-10)
+    assert np.allclose(block("full_glu"), g * gate, atol=1e-10)
+    assert not np.allclose(block("half_glu2"), m * MS.sigmoid(alpha * m), atol=1e-3)

@@ -45,7 +45,10 @@ F32_SHAPES = [
     (1, 70, 2, 64, 16, 16, 16),       # reference unit-test shapes (generic kernel for P=16)
     (1, 128, 3, 64, 16, 32, 32),
     (1, 200, 2, 128, 32, 32, 64),
-    (1, 1024, 4, 128, 64, 32, 64),    # reference GPU test shape (fp32, N=128)
+    (1, 1024, 4, 128, 64, 32, 64),    # reference GPU test shape (fp32, N=128): the float32 chunked kernel
+    (1, 333, 2, 128, 64, 64, 64),     # fp32 model geometry, rope on every state pair
+    (2, 97, 4, 128, 64, 32, 32),      # fp32 model geometry, ragged L, chunk 32
+    (1, 300, 2, 128, 64, 32, 128),    # fp32 model geometry, chunk 128: 32-token sub-chunks
     (2, 333, 4, 64, 32, 16, 32),
     (1, 97, 2, 32, 64, 8, 64),
     (1, 300, 2, 64, 64, 16, 128),     # chunk 128: 64-token sub-chunks
@@ -94,6 +97,8 @@ def test_gqa_heads(bf16):
     assert err <= (BF16_TOL if bf16 else F32_TOL)
     err = _run(1, 300, 4, 64, 64, 16, 64, bf16=bf16, seed=5, Hqk=1)
     assert err <= (BF16_TOL if bf16 else F32_TOL)
+    err = _run(1, 200, 4, 128, 64, 32, 64, bf16=bf16, seed=10, Hqk=2)     # the model's geometry
+    assert err <= (BF16_TOL if bf16 else F32_TOL)
 
 
 @pytest.mark.parametrize("bf16", [False, True])
@@ -140,13 +145,13 @@ def test_headline_config_subset_and_chunk_invariance():
         assert err <= BF16_TOL
 
 
-@pytest.mark.parametrize("bf16", [False, True])
-def test_repeat_calls_bitwise_identical(bf16):
+@pytest.mark.parametrize("bf16,N", [(False, 64), (False, 128), (True, 128)])
+def test_repeat_calls_bitwise_identical(bf16, N):
     """The kernels use no atomics and no cross-workgroup communication, so repeated
     calls must give bitwise-identical outputs; a race between waves (for example
     a read of per-chunk constants before the wave that writes them) shows up here."""
     torch = _torch()
-    B, L, H, N, P, R = (2, 2048, 16, 128, 64, 32) if bf16 else (2, 1024, 8, 64, 64, 16)
+    B, L, H, P, R = (2, 2048, 16, 64, N // 4) if bf16 else (2, 1024, 8, 64, N // 4)
     d = I.scan_inputs(B, L, H, N, P, R, seed=11, bf16=bf16)
     t = to_dev(d, torch.bfloat16 if bf16 else torch.float32)
     first = hip_scan(t, 64)
