@@ -50,7 +50,7 @@ void decode_step_kernel(DecodeArgs a) {
   __shared__ float sCos[kDecMaxN / 2], sSin[kDecMaxN / 2];
   __shared__ float sB[kDecMaxN], sKp[kDecMaxN], sC[kDecMaxN];
   __shared__ float sX[kDecMaxP], sVp[kDecMaxP], sY[kDecMaxP];
-  __shared__ float sQK;
+  __shared__ float sQK[kDecThreads / 64];   // legacy_double: per-wave sums of the QK dot
 
   // 1. issue the state loads first
   f32x4* hrow = reinterpret_cast<f32x4*>(a.h + (long)bh * P * N);
@@ -85,7 +85,6 @@ void decode_step_kernel(DecodeArgs a) {
     sCos[r] = c;
     sSin[r] = s;
   }
-  if (tid == 0) sQK = 0.0f;
   __syncthreads();
 
   // 3. rotated key/query for this step; new carries
@@ -109,7 +108,11 @@ void decode_step_kernel(DecodeArgs a) {
     a.kprev[bhN + n0 + 1] = b1;
     qk_part += c0 * b0 + c1 * b1;
   }
-  if (a.legacy_double) atomicAdd(&sQK, qk_part);
+  if (a.legacy_double) {
+    // butterfly sum within the wave, then the waves' sums in order: deterministic
+    for (int o = 32; o > 0; o >>= 1) qk_part += __shfl_xor(qk_part, o);
+    if ((tid & 63) == 0) sQK[tid >> 6] = qk_part;
+  }
   for (int p = tid; p < P; p += kDecThreads) a.vprev[bhP + p] = sX[p];
   __syncthreads();
 
@@ -143,7 +146,11 @@ void decode_step_kernel(DecodeArgs a) {
 
   // 5. output
   const float Dh = a.D ? a.D[hh] : 0.0f;
-  const float qk = a.legacy_double ? sQK * (dtv * trv) : 0.0f;
+  float qk = 0.0f;
+  if (a.legacy_double) {
+    for (int w = 0; w < kDecThreads / 64; ++w) qk += sQK[w];
+    qk *= dtv * trv;
+  }
   for (int p = tid; p < P; p += kDecThreads) {
     float yv = sY[p] + Dh * sX[p];
     if (a.legacy_double) yv += qk * sX[p];

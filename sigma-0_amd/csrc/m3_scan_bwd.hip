@@ -727,24 +727,43 @@ __global__ __launch_bounds__(64 * kFinWaves)
 void scan_bwd_finish_kernel(BwdArgs a) {
   __shared__ float part[kFinWaves][64];
   __shared__ float carry[65];                // [0]: dA of the later chunks, [1 + r]: d(theta)
+  __shared__ float total[65];                // the same over every chunk
   __shared__ float tdth[CS][65];             // d(theta), then dAngles, of (token, pair)
   __shared__ float tang[CS][65];             // angle rates
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x, bh = blockIdx.y, b = bh / a.s.H, h = bh % a.s.H;
   const int L = a.s.L, H = a.s.H, R = a.s.R, nc = a.nc;
   const float kPi = 3.14159265358979323846f;
-  // suffix sums of the chunk totals over chunks c+1.., one value per wave pass
+  // suffix sums of the chunk totals over chunks c+1.., and their sum over all chunks,
+  // one value per wave pass
   for (int v = wave; v <= R; v += kFinWaves) {
-    float s = 0.0f;
-    for (int cc = c + 1 + lane; cc < nc; cc += 64) s += a.ctot[((long)bh * nc + cc) * (R + 1) + v];
+    float s = 0.0f, s_all = 0.0f;
+    for (int cc = lane; cc < nc; cc += 64) {
+      const float x = a.ctot[((long)bh * nc + cc) * (R + 1) + v];
+      s_all += x;
+      if (cc > c) s += x;
+    }
     s = wave_sum(s);
-    if (lane == 0) carry[v] = s;
+    s_all = wave_sum(s_all);
+    if (lane == 0) {
+      carry[v] = s;
+      total[v] = s_all;
+    }
   }
   __syncthreads();
   const int t = c * CS + lane;
   const bool tok = lane < CS && t < L;
   const long o = (long)bh * L + t;
   const float dt = tok ? a.s.dt[o] : 0.0f;
+  // The output depends on the angles and on A only through differences theta_t -
+  // theta_s and A_t - A_s (there is no initial carry), so the per-token d(theta) and
+  // dA sum to exactly zero over the sequence, for every pair.  The reverse cumsum S_t
+  // of the computed values then carries the whole sequence's rounding error at t = 0,
+  // where the true value is 0.  S_t - T (L - t) / L, with T the computed total, is
+  // the blend (t / L) S_t - ((L - t) / L) F_t of the reverse sum and the negated
+  // forward sum F_t = T - S_t: the same value in exact arithmetic, and the
+  // minimum-variance combination of the two when the per-token errors are independent.
+  const float wfwd = (float)(L - t) / (float)L;
   const int nt = min(CS, L - c * CS);                                // tokens of this chunk
   const long row0 = (((long)b * L + c * CS) * H + h) * R;           // (token 0, pair 0)
   const int AH = a.s.ang_shared ? 1 : H;                             // angle-rate rows per token
@@ -758,7 +777,7 @@ void scan_bwd_finish_kernel(BwdArgs a) {
   float angp = 0.0f;
   for (int r = wave; r < R; r += kFinWaves) {
     const float d = tok ? tdth[lane][r] : 0.0f;
-    const float sum = wave_rev_scan(d, lane) + carry[1 + r];
+    const float sum = wave_rev_scan(d, lane) + carry[1 + r] - total[1 + r] * wfwd;
     if (tok) {
       const float tn = tanhf(tang[lane][r]);
       tdth[lane][r] = sum * kPi * dt * (1.0f - tn * tn);
@@ -773,7 +792,7 @@ void scan_bwd_finish_kernel(BwdArgs a) {
   }
   if (wave == 0) {
     const float dA = tok ? a.dadt[o] : 0.0f;
-    const float sum = wave_rev_scan(dA, lane) + carry[0];
+    const float sum = wave_rev_scan(dA, lane) + carry[0] - total[0] * wfwd;
     float angd = 0.0f;
     for (int w = 0; w < kFinWaves; ++w) angd += part[w][lane];
     if (tok) {

@@ -24,6 +24,7 @@ void scan_generic_kernel(ScanArgs a) {
   __shared__ float sTh[kGenMaxN / 2], sCos[kGenMaxN / 2], sSin[kGenMaxN / 2];
   __shared__ float sQ[kGenMaxN], sK[kGenMaxN], sKp[kGenMaxN];
   __shared__ float sX[kGenMaxP], sVp[kGenMaxP], sY[kGenMaxP];
+  __shared__ float sPart[kGenThreads];   // G > 1: row p's partial dot products at p * G + g
 
   const int tid = threadIdx.x;
   const int bh = blockIdx.x;
@@ -43,13 +44,13 @@ void scan_generic_kernel(ScanArgs a) {
   for (int e = tid; e < P * N; e += kGenThreads) sH[e] = a.init_h ? a.init_h[(long)bh * P * N + e] : 0.0f;
   for (int r = tid; r < R; r += kGenThreads) sTh[r] = a.init_theta ? a.init_theta[(long)bh * R + r] : 0.0f;
   for (int n = tid; n < N; n += kGenThreads) sKp[n] = a.init_k ? a.init_k[(long)bh * N + n] : 0.0f;
-  for (int p = tid; p < P; p += kGenThreads) {
-    sVp[p] = a.init_v ? a.init_v[(long)bh * P + p] : 0.0f;
-    sY[p] = 0.0f;
-  }
+  for (int p = tid; p < P; p += kGenThreads) sVp[p] = a.init_v ? a.init_v[(long)bh * P + p] : 0.0f;
   __syncthreads();
 
-  // row-slice mapping for the state update: G threads per state row
+  // row-slice mapping for the state update: G threads per state row (thread p * G + g
+  // takes columns g, g + G, ...).  With G > 1 every row has one pass (P * G <= the
+  // block) and its G partial dot products are summed in a fixed order, so the result
+  // does not depend on thread timing; with G = 1 a thread owns whole rows.
   int G = kGenThreads / P;
   if (G < 1) G = 1;
   int gpow = 1;
@@ -97,16 +98,20 @@ void scan_generic_kernel(ScanArgs a) {
         sH[p * N + n] = v;
         part += sQ[n] * v;
       }
-      atomicAdd(&sY[p], part);
+      if (G == 1) sY[p] = part;
+      else sPart[tid] = part;
     }
     __syncthreads();
     // D: output, carries
     for (int p = tid; p < P; p += kGenThreads) {
-      float y = sY[p] + Dh * sX[p];
+      float acc = 0.0f;
+      if (G == 1) acc = sY[p];
+      else
+        for (int j = 0; j < G; ++j) acc += sPart[p * G + j];
+      float y = acc + Dh * sX[p];
       if (Z) y *= silu_fast(Elem<T>::to_f(Z[(tok * H + h) * P + p]));
       O[(tok * H + h) * P + p] = Elem<T>::from_f(y);
       sVp[p] = sX[p];
-      sY[p] = 0.0f;
     }
     for (int n = tid; n < N; n += kGenThreads) sKp[n] = sK[n];
     __syncthreads();

@@ -68,6 +68,14 @@ def test_decode_modes(angle_mode, diag_mode):
     assert rel(c[0], cr[0]) <= 1e-4
 
 
+def test_decode_legacy_double_bitwise_repeatable():
+    """legacy_double's QK dot is summed in a fixed order (no atomics): repeated steps
+    from the same carry give bitwise-identical outputs."""
+    ys = [_decode(2, 3, 128, 64, 32, steps=3, seed=14, bf16=True, diag_mode="legacy_double")[0]
+          for _ in range(3)]
+    assert all(np.array_equal(ys[0], y) for y in ys[1:])
+
+
 def test_decode_bf16_output():
     import torch
     y, yr, _, _ = _decode(2, 2, 128, 64, 32, steps=4, seed=13, bf16=True, out_dtype=torch.bfloat16)

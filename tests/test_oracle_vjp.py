@@ -83,3 +83,47 @@ def test_every_gradient_is_exercised():
     _, grads = V.vjp(d, cot, 8)
     for name, g in zip(V.NAMES, grads):
         assert np.abs(g).max() > 1e-3, f"d{name} is (nearly) zero in the test problem"
+
+
+def test_shift_invariances_of_angles_and_decay():
+    """The backward's finishing pass relies on two exact facts of the operator: it
+    depends on the rope angles and on the decay prefix A only through differences
+    (theta_t - theta_s, A_t - A_s), so shifting every token's angle of one pair (by
+    changing token 0's rate) or every A_t (token 0's adt) leaves the output unchanged,
+    and the per-token d(theta) and dA sum to zero: dADT and dAngles vanish at token 0.
+    A planted mistake that breaks the difference form (keys left unrotated) makes the
+    forward check fail."""
+    B, L, H, N, P, R = 1, 50, 2, 16, 8, 4
+    d = I.scan_inputs(B, L, H, N, P, R, seed=21, Hqk=1)
+    d = {k: np.asarray(v, dtype=np.float64) for k, v in d.items()}
+
+    def fwd(dd):
+        return M.mamba3_ssd_chunked_batched(
+            dd["Q"], dd["K"], dd["V"], dd["ADT"], dd["DT"], dd["Trap"], dd["Angles"], dd["Q_bias"],
+            dd["K_bias"], dd["D"], dd["Z"], chunk_size=8)
+
+    y0 = fwd(d)
+    e = dict(d)
+    e["Angles"] = d["Angles"].copy()
+    e["Angles"][:, 0, :, 1] += 0.9          # pair 1 of every head turns by a constant
+    e["ADT"] = d["ADT"].copy()
+    e["ADT"][:, :, 0] -= 0.7                # every A_t moves by the same amount
+    assert np.abs(fwd(e) - y0).max() <= 1e-12 * np.abs(y0).max()
+    # the same shift through a rope that is not a difference form changes the output
+    rot, calls = M.apply_rope, [0]
+
+    def q_only(x, c, s):                    # calls alternate Q, K: leave K unrotated
+        calls[0] += 1
+        return rot(x, c, s) if calls[0] % 2 else x
+    try:
+        M.apply_rope = q_only
+        planted0, planted1 = fwd(d), fwd(e)
+    finally:
+        M.apply_rope = rot
+    assert np.abs(planted1 - planted0).max() > 1e-3 * np.abs(y0).max()
+
+    cot = V.cotangent(B, L, H, P, seed=22)
+    _, g = V.vjp(d, cot, 8)
+    gd = dict(zip(V.NAMES, g))
+    assert np.abs(gd["ADT"][:, :, 0]).max() <= 1e-12 * np.abs(gd["ADT"]).max()
+    assert np.abs(gd["Angles"][:, 0]).max() <= 1e-12 * np.abs(gd["Angles"]).max()

@@ -145,13 +145,19 @@ def test_headline_config_subset_and_chunk_invariance():
         assert err <= BF16_TOL
 
 
-@pytest.mark.parametrize("bf16,N", [(False, 64), (False, 128), (True, 128)])
-def test_repeat_calls_bitwise_identical(bf16, N):
+@pytest.mark.parametrize("bf16,N,P,R,impl", [(False, 64, 64, 16, 1), (False, 128, 64, 32, 1),
+                                              (True, 128, 64, 32, 1), (False, 128, 64, 0, 2),
+                                              (True, 48, 16, 12, 2)])
+def test_repeat_calls_bitwise_identical(bf16, N, P, R, impl):
     """The kernels use no atomics and no cross-workgroup communication, so repeated
     calls must give bitwise-identical outputs; a race between waves (for example
-    a read of per-chunk constants before the wave that writes them) shows up here."""
+    a read of per-chunk constants before the wave that writes them) shows up here.
+    The last two cases take the generic kernel (impl 2), whose per-row dot products
+    are summed in a fixed order."""
     torch = _torch()
-    B, L, H, P, R = (2, 2048, 16, 64, N // 4) if bf16 else (2, 1024, 8, 64, N // 4)
+    from mamba3_rocm import _lib
+    assert _lib.load().m3_chunk_scan_impl(int(bf16), N, P, R, 64) == impl
+    B, L, H = ((2, 2048, 16) if bf16 else (2, 1024, 8)) if impl == 1 else (2, 300, 4)
     d = I.scan_inputs(B, L, H, N, P, R, seed=11, bf16=bf16)
     t = to_dev(d, torch.bfloat16 if bf16 else torch.float32)
     first = hip_scan(t, 64)

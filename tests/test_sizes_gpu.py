@@ -6,7 +6,9 @@ that the float64 oracle finishes quickly).
   float64 oracle (bf16 bar 2e-2), and the split against one pass over the whole
   output.
 * The backward at configuration 2's length, L=4096 (and 5120), on two heads: every
-  gradient against autograd of the float64 oracle (bf16 bar 3e-2).
+  gradient against autograd of the float64 oracle (bar 2e-2, tighter than the
+  suite's 3e-2 for bf16 gradients: the whole-sequence cumsums behind dADT, dDT and
+  dAngles are the ones that lose precision with length).
 * Configuration 5, the 12-layer backbone at L=12288: batch row 0 against the oracle
   backbone's log-probabilities (a committed fixture, tests/golden/
   make_golden_config5.py: the oracle takes minutes at this size): 64 positions within
@@ -22,7 +24,7 @@ from _util import I, M, device_scan_inputs, heads_to_numpy, rel
 pytestmark = pytest.mark.gpu
 
 BF16_TOL = 2e-2
-GRAD_TOL = 3e-2
+GRAD_TOL = 2e-2
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
