@@ -24,6 +24,9 @@
 //      cumsums over the sequence, the trapezoid and angle chains), and
 //      scan_bwd_reduce_kernel sums the bias and D gradients over batch and chunks.
 // Every sum runs in a fixed order, so the gradients are deterministic.
+#include <stdlib.h>
+#include <string.h>
+
 #include <type_traits>
 
 #include "m3_chunk_common.h"
@@ -714,6 +717,632 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
   }
 }
 
+// ------------------------------------------------ reverse walk (adjoint fused in)
+// One workgroup per (b, h) walks the chunks from the last to the first.  The adjoint
+// state G (N x P, float32) stays in MFMA accumulators for the whole walk, as the
+// forward keeps the state: each chunk writes G_c, the adjoint state after it, to LDS
+// for its dV and dk~ products, then advances G <- e^{A_end} G + sum_t e^{A_cum,t}
+// dy_t (x) q~_t with its own q~ and dy.  Against the chunk-parallel route this removes
+// the adjoint pass (a second read of Q, dOut, Z and the rates) and the round trip of
+// every G_c through the workspace.  The next chunk's global inputs are requested
+// before the current chunk's work, so their latency hides behind it.  The bias and D
+// gradients are summed in registers over the walk, and the reverse cumsums of dA and
+// d(theta) over the sequence are carried from chunk to chunk: the walk writes the
+// suffix sums themselves (and their totals), which scan_bwd_walk_finish_kernel turns
+// into dADT, dAngles, dDT and dTrap.
+template <typename T, int CS, int N, int P, int R>
+struct WalkLoads {
+  static constexpr int GH = N / 16;                                       // column groups per half
+  static constexpr int HP = (P * N / 8 + kBwdThreads - 1) / kBwdThreads;  // 8-element state pieces per thread
+  static constexpr int VGW = (P / 8 + kBwdWaves - 1) / kBwdWaves;         // value groups per wave
+  Vec8<T> hpc[HP], qraw[2], kraw[2], vraw[VGW], dyraw[VGW], zraw[VGW];
+  float4 rates[2], th0[2];
+  float adt, dt, trap, dtn, trapn;
+  // Every load is unconditional, from a clamped valid address where a lane or wave has
+  // nothing to load; the unused values are ignored.
+  __device__ __forceinline__ void issue(const BwdArgs& a, int c, int bh, int tid, int wave, int lane) {
+    const int b = bh / a.s.H, h = bh % a.s.H, hq = h / (a.s.H / a.s.Hqk);
+    const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc, t0 = c * CS;
+    const int tcl = min(t0 + lane, L - 1);
+    const long qrow = (((long)b * L + tcl) * HQ + hq) * N;
+    const long vrow = (((long)b * L + tcl) * H + h) * P;
+    const T* hsrc = reinterpret_cast<const T*>(a.hs) + ((long)bh * nc + c) * P * N;
+#pragma unroll
+    for (int k = 0; k < HP; ++k) hpc[k].load(hsrc + 8 * min(tid + k * kBwdThreads, P * N / 8 - 1));
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int g = min(hh * GH + wave, N / 8 - 1);
+      qraw[hh].load(reinterpret_cast<const T*>(a.s.q) + qrow + 8 * g);
+      kraw[hh].load(reinterpret_cast<const T*>(a.s.k) + qrow + 8 * g);
+      rates[hh] = th0[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (R > 0) {
+        const int gr = min(g, R / 4 - 1);
+        const long arow = a.s.ang_shared ? (long)b * L + tcl : ((long)b * L + tcl) * H + h;
+        rates[hh] = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * gr);
+        th0[hh] = *reinterpret_cast<const float4*>(a.th0 + ((long)bh * nc + c) * R + 4 * gr);
+      }
+    }
+    const long srow = (long)bh * L;
+    const int tn = min(t0 + CS, L - 1);
+    adt = a.s.adt[srow + tcl];
+    dt = a.s.dt[srow + tcl];
+    trap = a.s.trap[srow + tcl];
+    dtn = a.s.dt[srow + tn];
+    trapn = a.s.trap[srow + tn];
+    const T* gv = reinterpret_cast<const T*>(a.s.v);
+    const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) : gv;
+#pragma unroll
+    for (int k = 0; k < VGW; ++k) {
+      const int g = min(wave + k * kBwdWaves, P / 8 - 1);
+      vraw[k].load(gv + vrow + 8 * g);
+      dyraw[k].load(reinterpret_cast<const T*>(a.dout) + vrow + 8 * g);
+      zraw[k].load(gz + vrow + 8 * g);
+    }
+  }
+};
+
+__device__ __forceinline__ float lane63(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <typename T, int CS, int N, int P, int R>
+__global__ __launch_bounds__(kBwdThreads, 1)
+void scan_bwd_walk_kernel(BwdArgs a) {
+  typedef MF16<T> W;
+  typedef GradSmem<T, CS, N, P, R> S;
+  typedef WalkLoads<T, CS, N, P, R> Loads;
+  static_assert(sizeof(S) <= 160 * 1024, "LDS budget");
+  __shared__ S sm;
+  constexpr int PAD = S::PAD, KS = W::KSTEP, NH = S::NH;
+  constexpr int TB = CS / 16;                          // 16-token blocks
+  constexpr int GH = NH / 8, HP = Loads::HP, VGW = Loads::VGW;
+  constexpr int NT = N / 16, NTILE = (P / 16) * NT, TPW = (NTILE + kBwdWaves - 1) / kBwdWaves;
+  static_assert(kBwdWaves % NT == 0, "the adjoint tiles of a wave share one column tile");
+  constexpr bool BF = std::is_same<T, bf16>::value;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave >= 0 && wave < kBwdWaves);
+  const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
+  const bool qkw = wave < GH;
+  const int bh = blockIdx.x, b = bh / H, h = bh % H, hq = h / (H / HQ);
+  const T* gz = reinterpret_cast<const T*>(a.s.z);
+  const float Dh = a.s.D ? a.s.D[h] : 0.0f;
+
+  f32x4 G[TPW];                                        // adjoint state tiles [p][n]
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) G[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // Bias gradients: per pass (q~ half 0, half 1, k~ half 0, half 1), thread (n, tg) sums
+  // column n of the half over the tokens of its token group tg, over the whole walk.
+  constexpr int TPG = CS * NH / kBwdThreads;           // tokens per group
+  static_assert(TPG >= 1 && CS * NH % kBwdThreads == 0, "bias column sums: whole token groups");
+  const int bn = tid % NH, btg = tid / NH;
+  float bacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float cth[2][4];                                     // d(theta) over the later chunks, per pair
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cth[hh][j] = 0.0f;
+  float cda = 0.0f, dsum = 0.0f;                       // wave 0: dA over the later chunks; dD
+
+  // One register set of loads: chunk c's inputs are consumed by the end of its
+  // preparation, and chunk c - 1's are requested right after it, so their latency hides
+  // behind the rest of chunk c's work.
+  Loads cur;
+  cur.issue(a, nc - 1, bh, tid, wave, lane);
+  for (int c = nc - 1; c >= 0; --c) {
+    // lane and thread indices made opaque per chunk, so that the compiler forms the
+    // lane-dependent LDS and global addresses inside the chunk instead of hoisting them
+    // all out of the walk and keeping each live in a register for the whole loop
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+    const int t0 = c * CS;
+    const bool tok = lane < CS && t0 + lane < L;
+    const long qrow = (((long)b * L + t0 + lane) * HQ + hq) * N;   // this lane's token (stores)
+    const float dtl = tok ? cur.dt : 0.0f;
+
+    // ---- G_c and the saved state h_c into LDS; the token constants
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = wave + kBwdWaves * i;
+      if (tile < NTILE) {
+        const float gv[4] = {G[i][0], G[i][1], G[i][2], G[i][3]};
+        store4(&sm.gt[16 * (tile % NT) + (lane & 15)][16 * (tile / NT) + 4 * (lane >> 4)], gv);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < HP; ++k) {
+      const int i = tid + k * kBwdThreads;
+      if (i < P * N / 8) *reinterpret_cast<Vec8<T>*>(&sm.h[i / (N / 8)][8 * (i % (N / 8))]) = cur.hpc[k];
+    }
+    if (wave == 0) {
+      const float adt = tok ? cur.adt : 0.0f, tr = tok ? cur.trap : 0.0f;
+      const float sg = 1.0f / (1.0f + expf(-tr));
+      const float gm = dtl * sg;
+      float un = __shfl_down(dtl * (1.0f - sg), 1, 64);             // next token's dt (1 - sigmoid)
+      if (lane == CS - 1) {
+        const bool nx = t0 + CS < L;
+        const float dtn = nx ? cur.dtn : 0.0f, trn = nx ? cur.trapn : 0.0f;
+        un = dtn * (1.0f - 1.0f / (1.0f + expf(-trn)));
+      }
+      const float acum = wave_incl_scan(lane < CS ? adt : 0.0f);
+      const float ae = __shfl(acum, CS - 1, 64);
+      if (lane < CS) {
+        sm.ac[lane] = acum;
+        sm.gam[lane] = gm;
+        sm.scl[lane] = tok ? gm + un : 0.0f;
+        sm.dtv[lane] = dtl;
+      }
+      if (lane == 0) sm.aend = ae;
+    }
+
+    // ---- this thread's two column groups: q^ = q + qb, k^ = k + kb and the rope
+    // cos/sin of their pairs, in registers for every phase of the chunk
+    float qh[2][8], kh[2][8], cs[2][4], sn[2][4];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int g = hh * GH + wave;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qh[hh][e] = kh[hh][e] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cs[hh][j] = 1.0f, sn[hh][j] = 0.0f;
+      if (qkw) {
+        float th4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (R > 0) {
+          if (4 * g < R) {
+            const float rv[4] = {cur.rates[hh].x, cur.rates[hh].y, cur.rates[hh].z, cur.rates[hh].w};
+            const float tv[4] = {cur.th0[hh].x, cur.th0[hh].y, cur.th0[hh].z, cur.th0[hh].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              th4[j] = __builtin_amdgcn_fractf(tv[j] + wave_incl_scan(angle_step(rv[j], dtl)));
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          cs[hh][j] = __builtin_amdgcn_cosf(th4[j]);
+          sn[hh][j] = __builtin_amdgcn_sinf(th4[j]);
+        }
+        if (tok) {
+          cur.qraw[hh].to_f(qh[hh]);
+          cur.kraw[hh].to_f(kh[hh]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            qh[hh][e] += a.s.qbias[(long)h * N + 8 * g + e];
+            kh[hh][e] += a.s.kbias[(long)h * N + 8 * g + e];
+          }
+        }
+      }
+    }
+    __syncthreads();   // token constants, G_c, h_c
+
+    // ---- preparation, lane = token: q~, k~, v, dy and the row dot products
+    if (qkw) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int g = hh * GH + wave;
+        float q[8], k[8], dot = 0.0f;
+        const float sc = tok ? sm.scl[lane] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          q[e] = qh[hh][e];
+          k[e] = kh[hh][e];
+          dot += q[e] * k[e];
+        }
+        rot8<R>(q, cs[hh], sn[hh], g, 1.0f);
+        rot8<R>(k, cs[hh], sn[hh], g, 1.0f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) k[e] *= sc;
+        if (lane < CS) {
+          store8(&sm.qt[lane][8 * g], q);
+          store8(&sm.kt[lane][8 * g], k);
+          sm.pq[g][lane] = dot;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < VGW; ++k) {
+      const int g = wave + k * kBwdWaves;
+      if (g >= P / 8) continue;
+      float v[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dy[8] = {0, 0, 0, 0, 0, 0, 0, 0}, fz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      float dot = 0.0f;
+      if (tok) {
+        cur.vraw[k].to_f(v);
+        cur.dyraw[k].to_f(dy);
+        if (gz) {
+          float z[8];
+          cur.zraw[k].to_f(z);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float sz = sigmoid_fast(z[e]);
+            fz[e] = dy[e] * sz * (1.0f + z[e] * (1.0f - sz));
+            dy[e] *= z[e] * sz;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dot += dy[e] * v[e];
+      }
+      if (lane < CS) {
+        store8(&sm.v[lane][8 * g], v);
+        store8(&sm.dy[lane][8 * g], dy);
+        store8(&sm.fz[lane][8 * g], fz);
+        sm.pv[g][lane] = dot;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      float qk = 0.0f, dqk = 0.0f;
+      if (lane < CS) {
+        for (int g = 0; g < N / 8; ++g) qk += sm.pq[g][lane];
+        for (int g = 0; g < P / 8; ++g) dqk += sm.pv[g][lane];
+        sm.qk[lane] = qk;
+        sm.dqk[lane] = dqk;
+      }
+      dsum += dqk;                                   // padding tokens hold dy = 0
+    }
+    if (c > 0) cur.issue(a, c - 1, bh, tid, wave, lane);   // every use of chunk c's loads is above
+
+    // ---- S = q~ k~^T and dP = dy v^T, masked (s < t) and decayed e^{A_t - A_s}
+    for (int i = wave; i < 2 * TB * TB; i += kBwdWaves) {
+      const int which = i / (TB * TB), tt = (i % (TB * TB)) / TB, st = (i % (TB * TB)) % TB;
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (st <= tt) {
+        if (which == 0) {
+          for (int k0 = 0; k0 < N; k0 += KS)
+            acc = W::mma(W::ld(&sm.qt[0][0], N + PAD, 16 * tt, k0, lane), W::ld(&sm.kt[0][0], N + PAD, 16 * st, k0, lane),
+                         acc);
+        } else {
+          for (int k0 = 0; k0 < P; k0 += KS)
+            acc = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * tt, k0, lane), W::ld(&sm.v[0][0], P + PAD, 16 * st, k0, lane),
+                         acc);
+        }
+      }
+      const int s = 16 * st + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * tt + 4 * (lane >> 4) + r;
+        const float val = s < t ? acc[r] * exp2_fast((sm.ac[t] - sm.ac[s]) * kLog2e) : 0.0f;
+        if (which == 0) sm.sm[t][s] = (T)val;
+        else sm.dpm[t][s] = (T)val;
+      }
+    }
+    __syncthreads();
+
+    // ---- y (for dZ) and dV, per 16 x 16 tile of (token, value column)
+    const float aend = sm.aend;
+    for (int i = wave; i < 2 * TB * (P / 16); i += kBwdWaves) {
+      const int which = i / (TB * (P / 16)), rt = (i % (TB * (P / 16))) / (P / 16), pt = i % (P / 16);
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (which == 0) {
+        if (!gz || !a.dz) continue;
+        // y_t = sum_s Sm[t][s] v_s + e^{A_t} q~_t . h + (D + QK_t) v_t
+        for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS)
+          acc = W::mma(W::ld(&sm.sm[0][0], CS + PAD, 16 * rt, k0, lane), ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane),
+                       acc);
+        for (int k0 = 0; k0 < N; k0 += KS)
+          acc2 = W::mma(W::ld(&sm.qt[0][0], N + PAD, 16 * rt, k0, lane), W::ld(&sm.h[0][0], N + PAD, 16 * pt, k0, lane),
+                        acc2);
+        const int p = 16 * pt + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * rt + 4 * (lane >> 4) + r;
+          if (t0 + t < L) {
+            const long o = (((long)b * L + t0 + t) * H + h) * P + p;
+            const float y = acc[r] + exp2_fast(sm.ac[t] * kLog2e) * acc2[r] +
+                            (Dh + sm.gam[t] * sm.qk[t]) * (float)sm.v[t][p];
+            reinterpret_cast<T*>(a.dz)[o] = (T)(y * (float)sm.fz[t][p]);
+          }
+        }
+      } else {
+        // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G k~_s + (D + QK_s) dy_s
+        for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS)
+          acc = W::mma(ld_tr(&sm.sm[0][0], CS + PAD, k0, 16 * rt, lane), ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane),
+                       acc);
+        for (int k0 = 0; k0 < N; k0 += KS)
+          acc2 = W::mma(W::ld(&sm.kt[0][0], N + PAD, 16 * rt, k0, lane), ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane),
+                        acc2);
+        const int p = 16 * pt + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = 16 * rt + 4 * (lane >> 4) + r;
+          if (t0 + s < L) {
+            const float dv = acc[r] + exp2_fast((aend - sm.ac[s]) * kLog2e) * acc2[r] +
+                             (Dh + sm.gam[s] * sm.qk[s]) * (float)sm.dy[s][p];
+            reinterpret_cast<T*>(a.dv)[(((long)b * L + t0 + s) * H + h) * P + p] = (T)dv;
+          }
+        }
+      }
+    }
+
+    // ---- advance the adjoint state to the one after chunk c - 1:
+    // G <- e^{A_end} G + sum_t e^{A_cum,t} dy_t (x) q~_t (G_c is already in LDS)
+    {
+      const float dec = exp2_fast(aend * kLog2e);
+      const int nt = wave % NT;
+      f32x4 acc[TPW];
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) acc[i] = G[i] * dec;
+#pragma unroll
+      for (int k0 = 0; k0 < CS; k0 += KS) {
+        float w[W::WN];
+#pragma unroll
+        for (int j = 0; j < W::WN; ++j) w[j] = exp2_fast(sm.ac[W::ktok(k0, lane) + j] * kLog2e);
+        const typename W::frag qf = W::scale(ld_tr(&sm.qt[0][0], N + PAD, k0, 16 * nt, lane), w);
+#pragma unroll
+        for (int i = 0; i < TPW; ++i) {
+          const int tile = wave + kBwdWaves * i;
+          if (tile < NTILE) acc[i] = W::mma(ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * (tile / NT), lane), qf, acc[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) G[i] = acc[i];
+    }
+
+    // ---- dq~ then dk~, half the columns at a time, each followed by its chain rule
+    float dthq[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};   // d(theta) from dq~, for pass K
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const bool isq = pass < 2;
+      const int n0 = (pass & 1) * NH;
+      const int hh = pass & 1;
+      float gq8[8], gk8[8], gcs[4], gsn[4];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gq8[e] = hh ? qh[1][e] : qh[0][e];
+        gk8[e] = hh ? kh[1][e] : kh[0][e];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        gcs[j] = hh ? cs[1][j] : cs[0][j];
+        gsn[j] = hh ? sn[1][j] : sn[0][j];
+      }
+      if constexpr (BF) {
+        // rounding residual of the operand this pass multiplies: k~ (dq~) or q~ (dk~)
+        if (qkw) {
+          const int g = n0 / 8 + wave;
+          float x[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = isq ? gk8[e] : gq8[e];
+          rot8<R>(x, gcs, gsn, g, 1.0f);
+          const float sc = isq && tok ? sm.scl[lane] : 1.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            x[e] *= sc;
+            x[e] -= (float)(bf16)x[e];
+          }
+          if (lane < CS) store8(&sm.lo[lane][8 * wave], x);
+        }
+        __syncthreads();
+      }
+      for (int i = wave; i < TB * (NH / 16); i += kBwdWaves) {
+        const int rt = i / (NH / 16), nt = i % (NH / 16);
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (isq) {
+          // dq~_t = sum_s dPm[t][s] k~_s + e^{A_t} dy_t h
+          for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS) {
+            const typename W::frag fa = W::ld(&sm.dpm[0][0], CS + PAD, 16 * rt, k0, lane);
+            acc = W::mma(fa, ld_tr(&sm.kt[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc);
+            if constexpr (BF) acc = W::mma(fa, ld_tr(&sm.lo[0][0], NH + PAD, k0, 16 * nt, lane), acc);
+          }
+          for (int k0 = 0; k0 < P; k0 += KS)
+            acc2 = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * rt, k0, lane),
+                          ld_tr(&sm.h[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc2);
+        } else {
+          // dk~_s = sum_t dPm[t][s] q~_t + e^{A_end - A_s} v_s G
+          for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS) {
+            const typename W::frag fa = ld_tr(&sm.dpm[0][0], CS + PAD, k0, 16 * rt, lane);
+            acc = W::mma(fa, ld_tr(&sm.qt[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc);
+            if constexpr (BF) acc = W::mma(fa, ld_tr(&sm.lo[0][0], NH + PAD, k0, 16 * nt, lane), acc);
+          }
+          for (int k0 = 0; k0 < P; k0 += KS)
+            acc2 = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * rt, k0, lane),
+                          W::ld(&sm.gt[0][0], P + PAD, n0 + 16 * nt, k0, lane), acc2);
+        }
+        const int nl = 16 * nt + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * rt + 4 * (lane >> 4) + r;
+          const float w = exp2_fast((isq ? sm.ac[t] : aend - sm.ac[t]) * kLog2e);
+          sm.res[t][nl] = acc[r] + w * acc2[r];
+        }
+      }
+      __syncthreads();
+      // chain rule, lane = token, one 8-column group per wave
+      const int g = n0 / 8 + wave;
+      if (qkw) {
+        float dx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, out[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float dot = 0.0f, dsc = 0.0f, dth[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (tok) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dx[e] = sm.res[lane][8 * (g - n0 / 8) + e];
+          const float sc = sm.scl[lane], gqk = sm.dqk[lane] * sm.gam[lane];
+          float xr[8];                                    // q~ (pass Q) or rot(k^) (pass K)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xr[e] = isq ? gq8[e] : gk8[e];
+          rot8<R>(xr, gcs, gsn, g, 1.0f);
+          const float f = isq ? 1.0f : sc;                // k~ = scale rot(k^)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            dot += f * xr[e] * dx[e];
+            dsc += xr[e] * dx[e];
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dth[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
+          // d(q^) = rot^T dq~ + dQK gamma k^;  d(k^) = scale rot^T dk~ + dQK gamma q^
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] = f * dx[e];
+          rot8<R>(out, gcs, gsn, g, -1.0f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] += gqk * (isq ? gk8[e] : gq8[e]);
+          if (a.dqh) {
+            float* dst = (isq ? a.dqh : a.dkh) + (((long)b * L + t0 + lane) * H + h) * N + 8 * g;
+            store8(dst, out);
+          } else {
+            T* dst = reinterpret_cast<T*>(isq ? a.dq : a.dk) + qrow + 8 * g;
+            store8(dst, out);
+          }
+        }
+        // d(q^) / d(k^) back into the thread's own slots of res, for the column sums
+        if (lane < CS) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm.res[lane][8 * (g - n0 / 8) + e] = out[e];
+        }
+        if (isq) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dthq[hh][j] = dth[j];
+        } else {
+          // the token's d(theta) of each pair; its reverse cumsum over the sequence is
+          // the chunk's suffix sum plus the later chunks' total (0 on padding tokens)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (4 * g + j < R) {
+              const float d = dthq[hh][j] + dth[j];
+              const float f = wave_incl_scan(d);
+              const float tot = lane63(f);
+              if (tok) a.dang[(((long)b * L + t0 + lane) * H + h) * R + 4 * g + j] = cth[hh][j] + tot - f + d;
+              cth[hh][j] += tot;
+            }
+          }
+        }
+        if (lane < CS) {
+          if (isq) sm.pq[g][lane] = dot;   // the same thread subtracts k~.dk~ in pass K
+          else {
+            sm.pq[g][lane] -= dot;
+            sm.ps[g][lane] = dsc;
+          }
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < TPG; ++i) bacc[pass] += sm.res[btg * TPG + i][bn];
+      // the next pass writes res after its residual barrier (bf16) or this one
+      if constexpr (!BF) __syncthreads();
+    }
+
+    // ---- per token: dA (its reverse cumsum into dADT), d(gamma) into dDT, d(scale)
+    // into the workspace
+    if (wave == 0) {
+      float da = 0.0f, ds = 0.0f;
+      if (tok) {
+        for (int g = 0; g < N / 8; ++g) {
+          da += sm.pq[g][lane];
+          ds += sm.ps[g][lane];
+        }
+        const long o = (long)bh * L + t0 + lane;
+        a.dsc[o] = ds;
+        a.ddt[o] = sm.dqk[lane] * sm.qk[lane] + ds;
+      }
+      const float f = wave_incl_scan(da);
+      const float tot = lane63(f);
+      if (tok) a.dadt[(long)bh * L + t0 + lane] = cda + tot - f + da;
+      cda += tot;
+    }
+  }
+
+  // ---- the walk's totals: bias and D gradients of this (b, h), and the sums over the
+  // sequence of dA and of d(theta) per pair (rounding only: both are exactly zero)
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    __syncthreads();
+    sm.res[btg][bn] = bacc[pass];
+    __syncthreads();
+    if (tid < NH) {
+      float s = 0.0f;
+      for (int i = 0; i < kBwdThreads / NH; ++i) s += sm.res[i][tid];
+      (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + tid] = s;
+    }
+  }
+  if (qkw) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * (hh * GH + wave) + j;
+        if (r < R && lane == 0) a.ctot[(long)bh * (R + 1) + 1 + r] = cth[hh][j];
+      }
+  }
+  if (wave == 0) {
+    const float tot = wave_sum(dsum);
+    if (lane == 0) {
+      if (a.pd) a.pd[bh] = tot;
+      a.ctot[(long)bh * (R + 1)] = cda;
+    }
+  }
+}
+
+// Finishing pass of the walk, one workgroup per (chunk, b, h).  dADT and dAngles hold
+// the reverse cumsums S_t of dA and d(theta), ctot their totals T over the sequence.
+// The output depends on the angles and on A only through differences theta_t -
+// theta_s and A_t - A_s (there is no initial carry), so the per-token d(theta) and dA
+// sum to exactly zero over the sequence, for every pair.  S_t then carries the whole
+// sequence's rounding error at t = 0, where the true value is 0.  S_t - T (L - t) / L
+// is the blend (t / L) S_t - ((L - t) / L) F_t of the reverse sum and the negated
+// forward sum F_t = T - S_t: the same value in exact arithmetic, and the
+// minimum-variance combination of the two when the per-token errors are independent.
+// Then dAngles = S pi dt (1 - tanh^2 rate), the angle part of dDT = pi sum_r S tanh,
+// du_t = d(scale)_{t-1}, dDT = dgamma sigmoid + du (1 - sigmoid) + angle part and
+// dTrap = (dgamma - du) dt sigmoid (1 - sigmoid).
+template <int CS>
+__global__ __launch_bounds__(256)
+void scan_bwd_walk_finish_kernel(BwdArgs a) {
+  __shared__ float tot[65];
+  __shared__ float dts[CS], angp[CS];
+  const int tid = threadIdx.x;
+  const int c = blockIdx.x, bh = blockIdx.y, b = bh / a.s.H, h = bh % a.s.H;
+  const int L = a.s.L, H = a.s.H, R = a.s.R;
+  const int t0 = c * CS, nt = min(CS, L - t0);
+  const float* ct = a.ctot + (long)bh * (R + 1);
+  if (tid <= R) tot[tid] = ct[tid];
+  if (tid < CS) {
+    dts[tid] = tid < nt ? a.s.dt[(long)bh * L + t0 + tid] : 0.0f;
+    angp[tid] = 0.0f;
+  }
+  __syncthreads();
+  if (R > 0) {
+    // (token, 4 pairs) pieces; the R / 4 pieces of a token sit in consecutive lanes
+    const int QR = R / 4;
+    const long row0 = (((long)b * L + t0) * H + h) * R;
+    const int AH = a.s.ang_shared ? 1 : H;
+    const long arow0 = (((long)b * L + t0) * AH + (a.s.ang_shared ? 0 : h)) * R;
+    for (int base = 0; base < CS * QR; base += 256) {
+      const int i = base + tid, tt = i / QR, q = i % QR;
+      float part = 0.0f;
+      if (tt < nt) {
+        const float w = (float)(L - t0 - tt) / (float)L;
+        float4 s = *reinterpret_cast<const float4*>(a.dang + row0 + (long)tt * H * R + 4 * q);
+        const float4 rt = *reinterpret_cast<const float4*>(a.s.ang + arow0 + (long)tt * AH * R + 4 * q);
+        float sv[4] = {s.x, s.y, s.z, s.w};
+        const float rv[4] = {rt.x, rt.y, rt.z, rt.w};
+        const float f = kPi * dts[tt];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = sv[j] - tot[1 + 4 * q + j] * w;
+          const float tn = tanhf(rv[j]);
+          sv[j] = v * f * (1.0f - tn * tn);
+          part += v * tn;
+        }
+        *reinterpret_cast<float4*>(a.dang + row0 + (long)tt * H * R + 4 * q) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      }
+      // sum over the token's pieces (aligned groups of QR lanes)
+      if (QR == 4) part = group_sum<4>(part);
+      else if (QR == 8) part = group_sum<8>(part);
+      else part = group_sum<16>(part);
+      if (q == 0 && tt < nt) angp[tt] = part * kPi;
+    }
+    __syncthreads();
+  }
+  if (tid < nt) {
+    const long o = (long)bh * L + t0 + tid;
+    const int t = t0 + tid;
+    const float dt = dts[tid];
+    const float du = t > 0 ? a.dsc[o - 1] : 0.0f;
+    const float dg = a.ddt[o];
+    const float sg = 1.0f / (1.0f + expf(-a.s.trap[o]));
+    a.dadt[o] -= tot[0] * (float)(L - t) / (float)L;
+    a.ddt[o] = dg * sg + du * (1.0f - sg) + angp[tid];
+    a.dtrap[o] = (dg - du) * dt * sg * (1.0f - sg);
+  }
+}
+
 // --------------------------------------------------------------- finishing scans
 // One workgroup per (chunk, b, h), lane = token: dadt = reverse cumsum of dA; dPhi =
 // reverse cumsum of d(theta), dAngles = dPhi pi dt (1 - tanh^2), the angle part of
@@ -889,15 +1518,29 @@ struct BwdWs {
   size_t hs, gs, th, pqb, pkb, pd, dsc, ctot, dqh, dkh, dangh, total;
 };
 
+// Route of the backward.  The reverse walk runs one workgroup per (b, h), so it fills
+// the chip only when B * H is large; below kWalkMinBH the chunk-parallel kernels (one
+// workgroup per (chunk, b, h), with the adjoint pass before them) run instead.  The
+// environment variable M3_BWD_ROUTE = "walk" or "chunks" forces one of them (tests,
+// measurements).
+constexpr long kWalkMinBH = 128;
+bool bwd_walk(int B, int H) {
+  const char* e = getenv("M3_BWD_ROUTE");
+  if (e && !strcmp(e, "walk")) return true;
+  if (e && !strcmp(e, "chunks")) return false;
+  return (long)B * H >= kWalkMinBH;
+}
+
 BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared) {
   const int CS = bf16_io ? 64 : 32;
+  const bool walk = bwd_walk(B, H);
   const long nc = (L + CS - 1) / CS, bhc = (long)B * H * nc;
   const size_t ts = bf16_io ? 2 : 4;
   BwdWs w;
   size_t off = 0;
   auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
   w.hs = take(bhc * P * N * ts);
-  w.gs = take(bhc * P * N * ts);
+  w.gs = walk ? 0 : take(bhc * P * N * ts);     // the walk keeps the adjoint state on chip
   w.th = take(bhc * (R > 0 ? R : 1) * 4);
   w.pqb = take(bhc * N * 4);
   w.pkb = take(bhc * N * 4);
@@ -946,7 +1589,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.dang = w.dangh ? reinterpret_cast<float*>(base + w.dangh) : g.dang;   // per head, then summed
   a.dqb = g.dqb; a.dkb = g.dkb; a.dD = g.dD;
   a.hs = base + w.hs;
-  a.gs = base + w.gs;
+  a.gs = bwd_walk(s.B, s.H) ? nullptr : base + w.gs;
   a.th0 = reinterpret_cast<float*>(base + w.th);
   a.pqb = reinterpret_cast<float*>(base + w.pqb);
   a.pkb = reinterpret_cast<float*>(base + w.pkb);
@@ -971,6 +1614,32 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
 
   const dim3 grid_bh(s.B * s.H), grid_c(a.nc, s.B * s.H);
   bool found = false;
+  if (bwd_walk(s.B, s.H)) {
+#define X(T, cs, n, p, r)                                                                                  \
+  if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
+    found = true;                                                                                          \
+    hipLaunchKernelGGL((scan_bwd_walk_kernel<T, cs, n, p, r>), grid_bh, dim3(kBwdThreads), 0, st, a);      \
+    if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
+    if (a.dqh) {                                                                                           \
+      hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \
+      if ((e = hipGetLastError()) != hipSuccess) return e;                                                 \
+    }                                                                                                      \
+  }
+    M3_BWD_SHAPES(X)
+#undef X
+    if (!found) return hipErrorInvalidValue;
+    if (CS == 64) hipLaunchKernelGGL(scan_bwd_walk_finish_kernel<64>, grid_c, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(scan_bwd_walk_finish_kernel<32>, grid_c, dim3(256), 0, st, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (w.dangh) {
+      hipLaunchKernelGGL(scan_bwd_angle_heads_kernel, dim3(1024), dim3(256), 0, st, a, g.dang);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    BwdArgs ar = a;
+    ar.nc = 1;                                   // one bias/D partial per (b, h)
+    hipLaunchKernelGGL(scan_bwd_reduce_kernel, dim3(s.H, (s.N + 15) / 16), dim3(256), 0, st, ar);
+    return hipGetLastError();
+  }
 #define X(T, cs, n, p, r)                                                                                  \
   if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
     found = true;                                                                                          \

@@ -30,3 +30,12 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(params=["chunks", "walk"])
+def bwd_route(request, monkeypatch):
+    """Runs a backward test on both routes of the library's backward: the
+    chunk-parallel kernels and the reverse walk (the library reads M3_BWD_ROUTE at
+    each call; unset, it picks by B * H)."""
+    monkeypatch.setenv("M3_BWD_ROUTE", request.param)
+    return request.param

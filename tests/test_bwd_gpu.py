@@ -71,7 +71,7 @@ BF16_SHAPES = [
 
 
 @pytest.mark.parametrize("B,L,H,Hqk,N,P,R", BF16_SHAPES)
-def test_bf16_gradients_match_oracle(B, L, H, Hqk, N, P, R):
+def test_bf16_gradients_match_oracle(B, L, H, Hqk, N, P, R, bwd_route):
     _check(B, L, H, Hqk, N, P, R, bf16=True, seed=31)
 
 
@@ -82,16 +82,16 @@ F32_SHAPES = [
 
 
 @pytest.mark.parametrize("B,L,H,Hqk,N,P,R", F32_SHAPES)
-def test_f32_gradients_match_oracle(B, L, H, Hqk, N, P, R):
+def test_f32_gradients_match_oracle(B, L, H, Hqk, N, P, R, bwd_route):
     _check(B, L, H, Hqk, N, P, R, bf16=False, seed=32)
 
 
-def test_gradients_without_d_and_z():
+def test_gradients_without_d_and_z(bwd_route):
     _check(1, 120, 2, 2, 128, 64, 32, bf16=True, seed=33, no_d=True, no_z=True)
     _check(1, 90, 2, 2, 64, 32, 16, bf16=False, seed=34, no_d=True, no_z=True)
 
 
-def test_autograd_matches_functional_backward_and_is_deterministic():
+def test_autograd_matches_functional_backward_and_is_deterministic(bwd_route):
     """mamba3_siso_hip under torch autograd (the custom_vjp) gives the functional
     backward's gradients, bitwise, on repeated calls."""
     torch = _torch()
@@ -116,7 +116,7 @@ def test_autograd_matches_functional_backward_and_is_deterministic():
     (1, 1280, 16, 16, 128, 64, 32, True),   # 20 chunks x 16 heads = 320 items
     (1, 2600, 4, 4, 64, 32, 16, False),     # 82 chunks (of 32) x 4 heads = 328 items
 ])
-def test_gradients_with_more_items_than_compute_units(B, L, H, Hqk, N, P, R, bf16):
+def test_gradients_with_more_items_than_compute_units(B, L, H, Hqk, N, P, R, bf16, bwd_route):
     """More (chunk, b, h) items than compute units (longer sequences and more heads
     than the cases above): several waves of chunk-gradient workgroups per launch."""
     _check(B, L, H, Hqk, N, P, R, bf16=bf16, seed=37)

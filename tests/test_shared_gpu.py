@@ -74,7 +74,7 @@ def test_shared_forward_matches_repeated_oracle(B, L, H, N, P, R, CS, bf16):
     (1, 200, 4, 128, 64, 32, True),
     (2, 90, 2, 64, 32, 16, False),
 ])
-def test_shared_gradients_match_oracle(B, L, H, N, P, R, bf16):
+def test_shared_gradients_match_oracle(B, L, H, N, P, R, bf16, bwd_route):
     torch = _torch()
     shared, rep = _inputs(B, L, H, N, P, R, seed=42, bf16=bf16)
     dt = torch.bfloat16 if bf16 else torch.float32

@@ -55,12 +55,12 @@ def test_config3_full_size_split_matches_oracle_and_one_pass():
 
 @pytest.mark.timeout(300)
 @pytest.mark.parametrize("L", [4096, 5120])
-def test_backward_at_config2_length(L):
+def test_backward_at_config2_length(L, bwd_route):
     import torch
     from mamba3_rocm import mamba3_siso_hip_bwd
     from oracle import mamba3_vjp as V
     B, H, N, P, R, CS = 1, 2, 128, 64, 32, 64
-    print(f"[sizes] backward {(B, L, H, N, P, R, CS)}", flush=True)
+    print(f"[sizes] backward {(B, L, H, N, P, R, CS)} route={bwd_route}", flush=True)
     d = I.scan_inputs(B, L, H, N, P, R, seed=38, bf16=True)
     cot = I.bf16_round(V.cotangent(B, L, H, P, seed=39))
     t = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in d.items()}
