@@ -724,89 +724,197 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
 // for its dV and dk~ products, then advances G <- e^{A_end} G + sum_t e^{A_cum,t}
 // dy_t (x) q~_t with its own q~ and dy.  Against the chunk-parallel route this removes
 // the adjoint pass (a second read of Q, dOut, Z and the rates) and the round trip of
-// every G_c through the workspace.  The next chunk's global inputs are requested
-// before the current chunk's work, so their latency hides behind it.  The bias and D
-// gradients are summed in registers over the walk, and the reverse cumsums of dA and
-// d(theta) over the sequence are carried from chunk to chunk: the walk writes the
-// suffix sums themselves (and their totals), which scan_bwd_walk_finish_kernel turns
-// into dADT, dAngles, dDT and dTrap.
+// every G_c through the workspace.  The bias and D gradients are summed over the walk,
+// and the reverse cumsums of dA and d(theta) over the sequence are carried from chunk
+// to chunk: the walk writes the suffix sums themselves (and their totals), which
+// scan_bwd_walk_finish_kernel turns into dADT, dAngles, dDT and dTrap.
+//
+// Memory access.  Every compute unit runs a walk at the same pace, so the chip's HBM
+// traffic comes in per-chunk bursts; what limits a burst is the number of cache lines
+// each load or store instruction touches.  Q, K, V, dOut and Z are therefore read as
+// whole rows (consecutive lanes on consecutive 16-byte pieces of a row): V, dOut and
+// Z are prepared in that layout directly, and Q and K pass through an LDS staging tile
+// (XOR-swizzled 16-byte slots) to the token-per-lane layout of the rope.  dZ, dV, dQ,
+// dK and dAngles are staged in LDS and written as whole rows.  The next chunk's loads
+// are requested in four parts spread over the current chunk, behind whose work their
+// latency hides.
 template <typename T, int CS, int N, int P, int R>
 struct WalkLoads {
   static constexpr int GH = N / 16;                                       // column groups per half
   static constexpr int HP = (P * N / 8 + kBwdThreads - 1) / kBwdThreads;  // 8-element state pieces per thread
-  static constexpr int VGW = (P / 8 + kBwdWaves - 1) / kBwdWaves;         // value groups per wave
-  Vec8<T> hpc[HP], qraw[2], kraw[2], vraw[VGW], dyraw[VGW], zraw[VGW];
+  static constexpr int QPT = (CS * N / 8 + kBwdThreads - 1) / kBwdThreads; // Q (K) row pieces per thread
+  static constexpr int VPT = (CS * P / 8 + kBwdThreads - 1) / kBwdThreads; // V (dOut, Z) row pieces per thread
+  static constexpr int HK = 8 * (int)sizeof(T) / 16;                     // 16-byte words per state piece
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));             // (a plain vector: kept in registers)
+  u32x4 hpc[HP][HK];
+  Vec8<T> qpc[QPT], kpc[QPT], vpc[VPT], dypc[VPT], zpc[VPT];
   float4 rates[2], th0[2];
   float adt, dt, trap, dtn, trapn;
-  // Every load is unconditional, from a clamped valid address where a lane or wave has
-  // nothing to load; the unused values are ignored.
+  // Every load is unconditional, from a clamped valid address where a lane has nothing
+  // to load (rows past the sequence end read the last token's row); those values are
+  // ignored or zeroed at their use.
+  template <int PART>
   __device__ __forceinline__ void issue(const BwdArgs& a, int c, int bh, int tid, int wave, int lane) {
     const int b = bh / a.s.H, h = bh % a.s.H, hq = h / (a.s.H / a.s.Hqk);
     const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc, t0 = c * CS;
-    const int tcl = min(t0 + lane, L - 1);
-    const long qrow = (((long)b * L + tcl) * HQ + hq) * N;
-    const long vrow = (((long)b * L + tcl) * H + h) * P;
-    const T* hsrc = reinterpret_cast<const T*>(a.hs) + ((long)bh * nc + c) * P * N;
+    if constexpr (PART == 0) {
+      const T* hsrc = reinterpret_cast<const T*>(a.hs) + ((long)bh * nc + c) * P * N;
 #pragma unroll
-    for (int k = 0; k < HP; ++k) hpc[k].load(hsrc + 8 * min(tid + k * kBwdThreads, P * N / 8 - 1));
+      for (int k = 0; k < HP; ++k) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(hsrc + 8 * min(tid + k * kBwdThreads, P * N / 8 - 1));
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int g = min(hh * GH + wave, N / 8 - 1);
-      qraw[hh].load(reinterpret_cast<const T*>(a.s.q) + qrow + 8 * g);
-      kraw[hh].load(reinterpret_cast<const T*>(a.s.k) + qrow + 8 * g);
-      rates[hh] = th0[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if constexpr (R > 0) {
-        const int gr = min(g, R / 4 - 1);
-        const long arow = a.s.ang_shared ? (long)b * L + tcl : ((long)b * L + tcl) * H + h;
-        rates[hh] = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * gr);
-        th0[hh] = *reinterpret_cast<const float4*>(a.th0 + ((long)bh * nc + c) * R + 4 * gr);
+        for (int j = 0; j < HK; ++j) hpc[k][j] = src[j];
+      }
+      const long srow = (long)bh * L;
+      const int tcl = min(t0 + lane, L - 1), tn = min(t0 + CS, L - 1);
+      adt = a.s.adt[srow + tcl];
+      dt = a.s.dt[srow + tcl];
+      trap = a.s.trap[srow + tcl];
+      dtn = a.s.dt[srow + tn];
+      trapn = a.s.trap[srow + tn];
+    } else if constexpr (PART == 1) {
+#pragma unroll
+      for (int k = 0; k < QPT; ++k) {
+        const int p = min(tid + k * kBwdThreads, CS * N / 8 - 1);
+        const long row = (((long)b * L + min(t0 + p / (N / 8), L - 1)) * HQ + hq) * N + 8 * (p % (N / 8));
+        qpc[k].load(reinterpret_cast<const T*>(a.s.q) + row);
+        kpc[k].load(reinterpret_cast<const T*>(a.s.k) + row);
+      }
+    } else if constexpr (PART == 2) {
+      const T* gv = reinterpret_cast<const T*>(a.s.v);
+      const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) : gv;
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const int p = min(tid + k * kBwdThreads, CS * P / 8 - 1);
+        const long row = (((long)b * L + min(t0 + p / (P / 8), L - 1)) * H + h) * P + 8 * (p % (P / 8));
+        vpc[k].load(gv + row);
+        dypc[k].load(reinterpret_cast<const T*>(a.dout) + row);
+        zpc[k].load(gz + row);
+      }
+    } else {
+      const int tcl = min(t0 + lane, L - 1);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        rates[hh] = th0[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (R > 0) {
+          const int gr = min(min(hh * GH + wave, N / 8 - 1), R / 4 - 1);
+          const long arow = a.s.ang_shared ? (long)b * L + tcl : ((long)b * L + tcl) * H + h;
+          rates[hh] = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * gr);
+          th0[hh] = *reinterpret_cast<const float4*>(a.th0 + ((long)bh * nc + c) * R + 4 * gr);
+        }
       }
     }
-    const long srow = (long)bh * L;
-    const int tn = min(t0 + CS, L - 1);
-    adt = a.s.adt[srow + tcl];
-    dt = a.s.dt[srow + tcl];
-    trap = a.s.trap[srow + tcl];
-    dtn = a.s.dt[srow + tn];
-    trapn = a.s.trap[srow + tn];
-    const T* gv = reinterpret_cast<const T*>(a.s.v);
-    const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) : gv;
-#pragma unroll
-    for (int k = 0; k < VGW; ++k) {
-      const int g = min(wave + k * kBwdWaves, P / 8 - 1);
-      vraw[k].load(gv + vrow + 8 * g);
-      dyraw[k].load(reinterpret_cast<const T*>(a.dout) + vrow + 8 * g);
-      zraw[k].load(gz + vrow + 8 * g);
-    }
   }
+  __device__ __forceinline__ void issue_all(const BwdArgs& a, int c, int bh, int tid, int wave, int lane) {
+    issue<0>(a, c, bh, tid, wave, lane);
+    issue<1>(a, c, bh, tid, wave, lane);
+    issue<2>(a, c, bh, tid, wave, lane);
+    issue<3>(a, c, bh, tid, wave, lane);
+  }
+};
+
+// LDS of the walk.  The arrays live for the whole chunk except those in `u`, whose
+// members are used in three windows separated by barriers: (A) the Q/K staging tiles
+// (written at the top of the chunk, read in its preparation), (B) the masked S and the
+// dZ/dV output tiles (S/dP to the dZ/dV stores), (C) the bf16 residuals, the dq~ / dk~
+// results and the d(theta) output tile (the four dq~/dk~ passes).  Within (B) and (C)
+// the offsets keep apart what is live at the same time: lo is written while the
+// output tiles are still being stored, res while the dAngles tile is read.
+template <typename T, int CS, int N, int P, int R>
+struct WalkSmem {
+  static constexpr bool BF = std::is_same<T, bf16>::value;
+  static constexpr int PAD = BF ? 8 : 4;
+  static constexpr int NH = N / 2;
+  static constexpr int SQ = N * (int)sizeof(T) / 16;        // 16-byte slots per Q/K row
+  static constexpr int RH = NH / 2 + 4;                     // row of the dAngles tile (a half's pairs)
+  static constexpr size_t SZ_Q = (size_t)CS * N * sizeof(T);
+  static constexpr size_t SZ_SM = (size_t)CS * (CS + PAD) * sizeof(T);
+  static constexpr size_t SZ_OUT = (size_t)2 * CS * (P + PAD) * sizeof(T);
+  static constexpr size_t SZ_LO = BF ? (size_t)CS * (NH + PAD) * sizeof(T) : 0;
+  static constexpr size_t SZ_RES = (size_t)CS * (NH + 4) * 4;
+  static constexpr size_t SZ_DTH = (size_t)CS * RH * 4;
+  static constexpr size_t OFF_K = SZ_Q, OFF_OUT = SZ_SM;
+  // bf16: res may overlap the output tiles (it is first written after the residual
+  // barrier); float has no residual barrier, so res starts after them
+  static constexpr size_t OFF_RES = BF ? SZ_LO : SZ_SM + SZ_OUT;
+  static constexpr size_t OFF_DTH = OFF_RES + SZ_RES;
+  static constexpr size_t U1 = 2 * SZ_Q, U2 = SZ_SM + SZ_OUT, U3 = OFF_DTH + SZ_DTH;
+  static constexpr size_t U = U1 > U2 ? (U1 > U3 ? U1 : U3) : (U2 > U3 ? U2 : U3);
+  alignas(16) T qt[CS][N + PAD];       // q~
+  alignas(16) T kt[CS][N + PAD];       // k~
+  alignas(16) T v[CS][P + PAD];
+  alignas(16) T dy[CS][P + PAD];
+  alignas(16) T fz[CS][P + PAD];       // dOut sigmoid(z) (1 + z (1 - sigmoid(z))): dZ = y fz
+  alignas(16) T h[P][N + PAD];         // state entering the chunk
+  alignas(16) T gt[N][P + PAD];        // adjoint state after the chunk, [n][p]
+  alignas(16) T dpm[CS][CS + PAD];     // dP masked and decayed
+  alignas(16) char u[U];
+  float ac[CS], gam[CS], scl[CS], dtv[CS], qk[CS], dqk[CS];
+  float pq[N / 8][CS];                 // per column group: q^.k^, then q~.dq~ - k~.dk~
+  float ps[N / 8][CS];                 // per column group: dk~ . rot(k^)
+  float qb[N], kb[N];                  // the head's biases
+  float aend;
+  __device__ __forceinline__ uint4* qstage() { return reinterpret_cast<uint4*>(u); }
+  __device__ __forceinline__ uint4* kstage() { return reinterpret_cast<uint4*>(u + OFF_K); }
+  __device__ __forceinline__ T* smk() { return reinterpret_cast<T*>(u); }                  // [CS][CS + PAD]
+  __device__ __forceinline__ T* outs(int w) { return reinterpret_cast<T*>(u + OFF_OUT) + (size_t)w * CS * (P + PAD); }
+  __device__ __forceinline__ T* lo() { return reinterpret_cast<T*>(u); }                   // [CS][NH + PAD]
+  __device__ __forceinline__ float* res() { return reinterpret_cast<float*>(u + OFF_RES); }  // [CS][NH + 4]
+  __device__ __forceinline__ float* dth() { return reinterpret_cast<float*>(u + OFF_DTH); }  // [CS][RH]
 };
 
 __device__ __forceinline__ float lane63(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// 16-byte slots j of a staged row piece: bf16 pieces are one slot, float pieces two.
+template <typename T> struct Slots;
+template <> struct Slots<bf16> {
+  static constexpr int K = 1;
+  __device__ __forceinline__ static uint4 get(const Vec8<bf16>& v, int) { return v.raw; }
+  template <int S>
+  __device__ __forceinline__ static void read(Vec8<bf16>& v, const uint4* buf, int row, int g) {
+    v.raw = staged<S>(buf, row, g);
+  }
+};
+template <> struct Slots<float> {
+  static constexpr int K = 2;
+  __device__ __forceinline__ static uint4 get(const Vec8<float>& v, int j) {
+    const float4 f = j ? v.b : v.a;
+    return make_uint4(__float_as_uint(f.x), __float_as_uint(f.y), __float_as_uint(f.z), __float_as_uint(f.w));
+  }
+  template <int S>
+  __device__ __forceinline__ static void read(Vec8<float>& v, const uint4* buf, int row, int g) {
+    v.raw_set2(staged<S>(buf, row, 2 * g), staged<S>(buf, row, 2 * g + 1));
+  }
+};
+
 template <typename T, int CS, int N, int P, int R>
 __global__ __launch_bounds__(kBwdThreads, 1)
 void scan_bwd_walk_kernel(BwdArgs a) {
   typedef MF16<T> W;
-  typedef GradSmem<T, CS, N, P, R> S;
+  typedef WalkSmem<T, CS, N, P, R> S;
   typedef WalkLoads<T, CS, N, P, R> Loads;
   static_assert(sizeof(S) <= 160 * 1024, "LDS budget");
   __shared__ S sm;
-  constexpr int PAD = S::PAD, KS = W::KSTEP, NH = S::NH;
+  constexpr int PAD = S::PAD, KS = W::KSTEP, NH = S::NH, SQ = S::SQ, RH = S::RH;
   constexpr int TB = CS / 16;                          // 16-token blocks
-  constexpr int GH = NH / 8, HP = Loads::HP, VGW = Loads::VGW;
+  constexpr int GH = NH / 8, QPT = Loads::QPT, VPT = Loads::VPT;
   constexpr int NT = N / 16, NTILE = (P / 16) * NT, TPW = (NTILE + kBwdWaves - 1) / kBwdWaves;
   static_assert(kBwdWaves % NT == 0, "the adjoint tiles of a wave share one column tile");
-  constexpr bool BF = std::is_same<T, bf16>::value;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr bool BF = S::BF;
+  constexpr int HP = Loads::HP;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __builtin_assume(wave >= 0 && wave < kBwdWaves);
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
   const bool qkw = wave < GH;
   const int bh = blockIdx.x, b = bh / H, h = bh % H, hq = h / (H / HQ);
   const T* gz = reinterpret_cast<const T*>(a.s.z);
   const float Dh = a.s.D ? a.s.D[h] : 0.0f;
+  T* const smk = sm.smk();
+  T* const lo = sm.lo();
+  float* const res = sm.res();
+  float* const dth = sm.dth();
 
   f32x4 G[TPW];                                        // adjoint state tiles [p][n]
 #pragma unroll
@@ -815,7 +923,6 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   // column n of the half over the tokens of its token group tg, over the whole walk.
   constexpr int TPG = CS * NH / kBwdThreads;           // tokens per group
   static_assert(TPG >= 1 && CS * NH % kBwdThreads == 0, "bias column sums: whole token groups");
-  const int bn = tid % NH, btg = tid / NH;
   float bacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float cth[2][4];                                     // d(theta) over the later chunks, per pair
 #pragma unroll
@@ -825,10 +932,17 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   float cda = 0.0f, dsum = 0.0f;                       // wave 0: dA over the later chunks; dD
 
   // One register set of loads: chunk c's inputs are consumed by the end of its
-  // preparation, and chunk c - 1's are requested right after it, so their latency hides
-  // behind the rest of chunk c's work.
+  // preparation, and chunk c - 1's are requested in parts during the rest of chunk c.
   Loads cur;
-  cur.issue(a, nc - 1, bh, tid, wave, lane);
+  {
+    const int tid = threadIdx.x;
+    cur.issue_all(a, nc - 1, bh, tid, wave, tid & 63);
+    // the head's biases into LDS (read by every chunk's preparation)
+    if (tid < N) {
+      sm.qb[tid] = a.s.qbias[(long)h * N + tid];
+      sm.kb[tid] = a.s.kbias[(long)h * N + tid];
+    }
+  }
   for (int c = nc - 1; c >= 0; --c) {
     // lane and thread indices made opaque per chunk, so that the compiler forms the
     // lane-dependent LDS and global addresses inside the chunk instead of hoisting them
@@ -837,11 +951,25 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
     const int t0 = c * CS;
-    const bool tok = lane < CS && t0 + lane < L;
-    const long qrow = (((long)b * L + t0 + lane) * HQ + hq) * N;   // this lane's token (stores)
+    const int nt = min(CS, L - t0);                   // tokens of this chunk
+    const bool tok = lane < nt;
     const float dtl = tok ? cur.dt : 0.0f;
 
-    // ---- G_c and the saved state h_c into LDS; the token constants
+    // ---- top: Q/K row pieces into the staging tiles, G_c and the saved state h_c
+    // into LDS, the token constants
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+      const int p = tid + k * kBwdThreads;
+      if (p < CS * N / 8) {
+        const int row = p / (N / 8), pc = p % (N / 8);
+#pragma unroll
+        for (int j = 0; j < Slots<T>::K; ++j) {
+          const int sl = Slots<T>::K * pc + j;
+          sm.qstage()[row * SQ + (sl ^ (row & (SQ - 1)))] = Slots<T>::get(cur.qpc[k], j);
+          sm.kstage()[row * SQ + (sl ^ (row & (SQ - 1)))] = Slots<T>::get(cur.kpc[k], j);
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int tile = wave + kBwdWaves * i;
@@ -853,7 +981,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
     for (int k = 0; k < HP; ++k) {
       const int i = tid + k * kBwdThreads;
-      if (i < P * N / 8) *reinterpret_cast<Vec8<T>*>(&sm.h[i / (N / 8)][8 * (i % (N / 8))]) = cur.hpc[k];
+      if (i < P * N / 8) {
+#pragma unroll
+        for (int j = 0; j < Loads::HK; ++j)
+          reinterpret_cast<typename Loads::u32x4*>(&sm.h[i / (N / 8)][8 * (i % (N / 8))])[j] = cur.hpc[k][j];
+      }
     }
     if (wave == 0) {
       const float adt = tok ? cur.adt : 0.0f, tr = tok ? cur.trap : 0.0f;
@@ -875,9 +1007,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       }
       if (lane == 0) sm.aend = ae;
     }
+    __syncthreads();   // staging, token constants, G_c, h_c
 
-    // ---- this thread's two column groups: q^ = q + qb, k^ = k + kb and the rope
-    // cos/sin of their pairs, in registers for every phase of the chunk
+    // ---- preparation.  Q/K, lane = token: this thread's two column groups (one per
+    // half of the state columns): q^ = q + qb, k^ = k + kb and the rope cos/sin of
+    // their pairs stay in registers for every phase below; q~ and k~ go to LDS.
     float qh[2][8], kh[2][8], cs[2][4], sn[2][4];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -903,23 +1037,17 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           sn[hh][j] = __builtin_amdgcn_sinf(th4[j]);
         }
         if (tok) {
-          cur.qraw[hh].to_f(qh[hh]);
-          cur.kraw[hh].to_f(kh[hh]);
+          Vec8<T> qv, kv;
+          Slots<T>::template read<SQ>(qv, sm.qstage(), lane, g);
+          Slots<T>::template read<SQ>(kv, sm.kstage(), lane, g);
+          qv.to_f(qh[hh]);
+          kv.to_f(kh[hh]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            qh[hh][e] += a.s.qbias[(long)h * N + 8 * g + e];
-            kh[hh][e] += a.s.kbias[(long)h * N + 8 * g + e];
+            qh[hh][e] += sm.qb[8 * g + e];
+            kh[hh][e] += sm.kb[8 * g + e];
           }
         }
-      }
-    }
-    __syncthreads();   // token constants, G_c, h_c
-
-    // ---- preparation, lane = token: q~, k~, v, dy and the row dot products
-    if (qkw) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int g = hh * GH + wave;
         float q[8], k[8], dot = 0.0f;
         const float sc = tok ? sm.scl[lane] : 0.0f;
 #pragma unroll
@@ -939,47 +1067,47 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
       }
     }
+    // V, dOut, Z in row layout: dy = dOut silu(z), the dZ factor, and dy . v per token
 #pragma unroll
-    for (int k = 0; k < VGW; ++k) {
-      const int g = wave + k * kBwdWaves;
-      if (g >= P / 8) continue;
-      float v[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dy[8] = {0, 0, 0, 0, 0, 0, 0, 0}, fz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      float dot = 0.0f;
-      if (tok) {
-        cur.vraw[k].to_f(v);
-        cur.dyraw[k].to_f(dy);
-        if (gz) {
-          float z[8];
-          cur.zraw[k].to_f(z);
+    for (int k = 0; k < VPT; ++k) {
+      const int p = tid + k * kBwdThreads;
+      if (p < CS * P / 8) {                           // wave-uniform
+        const int row = p / (P / 8), pc = p % (P / 8);
+        float v[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dy[8] = {0, 0, 0, 0, 0, 0, 0, 0}, fz[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float dot = 0.0f;
+        if (row < nt) {
+          cur.vpc[k].to_f(v);
+          cur.dypc[k].to_f(dy);
+          if (gz) {
+            float z[8];
+            cur.zpc[k].to_f(z);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float sz = sigmoid_fast(z[e]);
-            fz[e] = dy[e] * sz * (1.0f + z[e] * (1.0f - sz));
-            dy[e] *= z[e] * sz;
+            for (int e = 0; e < 8; ++e) {
+              const float sz = sigmoid_fast(z[e]);
+              fz[e] = dy[e] * sz * (1.0f + z[e] * (1.0f - sz));
+              dy[e] *= z[e] * sz;
+            }
           }
-        }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dot += dy[e] * v[e];
-      }
-      if (lane < CS) {
-        store8(&sm.v[lane][8 * g], v);
-        store8(&sm.dy[lane][8 * g], dy);
-        store8(&sm.fz[lane][8 * g], fz);
-        sm.pv[g][lane] = dot;
+          for (int e = 0; e < 8; ++e) dot += dy[e] * v[e];
+        }
+        store8(&sm.v[row][8 * pc], v);
+        store8(&sm.dy[row][8 * pc], dy);
+        store8(&sm.fz[row][8 * pc], fz);
+        dot = group_sum<P / 8>(dot);                   // the row's pieces sit in aligned lanes
+        if (pc == 0) sm.dqk[row] = dot;
       }
     }
     __syncthreads();
     if (wave == 0) {
-      float qk = 0.0f, dqk = 0.0f;
+      float qk = 0.0f;
       if (lane < CS) {
         for (int g = 0; g < N / 8; ++g) qk += sm.pq[g][lane];
-        for (int g = 0; g < P / 8; ++g) dqk += sm.pv[g][lane];
         sm.qk[lane] = qk;
-        sm.dqk[lane] = dqk;
+        dsum += sm.dqk[lane];                         // padding tokens hold dy = 0
       }
-      dsum += dqk;                                   // padding tokens hold dy = 0
     }
-    if (c > 0) cur.issue(a, c - 1, bh, tid, wave, lane);   // every use of chunk c's loads is above
+    if (c > 0) cur.template issue<0>(a, c - 1, bh, tid, wave, lane);   // every use of chunk c's loads is above
 
     // ---- S = q~ k~^T and dP = dy v^T, masked (s < t) and decayed e^{A_t - A_s}
     for (int i = wave; i < 2 * TB * TB; i += kBwdWaves) {
@@ -997,67 +1125,73 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
       }
       const int s = 16 * st + (lane & 15);
+      T* dst = which == 0 ? smk : &sm.dpm[0][0];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * tt + 4 * (lane >> 4) + r;
         const float val = s < t ? acc[r] * exp2_fast((sm.ac[t] - sm.ac[s]) * kLog2e) : 0.0f;
-        if (which == 0) sm.sm[t][s] = (T)val;
-        else sm.dpm[t][s] = (T)val;
+        dst[t * (CS + PAD) + s] = (T)val;
       }
     }
     __syncthreads();
+    if (c > 0) cur.template issue<1>(a, c - 1, bh, tid, wave, lane);
 
-    // ---- y (for dZ) and dV, per 16 x 16 tile of (token, value column)
+    // ---- y (for dZ) and dV as transposed 16 x 16 tiles [p][token]: each lane holds 4
+    // consecutive p of one token, written to the output tiles in LDS
     const float aend = sm.aend;
     for (int i = wave; i < 2 * TB * (P / 16); i += kBwdWaves) {
       const int which = i / (TB * (P / 16)), rt = (i % (TB * (P / 16))) / (P / 16), pt = i % (P / 16);
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int tl = 16 * rt + (lane & 15), p = 16 * pt + 4 * (lane >> 4);
       if (which == 0) {
         if (!gz || !a.dz) continue;
-        // y_t = sum_s Sm[t][s] v_s + e^{A_t} q~_t . h + (D + QK_t) v_t
+        // y_t = sum_s Sm[t][s] v_s + e^{A_t} h q~_t + (D + QK_t) v_t
         for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS)
-          acc = W::mma(W::ld(&sm.sm[0][0], CS + PAD, 16 * rt, k0, lane), ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane),
-                       acc);
+          acc = W::mma(ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane), W::ld(smk, CS + PAD, 16 * rt, k0, lane), acc);
         for (int k0 = 0; k0 < N; k0 += KS)
-          acc2 = W::mma(W::ld(&sm.qt[0][0], N + PAD, 16 * rt, k0, lane), W::ld(&sm.h[0][0], N + PAD, 16 * pt, k0, lane),
+          acc2 = W::mma(W::ld(&sm.h[0][0], N + PAD, 16 * pt, k0, lane), W::ld(&sm.qt[0][0], N + PAD, 16 * rt, k0, lane),
                         acc2);
-        const int p = 16 * pt + (lane & 15);
+        float vv[4], ff[4], o[4];
+        load4(&sm.v[tl][p], vv);
+        load4(&sm.fz[tl][p], ff);
+        const float ea = exp2_fast(sm.ac[tl] * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * rt + 4 * (lane >> 4) + r;
-          if (t0 + t < L) {
-            const long o = (((long)b * L + t0 + t) * H + h) * P + p;
-            const float y = acc[r] + exp2_fast(sm.ac[t] * kLog2e) * acc2[r] +
-                            (Dh + sm.gam[t] * sm.qk[t]) * (float)sm.v[t][p];
-            reinterpret_cast<T*>(a.dz)[o] = (T)(y * (float)sm.fz[t][p]);
-          }
-        }
+        for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
+        store4(sm.outs(0) + tl * (P + PAD) + p, o);
       } else {
-        // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G k~_s + (D + QK_s) dy_s
+        // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G^T k~_s + (D + QK_s) dy_s
         for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS)
-          acc = W::mma(ld_tr(&sm.sm[0][0], CS + PAD, k0, 16 * rt, lane), ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane),
-                       acc);
+          acc = W::mma(ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane), ld_tr(smk, CS + PAD, k0, 16 * rt, lane), acc);
         for (int k0 = 0; k0 < N; k0 += KS)
-          acc2 = W::mma(W::ld(&sm.kt[0][0], N + PAD, 16 * rt, k0, lane), ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane),
+          acc2 = W::mma(ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane), W::ld(&sm.kt[0][0], N + PAD, 16 * rt, k0, lane),
                         acc2);
-        const int p = 16 * pt + (lane & 15);
+        float yy[4], o[4];
+        load4(&sm.dy[tl][p], yy);
+        const float ea = exp2_fast((aend - sm.ac[tl]) * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = 16 * rt + 4 * (lane >> 4) + r;
-          if (t0 + s < L) {
-            const float dv = acc[r] + exp2_fast((aend - sm.ac[s]) * kLog2e) * acc2[r] +
-                             (Dh + sm.gam[s] * sm.qk[s]) * (float)sm.dy[s][p];
-            reinterpret_cast<T*>(a.dv)[(((long)b * L + t0 + s) * H + h) * P + p] = (T)dv;
-          }
+        for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
+        store4(sm.outs(1) + tl * (P + PAD) + p, o);
+      }
+    }
+    __syncthreads();
+    // ---- dZ and dV rows from the output tiles
+    {
+      T* const gdz = reinterpret_cast<T*>(a.dz);
+      T* const gdv = reinterpret_cast<T*>(a.dv);
+      for (int p = tid; p < 2 * CS * (P / 8); p += kBwdThreads) {
+        const int w = p / (CS * (P / 8)), q = p % (CS * (P / 8)), row = q / (P / 8), pc = q % (P / 8);
+        if (row < nt && (w == 1 || (gz && gdz))) {
+          const long o = (((long)b * L + t0 + row) * H + h) * P + 8 * pc;
+          *reinterpret_cast<Vec8<T>*>((w ? gdv : gdz) + o) =
+              *reinterpret_cast<const Vec8<T>*>(sm.outs(w) + row * (P + PAD) + 8 * pc);
         }
       }
     }
-
     // ---- advance the adjoint state to the one after chunk c - 1:
     // G <- e^{A_end} G + sum_t e^{A_cum,t} dy_t (x) q~_t (G_c is already in LDS)
     {
       const float dec = exp2_fast(aend * kLog2e);
-      const int nt = wave % NT;
+      const int ntile = wave % NT;
       f32x4 acc[TPW];
 #pragma unroll
       for (int i = 0; i < TPW; ++i) acc[i] = G[i] * dec;
@@ -1066,7 +1200,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         float w[W::WN];
 #pragma unroll
         for (int j = 0; j < W::WN; ++j) w[j] = exp2_fast(sm.ac[W::ktok(k0, lane) + j] * kLog2e);
-        const typename W::frag qf = W::scale(ld_tr(&sm.qt[0][0], N + PAD, k0, 16 * nt, lane), w);
+        const typename W::frag qf = W::scale(ld_tr(&sm.qt[0][0], N + PAD, k0, 16 * ntile, lane), w);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
           const int tile = wave + kBwdWaves * i;
@@ -1076,6 +1210,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
       for (int i = 0; i < TPW; ++i) G[i] = acc[i];
     }
+    if (c > 0) cur.template issue<2>(a, c - 1, bh, tid, wave, lane);
 
     // ---- dq~ then dk~, half the columns at a time, each followed by its chain rule
     float dthq[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};   // d(theta) from dq~, for pass K
@@ -1109,40 +1244,40 @@ void scan_bwd_walk_kernel(BwdArgs a) {
             x[e] *= sc;
             x[e] -= (float)(bf16)x[e];
           }
-          if (lane < CS) store8(&sm.lo[lane][8 * wave], x);
+          if (lane < CS) store8(lo + lane * (NH + PAD) + 8 * wave, x);
         }
         __syncthreads();
       }
       for (int i = wave; i < TB * (NH / 16); i += kBwdWaves) {
-        const int rt = i / (NH / 16), nt = i % (NH / 16);
+        const int rt = i / (NH / 16), ntl = i % (NH / 16);
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
         if (isq) {
           // dq~_t = sum_s dPm[t][s] k~_s + e^{A_t} dy_t h
           for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS) {
             const typename W::frag fa = W::ld(&sm.dpm[0][0], CS + PAD, 16 * rt, k0, lane);
-            acc = W::mma(fa, ld_tr(&sm.kt[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc);
-            if constexpr (BF) acc = W::mma(fa, ld_tr(&sm.lo[0][0], NH + PAD, k0, 16 * nt, lane), acc);
+            acc = W::mma(fa, ld_tr(&sm.kt[0][0], N + PAD, k0, n0 + 16 * ntl, lane), acc);
+            if constexpr (BF) acc = W::mma(fa, ld_tr(lo, NH + PAD, k0, 16 * ntl, lane), acc);
           }
           for (int k0 = 0; k0 < P; k0 += KS)
             acc2 = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * rt, k0, lane),
-                          ld_tr(&sm.h[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc2);
+                          ld_tr(&sm.h[0][0], N + PAD, k0, n0 + 16 * ntl, lane), acc2);
         } else {
           // dk~_s = sum_t dPm[t][s] q~_t + e^{A_end - A_s} v_s G
           for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS) {
             const typename W::frag fa = ld_tr(&sm.dpm[0][0], CS + PAD, k0, 16 * rt, lane);
-            acc = W::mma(fa, ld_tr(&sm.qt[0][0], N + PAD, k0, n0 + 16 * nt, lane), acc);
-            if constexpr (BF) acc = W::mma(fa, ld_tr(&sm.lo[0][0], NH + PAD, k0, 16 * nt, lane), acc);
+            acc = W::mma(fa, ld_tr(&sm.qt[0][0], N + PAD, k0, n0 + 16 * ntl, lane), acc);
+            if constexpr (BF) acc = W::mma(fa, ld_tr(lo, NH + PAD, k0, 16 * ntl, lane), acc);
           }
           for (int k0 = 0; k0 < P; k0 += KS)
             acc2 = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * rt, k0, lane),
-                          W::ld(&sm.gt[0][0], P + PAD, n0 + 16 * nt, k0, lane), acc2);
+                          W::ld(&sm.gt[0][0], P + PAD, n0 + 16 * ntl, k0, lane), acc2);
         }
-        const int nl = 16 * nt + (lane & 15);
+        const int nl = 16 * ntl + (lane & 15);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * rt + 4 * (lane >> 4) + r;
           const float w = exp2_fast((isq ? sm.ac[t] : aend - sm.ac[t]) * kLog2e);
-          sm.res[t][nl] = acc[r] + w * acc2[r];
+          res[t * (NH + 4) + nl] = acc[r] + w * acc2[r];
         }
       }
       __syncthreads();
@@ -1150,10 +1285,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       const int g = n0 / 8 + wave;
       if (qkw) {
         float dx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, out[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        float dot = 0.0f, dsc = 0.0f, dth[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float dot = 0.0f, dsc = 0.0f, dthv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (tok) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dx[e] = sm.res[lane][8 * (g - n0 / 8) + e];
+          for (int e = 0; e < 8; ++e) dx[e] = res[lane * (NH + 4) + 8 * wave + e];
           const float sc = sm.scl[lane], gqk = sm.dqk[lane] * sm.gam[lane];
           float xr[8];                                    // q~ (pass Q) or rot(k^) (pass K)
 #pragma unroll
@@ -1166,42 +1301,36 @@ void scan_bwd_walk_kernel(BwdArgs a) {
             dsc += xr[e] * dx[e];
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) dth[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
+          for (int j = 0; j < 4; ++j) dthv[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
           // d(q^) = rot^T dq~ + dQK gamma k^;  d(k^) = scale rot^T dk~ + dQK gamma q^
 #pragma unroll
           for (int e = 0; e < 8; ++e) out[e] = f * dx[e];
           rot8<R>(out, gcs, gsn, g, -1.0f);
 #pragma unroll
           for (int e = 0; e < 8; ++e) out[e] += gqk * (isq ? gk8[e] : gq8[e]);
-          if (a.dqh) {
-            float* dst = (isq ? a.dqh : a.dkh) + (((long)b * L + t0 + lane) * H + h) * N + 8 * g;
-            store8(dst, out);
-          } else {
-            T* dst = reinterpret_cast<T*>(isq ? a.dq : a.dk) + qrow + 8 * g;
-            store8(dst, out);
-          }
         }
-        // d(q^) / d(k^) back into the thread's own slots of res, for the column sums
+        // d(q^) / d(k^) back into the thread's own slots of res, for the row stores and
+        // the bias column sums
         if (lane < CS) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sm.res[lane][8 * (g - n0 / 8) + e] = out[e];
+          for (int e = 0; e < 8; ++e) res[lane * (NH + 4) + 8 * wave + e] = out[e];
         }
         if (isq) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) dthq[hh][j] = dth[j];
-        } else {
+          for (int j = 0; j < 4; ++j) dthq[hh][j] = dthv[j];
+        } else if (4 * g < R) {
           // the token's d(theta) of each pair; its reverse cumsum over the sequence is
           // the chunk's suffix sum plus the later chunks' total (0 on padding tokens)
+          float sv[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            if (4 * g + j < R) {
-              const float d = dthq[hh][j] + dth[j];
-              const float f = wave_incl_scan(d);
-              const float tot = lane63(f);
-              if (tok) a.dang[(((long)b * L + t0 + lane) * H + h) * R + 4 * g + j] = cth[hh][j] + tot - f + d;
-              cth[hh][j] += tot;
-            }
+            const float d = dthq[hh][j] + dthv[j];
+            const float f = wave_incl_scan(d);
+            const float tot = lane63(f);
+            sv[j] = cth[hh][j] + tot - f + d;
+            cth[hh][j] += tot;
           }
+          if (lane < CS) store4(dth + lane * RH + 4 * wave, sv);
         }
         if (lane < CS) {
           if (isq) sm.pq[g][lane] = dot;   // the same thread subtracts k~.dk~ in pass K
@@ -1212,10 +1341,42 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
       }
       __syncthreads();
+      // d(q^) / d(k^) rows of the half, the bias column sums, and (pass K) the half's
+      // d(theta) rows
+      {
+        for (int p = tid; p < CS * (NH / 8); p += kBwdThreads) {
+          const int row = p / (NH / 8), pc = p % (NH / 8);
+          if (row < nt) {
+            float o8[8];
 #pragma unroll
-      for (int i = 0; i < TPG; ++i) bacc[pass] += sm.res[btg * TPG + i][bn];
-      // the next pass writes res after its residual barrier (bf16) or this one
+            for (int e = 0; e < 8; ++e) o8[e] = res[row * (NH + 4) + 8 * pc + e];
+            if (a.dqh) {
+              store8((isq ? a.dqh : a.dkh) + (((long)b * L + t0 + row) * H + h) * N + n0 + 8 * pc, o8);
+            } else {
+              store8(reinterpret_cast<T*>(isq ? a.dq : a.dk) + (((long)b * L + t0 + row) * HQ + hq) * N + n0 + 8 * pc,
+                     o8);
+            }
+          }
+        }
+        const int bn = tid % NH, btg = tid / NH;
+#pragma unroll
+        for (int i = 0; i < TPG; ++i) bacc[pass] += res[(btg * TPG + i) * (NH + 4) + bn];
+        if (!isq) {
+          const int R0 = (pass & 1) * (NH / 2);                 // first pair of the half
+          const int RN = R - R0 < 0 ? 0 : (R - R0 < NH / 2 ? R - R0 : NH / 2);
+          if (RN > 0) {
+            for (int p = tid; p < CS * (RN / 4); p += kBwdThreads) {
+              const int row = p / (RN / 4), q4 = p % (RN / 4);
+              if (row < nt)
+                *reinterpret_cast<float4*>(a.dang + (((long)b * L + t0 + row) * H + h) * R + R0 + 4 * q4) =
+                    *reinterpret_cast<const float4*>(dth + row * RH + 4 * q4);
+            }
+          }
+        }
+      }
+      // the next pass writes res and lo after its residual barrier (bf16) or this one
       if constexpr (!BF) __syncthreads();
+      if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
     }
 
     // ---- per token: dA (its reverse cumsum into dADT), d(gamma) into dDT, d(scale)
@@ -1236,35 +1397,41 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       if (tok) a.dadt[(long)bh * L + t0 + lane] = cda + tot - f + da;
       cda += tot;
     }
+    // the next chunk's staging overlaps res and the d(theta) tile read above
+    if constexpr (BF) __syncthreads();
   }
 
   // ---- the walk's totals: bias and D gradients of this (b, h), and the sums over the
   // sequence of dA and of d(theta) per pair (rounding only: both are exactly zero)
+  {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int bn = tid % NH, btg = tid / NH;
 #pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    __syncthreads();
-    sm.res[btg][bn] = bacc[pass];
-    __syncthreads();
-    if (tid < NH) {
-      float s = 0.0f;
-      for (int i = 0; i < kBwdThreads / NH; ++i) s += sm.res[i][tid];
-      (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + tid] = s;
-    }
-  }
-  if (qkw) {
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * (hh * GH + wave) + j;
-        if (r < R && lane == 0) a.ctot[(long)bh * (R + 1) + 1 + r] = cth[hh][j];
+    for (int pass = 0; pass < 4; ++pass) {
+      __syncthreads();
+      res[btg * (NH + 4) + bn] = bacc[pass];
+      __syncthreads();
+      if (tid < NH) {
+        float s = 0.0f;
+        for (int i = 0; i < kBwdThreads / NH; ++i) s += res[i * (NH + 4) + tid];
+        (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + tid] = s;
       }
-  }
-  if (wave == 0) {
-    const float tot = wave_sum(dsum);
-    if (lane == 0) {
-      if (a.pd) a.pd[bh] = tot;
-      a.ctot[(long)bh * (R + 1)] = cda;
+    }
+    if (qkw) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * (hh * GH + wave) + j;
+          if (r < R && lane == 0) a.ctot[(long)bh * (R + 1) + 1 + r] = cth[hh][j];
+        }
+    }
+    if (wave == 0) {
+      const float tot = wave_sum(dsum);
+      if (lane == 0) {
+        if (a.pd) a.pd[bh] = tot;
+        a.ctot[(long)bh * (R + 1)] = cda;
+      }
     }
   }
 }
