@@ -824,6 +824,10 @@ template <typename T, int CS, int N, int P, int R>
 struct WalkSmem {
   static constexpr bool BF = std::is_same<T, bf16>::value;
   static constexpr int PAD = BF ? 8 : 4;
+  // Rows of 256 bytes (bf16, d_state 128) get 48 bytes of padding: a stride of 304 bytes
+  // (48 mod 256) keeps both the 16-row MFMA operand reads and the transposed 4-row reads
+  // of these tiles free of bank conflicts (272 bytes overlaps the transposed reads).
+  static constexpr int PADN = BF && N == 128 ? 24 : PAD;
   static constexpr int NH = N / 2;
   static constexpr int SQ = N * (int)sizeof(T) / 16;        // 16-byte slots per Q/K row
   static constexpr int RH = NH / 2 + 4;                     // row of the dAngles tile (a half's pairs)
@@ -840,16 +844,17 @@ struct WalkSmem {
   static constexpr size_t OFF_DTH = OFF_RES + SZ_RES;
   static constexpr size_t U1 = 2 * SZ_Q, U2 = SZ_SM + SZ_OUT, U3 = OFF_DTH + SZ_DTH;
   static constexpr size_t U = U1 > U2 ? (U1 > U3 ? U1 : U3) : (U2 > U3 ? U2 : U3);
-  alignas(16) T qt[CS][N + PAD];       // q~
-  alignas(16) T kt[CS][N + PAD];       // k~
+  alignas(16) T qt[CS][N + PADN];       // q~
+  alignas(16) T kt[CS][N + PADN];       // k~
   alignas(16) T v[CS][P + PAD];
   alignas(16) T dy[CS][P + PAD];
   alignas(16) T fz[CS][P + PAD];       // dOut sigmoid(z) (1 + z (1 - sigmoid(z))): dZ = y fz
-  alignas(16) T h[P][N + PAD];         // state entering the chunk
+  alignas(16) T h[P][N + PADN];         // state entering the chunk
   alignas(16) T gt[N][P + PAD];        // adjoint state after the chunk, [n][p]
   alignas(16) T dpm[CS][CS + PAD];     // dP masked and decayed
   alignas(16) char u[U];
-  float ac[CS], gam[CS], scl[CS], dtv[CS], qk[CS], dqk[CS];
+  alignas(16) float ac[CS];
+  float gam[CS], scl[CS], dtv[CS], qk[CS], dqk[CS];
   float pq[N / 8][CS];                 // per column group: q^.k^, then q~.dq~ - k~.dk~
   float ps[N / 8][CS];                 // per column group: dk~ . rot(k^)
   float qb[N], kb[N];                  // the head's biases
@@ -897,7 +902,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   typedef WalkLoads<T, CS, N, P, R> Loads;
   static_assert(sizeof(S) <= 160 * 1024, "LDS budget");
   __shared__ S sm;
-  constexpr int PAD = S::PAD, KS = W::KSTEP, NH = S::NH, SQ = S::SQ, RH = S::RH;
+  constexpr int PAD = S::PAD, PADN = S::PADN, KS = W::KSTEP, NH = S::NH, SQ = S::SQ, RH = S::RH;
   constexpr int TB = CS / 16;                          // 16-token blocks
   constexpr int GH = NH / 8, QPT = Loads::QPT, VPT = Loads::VPT;
   constexpr int NT = N / 16, NTILE = (P / 16) * NT, TPW = (NTILE + kBwdWaves - 1) / kBwdWaves;
@@ -1109,47 +1114,61 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     }
     if (c > 0) cur.template issue<0>(a, c - 1, bh, tid, wave, lane);   // every use of chunk c's loads is above
 
-    // ---- S = q~ k~^T and dP = dy v^T, masked (s < t) and decayed e^{A_t - A_s}
-    for (int i = wave; i < 2 * TB * TB; i += kBwdWaves) {
-      const int which = i / (TB * TB), tt = (i % (TB * TB)) / TB, st = (i % (TB * TB)) % TB;
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (st <= tt) {
-        if (which == 0) {
-          for (int k0 = 0; k0 < N; k0 += KS)
-            acc = W::mma(W::ld(&sm.qt[0][0], N + PAD, 16 * tt, k0, lane), W::ld(&sm.kt[0][0], N + PAD, 16 * st, k0, lane),
-                         acc);
-        } else {
-          for (int k0 = 0; k0 < P; k0 += KS)
-            acc = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * tt, k0, lane), W::ld(&sm.v[0][0], P + PAD, 16 * st, k0, lane),
-                         acc);
-        }
-      }
-      const int s = 16 * st + (lane & 15);
-      T* dst = which == 0 ? smk : &sm.dpm[0][0];
+    // ---- S = q~ k~^T and dP = dy v^T, masked (s < t) and decayed e^{A_t - A_s}.  Each
+    // wave's tiles form a fixed number of iterations without branches (the tiles above
+    // the diagonal are computed and masked like the others), so that their loads and
+    // MFMA chains interleave.
+    static_assert(2 * TB * TB % kBwdWaves == 0, "S/dP tiles: whole rounds");
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * tt + 4 * (lane >> 4) + r;
-        const float val = s < t ? acc[r] * exp2_fast((sm.ac[t] - sm.ac[s]) * kLog2e) : 0.0f;
-        dst[t * (CS + PAD) + s] = (T)val;
+    for (int j = 0; j < 2 * TB * TB / kBwdWaves; ++j) {
+      const int i = wave + kBwdWaves * j;
+      const int which = i / (TB * TB), tt = (i % (TB * TB)) / TB, st = (i % (TB * TB)) % TB;
+      // transposed tiles [s][t]: each lane holds 4 consecutive keys s of one query t
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (which == 0) {
+#pragma unroll
+        for (int k0 = 0; k0 < N; k0 += KS)
+          acc = W::mma(W::ld(&sm.kt[0][0], N + PADN, 16 * st, k0, lane), W::ld(&sm.qt[0][0], N + PADN, 16 * tt, k0, lane),
+                       acc);
+      } else {
+#pragma unroll
+        for (int k0 = 0; k0 < P; k0 += KS)
+          acc = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * st, k0, lane), W::ld(&sm.dy[0][0], P + PAD, 16 * tt, k0, lane),
+                       acc);
       }
+      const int t = 16 * tt + (lane & 15), s0 = 16 * st + 4 * (lane >> 4);
+      T* dst = which == 0 ? smk : &sm.dpm[0][0];
+      const float at = sm.ac[t];
+      float as[4], val[4];
+      load4(&sm.ac[s0], as);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) val[r] = s0 + r < t ? acc[r] * exp2_fast((at - as[r]) * kLog2e) : 0.0f;
+      store4(dst + t * (CS + PAD) + s0, val);
     }
     __syncthreads();
     if (c > 0) cur.template issue<1>(a, c - 1, bh, tid, wave, lane);
 
     // ---- y (for dZ) and dV as transposed 16 x 16 tiles [p][token]: each lane holds 4
     // consecutive p of one token, written to the output tiles in LDS
+    // The tiles' k ranges cover the whole chunk (the masked S is zero outside the causal
+    // range), so each wave's tiles are fixed iterations without branches.
     const float aend = sm.aend;
-    for (int i = wave; i < 2 * TB * (P / 16); i += kBwdWaves) {
+    static_assert(2 * TB * (P / 16) % kBwdWaves == 0, "y/dV tiles: whole rounds");
+#pragma unroll
+    for (int j = 0; j < 2 * TB * (P / 16) / kBwdWaves; ++j) {
+      const int i = wave + kBwdWaves * j;
       const int which = i / (TB * (P / 16)), rt = (i % (TB * (P / 16))) / (P / 16), pt = i % (P / 16);
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
       const int tl = 16 * rt + (lane & 15), p = 16 * pt + 4 * (lane >> 4);
       if (which == 0) {
         if (!gz || !a.dz) continue;
         // y_t = sum_s Sm[t][s] v_s + e^{A_t} h q~_t + (D + QK_t) v_t
-        for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS)
+#pragma unroll
+        for (int k0 = 0; k0 < CS; k0 += KS)
           acc = W::mma(ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane), W::ld(smk, CS + PAD, 16 * rt, k0, lane), acc);
+#pragma unroll
         for (int k0 = 0; k0 < N; k0 += KS)
-          acc2 = W::mma(W::ld(&sm.h[0][0], N + PAD, 16 * pt, k0, lane), W::ld(&sm.qt[0][0], N + PAD, 16 * rt, k0, lane),
+          acc2 = W::mma(W::ld(&sm.h[0][0], N + PADN, 16 * pt, k0, lane), W::ld(&sm.qt[0][0], N + PADN, 16 * rt, k0, lane),
                         acc2);
         float vv[4], ff[4], o[4];
         load4(&sm.v[tl][p], vv);
@@ -1160,10 +1179,12 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         store4(sm.outs(0) + tl * (P + PAD) + p, o);
       } else {
         // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G^T k~_s + (D + QK_s) dy_s
-        for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS)
+#pragma unroll
+        for (int k0 = 0; k0 < CS; k0 += KS)
           acc = W::mma(ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane), ld_tr(smk, CS + PAD, k0, 16 * rt, lane), acc);
+#pragma unroll
         for (int k0 = 0; k0 < N; k0 += KS)
-          acc2 = W::mma(ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane), W::ld(&sm.kt[0][0], N + PAD, 16 * rt, k0, lane),
+          acc2 = W::mma(ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane), W::ld(&sm.kt[0][0], N + PADN, 16 * rt, k0, lane),
                         acc2);
         float yy[4], o[4];
         load4(&sm.dy[tl][p], yy);
@@ -1200,7 +1221,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         float w[W::WN];
 #pragma unroll
         for (int j = 0; j < W::WN; ++j) w[j] = exp2_fast(sm.ac[W::ktok(k0, lane) + j] * kLog2e);
-        const typename W::frag qf = W::scale(ld_tr(&sm.qt[0][0], N + PAD, k0, 16 * ntile, lane), w);
+        const typename W::frag qf = W::scale(ld_tr(&sm.qt[0][0], N + PADN, k0, 16 * ntile, lane), w);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
           const int tile = wave + kBwdWaves * i;
@@ -1248,26 +1269,40 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
         __syncthreads();
       }
-      for (int i = wave; i < TB * (NH / 16); i += kBwdWaves) {
-        const int rt = i / (NH / 16), ntl = i % (NH / 16);
+      // Each wave's tiles are fixed iterations; a tile's k range is that of the
+      // wave's largest (dq~) or smallest (dk~) row block in the iteration, which covers
+      // its own (the masked dP is zero outside the causal range), so the ranges are
+      // compile-time constants once the loop is unrolled.
+      constexpr int NT2 = NH / 16, QT = TB * NT2, QJ = (QT + kBwdWaves - 1) / kBwdWaves;
+#pragma unroll
+      for (int j = 0; j < QJ; ++j) {
+        const int i = wave + kBwdWaves * j;
+        if (QT % kBwdWaves != 0 && i >= QT) continue;
+        const int rt = i / NT2, ntl = i % NT2;
+        const int rlo = min(kBwdWaves * j / NT2, TB - 1), rhi = min((kBwdWaves * j + kBwdWaves - 1) / NT2, TB - 1);
+        const int kq = ((16 * (rhi + 1) + KS - 1) / KS) * KS, kk = (16 * rlo / KS) * KS;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
         if (isq) {
           // dq~_t = sum_s dPm[t][s] k~_s + e^{A_t} dy_t h
-          for (int k0 = 0; k0 < 16 * (rt + 1); k0 += KS) {
+#pragma unroll
+          for (int k0 = 0; k0 < kq; k0 += KS) {
             const typename W::frag fa = W::ld(&sm.dpm[0][0], CS + PAD, 16 * rt, k0, lane);
-            acc = W::mma(fa, ld_tr(&sm.kt[0][0], N + PAD, k0, n0 + 16 * ntl, lane), acc);
+            acc = W::mma(fa, ld_tr(&sm.kt[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc);
             if constexpr (BF) acc = W::mma(fa, ld_tr(lo, NH + PAD, k0, 16 * ntl, lane), acc);
           }
+#pragma unroll
           for (int k0 = 0; k0 < P; k0 += KS)
             acc2 = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * rt, k0, lane),
-                          ld_tr(&sm.h[0][0], N + PAD, k0, n0 + 16 * ntl, lane), acc2);
+                          ld_tr(&sm.h[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc2);
         } else {
           // dk~_s = sum_t dPm[t][s] q~_t + e^{A_end - A_s} v_s G
-          for (int k0 = (16 * rt / KS) * KS; k0 < CS; k0 += KS) {
+#pragma unroll
+          for (int k0 = kk; k0 < CS; k0 += KS) {
             const typename W::frag fa = ld_tr(&sm.dpm[0][0], CS + PAD, k0, 16 * rt, lane);
-            acc = W::mma(fa, ld_tr(&sm.qt[0][0], N + PAD, k0, n0 + 16 * ntl, lane), acc);
+            acc = W::mma(fa, ld_tr(&sm.qt[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc);
             if constexpr (BF) acc = W::mma(fa, ld_tr(lo, NH + PAD, k0, 16 * ntl, lane), acc);
           }
+#pragma unroll
           for (int k0 = 0; k0 < P; k0 += KS)
             acc2 = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * rt, k0, lane),
                           W::ld(&sm.gt[0][0], P + PAD, n0 + 16 * ntl, k0, lane), acc2);
