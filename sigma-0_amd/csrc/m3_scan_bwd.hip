@@ -1032,8 +1032,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
             const float rv[4] = {cur.rates[hh].x, cur.rates[hh].y, cur.rates[hh].z, cur.rates[hh].w};
             const float tv[4] = {cur.th0[hh].x, cur.th0[hh].y, cur.th0[hh].z, cur.th0[hh].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              th4[j] = __builtin_amdgcn_fractf(tv[j] + wave_incl_scan(angle_step(rv[j], dtl)));
+            for (int j = 0; j < 4; ++j) th4[j] = angle_step(rv[j], dtl);
+            wave_incl_scan4(th4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) th4[j] = __builtin_amdgcn_fractf(tv[j] + th4[j]);
           }
         }
 #pragma unroll
@@ -1154,6 +1156,67 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     // range), so each wave's tiles are fixed iterations without branches.
     const float aend = sm.aend;
     static_assert(2 * TB * (P / 16) % kBwdWaves == 0, "y/dV tiles: whole rounds");
+    if constexpr (TB * (P / 16) == 2 * kBwdWaves) {
+      // two tiles of one value-column block per wave and product: the A fragments (v or
+      // dy columns, h rows or G columns of the block) are read once for both
+      const int pt = wave % (P / 16), r0 = wave / (P / 16), r1 = r0 + kBwdWaves / (P / 16);
+      const int p = 16 * pt + 4 * (lane >> 4);
+      if (gz && a.dz) {
+        // y_t = sum_s Sm[t][s] v_s + e^{A_t} h q~_t + (D + QK_t) v_t
+        f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
+#pragma unroll
+        for (int k0 = 0; k0 < CS; k0 += KS) {
+          const typename W::frag fa = ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane);
+          c0 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r0, k0, lane), c0);
+          c1 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r1, k0, lane), c1);
+        }
+#pragma unroll
+        for (int k0 = 0; k0 < N; k0 += KS) {
+          const typename W::frag fh = W::ld(&sm.h[0][0], N + PADN, 16 * pt, k0, lane);
+          d0 = W::mma(fh, W::ld(&sm.qt[0][0], N + PADN, 16 * r0, k0, lane), d0);
+          d1 = W::mma(fh, W::ld(&sm.qt[0][0], N + PADN, 16 * r1, k0, lane), d1);
+        }
+#pragma unroll
+        for (int u2 = 0; u2 < 2; ++u2) {
+          const int tl = 16 * (u2 ? r1 : r0) + (lane & 15);
+          const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
+          float vv[4], ff[4], o[4];
+          load4(&sm.v[tl][p], vv);
+          load4(&sm.fz[tl][p], ff);
+          const float ea = exp2_fast(sm.ac[tl] * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
+          store4(sm.outs(0) + tl * (P + PAD) + p, o);
+        }
+      }
+      {
+        // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G^T k~_s + (D + QK_s) dy_s
+        f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
+#pragma unroll
+        for (int k0 = 0; k0 < CS; k0 += KS) {
+          const typename W::frag fa = ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane);
+          c0 = W::mma(fa, ld_tr(smk, CS + PAD, k0, 16 * r0, lane), c0);
+          c1 = W::mma(fa, ld_tr(smk, CS + PAD, k0, 16 * r1, lane), c1);
+        }
+#pragma unroll
+        for (int k0 = 0; k0 < N; k0 += KS) {
+          const typename W::frag fg = ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane);
+          d0 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r0, k0, lane), d0);
+          d1 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r1, k0, lane), d1);
+        }
+#pragma unroll
+        for (int u2 = 0; u2 < 2; ++u2) {
+          const int tl = 16 * (u2 ? r1 : r0) + (lane & 15);
+          const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
+          float yy[4], o[4];
+          load4(&sm.dy[tl][p], yy);
+          const float ea = exp2_fast((aend - sm.ac[tl]) * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
+          store4(sm.outs(1) + tl * (P + PAD) + p, o);
+        }
+      }
+    } else
 #pragma unroll
     for (int j = 0; j < 2 * TB * (P / 16) / kBwdWaves; ++j) {
       const int i = wave + kBwdWaves * j;
@@ -1356,13 +1419,14 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         } else if (4 * g < R) {
           // the token's d(theta) of each pair; its reverse cumsum over the sequence is
           // the chunk's suffix sum plus the later chunks' total (0 on padding tokens)
-          float sv[4];
+          float sv[4], d[4], f[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) f[j] = d[j] = dthq[hh][j] + dthv[j];
+          wave_incl_scan4(f);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float d = dthq[hh][j] + dthv[j];
-            const float f = wave_incl_scan(d);
-            const float tot = lane63(f);
-            sv[j] = cth[hh][j] + tot - f + d;
+            const float tot = lane63(f[j]);
+            sv[j] = cth[hh][j] + tot - f[j] + d[j];
             cth[hh][j] += tot;
           }
           if (lane < CS) store4(dth + lane * RH + 4 * wave, sv);
