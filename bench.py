@@ -14,9 +14,11 @@ Also reported on the same JSON line:
                 (oracle/, the reference's own JAX is not installed) timed on
                 the host on a bounded sample (one of the 8 sequences)
   secondary     decode state update (config 4, HBM GB/s), the long-context
-                scan (config 3), the shared-B/C scan and the scan backward at
-                config 2, each with its own roofline, and the 12-layer backbone
-                prefill with its log-probabilities (config 5)
+                scan (config 3), the shared-B/C scan, the float32-I/O scan, the scan
+                backward at config 2 (recomputing its chunk states) and the
+                training pair (forward with residuals, backward from them), each
+                with its own roofline, and the 12-layer backbone prefill with its
+                log-probabilities (config 5)
 
 Before the warm-up of the headline, the kernel is launched untimed until at least
 100 launches and 0.3 s have run (the GPU clocks ramp up over the first ~100
@@ -25,7 +27,7 @@ launches of a process); the JSON line reports this as ``clock_settle``, apart fr
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-secondary]
-                       [--mode scan|decode|long|bwd|shared|layer|stack|copy|fp32]
+                       [--mode scan|decode|long|bwd|train|shared|layer|stack|copy|fp32]
        python bench.py --mode traffic --pmc-dir DIR   (writes the traffic JSON of
                        the headline kernel from rocprofv3 --pmc FETCH_SIZE /
                        WRITE_SIZE runs of the scan and of the copy kernel)
@@ -179,6 +181,28 @@ def bench_bwd(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
     wall, kern = time_calls(torch, fn, steps, warmup)
     nbytes = bwd_bytes(B, L, H, N, P, R, 2)
     return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
+
+
+def bench_train(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
+    """The training pair on the config's inputs: the forward that also writes the
+    backward's residuals (the state and rope angle entering every chunk) and the
+    backward that reads them instead of recomputing the chunk states -- the
+    reference's mamba3_siso_fwd / mamba3_siso_bwd(saved, ...) (mamba3_ops.py:788-902).
+    Each is timed on its own (HIP events), with an N(0, 1) output cotangent."""
+    from mamba3_rocm import mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
+    args = make_scan_inputs(torch, B, L, H, N, P, R, seed, torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1000)
+    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(torch.bfloat16)
+    _, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=CS)
+    fwd = lambda: mamba3_siso_hip_fwd_train(*args, chunk_size=CS)  # noqa: E731
+    bwd = lambda: mamba3_siso_hip_bwd(*args, dout, chunk_size=CS, saved=saved)  # noqa: E731
+    wf, kf = time_calls(torch, fwd, steps, warmup)
+    wb, kb = time_calls(torch, bwd, steps, warmup)
+    fbytes = scan_bytes(B, L, H, N, P, R, 2) + saved.numel()          # + the residuals written
+    bbytes = bwd_bytes(B, L, H, N, P, R, 2)
+    return dict(fwd_s=kf, bwd_s=kb, wall_s=wf + wb, saved_bytes=saved.numel(),
+                fwd_gbs=fbytes / kf / 1e9, bwd_gbs=bbytes / kb / 1e9)
 
 
 def bench_shared(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
@@ -396,8 +420,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "shared", "layer", "stack", "copy", "fp32",
-                                       "traffic"), default="scan")
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "train", "shared", "layer", "stack", "copy",
+                                       "fp32", "traffic"), default="scan")
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
@@ -435,6 +459,14 @@ def main():
                           "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
                           "achieved_gbs": round(r["achieved_gbs"], 1),
                           "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        return
+    if args.mode == "train":
+        # the training pair at config 2 (forward with residuals, backward from them)
+        r = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)
+        print(json.dumps({"mode": "train", "fwd_ms": round(r["fwd_s"] * 1e3, 4),
+                          "bwd_ms": round(r["bwd_s"] * 1e3, 4),
+                          "step_ms": round((r["fwd_s"] + r["bwd_s"]) * 1e3, 4),
+                          "bwd_frac_hbm": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
         return
     if args.mode == "layer":
         r = bench_layer(torch, 4, 12288, 768, args.steps, args.warmup, seed=5)
@@ -506,6 +538,7 @@ def main():
         dec = bench_decode(torch, 512, 32, 128, 64, 32, 256, 16, seed=4)
         lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
         bw = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
+        tr = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         sh = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         f32 = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2,
                          io_dtype=torch.float32)
@@ -538,6 +571,14 @@ def main():
                                  "tokens_per_s": round(8 * 4096 / bw["wall_s"], 1),
                                  "achieved_gbs": round(bw["achieved_gbs"], 1),
                                  "frac_hbm": round(bw["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "training_pair_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
+                                      "fwd_with_residuals_ms": round(tr["fwd_s"] * 1e3, 4),
+                                      "bwd_from_residuals_ms": round(tr["bwd_s"] * 1e3, 4),
+                                      "step_ms": round((tr["fwd_s"] + tr["bwd_s"]) * 1e3, 4),
+                                      "tokens_per_s": round(8 * 4096 / tr["wall_s"], 1),
+                                      "residual_bytes": tr["saved_bytes"],
+                                      "bwd_achieved_gbs": round(tr["bwd_gbs"], 1),
+                                      "bwd_frac_hbm": round(tr["bwd_gbs"] / HBM_PEAK_GBS, 4)},
             "backbone_prefill_config5": {"B": 4, "L": 12288, "layers": 12, "d_model": 768, "vocab": 2112,
                                          "activation": "half_glu1", "prenorm": True, "dtype": "bf16",
                                          "ms": round(bb["kernel_s"] * 1e3, 4),

@@ -173,6 +173,46 @@ int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
                       int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The training pair: the reference's mamba3_siso_fwd, which returns the output and
+ * the residuals its backward reads (per-chunk SSM states among them;
+ * src/base_model/models/mamba3_ops.py:788-818, siso_fwd_triton's SSM_States
+ * :272-285), and mamba3_siso_bwd(saved, grad_output) (:821-902).
+ *
+ * m3_chunk_scan_saved_bytes: bytes of the residual buffer, the state entering every
+ * chunk of the backward's chunking (64 tokens bf16, 32 float32; io dtype) and its
+ * rope angles (float32); 0 when the backward has no kernel for the shape.
+ *
+ * m3_chunk_scan_fwd_train: m3_chunk_scan_fwd_ws that also writes the residuals into
+ * `saved` (>= m3_chunk_scan_saved_bytes, 16-byte aligned).  No initial carry (the
+ * backward differentiates from a zero state).  chunk_size must be a multiple of the
+ * backward's chunk; shapes without a backward return M3_E_UNSUPPORTED.  Out is
+ * bitwise that of m3_chunk_scan_fwd_ws.
+ *
+ * m3_chunk_scan_bwd_saved: m3_chunk_scan_bwd reading the residuals of the
+ * m3_chunk_scan_fwd_train call on the same inputs instead of recomputing the chunk
+ * states; its workspace is m3_chunk_scan_bwd_saved_ws_bytes.
+ */
+size_t m3_chunk_scan_saved_bytes(int B, int L, int H, int N, int P, int R, int io_dtype);
+int m3_chunk_scan_fwd_train(const void* Q, const void* K, const void* V,
+                            const float* ADT, const float* DT, const float* Trap,
+                            const float* Q_bias, const float* K_bias, const float* Angles,
+                            const float* D, const void* Z, void* Out,
+                            int B, int L, int H, int Hqk, int N, int P, int R,
+                            int chunk_size, int io_dtype, void* saved, size_t saved_bytes,
+                            void* ws, size_t ws_bytes, void* stream);
+size_t m3_chunk_scan_bwd_saved_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
+                                        int io_dtype);
+int m3_chunk_scan_bwd_saved(const void* Q, const void* K, const void* V,
+                            const float* ADT, const float* DT, const float* Trap,
+                            const float* Q_bias, const float* K_bias, const float* Angles,
+                            const float* D, const void* Z, const void* dOut,
+                            void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                            float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                            int B, int L, int H, int Hqk, int N, int P, int R,
+                            int chunk_size, int io_dtype, const void* saved, size_t saved_bytes,
+                            void* ws, size_t ws_bytes, void* stream);
+
+/*
  * The fused front end's contract: Q, K (B,L,N) and the angle rates (B,L,R) shared
  * over the H heads, the rest per head as in m3_chunk_scan_fwd.  Replaces the
  * reference's mamba3_ssd_chunked_pallas (src/base_model/models/mamba3_pallas.py:

@@ -78,7 +78,7 @@ int scan_fwd(const void* Q, const void* K, const void* V,
              float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
              int B, int L, int H, int Hqk, int N, int P, int R,
              int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared,
-             long vz_tok = 0, long vz_bat = 0) {
+             long vz_tok = 0, long vz_bat = 0, void* saved = nullptr, size_t saved_bytes = 0) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
@@ -119,6 +119,22 @@ int scan_fwd(const void* Q, const void* K, const void* V,
   a.ang_shared = ang_shared ? 1 : 0;
   a.vz_tok = vz_tok; a.vz_bat = vz_bat;
   const bool bf = io_dtype == M3_DTYPE_BF16;
+  if (saved) {
+    // the training forward: the backward's residuals (chunk states and angles)
+    const int kbwd = bf ? 64 : 32;
+    if (!m3::scan_bwd_supported(bf, N, P, R) || impl != M3_IMPL_CHUNKED_MFMA)
+      return fail(M3_E_UNSUPPORTED, "no backward (saved states) for io_dtype=%d d_state=%d headdim=%d R=%d",
+                  io_dtype, N, P, R);
+    if (chunk_size % kbwd != 0)
+      return fail(M3_E_UNSUPPORTED, "saved states need chunk_size a multiple of %d, got %d", kbwd, chunk_size);
+    if (any_init) return fail(M3_E_ARG, "the training forward takes no initial carry");
+    const size_t need = m3::scan_bwd_saved_bytes(bf, B, L, H, N, P, R);
+    if (saved_bytes < need)
+      return fail(M3_E_ARG, "saved-state buffer of %zu bytes, the shape needs %zu (m3_chunk_scan_saved_bytes)",
+                  saved_bytes, need);
+    if (!aligned16(saved)) return fail(M3_E_ALIGN, "saved-state buffer must be 16-byte aligned");
+    m3::scan_bwd_saved_ptrs(saved, bf, B, L, H, N, P, R, &a.chunk_h, &a.chunk_th);
+  }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (impl == M3_IMPL_CHUNKED_MFMA) {
     const size_t need = ws ? m3::scan_split_ws_bytes(bf, B, L, H, N, P, R, chunk_size) : 0;
@@ -263,7 +279,8 @@ int scan_bwd(const void* Q, const void* K, const void* V,
              void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
              float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
              int B, int L, int H, int Hqk, int N, int P, int R,
-             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared) {
+             int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared,
+             const void* saved = nullptr, size_t saved_bytes = 0) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
@@ -285,10 +302,18 @@ int scan_bwd(const void* Q, const void* K, const void* V,
   const void* vec_ptrs[] = {Q, K, V, Z, dOut, dQ, dK, dV, dZ};
   for (const void* p : vec_ptrs)
     if (!aligned16(p)) return fail(M3_E_ALIGN, "Q, K, V, Z, dOut and their gradients must be 16-byte aligned");
-  const size_t need = m3::scan_bwd_ws_bytes(bf, B, L, H, Hqk, N, P, R, ang_shared);
+  const size_t need = m3::scan_bwd_ws_bytes(bf, B, L, H, Hqk, N, P, R, ang_shared, saved != nullptr);
   if (ws == nullptr || ws_bytes < need)
-    return fail(M3_E_ARG, "workspace of %zu bytes, the backward needs %zu (m3_chunk_scan_bwd_ws_bytes)", ws_bytes, need);
+    return fail(M3_E_ARG, "workspace of %zu bytes, the backward needs %zu (m3_chunk_scan_bwd%s_ws_bytes)", ws_bytes,
+                need, saved ? "_saved" : "");
   if (!aligned16(ws)) return fail(M3_E_ALIGN, "workspace must be 16-byte aligned");
+  if (saved) {
+    const size_t sneed = m3::scan_bwd_saved_bytes(bf, B, L, H, N, P, R);
+    if (saved_bytes < sneed)
+      return fail(M3_E_ARG, "saved-state buffer of %zu bytes, the shape needs %zu (m3_chunk_scan_saved_bytes)",
+                  saved_bytes, sneed);
+    if (!aligned16(saved)) return fail(M3_E_ALIGN, "saved-state buffer must be 16-byte aligned");
+  }
   m3::ScanBwd g;
   m3::ScanArgs& a = g.fwd;
   a.q = Q; a.k = K; a.v = V; a.adt = ADT; a.dt = DT; a.trap = Trap;
@@ -301,9 +326,50 @@ int scan_bwd(const void* Q, const void* K, const void* V,
   g.dq = dQ; g.dk = dK; g.dv = dV; g.dz = dZ;
   g.dadt = dADT; g.ddt = dDT; g.dtrap = dTrap; g.dang = dAngles;
   g.dqb = dQ_bias; g.dkb = dK_bias; g.dD = D ? dD : nullptr;
-  return check_launch(m3::scan_bwd_launch(g, bf, ws, reinterpret_cast<hipStream_t>(stream)), "scan backward");
+  return check_launch(m3::scan_bwd_launch(g, bf, ws, reinterpret_cast<hipStream_t>(stream), saved), "scan backward");
 }
 }  // namespace
+
+size_t m3_chunk_scan_saved_bytes(int B, int L, int H, int N, int P, int R, int io_dtype) {
+  if ((io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16) || B <= 0 || L <= 0 || H <= 0) return 0;
+  return m3::scan_bwd_saved_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, N, P, R);
+}
+
+int m3_chunk_scan_fwd_train(const void* Q, const void* K, const void* V,
+                            const float* ADT, const float* DT, const float* Trap,
+                            const float* Q_bias, const float* K_bias, const float* Angles,
+                            const float* D, const void* Z, void* Out,
+                            int B, int L, int H, int Hqk, int N, int P, int R,
+                            int chunk_size, int io_dtype, void* saved, size_t saved_bytes,
+                            void* ws, size_t ws_bytes, void* stream) {
+  if (saved == nullptr) return fail(M3_E_ARG, "NULL saved-state buffer");
+  return scan_fwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, nullptr, nullptr, nullptr, nullptr,
+                  nullptr, nullptr, nullptr, nullptr, B, L, H, Hqk, N, P, R, chunk_size, io_dtype, ws, ws_bytes,
+                  stream, false, 0, 0, saved, saved_bytes);
+}
+
+size_t m3_chunk_scan_bwd_saved_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
+                                        int io_dtype) {
+  if ((io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16) || B <= 0 || L <= 0 || H <= 0 || Hqk <= 0 ||
+      H % Hqk != 0 || chunk_size <= 0)
+    return 0;
+  return m3::scan_bwd_ws_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, Hqk, N, P, R, false, true);
+}
+
+int m3_chunk_scan_bwd_saved(const void* Q, const void* K, const void* V,
+                            const float* ADT, const float* DT, const float* Trap,
+                            const float* Q_bias, const float* K_bias, const float* Angles,
+                            const float* D, const void* Z, const void* dOut,
+                            void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                            float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                            int B, int L, int H, int Hqk, int N, int P, int R,
+                            int chunk_size, int io_dtype, const void* saved, size_t saved_bytes,
+                            void* ws, size_t ws_bytes, void* stream) {
+  if (saved == nullptr) return fail(M3_E_ARG, "NULL saved-state buffer");
+  return scan_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dOut, dQ, dK, dV, dADT, dDT, dTrap,
+                  dQ_bias, dK_bias, dAngles, dD, dZ, B, L, H, Hqk, N, P, R, chunk_size, io_dtype, ws, ws_bytes,
+                  stream, false, saved, saved_bytes);
+}
 
 size_t m3_chunk_scan_bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
                                   int io_dtype) {

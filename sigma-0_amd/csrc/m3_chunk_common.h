@@ -120,6 +120,22 @@ __device__ __forceinline__ bf16x8 staged_tr(const uint4* buf, int r_lo, int r_hi
   return f;
 }
 
+// Saved chunk states (the backward's residuals): each chunk's P x N state as 16 x 16
+// tiles (p-tile pr, n-tile nb) at element offset (pr * N/16 + nb) * 256, each tile in
+// the MFMA accumulator order (lane l, register r hold p = 16 pr + l % 16, n = 16 nb +
+// 4 (l / 16) + r), so that the state waves store whole 512-byte (bf16) rows of it.
+template <int N>
+__device__ __forceinline__ int saved_tile_off(int pr, int nb, int lane) {
+  return (pr * (N / 16) + nb) * 256 + 4 * lane;
+}
+// (p, n) of the four consecutive elements at offset 4 q of a saved chunk state.
+template <int N>
+__device__ __forceinline__ void saved_pos(int q, int& p, int& n) {
+  const int tile = q >> 6, ln = q & 63;
+  p = 16 * (tile / (N / 16)) + (ln & 15);
+  n = 16 * (tile % (N / 16)) + 4 * (ln >> 4);
+}
+
 // Store 4 consecutive elements (8 bytes bf16, 16 bytes f32).
 __device__ __forceinline__ void store4(bf16* p, const float* f) {
   bf16x4 v;

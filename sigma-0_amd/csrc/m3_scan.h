@@ -72,8 +72,16 @@ struct ScanBwd {
   float* dqb; float* dkb; float* dD;                   // (H, N), (H, N), (H,) or null
 };
 bool scan_bwd_supported(bool bf16_io, int N, int P, int R);
-size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared);
-hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st);
+// saved: the chunk states come from the training forward (no state-only pass)
+size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared,
+                         bool saved = false);
+// The training forward's saved chunk states: the state entering every chunk of the
+// backward's chunking ([bh][chunk][P][N], io type) and its rope angle ([bh][chunk][R]
+// f32, revolutions); bytes, and the two arrays' addresses in a buffer of that size.
+size_t scan_bwd_saved_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R);
+void scan_bwd_saved_ptrs(void* saved, bool bf16_io, int B, int L, int H, int N, int P, int R, void** h,
+                         float** th);
+hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st, const void* saved = nullptr);
 
 // Mamba3 mixer layer: the elementwise work around the scan.
 struct LayerPreArgs {

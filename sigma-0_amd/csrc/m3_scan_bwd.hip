@@ -376,7 +376,18 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
   for (int k = 0; k < HP; ++k) {
     const int i = tid + k * kBwdThreads;
     if (i < P * N / 8) {
-      *reinterpret_cast<Vec8<T>*>(&sm.h[i / (N / 8)][8 * (i % (N / 8))]) = cur.hpc[k];
+      // the state piece holds two 4-element groups of the saved tile order
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        int p, n;
+        saved_pos<N>(2 * i + j, p, n);
+        if constexpr (std::is_same<T, bf16>::value) {
+          const uint2 w = j ? make_uint2(cur.hpc[k].raw.z, cur.hpc[k].raw.w) : make_uint2(cur.hpc[k].raw.x, cur.hpc[k].raw.y);
+          *reinterpret_cast<uint2*>(&sm.h[p][n]) = w;
+        } else {
+          *reinterpret_cast<float4*>(&sm.h[p][n]) = j ? cur.hpc[k].b : cur.hpc[k].a;
+        }
+      }
       *reinterpret_cast<Vec8<T>*>(&sm.gt[i / (P / 8)][8 * (i % (P / 8))]) = cur.gpc[k];
     }
   }
@@ -987,9 +998,19 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     for (int k = 0; k < HP; ++k) {
       const int i = tid + k * kBwdThreads;
       if (i < P * N / 8) {
+        // the state piece holds two 4-element groups of the saved tile order
 #pragma unroll
-        for (int j = 0; j < Loads::HK; ++j)
-          reinterpret_cast<typename Loads::u32x4*>(&sm.h[i / (N / 8)][8 * (i % (N / 8))])[j] = cur.hpc[k][j];
+        for (int j = 0; j < 2; ++j) {
+          int p, n;
+          saved_pos<N>(2 * i + j, p, n);
+          if constexpr (Loads::HK == 1) {
+            typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+            const typename Loads::u32x4 w = cur.hpc[k][0];
+            *reinterpret_cast<u32x2*>(&sm.h[p][n]) = j ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]};
+          } else {
+            *reinterpret_cast<typename Loads::u32x4*>(&sm.h[p][n]) = cur.hpc[k][j];
+          }
+        }
       }
     }
     if (wave == 0) {
@@ -1797,7 +1818,22 @@ bool bwd_walk(int B, int H) {
   return (long)B * H >= kWalkMinBH;
 }
 
-BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared) {
+// The chunk states and angles the backward reads: computed by its own state-only pass
+// (in the workspace), or saved by the training forward (scan_bwd_saved_bytes, in the
+// caller's buffer, the same layout).
+size_t saved_h_bytes(bool bf16_io, int B, int L, int H, int N, int P) {
+  const int CS = bf16_io ? 64 : 32;
+  const long nc = (L + CS - 1) / CS;
+  return al256((size_t)B * H * nc * P * N * (bf16_io ? 2 : 4));
+}
+size_t saved_th_bytes(bool bf16_io, int B, int L, int H, int R) {
+  const int CS = bf16_io ? 64 : 32;
+  const long nc = (L + CS - 1) / CS;
+  return al256((size_t)B * H * nc * (R > 0 ? R : 1) * 4);
+}
+
+BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared,
+                 bool saved = false) {
   const int CS = bf16_io ? 64 : 32;
   const bool walk = bwd_walk(B, H);
   const long nc = (L + CS - 1) / CS, bhc = (long)B * H * nc;
@@ -1805,9 +1841,9 @@ BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R
   BwdWs w;
   size_t off = 0;
   auto take = [&](size_t bytes) { const size_t o = off; off += al256(bytes); return o; };
-  w.hs = take(bhc * P * N * ts);
+  w.hs = saved ? 0 : take(bhc * P * N * ts);
   w.gs = walk ? 0 : take(bhc * P * N * ts);     // the walk keeps the adjoint state on chip
-  w.th = take(bhc * (R > 0 ? R : 1) * 4);
+  w.th = saved ? 0 : take(bhc * (R > 0 ? R : 1) * 4);
   w.pqb = take(bhc * N * 4);
   w.pkb = take(bhc * N * 4);
   w.pd = take(bhc * 4);
@@ -1836,15 +1872,28 @@ bool scan_bwd_supported(bool bf16_io, int N, int P, int R) {
   return false;
 }
 
-size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared) {
+size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared,
+                         bool saved) {
   if (!scan_bwd_supported(bf16_io, N, P, R) || B <= 0 || L <= 0) return 0;
-  return bwd_layout(bf16_io, B, L, H, Hqk, N, P, R, ang_shared).total;
+  return bwd_layout(bf16_io, B, L, H, Hqk, N, P, R, ang_shared, saved).total;
 }
 
-hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st) {
+size_t scan_bwd_saved_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R) {
+  if (!scan_bwd_supported(bf16_io, N, P, R) || B <= 0 || L <= 0) return 0;
+  return saved_h_bytes(bf16_io, B, L, H, N, P) + saved_th_bytes(bf16_io, B, L, H, R);
+}
+
+void scan_bwd_saved_ptrs(void* saved, bool bf16_io, int B, int L, int H, int N, int P, int R, void** h,
+                         float** th) {
+  *h = saved;
+  *th = R > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(saved) + saved_h_bytes(bf16_io, B, L, H, N, P))
+              : nullptr;
+}
+
+hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st, const void* saved) {
   const ScanArgs& s = g.fwd;
   const int CS = bf16_io ? 64 : 32;
-  const BwdWs w = bwd_layout(bf16_io, s.B, s.L, s.H, s.Hqk, s.N, s.P, s.R, s.ang_shared != 0);
+  const BwdWs w = bwd_layout(bf16_io, s.B, s.L, s.H, s.Hqk, s.N, s.P, s.R, s.ang_shared != 0, saved != nullptr);
   char* base = reinterpret_cast<char*>(ws);
   BwdArgs a;
   a.s = s;
@@ -1854,9 +1903,17 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.dadt = g.dadt; a.ddt = g.ddt; a.dtrap = g.dtrap;
   a.dang = w.dangh ? reinterpret_cast<float*>(base + w.dangh) : g.dang;   // per head, then summed
   a.dqb = g.dqb; a.dkb = g.dkb; a.dD = g.dD;
-  a.hs = base + w.hs;
+  if (saved) {
+    void* sh;
+    float* sth;
+    scan_bwd_saved_ptrs(const_cast<void*>(saved), bf16_io, s.B, s.L, s.H, s.N, s.P, s.R, &sh, &sth);
+    a.hs = sh;
+    a.th0 = sth;
+  } else {
+    a.hs = base + w.hs;
+    a.th0 = reinterpret_cast<float*>(base + w.th);
+  }
   a.gs = bwd_walk(s.B, s.H) ? nullptr : base + w.gs;
-  a.th0 = reinterpret_cast<float*>(base + w.th);
   a.pqb = reinterpret_cast<float*>(base + w.pqb);
   a.pkb = reinterpret_cast<float*>(base + w.pkb);
   a.pd = reinterpret_cast<float*>(base + w.pd);
@@ -1866,17 +1923,20 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.ctot = reinterpret_cast<float*>(base + w.ctot);
   a.nc = (s.L + CS - 1) / CS;
 
-  // 1. chunk states and angles (the forward's state-only pass)
-  ScanArgs p1 = s;
-  p1.CS = CS;
-  p1.seg_len = 0; p1.init_per_seg = 0; p1.fin_per_seg = 0;
-  p1.init_theta = p1.init_h = p1.init_k = p1.init_v = nullptr;
-  p1.fin_theta = p1.fin_h = p1.fin_k = p1.fin_v = nullptr;
-  p1.fin_logdec = nullptr;
-  p1.chunk_h = base + w.hs;
-  p1.chunk_th = s.R > 0 ? reinterpret_cast<float*>(base + w.th) : nullptr;
-  hipError_t e = scan_state_launch(p1, bf16_io, st);
-  if (e != hipSuccess) return e;
+  // 1. chunk states and angles (the forward's state-only pass), unless saved
+  hipError_t e = hipSuccess;
+  if (!saved) {
+    ScanArgs p1 = s;
+    p1.CS = CS;
+    p1.seg_len = 0; p1.init_per_seg = 0; p1.fin_per_seg = 0;
+    p1.init_theta = p1.init_h = p1.init_k = p1.init_v = nullptr;
+    p1.fin_theta = p1.fin_h = p1.fin_k = p1.fin_v = nullptr;
+    p1.fin_logdec = nullptr;
+    p1.chunk_h = base + w.hs;
+    p1.chunk_th = s.R > 0 ? reinterpret_cast<float*>(base + w.th) : nullptr;
+    e = scan_state_launch(p1, bf16_io, st);
+    if (e != hipSuccess) return e;
+  }
 
   const dim3 grid_bh(s.B * s.H), grid_c(a.nc, s.B * s.H);
   bool found = false;

@@ -133,7 +133,9 @@ __device__ __forceinline__ void raw4_to_f(const uint4& r, float f[4]) {
 
 // SO (state only): the pass that produces each segment's exit carry from a zero
 // entering carry; it skips Q, Y_diag, Y_off, the gate and the output.
-template <typename T, int CS, int N, int P, int R, int NW, bool SO>
+// SAVE (full pass): also write each chunk's entering state and angles (chunk_h,
+// chunk_th), the residuals the backward reads instead of running the state-only pass.
+template <typename T, int CS, int N, int P, int R, int NW, bool SO, bool SAVE = false>
 __global__ __launch_bounds__(64 * NW, 1)
 void scan_chunked_kernel(ScanArgs a) {
   typedef Geo<T, CS, N, P, R, NW> G;
@@ -156,6 +158,9 @@ void scan_chunked_kernel(ScanArgs a) {
   const int L = a.seg_len > 0 ? min(Lg - tb, a.seg_len) : Lg;
   const int Lnx = Lg - tb;
   const int nc = (L + CS - 1) / CS;
+  // chunk-state outputs (the backward's saved states, chunk_h / chunk_th): indexed by
+  // the chunk over the whole sequence, so that the segments of a split pass write theirs
+  const long ch0 = (long)bh * ((Lg + CS - 1) / CS) + tb / CS;
   // carry slots: per (b, h) or per (b, h, segment)
   const int ci_in = a.init_per_seg ? bh * nseg + seg : bh;
   const int ci_out = a.fin_per_seg ? bh * nseg + seg : bh;
@@ -354,8 +359,9 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float th = __builtin_amdgcn_fractf(carry[k][j] + d[j]);
-          if constexpr (SO) {            // backward: the angle entering chunk cc (revolutions)
-            if (a.chunk_th && lane == 0) a.chunk_th[((long)bh * nc + cc) * R + 4 * g + j] = carry[k][j];
+          // the angle entering chunk cc (revolutions), for the backward
+          if constexpr (SO || SAVE) {
+            if (a.chunk_th && lane == 0) a.chunk_th[(ch0 + cc) * R + 4 * g + j] = carry[k][j];
           }
           carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
           p_cs[k][j] = __builtin_amdgcn_cosf(th);
@@ -619,13 +625,14 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
         for (int ks = 0; ks < CS / W::KSTEP; ++ks) W::load_w(&sm.wdec[pc][W::ktok(ks * W::KSTEP, ln)], wv[ks]);
         // ---- phases 4-5: h <- e^{A_end} h + K^T (w V) for my p-tile
-        if constexpr (SO) {                // backward: the state entering chunk c, [p][n]
+        // the state entering chunk c, for the backward
+        if constexpr (SO || SAVE) {
           if (a.chunk_h && part == 0) {
-            T* dst = reinterpret_cast<T*>(a.chunk_h) + ((long)(bh * nc + c) * P + pcol) * N + g4;
+            T* dst = reinterpret_cast<T*>(a.chunk_h) + (ch0 + c) * P * N;
 #pragma unroll
             for (int nb = 0; nb < G::NB16; ++nb) {
               const float hv[4] = {hs[nb][0], hs[nb][1], hs[nb][2], hs[nb][3]};
-              store4(dst + 16 * nb, hv);
+              store4(dst + saved_tile_off<N>(pr, nb, lane), hv);
             }
           }
         }
@@ -706,10 +713,25 @@ bool scan_chunked_supported(bool bf16_io, int CS_, int N, int P, int R) {
   return false;
 }
 
+// bf16 shapes whose full pass can also write the chunk states (the backward's shapes)
+#define M3_SAVE_SHAPES(X) \
+  X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0) X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 32, 16)
+
 hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
   if (!bf16_io) return scan_chunked_f32_launch(a, st);
   const int CS = kernel_chunk(bf16_io, a.CS);
   const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
+  if (a.chunk_h) {
+#define X(T, cs, n, p, r)                                                                            \
+  if (CS == cs && a.N == n && a.P == p && a.R == r) {                                                \
+    hipLaunchKernelGGL((scan_chunked_kernel<T, cs, n, p, r, kChunkWaves, false, true>), dim3(a.B * a.H, nseg), \
+                       dim3(64 * kChunkWaves), 0, st, a);                                             \
+    return hipGetLastError();                                                                         \
+  }
+    M3_SAVE_SHAPES(X)
+#undef X
+    return hipErrorInvalidValue;
+  }
 #define X(T, cs, n, p, r)                                                                            \
   if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && a.N == n && a.P == p && a.R == r) {   \
     hipLaunchKernelGGL((scan_chunked_kernel<T, cs, n, p, r, kChunkWaves, false>), dim3(a.B * a.H, nseg), \

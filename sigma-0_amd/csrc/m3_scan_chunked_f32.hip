@@ -116,7 +116,9 @@ struct __attribute__((aligned(16))) Smem {
 
 // SO (state only): the pass that produces each segment's exit carry from a zero
 // entering carry; it skips Q, Y_diag, Y_off, the gate and the output.
-template <typename T, int CS, int N, int P, int R, int NW, bool SO>
+// SAVE (full pass): also write each chunk's entering state and angles (chunk_h,
+// chunk_th), the residuals the backward reads instead of running the state-only pass.
+template <typename T, int CS, int N, int P, int R, int NW, bool SO, bool SAVE = false>
 __global__ __launch_bounds__(64 * NW, 1)
 void scan_chunked_f32_kernel(ScanArgs a) {
   typedef Geo<T, CS, N, P, R, NW> G;
@@ -139,6 +141,9 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   const int L = a.seg_len > 0 ? min(Lg - tb, a.seg_len) : Lg;
   const int Lnx = Lg - tb;
   const int nc = (L + CS - 1) / CS;
+  // chunk-state outputs (the backward's saved states, chunk_h / chunk_th): indexed by
+  // the chunk over the whole sequence, so that the segments of a split pass write theirs
+  const long ch0 = (long)bh * ((Lg + CS - 1) / CS) + tb / CS;
   // carry slots: per (b, h) or per (b, h, segment)
   const int ci_in = a.init_per_seg ? bh * nseg + seg : bh;
   const int ci_out = a.fin_per_seg ? bh * nseg + seg : bh;
@@ -355,8 +360,9 @@ void scan_chunked_f32_kernel(ScanArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float th = __builtin_amdgcn_fractf(carry[k][j] + d[j]);
-          if constexpr (SO) {            // backward: the angle entering chunk cc (revolutions)
-            if (a.chunk_th && lane == 0) a.chunk_th[((long)bh * nc + cc) * R + 4 * g + j] = carry[k][j];
+          // the angle entering chunk cc (revolutions), for the backward
+          if constexpr (SO || SAVE) {
+            if (a.chunk_th && lane == 0) a.chunk_th[(ch0 + cc) * R + 4 * g + j] = carry[k][j];
           }
           carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
           p_cs[k][j] = __builtin_amdgcn_cosf(th);
@@ -586,13 +592,14 @@ void scan_chunked_f32_kernel(ScanArgs a) {
         load_wv();
       }
       // ---- phases 4-5: h <- e^{A_end} h + K_s^T (w V) for my p-tile
-      if constexpr (SO) {                // backward: the state entering chunk c, [p][n]
+      // the state entering chunk c, [p][n], for the backward
+      if constexpr (SO || SAVE) {
         if (a.chunk_h && part == 0) {
-          T* dst = reinterpret_cast<T*>(a.chunk_h) + ((long)(bh * nc + c) * P + pcol) * N + g4;
+          T* dst = reinterpret_cast<T*>(a.chunk_h) + (ch0 + c) * P * N;
 #pragma unroll
           for (int nb = 0; nb < G::NB16; ++nb) {
             const float hv[4] = {hs[nb][0], hs[nb][1], hs[nb][2], hs[nb][3]};
-            store4(dst + 16 * nb, hv);
+            store4(dst + saved_tile_off<N>(pr, nb, lane), hv);
           }
         }
       }
@@ -666,9 +673,23 @@ bool scan_chunked_f32_supported(int CS_, int N, int P, int R) {
   return false;
 }
 
+// shapes whose full pass can also write the chunk states (the backward's float32 shapes)
+#define M3_F32_SAVE_SHAPES(X) X(32, 64, 64, 16) X(32, 64, 32, 16)
+
 hipError_t scan_chunked_f32_launch(const ScanArgs& a, hipStream_t st) {
   const int CS = f32_kernel_chunk(a.CS);
   const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
+  if (a.chunk_h) {
+#define X(cs, n, p, r)                                                                                 \
+  if (CS == cs && a.N == n && a.P == p && a.R == r) {                                                  \
+    hipLaunchKernelGGL((chunked_f32::scan_chunked_f32_kernel<float, cs, n, p, r, kF32Waves, false, true>), \
+                       dim3(a.B * a.H, nseg), dim3(64 * kF32Waves), 0, st, a);                         \
+    return hipGetLastError();                                                                          \
+  }
+    M3_F32_SAVE_SHAPES(X)
+#undef X
+    return hipErrorInvalidValue;
+  }
 #define X(cs, n, p, r)                                                                                 \
   if (CS == cs && a.N == n && a.P == p && a.R == r) {                                                  \
     hipLaunchKernelGGL((chunked_f32::scan_chunked_f32_kernel<float, cs, n, p, r, kF32Waves, false>),   \

@@ -18,10 +18,10 @@ from .decode import recurrent_angle_mode, recurrent_diagonal_mode, rnn_step_hip 
 from .layer import Mamba3Layer  # noqa: F401
 from .stack import Mamba3Stack  # noqa: F401
 from .ops import (mamba3_contraction_precision_mode, mamba3_siso_hip, mamba3_siso_hip_bwd,  # noqa: F401
-                  mamba3_siso_hip_carry, mamba3_ssd_chunked_hip, mamba3_ssd_chunked_shared_hip,
+                  mamba3_siso_hip_fwd_train, mamba3_siso_hip_carry, mamba3_ssd_chunked_hip, mamba3_ssd_chunked_shared_hip,
                   mamba3_ssd_chunked_shared_hip_bwd, new_carry)
 
-__all__ = ["mamba3_siso_hip", "mamba3_siso_hip_bwd", "mamba3_ssd_chunked_hip",
+__all__ = ["mamba3_siso_hip", "mamba3_siso_hip_bwd", "mamba3_siso_hip_fwd_train", "mamba3_ssd_chunked_hip",
            "mamba3_ssd_chunked_shared_hip", "mamba3_ssd_chunked_shared_hip_bwd", "mamba3_siso_hip_carry", "new_carry",
            "rnn_step_hip", "Mamba3Layer", "Mamba3Stack", "recurrent_angle_mode", "recurrent_diagonal_mode", "load",
            "Mamba3LibraryError", "mamba3_contraction_precision_mode"]

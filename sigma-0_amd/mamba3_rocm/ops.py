@@ -158,14 +158,44 @@ def _forward(args, chunk_size, seq_split):
     return out[0] if unbatched else out
 
 
+def _forward_train(args, chunk_size, seq_split):
+    """The forward plus the residuals its backward reads (the chunk states and their
+    rope angles), as the reference's mamba3_siso_fwd returns them
+    (mamba3_ops.py:788-818).  Returns (out, saved); saved is None where the library
+    has no saved-state path for the shape (the backward then recomputes)."""
+    p, (B, L, H, HQ, N, P, R), unbatched = _prep(*args)
+    out = torch.empty_like(p["V"])
+    if not out.numel():
+        return (out[0] if unbatched else out), None
+    lib = _lib.load()
+    io = _IO[p["V"].dtype]
+    kbwd = 64 if io == _lib.DTYPE_BF16 else 32
+    nbytes = lib.m3_chunk_scan_saved_bytes(B, L, H, N, P, R, io)
+    if nbytes == 0 or int(chunk_size) % kbwd != 0 or \
+            lib.m3_chunk_scan_impl(io, N, P, R, int(chunk_size)) != _lib.IMPL_CHUNKED_MFMA:
+        _launch(p, (B, L, H, HQ, N, P, R), chunk_size, out, seq_split=seq_split)
+        return (out[0] if unbatched else out), None
+    saved = torch.empty(nbytes, dtype=torch.uint8, device=p["V"].device)
+    ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, H, N, P, R, int(chunk_size), io) if seq_split else 0
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=p["V"].device)
+    rc = lib.m3_chunk_scan_fwd_train(
+        _ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
+        _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(out),
+        B, L, H, HQ, N, P, R, int(chunk_size), io, saved.data_ptr(), nbytes,
+        ws.data_ptr() if ws_bytes else None, ws_bytes, _stream(p["V"]))
+    _lib.check(rc, "m3_chunk_scan_fwd_train")
+    return (out[0] if unbatched else out), saved
+
+
 def mamba3_siso_hip_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dOut,
-                        chunk_size: int = 64):
+                        chunk_size: int = 64, saved: Optional[torch.Tensor] = None):
     """Gradients of mamba3_siso_hip's output against every input, given dOut (the
     output cotangent, V's shape).  The reference's backward (mamba3_siso_bwd,
     mamba3_ops.py:821-902) returns the same tuple:
     (dQ, dK, dV, dADT, dDT, dTrap, dQ_bias, dK_bias, dAngles, dD, dZ), each in its
-    input's shape; dD and dZ are None when D and Z are.  The forward is recomputed
-    from the inputs (no saved state)."""
+    input's shape; dD and dZ are None when D and Z are.  ``saved``: the residuals of
+    the training forward on the same inputs (mamba3_siso_hip_fwd_train); without
+    them the chunk states are recomputed from the inputs."""
     p, (B, L, H, HQ, N, P, R), unbatched = _prep(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z)
     io = _IO[p["V"].dtype]
     dO = (dOut[None] if unbatched else dOut).to(p["V"].dtype).contiguous()
@@ -180,17 +210,24 @@ def mamba3_siso_hip_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dO
              Z=None if p["Z"] is None else torch.empty_like(p["Z"]))
     if B and L:
         lib = _lib.load()
-        ws_bytes = lib.m3_chunk_scan_bwd_ws_bytes(B, L, H, HQ, N, P, R, int(chunk_size), io)
+        if saved is None:
+            ws_bytes = lib.m3_chunk_scan_bwd_ws_bytes(B, L, H, HQ, N, P, R, int(chunk_size), io)
+        else:
+            ws_bytes = lib.m3_chunk_scan_bwd_saved_ws_bytes(B, L, H, HQ, N, P, R, int(chunk_size), io)
         if ws_bytes == 0:
             raise _lib.Mamba3LibraryError(
                 f"no backward kernel for dtype={dt} d_state={N} headdim={P} rope angles={R}")
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        rc = lib.m3_chunk_scan_bwd(
-            _ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
-            _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(dO),
-            _ptr(g["Q"]), _ptr(g["K"]), _ptr(g["V"]), _ptr(g["ADT"]), _ptr(g["DT"]), _ptr(g["Trap"]),
-            _ptr(g["Q_bias"]), _ptr(g["K_bias"]), _ptr(g["Angles"]), _ptr(g["D"]), _ptr(g["Z"]),
-            B, L, H, HQ, N, P, R, int(chunk_size), io, ws.data_ptr(), ws_bytes, _stream(p["V"]))
+        ptrs = (_ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
+                _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(dO),
+                _ptr(g["Q"]), _ptr(g["K"]), _ptr(g["V"]), _ptr(g["ADT"]), _ptr(g["DT"]), _ptr(g["Trap"]),
+                _ptr(g["Q_bias"]), _ptr(g["K_bias"]), _ptr(g["Angles"]), _ptr(g["D"]), _ptr(g["Z"]),
+                B, L, H, HQ, N, P, R, int(chunk_size), io)
+        if saved is None:
+            rc = lib.m3_chunk_scan_bwd(*ptrs, ws.data_ptr(), ws_bytes, _stream(p["V"]))
+        else:
+            rc = lib.m3_chunk_scan_bwd_saved(*ptrs, saved.data_ptr(), saved.numel(), ws.data_ptr(), ws_bytes,
+                                             _stream(p["V"]))
         _lib.check(rc, "m3_chunk_scan_bwd")
     else:
         for t in g.values():
@@ -203,20 +240,30 @@ def mamba3_siso_hip_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dO
     return tuple(g[k] for k in order)
 
 
+def mamba3_siso_hip_fwd_train(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
+                              chunk_size: int = 64, seq_split: bool = True):
+    """The reference's mamba3_siso_fwd (mamba3_ops.py:788-818): the output and the
+    residuals for mamba3_siso_hip_bwd(..., saved=...) (None where the shape has no
+    saved-state path)."""
+    return _forward_train((Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z), chunk_size, seq_split)
+
+
 class _Mamba3Siso(torch.autograd.Function):
     """mamba3_siso_hip with its backward: the reference's custom_vjp pair
-    (mamba3_ops.py:909-1045).  Saves the inputs only; the backward recomputes."""
+    (mamba3_ops.py:909-1045).  Saves the inputs and the forward's chunk states, which
+    the backward reads instead of recomputing them."""
 
     @staticmethod
     def forward(ctx, chunk_size, seq_split, *args):
         ctx.chunk_size = chunk_size
-        ctx.save_for_backward(*(t if isinstance(t, torch.Tensor) else None for t in args))
-        return _forward(args, chunk_size, seq_split)
+        out, saved = _forward_train(args, chunk_size, seq_split)
+        ctx.save_for_backward(*(t if isinstance(t, torch.Tensor) else None for t in args), saved)
+        return out
 
     @staticmethod
     def backward(ctx, dout):
-        args = ctx.saved_tensors
-        grads = mamba3_siso_hip_bwd(*args, dout, chunk_size=ctx.chunk_size)
+        *args, saved = ctx.saved_tensors
+        grads = mamba3_siso_hip_bwd(*args, dout, chunk_size=ctx.chunk_size, saved=saved)
         out = []
         for t, gr in zip(args, grads):
             out.append(None if t is None or gr is None else gr.to(t.dtype))

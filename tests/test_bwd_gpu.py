@@ -120,3 +120,52 @@ def test_gradients_with_more_items_than_compute_units(B, L, H, Hqk, N, P, R, bf1
     """More (chunk, b, h) items than compute units (longer sequences and more heads
     than the cases above): several waves of chunk-gradient workgroups per launch."""
     _check(B, L, H, Hqk, N, P, R, bf16=bf16, seed=37)
+
+
+@pytest.mark.parametrize("B,L,H,Hqk,N,P,R,bf16,split", [
+    (1, 200, 2, 2, 128, 64, 32, True, False),
+    (2, 130, 4, 2, 128, 64, 32, True, False),     # GQA
+    (1, 1100, 3, 3, 128, 64, 32, True, True),     # the forward takes the sequence split
+    (1, 150, 2, 2, 64, 32, 16, False, False),
+])
+def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_route):
+    """The training forward (the reference's mamba3_siso_fwd, which returns the
+    per-chunk states with its output, mamba3_ops.py:788-818) gives the plain forward's
+    output bitwise, and the backward that reads its saved chunk states gives the
+    recomputing backward's gradients: bitwise where both produce the states with the
+    same kernel code (bf16 one pass), within rounding where the forward's states come
+    from another kernel (float32 I/O, the split), and within the bars against the
+    oracle."""
+    torch = _torch()
+    from mamba3_rocm import mamba3_siso_hip, mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
+    from mamba3_rocm import _lib
+    d = I.scan_inputs(B, L, H, N, P, R, seed=41, Hqk=Hqk, bf16=bf16)
+    cot = V.cotangent(B, L, H, P, seed=42)
+    tdt = torch.bfloat16 if bf16 else torch.float32
+    if bf16:
+        cot = I.bf16_round(cot)
+    print(f"case training pair {(B, L, H, Hqk, N, P, R)} bf16={bf16} split={split}", flush=True)
+    t = to_dev(d, tdt)
+    args = tuple(t[k] for k in V.NAMES)
+    io = _lib.DTYPE_BF16 if bf16 else _lib.DTYPE_F32
+    assert (_lib.load().m3_chunk_scan_ws_bytes(B, L, H, N, P, R, 64, io) > 0) == split
+    out_tr, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=64)
+    out = mamba3_siso_hip(*args, chunk_size=64)
+    torch.cuda.synchronize()
+    assert saved is not None
+    assert torch.equal(out_tr, out), "training forward output differs from the forward"
+    dout = torch.from_numpy(np.ascontiguousarray(cot)).to("cuda").to(tdt)
+    g_saved = mamba3_siso_hip_bwd(*args, dout, chunk_size=64, saved=saved)
+    g_re = mamba3_siso_hip_bwd(*args, dout, chunk_size=64)
+    torch.cuda.synchronize()
+    _, ref = V.vjp(d, cot, 16)
+    exact = bf16 and not split
+    for name, a, b, r in zip(V.NAMES, g_saved, g_re, ref):
+        if r is None:
+            continue
+        a, b = a.float().cpu().numpy(), b.float().cpu().numpy()
+        if exact:
+            assert np.array_equal(a, b), f"d{name}: saved-state backward differs from the recompute"
+        else:
+            assert rel(a, b) <= (1e-2 if bf16 else 1e-5), (name, rel(a, b))
+        assert rel(a, r) <= (BF16_TOL if bf16 else F32_TOL), (name, rel(a, r))

@@ -41,7 +41,9 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_ws", "m3_chunk_scan_fwd_noalloc",
                             "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd",
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
-                            "m3_chunk_scan_bwd_shared", "m3_decode_step", "m3_layer_pre",
+                            "m3_chunk_scan_bwd_shared", "m3_chunk_scan_saved_bytes",
+                            "m3_chunk_scan_fwd_train", "m3_chunk_scan_bwd_saved_ws_bytes",
+                            "m3_chunk_scan_bwd_saved", "m3_decode_step", "m3_layer_pre",
                             "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu",
                             "m3_block_act", "m3_block_act_norm", "m3_log_softmax"])
     for n in names:
@@ -98,29 +100,75 @@ def test_split_workspace_sizes(lib):
     assert f(1, 1061, 3, 128, 64, 32, 64, bf) > 0
 
 
-def test_backward_workspace_sizes(lib):
-    """Backward workspace: chunk-entering states and adjoint states (B*H*nc*P*N in
-    the I/O type each, 64-token chunks for bf16, 32 for fp32), chunk angles, bias and
-    D partials, per-token d(scale), chunk sums of dA and d(theta), and per-head dQ/dK
-    (float32) when Hqk < H; 0 without a kernel."""
+def _bwd_ws_expect(B, L, H, Hqk, N, P, R, io, saved=False):
+    """Backward workspace: chunk-entering states (B*H*nc*P*N in the I/O type, 64-token
+    chunks for bf16, 32 for fp32) and chunk angles (unless the training forward saved
+    them), adjoint states after each chunk (chunk-parallel route, B*H < 128, only),
+    bias and D partials, per-token d(scale), chunk sums of dA and d(theta), and
+    per-head dQ/dK (float32) when Hqk < H."""
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    cs = 64 if io == 1 else 32
+    bhc = B * H * ((L + cs - 1) // cs)
+    ts = 2 if io == 1 else 4
+    walk = B * H >= 128
+    n = 2 * al(bhc * N * 4) + al(bhc * 4) + al(B * H * L * 4) + al(bhc * (R + 1) * 4)
+    if not saved:
+        n += al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4)
+    if not walk:
+        n += al(bhc * P * N * ts)
+    if Hqk < H:
+        n += 2 * al(B * L * H * N * 4)
+    return n
+
+
+def test_backward_workspace_sizes(lib, monkeypatch):
+    monkeypatch.delenv("M3_BWD_ROUTE", raising=False)
     f = lib.m3_chunk_scan_bwd_ws_bytes
     bf, f32 = 1, 0
-    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
-
-    def expect(B, L, H, Hqk, N, P, R, io):
-        cs = 64 if io == bf else 32
-        bhc = B * H * ((L + cs - 1) // cs)
-        ts = 2 if io == bf else 4
-        n = (2 * al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4) + 2 * al(bhc * N * 4) + al(bhc * 4)
-             + al(B * H * L * 4) + al(bhc * (R + 1) * 4))
-        if Hqk < H:
-            n += 2 * al(B * L * H * N * 4)
-        return n
-    assert f(8, 4096, 32, 32, 128, 64, 32, 64, bf) == expect(8, 4096, 32, 32, 128, 64, 32, bf)
-    assert f(2, 300, 4, 2, 64, 32, 16, 64, f32) == expect(2, 300, 4, 2, 64, 32, 16, f32)
+    assert f(8, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, bf)
+    assert f(2, 300, 4, 2, 64, 32, 16, 64, f32) == _bwd_ws_expect(2, 300, 4, 2, 64, 32, 16, f32)
     assert f(1, 100, 2, 2, 64, 16, 16, 64, bf) == 0        # headdim 16: no backward kernel
     assert f(1, 100, 2, 2, 128, 64, 32, 64, 7) == 0        # unknown dtype
     assert f(1, 100, 3, 2, 128, 64, 32, 64, bf) == 0       # H not a multiple of Hqk
+    # the route can be forced (the chunk-parallel route adds the adjoint states)
+    monkeypatch.setenv("M3_BWD_ROUTE", "chunks")
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    assert f(8, 4096, 32, 32, 128, 64, 32, 64, bf) == (_bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, bf)
+                                                        + al(8 * 32 * 64 * 64 * 128 * 2))
+
+
+def test_saved_state_sizes_and_validation(lib, monkeypatch):
+    """The training pair: the residual buffer holds the chunk-entering states (io type)
+    and chunk angles (float32) of the backward's chunking; the saved-state backward's
+    workspace drops them; calls validate before any launch."""
+    monkeypatch.delenv("M3_BWD_ROUTE", raising=False)
+    E_ARG, E_UNSUP = _header_define("M3_E_ARG"), _header_define("M3_E_UNSUPPORTED")
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    bf, f32 = 1, 0
+    sb = lib.m3_chunk_scan_saved_bytes
+    assert sb(8, 4096, 32, 128, 64, 32, bf) == al(8 * 32 * 64 * 64 * 128 * 2) + al(8 * 32 * 64 * 32 * 4)
+    assert sb(2, 300, 4, 64, 32, 16, f32) == al(2 * 4 * 10 * 32 * 64 * 4) + al(2 * 4 * 10 * 16 * 4)
+    assert sb(1, 100, 2, 64, 16, 16, bf) == 0               # no backward kernel
+    wsb = lib.m3_chunk_scan_bwd_saved_ws_bytes
+    assert wsb(8, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, bf, True)
+    assert wsb(2, 300, 4, 2, 64, 32, 16, 64, f32) == _bwd_ws_expect(2, 300, 4, 2, 64, 32, 16, f32, True)
+    p = ctypes.c_void_p(4096)
+
+    def fwd(saved=p, nbytes=1 << 40, CS=64, N=128, P=64, R=32, io=bf):
+        return lib.m3_chunk_scan_fwd_train(p, p, p, p, p, p, p, p, p, p, p, p, 1, 8, 2, 2, N, P, R, CS, io,
+                                           saved, nbytes, None, 0, None)
+    assert fwd(saved=None) == E_ARG
+    assert fwd(nbytes=16) == E_ARG and b"saved-state buffer" in lib.m3_last_error()
+    assert fwd(CS=32) == E_UNSUP and b"multiple of 64" in lib.m3_last_error()
+    assert fwd(P=16) == E_UNSUP                              # no backward for the shape
+    assert fwd(io=f32, CS=48, N=64, P=64, R=16) == E_UNSUP   # f32: multiple of 32
+
+    def bwd(saved=p, nbytes=1 << 40):
+        return lib.m3_chunk_scan_bwd_saved(p, p, p, p, p, p, p, p, p, p, p, p,
+                                           p, p, p, p, p, p, p, p, p, p, p,
+                                           1, 8, 2, 2, 128, 64, 32, 64, bf, saved, nbytes, p, 1 << 40, None)
+    assert bwd(saved=None) == E_ARG
+    assert bwd(nbytes=16) == E_ARG and b"saved-state buffer" in lib.m3_last_error()
 
 
 def test_backward_validation(lib):
