@@ -1807,10 +1807,13 @@ struct BwdWs {
 
 // Route of the backward.  The reverse walk runs one workgroup per (b, h), so it fills
 // the chip only when B * H is large; below kWalkMinBH the chunk-parallel kernels (one
-// workgroup per (chunk, b, h), with the adjoint pass before them) run instead.  The
+// workgroup per (chunk, b, h), with the adjoint pass before them) run instead.
+// Measured (bf16, d_state 128, headdim 64): the routes tie at 64 pairs (1.08 / 1.05
+// ms at L=4096), the walk wins at 96 (3.25 / 3.97 ms at config 5's B=4, L=12288,
+// H=24) and 128 (1.12 / 1.54 ms), the chunks at 32 (2.11 / 1.60 ms at L=8192).  The
 // environment variable M3_BWD_ROUTE = "walk" or "chunks" forces one of them (tests,
 // measurements).
-constexpr long kWalkMinBH = 128;
+constexpr long kWalkMinBH = 80;
 bool bwd_walk(int B, int H) {
   const char* e = getenv("M3_BWD_ROUTE");
   if (e && !strcmp(e, "walk")) return true;

@@ -110,7 +110,7 @@ def _bwd_ws_expect(B, L, H, Hqk, N, P, R, io, saved=False):
     cs = 64 if io == 1 else 32
     bhc = B * H * ((L + cs - 1) // cs)
     ts = 2 if io == 1 else 4
-    walk = B * H >= 128
+    walk = B * H >= 80
     n = 2 * al(bhc * N * 4) + al(bhc * 4) + al(B * H * L * 4) + al(bhc * (R + 1) * 4)
     if not saved:
         n += al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4)
