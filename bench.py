@@ -16,9 +16,10 @@ Also reported on the same JSON line:
   secondary     decode state update (config 4, HBM GB/s), the long-context
                 scan (config 3), the shared-B/C scan, the float32-I/O scan, the scan
                 backward at config 2 (recomputing its chunk states) and the
-                training pair (forward with residuals, backward from them), each
-                with its own roofline, and the 12-layer backbone prefill with its
-                log-probabilities (config 5)
+                training pair (forward with residuals, backward from them), with bf16
+                and with float32 I/O (what the model's training hands the scan),
+                each with its own roofline, and the 12-layer backbone prefill with
+                its log-probabilities (config 5)
 
 Before the warm-up of the headline, the kernel is launched untimed until at least
 100 launches and 0.3 s have run (the GPU clocks ramp up over the first ~100
@@ -28,6 +29,7 @@ launches of a process); the JSON line reports this as ``clock_settle``, apart fr
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-secondary]
                        [--mode scan|decode|long|bwd|train|shared|layer|stack|copy|fp32]
+                       [--io bf16|f32]   (--mode bwd / train)
        python bench.py --mode traffic --pmc-dir DIR   (writes the traffic JSON of
                        the headline kernel from rocprofv3 --pmc FETCH_SIZE /
                        WRITE_SIZE runs of the scan and of the copy kernel)
@@ -90,6 +92,14 @@ def bwd_bytes(B, L, H, N, P, R, s_io):
     written once (dQ, dK; dV, dZ at s_io; dADT, dDT, dTrap, dAngles f32), per
     token-head.  The chunk states it keeps in its workspace are not counted."""
     return B * L * H * ((2 * N + 3 * P) * s_io + 3 * 4 + R * 4 + (2 * N + 2 * P) * s_io + 3 * 4 + R * 4)
+
+
+def bwd_flops(B, L, H, N, P, CS):
+    """Dense-tile MFMA FLOP count of one backward call, per token-head: the chunk's
+    S = q~ k~^T, dP = dy v^T, y and dV (intra-chunk S v / S^T dy, inter-chunk q~ h and
+    k~ G), the adjoint update dy^T q~, dq~ and dk~ (dP k~ + dy h, dP^T q~ + v G):
+    3 (2 CS N) + 3 (2 CS P) + 5 (2 P N)."""
+    return B * L * H * (6 * CS * N + 6 * CS * P + 10 * P * N)
 
 
 def decode_bytes(B, H, N, P, R, s_in, s_out):
@@ -169,40 +179,51 @@ def bench_scan(torch, B, L, H, N, P, R, CS, steps, warmup, seed, settle=False, i
                 achieved_gbs=nbytes / kern / 1e9, settle=settled)
 
 
-def bench_bwd(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
+def bwd_chunk(torch, io_dtype):
+    """The backward kernels' chunk: 64 tokens with bf16 I/O, 32 with float32."""
+    return 64 if io_dtype == torch.bfloat16 else 32
+
+
+def bench_bwd(torch, B, L, H, N, P, R, CS, steps, warmup, seed, io_dtype=None):
     """Backward of the scan (all eleven input gradients) on the config's inputs and a
     N(0, 1) output cotangent."""
     from mamba3_rocm import mamba3_siso_hip_bwd
-    args = make_scan_inputs(torch, B, L, H, N, P, R, seed, torch.bfloat16)
+    io_dtype = io_dtype or torch.bfloat16
+    args = make_scan_inputs(torch, B, L, H, N, P, R, seed, io_dtype)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 1000)
-    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(torch.bfloat16)
+    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(io_dtype)
     fn = lambda: mamba3_siso_hip_bwd(*args, dout, chunk_size=CS)  # noqa: E731
     wall, kern = time_calls(torch, fn, steps, warmup)
-    nbytes = bwd_bytes(B, L, H, N, P, R, 2)
-    return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
+    nbytes = bwd_bytes(B, L, H, N, P, R, args[0].element_size())
+    flops = bwd_flops(B, L, H, N, P, bwd_chunk(torch, io_dtype))
+    return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9, flops=flops)
 
 
-def bench_train(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
+def bench_train(torch, B, L, H, N, P, R, CS, steps, warmup, seed, io_dtype=None):
     """The training pair on the config's inputs: the forward that also writes the
     backward's residuals (the state and rope angle entering every chunk) and the
     backward that reads them instead of recomputing the chunk states -- the
     reference's mamba3_siso_fwd / mamba3_siso_bwd(saved, ...) (mamba3_ops.py:788-902).
     Each is timed on its own (HIP events), with an N(0, 1) output cotangent."""
     from mamba3_rocm import mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
-    args = make_scan_inputs(torch, B, L, H, N, P, R, seed, torch.bfloat16)
+    io_dtype = io_dtype or torch.bfloat16
+    args = make_scan_inputs(torch, B, L, H, N, P, R, seed, io_dtype)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 1000)
-    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(torch.bfloat16)
+    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(io_dtype)
     _, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=CS)
     fwd = lambda: mamba3_siso_hip_fwd_train(*args, chunk_size=CS)  # noqa: E731
     bwd = lambda: mamba3_siso_hip_bwd(*args, dout, chunk_size=CS, saved=saved)  # noqa: E731
     wf, kf = time_calls(torch, fwd, steps, warmup)
     wb, kb = time_calls(torch, bwd, steps, warmup)
-    fbytes = scan_bytes(B, L, H, N, P, R, 2) + saved.numel()          # + the residuals written
-    bbytes = bwd_bytes(B, L, H, N, P, R, 2)
+    s_io = args[0].element_size()
+    fbytes = scan_bytes(B, L, H, N, P, R, s_io) + saved.numel()       # + the residuals written
+    bbytes = bwd_bytes(B, L, H, N, P, R, s_io)
     return dict(fwd_s=kf, bwd_s=kb, wall_s=wf + wb, saved_bytes=saved.numel(),
-                fwd_gbs=fbytes / kf / 1e9, bwd_gbs=bbytes / kb / 1e9)
+                fwd_gbs=fbytes / kf / 1e9, bwd_gbs=bbytes / kb / 1e9,
+                fwd_flops=scan_flops(B, L, H, N, P, bwd_chunk(torch, io_dtype)),
+                bwd_flops=bwd_flops(B, L, H, N, P, bwd_chunk(torch, io_dtype)))
 
 
 def bench_shared(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
@@ -415,6 +436,31 @@ def write_traffic(pmc_dir, kernel_avg_us=None):
     print(json.dumps(d), flush=True)
 
 
+def bwd_line(r, fp32=False):
+    """The JSON fields of a backward measurement: time, tokens/s, and its roofline --
+    HBM for bf16 I/O; float32 MFMA for float32 I/O, whose dense-tile MFMA work takes
+    longer at the float32 peak than its bytes at the HBM peak."""
+    d = {"ms": round(r["kernel_s"] * 1e3, 4), "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
+         "achieved_gbs": round(r["achieved_gbs"], 1), "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}
+    if fp32:
+        tf = r["flops"] / r["kernel_s"] / 1e12
+        d.update(bound="mfma_fp32", tflops=round(tf, 1), frac_mfma_fp32=round(tf / FP32_MFMA_PEAK_TFLOPS, 4))
+    return d
+
+
+def train_line(r, fp32=False):
+    """The JSON fields of a training-pair measurement (forward with residuals, backward
+    from them); the backward's roofline as in bwd_line."""
+    d = {"fwd_with_residuals_ms": round(r["fwd_s"] * 1e3, 4), "bwd_from_residuals_ms": round(r["bwd_s"] * 1e3, 4),
+         "step_ms": round((r["fwd_s"] + r["bwd_s"]) * 1e3, 4), "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
+         "residual_bytes": r["saved_bytes"], "bwd_achieved_gbs": round(r["bwd_gbs"], 1),
+         "bwd_frac_hbm": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4)}
+    if fp32:
+        tf = r["bwd_flops"] / r["bwd_s"] / 1e12
+        d.update(bwd_bound="mfma_fp32", bwd_tflops=round(tf, 1), bwd_frac_mfma_fp32=round(tf / FP32_MFMA_PEAK_TFLOPS, 4))
+    return d
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -425,6 +471,7 @@ def main():
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--io", choices=("bf16", "f32"), default="bf16", help="--mode bwd / train: the I/O dtype")
     args = ap.parse_args()
 
     if args.mode == "traffic":
@@ -452,21 +499,16 @@ def main():
         print(json.dumps({"mode": "decode", **r}), flush=True)
         return
 
+    io = torch.float32 if args.io == "f32" else torch.bfloat16
     if args.mode == "bwd":
         # backward at config 2 alone, for profiling
-        r = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)
-        print(json.dumps({"mode": "bwd", "ms": round(r["kernel_s"] * 1e3, 4),
-                          "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
-                          "achieved_gbs": round(r["achieved_gbs"], 1),
-                          "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        r = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2, io_dtype=io)
+        print(json.dumps({"mode": "bwd", "io_dtype": args.io, **bwd_line(r)}), flush=True)
         return
     if args.mode == "train":
         # the training pair at config 2 (forward with residuals, backward from them)
-        r = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)
-        print(json.dumps({"mode": "train", "fwd_ms": round(r["fwd_s"] * 1e3, 4),
-                          "bwd_ms": round(r["bwd_s"] * 1e3, 4),
-                          "step_ms": round((r["fwd_s"] + r["bwd_s"]) * 1e3, 4),
-                          "bwd_frac_hbm": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4)}), flush=True)
+        r = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2, io_dtype=io)
+        print(json.dumps({"mode": "train", "io_dtype": args.io, **train_line(r)}), flush=True)
         return
     if args.mode == "layer":
         r = bench_layer(torch, 4, 12288, 768, args.steps, args.warmup, seed=5)
@@ -539,6 +581,10 @@ def main():
         lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
         bw = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         tr = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
+        bw32 = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 10), 2, seed=2,
+                         io_dtype=torch.float32)
+        tr32 = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 10), 2, seed=2,
+                           io_dtype=torch.float32)
         sh = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         f32 = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2,
                          io_dtype=torch.float32)
@@ -566,19 +612,12 @@ def main():
                                 "frac_mfma_fp32": round(f32["flops"] / f32["kernel_s"] / 1e12
                                                         / FP32_MFMA_PEAK_TFLOPS, 4),
                                 "achieved_gbs": round(f32["achieved_gbs"], 1)},
-            "backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
-                                 "ms": round(bw["kernel_s"] * 1e3, 4),
-                                 "tokens_per_s": round(8 * 4096 / bw["wall_s"], 1),
-                                 "achieved_gbs": round(bw["achieved_gbs"], 1),
-                                 "frac_hbm": round(bw["achieved_gbs"] / HBM_PEAK_GBS, 4)},
-            "training_pair_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
-                                      "fwd_with_residuals_ms": round(tr["fwd_s"] * 1e3, 4),
-                                      "bwd_from_residuals_ms": round(tr["bwd_s"] * 1e3, 4),
-                                      "step_ms": round((tr["fwd_s"] + tr["bwd_s"]) * 1e3, 4),
-                                      "tokens_per_s": round(8 * 4096 / tr["wall_s"], 1),
-                                      "residual_bytes": tr["saved_bytes"],
-                                      "bwd_achieved_gbs": round(tr["bwd_gbs"], 1),
-                                      "bwd_frac_hbm": round(tr["bwd_gbs"] / HBM_PEAK_GBS, 4)},
+            "backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **bwd_line(bw)},
+            "training_pair_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **train_line(tr)},
+            "backward_fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",
+                                         **bwd_line(bw32, fp32=True)},
+            "training_pair_fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",
+                                              **train_line(tr32, fp32=True)},
             "backbone_prefill_config5": {"B": 4, "L": 12288, "layers": 12, "d_model": 768, "vocab": 2112,
                                          "activation": "half_glu1", "prenorm": True, "dtype": "bf16",
                                          "ms": round(bb["kernel_s"] * 1e3, 4),

@@ -58,6 +58,9 @@ hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st);
 // Its float32-I/O kernel (m3_scan_chunked_f32.hip), reached through the two above.
 bool scan_chunked_f32_supported(int CS, int N, int P, int R);
 hipError_t scan_chunked_f32_launch(const ScanArgs& a, hipStream_t st);
+// and its state-only pass (the backward's chunk states at float32, d_state 128)
+bool scan_state_f32_supported(int CS, int N, int P, int R);
+hipError_t scan_state_f32_launch(const ScanArgs& a, hipStream_t st);
 
 // State-only pass of the chunked kernel (sequence split pass 1, backward chunk states).
 bool scan_state_supported(bool bf16_io, int CS, int N, int P, int R);

@@ -831,6 +831,11 @@ struct WalkLoads {
 // results and the d(theta) output tile (the four dq~/dk~ passes).  Within (B) and (C)
 // the offsets keep apart what is live at the same time: lo is written while the
 // output tiles are still being stored, res while the dAngles tile is read.
+// float keeps the LDS of d_state 128 under the 160 KB limit with two more reuses:
+// Q and K rows are staged in qt / kt themselves (the preparation reads each thread's
+// own 8 raw elements and writes its q~ / k~ back to the same place), and window (C)
+// lives outside `u`: res in fz's storage and the d(theta) tile in the masked S's,
+// both dead after the y/dV phase.
 template <typename T, int CS, int N, int P, int R>
 struct WalkSmem {
   static constexpr bool BF = std::is_same<T, bf16>::value;
@@ -850,10 +855,12 @@ struct WalkSmem {
   static constexpr size_t SZ_DTH = (size_t)CS * RH * 4;
   static constexpr size_t OFF_K = SZ_Q, OFF_OUT = SZ_SM;
   // bf16: res may overlap the output tiles (it is first written after the residual
-  // barrier); float has no residual barrier, so res starts after them
-  static constexpr size_t OFF_RES = BF ? SZ_LO : SZ_SM + SZ_OUT;
+  // barrier)
+  static constexpr size_t OFF_RES = SZ_LO;
   static constexpr size_t OFF_DTH = OFF_RES + SZ_RES;
-  static constexpr size_t U1 = 2 * SZ_Q, U2 = SZ_SM + SZ_OUT, U3 = OFF_DTH + SZ_DTH;
+  static constexpr size_t U1 = BF ? 2 * SZ_Q : 0, U2 = SZ_SM + SZ_OUT, U3 = BF ? OFF_DTH + SZ_DTH : 0;
+  static_assert(BF || (SZ_RES <= (size_t)CS * (P + PAD) * sizeof(T) && SZ_DTH <= SZ_SM),
+                "float: res fits fz's storage, the d(theta) tile the masked S's");
   static constexpr size_t U = U1 > U2 ? (U1 > U3 ? U1 : U3) : (U2 > U3 ? U2 : U3);
   alignas(16) T qt[CS][N + PADN];       // q~
   alignas(16) T kt[CS][N + PADN];       // k~
@@ -875,35 +882,19 @@ struct WalkSmem {
   __device__ __forceinline__ T* smk() { return reinterpret_cast<T*>(u); }                  // [CS][CS + PAD]
   __device__ __forceinline__ T* outs(int w) { return reinterpret_cast<T*>(u + OFF_OUT) + (size_t)w * CS * (P + PAD); }
   __device__ __forceinline__ T* lo() { return reinterpret_cast<T*>(u); }                   // [CS][NH + PAD]
-  __device__ __forceinline__ float* res() { return reinterpret_cast<float*>(u + OFF_RES); }  // [CS][NH + 4]
-  __device__ __forceinline__ float* dth() { return reinterpret_cast<float*>(u + OFF_DTH); }  // [CS][RH]
+  __device__ __forceinline__ float* res() {                                                  // [CS][NH + 4]
+    if constexpr (BF) return reinterpret_cast<float*>(u + OFF_RES);
+    else return reinterpret_cast<float*>(&fz[0][0]);
+  }
+  __device__ __forceinline__ float* dth() {                                                  // [CS][RH]
+    if constexpr (BF) return reinterpret_cast<float*>(u + OFF_DTH);
+    else return reinterpret_cast<float*>(u);
+  }
 };
 
 __device__ __forceinline__ float lane63(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
-
-// 16-byte slots j of a staged row piece: bf16 pieces are one slot, float pieces two.
-template <typename T> struct Slots;
-template <> struct Slots<bf16> {
-  static constexpr int K = 1;
-  __device__ __forceinline__ static uint4 get(const Vec8<bf16>& v, int) { return v.raw; }
-  template <int S>
-  __device__ __forceinline__ static void read(Vec8<bf16>& v, const uint4* buf, int row, int g) {
-    v.raw = staged<S>(buf, row, g);
-  }
-};
-template <> struct Slots<float> {
-  static constexpr int K = 2;
-  __device__ __forceinline__ static uint4 get(const Vec8<float>& v, int j) {
-    const float4 f = j ? v.b : v.a;
-    return make_uint4(__float_as_uint(f.x), __float_as_uint(f.y), __float_as_uint(f.z), __float_as_uint(f.w));
-  }
-  template <int S>
-  __device__ __forceinline__ static void read(Vec8<float>& v, const uint4* buf, int row, int g) {
-    v.raw_set2(staged<S>(buf, row, 2 * g), staged<S>(buf, row, 2 * g + 1));
-  }
-};
 
 template <typename T, int CS, int N, int P, int R>
 __global__ __launch_bounds__(kBwdThreads, 1)
@@ -978,11 +969,19 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       const int p = tid + k * kBwdThreads;
       if (p < CS * N / 8) {
         const int row = p / (N / 8), pc = p % (N / 8);
-#pragma unroll
-        for (int j = 0; j < Slots<T>::K; ++j) {
-          const int sl = Slots<T>::K * pc + j;
-          sm.qstage()[row * SQ + (sl ^ (row & (SQ - 1)))] = Slots<T>::get(cur.qpc[k], j);
-          sm.kstage()[row * SQ + (sl ^ (row & (SQ - 1)))] = Slots<T>::get(cur.kpc[k], j);
+        if constexpr (BF) {
+          // bf16: one 16-byte slot per piece, XOR-swizzled by row
+          sm.qstage()[row * SQ + (pc ^ (row & (SQ - 1)))] = cur.qpc[k].raw;
+          sm.kstage()[row * SQ + (pc ^ (row & (SQ - 1)))] = cur.kpc[k].raw;
+        } else {
+          // float: in place, in the row's own slots of q~ / k~ (member by member: a
+          // copy of the whole struct goes through scratch memory)
+          float4* dq = reinterpret_cast<float4*>(&sm.qt[row][8 * pc]);
+          float4* dk = reinterpret_cast<float4*>(&sm.kt[row][8 * pc]);
+          dq[0] = cur.qpc[k].a;
+          dq[1] = cur.qpc[k].b;
+          dk[0] = cur.kpc[k].a;
+          dk[1] = cur.kpc[k].b;
         }
       }
     }
@@ -1066,8 +1065,14 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
         if (tok) {
           Vec8<T> qv, kv;
-          Slots<T>::template read<SQ>(qv, sm.qstage(), lane, g);
-          Slots<T>::template read<SQ>(kv, sm.kstage(), lane, g);
+          if constexpr (BF) {
+            qv.raw = staged<SQ>(sm.qstage(), lane, g);
+            kv.raw = staged<SQ>(sm.kstage(), lane, g);
+          } else {
+            // the raw rows staged in place: this thread alone reads and then rewrites them
+            qv.load(&sm.qt[lane][8 * g]);
+            kv.load(&sm.kt[lane][8 * g]);
+          }
           qv.to_f(qh[hh]);
           kv.to_f(kh[hh]);
 #pragma unroll
@@ -1865,7 +1870,8 @@ BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R
 // (dtype, kernel chunk, d_state, headdim, rotation width) of the backward
 #define M3_BWD_SHAPES(X)                                                                    \
   X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0)                 \
-  X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 32, 16) X(float, 32, 64, 64, 16) X(float, 32, 64, 32, 16)
+  X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 32, 16) X(float, 32, 128, 64, 32) X(float, 32, 128, 64, 64)           \
+  X(float, 32, 64, 64, 16) X(float, 32, 64, 32, 16)
 
 bool scan_bwd_supported(bool bf16_io, int N, int P, int R) {
 #define X(T, cs, n, p, r) \

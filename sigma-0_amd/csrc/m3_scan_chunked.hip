@@ -744,12 +744,14 @@ hipError_t scan_chunked_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) 
 }
 
 // The state-only pass: the sequence split's first pass (bf16, d_state 128, headdim
-// 64) and the backward's chunk states (the backward's shapes).
+// 64) and the backward's chunk states (the backward's shapes; float32 at d_state 128
+// runs the float32 kernel's state-only pass).
 #define M3_STATE_SHAPES(X)                                                                  \
   X(bf16, 64, 128, 64, 32) X(bf16, 64, 128, 64, 64) X(bf16, 64, 128, 64, 0)                 \
   X(bf16, 64, 64, 64, 16) X(bf16, 64, 64, 32, 16) X(float, 32, 64, 64, 16) X(float, 32, 64, 32, 16)
 
 bool scan_state_supported(bool bf16_io, int CS_, int N, int P, int R) {
+  if (!bf16_io && scan_state_f32_supported(CS_, N, P, R)) return true;
   const int CS = kernel_chunk(bf16_io, CS_);
 #define X(T, cs, n, p, r) \
   if ((std::is_same<T, bf16>::value == bf16_io) && CS == cs && N == n && P == p && R == r) return true;
@@ -759,6 +761,7 @@ bool scan_state_supported(bool bf16_io, int CS_, int N, int P, int R) {
 }
 
 hipError_t scan_state_launch(const ScanArgs& a, bool bf16_io, hipStream_t st) {
+  if (!bf16_io && scan_state_f32_supported(a.CS, a.N, a.P, a.R)) return scan_state_f32_launch(a, st);
   const int CS = kernel_chunk(bf16_io, a.CS);
   const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
 #define X(T, cs, n, p, r)                                                                           \

@@ -674,7 +674,34 @@ bool scan_chunked_f32_supported(int CS_, int N, int P, int R) {
 }
 
 // shapes whose full pass can also write the chunk states (the backward's float32 shapes)
-#define M3_F32_SAVE_SHAPES(X) X(32, 64, 64, 16) X(32, 64, 32, 16)
+#define M3_F32_SAVE_SHAPES(X) X(32, 128, 64, 32) X(32, 128, 64, 64) X(32, 64, 64, 16) X(32, 64, 32, 16)
+
+// the state-only pass of this kernel (the backward's chunk states) at the backward's
+// float32 d_state-128 shapes
+#define M3_F32_STATE_SHAPES(X) X(32, 128, 64, 32) X(32, 128, 64, 64)
+
+bool scan_state_f32_supported(int CS_, int N, int P, int R) {
+  const int CS = f32_kernel_chunk(CS_);
+#define X(cs, n, p, r) \
+  if (CS == cs && N == n && P == p && R == r) return true;
+  M3_F32_STATE_SHAPES(X)
+#undef X
+  return false;
+}
+
+hipError_t scan_state_f32_launch(const ScanArgs& a, hipStream_t st) {
+  const int CS = f32_kernel_chunk(a.CS);
+  const int nseg = a.seg_len > 0 ? (a.L + a.seg_len - 1) / a.seg_len : 1;
+#define X(cs, n, p, r)                                                                               \
+  if (CS == cs && a.N == n && a.P == p && a.R == r) {                                                \
+    hipLaunchKernelGGL((chunked_f32::scan_chunked_f32_kernel<float, cs, n, p, r, kF32Waves, true>),  \
+                       dim3(a.B * a.H, nseg), dim3(64 * kF32Waves), 0, st, a);                       \
+    return hipGetLastError();                                                                        \
+  }
+  M3_F32_STATE_SHAPES(X)
+#undef X
+  return hipErrorInvalidValue;
+}
 
 hipError_t scan_chunked_f32_launch(const ScanArgs& a, hipStream_t st) {
   const int CS = f32_kernel_chunk(a.CS);

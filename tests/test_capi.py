@@ -127,6 +127,10 @@ def test_backward_workspace_sizes(lib, monkeypatch):
     bf, f32 = 1, 0
     assert f(8, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, bf)
     assert f(2, 300, 4, 2, 64, 32, 16, 64, f32) == _bwd_ws_expect(2, 300, 4, 2, 64, 32, 16, f32)
+    # float32 at the model's geometry (what Mamba3SSM hands its scan), both routes
+    for B, H in ((8, 32), (1, 4)):
+        for R in (32, 64):
+            assert f(B, 4096, H, H, 128, 64, R, 64, f32) == _bwd_ws_expect(B, 4096, H, H, 128, 64, R, f32)
     assert f(1, 100, 2, 2, 64, 16, 16, 64, bf) == 0        # headdim 16: no backward kernel
     assert f(1, 100, 2, 2, 128, 64, 32, 64, 7) == 0        # unknown dtype
     assert f(1, 100, 3, 2, 128, 64, 32, 64, bf) == 0       # H not a multiple of Hqk
@@ -148,10 +152,12 @@ def test_saved_state_sizes_and_validation(lib, monkeypatch):
     sb = lib.m3_chunk_scan_saved_bytes
     assert sb(8, 4096, 32, 128, 64, 32, bf) == al(8 * 32 * 64 * 64 * 128 * 2) + al(8 * 32 * 64 * 32 * 4)
     assert sb(2, 300, 4, 64, 32, 16, f32) == al(2 * 4 * 10 * 32 * 64 * 4) + al(2 * 4 * 10 * 16 * 4)
+    assert sb(8, 4096, 32, 128, 64, 32, f32) == al(8 * 32 * 128 * 64 * 128 * 4) + al(8 * 32 * 128 * 32 * 4)
     assert sb(1, 100, 2, 64, 16, 16, bf) == 0               # no backward kernel
     wsb = lib.m3_chunk_scan_bwd_saved_ws_bytes
     assert wsb(8, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, bf, True)
     assert wsb(2, 300, 4, 2, 64, 32, 16, 64, f32) == _bwd_ws_expect(2, 300, 4, 2, 64, 32, 16, f32, True)
+    assert wsb(8, 4096, 32, 32, 128, 64, 32, 64, f32) == _bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, f32, True)
     p = ctypes.c_void_p(4096)
 
     def fwd(saved=p, nbytes=1 << 40, CS=64, N=128, P=64, R=32, io=bf):
@@ -291,6 +297,14 @@ def test_bench_byte_and_flop_formulas():
     # f32 carry traffic + bf16 step inputs + f32 y (the reference returns y in f32)
     assert bench.decode_bytes(512, 32, 128, 64, 32, 2, 4) == 512 * 32 * 68492
     assert abs(bench.scan_bytes(8, 4096, 32, 128, 64, 32, 2) / 8e12 * 1e6 - 135.8) < 0.1
+    # backward: 1944 B per token-head with bf16 I/O, 3608 with float32; float32 MFMA work
+    # per 32-token chunk-head: S, dq~, dk~ intra (3 CS^2 N), dP, y, dV intra (3 CS^2 P),
+    # and five CS N P products, two FLOPs per MAC
+    assert bench.bwd_bytes(8, 4096, 32, 128, 64, 32, 2) == 8 * 4096 * 32 * 1944
+    assert bench.bwd_bytes(8, 4096, 32, 128, 64, 32, 4) == 8 * 4096 * 32 * 3608
+    CS, N, P = 32, 128, 64
+    per_chunk = 2 * (3 * CS * CS * N + 3 * CS * CS * P + 5 * CS * N * P)
+    assert bench.bwd_flops(8, 4096, 32, N, P, CS) * CS == 8 * 4096 * 32 * per_chunk
 
 
 def test_bf16_rounding_matches_torch():

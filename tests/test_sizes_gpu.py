@@ -6,9 +6,10 @@ that the float64 oracle finishes quickly).
   float64 oracle (bf16 bar 2e-2), and the split against one pass over the whole
   output.
 * The backward at configuration 2's length, L=4096 (and 5120), on two heads: every
-  gradient against autograd of the float64 oracle (bar 2e-2, tighter than the
+  gradient against autograd of the float64 oracle (bf16 bar 2e-2, tighter than the
   suite's 3e-2 for bf16 gradients: the whole-sequence cumsums behind dADT, dDT and
-  dAngles are the ones that lose precision with length).
+  dAngles are the ones that lose precision with length; float32 I/O at the model's
+  geometry, the suite's 2e-5).
 * Configuration 5, the 12-layer backbone at L=12288: batch row 0 against the oracle
   backbone's log-probabilities (a committed fixture, tests/golden/
   make_golden_config5.py: the oracle takes minutes at this size): 64 positions within
@@ -25,6 +26,7 @@ pytestmark = pytest.mark.gpu
 
 BF16_TOL = 2e-2
 GRAD_TOL = 2e-2
+F32_GRAD_TOL = 2e-5
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
@@ -54,19 +56,22 @@ def test_config3_full_size_split_matches_oracle_and_one_pass():
 
 
 @pytest.mark.timeout(300)
-@pytest.mark.parametrize("L", [4096, 5120])
-def test_backward_at_config2_length(L, bwd_route):
+@pytest.mark.parametrize("L,bf16", [(4096, True), (5120, True), (4096, False)])
+def test_backward_at_config2_length(L, bf16, bwd_route):
     import torch
     from mamba3_rocm import mamba3_siso_hip_bwd
     from oracle import mamba3_vjp as V
     B, H, N, P, R, CS = 1, 2, 128, 64, 32, 64
-    print(f"[sizes] backward {(B, L, H, N, P, R, CS)} route={bwd_route}", flush=True)
-    d = I.scan_inputs(B, L, H, N, P, R, seed=38, bf16=True)
-    cot = I.bf16_round(V.cotangent(B, L, H, P, seed=39))
+    print(f"[sizes] backward {(B, L, H, N, P, R, CS)} bf16={bf16} route={bwd_route}", flush=True)
+    d = I.scan_inputs(B, L, H, N, P, R, seed=38, bf16=bf16)
+    cot = V.cotangent(B, L, H, P, seed=39)
+    if bf16:
+        cot = I.bf16_round(cot)
+    io = torch.bfloat16 if bf16 else torch.float32
     t = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in d.items()}
     for k in ("Q", "K", "V", "Z"):
-        t[k] = t[k].to(torch.bfloat16)
-    dout = torch.from_numpy(cot).cuda().to(torch.bfloat16)
+        t[k] = t[k].to(io)
+    dout = torch.from_numpy(np.ascontiguousarray(cot)).cuda().to(io)
     got = mamba3_siso_hip_bwd(*(t[k] for k in V.NAMES), dout, chunk_size=CS)
     torch.cuda.synchronize()
     _, ref = V.vjp(d, cot, CS)
@@ -76,8 +81,9 @@ def test_backward_at_config2_length(L, bwd_route):
         assert np.isfinite(a).all(), name
         errs[name] = rel(a, b)
     print("  " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
-    bad = {k: v for k, v in errs.items() if v > GRAD_TOL}
-    assert not bad, f"gradients above {GRAD_TOL}: {bad}"
+    tol = GRAD_TOL if bf16 else F32_GRAD_TOL
+    bad = {k: v for k, v in errs.items() if v > tol}
+    assert not bad, f"gradients above {tol}: {bad}"
 
 
 def _torch_params(p):
