@@ -896,10 +896,49 @@ __device__ __forceinline__ float lane63(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// MFMA operand access of the walk.  bf16: MF16<bf16>, with transposed reads by ld_tr.
+// float: each fragment holds four k-steps of v_mfma_f32_16x16x4_f32.  In step s of a
+// 16-wide k block, the instruction's k slot i / 16 of lane i stands for k = k0 +
+// 4 (i / 16) + s, in both operands of a product (the sum over k is the same in any
+// order of its terms), so an operand stored with k contiguous is one 16-byte LDS read
+// per four MFMAs, and a transposed operand is four reads from rows 4 apart, whose
+// 4-row strides (528, 272 and 144 bytes, all 64 mod 256) put the 64 lanes on 64
+// different banks.
+template <typename T> struct WalkMma;
+template <> struct WalkMma<bf16> : MF16<bf16> {
+  __device__ __forceinline__ static frag ldt(const bf16* buf, int ld, int k0, int c0, int lane) {
+    return ld_tr(buf, ld, k0, c0, lane);
+  }
+};
+template <> struct WalkMma<float> {
+  static constexpr int KSTEP = 16;
+  typedef float4 frag;
+  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+  }
+  // rows row0 + lane%16 of a [row][k] tile, k = k0 + 4 (lane/16) + 0..3
+  __device__ __forceinline__ static frag ld(const float* buf, int ldm, int row0, int k0, int lane) {
+    return *reinterpret_cast<const float4*>(buf + (row0 + (lane & 15)) * ldm + k0 + 4 * (lane >> 4));
+  }
+  // column c0 + lane%16 of a [k][col] tile, the same k
+  __device__ __forceinline__ static frag ldt(const float* buf, int ld, int k0, int c0, int lane) {
+    const float* p = buf + (k0 + 4 * (lane >> 4)) * ld + c0 + (lane & 15);
+    return make_float4(p[0], p[ld], p[2 * ld], p[3 * ld]);
+  }
+  static constexpr int WN = 4;
+  __device__ __forceinline__ static int ktok(int k0, int lane) { return k0 + 4 * (lane >> 4); }
+  __device__ __forceinline__ static frag scale(frag v, const float w[WN]) {
+    return make_float4(v.x * w[0], v.y * w[1], v.z * w[2], v.w * w[3]);
+  }
+};
+
 template <typename T, int CS, int N, int P, int R>
 __global__ __launch_bounds__(kBwdThreads, 1)
 void scan_bwd_walk_kernel(BwdArgs a) {
-  typedef MF16<T> W;
+  typedef WalkMma<T> W;
   typedef WalkSmem<T, CS, N, P, R> S;
   typedef WalkLoads<T, CS, N, P, R> Loads;
   static_assert(sizeof(S) <= 160 * 1024, "LDS budget");
@@ -1192,7 +1231,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
 #pragma unroll
         for (int k0 = 0; k0 < CS; k0 += KS) {
-          const typename W::frag fa = ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane);
+          const typename W::frag fa = W::ldt(&sm.v[0][0], P + PAD, k0, 16 * pt, lane);
           c0 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r0, k0, lane), c0);
           c1 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r1, k0, lane), c1);
         }
@@ -1220,13 +1259,13 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
 #pragma unroll
         for (int k0 = 0; k0 < CS; k0 += KS) {
-          const typename W::frag fa = ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane);
-          c0 = W::mma(fa, ld_tr(smk, CS + PAD, k0, 16 * r0, lane), c0);
-          c1 = W::mma(fa, ld_tr(smk, CS + PAD, k0, 16 * r1, lane), c1);
+          const typename W::frag fa = W::ldt(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane);
+          c0 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r0, lane), c0);
+          c1 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r1, lane), c1);
         }
 #pragma unroll
         for (int k0 = 0; k0 < N; k0 += KS) {
-          const typename W::frag fg = ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane);
+          const typename W::frag fg = W::ldt(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane);
           d0 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r0, k0, lane), d0);
           d1 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r1, k0, lane), d1);
         }
@@ -1254,7 +1293,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         // y_t = sum_s Sm[t][s] v_s + e^{A_t} h q~_t + (D + QK_t) v_t
 #pragma unroll
         for (int k0 = 0; k0 < CS; k0 += KS)
-          acc = W::mma(ld_tr(&sm.v[0][0], P + PAD, k0, 16 * pt, lane), W::ld(smk, CS + PAD, 16 * rt, k0, lane), acc);
+          acc = W::mma(W::ldt(&sm.v[0][0], P + PAD, k0, 16 * pt, lane), W::ld(smk, CS + PAD, 16 * rt, k0, lane), acc);
 #pragma unroll
         for (int k0 = 0; k0 < N; k0 += KS)
           acc2 = W::mma(W::ld(&sm.h[0][0], N + PADN, 16 * pt, k0, lane), W::ld(&sm.qt[0][0], N + PADN, 16 * rt, k0, lane),
@@ -1270,10 +1309,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G^T k~_s + (D + QK_s) dy_s
 #pragma unroll
         for (int k0 = 0; k0 < CS; k0 += KS)
-          acc = W::mma(ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane), ld_tr(smk, CS + PAD, k0, 16 * rt, lane), acc);
+          acc = W::mma(W::ldt(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane), W::ldt(smk, CS + PAD, k0, 16 * rt, lane), acc);
 #pragma unroll
         for (int k0 = 0; k0 < N; k0 += KS)
-          acc2 = W::mma(ld_tr(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane), W::ld(&sm.kt[0][0], N + PADN, 16 * rt, k0, lane),
+          acc2 = W::mma(W::ldt(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane), W::ld(&sm.kt[0][0], N + PADN, 16 * rt, k0, lane),
                         acc2);
         float yy[4], o[4];
         load4(&sm.dy[tl][p], yy);
@@ -1310,11 +1349,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         float w[W::WN];
 #pragma unroll
         for (int j = 0; j < W::WN; ++j) w[j] = exp2_fast(sm.ac[W::ktok(k0, lane) + j] * kLog2e);
-        const typename W::frag qf = W::scale(ld_tr(&sm.qt[0][0], N + PADN, k0, 16 * ntile, lane), w);
+        const typename W::frag qf = W::scale(W::ldt(&sm.qt[0][0], N + PADN, k0, 16 * ntile, lane), w);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
           const int tile = wave + kBwdWaves * i;
-          if (tile < NTILE) acc[i] = W::mma(ld_tr(&sm.dy[0][0], P + PAD, k0, 16 * (tile / NT), lane), qf, acc[i]);
+          if (tile < NTILE) acc[i] = W::mma(W::ldt(&sm.dy[0][0], P + PAD, k0, 16 * (tile / NT), lane), qf, acc[i]);
         }
       }
 #pragma unroll
@@ -1376,20 +1415,20 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
           for (int k0 = 0; k0 < kq; k0 += KS) {
             const typename W::frag fa = W::ld(&sm.dpm[0][0], CS + PAD, 16 * rt, k0, lane);
-            acc = W::mma(fa, ld_tr(&sm.kt[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc);
-            if constexpr (BF) acc = W::mma(fa, ld_tr(lo, NH + PAD, k0, 16 * ntl, lane), acc);
+            acc = W::mma(fa, W::ldt(&sm.kt[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc);
+            if constexpr (BF) acc = W::mma(fa, W::ldt(lo, NH + PAD, k0, 16 * ntl, lane), acc);
           }
 #pragma unroll
           for (int k0 = 0; k0 < P; k0 += KS)
             acc2 = W::mma(W::ld(&sm.dy[0][0], P + PAD, 16 * rt, k0, lane),
-                          ld_tr(&sm.h[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc2);
+                          W::ldt(&sm.h[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc2);
         } else {
           // dk~_s = sum_t dPm[t][s] q~_t + e^{A_end - A_s} v_s G
 #pragma unroll
           for (int k0 = kk; k0 < CS; k0 += KS) {
-            const typename W::frag fa = ld_tr(&sm.dpm[0][0], CS + PAD, k0, 16 * rt, lane);
-            acc = W::mma(fa, ld_tr(&sm.qt[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc);
-            if constexpr (BF) acc = W::mma(fa, ld_tr(lo, NH + PAD, k0, 16 * ntl, lane), acc);
+            const typename W::frag fa = W::ldt(&sm.dpm[0][0], CS + PAD, k0, 16 * rt, lane);
+            acc = W::mma(fa, W::ldt(&sm.qt[0][0], N + PADN, k0, n0 + 16 * ntl, lane), acc);
+            if constexpr (BF) acc = W::mma(fa, W::ldt(lo, NH + PAD, k0, 16 * ntl, lane), acc);
           }
 #pragma unroll
           for (int k0 = 0; k0 < P; k0 += KS)
