@@ -9,7 +9,8 @@
 // The work is split differently from the bf16 kernel because a float32 MFMA costs
 // 16 times a bf16 one per FLOP, so the matrix work must be spread over every SIMD:
 // one workgroup of 12 waves per (batch, head) walks the chunks in order.  Output
-// waves 0-1 each own a 16-row query block of Y_diag (S^T, the causal mask, M V).
+// waves 0-2 each own one (query block, key block) item of Y_diag (an S^T block, the
+// causal mask or the decay, M V over its keys), so three of the four SIMDs share it.
 // State waves 4-7 each own 16 columns of the value dimension (a p-tile): h^T[:, p-tile]
 // (all N rows) as 16x16 accumulators, that p-tile's Y_off = Q_r h^T and its state
 // update.  Auxiliary waves 8-11 take the larger share of the preparation (the rope'd
@@ -51,7 +52,7 @@ struct Geo {
   // LDS bytes besides the Q/K staging.  The Q/K staging is double-buffered where it
   // fits; otherwise (rotation width N/2 at d_state 128) it is single-buffered and its
   // loads wait until the preparation phase has consumed it.
-  static constexpr int FIXED = 2 * CS * LDQ * TS + 2 * CS * LDY * TS + (2 * CS * SV + 2 * CS * SA) * 16 +
+  static constexpr int FIXED = 2 * CS * LDQ * TS + 2 * CS * LDY * TS + 16 * LDY * TS + (2 * CS * SV + 2 * CS * SA) * 16 +
                                2 * 3 * (CS + 4) * 4 + 8 * N + 2 * 6 * CS * 4 + 64;
   static constexpr bool DBQK = FIXED + 4 * CS * SQ * 16 <= 160 * 1024 - 512;
   static constexpr int NQK = DBQK ? 2 : 1;
@@ -92,6 +93,7 @@ struct __attribute__((aligned(16))) Smem {
   // its e^{A_cum} row scale)
   alignas(16) T yd[G::CS * G::LDY];
   alignas(16) T yo[G::CS * G::LDY];
+  alignas(16) T ydo[16 * G::LDY];        // the off-diagonal phase-3 item's part of rows 16..31
   // raw inputs staged by direct-to-LDS loads, by chunk parity: 16-byte slots, row t slot
   // s stored at t * S + (s ^ (t mod S)) so that a lane-per-row read is bank-conflict free
   alignas(16) uint4 rq[G::NQK][G::CS * G::SQ];
@@ -254,6 +256,14 @@ void scan_chunked_f32_kernel(ScanArgs a) {
       yb.to_f(ob);
 #pragma unroll
       for (int q = 0; q < 8; ++q) o[q] = fmaf(ob[q], ea, o[q]);
+      if (erow >= 16) {                    // rows 16..31: the off-diagonal phase-3 item
+        Vec8<T> yc;
+        float oc[8];
+        yc.load(&sm.ydo[(erow - 16) * G::LDY + 8 * egrp]);
+        yc.to_f(oc);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q] += oc[q];
+      }
       if (has_z) {
         float zf[8];
         zr.to_f(zf);
@@ -308,8 +318,8 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
   // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
   // the angles of its own rope pairs in registers.
-  // (wave 8 shares a SIMD with the lightest output wave)
-  constexpr int kScalarWave = G::NWY + G::NST;
+  // (full pass: the last auxiliary wave, on the one SIMD without a phase-3 item)
+  constexpr int kScalarWave = SO ? G::NWY + G::NST : G::NW - 1;
   float p_cs[G::QGW][4], p_sn[G::QGW][4];
   float logdec = 0.0f;                     // state-only pass: sum of the chunks' log-decays
   auto pre = [&](int cc) {
@@ -459,83 +469,80 @@ void scan_chunked_f32_kernel(ScanArgs a) {
     if (c + 1 < nc) stage_v(c + 1);
     if (c + 2 < nc) stage_ars(c + 2);
 
-    // ---- phase 3 for query rows l in [16 lb, 16 lb + 16), all p-tiles (output wave lb):
-    //   Y_diag = mask(K_s Q_r^T)^T V, the mask's diagonal carrying D + gamma QK.
-    // Instantiated per query block so every loop over key blocks is static.
-    auto out_block = [&](auto lb_c) {
-      constexpr int lb = decltype(lb_c)::value;
+    // ---- phase 3 as (query block lb, key block sb <= lb) items, one per output wave:
+    // three at 32-token chunks, on three SIMDs (each also holds a state wave).  An item
+    // is the 16 x 16 block S^T of keys 16 sb.. against queries 16 lb.., masked -- decayed
+    // off the diagonal block; on it causal, with D + gamma QK on the diagonal -- then
+    // M V over those 16 keys for every p-tile.  The diagonal items write their rows of
+    // Y_diag to yd, the off-diagonal one to ydo, which the gate adds.  The S^T operands
+    // are read four k-steps at a time: in step s of a 16-wide block of the d_state axis,
+    // k slot i/16 of lane i stands for column k0 + 4 (i/16) + s in both operands (the
+    // dot product is the same sum in another order), one 16-byte read per operand per
+    // four MFMAs.
+    auto diag_item = [&](auto lb_c, auto sb_c) {
+      constexpr int lb = decltype(lb_c)::value, sb = decltype(sb_c)::value;
+      static_assert(sb <= lb, "causal items only");
       // lane-derived addresses are recomputed here, not kept live across the loop
       int ln = lane;
       asm volatile("" : "+v"(ln));
       const int g4l = 4 * (ln >> 4);
       const int l = 16 * lb + (ln & 15);
       const float al = sm.ac2[pc][l];
-      const float dgl = sm.dg[pc][l];
-      constexpr int NK = N / W::KSTEP;
-      // query fragments first (B operand of every S^T block), then the key blocks'
-      // chains side by side
-      typename W::frag qf[NK];
+      const float* kr = &sm.k[(16 * sb + (ln & 15)) * G::LDQ + 4 * (ln >> 4)];
+      const float* qr = &sm.q[(16 * lb + (ln & 15)) * G::LDQ + 4 * (ln >> 4)];
+      f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) qf[kk] = W::ld(sm.q, G::LDQ, 16 * lb, kk * W::KSTEP, ln);
-      f32x4 st[lb + 2];
+      for (int k0 = 0; k0 < N; k0 += 16) {
+        const float4 ka = *reinterpret_cast<const float4*>(kr + k0);
+        const float4 qa = *reinterpret_cast<const float4*>(qr + k0);
+        st = W::mma(ka.x, qa.x, st);
+        st = W::mma(ka.y, qa.y, st);
+        st = W::mma(ka.z, qa.z, st);
+        st = W::mma(ka.w, qa.w, st);
+      }
+      const int s0 = 16 * sb + g4l;
+      if constexpr (sb < lb) {
+        // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
+        const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
+        const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
+        st[0] *= f * gg.x; st[1] *= f * gg.y; st[2] *= f * gg.z; st[3] *= f * gg.w;
+      } else {
+        // diagonal block: causal decay below the diagonal; on it, D plus the
+        // QK skip gamma_l (q_l . k_l) (the stored key carries the scale)
+        const float dgl = sm.dg[pc][l];
+        const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
+        const float asv[4] = {as.x, as.y, as.z, as.w};
 #pragma unroll
-      for (int sb = 0; sb < lb + 2; ++sb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) st[sb][r] = 0.0f;
-#pragma unroll
-      for (int kk = 0; kk < NK; ++kk)
-#pragma unroll
-        for (int sb = 0; sb <= lb; ++sb)
-          st[sb] = W::mma(W::ld(sm.k, G::LDQ, 16 * sb, kk * W::KSTEP, ln), qf[kk], st[sb]);
-#pragma unroll
-      for (int sb = 0; sb <= lb; ++sb) {
-        const int s0 = 16 * sb + g4l;
-        if (sb < lb) {
-          // off-diagonal block: e^{A_l - A_s} = e^{A_l - A_e} e^{A_e - A_s}, both <= 1
-          const float f = exp2_fast(fminf(al - sm.ac2[pc][16 * sb + 15], 0.0f));
-          const float4 gg = *reinterpret_cast<const float4*>(&sm.g16[pc][s0]);
-          st[sb][0] *= f * gg.x; st[sb][1] *= f * gg.y; st[sb][2] *= f * gg.z; st[sb][3] *= f * gg.w;
-        } else {
-          // diagonal block: causal decay below the diagonal; on it, D plus the
-          // QK skip gamma_l (q_l . k_l) (the stored key carries the scale)
-          const float4 as = *reinterpret_cast<const float4*>(&sm.ac2[pc][s0]);
-          const float asv[4] = {as.x, as.y, as.z, as.w};
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float v = st[sb][r] * exp2_fast(fminf(al - asv[r], 0.0f));
-            st[sb][r] = (s0 + r < l) ? v : (s0 + r == l ? Dh + st[sb][r] * dgl : 0.0f);
-          }
+        for (int r = 0; r < 4; ++r) {
+          const float v = st[r] * exp2_fast(fminf(al - asv[r], 0.0f));
+          st[r] = (s0 + r < l) ? v : (s0 + r == l ? Dh + st[r] * dgl : 0.0f);
         }
       }
+      // M V: the A operand is the masked block itself (lane i, reg j: query l, key
+      // 16 sb + 4 (i/16) + j), matched by V's rows
       f32x4 yd[G::PT];
 #pragma unroll
       for (int pt = 0; pt < G::PT; ++pt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) yd[pt][r] = 0.0f;
 #pragma unroll
-      for (int sp = 0; sp <= lb; sp += 2) {
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < W::STEPS; ++j) {
-          const typename W::frag mf = W::from_acc(st[sp], st[sp + 1], j);
-#pragma unroll
-          for (int pt = 0; pt < G::PT; ++pt)
-            yd[pt] = W::mma(mf, W::template vdiag<G::SV>(sv, 16 * pt, 16 * sp, j, ln), yd[pt]);
-        }
-      }
+        for (int pt = 0; pt < G::PT; ++pt)
+          yd[pt] = W::mma(st[j], W::template vdiag<G::SV>(sv, 16 * pt, 16 * sb, j, ln), yd[pt]);
+      T* dst = sb == lb ? sm.yd + 16 * lb * G::LDY : sm.ydo;
 #pragma unroll
       for (int pt = 0; pt < G::PT; ++pt)
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
-          store_pair(&sm.yd[(16 * lb + g4l + r) * G::LDY + 16 * pt + (ln & 15)],
-                     &sm.yd[(16 * lb + g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
+          store_pair(&dst[(g4l + r) * G::LDY + 16 * pt + (ln & 15)],
+                     &dst[(g4l + r + 1) * G::LDY + 16 * pt + (ln & 15)], yd[pt][r], yd[pt][r + 1]);
     };
     if (!SO && ywave) {                 // the state-only pass has no Y_diag
-      if (wave == 0) out_block(std::integral_constant<int, 0>{});
-      if (wave == 1) out_block(std::integral_constant<int, 1>{});
-      if constexpr (G::LB16 > 2) {
-        if (wave == 2) out_block(std::integral_constant<int, 2>{});
-        if (wave == 3) out_block(std::integral_constant<int, 3>{});
-      }
+      static_assert(G::LB16 == 2 && G::NWY >= 3, "three phase-3 items on three output waves");
+      if (wave == 0) diag_item(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+      if (wave == 1) diag_item(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+      if (wave == 2) diag_item(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
     } else if (swave) {
       // the state update's decay and per-token weights are read before this wave's
       // stores (a read issued after them would wait for them too)
