@@ -62,8 +62,10 @@ struct Geo {
   static_assert(QG <= 2 * NAUX + NWY + NST, "column groups per wave");
   // Q/K 8-column group k (< QGW) of a wave, or QG for none.  The first groups are the
   // rope columns, and their owner also computes their angles for the next chunk.  Full
-  // pass: the auxiliary waves take the first groups, two each, so the angle work stays
-  // off the matrix waves; the remaining groups go one per matrix wave.  State-only pass
+  // pass: the output and auxiliary waves take the first groups, one each, so the angle
+  // work stays off the state waves (the matrix phase ends with them); then the state
+  // waves (which also run the gate in the preparation) and the auxiliary waves take
+  // one each of the rest.  State-only pass
   // (no Q and no Y, so the output waves have no matrix work): the output waves and then
   // the auxiliary waves take the first groups, one each, and the state waves two each
   // of the rest, which halves the angle work per wave.
@@ -75,7 +77,9 @@ struct Geo {
       else if (wave >= NWY + NST) g = k == 0 ? NWY + (wave - NWY - NST) : QG;
       else g = NWY + NAUX + 2 * (wave - NWY) + k;
     } else {
-      g = wave >= NWY + NST ? 2 * (wave - NWY - NST) + k : 2 * NAUX + wave + (NWY + NST) * k;
+      if (wave < NWY) g = k == 0 ? wave : QG;
+      else if (wave < NWY + NST) g = k == 0 ? NWY + NAUX + (wave - NWY) : QG;
+      else g = k == 0 ? NWY + (wave - NWY - NST) : 2 * NWY + NAUX + (wave - NWY - NST);
     }
     return g < QG ? g : QG;
   }
@@ -236,9 +240,12 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   };
 
   // ---- gate (phase 7): thread -> (row, 8-column group) of a chunk's Y tile
+  // (the state waves' threads: their share of the preparation is the lightest)
   constexpr int GROUPS = CS * (P / 8);
-  const int erow = tid / (P / 8), egrp = tid % (P / 8);
-  const bool eact = tid < GROUPS;
+  static_assert(GROUPS <= 64 * G::NST, "the gate on the state waves' threads");
+  const int gtid = tid - 64 * G::NWY;
+  const int erow = max(gtid, 0) / (P / 8), egrp = max(gtid, 0) % (P / 8);
+  const bool eact = gtid >= 0 && gtid < GROUPS;
   Vec8<T> zr;                              // Z of the chunk waiting for its gate
   zr.zero();
   auto load_z = [&](int c) {
