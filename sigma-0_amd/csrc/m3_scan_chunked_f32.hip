@@ -30,6 +30,21 @@
 namespace m3 {
 namespace chunked_f32 {
 
+// Two inclusive scans over each 32-lane half of the wavefront on its own: the steps of
+// wave_incl_scan without the carry from the lower half into the upper one.
+__device__ __forceinline__ void half_incl_scan2(float v[2]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr1>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr2>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr4>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr8>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowBcast15, 0xa>(v[j]);
+}
+
 // Compile-time geometry of one instantiation.
 template <typename T, int CS_, int N_, int P_, int R_, int NW_>
 struct Geo {
@@ -305,13 +320,18 @@ void scan_chunked_f32_kernel(ScanArgs a) {
                         : 0.0f;
       }
   }
-  float carry[G::QGW][4];
+  // The Q/K column groups are worked on with two lanes per token: lane = token tkn
+  // (< CS = 32) in half hf of the wave, which takes columns 8 g + 4 hf .. + 3 of group
+  // g, i.e. its rope pairs 4 g + 2 hf + {0, 1}.
+  static_assert(CS == 32, "two lanes per token");
+  const int tkn = lane & (CS - 1), hf = lane / CS;
+  float carry[G::QGW][2];                      // angles of this lane's two pairs, revolutions
 #pragma unroll
   for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = 4 * G::template qgroup<SO>(wave, k) + j;
-      carry[k][j] = (a.init_theta && has_init && r < R) ? a.init_theta[(long)ci_in * R + r] * kInvTwoPi : 0.0f;  // revolutions
+    for (int j = 0; j < 2; ++j) {
+      const int r = 4 * G::template qgroup<SO>(wave, k) + 2 * hf + j;
+      carry[k][j] = (a.init_theta && has_init && r < R) ? a.init_theta[(long)ci_in * R + r] * kInvTwoPi : 0.0f;
     }
   // staging never holds uninitialised bits: rows past the sequence end are not loaded
   for (int i = tid; i < G::NQK * G::CS * G::SQ; i += G::NT) {
@@ -322,12 +342,12 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   for (int i = tid; i < 2 * G::CS * G::SA; i += G::NT) (&sm.ra[0][0])[i] = make_uint4(0, 0, 0, 0);
   for (int i = tid; i < 2 * 3 * (G::CS + 4); i += G::NT) (&sm.rs[0][0][0])[i] = 0.0f;
 
-  // ---- chunk constants and rotations of chunk cc, computed a chunk ahead: lane = token.
-  // Wave kScalarWave writes the per-token constants to LDS; every wave keeps cos/sin of
-  // the angles of its own rope pairs in registers.
+  // ---- chunk constants and rotations of chunk cc, computed a chunk ahead.  Wave
+  // kScalarWave writes the per-token constants to LDS (lane = token); every wave keeps
+  // cos/sin of the angles of its own rope pairs in registers (two lanes per token).
   // (full pass: the last auxiliary wave, on the one SIMD without a phase-3 item)
   constexpr int kScalarWave = SO ? G::NWY + G::NST : G::NW - 1;
-  float p_cs[G::QGW][4], p_sn[G::QGW][4];
+  float p_cs[G::QGW][2], p_sn[G::QGW][2];
   float logdec = 0.0f;                     // state-only pass: sum of the chunks' log-decays
   auto pre = [&](int cc) {
     const int t0 = cc * CS;
@@ -362,26 +382,30 @@ void scan_chunked_f32_kernel(ScanArgs a) {
     for (int k = 0; k < G::QGW; ++k) {
       const int g = G::template qgroup<SO>(wave, k);
       if (g < G::QG && 4 * g < R) {
-        const uint4 rr = staged<G::SA>(sm.ra[pb], tl, g);
-        const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
-                              __uint_as_float(rr.w)};
-        const float hdt = 0.5f * s_dt;
+        // two lanes per token (tkn, hf): this lane's pairs 4 g + 2 hf + {0, 1}
+        const bool ttok = t0 + tkn < L;
+        const float h_dt = ttok ? sm.rs[pb][1][tkn] : 0.0f;
+        const uint4 rr = staged<G::SA>(sm.ra[pb], tkn, g);
+        const float rav[2] = {__uint_as_float(hf ? rr.z : rr.x), __uint_as_float(hf ? rr.w : rr.y)};
+        const float hdt = 0.5f * h_dt;
         // angle in revolutions: carry + prefix of tanh(rate) pi dt / 2pi = tanh(rate) dt / 2,
         // with tanh(x) = 1 - 2 / (1 + e^{2x}); the fractional part is the reference's
         // mod-2pi wrap, and the hardware sin/cos take revolutions
-        float d[4];
+        float d[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          d[j] = fmaf(-s_dt, rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j])), hdt);   // s_dt = 0 past the end
-        wave_incl_scan4(d);
+        for (int j = 0; j < 2; ++j)
+          d[j] = fmaf(-h_dt, rcp_fast(1.0f + exp2_fast(2.0f * kLog2e * rav[j])), hdt);   // dt = 0 past the end
+        half_incl_scan2(d);                    // over the tokens, in each half
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 2; ++j) {
           const float th = __builtin_amdgcn_fractf(carry[k][j] + d[j]);
           // the angle entering chunk cc (revolutions), for the backward
           if constexpr (SO || SAVE) {
-            if (a.chunk_th && lane == 0) a.chunk_th[(ch0 + cc) * R + 4 * g + j] = carry[k][j];
+            if (a.chunk_th && tkn == 0) a.chunk_th[(ch0 + cc) * R + 4 * g + 2 * hf + j] = carry[k][j];
           }
-          carry[k][j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
+          const float c0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), CS - 1));
+          const float c1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(th), 2 * CS - 1));
+          carry[k][j] = hf ? c1 : c0;
           p_cs[k][j] = __builtin_amdgcn_cosf(th);
           p_sn[k][j] = __builtin_amdgcn_sinf(th);
         }
@@ -401,50 +425,31 @@ void scan_chunked_f32_kernel(ScanArgs a) {
 
   for (int c = 0; c < nc; ++c) {
     const int t0 = c * CS;
-    const bool tok = lane < CS && t0 + lane < L;
-    const int tl = lane < CS ? lane : 0;        // staging row of this lane
     const int pc = c & 1;
     const uint4* sq = sm.rq[c % G::NQK];
     const uint4* sk = sm.rk[c % G::NQK];
     const uint4* sv = sm.rv[pc];
 
-    // ================= preparation: lane = token =================
+    // ================= preparation =================
     // Rows past the sequence end hold stale (finite) inputs: their key scale is 0,
     // so they add nothing to S or h, and their outputs are never stored.
-    const float scl = sm.scl[pc][tl];
-    // Q/K column groups: rotation angles, biases, rope, key scale
+    // Q/K column groups, two lanes per token: biases, rope, key scale
+    const float hscl = sm.scl[pc][tkn];
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
       const int g = G::template qgroup<SO>(wave, k);
       if (g < G::QG) {
-        float qf[8], kf[8];
-        {
-          Vec8<T> qv, kv;
-          if constexpr (G::BF) {
-            qv.raw_set(staged<G::SQ>(sq, tl, g));
-            kv.raw_set(staged<G::SQ>(sk, tl, g));
-          } else {
-            qv.raw_set2(staged<G::SQ>(sq, tl, 2 * g), staged<G::SQ>(sq, tl, 2 * g + 1));
-            kv.raw_set2(staged<G::SQ>(sk, tl, 2 * g), staged<G::SQ>(sk, tl, 2 * g + 1));
-          }
-          qv.to_f(qf);
-          kv.to_f(kf);
-        }
-        {
-          const float4* qb4 = reinterpret_cast<const float4*>(&sm.qb[8 * g]);
-          const float4* kb4 = reinterpret_cast<const float4*>(&sm.kb[8 * g]);
-          const float4 qa = qb4[0], qc = qb4[1], ka = kb4[0], kc = kb4[1];
-          const float qbv[8] = {qa.x, qa.y, qa.z, qa.w, qc.x, qc.y, qc.z, qc.w};
-          const float kbv[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            qf[e] += qbv[e];
-            kf[e] += kbv[e];
-          }
-        }
+        const int col = 8 * g + 4 * hf;        // this lane's 4 columns
+        const uint4 qr = staged<G::SQ>(sq, tkn, 2 * g + hf), kr = staged<G::SQ>(sk, tkn, 2 * g + hf);
+        const float4 qb = *reinterpret_cast<const float4*>(&sm.qb[col]);
+        const float4 kb = *reinterpret_cast<const float4*>(&sm.kb[col]);
+        float qf[4] = {__uint_as_float(qr.x) + qb.x, __uint_as_float(qr.y) + qb.y, __uint_as_float(qr.z) + qb.z,
+                       __uint_as_float(qr.w) + qb.w};
+        float kf[4] = {__uint_as_float(kr.x) + kb.x, __uint_as_float(kr.y) + kb.y, __uint_as_float(kr.z) + kb.z,
+                       __uint_as_float(kr.w) + kb.w};
         if (4 * g < R) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < 2; ++j) {
             const float cs = p_cs[k][j], sn = p_sn[k][j];
             const float q0 = qf[2 * j], q1 = qf[2 * j + 1];
             qf[2 * j] = q0 * cs - q1 * sn;
@@ -454,13 +459,11 @@ void scan_chunked_f32_kernel(ScanArgs a) {
             kf[2 * j + 1] = k0 * sn + k1 * cs;
           }
         }
-        if (tok && t0 + lane == L - 1) store8(&sm.fink[8 * g], kf);   // the final carry's key, written after the loop
+        if (t0 + tkn == L - 1) store4(&sm.fink[col], kf);   // the final carry's key, written after the loop
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] *= scl;
-        if (lane < CS) {
-          if constexpr (!SO) store8(&sm.q[lane * G::LDQ + 8 * g], qf);
-          store8(&sm.k[lane * G::LDQ + 8 * g], kf);
-        }
+        for (int e = 0; e < 4; ++e) kf[e] *= hscl;
+        if constexpr (!SO) store4(&sm.q[tkn * G::LDQ + col], qf);
+        store4(&sm.k[tkn * G::LDQ + col], kf);
       }
     }
     // gate of the previous chunk (its Y tiles were written before the last barrier),
@@ -652,12 +655,12 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   if constexpr (SO) {
     if (a.fin_logdec && fin_here && wave == kScalarWave && lane == 0) a.fin_logdec[ci_out] = logdec;
   }
-  if (a.fin_theta && fin_here && lane == 0) {
+  if (a.fin_theta && fin_here && tkn == 0) {
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * G::template qgroup<SO>(wave, k) + j;
+      for (int j = 0; j < 2; ++j) {
+        const int r = 4 * G::template qgroup<SO>(wave, k) + 2 * hf + j;
         if (r < R) a.fin_theta[(long)ci_out * R + r] = carry[k][j] * kTwoPi;
       }
   }
