@@ -74,6 +74,61 @@ __device__ __forceinline__ void rot8(float x[8], const float cs[4], const float 
   }
 }
 
+// rot8 for a lane that holds PRS of the group's four pairs (2 PRS columns); rope: the
+// group's pairs are rope pairs (R is a multiple of 4, so all four or none are).
+template <int PRS>
+__device__ __forceinline__ void rotp(float* x, const float* cs, const float* sn, bool rope, float sgn) {
+  if (!rope) return;
+#pragma unroll
+  for (int j = 0; j < PRS; ++j) {
+    const float c = cs[j], s = sgn * sn[j];
+    const float x0 = x[2 * j], x1 = x[2 * j + 1];
+    x[2 * j] = x0 * c - x1 * s;
+    x[2 * j + 1] = x0 * s + x1 * c;
+  }
+}
+
+// Inclusive scans over the tokens of a chunk: over the 64 lanes (4 values: one lane
+// per token) or over each 32-lane half (2 values: two lanes per token, the halves
+// holding the same tokens and different pairs).
+template <int PRS>
+__device__ __forceinline__ void token_scan(float* v) {
+  if constexpr (PRS == 4) {
+    wave_incl_scan4(v);
+  } else {
+    static_assert(PRS == 2, "one or two lanes per token");
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr1>(v[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr2>(v[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr4>(v[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowShr8>(v[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[j] += dpp0<kDppRowBcast15, 0xa>(v[j]);
+  }
+}
+
+// The total of a token scan: the value in the last lane of the lane's token range.
+template <int PRS>
+__device__ __forceinline__ float token_scan_total(float v, int hf) {
+  if constexpr (PRS == 4) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  } else {
+    const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return hf ? t1 : t0;
+  }
+}
+
+// Sum of a token's value over its TPL lanes (lanes l and l + 32 at two lanes per token).
+template <int TPL>
+__device__ __forceinline__ float token_pair_sum(float v) {
+  if constexpr (TPL == 1) return v;
+  else return v + __shfl_xor(v, 32, 64);
+}
+
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
 // Reverse inclusive scan over the 64 lanes (lane i gets the sum over lanes >= i).
@@ -777,7 +832,8 @@ struct WalkLoads {
         for (int j = 0; j < HK; ++j) hpc[k][j] = src[j];
       }
       const long srow = (long)bh * L;
-      const int tcl = min(t0 + lane, L - 1), tn = min(t0 + CS, L - 1);
+      // lane & (CS - 1): the token of a lane (two lanes per token at 32-token chunks)
+      const int tcl = min(t0 + (lane & (CS - 1)), L - 1), tn = min(t0 + CS, L - 1);
       adt = a.s.adt[srow + tcl];
       dt = a.s.dt[srow + tcl];
       trap = a.s.trap[srow + tcl];
@@ -803,7 +859,7 @@ struct WalkLoads {
         zpc[k].load(gz + row);
       }
     } else {
-      const int tcl = min(t0 + lane, L - 1);
+      const int tcl = min(t0 + (lane & (CS - 1)), L - 1);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         rates[hh] = th0[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -950,6 +1006,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   static_assert(kBwdWaves % NT == 0, "the adjoint tiles of a wave share one column tile");
   constexpr bool BF = S::BF;
   constexpr int HP = Loads::HP;
+  // lanes per token (two at 32-token chunks: lanes l and l + 32), and per lane the
+  // columns of an 8-column group and its rope pairs
+  constexpr int TPL = 64 / CS, EL = 8 / TPL, PRS = 4 / TPL;
+  static_assert(CS * TPL == 64, "64- or 32-token chunks");
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __builtin_assume(wave >= 0 && wave < kBwdWaves);
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
@@ -970,11 +1030,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   constexpr int TPG = CS * NH / kBwdThreads;           // tokens per group
   static_assert(TPG >= 1 && CS * NH % kBwdThreads == 0, "bias column sums: whole token groups");
   float bacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float cth[2][4];                                     // d(theta) over the later chunks, per pair
+  float cth[2][PRS];                                   // d(theta) over the later chunks, per pair
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cth[hh][j] = 0.0f;
+    for (int j = 0; j < PRS; ++j) cth[hh][j] = 0.0f;
   float cda = 0.0f, dsum = 0.0f;                       // wave 0: dA over the later chunks; dD
 
   // One register set of loads: chunk c's inputs are consumed by the end of its
@@ -996,9 +1056,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
+    const int tkn = lane & (CS - 1), hf = lane / CS;  // token of the lane and its half (two lanes per token)
     const int t0 = c * CS;
     const int nt = min(CS, L - t0);                   // tokens of this chunk
-    const bool tok = lane < nt;
+    const bool tok = tkn < nt;
     const float dtl = tok ? cur.dt : 0.0f;
 
     // ---- top: Q/K row pieces into the staging tiles, G_c and the saved state h_c
@@ -1073,70 +1134,87 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     }
     __syncthreads();   // staging, token constants, G_c, h_c
 
-    // ---- preparation.  Q/K, lane = token: this thread's two column groups (one per
+    // ---- preparation.  Q/K, lane = token (two lanes per token at 32-token chunks,
+    // each with EL of the group's 8 columns): this thread's two column groups (one per
     // half of the state columns): q^ = q + qb, k^ = k + kb and the rope cos/sin of
     // their pairs stay in registers for every phase below; q~ and k~ go to LDS.
-    float qh[2][8], kh[2][8], cs[2][4], sn[2][4];
+    float qh[2][EL], kh[2][EL], cs[2][PRS], sn[2][PRS];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int g = hh * GH + wave;
+      const int col = 8 * g + EL * hf;          // this lane's first column of the group
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qh[hh][e] = kh[hh][e] = 0.0f;
+      for (int e = 0; e < EL; ++e) qh[hh][e] = kh[hh][e] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) cs[hh][j] = 1.0f, sn[hh][j] = 0.0f;
+      for (int j = 0; j < PRS; ++j) cs[hh][j] = 1.0f, sn[hh][j] = 0.0f;
       if (qkw) {
-        float th4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float thp[PRS];
+#pragma unroll
+        for (int j = 0; j < PRS; ++j) thp[j] = 0.0f;
         if constexpr (R > 0) {
           if (4 * g < R) {
-            const float rv[4] = {cur.rates[hh].x, cur.rates[hh].y, cur.rates[hh].z, cur.rates[hh].w};
-            const float tv[4] = {cur.th0[hh].x, cur.th0[hh].y, cur.th0[hh].z, cur.th0[hh].w};
+            // the rates and entering angles of this lane's pairs (a select per component:
+            // an index by hf would put the arrays in scratch memory)
+            const float4 rq = cur.rates[hh], tq = cur.th0[hh];
+            float rv[PRS], tv[PRS];
+            if constexpr (PRS == 4) {
+              rv[0] = rq.x; rv[1] = rq.y; rv[2] = rq.z; rv[3] = rq.w;
+              tv[0] = tq.x; tv[1] = tq.y; tv[2] = tq.z; tv[3] = tq.w;
+            } else {
+              rv[0] = hf ? rq.z : rq.x; rv[1] = hf ? rq.w : rq.y;
+              tv[0] = hf ? tq.z : tq.x; tv[1] = hf ? tq.w : tq.y;
+            }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) th4[j] = angle_step(rv[j], dtl);
-            wave_incl_scan4(th4);
+            for (int j = 0; j < PRS; ++j) thp[j] = angle_step(rv[j], dtl);
+            token_scan<PRS>(thp);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) th4[j] = __builtin_amdgcn_fractf(tv[j] + th4[j]);
+            for (int j = 0; j < PRS; ++j) thp[j] = __builtin_amdgcn_fractf(tv[j] + thp[j]);
           }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          cs[hh][j] = __builtin_amdgcn_cosf(th4[j]);
-          sn[hh][j] = __builtin_amdgcn_sinf(th4[j]);
+        for (int j = 0; j < PRS; ++j) {
+          cs[hh][j] = __builtin_amdgcn_cosf(thp[j]);
+          sn[hh][j] = __builtin_amdgcn_sinf(thp[j]);
         }
         if (tok) {
-          Vec8<T> qv, kv;
           if constexpr (BF) {
+            Vec8<T> qv, kv;
             qv.raw = staged<SQ>(sm.qstage(), lane, g);
             kv.raw = staged<SQ>(sm.kstage(), lane, g);
+            qv.to_f(qh[hh]);
+            kv.to_f(kh[hh]);
           } else {
             // the raw rows staged in place: this thread alone reads and then rewrites them
-            qv.load(&sm.qt[lane][8 * g]);
-            kv.load(&sm.kt[lane][8 * g]);
+            load4(&sm.qt[tkn][col], qh[hh]);
+            load4(&sm.kt[tkn][col], kh[hh]);
           }
-          qv.to_f(qh[hh]);
-          kv.to_f(kh[hh]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            qh[hh][e] += sm.qb[8 * g + e];
-            kh[hh][e] += sm.kb[8 * g + e];
+          for (int e = 0; e < EL; ++e) {
+            qh[hh][e] += sm.qb[col + e];
+            kh[hh][e] += sm.kb[col + e];
           }
         }
-        float q[8], k[8], dot = 0.0f;
-        const float sc = tok ? sm.scl[lane] : 0.0f;
+        float q[EL], k[EL], dot = 0.0f;
+        const float sc = tok ? sm.scl[tkn] : 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int e = 0; e < EL; ++e) {
           q[e] = qh[hh][e];
           k[e] = kh[hh][e];
           dot += q[e] * k[e];
         }
-        rot8<R>(q, cs[hh], sn[hh], g, 1.0f);
-        rot8<R>(k, cs[hh], sn[hh], g, 1.0f);
+        rotp<PRS>(q, cs[hh], sn[hh], 4 * g < R, 1.0f);
+        rotp<PRS>(k, cs[hh], sn[hh], 4 * g < R, 1.0f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) k[e] *= sc;
-        if (lane < CS) {
-          store8(&sm.qt[lane][8 * g], q);
-          store8(&sm.kt[lane][8 * g], k);
-          sm.pq[g][lane] = dot;
+        for (int e = 0; e < EL; ++e) k[e] *= sc;
+        dot = token_pair_sum<TPL>(dot);
+        if constexpr (BF) {
+          store8(&sm.qt[tkn][col], q);
+          store8(&sm.kt[tkn][col], k);
+        } else {
+          store4(&sm.qt[tkn][col], q);
+          store4(&sm.kt[tkn][col], k);
         }
+        if (hf == 0) sm.pq[g][tkn] = dot;
       }
     }
     // V, dOut, Z in row layout: dy = dOut silu(z), the dZ factor, and dy . v per token
@@ -1362,20 +1440,24 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     if (c > 0) cur.template issue<2>(a, c - 1, bh, tid, wave, lane);
 
     // ---- dq~ then dk~, half the columns at a time, each followed by its chain rule
-    float dthq[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};   // d(theta) from dq~, for pass K
+    float dthq[2][PRS];                               // d(theta) from dq~, for pass K
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int j = 0; j < PRS; ++j) dthq[hh][j] = 0.0f;
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
       const bool isq = pass < 2;
       const int n0 = (pass & 1) * NH;
       const int hh = pass & 1;
-      float gq8[8], gk8[8], gcs[4], gsn[4];
+      float gq8[EL], gk8[EL], gcs[PRS], gsn[PRS];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < EL; ++e) {
         gq8[e] = hh ? qh[1][e] : qh[0][e];
         gk8[e] = hh ? kh[1][e] : kh[0][e];
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < PRS; ++j) {
         gcs[j] = hh ? cs[1][j] : cs[0][j];
         gsn[j] = hh ? sn[1][j] : sn[0][j];
       }
@@ -1386,7 +1468,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           float x[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) x[e] = isq ? gk8[e] : gq8[e];
-          rot8<R>(x, gcs, gsn, g, 1.0f);
+          rotp<PRS>(x, gcs, gsn, 4 * g < R, 1.0f);
           const float sc = isq && tok ? sm.scl[lane] : 1.0f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -1444,63 +1526,70 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
       }
       __syncthreads();
-      // chain rule, lane = token, one 8-column group per wave
+      // chain rule, lane = token (two lanes per token at 32-token chunks, EL columns
+      // each), one 8-column group per wave
       const int g = n0 / 8 + wave;
       if (qkw) {
-        float dx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, out[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        float dot = 0.0f, dsc = 0.0f, dthv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int rc = tkn * (NH + 4) + 8 * wave + EL * hf;   // this lane's slots of res
+        float dx[EL], out[EL], dthv[PRS];
+#pragma unroll
+        for (int e = 0; e < EL; ++e) dx[e] = out[e] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PRS; ++j) dthv[j] = 0.0f;
+        float dot = 0.0f, dsc = 0.0f;
         if (tok) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dx[e] = res[lane * (NH + 4) + 8 * wave + e];
-          const float sc = sm.scl[lane], gqk = sm.dqk[lane] * sm.gam[lane];
-          float xr[8];                                    // q~ (pass Q) or rot(k^) (pass K)
+          for (int e = 0; e < EL; ++e) dx[e] = res[rc + e];
+          const float sc = sm.scl[tkn], gqk = sm.dqk[tkn] * sm.gam[tkn];
+          float xr[EL];                                   // q~ (pass Q) or rot(k^) (pass K)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xr[e] = isq ? gq8[e] : gk8[e];
-          rot8<R>(xr, gcs, gsn, g, 1.0f);
+          for (int e = 0; e < EL; ++e) xr[e] = isq ? gq8[e] : gk8[e];
+          rotp<PRS>(xr, gcs, gsn, 4 * g < R, 1.0f);
           const float f = isq ? 1.0f : sc;                // k~ = scale rot(k^)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
+          for (int e = 0; e < EL; ++e) {
             dot += f * xr[e] * dx[e];
             dsc += xr[e] * dx[e];
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) dthv[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
+          for (int j = 0; j < PRS; ++j) dthv[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
           // d(q^) = rot^T dq~ + dQK gamma k^;  d(k^) = scale rot^T dk~ + dQK gamma q^
 #pragma unroll
-          for (int e = 0; e < 8; ++e) out[e] = f * dx[e];
-          rot8<R>(out, gcs, gsn, g, -1.0f);
+          for (int e = 0; e < EL; ++e) out[e] = f * dx[e];
+          rotp<PRS>(out, gcs, gsn, 4 * g < R, -1.0f);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) out[e] += gqk * (isq ? gk8[e] : gq8[e]);
+          for (int e = 0; e < EL; ++e) out[e] += gqk * (isq ? gk8[e] : gq8[e]);
         }
+        dot = token_pair_sum<TPL>(dot);
+        dsc = token_pair_sum<TPL>(dsc);
         // d(q^) / d(k^) back into the thread's own slots of res, for the row stores and
         // the bias column sums
-        if (lane < CS) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) res[lane * (NH + 4) + 8 * wave + e] = out[e];
-        }
+        for (int e = 0; e < EL; ++e) res[rc + e] = out[e];
         if (isq) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) dthq[hh][j] = dthv[j];
+          for (int j = 0; j < PRS; ++j) dthq[hh][j] = dthv[j];
         } else if (4 * g < R) {
           // the token's d(theta) of each pair; its reverse cumsum over the sequence is
           // the chunk's suffix sum plus the later chunks' total (0 on padding tokens)
-          float sv[4], d[4], f[4];
+          float sv[PRS], d[PRS], f[PRS];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) f[j] = d[j] = dthq[hh][j] + dthv[j];
-          wave_incl_scan4(f);
+          for (int j = 0; j < PRS; ++j) f[j] = d[j] = dthq[hh][j] + dthv[j];
+          token_scan<PRS>(f);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float tot = lane63(f[j]);
+          for (int j = 0; j < PRS; ++j) {
+            const float tot = token_scan_total<PRS>(f[j], hf);
             sv[j] = cth[hh][j] + tot - f[j] + d[j];
             cth[hh][j] += tot;
           }
-          if (lane < CS) store4(dth + lane * RH + 4 * wave, sv);
+          if constexpr (PRS == 4) store4(dth + tkn * RH + 4 * wave, sv);
+          else *reinterpret_cast<float2*>(dth + tkn * RH + 4 * wave + 2 * hf) = make_float2(sv[0], sv[1]);
         }
-        if (lane < CS) {
-          if (isq) sm.pq[g][lane] = dot;   // the same thread subtracts k~.dk~ in pass K
+        if (hf == 0) {
+          if (isq) sm.pq[g][tkn] = dot;   // the same thread subtracts k~.dk~ in pass K
           else {
-            sm.pq[g][lane] -= dot;
-            sm.ps[g][lane] = dsc;
+            sm.pq[g][tkn] -= dot;
+            sm.ps[g][tkn] = dsc;
           }
         }
       }
@@ -1546,8 +1635,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     // ---- per token: dA (its reverse cumsum into dADT), d(gamma) into dDT, d(scale)
     // into the workspace
     if (wave == 0) {
+      // lane = token here (lanes CS.. hold no token)
+      const bool ltok = lane < nt;
       float da = 0.0f, ds = 0.0f;
-      if (tok) {
+      if (ltok) {
         for (int g = 0; g < N / 8; ++g) {
           da += sm.pq[g][lane];
           ds += sm.ps[g][lane];
@@ -1558,7 +1649,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       }
       const float f = wave_incl_scan(da);
       const float tot = lane63(f);
-      if (tok) a.dadt[(long)bh * L + t0 + lane] = cda + tot - f + da;
+      if (ltok) a.dadt[(long)bh * L + t0 + lane] = cda + tot - f + da;
       cda += tot;
     }
     // the next chunk's staging overlaps res and the d(theta) tile read above
@@ -1582,12 +1673,13 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       }
     }
     if (qkw) {
+      const int tkn = lane & (CS - 1), hf = lane / CS;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 4 * (hh * GH + wave) + j;
-          if (r < R && lane == 0) a.ctot[(long)bh * (R + 1) + 1 + r] = cth[hh][j];
+        for (int j = 0; j < PRS; ++j) {
+          const int r = 4 * (hh * GH + wave) + PRS * hf + j;
+          if (r < R && tkn == 0) a.ctot[(long)bh * (R + 1) + 1 + r] = cth[hh][j];
         }
     }
     if (wave == 0) {
