@@ -311,7 +311,10 @@ void scan_chunked_kernel(ScanArgs a) {
   constexpr int kScalarWave = G::NWY + G::NST;
   float p_cs[G::QGW][4], p_sn[G::QGW][4];
   float logdec = 0.0f;                     // state-only pass: sum of the chunks' log-decays
-  auto pre = [&](int cc) {
+  // rope_c: whether the calling role's waves can own rope groups (a compile-time flag,
+  // so that the loops of the other roles keep no angle registers live)
+  auto pre = [&](int cc, auto rope_c) {
+    constexpr bool RP = decltype(rope_c)::value;
     const int t0 = cc * CS;
     const int pb = cc & 1;
     const bool tok = lane < CS && t0 + lane < L;
@@ -343,7 +346,7 @@ void scan_chunked_kernel(ScanArgs a) {
 #pragma unroll
     for (int k = 0; k < G::QGW; ++k) {
       const int g = G::template qgroup<SO>(wave, k);
-      if (g < G::QG && 4 * g < R) {
+      if (RP && g < G::QG && 4 * g < R) {
         const uint4 rr = staged<G::SA>(sm.ra[pb], tl, g);
         const float rav[4] = {__uint_as_float(rr.x), __uint_as_float(rr.y), __uint_as_float(rr.z),
                               __uint_as_float(rr.w)};
@@ -378,14 +381,15 @@ void scan_chunked_kernel(ScanArgs a) {
   if (nc > 1) stage_ars(1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  pre(0);
+  pre(0, std::true_type{});
   __syncthreads();   // chunk 0's per-token constants (one wave writes them) before its preparation
 
   // ================= preparation, lane = token: this wave's Q/K column groups =========
   // (biases and rope into the Q/K tiles).  Rows past the sequence end hold stale
   // (finite) inputs: their key scale is 0, so they add nothing to S or h, and their
   // outputs are never stored.
-  auto prep_groups = [&](int c) {
+  auto prep_groups = [&](int c, auto rope_c) {
+    constexpr bool RP = decltype(rope_c)::value;
     const int t0 = c * CS;
     const bool tok = lane < CS && t0 + lane < L;
     const int tl = lane < CS ? lane : 0;        // staging row of this lane
@@ -420,7 +424,7 @@ void scan_chunked_kernel(ScanArgs a) {
             kf[e] += kbv[e];
           }
         }
-        if (4 * g < R) {
+        if (RP && 4 * g < R) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const float cs = p_cs[k][j], sn = p_sn[k][j];
@@ -559,8 +563,9 @@ void scan_chunked_kernel(ScanArgs a) {
 
   // final carry, the parts held in registers: this wave's rope angles (and, for the
   // state-only pass's scalar wave, the total log-decay)
-  auto fin_regs = [&]() {
-    if (a.fin_theta && fin_here && lane == 0) {
+  auto fin_regs = [&](auto rope_c) {
+    constexpr bool RP = decltype(rope_c)::value;
+    if (RP && a.fin_theta && fin_here && lane == 0) {
 #pragma unroll
       for (int k = 0; k < G::QGW; ++k)
 #pragma unroll
@@ -576,10 +581,13 @@ void scan_chunked_kernel(ScanArgs a) {
 
   // ---- the chunk loop, one per role: the roles share no loop-carried registers
   // (the state accumulators live only in the state waves' loop), and every loop passes
-  // the same two barriers per chunk.
+  // the same two barriers per chunk.  In the full pass the auxiliary waves own the
+  // first 2 NAUX groups, so at rope widths up to 8 NAUX (the model's N/4 included) the
+  // output and state waves own no rope group.
+  const std::integral_constant<bool, SO || (R > 8 * G::NAUX)> rys{};
   if (ywave) {
     for (int c = 0; c < nc; ++c) {
-      prep_groups(c);
+      prep_groups(c, rys);
       // Z for this chunk's gate, then the loads of the next chunk's Q/K
       if (!SO) load_z(c);
       if (G::DBQK && c + 1 < nc) stage_qk(c + 1);
@@ -592,17 +600,17 @@ void scan_chunked_kernel(ScanArgs a) {
           if (wave == 3) out_block(std::integral_constant<int, 3>{}, c);
         }
       }
-      if (c + 1 < nc) pre(c + 1);
+      if (c + 1 < nc) pre(c + 1, rys);
       // staged loads have landed before the barrier (a wave with a query block waited
       // before its gate, so that the gate's stores are not waited for)
       if (SO || 16 * wave >= CS) __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
-    fin_regs();
+    fin_regs(rys);
   } else if (swave) {
     for (int c = 0; c < nc; ++c) {
       const int pc = c & 1;
-      prep_groups(c);
+      prep_groups(c, rys);
       // the state entering this chunk, h[p][n] in the io type, for the output waves'
       // Y_off (the state waves of a p-tile hold it alike; the first writes it)
       if (!SO && part == 0) {
@@ -648,11 +656,11 @@ void scan_chunked_kernel(ScanArgs a) {
             hs[nb] = W::mma(W::kstate(sm.k, G::LDQ, ks * W::KSTEP, 16 * nb, ln), vb, hs[nb]);
         }
       }
-      if (c + 1 < nc) pre(c + 1);
+      if (c + 1 < nc) pre(c + 1, rys);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
-    fin_regs();
+    fin_regs(rys);
     if (a.fin_h && fin_here && part == 0) {
 #pragma unroll
       for (int nb = 0; nb < G::NB16; ++nb)
@@ -661,15 +669,15 @@ void scan_chunked_kernel(ScanArgs a) {
     }
   } else {
     for (int c = 0; c < nc; ++c) {
-      prep_groups(c);
+      prep_groups(c, std::true_type{});
       __syncthreads();
       // single-buffered Q/K staging: every wave has read this chunk's rows
       if (!G::DBQK && c + 1 < nc) stage_qk(c + 1);
-      if (c + 1 < nc) pre(c + 1);
+      if (c + 1 < nc) pre(c + 1, std::true_type{});
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
-    fin_regs();
+    fin_regs(std::true_type{});
   }
 
   // final carry: k of the last token (kept in LDS by its preparation) and its v (still
