@@ -202,7 +202,10 @@ void scan_chunked_kernel(ScanArgs a) {
   // waves at the start of the matrix phase.  Every issuing wave waits for its loads
   // before the chunk's closing barrier (the output waves before their gate).
   constexpr int kWQ0 = G::DBQK ? 0 : 8, kWQ1 = G::DBQK ? 1 : 9, kWK0 = G::DBQK ? 2 : 10, kWK1 = G::DBQK ? 3 : 11;
-  constexpr int kWV = 6, kWA = 7;
+  // V and the rates: state waves 6 and 7 in the full pass (the output waves carry the
+  // chunk's longest work there), output waves 0 and 1 in the state-only pass (idle
+  // after the preparation, while the state waves' update ends the chunk)
+  constexpr int kWV = SO ? 0 : 6, kWA = SO ? 1 : 7;
   auto stage_qk = [&](int c) {
     const int t0 = c * CS;
     const int valid = L - t0;
@@ -592,6 +595,10 @@ void scan_chunked_kernel(ScanArgs a) {
       if (!SO) load_z(c);
       if (G::DBQK && c + 1 < nc) stage_qk(c + 1);
       __syncthreads();
+      if constexpr (SO) {
+        if (c + 1 < nc) stage_v(c + 1);
+        if (c + 2 < nc) stage_ars(c + 2);
+      }
       if constexpr (!SO) {
         if (wave == 0) out_block(std::integral_constant<int, 0>{}, c);
         if (wave == 1) out_block(std::integral_constant<int, 1>{}, c);
@@ -621,8 +628,10 @@ void scan_chunked_kernel(ScanArgs a) {
         }
       }
       __syncthreads();
-      if (c + 1 < nc) stage_v(c + 1);
-      if (c + 2 < nc) stage_ars(c + 2);
+      if constexpr (!SO) {
+        if (c + 1 < nc) stage_v(c + 1);
+        if (c + 2 < nc) stage_ars(c + 2);
+      }
       {
         // lane-derived addresses are recomputed here, not kept live across the loop
         int ln = lane;
