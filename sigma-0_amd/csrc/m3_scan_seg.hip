@@ -116,20 +116,32 @@ void seg_combine_kernel(ScanArgs a, int nseg, Carries loc, Carries in) {
     h += (1.0f - 1.0f / (1.0f + expf(-tr0))) * dt0 * a.init_v[(long)bh * P + p] * a.init_k[(long)bh * N + n];
   }
   float th = rope && a.init_theta ? a.init_theta[(long)bh * R + r] : 0.0f;
-  for (int i = 0; i + 1 < nseg; ++i) {
+  // a segment's values (the element's rope pair of its exit state, its angle advance
+  // and log-decay) are loaded one step ahead of their use, so that the loads overlap
+  // the previous step's arithmetic instead of each step waiting for its own
+  auto load_seg = [&](int i, float2& hp, float& dth, float& ld) {
     const long ci = c0 + i;
-    const float* lh = loc.h + ci * P * N;
-    float own = lh[e];
+    hp = *reinterpret_cast<const float2*>(loc.h + ci * P * N + p * N + 2 * r);
+    dth = rope ? loc.th[ci * R + r] : 0.0f;
+    ld = loc.ld[ci];
+  };
+  float2 nhp = make_float2(0.0f, 0.0f);
+  float ndth = 0.0f, nld = 0.0f;
+  if (nseg > 1) load_seg(0, nhp, ndth, nld);
+  for (int i = 0; i + 1 < nseg; ++i) {
+    const float2 hp = nhp;
+    const float dth = ndth, ld = nld;
+    if (i + 2 < nseg) load_seg(i + 1, nhp, ndth, nld);
+    float own = (n & 1) ? hp.y : hp.x;
     if (rope) {                          // segment-local key frame -> entering frame
       float sn, cs;
       sincosf(th, &sn, &cs);
-      const float h0 = lh[p * N + 2 * r], h1 = lh[p * N + 2 * r + 1];
-      own = (n & 1) ? h0 * sn + h1 * cs : h0 * cs - h1 * sn;
-      const float x = th + loc.th[ci * R + r];
+      own = (n & 1) ? hp.x * sn + hp.y * cs : hp.x * cs - hp.y * sn;
+      const float x = th + dth;
       th = x - kTwoPi * floorf(x * kInvTwoPi);
     }
-    h = expf(loc.ld[ci]) * h + own;
-    in.h[(ci + 1) * P * N + e] = h;
+    h = expf(ld) * h + own;
+    in.h[(c0 + i + 1) * P * N + e] = h;
   }
 }
 
