@@ -1035,7 +1035,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
     for (int j = 0; j < PRS; ++j) cth[hh][j] = 0.0f;
-  float cda = 0.0f, dsum = 0.0f;                       // wave 0: dA over the later chunks; dD
+  // The per-token dA of a chunk (sums over the column groups, reverse cumsum) runs on
+  // the last wave: wave 0 computes the next chunk's token constants at the top of the
+  // next chunk, and the other waves wait for both at its first barrier.
+  constexpr int kDaWave = kBwdWaves - 1;
+  float cda = 0.0f, dsum = 0.0f;                       // wave kDaWave: dA over the later chunks; wave 0: dD
 
   // One register set of loads: chunk c's inputs are consumed by the end of its
   // preparation, and chunk c - 1's are requested in parts during the rest of chunk c.
@@ -1299,65 +1303,78 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     // range), so each wave's tiles are fixed iterations without branches.
     const float aend = sm.aend;
     static_assert(2 * TB * (P / 16) % kBwdWaves == 0, "y/dV tiles: whole rounds");
-    if constexpr (TB * (P / 16) == 2 * kBwdWaves) {
-      // two tiles of one value-column block per wave and product: the A fragments (v or
-      // dy columns, h rows or G columns of the block) are read once for both
-      const int pt = wave % (P / 16), r0 = wave / (P / 16), r1 = r0 + kBwdWaves / (P / 16);
+    // two tiles of one value-column block pt (row blocks r0, r1) of y or dV: the A
+    // fragments (v or dy columns, h rows or G columns of the block) are read once for both
+    auto ypair = [&](int pt, int r0, int r1) {
       const int p = 16 * pt + 4 * (lane >> 4);
-      if (gz && a.dz) {
-        // y_t = sum_s Sm[t][s] v_s + e^{A_t} h q~_t + (D + QK_t) v_t
-        f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
+      // y_t = sum_s Sm[t][s] v_s + e^{A_t} h q~_t + (D + QK_t) v_t
+      f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
 #pragma unroll
-        for (int k0 = 0; k0 < CS; k0 += KS) {
-          const typename W::frag fa = W::ldt(&sm.v[0][0], P + PAD, k0, 16 * pt, lane);
-          c0 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r0, k0, lane), c0);
-          c1 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r1, k0, lane), c1);
-        }
-#pragma unroll
-        for (int k0 = 0; k0 < N; k0 += KS) {
-          const typename W::frag fh = W::ld(&sm.h[0][0], N + PADN, 16 * pt, k0, lane);
-          d0 = W::mma(fh, W::ld(&sm.qt[0][0], N + PADN, 16 * r0, k0, lane), d0);
-          d1 = W::mma(fh, W::ld(&sm.qt[0][0], N + PADN, 16 * r1, k0, lane), d1);
-        }
-#pragma unroll
-        for (int u2 = 0; u2 < 2; ++u2) {
-          const int tl = 16 * (u2 ? r1 : r0) + (lane & 15);
-          const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
-          float vv[4], ff[4], o[4];
-          load4(&sm.v[tl][p], vv);
-          load4(&sm.fz[tl][p], ff);
-          const float ea = exp2_fast(sm.ac[tl] * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
-          store4(sm.outs(0) + tl * (P + PAD) + p, o);
-        }
+      for (int k0 = 0; k0 < CS; k0 += KS) {
+        const typename W::frag fa = W::ldt(&sm.v[0][0], P + PAD, k0, 16 * pt, lane);
+        c0 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r0, k0, lane), c0);
+        c1 = W::mma(fa, W::ld(smk, CS + PAD, 16 * r1, k0, lane), c1);
       }
-      {
-        // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G^T k~_s + (D + QK_s) dy_s
-        f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
 #pragma unroll
-        for (int k0 = 0; k0 < CS; k0 += KS) {
-          const typename W::frag fa = W::ldt(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane);
-          c0 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r0, lane), c0);
-          c1 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r1, lane), c1);
-        }
+      for (int k0 = 0; k0 < N; k0 += KS) {
+        const typename W::frag fh = W::ld(&sm.h[0][0], N + PADN, 16 * pt, k0, lane);
+        d0 = W::mma(fh, W::ld(&sm.qt[0][0], N + PADN, 16 * r0, k0, lane), d0);
+        d1 = W::mma(fh, W::ld(&sm.qt[0][0], N + PADN, 16 * r1, k0, lane), d1);
+      }
 #pragma unroll
-        for (int k0 = 0; k0 < N; k0 += KS) {
-          const typename W::frag fg = W::ldt(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane);
-          d0 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r0, k0, lane), d0);
-          d1 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r1, k0, lane), d1);
-        }
+      for (int u2 = 0; u2 < 2; ++u2) {
+        const int tl = 16 * (u2 ? r1 : r0) + (lane & 15);
+        const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
+        float vv[4], ff[4], o[4];
+        load4(&sm.v[tl][p], vv);
+        load4(&sm.fz[tl][p], ff);
+        const float ea = exp2_fast(sm.ac[tl] * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
-        for (int u2 = 0; u2 < 2; ++u2) {
-          const int tl = 16 * (u2 ? r1 : r0) + (lane & 15);
-          const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
-          float yy[4], o[4];
-          load4(&sm.dy[tl][p], yy);
-          const float ea = exp2_fast((aend - sm.ac[tl]) * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+        for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
+        store4(sm.outs(0) + tl * (P + PAD) + p, o);
+      }
+    };
+    auto dvpair = [&](int pt, int r0, int r1) {
+      const int p = 16 * pt + 4 * (lane >> 4);
+      // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G^T k~_s + (D + QK_s) dy_s
+      f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
-          store4(sm.outs(1) + tl * (P + PAD) + p, o);
-        }
+      for (int k0 = 0; k0 < CS; k0 += KS) {
+        const typename W::frag fa = W::ldt(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane);
+        c0 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r0, lane), c0);
+        c1 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r1, lane), c1);
+      }
+#pragma unroll
+      for (int k0 = 0; k0 < N; k0 += KS) {
+        const typename W::frag fg = W::ldt(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane);
+        d0 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r0, k0, lane), d0);
+        d1 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r1, k0, lane), d1);
+      }
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2) {
+        const int tl = 16 * (u2 ? r1 : r0) + (lane & 15);
+        const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
+        float yy[4], o[4];
+        load4(&sm.dy[tl][p], yy);
+        const float ea = exp2_fast((aend - sm.ac[tl]) * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
+        store4(sm.outs(1) + tl * (P + PAD) + p, o);
+      }
+    };
+    if constexpr (TB * (P / 16) == 2 * kBwdWaves) {
+      // both products per wave, two row blocks each
+      const int pt = wave % (P / 16), r0 = wave / (P / 16), r1 = r0 + kBwdWaves / (P / 16);
+      if (gz && a.dz) ypair(pt, r0, r1);
+      dvpair(pt, r0, r1);
+    } else if constexpr (TB == 2 && TB * (P / 16) == kBwdWaves) {
+      // one product per wave, both row blocks: the first P/16 waves y, the others dV
+      // (a y wave and a dV wave on each SIMD)
+      const int pt = wave % (P / 16);
+      if (wave < P / 16) {
+        if (gz && a.dz) ypair(pt, 0, 1);
+      } else {
+        dvpair(pt, 0, 1);
       }
     } else
 #pragma unroll
@@ -1634,7 +1651,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 
     // ---- per token: dA (its reverse cumsum into dADT), d(gamma) into dDT, d(scale)
     // into the workspace
-    if (wave == 0) {
+    if (wave == kDaWave) {
       // lane = token here (lanes CS.. hold no token)
       const bool ltok = lane < nt;
       float da = 0.0f, ds = 0.0f;
@@ -1684,11 +1701,9 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     }
     if (wave == 0) {
       const float tot = wave_sum(dsum);
-      if (lane == 0) {
-        if (a.pd) a.pd[bh] = tot;
-        a.ctot[(long)bh * (R + 1)] = cda;
-      }
+      if (lane == 0 && a.pd) a.pd[bh] = tot;
     }
+    if (wave == kDaWave && lane == 0) a.ctot[(long)bh * (R + 1)] = cda;
   }
 }
 
