@@ -942,6 +942,10 @@ struct WalkSmem {
     if constexpr (BF) return reinterpret_cast<float*>(u + OFF_RES);
     else return reinterpret_cast<float*>(&fz[0][0]);
   }
+  // float: the second product tile of the pipelined passes (the staging and output
+  // tiles are done by then)
+  __device__ __forceinline__ float* res2() { return reinterpret_cast<float*>(u); }
+  static_assert(BF || SZ_RES <= U, "float: the second product tile fits u");
   __device__ __forceinline__ float* dth() {                                                  // [CS][RH]
     if constexpr (BF) return reinterpret_cast<float*>(u + OFF_DTH);
     else return reinterpret_cast<float*>(u);
@@ -1010,6 +1014,9 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   // columns of an 8-column group and its rope pairs
   constexpr int TPL = 64 / CS, EL = 8 / TPL, PRS = 4 / TPL;
   static_assert(CS * TPL == 64, "64- or 32-token chunks");
+  // float: the dq~/dk~ passes are software-pipelined and their chain rule stores its
+  // rows itself (bf16 has no LDS left for the second product tile)
+  constexpr bool kDirect = !BF;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __builtin_assume(wave >= 0 && wave < kBwdWaves);
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
@@ -1030,6 +1037,12 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   constexpr int TPG = CS * NH / kBwdThreads;           // tokens per group
   static_assert(TPG >= 1 && CS * NH % kBwdThreads == 0, "bias column sums: whole token groups");
   float bacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // (float) per pass, this lane's EL columns of the bias sums over its tokens
+  float bq[4][EL];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < EL; ++e) bq[i][e] = 0.0f;
   float cth[2][PRS];                                   // d(theta) over the later chunks, per pair
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
@@ -1457,17 +1470,16 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     if (c > 0) cur.template issue<2>(a, c - 1, bh, tid, wave, lane);
 
     // ---- dq~ then dk~, half the columns at a time, each followed by its chain rule
+    // (passes: q~ half 0, q~ half 1, k~ half 0, k~ half 1)
     float dthq[2][PRS];                               // d(theta) from dq~, for pass K
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int j = 0; j < PRS; ++j) dthq[hh][j] = 0.0f;
-#pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-      const bool isq = pass < 2;
-      const int n0 = (pass & 1) * NH;
+    // this lane's q^ / k^ columns and rope pair of the pass's half
+    float gq8[EL], gk8[EL], gcs[PRS], gsn[PRS];
+    auto pass_regs = [&](int pass) {
       const int hh = pass & 1;
-      float gq8[EL], gk8[EL], gcs[PRS], gsn[PRS];
 #pragma unroll
       for (int e = 0; e < EL; ++e) {
         gq8[e] = hh ? qh[1][e] : qh[0][e];
@@ -1478,28 +1490,15 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         gcs[j] = hh ? cs[1][j] : cs[0][j];
         gsn[j] = hh ? sn[1][j] : sn[0][j];
       }
-      if constexpr (BF) {
-        // rounding residual of the operand this pass multiplies: k~ (dq~) or q~ (dk~)
-        if (qkw) {
-          const int g = n0 / 8 + wave;
-          float x[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = isq ? gk8[e] : gq8[e];
-          rotp<PRS>(x, gcs, gsn, 4 * g < R, 1.0f);
-          const float sc = isq && tok ? sm.scl[lane] : 1.0f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            x[e] *= sc;
-            x[e] -= (float)(bf16)x[e];
-          }
-          if (lane < CS) store8(lo + lane * (NH + PAD) + 8 * wave, x);
-        }
-        __syncthreads();
-      }
-      // Each wave's tiles are fixed iterations; a tile's k range is that of the
-      // wave's largest (dq~) or smallest (dk~) row block in the iteration, which covers
-      // its own (the masked dP is zero outside the causal range), so the ranges are
-      // compile-time constants once the loop is unrolled.
+    };
+    // The products of a pass into rb [CS][NH + 4] (token rows): dq~ (passes 0, 1) or
+    // dk~ (2, 3).  Each wave's tiles are fixed iterations; a tile's k range is that of
+    // the wave's largest (dq~) or smallest (dk~) row block in the iteration, which
+    // covers its own (the masked dP is zero outside the causal range), so the ranges
+    // are compile-time constants once the loop is unrolled.
+    auto pass_mfma = [&](int pass, float* rb) {
+      const bool isq = pass < 2;
+      const int n0 = (pass & 1) * NH;
       constexpr int NT2 = NH / 16, QT = TB * NT2, QJ = (QT + kBwdWaves - 1) / kBwdWaves;
 #pragma unroll
       for (int j = 0; j < QJ; ++j) {
@@ -1539,114 +1538,190 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * rt + 4 * (lane >> 4) + r;
           const float w = exp2_fast((isq ? sm.ac[t] : aend - sm.ac[t]) * kLog2e);
-          res[t * (NH + 4) + nl] = acc[r] + w * acc2[r];
+          rb[t * (NH + 4) + nl] = acc[r] + w * acc2[r];
         }
       }
-      __syncthreads();
-      // chain rule, lane = token (two lanes per token at 32-token chunks, EL columns
-      // each), one 8-column group per wave
+    };
+    // The chain rule of a pass from its products in rb, lane = token (two lanes per
+    // token at 32-token chunks, EL columns each), one 8-column group per wave.  float
+    // (kDirect): the lanes store their d(q^) / d(k^) columns and d(theta) pairs
+    // straight to the gradients and add the bias column sums in registers; bf16: they go
+    // back into rb and the d(theta) tile, for row stores after a barrier.
+    auto pass_chain = [&](int pass, float* rb) {
+      const bool isq = pass < 2;
+      const int n0 = (pass & 1) * NH;
+      const int hh = pass & 1;
       const int g = n0 / 8 + wave;
-      if (qkw) {
-        const int rc = tkn * (NH + 4) + 8 * wave + EL * hf;   // this lane's slots of res
-        float dx[EL], out[EL], dthv[PRS];
+      if (!qkw) return;
+      const int rc = tkn * (NH + 4) + 8 * wave + EL * hf;   // this lane's slots of rb
+      float dx[EL], out[EL], dthv[PRS];
 #pragma unroll
-        for (int e = 0; e < EL; ++e) dx[e] = out[e] = 0.0f;
+      for (int e = 0; e < EL; ++e) dx[e] = out[e] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < PRS; ++j) dthv[j] = 0.0f;
-        float dot = 0.0f, dsc = 0.0f;
-        if (tok) {
+      for (int j = 0; j < PRS; ++j) dthv[j] = 0.0f;
+      float dot = 0.0f, dsc = 0.0f;
+      if (tok) {
 #pragma unroll
-          for (int e = 0; e < EL; ++e) dx[e] = res[rc + e];
-          const float sc = sm.scl[tkn], gqk = sm.dqk[tkn] * sm.gam[tkn];
-          float xr[EL];                                   // q~ (pass Q) or rot(k^) (pass K)
+        for (int e = 0; e < EL; ++e) dx[e] = rb[rc + e];
+        const float sc = sm.scl[tkn], gqk = sm.dqk[tkn] * sm.gam[tkn];
+        float xr[EL];                                   // q~ (pass Q) or rot(k^) (pass K)
 #pragma unroll
-          for (int e = 0; e < EL; ++e) xr[e] = isq ? gq8[e] : gk8[e];
-          rotp<PRS>(xr, gcs, gsn, 4 * g < R, 1.0f);
-          const float f = isq ? 1.0f : sc;                // k~ = scale rot(k^)
+        for (int e = 0; e < EL; ++e) xr[e] = isq ? gq8[e] : gk8[e];
+        rotp<PRS>(xr, gcs, gsn, 4 * g < R, 1.0f);
+        const float f = isq ? 1.0f : sc;                // k~ = scale rot(k^)
 #pragma unroll
-          for (int e = 0; e < EL; ++e) {
-            dot += f * xr[e] * dx[e];
-            dsc += xr[e] * dx[e];
-          }
-#pragma unroll
-          for (int j = 0; j < PRS; ++j) dthv[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
-          // d(q^) = rot^T dq~ + dQK gamma k^;  d(k^) = scale rot^T dk~ + dQK gamma q^
-#pragma unroll
-          for (int e = 0; e < EL; ++e) out[e] = f * dx[e];
-          rotp<PRS>(out, gcs, gsn, 4 * g < R, -1.0f);
-#pragma unroll
-          for (int e = 0; e < EL; ++e) out[e] += gqk * (isq ? gk8[e] : gq8[e]);
+        for (int e = 0; e < EL; ++e) {
+          dot += f * xr[e] * dx[e];
+          dsc += xr[e] * dx[e];
         }
-        dot = token_pair_sum<TPL>(dot);
-        dsc = token_pair_sum<TPL>(dsc);
-        // d(q^) / d(k^) back into the thread's own slots of res, for the row stores and
+#pragma unroll
+        for (int j = 0; j < PRS; ++j) dthv[j] = f * (dx[2 * j + 1] * xr[2 * j] - dx[2 * j] * xr[2 * j + 1]);
+        // d(q^) = rot^T dq~ + dQK gamma k^;  d(k^) = scale rot^T dk~ + dQK gamma q^
+#pragma unroll
+        for (int e = 0; e < EL; ++e) out[e] = f * dx[e];
+        rotp<PRS>(out, gcs, gsn, 4 * g < R, -1.0f);
+#pragma unroll
+        for (int e = 0; e < EL; ++e) out[e] += gqk * (isq ? gk8[e] : gq8[e]);
+      }
+      dot = token_pair_sum<TPL>(dot);
+      dsc = token_pair_sum<TPL>(dsc);
+      if constexpr (kDirect) {
+        if (tok) {
+          const long row = (long)b * L + t0 + tkn;
+          const int col = n0 + 8 * wave + EL * hf;
+          if (a.dqh) {
+            float* dst = (isq ? a.dqh : a.dkh) + (row * H + h) * N + col;
+            if constexpr (EL == 4) store4(dst, out); else store8(dst, out);
+          } else {
+            T* dst = reinterpret_cast<T*>(isq ? a.dq : a.dk) + (row * HQ + hq) * N + col;
+            if constexpr (EL == 4) store4(dst, out); else store8(dst, out);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < EL; ++e) bq[pass][e] += out[e];   // 0 on padding tokens
+      } else {
+        // d(q^) / d(k^) back into the thread's own slots of rb, for the row stores and
         // the bias column sums
 #pragma unroll
-        for (int e = 0; e < EL; ++e) res[rc + e] = out[e];
-        if (isq) {
+        for (int e = 0; e < EL; ++e) rb[rc + e] = out[e];
+      }
+      if (isq) {
 #pragma unroll
-          for (int j = 0; j < PRS; ++j) dthq[hh][j] = dthv[j];
-        } else if (4 * g < R) {
-          // the token's d(theta) of each pair; its reverse cumsum over the sequence is
-          // the chunk's suffix sum plus the later chunks' total (0 on padding tokens)
-          float sv[PRS], d[PRS], f[PRS];
+        for (int j = 0; j < PRS; ++j) dthq[hh][j] = dthv[j];
+      } else if (4 * g < R) {
+        // the token's d(theta) of each pair; its reverse cumsum over the sequence is
+        // the chunk's suffix sum plus the later chunks' total (0 on padding tokens)
+        float sv[PRS], d[PRS], f[PRS];
 #pragma unroll
-          for (int j = 0; j < PRS; ++j) f[j] = d[j] = dthq[hh][j] + dthv[j];
-          token_scan<PRS>(f);
+        for (int j = 0; j < PRS; ++j) f[j] = d[j] = dthq[hh][j] + dthv[j];
+        token_scan<PRS>(f);
 #pragma unroll
-          for (int j = 0; j < PRS; ++j) {
-            const float tot = token_scan_total<PRS>(f[j], hf);
-            sv[j] = cth[hh][j] + tot - f[j] + d[j];
-            cth[hh][j] += tot;
+        for (int j = 0; j < PRS; ++j) {
+          const float tot = token_scan_total<PRS>(f[j], hf);
+          sv[j] = cth[hh][j] + tot - f[j] + d[j];
+          cth[hh][j] += tot;
+        }
+        if constexpr (kDirect) {
+          // pairs 4 g + PRS hf + j (4 g < R, R a multiple of 4)
+          if (tok) {
+            float* dst = a.dang + (((long)b * L + t0 + tkn) * H + h) * R + 4 * g + PRS * hf;
+            if constexpr (PRS == 4) store4(dst, sv);
+            else *reinterpret_cast<float2*>(dst) = make_float2(sv[0], sv[1]);
           }
+        } else {
           if constexpr (PRS == 4) store4(dth + tkn * RH + 4 * wave, sv);
           else *reinterpret_cast<float2*>(dth + tkn * RH + 4 * wave + 2 * hf) = make_float2(sv[0], sv[1]);
         }
-        if (hf == 0) {
-          if (isq) sm.pq[g][tkn] = dot;   // the same thread subtracts k~.dk~ in pass K
-          else {
-            sm.pq[g][tkn] -= dot;
-            sm.ps[g][tkn] = dsc;
-          }
+      }
+      if (hf == 0) {
+        if (isq) sm.pq[g][tkn] = dot;   // the same thread subtracts k~.dk~ in pass K
+        else {
+          sm.pq[g][tkn] -= dot;
+          sm.ps[g][tkn] = dsc;
         }
       }
+    };
+    if constexpr (kDirect) {
+      // Software pipeline, one barrier per pass: each wave's products of pass p + 1 go
+      // into one tile while the chain rule of pass p reads the other, so that a SIMD's
+      // two waves overlap MFMA and VALU work.
+      float* const rbuf[2] = {res, sm.res2()};
+      pass_mfma(0, rbuf[0]);
       __syncthreads();
-      // d(q^) / d(k^) rows of the half, the bias column sums, and (pass K) the half's
-      // d(theta) rows
-      {
-        for (int p = tid; p < CS * (NH / 8); p += kBwdThreads) {
-          const int row = p / (NH / 8), pc = p % (NH / 8);
-          if (row < nt) {
-            float o8[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o8[e] = res[row * (NH + 4) + 8 * pc + e];
-            if (a.dqh) {
-              store8((isq ? a.dqh : a.dkh) + (((long)b * L + t0 + row) * H + h) * N + n0 + 8 * pc, o8);
-            } else {
-              store8(reinterpret_cast<T*>(isq ? a.dq : a.dk) + (((long)b * L + t0 + row) * HQ + hq) * N + n0 + 8 * pc,
-                     o8);
-            }
-          }
-        }
-        const int bn = tid % NH, btg = tid / NH;
-#pragma unroll
-        for (int i = 0; i < TPG; ++i) bacc[pass] += res[(btg * TPG + i) * (NH + 4) + bn];
-        if (!isq) {
-          const int R0 = (pass & 1) * (NH / 2);                 // first pair of the half
-          const int RN = R - R0 < 0 ? 0 : (R - R0 < NH / 2 ? R - R0 : NH / 2);
-          if (RN > 0) {
-            for (int p = tid; p < CS * (RN / 4); p += kBwdThreads) {
-              const int row = p / (RN / 4), q4 = p % (RN / 4);
-              if (row < nt)
-                *reinterpret_cast<float4*>(a.dang + (((long)b * L + t0 + row) * H + h) * R + R0 + 4 * q4) =
-                    *reinterpret_cast<const float4*>(dth + row * RH + 4 * q4);
-            }
-          }
-        }
+      for (int pass = 0; pass < 4; ++pass) {
+        if (pass < 3) pass_mfma(pass + 1, rbuf[(pass + 1) & 1]);
+        pass_regs(pass);
+        pass_chain(pass, rbuf[pass & 1]);
+        if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
+        // the tile read above is written by pass p + 2's products; the last pass's
+        // per-token sums are read by the dA below
+        __syncthreads();
       }
-      // the next pass writes res and lo after its residual barrier (bf16) or this one
-      if constexpr (!BF) __syncthreads();
-      if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
+    } else {
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const bool isq = pass < 2;
+        const int n0 = (pass & 1) * NH;
+        pass_regs(pass);
+        if constexpr (BF) {
+          // rounding residual of the operand this pass multiplies: k~ (dq~) or q~ (dk~)
+          if (qkw) {
+            const int g = n0 / 8 + wave;
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = isq ? gk8[e] : gq8[e];
+            rotp<PRS>(x, gcs, gsn, 4 * g < R, 1.0f);
+            const float sc = isq && tok ? sm.scl[lane] : 1.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              x[e] *= sc;
+              x[e] -= (float)(bf16)x[e];
+            }
+            if (lane < CS) store8(lo + lane * (NH + PAD) + 8 * wave, x);
+          }
+          __syncthreads();
+        }
+        pass_mfma(pass, res);
+        __syncthreads();
+        pass_chain(pass, res);
+        __syncthreads();
+        // d(q^) / d(k^) rows of the half, the bias column sums, and (pass K) the half's
+        // d(theta) rows
+        {
+          for (int p = tid; p < CS * (NH / 8); p += kBwdThreads) {
+            const int row = p / (NH / 8), pc = p % (NH / 8);
+            if (row < nt) {
+              float o8[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) o8[e] = res[row * (NH + 4) + 8 * pc + e];
+              if (a.dqh) {
+                store8((isq ? a.dqh : a.dkh) + (((long)b * L + t0 + row) * H + h) * N + n0 + 8 * pc, o8);
+              } else {
+                store8(reinterpret_cast<T*>(isq ? a.dq : a.dk) + (((long)b * L + t0 + row) * HQ + hq) * N + n0 + 8 * pc,
+                       o8);
+              }
+            }
+          }
+          const int bn = tid % NH, btg = tid / NH;
+#pragma unroll
+          for (int i = 0; i < TPG; ++i) bacc[pass] += res[(btg * TPG + i) * (NH + 4) + bn];
+          if (!isq) {
+            const int R0 = (pass & 1) * (NH / 2);                 // first pair of the half
+            const int RN = R - R0 < 0 ? 0 : (R - R0 < NH / 2 ? R - R0 : NH / 2);
+            if (RN > 0) {
+              for (int p = tid; p < CS * (RN / 4); p += kBwdThreads) {
+                const int row = p / (RN / 4), q4 = p % (RN / 4);
+                if (row < nt)
+                  *reinterpret_cast<float4*>(a.dang + (((long)b * L + t0 + row) * H + h) * R + R0 + 4 * q4) =
+                      *reinterpret_cast<const float4*>(dth + row * RH + 4 * q4);
+              }
+            }
+          }
+        }
+        // (bf16) the next pass writes res and lo after its residual barrier
+        if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
+      }
     }
 
     // ---- per token: dA (its reverse cumsum into dADT), d(gamma) into dDT, d(scale)
@@ -1677,16 +1752,33 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   // sequence of dA and of d(theta) per pair (rounding only: both are exactly zero)
   {
     const int tid = threadIdx.x, lane = tid & 63;
-    const int bn = tid % NH, btg = tid / NH;
+    if constexpr (kDirect) {
+      // sums over the token lanes (the lanes of one hf hold the same columns)
+      if (qkw) {
+        const int tkn = lane & (CS - 1), hf = lane / CS;
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-      __syncthreads();
-      res[btg * (NH + 4) + bn] = bacc[pass];
-      __syncthreads();
-      if (tid < NH) {
-        float s = 0.0f;
-        for (int i = 0; i < kBwdThreads / NH; ++i) s += res[i * (NH + 4) + tid];
-        (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + tid] = s;
+        for (int pass = 0; pass < 4; ++pass)
+#pragma unroll
+          for (int e = 0; e < EL; ++e) {
+            float v = bq[pass][e];
+#pragma unroll
+            for (int m = 1; m < CS; m <<= 1) v += __shfl_xor(v, m, 64);
+            if (tkn == 0)
+              (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + 8 * wave + EL * hf + e] = v;
+          }
+      }
+    } else {
+      const int bn = tid % NH, btg = tid / NH;
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        __syncthreads();
+        res[btg * (NH + 4) + bn] = bacc[pass];
+        __syncthreads();
+        if (tid < NH) {
+          float s = 0.0f;
+          for (int i = 0; i < kBwdThreads / NH; ++i) s += res[i * (NH + 4) + tid];
+          (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + tid] = s;
+        }
       }
     }
     if (qkw) {
