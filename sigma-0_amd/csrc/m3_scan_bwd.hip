@@ -914,7 +914,18 @@ struct WalkSmem {
   // barrier)
   static constexpr size_t OFF_RES = SZ_LO;
   static constexpr size_t OFF_DTH = OFF_RES + SZ_RES;
-  static constexpr size_t U1 = BF ? 2 * SZ_Q : 0, U2 = SZ_SM + SZ_OUT, U3 = BF ? OFF_DTH + SZ_DTH : 0;
+  // bf16 at d_state 128: the dq~/dk~ passes run in quarters of 32 columns,
+  // software-pipelined over two residual tiles (lo) and two product tiles, at u + 0,
+  // u + 3 SZ_QT (residuals) and u + SZ_QT, u + 2 SZ_QT (products): the residuals of the
+  // first two quarters are written while the dZ/dV rows are stored from the output
+  // tiles, which lie in [SZ_SM, SZ_SM + SZ_OUT) = [SZ_QT, 3 SZ_QT).
+  static constexpr bool QP = BF && N == 128;
+  static constexpr int NQ = 32;                             // columns of a quarter
+  static constexpr size_t SZ_QT = (size_t)CS * (NQ + 4) * 4;
+  static_assert(!QP || (SZ_QT == (size_t)CS * (NH + PAD) * sizeof(T) && SZ_SM == SZ_QT &&
+                        SZ_OUT == 2 * SZ_QT), "quarter tiles: a residual tile [CS][NH + PAD] bf16 per slot");
+  static constexpr size_t U1 = BF ? 2 * SZ_Q : 0, U2 = SZ_SM + SZ_OUT,
+                          U3 = QP ? 4 * SZ_QT : (BF ? OFF_DTH + SZ_DTH : 0);
   static_assert(BF || (SZ_RES <= (size_t)CS * (P + PAD) * sizeof(T) && SZ_DTH <= SZ_SM),
                 "float: res fits fz's storage, the d(theta) tile the masked S's");
   static constexpr size_t U = U1 > U2 ? (U1 > U3 ? U1 : U3) : (U2 > U3 ? U2 : U3);
@@ -942,6 +953,10 @@ struct WalkSmem {
     if constexpr (BF) return reinterpret_cast<float*>(u + OFF_RES);
     else return reinterpret_cast<float*>(&fz[0][0]);
   }
+  // quarter passes: residual tile i ([CS][NH + PAD] bf16, NQ columns used) and product
+  // tile i ([CS][NQ + 4] float)
+  __device__ __forceinline__ T* loq(int i) { return reinterpret_cast<T*>(u + (i ? 3 * SZ_QT : 0)); }
+  __device__ __forceinline__ float* rq(int i) { return reinterpret_cast<float*>(u + (i ? 2 * SZ_QT : SZ_QT)); }
   // float: the second product tile of the pipelined passes (the staging and output
   // tiles are done by then)
   __device__ __forceinline__ float* res2() { return reinterpret_cast<float*>(u); }
@@ -1015,8 +1030,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   constexpr int TPL = 64 / CS, EL = 8 / TPL, PRS = 4 / TPL;
   static_assert(CS * TPL == 64, "64- or 32-token chunks");
   // float: the dq~/dk~ passes are software-pipelined and their chain rule stores its
-  // rows itself (bf16 has no LDS left for the second product tile)
-  constexpr bool kDirect = !BF;
+  // rows itself; bf16 at d_state 128 the same in quarters of the columns (kQP); other
+  // bf16 shapes keep the row stores from LDS after each pass
+  constexpr bool kQP = S::QP;
+  constexpr bool kDirect = !BF || kQP;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __builtin_assume(wave >= 0 && wave < kBwdWaves);
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
@@ -1048,10 +1065,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
     for (int j = 0; j < PRS; ++j) cth[hh][j] = 0.0f;
-  // The per-token dA of a chunk (sums over the column groups, reverse cumsum) runs on
-  // the last wave: wave 0 computes the next chunk's token constants at the top of the
-  // next chunk, and the other waves wait for both at its first barrier.
-  constexpr int kDaWave = kBwdWaves - 1;
+  // The per-token dA of a chunk (sums over the column groups, reverse cumsum).  float:
+  // on the last wave, beside wave 0's token constants at the top of the next chunk;
+  // bf16 outside the quarter passes (a barrier follows it): wave 0, measured 1%
+  // faster there.
+  constexpr int kDaWave = BF && !S::QP ? 0 : kBwdWaves - 1;
   float cda = 0.0f, dsum = 0.0f;                       // wave kDaWave: dA over the later chunks; wave 0: dD
 
   // One register set of loads: chunk c's inputs are consumed by the end of its
@@ -1542,18 +1560,19 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
       }
     };
-    // The chain rule of a pass from its products in rb, lane = token (two lanes per
-    // token at 32-token chunks, EL columns each), one 8-column group per wave.  float
-    // (kDirect): the lanes store their d(q^) / d(k^) columns and d(theta) pairs
-    // straight to the gradients and add the bias column sums in registers; bf16: they go
-    // back into rb and the d(theta) tile, for row stores after a barrier.
-    auto pass_chain = [&](int pass, float* rb) {
+    // The chain rule of a pass from its products in rb (row stride ldr, this wave's
+    // group at column cofs), lane = token (two lanes per token at 32-token chunks, EL
+    // columns each), one 8-column group per wave.  kDirect: the lanes store their
+    // d(q^) / d(k^) columns and d(theta) pairs straight to the gradients and add up the
+    // bias column sums in registers; otherwise they go back into rb and the d(theta)
+    // tile, for row stores after a barrier.
+    auto pass_chain = [&](int pass, float* rb, int ldr, int cofs) {
       const bool isq = pass < 2;
       const int n0 = (pass & 1) * NH;
       const int hh = pass & 1;
       const int g = n0 / 8 + wave;
       if (!qkw) return;
-      const int rc = tkn * (NH + 4) + 8 * wave + EL * hf;   // this lane's slots of rb
+      const int rc = tkn * ldr + cofs + EL * hf;   // this lane's slots of rb
       float dx[EL], out[EL], dthv[PRS];
 #pragma unroll
       for (int e = 0; e < EL; ++e) dx[e] = out[e] = 0.0f;
@@ -1597,8 +1616,23 @@ void scan_bwd_walk_kernel(BwdArgs a) {
             if constexpr (EL == 4) store4(dst, out); else store8(dst, out);
           }
         }
+        if constexpr (!BF) {
 #pragma unroll
-        for (int e = 0; e < EL; ++e) bq[pass][e] += out[e];   // 0 on padding tokens
+          for (int e = 0; e < EL; ++e) bq[pass][e] += out[e];   // 0 on padding tokens
+        } else {
+          // the 8 columns summed over the 64 lanes by halving exchanges: lane l keeps
+          // column l / 8 of the group, summed over the lanes that share l % 8 (their
+          // sum over the walk follows at its end)
+          const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+          float v4[4], v2[2];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v4[j] = (b5 ? out[j + 4] : out[j]) + __shfl_xor(b5 ? out[j] : out[j + 4], 32, 64);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            v2[j] = (b4 ? v4[j + 2] : v4[j]) + __shfl_xor(b4 ? v4[j] : v4[j + 2], 16, 64);
+          bacc[pass] += (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
+        }
       } else {
         // d(q^) / d(k^) back into the thread's own slots of rb, for the row stores and
         // the bias column sums
@@ -1641,7 +1675,112 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
       }
     };
-    if constexpr (kDirect) {
+    if constexpr (kQP) {
+      // bf16, d_state 128: quarter q (0..7) is pass q / 2, columns 32 (q % 2) .. + 31 of
+      // its half, whose 8-column groups belong to waves 4 (q % 2) .. + 3.  Software
+      // pipeline, one barrier per quarter: the products of quarter q + 1 beside the chain
+      // rule of quarter q and the rounding residual of quarter q + 2, over two product
+      // and two residual tiles.
+      // rounding residual of the operand of pass `pass`, k~ (dq~) or q~ (dk~), in this
+      // wave's quarter (the waves of one half), into residual tile `slot`
+      auto quarter_lo = [&](int pass, int slot) {
+        const int hh = pass & 1;
+        const bool isq = pass < 2;
+        const int g = hh * GH + wave;
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = isq ? kh[hh][e] : qh[hh][e];
+        rotp<PRS>(x, cs[hh], sn[hh], 4 * g < R, 1.0f);
+        const float sc = isq && tok ? sm.scl[lane] : 1.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[e] *= sc;
+          x[e] -= (float)(bf16)x[e];
+        }
+        store8(sm.loq(slot) + lane * (NH + PAD) + 8 * (wave & 3), x);
+      };
+      // The products of quarter q into rb, tiles (row block rt, column tile ntl): with
+      // `both`, the two tiles (rt, ntl) and (rt + 2, ntl) of rt = (wave % 4) / 2, ntl =
+      // wave % 2 (the waves of one half cover the quarter), else the one tile (wave / 2,
+      // wave % 2).  The two tiles share their k~ / q~, residual and h / G fragments, and
+      // k blocks outside the causal range are skipped (the masked dP is zero there).
+      auto quarter_mfma = [&](int q, float* rb, auto both) {
+        constexpr bool B2 = decltype(both)::value;
+        const int pass = q >> 1;
+        const bool isq = pass < 2;
+        const int c0 = (pass & 1) * NH + S::NQ * (q & 1) + 16 * (wave & 1);
+        const int ra = B2 ? (wave & 3) >> 1 : wave >> 1;
+        const T* lq = sm.loq(q & 1) + 16 * (wave & 1);
+        f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, b0 = a0, b1 = a0;
+#pragma unroll
+        for (int k0 = 0; k0 < CS; k0 += KS) {
+          // which tiles take this k block (B2: ra <= 1; dq~ block 0 both, block 1 the
+          // lower tile; dk~ block 1 both, block 0 the upper tile)
+          const bool ta = B2 ? (isq ? k0 == 0 : true) : (isq ? k0 < 16 * (ra + 1) : k0 + KS > 16 * ra);
+          const bool tb = B2 && (isq ? true : k0 > 0);
+          if (!ta && !tb) continue;
+          const typename W::frag fo = W::ldt(isq ? &sm.kt[0][0] : &sm.qt[0][0], N + PADN, k0, c0, lane);
+          const typename W::frag fl = W::ldt(lq, NH + PAD, k0, 0, lane);
+          if (ta) {
+            const typename W::frag fa = isq ? W::ld(&sm.dpm[0][0], CS + PAD, 16 * ra, k0, lane)
+                                            : W::ldt(&sm.dpm[0][0], CS + PAD, k0, 16 * ra, lane);
+            a0 = W::mma(fa, fo, a0);
+            a0 = W::mma(fa, fl, a0);
+          }
+          if (tb) {
+            const typename W::frag fb = isq ? W::ld(&sm.dpm[0][0], CS + PAD, 16 * (ra + 2), k0, lane)
+                                            : W::ldt(&sm.dpm[0][0], CS + PAD, k0, 16 * (ra + 2), lane);
+            a1 = W::mma(fb, fo, a1);
+            a1 = W::mma(fb, fl, a1);
+          }
+        }
+#pragma unroll
+        for (int k0 = 0; k0 < P; k0 += KS) {
+          // dq~: e^{A_t} dy_t h;  dk~: e^{A_end - A_s} v_s G
+          const typename W::frag fs = isq ? W::ldt(&sm.h[0][0], N + PADN, k0, c0, lane)
+                                          : W::ld(&sm.gt[0][0], P + PAD, c0, k0, lane);
+          const T* xs = isq ? &sm.dy[0][0] : &sm.v[0][0];
+          b0 = W::mma(W::ld(xs, P + PAD, 16 * ra, k0, lane), fs, b0);
+          if (B2) b1 = W::mma(W::ld(xs, P + PAD, 16 * (ra + 2), k0, lane), fs, b1);
+        }
+        const int nl = 16 * (wave & 1) + (lane & 15);
+#pragma unroll
+        for (int u2 = 0; u2 < (B2 ? 2 : 1); ++u2) {
+          const f32x4 acc = u2 ? a1 : a0, acc2 = u2 ? b1 : b0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * (ra + 2 * u2) + 4 * (lane >> 4) + r;
+            const float w = exp2_fast((isq ? sm.ac[t] : aend - sm.ac[t]) * kLog2e);
+            rb[t * (S::NQ + 4) + nl] = acc[r] + w * acc2[r];
+          }
+        }
+      };
+      static_assert(!kQP || (CS == 64 && KS == 32 && GH == kBwdWaves && TB * (S::NQ / 16) == kBwdWaves),
+                    "quarter passes: 8 product tiles and four groups per quarter, two k blocks");
+      // quarters 0 and 1 (their residual tiles lie outside the output tiles that the
+      // dZ/dV row stores above still read)
+      quarter_lo(0, wave >> 2);
+      __syncthreads();
+      quarter_mfma(0, sm.rq(0), std::false_type());
+      __syncthreads();
+      // quarter q: the waves of half q % 2 run its chain rule and quarter q + 2's
+      // residual, the other half quarter q + 1's products (a VALU wave and an MFMA wave
+      // on each SIMD)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if ((wave >> 2) == (q & 1)) {
+          pass_regs(q >> 1);
+          pass_chain(q >> 1, sm.rq(q & 1), S::NQ + 4, 8 * (wave & 3));
+          if (q < 6) quarter_lo((q + 2) >> 1, q & 1);
+        } else if (q < 7) {
+          quarter_mfma(q + 1, sm.rq((q + 1) & 1), std::true_type());
+        }
+        if (q == 3 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
+        // the tiles read above are written two quarters on; the last quarter's
+        // per-token sums are read by the dA below
+        __syncthreads();
+      }
+    } else if constexpr (!BF) {
       // Software pipeline, one barrier per pass: each wave's products of pass p + 1 go
       // into one tile while the chain rule of pass p reads the other, so that a SIMD's
       // two waves overlap MFMA and VALU work.
@@ -1652,7 +1791,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       for (int pass = 0; pass < 4; ++pass) {
         if (pass < 3) pass_mfma(pass + 1, rbuf[(pass + 1) & 1]);
         pass_regs(pass);
-        pass_chain(pass, rbuf[pass & 1]);
+        pass_chain(pass, rbuf[pass & 1], NH + 4, 8 * wave);
         if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
         // the tile read above is written by pass p + 2's products; the last pass's
         // per-token sums are read by the dA below
@@ -1684,7 +1823,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         }
         pass_mfma(pass, res);
         __syncthreads();
-        pass_chain(pass, res);
+        pass_chain(pass, res, NH + 4, 8 * wave);
         __syncthreads();
         // d(q^) / d(k^) rows of the half, the bias column sums, and (pass K) the half's
         // d(theta) rows
@@ -1744,15 +1883,27 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       if (ltok) a.dadt[(long)bh * L + t0 + lane] = cda + tot - f + da;
       cda += tot;
     }
-    // the next chunk's staging overlaps res and the d(theta) tile read above
-    if constexpr (BF) __syncthreads();
+    // the next chunk's staging overlaps res and the d(theta) tile read above (the
+    // quarter passes end with a barrier and store their rows themselves)
+    if constexpr (BF && !kQP) __syncthreads();
   }
 
   // ---- the walk's totals: bias and D gradients of this (b, h), and the sums over the
   // sequence of dA and of d(theta) per pair (rounding only: both are exactly zero)
   {
     const int tid = threadIdx.x, lane = tid & 63;
-    if constexpr (kDirect) {
+    if constexpr (kQP) {
+      // lane l holds column l / 8 of the wave's group, summed over the lanes that share
+      // l % 8
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        float v = bacc[pass];
+        v += __shfl_xor(v, 1, 64);
+        v += __shfl_xor(v, 2, 64);
+        v += __shfl_xor(v, 4, 64);
+        if ((lane & 7) == 0) (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + 8 * wave + (lane >> 3)] = v;
+      }
+    } else if constexpr (kDirect) {
       // sums over the token lanes (the lanes of one hf hold the same columns)
       if (qkw) {
         const int tkn = lane & (CS - 1), hf = lane / CS;
