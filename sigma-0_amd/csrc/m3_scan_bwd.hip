@@ -1622,16 +1622,26 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         } else {
           // the 8 columns summed over the 64 lanes by halving exchanges: lane l keeps
           // column l / 8 of the group, summed over the lanes that share l % 8 (their
-          // sum over the walk follows at its end)
-          const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+          // sum over the walk follows at its end).  v_permlane32_swap exchanges the
+          // upper 32 lanes of its first operand with the lower 32 of its second, so the
+          // sum of the two results holds column j in lanes 0-31 and column j + 4 in
+          // lanes 32-63; v_permlane16_swap does the same with odd and even 16-lane rows.
           float v4[4], v2[2];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            v4[j] = (b5 ? out[j + 4] : out[j]) + __shfl_xor(b5 ? out[j] : out[j + 4], 32, 64);
+          for (int j = 0; j < 4; ++j) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(out[j]), __float_as_uint(out[j + 4]),
+                                                            false, false);
+            v4[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+          }
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            v2[j] = (b4 ? v4[j + 2] : v4[j]) + __shfl_xor(b4 ? v4[j] : v4[j + 2], 16, 64);
-          bacc[pass] += (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
+          for (int j = 0; j < 2; ++j) {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v4[j]), __float_as_uint(v4[j + 2]),
+                                                            false, false);
+            v2[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+          }
+          const bool b3 = lane & 8;
+          constexpr int kDppRowRor8 = 0x128;   // lane l <- lane l ^ 8 of its row
+          bacc[pass] += (b3 ? v2[1] : v2[0]) + dpp0<kDppRowRor8>(b3 ? v2[0] : v2[1]);
         }
       } else {
         // d(q^) / d(k^) back into the thread's own slots of rb, for the row stores and
