@@ -940,8 +940,10 @@ struct WalkSmem {
   alignas(16) char u[U];
   alignas(16) float ac[CS];
   float gam[CS], scl[CS], dtv[CS], qk[CS], dqk[CS];
-  float pq[N / 8][CS];                 // per column group: q^.k^, then q~.dq~ - k~.dk~
-  float ps[N / 8][CS];                 // per column group: dk~ . rot(k^)
+  // per token, one row per column-group wave (its two groups): q^.k^, then
+  // q~.dq~ - k~.dk~; dk~ . rot(k^)
+  float pq[N / 16][CS];
+  float ps[N / 16][CS];
   float qb[N], kb[N];                  // the head's biases
   float aend;
   __device__ __forceinline__ uint4* qstage() { return reinterpret_cast<uint4*>(u); }
@@ -1174,6 +1176,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     // half of the state columns): q^ = q + qb, k^ = k + kb and the rope cos/sin of
     // their pairs stay in registers for every phase below; q~ and k~ go to LDS.
     float qh[2][EL], kh[2][EL], cs[2][PRS], sn[2][PRS];
+    float pqw = 0.0f;                                 // q^.k^ over the wave's two groups
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int g = hh * GH + wave;
@@ -1249,9 +1252,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           store4(&sm.qt[tkn][col], q);
           store4(&sm.kt[tkn][col], k);
         }
-        if (hf == 0) sm.pq[g][tkn] = dot;
+        pqw += dot;
       }
     }
+    // per-token partial sums: one row of pq per column-group wave
+    if (qkw && hf == 0) sm.pq[wave][tkn] = pqw;
     // V, dOut, Z in row layout: dy = dOut silu(z), the dZ factor, and dy . v per token
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
@@ -1287,7 +1292,8 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     if (wave == 0) {
       float qk = 0.0f;
       if (lane < CS) {
-        for (int g = 0; g < N / 8; ++g) qk += sm.pq[g][lane];
+#pragma unroll
+        for (int w = 0; w < GH; ++w) qk += sm.pq[w][lane];
         sm.qk[lane] = qk;
         dsum += sm.dqk[lane];                         // padding tokens hold dy = 0
       }
@@ -1496,6 +1502,8 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       for (int j = 0; j < PRS; ++j) dthq[hh][j] = 0.0f;
     // this lane's q^ / k^ columns and rope pair of the pass's half
     float gq8[EL], gk8[EL], gcs[PRS], gsn[PRS];
+    // per token over the wave's groups: q~.dq~ - k~.dk~ and dk~.rot(k^)
+    float pacc = 0.0f, sacc = 0.0f;
     auto pass_regs = [&](int pass) {
       const int hh = pass & 1;
 #pragma unroll
@@ -1677,12 +1685,16 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           else *reinterpret_cast<float2*>(dth + tkn * RH + 4 * wave + 2 * hf) = make_float2(sv[0], sv[1]);
         }
       }
-      if (hf == 0) {
-        if (isq) sm.pq[g][tkn] = dot;   // the same thread subtracts k~.dk~ in pass K
-        else {
-          sm.pq[g][tkn] -= dot;
-          sm.ps[g][tkn] = dsc;
-        }
+      if (isq) {
+        pacc += dot;
+      } else {
+        pacc -= dot;
+        sacc += dsc;
+      }
+      // after the wave's last pass: its row of the per-token partial sums
+      if (pass == 3 && hf == 0) {
+        sm.pq[wave][tkn] = pacc;
+        sm.ps[wave][tkn] = sacc;
       }
     };
     if constexpr (kQP) {
@@ -1880,9 +1892,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       const bool ltok = lane < nt;
       float da = 0.0f, ds = 0.0f;
       if (ltok) {
-        for (int g = 0; g < N / 8; ++g) {
-          da += sm.pq[g][lane];
-          ds += sm.ps[g][lane];
+#pragma unroll
+        for (int w = 0; w < GH; ++w) {
+          da += sm.pq[w][lane];
+          ds += sm.ps[w][lane];
         }
         const long o = (long)bh * L + t0 + lane;
         a.dsc[o] = ds;
