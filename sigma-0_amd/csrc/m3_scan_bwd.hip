@@ -1574,23 +1574,28 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     // d(q^) / d(k^) columns and d(theta) pairs straight to the gradients and add up the
     // bias column sums in registers; otherwise they go back into rb and the d(theta)
     // tile, for row stores after a barrier.
-    auto pass_chain = [&](int pass, float* rb, int ldr, int cofs) {
+    // (the chain rule's LDS reads, apart from its computation, so that a caller can
+    // issue them ahead of other work)
+    auto chain_load = [&](const float* rb, int ldr, int cofs, float* dx, float& sc, float& gqk) {
+      const int rc = tkn * ldr + cofs + EL * hf;   // this lane's slots of rb
+#pragma unroll
+      for (int e = 0; e < EL; ++e) dx[e] = rb[rc + e];
+      sc = sm.scl[tkn];
+      gqk = sm.dqk[tkn] * sm.gam[tkn];
+    };
+    // Padding tokens (t >= nt) hold zeros in rb and in dQK, gamma and the scale, so
+    // their results are zeros without a branch; only their stores are skipped.
+    auto chain_compute = [&](int pass, const float* dx, float sc, float gqk) {
       const bool isq = pass < 2;
       const int n0 = (pass & 1) * NH;
       const int hh = pass & 1;
       const int g = n0 / 8 + wave;
-      if (!qkw) return;
-      const int rc = tkn * ldr + cofs + EL * hf;   // this lane's slots of rb
-      float dx[EL], out[EL], dthv[PRS];
-#pragma unroll
-      for (int e = 0; e < EL; ++e) dx[e] = out[e] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < PRS; ++j) dthv[j] = 0.0f;
+      if constexpr (GH < kBwdWaves) {
+        if (!qkw) return;
+      }
+      float out[EL], dthv[PRS];
       float dot = 0.0f, dsc = 0.0f;
-      if (tok) {
-#pragma unroll
-        for (int e = 0; e < EL; ++e) dx[e] = rb[rc + e];
-        const float sc = sm.scl[tkn], gqk = sm.dqk[tkn] * sm.gam[tkn];
+      {
         float xr[EL];                                   // q~ (pass Q) or rot(k^) (pass K)
 #pragma unroll
         for (int e = 0; e < EL; ++e) xr[e] = isq ? gq8[e] : gk8[e];
@@ -1652,10 +1657,10 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           bacc[pass] += (b3 ? v2[1] : v2[0]) + dpp0<kDppRowRor8>(b3 ? v2[0] : v2[1]);
         }
       } else {
-        // d(q^) / d(k^) back into the thread's own slots of rb, for the row stores and
-        // the bias column sums
+        // d(q^) / d(k^) back into the thread's own slots of the product tile (res),
+        // for the row stores and the bias column sums
 #pragma unroll
-        for (int e = 0; e < EL; ++e) rb[rc + e] = out[e];
+        for (int e = 0; e < EL; ++e) res[tkn * (NH + 4) + 8 * wave + EL * hf + e] = out[e];
       }
       if (isq) {
 #pragma unroll
@@ -1696,6 +1701,14 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         sm.pq[wave][tkn] = pacc;
         sm.ps[wave][tkn] = sacc;
       }
+    };
+    auto pass_chain = [&](int pass, const float* rb, int ldr, int cofs) {
+      if constexpr (GH < kBwdWaves) {
+        if (!qkw) return;
+      }
+      float dx[EL], sc, gqk;
+      chain_load(rb, ldr, cofs, dx, sc, gqk);
+      chain_compute(pass, dx, sc, gqk);
     };
     if constexpr (kQP) {
       // bf16, d_state 128: quarter q (0..7) is pass q / 2, columns 32 (q % 2) .. + 31 of
@@ -1811,9 +1824,13 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       __syncthreads();
 #pragma unroll
       for (int pass = 0; pass < 4; ++pass) {
+        // the chain rule's inputs first, so that its computation can interleave with
+        // the products' MFMA chains (their tile stores would otherwise order them)
+        float dx[EL], sc = 0.0f, gqk = 0.0f;
+        if (qkw) chain_load(rbuf[pass & 1], NH + 4, 8 * wave, dx, sc, gqk);
         if (pass < 3) pass_mfma(pass + 1, rbuf[(pass + 1) & 1]);
         pass_regs(pass);
-        pass_chain(pass, rbuf[pass & 1], NH + 4, 8 * wave);
+        chain_compute(pass, dx, sc, gqk);
         if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
         // the tile read above is written by pass p + 2's products; the last pass's
         // per-token sums are read by the dA below
