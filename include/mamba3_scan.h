@@ -179,8 +179,10 @@ int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
  * :272-285), and mamba3_siso_bwd(saved, grad_output) (:821-902).
  *
  * m3_chunk_scan_saved_bytes: bytes of the residual buffer, the state entering every
- * chunk of the backward's chunking (64 tokens bf16, 32 float32; io dtype) and its
- * rope angles (float32); 0 when the backward has no kernel for the shape.
+ * chunk of the backward's chunking (64 tokens bf16, 32 float32; io dtype), its rope
+ * angles (float32) and, for float32 I/O, the output before the gate (B x L x H x P,
+ * the reference's Out_v residual; written when Z is given); 0 when the backward has
+ * no kernel for the shape.
  *
  * m3_chunk_scan_fwd_train: m3_chunk_scan_fwd_ws that also writes the residuals into
  * `saved` (>= m3_chunk_scan_saved_bytes, 16-byte aligned).  No initial carry (the
@@ -190,7 +192,8 @@ int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
  *
  * m3_chunk_scan_bwd_saved: m3_chunk_scan_bwd reading the residuals of the
  * m3_chunk_scan_fwd_train call on the same inputs instead of recomputing the chunk
- * states; its workspace is m3_chunk_scan_bwd_saved_ws_bytes.
+ * states (and, float32 I/O with Z, dZ from the saved output before the gate); its
+ * workspace is m3_chunk_scan_bwd_saved_ws_bytes.
  */
 size_t m3_chunk_scan_saved_bytes(int B, int L, int H, int N, int P, int R, int io_dtype);
 int m3_chunk_scan_fwd_train(const void* Q, const void* K, const void* V,

@@ -133,7 +133,9 @@ int scan_fwd(const void* Q, const void* K, const void* V,
       return fail(M3_E_ARG, "saved-state buffer of %zu bytes, the shape needs %zu (m3_chunk_scan_saved_bytes)",
                   saved_bytes, need);
     if (!aligned16(saved)) return fail(M3_E_ALIGN, "saved-state buffer must be 16-byte aligned");
-    m3::scan_bwd_saved_ptrs(saved, bf, B, L, H, N, P, R, &a.chunk_h, &a.chunk_th);
+    void* yv;
+    m3::scan_bwd_saved_ptrs(saved, bf, B, L, H, N, P, R, &a.chunk_h, &a.chunk_th, &yv);
+    a.out_v = Z ? yv : nullptr;                      // null for bf16 I/O
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (impl == M3_IMPL_CHUNKED_MFMA) {

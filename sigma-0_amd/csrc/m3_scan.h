@@ -40,6 +40,10 @@ struct ScanArgs {
   // wider rows (the mixer layer's input projection); 0: the contiguous (B, L, H, P)
   // layout.  Honoured by the chunked kernel only; the output stays contiguous.
   long vz_tok = 0, vz_bat = 0;
+  // With chunk_h (the training forward) and Z: the output before the gate, (B, L, H, P)
+  // in the I/O type, which the backward multiplies into dZ instead of recomputing it
+  // (last, so that the other members keep their kernel-argument offsets).
+  void* out_v = nullptr;
 };
 
 // Block order for launches whose heads share Q/K rows: blocks are handed to the 8
@@ -78,12 +82,14 @@ bool scan_bwd_supported(bool bf16_io, int N, int P, int R);
 // saved: the chunk states come from the training forward (no state-only pass)
 size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared,
                          bool saved = false);
-// The training forward's saved chunk states: the state entering every chunk of the
-// backward's chunking ([bh][chunk][P][N], io type) and its rope angle ([bh][chunk][R]
-// f32, revolutions); bytes, and the two arrays' addresses in a buffer of that size.
+// The training forward's residuals: the state entering every chunk of the backward's
+// chunking ([bh][chunk][P][N], io type), its rope angle ([bh][chunk][R] f32,
+// revolutions) and, for float32 I/O, the output before the gate ((B, L, H, P) f32;
+// written when Z is given, else null); bytes, and the three arrays' addresses in a
+// buffer of that size.
 size_t scan_bwd_saved_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R);
 void scan_bwd_saved_ptrs(void* saved, bool bf16_io, int B, int L, int H, int N, int P, int R, void** h,
-                         float** th);
+                         float** th, void** yv);
 hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st, const void* saved = nullptr);
 
 // Mamba3 mixer layer: the elementwise work around the scan.

@@ -159,6 +159,8 @@ struct BwdArgs {
   float* dsc;                  // [bh][L] d(scale) per token
   float* ctot;                 // [bh][nc][1 + R] chunk sums of dA and of d(theta) per pair
   int nc;
+  const void* yv;              // (B, L, H, P) T: the output before the gate, saved by the
+                               // training forward (the walk then forms dZ = y_v fz), or null
 };
 
 // Per-chunk token constants shared by the adjoint and gradient kernels: lane = token.
@@ -804,7 +806,8 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
 // dK and dAngles are staged in LDS and written as whole rows.  The next chunk's loads
 // are requested in four parts spread over the current chunk, behind whose work their
 // latency hides.
-template <typename T, int CS, int N, int P, int R>
+// YV: also the saved output before the gate (the walk's training-pair variant)
+template <typename T, int CS, int N, int P, int R, bool YV>
 struct WalkLoads {
   static constexpr int GH = N / 16;                                       // column groups per half
   static constexpr int HP = (P * N / 8 + kBwdThreads - 1) / kBwdThreads;  // 8-element state pieces per thread
@@ -813,7 +816,7 @@ struct WalkLoads {
   static constexpr int HK = 8 * (int)sizeof(T) / 16;                     // 16-byte words per state piece
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));             // (a plain vector: kept in registers)
   u32x4 hpc[HP][HK];
-  Vec8<T> qpc[QPT], kpc[QPT], vpc[VPT], dypc[VPT], zpc[VPT];
+  Vec8<T> qpc[QPT], kpc[QPT], vpc[VPT], dypc[VPT], zpc[VPT], ypc[VPT];
   float4 rates[2], th0[2];
   float adt, dt, trap, dtn, trapn;
   // Every load is unconditional, from a clamped valid address where a lane has nothing
@@ -857,6 +860,7 @@ struct WalkLoads {
         vpc[k].load(gv + row);
         dypc[k].load(reinterpret_cast<const T*>(a.dout) + row);
         zpc[k].load(gz + row);
+        if constexpr (YV) ypc[k].load(reinterpret_cast<const T*>(a.yv) + row);
       }
     } else {
       const int tcl = min(t0 + (lane & (CS - 1)), L - 1);
@@ -1012,12 +1016,14 @@ template <> struct WalkMma<float> {
   }
 };
 
-template <typename T, int CS, int N, int P, int R>
+// YV: the training pair's variant that reads the saved output before the gate (a.yv)
+// and forms dZ from it in the preparation instead of recomputing y.
+template <typename T, int CS, int N, int P, int R, bool YV>
 __global__ __launch_bounds__(kBwdThreads, 1)
 void scan_bwd_walk_kernel(BwdArgs a) {
   typedef WalkMma<T> W;
   typedef WalkSmem<T, CS, N, P, R> S;
-  typedef WalkLoads<T, CS, N, P, R> Loads;
+  typedef WalkLoads<T, CS, N, P, R, YV> Loads;
   static_assert(sizeof(S) <= 160 * 1024, "LDS budget");
   __shared__ S sm;
   constexpr int PAD = S::PAD, PADN = S::PADN, KS = W::KSTEP, NH = S::NH, SQ = S::SQ, RH = S::RH;
@@ -1277,6 +1283,15 @@ void scan_bwd_walk_kernel(BwdArgs a) {
               fz[e] = dy[e] * sz * (1.0f + z[e] * (1.0f - sz));
               dy[e] *= z[e] * sz;
             }
+            if (YV && a.dz) {
+              // dZ = y_v fz, with y_v the training forward's saved output before the
+              // gate (the reference's Out_v residual)
+              float yv[8];
+              cur.ypc[k].to_f(yv);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) yv[e] *= fz[e];
+              store8(reinterpret_cast<T*>(a.dz) + (((long)b * L + t0 + row) * H + h) * P + 8 * pc, yv);
+            }
           }
 #pragma unroll
           for (int e = 0; e < 8; ++e) dot += dy[e] * v[e];
@@ -1371,7 +1386,9 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         store4(sm.outs(0) + tl * (P + PAD) + p, o);
       }
     };
-    auto dvpair = [&](int pt, int r0, int r1) {
+    // (two_c false: row block r0 alone)
+    auto dvpair = [&](int pt, int r0, int r1, auto two_c) {
+      constexpr bool TWO = decltype(two_c)::value;
       const int p = 16 * pt + 4 * (lane >> 4);
       // dv_s = sum_t Sm[t][s] dy_t + e^{A_end - A_s} G^T k~_s + (D + QK_s) dy_s
       f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, d0 = c0, d1 = c0;
@@ -1379,16 +1396,16 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       for (int k0 = 0; k0 < CS; k0 += KS) {
         const typename W::frag fa = W::ldt(&sm.dy[0][0], P + PAD, k0, 16 * pt, lane);
         c0 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r0, lane), c0);
-        c1 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r1, lane), c1);
+        if (TWO) c1 = W::mma(fa, W::ldt(smk, CS + PAD, k0, 16 * r1, lane), c1);
       }
 #pragma unroll
       for (int k0 = 0; k0 < N; k0 += KS) {
         const typename W::frag fg = W::ldt(&sm.gt[0][0], P + PAD, k0, 16 * pt, lane);
         d0 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r0, k0, lane), d0);
-        d1 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r1, k0, lane), d1);
+        if (TWO) d1 = W::mma(fg, W::ld(&sm.kt[0][0], N + PADN, 16 * r1, k0, lane), d1);
       }
 #pragma unroll
-      for (int u2 = 0; u2 < 2; ++u2) {
+      for (int u2 = 0; u2 < (TWO ? 2 : 1); ++u2) {
         const int tl = 16 * (u2 ? r1 : r0) + (lane & 15);
         const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
         float yy[4], o[4];
@@ -1399,19 +1416,24 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         store4(sm.outs(1) + tl * (P + PAD) + p, o);
       }
     };
+    // y is needed for dZ alone; with the training forward's saved output before the
+    // gate (a.yv) the preparation has written dZ already
+    const bool need_y = gz && a.dz && !YV;
     if constexpr (TB * (P / 16) == 2 * kBwdWaves) {
       // both products per wave, two row blocks each
       const int pt = wave % (P / 16), r0 = wave / (P / 16), r1 = r0 + kBwdWaves / (P / 16);
-      if (gz && a.dz) ypair(pt, r0, r1);
-      dvpair(pt, r0, r1);
+      if (need_y) ypair(pt, r0, r1);
+      dvpair(pt, r0, r1, std::true_type());
     } else if constexpr (TB == 2 && TB * (P / 16) == kBwdWaves) {
       // one product per wave, both row blocks: the first P/16 waves y, the others dV
-      // (a y wave and a dV wave on each SIMD)
+      // (a y wave and a dV wave on each SIMD); without y, dV one row block per wave
       const int pt = wave % (P / 16);
-      if (wave < P / 16) {
-        if (gz && a.dz) ypair(pt, 0, 1);
+      if (!need_y) {
+        dvpair(pt, wave / (P / 16), 0, std::false_type());
+      } else if (wave < P / 16) {
+        ypair(pt, 0, 1);
       } else {
-        dvpair(pt, 0, 1);
+        dvpair(pt, 0, 1, std::true_type());
       }
     } else
 #pragma unroll
@@ -1421,7 +1443,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
       const int tl = 16 * rt + (lane & 15), p = 16 * pt + 4 * (lane >> 4);
       if (which == 0) {
-        if (!gz || !a.dz) continue;
+        if (!need_y) continue;
         // y_t = sum_s Sm[t][s] v_s + e^{A_t} h q~_t + (D + QK_t) v_t
 #pragma unroll
         for (int k0 = 0; k0 < CS; k0 += KS)
@@ -1461,7 +1483,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       T* const gdv = reinterpret_cast<T*>(a.dv);
       for (int p = tid; p < 2 * CS * (P / 8); p += kBwdThreads) {
         const int w = p / (CS * (P / 8)), q = p % (CS * (P / 8)), row = q / (P / 8), pc = q % (P / 8);
-        if (row < nt && (w == 1 || (gz && gdz))) {
+        if (row < nt && (w == 1 || (gz && gdz && !YV))) {
           const long o = (((long)b * L + t0 + row) * H + h) * P + 8 * pc;
           *reinterpret_cast<Vec8<T>*>((w ? gdv : gdz) + o) =
               *reinterpret_cast<const Vec8<T>*>(sm.outs(w) + row * (P + PAD) + 8 * pc);
@@ -2316,16 +2338,38 @@ size_t scan_bwd_ws_bytes(bool bf16_io, int B, int L, int H, int Hqk, int N, int 
   return bwd_layout(bf16_io, B, L, H, Hqk, N, P, R, ang_shared, saved).total;
 }
 
+// The output before the gate (float32 I/O only: at bf16 the forward's extra writes
+// cost more than the walk's y tiles, measured).
+size_t saved_y_bytes(bool bf16_io, int B, int L, int H, int P) {
+  return bf16_io ? 0 : al256((size_t)B * L * H * P * 4);
+}
+
 size_t scan_bwd_saved_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R) {
   if (!scan_bwd_supported(bf16_io, N, P, R) || B <= 0 || L <= 0) return 0;
-  return saved_h_bytes(bf16_io, B, L, H, N, P) + saved_th_bytes(bf16_io, B, L, H, R);
+  return saved_h_bytes(bf16_io, B, L, H, N, P) + saved_th_bytes(bf16_io, B, L, H, R) +
+         saved_y_bytes(bf16_io, B, L, H, P);
 }
 
 void scan_bwd_saved_ptrs(void* saved, bool bf16_io, int B, int L, int H, int N, int P, int R, void** h,
-                         float** th) {
+                         float** th, void** yv) {
+  char* base = reinterpret_cast<char*>(saved);
+  const size_t hb = saved_h_bytes(bf16_io, B, L, H, N, P), tb = saved_th_bytes(bf16_io, B, L, H, R);
   *h = saved;
-  *th = R > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(saved) + saved_h_bytes(bf16_io, B, L, H, N, P))
-              : nullptr;
+  *th = R > 0 ? reinterpret_cast<float*>(base + hb) : nullptr;
+  *yv = bf16_io ? nullptr : base + hb + tb;
+}
+
+// The walk, in its training-pair variant when the forward saved the output before the
+// gate (float32 only: a.yv is never set for bf16).
+template <typename T, int CS, int N, int P, int R>
+void launch_walk(dim3 grid, hipStream_t st, const BwdArgs& a) {
+  if constexpr (std::is_same<T, float>::value) {
+    if (a.yv) {
+      hipLaunchKernelGGL((scan_bwd_walk_kernel<T, CS, N, P, R, true>), grid, dim3(kBwdThreads), 0, st, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((scan_bwd_walk_kernel<T, CS, N, P, R, false>), grid, dim3(kBwdThreads), 0, st, a);
 }
 
 hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st, const void* saved) {
@@ -2341,12 +2385,17 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.dadt = g.dadt; a.ddt = g.ddt; a.dtrap = g.dtrap;
   a.dang = w.dangh ? reinterpret_cast<float*>(base + w.dangh) : g.dang;   // per head, then summed
   a.dqb = g.dqb; a.dkb = g.dkb; a.dD = g.dD;
+  a.yv = nullptr;
   if (saved) {
     void* sh;
     float* sth;
-    scan_bwd_saved_ptrs(const_cast<void*>(saved), bf16_io, s.B, s.L, s.H, s.N, s.P, s.R, &sh, &sth);
+    void* syv;
+    scan_bwd_saved_ptrs(const_cast<void*>(saved), bf16_io, s.B, s.L, s.H, s.N, s.P, s.R, &sh, &sth, &syv);
     a.hs = sh;
     a.th0 = sth;
+    // the float32 walk reads the saved output before the gate (the chunk-parallel
+    // route and bf16 recompute it)
+    if (s.z && !bf16_io && bwd_walk(s.B, s.H)) a.yv = syv;
   } else {
     a.hs = base + w.hs;
     a.th0 = reinterpret_cast<float*>(base + w.th);
@@ -2382,7 +2431,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
 #define X(T, cs, n, p, r)                                                                                  \
   if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
     found = true;                                                                                          \
-    hipLaunchKernelGGL((scan_bwd_walk_kernel<T, cs, n, p, r>), grid_bh, dim3(kBwdThreads), 0, st, a);      \
+    launch_walk<T, cs, n, p, r>(grid_bh, st, a);                                                           \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
     if (a.dqh) {                                                                                           \
       hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \

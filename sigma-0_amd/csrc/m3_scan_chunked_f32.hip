@@ -138,7 +138,8 @@ struct __attribute__((aligned(16))) Smem {
 // SO (state only): the pass that produces each segment's exit carry from a zero
 // entering carry; it skips Q, Y_diag, Y_off, the gate and the output.
 // SAVE (full pass): also write each chunk's entering state and angles (chunk_h,
-// chunk_th), the residuals the backward reads instead of running the state-only pass.
+// chunk_th), the residuals the backward reads instead of running the state-only pass,
+// and with Z the output before the gate (out_v).
 template <typename T, int CS, int N, int P, int R, int NW, bool SO, bool SAVE = false>
 __global__ __launch_bounds__(64 * NW, 1)
 void scan_chunked_f32_kernel(ScanArgs a) {
@@ -285,6 +286,11 @@ void scan_chunked_f32_kernel(ScanArgs a) {
         yc.to_f(oc);
 #pragma unroll
         for (int q = 0; q < 8; ++q) o[q] += oc[q];
+      }
+      if constexpr (SAVE) {
+        // the training forward: the output before the gate, for the backward's dZ
+        if (has_z && a.out_v)
+          store8(reinterpret_cast<T*>(a.out_v) + (o_base - gO) + (long)(c * CS + erow) * v_stride + 8 * egrp, o);
       }
       if (has_z) {
         float zf[8];

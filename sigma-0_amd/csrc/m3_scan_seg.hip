@@ -170,8 +170,9 @@ hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStrea
   p1.fin_h = loc.h; p1.fin_k = loc.k; p1.fin_v = loc.v; p1.fin_theta = a.R > 0 ? loc.th : nullptr;
   p1.fin_logdec = loc.ld;
   p1.fin_per_seg = 1;
-  p1.chunk_h = nullptr;                              // the saved chunk states come from pass 3
+  p1.chunk_h = nullptr;                              // the saved residuals come from pass 3
   p1.chunk_th = nullptr;
+  p1.out_v = nullptr;
   p1.CS = 64;
   hipError_t e = scan_state_launch(p1, bf16_io, st);
   if (e != hipSuccess) return e;

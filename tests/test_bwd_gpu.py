@@ -94,10 +94,13 @@ def test_gradients_without_d_and_z(bwd_route):
 
 
 def test_autograd_matches_functional_backward_and_is_deterministic(bwd_route):
-    """mamba3_siso_hip under torch autograd (the custom_vjp) gives the functional
-    backward's gradients, bitwise, on repeated calls."""
+    """mamba3_siso_hip under torch autograd (the custom_vjp, which runs the training
+    pair) gives the functional training pair's gradients, bitwise, and the functional
+    backward is bitwise repeatable; the recomputing backward agrees within rounding
+    (the reverse walk's training-pair variant forms dZ from the saved output before
+    the gate and is compiled apart, so its float contractions may differ)."""
     torch = _torch()
-    from mamba3_rocm import mamba3_siso_hip, mamba3_siso_hip_bwd
+    from mamba3_rocm import mamba3_siso_hip, mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
     B, L, H, N, P, R = 1, 140, 2, 128, 64, 32
     d = I.scan_inputs(B, L, H, N, P, R, seed=35, bf16=True)
     t = to_dev(d, torch.bfloat16)
@@ -106,12 +109,16 @@ def test_autograd_matches_functional_backward_and_is_deterministic(bwd_route):
     leaves = {k: t[k].clone().requires_grad_(True) for k in names}
     y = mamba3_siso_hip(*(leaves[k] for k in names), chunk_size=64)
     y.backward(cot)
-    g1 = mamba3_siso_hip_bwd(*(t[k] for k in names), cot, chunk_size=64)
-    g2 = mamba3_siso_hip_bwd(*(t[k] for k in names), cot, chunk_size=64)
+    _, saved = mamba3_siso_hip_fwd_train(*(t[k] for k in names), chunk_size=64)
+    g1 = mamba3_siso_hip_bwd(*(t[k] for k in names), cot, chunk_size=64, saved=saved)
+    g2 = mamba3_siso_hip_bwd(*(t[k] for k in names), cot, chunk_size=64, saved=saved)
+    g3 = mamba3_siso_hip_bwd(*(t[k] for k in names), cot, chunk_size=64)
     torch.cuda.synchronize()
-    for k, a, b in zip(names, g1, g2):
+    for k, a, b, c in zip(names, g1, g2, g3):
         assert torch.equal(a, b), f"d{k} differs between two calls"
         assert torch.equal(leaves[k].grad.to(a.dtype), a), f"autograd d{k} differs"
+        ca, cc = a.float().cpu().numpy(), c.float().cpu().numpy()
+        assert rel(ca, cc) <= 1e-2, (f"d{k}: training pair vs recompute", rel(ca, cc))
 
 
 @pytest.mark.parametrize("B,L,H,Hqk,N,P,R,bf16", [
@@ -139,7 +146,10 @@ def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_rout
     same kernel code (bf16 one pass; float32 at d_state 128, whose state pass is the
     float32 kernel's), within rounding where the forward's states come from another
     kernel (float32 at d_state 64, the split), and within the bars against the
-    oracle."""
+    oracle.  On the reverse walk's route the comparison is within rounding: its
+    training-pair variant forms dZ from the saved output before the gate (the
+    reference's Out_v residual, in the I/O type) where the recompute forms it from its
+    own float32 product, and it is compiled apart."""
     torch = _torch()
     from mamba3_rocm import mamba3_siso_hip, mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
     from mamba3_rocm import _lib
@@ -163,13 +173,47 @@ def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_rout
     g_re = mamba3_siso_hip_bwd(*args, dout, chunk_size=64)
     torch.cuda.synchronize()
     _, ref = V.vjp(d, cot, 16)
-    exact = (bf16 and not split) or (not bf16 and N == 128)
+    # bitwise on the chunk-parallel route; the reverse walk's training-pair variant is
+    # compiled apart (dZ from the saved output before the gate), so within rounding
+    exact = ((bf16 and not split) or (not bf16 and N == 128)) and bwd_route == "chunks"
     for name, a, b, r in zip(V.NAMES, g_saved, g_re, ref):
         if r is None:
             continue
         a, b = a.float().cpu().numpy(), b.float().cpu().numpy()
-        if exact:
+        if exact and name != "Z":
             assert np.array_equal(a, b), f"d{name}: saved-state backward differs from the recompute"
         else:
             assert rel(a, b) <= (1e-2 if bf16 else 1e-5), (name, rel(a, b))
+        assert rel(a, r) <= (BF16_TOL if bf16 else F32_TOL), (name, rel(a, r))
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_training_pair_without_z(bf16, bwd_route):
+    """Without Z the training forward saves no output before the gate and the backward
+    from its residuals gives the recompute's gradients (dZ None)."""
+    torch = _torch()
+    from mamba3_rocm import mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
+    B, L, H, N, P, R = 1, 150, 2, 128, 64, 32
+    d = I.scan_inputs(B, L, H, N, P, R, seed=43, bf16=bf16)
+    cot = V.cotangent(B, L, H, P, seed=44)
+    tdt = torch.bfloat16 if bf16 else torch.float32
+    if bf16:
+        cot = I.bf16_round(cot)
+    print(f"case training pair without Z bf16={bf16}", flush=True)
+    t = to_dev(d, tdt)
+    t["Z"] = None
+    args = tuple(t[k] for k in V.NAMES)
+    out_tr, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=64)
+    assert saved is not None
+    dout = torch.from_numpy(np.ascontiguousarray(cot)).to("cuda").to(tdt)
+    g_saved = mamba3_siso_hip_bwd(*args, dout, chunk_size=64, saved=saved)
+    g_re = mamba3_siso_hip_bwd(*args, dout, chunk_size=64)
+    torch.cuda.synchronize()
+    _, ref = V.vjp(d, cot, 16, no_z=True)
+    for name, a, b, r in zip(V.NAMES, g_saved, g_re, ref):
+        if r is None:
+            assert a is None and b is None, name
+            continue
+        a, b = a.float().cpu().numpy(), b.float().cpu().numpy()
+        assert np.array_equal(a, b), f"d{name}: saved-state backward differs from the recompute"
         assert rel(a, r) <= (BF16_TOL if bf16 else F32_TOL), (name, rel(a, r))

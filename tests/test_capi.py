@@ -143,16 +143,19 @@ def test_backward_workspace_sizes(lib, monkeypatch):
 
 def test_saved_state_sizes_and_validation(lib, monkeypatch):
     """The training pair: the residual buffer holds the chunk-entering states (io type)
-    and chunk angles (float32) of the backward's chunking; the saved-state backward's
-    workspace drops them; calls validate before any launch."""
+    and chunk angles (float32) of the backward's chunking and the output before the
+    gate (float32 I/O only, B x L x H x P); the saved-state backward's workspace
+    drops the states; calls validate before any launch."""
     monkeypatch.delenv("M3_BWD_ROUTE", raising=False)
     E_ARG, E_UNSUP = _header_define("M3_E_ARG"), _header_define("M3_E_UNSUPPORTED")
     al = lambda n: (n + 255) // 256 * 256  # noqa: E731
     bf, f32 = 1, 0
     sb = lib.m3_chunk_scan_saved_bytes
     assert sb(8, 4096, 32, 128, 64, 32, bf) == al(8 * 32 * 64 * 64 * 128 * 2) + al(8 * 32 * 64 * 32 * 4)
-    assert sb(2, 300, 4, 64, 32, 16, f32) == al(2 * 4 * 10 * 32 * 64 * 4) + al(2 * 4 * 10 * 16 * 4)
-    assert sb(8, 4096, 32, 128, 64, 32, f32) == al(8 * 32 * 128 * 64 * 128 * 4) + al(8 * 32 * 128 * 32 * 4)
+    assert sb(2, 300, 4, 64, 32, 16, f32) == (al(2 * 4 * 10 * 32 * 64 * 4) + al(2 * 4 * 10 * 16 * 4)
+                                              + al(2 * 300 * 4 * 32 * 4))
+    assert sb(8, 4096, 32, 128, 64, 32, f32) == (al(8 * 32 * 128 * 64 * 128 * 4) + al(8 * 32 * 128 * 32 * 4)
+                                                + al(8 * 4096 * 32 * 64 * 4))
     assert sb(1, 100, 2, 64, 16, 16, bf) == 0               # no backward kernel
     wsb = lib.m3_chunk_scan_bwd_saved_ws_bytes
     assert wsb(8, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, bf, True)
