@@ -94,11 +94,15 @@ def bwd_bytes(B, L, H, N, P, R, s_io):
     return B * L * H * ((2 * N + 3 * P) * s_io + 3 * 4 + R * 4 + (2 * N + 2 * P) * s_io + 3 * 4 + R * 4)
 
 
-def bwd_flops(B, L, H, N, P, CS):
+def bwd_flops(B, L, H, N, P, CS, saved_y=False):
     """Dense-tile MFMA FLOP count of one backward call, per token-head: the chunk's
     S = q~ k~^T, dP = dy v^T, y and dV (intra-chunk S v / S^T dy, inter-chunk q~ h and
     k~ G), the adjoint update dy^T q~, dq~ and dk~ (dP k~ + dy h, dP^T q~ + v G):
-    3 (2 CS N) + 3 (2 CS P) + 5 (2 P N)."""
+    3 (2 CS N) + 3 (2 CS P) + 5 (2 P N).  saved_y: the float32 training pair's
+    backward, which reads the output before the gate instead of forming y (one
+    2 CS P and one 2 P N term fewer)."""
+    if saved_y:
+        return B * L * H * (6 * CS * N + 4 * CS * P + 8 * P * N)
     return B * L * H * (6 * CS * N + 6 * CS * P + 10 * P * N)
 
 
@@ -202,8 +206,9 @@ def bench_bwd(torch, B, L, H, N, P, R, CS, steps, warmup, seed, io_dtype=None):
 
 def bench_train(torch, B, L, H, N, P, R, CS, steps, warmup, seed, io_dtype=None):
     """The training pair on the config's inputs: the forward that also writes the
-    backward's residuals (the state and rope angle entering every chunk) and the
-    backward that reads them instead of recomputing the chunk states -- the
+    backward's residuals (the state and rope angle entering every chunk and, float32,
+    the output before the gate) and the backward that reads them instead of
+    recomputing the chunk states and (float32) y -- the
     reference's mamba3_siso_fwd / mamba3_siso_bwd(saved, ...) (mamba3_ops.py:788-902).
     Each is timed on its own (HIP events), with an N(0, 1) output cotangent."""
     from mamba3_rocm import mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
@@ -223,7 +228,8 @@ def bench_train(torch, B, L, H, N, P, R, CS, steps, warmup, seed, io_dtype=None)
     return dict(fwd_s=kf, bwd_s=kb, wall_s=wf + wb, saved_bytes=saved.numel(),
                 fwd_gbs=fbytes / kf / 1e9, bwd_gbs=bbytes / kb / 1e9,
                 fwd_flops=scan_flops(B, L, H, N, P, bwd_chunk(torch, io_dtype)),
-                bwd_flops=bwd_flops(B, L, H, N, P, bwd_chunk(torch, io_dtype)))
+                bwd_flops=bwd_flops(B, L, H, N, P, bwd_chunk(torch, io_dtype),
+                                    saved_y=io_dtype == torch.float32 and args[10] is not None))
 
 
 def bench_shared(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
