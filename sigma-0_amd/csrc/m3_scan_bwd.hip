@@ -887,15 +887,16 @@ struct WalkLoads {
 // LDS of the walk.  The arrays live for the whole chunk except those in `u`, whose
 // members are used in three windows separated by barriers: (A) the Q/K staging tiles
 // (written at the top of the chunk, read in its preparation), (B) the masked S and the
-// dZ/dV output tiles (S/dP to the dZ/dV stores), (C) the bf16 residuals, the dq~ / dk~
-// results and the d(theta) output tile (the four dq~/dk~ passes).  Within (B) and (C)
-// the offsets keep apart what is live at the same time: lo is written while the
-// output tiles are still being stored, res while the dAngles tile is read.
-// float keeps the LDS of d_state 128 under the 160 KB limit with two more reuses:
-// Q and K rows are staged in qt / kt themselves (the preparation reads each thread's
-// own 8 raw elements and writes its q~ / k~ back to the same place), and window (C)
-// lives outside `u`: res in fz's storage and the d(theta) tile in the masked S's,
-// both dead after the y/dV phase.
+// dZ/dV output tiles (S/dP to the dZ/dV stores), (C) the tiles of the dq~/dk~ passes:
+// bf16 at d_state 128 two residual and two product tiles of the pipelined quarters
+// (the residual tiles outside the output tiles, so that the first two are written
+// while the dZ/dV rows are still being stored); other bf16 shapes the residual, the
+// dq~ / dk~ results and the d(theta) output tile, apart in the same way; float the
+// second product tile of its pipelined passes.  float keeps the LDS of d_state 128
+// under the 160 KB limit with two more reuses: Q and K rows are staged in qt / kt
+// themselves (the preparation reads each thread's own 8 raw elements and writes its
+// q~ / k~ back to the same place), and its first product tile lives in fz's storage,
+// dead after the y/dV phase.
 template <typename T, int CS, int N, int P, int R>
 struct WalkSmem {
   static constexpr bool BF = std::is_same<T, bf16>::value;
