@@ -1079,7 +1079,12 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   // bf16 outside the quarter passes (a barrier follows it): wave 0, measured 1%
   // faster there.
   constexpr int kDaWave = BF && !S::QP ? 0 : kBwdWaves - 1;
-  float cda = 0.0f, dsum = 0.0f;                       // wave kDaWave: dA over the later chunks; wave 0: dD
+  // the per-token d(scale) and dDT sums and stores, beside the dA's scan on another wave
+  constexpr int kDsWave = BF && !S::QP ? 0 : kBwdWaves - 2;
+  // the per-token q^.k^ sums and the D gradient, in the S/dP phase: float on a wave of
+  // the dP tiles (which have half the S tiles' MFMAs at 32-token chunks)
+  constexpr int kQkWave = BF ? 0 : kBwdWaves - 3;
+  float cda = 0.0f, dsum = 0.0f;                       // wave kDaWave: dA over the later chunks; kQkWave: dD
 
   // One register set of loads: chunk c's inputs are consumed by the end of its
   // preparation, and chunk c - 1's are requested in parts during the rest of chunk c.
@@ -1305,7 +1310,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       }
     }
     __syncthreads();
-    if (wave == 0) {
+    if (wave == kQkWave) {
       float qk = 0.0f;
       if (lane < CS) {
 #pragma unroll
@@ -1927,19 +1932,21 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 
     // ---- per token: dA (its reverse cumsum into dADT), d(gamma) into dDT, d(scale)
     // into the workspace
+    // (lane = token here; lanes CS.. hold no token)
+    if (wave == kDsWave && lane < nt) {
+      float ds = 0.0f;
+#pragma unroll
+      for (int w = 0; w < GH; ++w) ds += sm.ps[w][lane];
+      const long o = (long)bh * L + t0 + lane;
+      a.dsc[o] = ds;
+      a.ddt[o] = sm.dqk[lane] * sm.qk[lane] + ds;
+    }
     if (wave == kDaWave) {
-      // lane = token here (lanes CS.. hold no token)
       const bool ltok = lane < nt;
-      float da = 0.0f, ds = 0.0f;
+      float da = 0.0f;
       if (ltok) {
 #pragma unroll
-        for (int w = 0; w < GH; ++w) {
-          da += sm.pq[w][lane];
-          ds += sm.ps[w][lane];
-        }
-        const long o = (long)bh * L + t0 + lane;
-        a.dsc[o] = ds;
-        a.ddt[o] = sm.dqk[lane] * sm.qk[lane] + ds;
+        for (int w = 0; w < GH; ++w) da += sm.pq[w][lane];
       }
       const float f = wave_incl_scan(da);
       const float tot = lane63(f);
@@ -2005,7 +2012,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           if (r < R && tkn == 0) a.ctot[(long)bh * (R + 1) + 1 + r] = cth[hh][j];
         }
     }
-    if (wave == 0) {
+    if (wave == kQkWave) {
       const float tot = wave_sum(dsum);
       if (lane == 0 && a.pd) a.pd[bh] = tot;
     }
