@@ -137,6 +137,7 @@ def test_gradients_with_more_items_than_compute_units(B, L, H, Hqk, N, P, R, bf1
     (1, 1100, 3, 3, 128, 64, 32, True, True),     # the forward takes the sequence split
     (1, 150, 2, 2, 64, 32, 16, False, False),
     (1, 150, 2, 2, 128, 64, 32, False, False),
+    (2, 100, 4, 2, 128, 64, 64, False, False),    # float32 GQA, rope on every pair
 ])
 def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_route):
     """The training forward (the reference's mamba3_siso_fwd, which returns the
