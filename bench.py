@@ -14,8 +14,9 @@ Also reported on the same JSON line:
                 (oracle/, the reference's own JAX is not installed) timed on
                 the host on a bounded sample (one of the 8 sequences)
   secondary     decode state update (config 4, HBM GB/s), the long-context
-                scan (config 3), the shared-B/C scan, the float32-I/O scan, the scan
-                backward at config 2 (recomputing its chunk states) and the
+                scan (config 3), the shared-B/C scan and its backward (recomputing,
+                and the training pair), the float32-I/O scan, the scan backward at
+                config 2 and at config 3's shape (recomputing its chunk states) and the
                 training pair (forward with residuals, backward from them), with bf16
                 and with float32 I/O (what the model's training hands the scan),
                 each with its own roofline, and the 12-layer backbone prefill with
@@ -28,7 +29,7 @@ launches of a process); the JSON line reports this as ``clock_settle``, apart fr
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-secondary]
-                       [--mode scan|decode|long|bwd|train|shared|layer|stack|copy|fp32]
+                       [--mode scan|decode|long|bwd|train|shared|shared_bwd|layer|stack|copy|fp32]
                        [--io bf16|f32]   (--mode bwd / train)
        python bench.py --mode traffic --pmc-dir DIR   (writes the traffic JSON of
                        the headline kernel from rocprofv3 --pmc FETCH_SIZE /
@@ -95,7 +96,9 @@ def bwd_bytes(B, L, H, N, P, R, s_io):
 
 
 def bwd_flops(B, L, H, N, P, CS, saved_y=False):
-    """Dense-tile MFMA FLOP count of one backward call, per token-head: the chunk's
+    """Dense-tile MFMA FLOP count of one backward call at the kernel's chunk CS (the
+    MFMA work the kernel executes: the intra-chunk tiles are counted whole, as in the
+    forward's dense-tile formula), per token-head: the chunk's
     S = q~ k~^T, dP = dy v^T, y and dV (intra-chunk S v / S^T dy, inter-chunk q~ h and
     k~ G), the adjoint update dy^T q~, dq~ and dk~ (dP k~ + dy h, dP^T q~ + v G):
     3 (2 CS N) + 3 (2 CS P) + 5 (2 P N).  saved_y: the float32 training pair's
@@ -180,7 +183,7 @@ def bench_scan(torch, B, L, H, N, P, R, CS, steps, warmup, seed, settle=False, i
     wall, kern = time_calls(torch, fn, steps, warmup)
     nbytes = scan_bytes(B, L, H, N, P, R, args[0].element_size())
     return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, flops=scan_flops(B, L, H, N, P, CS),
-                achieved_gbs=nbytes / kern / 1e9, settle=settled)
+                flops32=scan_flops(B, L, H, N, P, min(CS, 32)), achieved_gbs=nbytes / kern / 1e9, settle=settled)
 
 
 def bwd_chunk(torch, io_dtype):
@@ -242,6 +245,41 @@ def bench_shared(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
     wall, kern = time_calls(torch, fn, steps, warmup)
     nbytes = shared_bytes(B, L, H, N, P, R, 2)
     return dict(wall_s=wall, kernel_s=kern, bytes=nbytes, achieved_gbs=nbytes / kern / 1e9)
+
+
+def _shared_inputs(torch, B, L, H, N, P, R, seed, io_dtype):
+    Q, K, V, ADT, DT, Trap, Qb, Kb, Ang, D, Z = make_scan_inputs(torch, B, L, H, N, P, R, seed, io_dtype)
+    return (Q[:, :, 0].contiguous(), K[:, :, 0].contiguous(), V, ADT, DT, Trap, Ang[:, :, 0].contiguous(),
+            Qb, Kb, D, Z)
+
+
+def shared_bwd_bytes(B, L, H, N, P, R, s_io):
+    """Algorithmic HBM bytes of one backward call of the fused path's contract: the
+    forward's inputs and dOut read once, every gradient written once, with Q, K, the
+    angle rates and their gradients once per token (shared over heads)."""
+    return (B * L * (2 * N * s_io + R * 4) * 2
+            + B * L * H * ((3 * P * s_io + 3 * 4) + (2 * P * s_io + 3 * 4)))
+
+
+def bench_shared_bwd(torch, B, L, H, N, P, R, CS, steps, warmup, seed):
+    """The fused path's backward at config 2 (shared Q, K and angle rates): the
+    recomputing backward, and the training pair (forward with residuals, backward
+    from them), each timed on its own with an N(0, 1) output cotangent."""
+    from mamba3_rocm import mamba3_ssd_chunked_shared_hip_bwd, mamba3_ssd_chunked_shared_hip_fwd_train
+    args = _shared_inputs(torch, B, L, H, N, P, R, seed, torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1000)
+    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(torch.bfloat16)
+    _, saved = mamba3_ssd_chunked_shared_hip_fwd_train(*args, chunk_size=CS)
+    bwd = lambda: mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=CS)  # noqa: E731
+    fwd_tr = lambda: mamba3_ssd_chunked_shared_hip_fwd_train(*args, chunk_size=CS)  # noqa: E731
+    bwd_sv = lambda: mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=CS, saved=saved)  # noqa: E731
+    wb, kb = time_calls(torch, bwd, steps, warmup)
+    wf, kf = time_calls(torch, fwd_tr, steps, warmup)
+    ws, ks = time_calls(torch, bwd_sv, steps, warmup)
+    nbytes = shared_bwd_bytes(B, L, H, N, P, R, 2)
+    return dict(bwd_s=kb, bwd_wall_s=wb, fwd_train_s=kf, bwd_saved_s=ks, pair_wall_s=wf + ws, bytes=nbytes,
+                saved_bytes=saved.numel())
 
 
 def bench_layer(torch, B, L, d_model, steps, warmup, seed):
@@ -442,16 +480,36 @@ def write_traffic(pmc_dir, kernel_avg_us=None):
     print(json.dumps(d), flush=True)
 
 
-def bwd_line(r, fp32=False):
+FLOP_COUNT_NOTE = ("dense-tile MFMA FLOPs at the kernel's own chunk (32 tokens for float32 I/O): the "
+                   "matrix work the kernel executes, intra-chunk tiles counted whole")
+
+
+def bwd_line(r, fp32=False, tokens=8 * 4096):
     """The JSON fields of a backward measurement: time, tokens/s, and its roofline --
     HBM for bf16 I/O; float32 MFMA for float32 I/O, whose dense-tile MFMA work takes
     longer at the float32 peak than its bytes at the HBM peak."""
-    d = {"ms": round(r["kernel_s"] * 1e3, 4), "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
+    d = {"ms": round(r["kernel_s"] * 1e3, 4), "tokens_per_s": round(tokens / r["wall_s"], 1),
          "achieved_gbs": round(r["achieved_gbs"], 1), "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4)}
     if fp32:
         tf = r["flops"] / r["kernel_s"] / 1e12
-        d.update(bound="mfma_fp32", tflops=round(tf, 1), frac_mfma_fp32=round(tf / FP32_MFMA_PEAK_TFLOPS, 4))
+        d.update(bound="mfma_fp32", tflops=round(tf, 1), frac_mfma_fp32=round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                 flop_count=FLOP_COUNT_NOTE)
     return d
+
+
+def fp32_fwd_line(r):
+    """The float32-I/O forward's fields: its dense-tile FLOPs at the kernel's 32-token
+    chunk against the float32 MFMA peak, its bytes against HBM, and the fraction of
+    whichever roof binds (the longer of the two roofline times)."""
+    t_mfma = r["flops32"] / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+    t_hbm = r["bytes"] / (HBM_PEAK_GBS * 1e9)
+    bound = "mfma_fp32" if t_mfma >= t_hbm else "hbm"
+    tf = r["flops32"] / r["kernel_s"] / 1e12
+    return {"kernel_ms": round(r["kernel_s"] * 1e3, 4), "bound": bound,
+            "roofline_us": round(max(t_mfma, t_hbm) * 1e6, 1), "frac": round(max(t_mfma, t_hbm) / r["kernel_s"], 4),
+            "tflops": round(tf, 1), "frac_mfma_fp32": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "achieved_gbs": round(r["achieved_gbs"], 1), "frac_hbm": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4),
+            "flop_count": FLOP_COUNT_NOTE}
 
 
 def train_line(r, fp32=False):
@@ -467,13 +525,27 @@ def train_line(r, fp32=False):
     return d
 
 
+def shared_bwd_line(r):
+    """The fused path's backward fields: the recomputing backward and the training pair,
+    against the contract's algorithmic bytes (shared rows once per token)."""
+    return {"ms": round(r["bwd_s"] * 1e3, 4), "tokens_per_s": round(8 * 4096 / r["bwd_wall_s"], 1),
+            "achieved_gbs": round(r["bytes"] / r["bwd_s"] / 1e9, 1),
+            "frac_hbm": round(r["bytes"] / r["bwd_s"] / 1e9 / HBM_PEAK_GBS, 4),
+            "fwd_with_residuals_ms": round(r["fwd_train_s"] * 1e3, 4),
+            "bwd_from_residuals_ms": round(r["bwd_saved_s"] * 1e3, 4),
+            "pair_step_ms": round((r["fwd_train_s"] + r["bwd_saved_s"]) * 1e3, 4),
+            "pair_tokens_per_s": round(8 * 4096 / r["pair_wall_s"], 1),
+            "bwd_from_residuals_frac_hbm": round(r["bytes"] / r["bwd_saved_s"] / 1e9 / HBM_PEAK_GBS, 4),
+            "residual_bytes": r["saved_bytes"], "algorithmic_bytes": r["bytes"]}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "train", "shared", "layer", "stack", "copy",
-                                       "fp32", "traffic"), default="scan")
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "train", "shared", "shared_bwd", "layer",
+                                       "stack", "copy", "fp32", "traffic"), default="scan")
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
@@ -539,11 +611,12 @@ def main():
         # config 2's shape with float32 I/O (what the model hands the scan), for profiling
         r = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2,
                        io_dtype=torch.float32)
-        print(json.dumps({"mode": "fp32", "kernel_ms": round(r["kernel_s"] * 1e3, 4),
-                          "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
-                          "tflops": round(r["flops"] / r["kernel_s"] / 1e12, 1),
-                          "frac_mfma_fp32": round(r["flops"] / r["kernel_s"] / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
-                          "achieved_gbs": round(r["achieved_gbs"], 1)}), flush=True)
+        print(json.dumps({"mode": "fp32", "tokens_per_s": round(8 * 4096 / r["wall_s"], 1), **fp32_fwd_line(r)}),
+              flush=True)
+        return
+    if args.mode == "shared_bwd":
+        r = bench_shared_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2)
+        print(json.dumps({"mode": "shared_bwd", **shared_bwd_line(r)}), flush=True)
         return
     if args.mode == "long":
         # config 3 alone (B*H = 32: the sequence split runs), for profiling
@@ -592,6 +665,8 @@ def main():
         tr32 = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 10), 2, seed=2,
                            io_dtype=torch.float32)
         sh = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
+        shb = bench_shared_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
+        bw3 = bench_bwd(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 10), 2, seed=3)
         f32 = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2,
                          io_dtype=torch.float32)
         bb = bench_stack(torch, 4, 12288, 768, 12, 2112, 5, 2, seed=5)
@@ -611,14 +686,12 @@ def main():
                                   "tokens_per_s": round(8 * 4096 / sh["wall_s"], 1),
                                   "achieved_gbs": round(sh["achieved_gbs"], 1),
                                   "frac_hbm": round(sh["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "shared_bc_backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **shared_bwd_line(shb)},
             "fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",
-                                "kernel_ms": round(f32["kernel_s"] * 1e3, 4),
-                                "tokens_per_s": round(8 * 4096 / f32["wall_s"], 1),
-                                "bound": "mfma_fp32", "tflops": round(f32["flops"] / f32["kernel_s"] / 1e12, 1),
-                                "frac_mfma_fp32": round(f32["flops"] / f32["kernel_s"] / 1e12
-                                                        / FP32_MFMA_PEAK_TFLOPS, 4),
-                                "achieved_gbs": round(f32["achieved_gbs"], 1)},
+                                "tokens_per_s": round(8 * 4096 / f32["wall_s"], 1), **fp32_fwd_line(f32)},
             "backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **bwd_line(bw)},
+            "backward_config3_shape": {"B": 1, "L": 32768, "H": 32, "chunk": 128,
+                                       **bwd_line(bw3, tokens=32768)},
             "training_pair_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **train_line(tr)},
             "backward_fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",
                                          **bwd_line(bw32, fp32=True)},

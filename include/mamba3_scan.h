@@ -121,7 +121,9 @@ int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
 /*
  * m3_chunk_scan_fwd_ws without the workspace argument: the split's scratch is a
  * device array of 17 MiB that the library holds for the life of the process, one
- * copy per GPU (its address is looked up on the first call on each device).  No
+ * copy per GPU (its address is looked up on the first call with a stream of that
+ * device, NULL meaning the current device; a failed lookup is reported and tried
+ * again on the next call; make the first call on each device outside graph capture).  No
  * counterpart in the reference: this entry point is for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It allocates nothing and calls no allocating routine.  Shapes whose
@@ -246,6 +248,35 @@ int m3_chunk_scan_bwd_shared(const void* Q, const void* K, const void* V,
                              float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
                              int B, int L, int H, int N, int P, int R,
                              int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * The training pair of the fused path's contract: m3_chunk_scan_fwd_train and
+ * m3_chunk_scan_bwd_saved with Q, K (B,L,N) and the angle rates (B,L,R) shared over
+ * heads, as m3_chunk_scan_fwd_shared / m3_chunk_scan_bwd_shared take them.  The
+ * reference's fused chunk scan saves its residuals, the per-chunk states entering
+ * each chunk among them, for its backward (chunk_scan_fwd_rule / chunk_scan_bwd_rule,
+ * src/base_model/models/mamba3_pallas.py:602-645).  The residual buffer is
+ * m3_chunk_scan_saved_bytes of the shape (per (batch, head), as without sharing);
+ * the backward's workspace is m3_chunk_scan_bwd_saved_shared_ws_bytes.
+ */
+int m3_chunk_scan_fwd_train_shared(const void* Q, const void* K, const void* V,
+                                   const float* ADT, const float* DT, const float* Trap,
+                                   const float* Q_bias, const float* K_bias, const float* Angles,
+                                   const float* D, const void* Z, void* Out,
+                                   int B, int L, int H, int N, int P, int R,
+                                   int chunk_size, int io_dtype, void* saved, size_t saved_bytes,
+                                   void* ws, size_t ws_bytes, void* stream);
+size_t m3_chunk_scan_bwd_saved_shared_ws_bytes(int B, int L, int H, int N, int P, int R, int chunk_size,
+                                               int io_dtype);
+int m3_chunk_scan_bwd_saved_shared(const void* Q, const void* K, const void* V,
+                                   const float* ADT, const float* DT, const float* Trap,
+                                   const float* Q_bias, const float* K_bias, const float* Angles,
+                                   const float* D, const void* Z, const void* dOut,
+                                   void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                                   float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                                   int B, int L, int H, int N, int P, int R,
+                                   int chunk_size, int io_dtype, const void* saved, size_t saved_bytes,
+                                   void* ws, size_t ws_bytes, void* stream);
 
 /*
  * One decode step for a batch, in place on the carry.  Replaces the body of

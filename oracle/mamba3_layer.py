@@ -74,6 +74,21 @@ def init_params(d_model, seed, d_state=128, expand=2, headdim=64, rope_fraction=
     return p
 
 
+def split_proj(proj, di, N, nh):
+    """The in_proj output split [z, x, B, C, dd_dt, dd_A, trap, angles] along the last
+    axis, widths [di, di, N, N, nh, nh, nh, R] (mamba3.py:212-219)."""
+    cut = np.cumsum([di, di, N, N, nh, nh, nh])
+    return np.split(proj, cut, axis=-1)
+
+
+def decay(dd_dt, dd_A, dt_bias, A_floor):
+    """(A, DT): A = clip(-softplus(dd_A), max=-A_floor), DT = softplus(dd_dt + dt_bias)
+    (mamba3.py:251-254)."""
+    A = np.minimum(-softplus(dd_A), -A_floor)
+    DT = softplus(dd_dt + dt_bias)
+    return A, DT
+
+
 def layer_forward(p, x, d_state=128, headdim=64, rope_fraction=0.5, A_floor=1e-4, chunk_size=64,
                   bf16=False):
     """Mamba3SSM.__call__ on x (B, L, d_model) -> (B, L, d_model), float64 math."""
@@ -85,12 +100,10 @@ def layer_forward(p, x, d_state=128, headdim=64, rope_fraction=0.5, A_floor=1e-4
     di = nh * hd
     xin = r(x)
     proj = r(xin @ r(p["in_proj"]))                                     # in_proj (mamba3.py:210)
-    cut = np.cumsum([di, di, N, N, nh, nh, nh])
-    z, xv, Bm, Cm, dd_dt, dd_A, trap, ang = np.split(proj, cut, axis=-1)  # :212-219
+    z, xv, Bm, Cm, dd_dt, dd_A, trap, ang = split_proj(proj, di, N, nh)  # :212-219
     Bn = r(rmsnorm(Bm, p["B_norm"]))                                    # BCNorm, :240-242
     Cn = r(rmsnorm(Cm, p["C_norm"]))
-    A = np.minimum(-softplus(dd_A), -A_floor)                          # :251-254
-    DT = softplus(dd_dt + p["dt_bias"])
+    A, DT = decay(dd_dt, dd_A, p["dt_bias"], A_floor)                   # :251-254
     ADT = A * DT
     ang_rep = np.repeat(ang[:, :, None, :], nh, axis=2)                 # (B, L, nh, R)
     y = M.mamba3_ssd_chunked_batched(

@@ -53,7 +53,7 @@ bool decode_supported(int N, int P, int R) {
 
 extern "C" {
 
-int m3_abi_version(void) { return 100; }
+int m3_abi_version(void) { return 101; }
 
 const char* m3_last_error(void) { return g_err; }
 
@@ -193,23 +193,37 @@ __device__ __align__(256) char scratch[kNoallocScratchBytes];
 
 namespace {
 constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
-hipError_t g_scratch_err[kMaxDevices];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];   // null until a lookup on that device succeeded
 
-// The array's device address on the current device, looked up once per device with
-// that device current (each GPU holds its own copy at its own address).
-int scratch_on_current_device(void** ptr) {
+// The array's device address on the device that `stream` belongs to (the current
+// device for the null stream), looked up with that device current (each GPU holds
+// its own copy at its own address).  Only a successful lookup is kept: a failed one
+// is reported and tried again on the next call.  The first call on a device looks
+// the address up, so it must not be made under stream capture.
+int scratch_for_stream(hipStream_t stream, void** ptr) {
   int dev = -1;
-  const hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(M3_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(M3_E_LAUNCH, "device of the stream: %s", hipGetErrorString(e));
   if (dev < 0 || dev >= kMaxDevices) return fail(M3_E_ARG, "device %d beyond the %d supported", dev, kMaxDevices);
-  std::call_once(g_scratch_once[dev], [dev] {
-    g_scratch_err[dev] = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(m3::scratch));
-  });
-  if (g_scratch_err[dev] != hipSuccess)
-    return fail(M3_E_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
-                hipGetErrorString(g_scratch_err[dev]));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return fail(M3_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(M3_E_LAUNCH, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(m3::scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess && e2 != hipSuccess)
+        return fail(M3_E_LAUNCH, "hipSetDevice(%d): %s", cur, hipGetErrorString(e2));
+    }
+    if (e != hipSuccess)
+      return fail(M3_E_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
   *ptr = g_scratch_ptr[dev];
   return M3_OK;
 }
@@ -232,7 +246,7 @@ int m3_chunk_scan_fwd_noalloc(const void* Q, const void* K, const void* V,
                 "takes a workspace of any size)", need, m3::kNoallocScratchBytes);
   void* ws = nullptr;
   if (need > 0) {
-    const int rc = scratch_on_current_device(&ws);
+    const int rc = scratch_for_stream(reinterpret_cast<hipStream_t>(stream), &ws);
     if (rc != M3_OK) return rc;
   }
   return scan_fwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, init_theta, init_ssm, init_k, init_v,
@@ -406,6 +420,41 @@ int m3_chunk_scan_bwd_shared(const void* Q, const void* K, const void* V,
   return scan_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dOut, dQ, dK, dV, dADT, dDT, dTrap,
                   dQ_bias, dK_bias, dAngles, dD, dZ, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes,
                   stream, true);
+}
+
+int m3_chunk_scan_fwd_train_shared(const void* Q, const void* K, const void* V,
+                                   const float* ADT, const float* DT, const float* Trap,
+                                   const float* Q_bias, const float* K_bias, const float* Angles,
+                                   const float* D, const void* Z, void* Out,
+                                   int B, int L, int H, int N, int P, int R,
+                                   int chunk_size, int io_dtype, void* saved, size_t saved_bytes,
+                                   void* ws, size_t ws_bytes, void* stream) {
+  if (saved == nullptr) return fail(M3_E_ARG, "NULL saved-state buffer");
+  return scan_fwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, Out, nullptr, nullptr, nullptr, nullptr,
+                  nullptr, nullptr, nullptr, nullptr, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes,
+                  stream, true, 0, 0, saved, saved_bytes);
+}
+
+size_t m3_chunk_scan_bwd_saved_shared_ws_bytes(int B, int L, int H, int N, int P, int R, int chunk_size,
+                                               int io_dtype) {
+  if ((io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16) || B <= 0 || L <= 0 || H <= 0 || chunk_size <= 0)
+    return 0;
+  return m3::scan_bwd_ws_bytes(io_dtype == M3_DTYPE_BF16, B, L, H, 1, N, P, R, true, true);
+}
+
+int m3_chunk_scan_bwd_saved_shared(const void* Q, const void* K, const void* V,
+                                   const float* ADT, const float* DT, const float* Trap,
+                                   const float* Q_bias, const float* K_bias, const float* Angles,
+                                   const float* D, const void* Z, const void* dOut,
+                                   void* dQ, void* dK, void* dV, float* dADT, float* dDT, float* dTrap,
+                                   float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
+                                   int B, int L, int H, int N, int P, int R,
+                                   int chunk_size, int io_dtype, const void* saved, size_t saved_bytes,
+                                   void* ws, size_t ws_bytes, void* stream) {
+  if (saved == nullptr) return fail(M3_E_ARG, "NULL saved-state buffer");
+  return scan_bwd(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z, dOut, dQ, dK, dV, dADT, dDT, dTrap,
+                  dQ_bias, dK_bias, dAngles, dD, dZ, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes,
+                  stream, true, saved, saved_bytes);
 }
 
 int m3_decode_step(float* theta, float* ssm, float* k, float* v,

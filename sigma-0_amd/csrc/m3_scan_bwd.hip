@@ -11,19 +11,33 @@
 //   dk~_s = sum_{t>s} e^{A_t - A_s} (dy_t . v_s) q~_t
 //   dA_t  = q~_t . dq~_t - k~_t . dk~_t,   dadt = reverse cumsum of dA
 //
-// and the chain through rope, bias, trapezoid weights and the angle cumsum.  Four
-// launches per call:
-//   1. the chunked kernel's state-only pass saves the state entering every chunk
-//      h_c and the rope angle entering it (scan_state_launch with chunk_h/chunk_th);
-//   2. scan_adjoint_kernel walks each (b, h) backwards and saves the adjoint state
-//      G_c = sum_{t after chunk c} e^{A_t - A_end(c)} dy_t (x) q~_t of every chunk;
-//   3. scan_bwd_chunk_kernel, one workgroup per (chunk, b, h), computes the chunk's
-//      terms from h_c and G_c on MFMA: dZ, dV, dQ, dK, and per token dA, d(theta),
-//      d(scale), d(gamma) (kept in the dADT, dAngles, dTrap, dDT outputs);
-//   4. scan_bwd_finish_kernel turns those into dADT, dAngles, dDT, dTrap (reverse
-//      cumsums over the sequence, the trapezoid and angle chains), and
-//      scan_bwd_reduce_kernel sums the bias and D gradients over batch and chunks.
-// Every sum runs in a fixed order, so the gradients are deterministic.
+// and the chain through rope, bias, trapezoid weights and the angle cumsum.  The
+// chunk-level form needs, for every chunk c, the state h_c entering it and the
+// adjoint state G_c = sum_{t after chunk c} e^{A_t - A_end(c)} dy_t (x) q~_t after it.
+// h_c and the rope angle entering chunk c come from the chunked kernel's state-only
+// pass (scan_state_launch with chunk_h/chunk_th) or, in the training pair, from the
+// training forward's residuals.  Then one of two routes, picked by B*H (bwd_walk):
+//
+// * The reverse walk (B*H >= 80: one workgroup per (b, h) fills the chip).
+//   scan_bwd_walk_kernel walks each (b, h) from its last chunk to its first with
+//   G in MFMA accumulators for the whole walk; per chunk it forms S and dP, y (for
+//   dZ) and dV, advances G, then runs the dq~/dk~ passes (software-pipelined:
+//   products of one column block beside the chain rule of the previous) and the
+//   per-token dA.  It carries the reverse cumsums of dA and d(theta) from chunk to
+//   chunk and sums the bias and D gradients over the walk.
+//   scan_bwd_walk_finish_kernel then applies the trapezoid and angle chains and
+//   the blend of the reverse and forward sums to dADT, dAngles, dDT and dTrap,
+//   and scan_bwd_reduce_kernel sums the bias and D partials over the batch.
+// * The chunk-parallel route (few (b, h) pairs).  scan_adjoint_kernel walks each
+//   (b, h) backwards and saves every G_c; scan_bwd_chunk_kernel, one workgroup per
+//   (chunk, b, h), computes the chunk's terms from h_c and G_c on MFMA: dZ, dV, dQ,
+//   dK, and per token dA, d(theta), d(scale), d(gamma) (kept in the dADT, dAngles,
+//   dTrap, dDT outputs); scan_bwd_finish_kernel turns those into dADT, dAngles, dDT,
+//   dTrap (reverse cumsums over the sequence, the trapezoid and angle chains), and
+//   scan_bwd_reduce_kernel sums the bias and D gradients over batch and chunks.
+// With Q/K shared over heads (GQA, the fused path) the per-head dQ/dK and dAngles
+// are summed by scan_bwd_gqa_kernel and scan_bwd_angle_heads_kernel.  Every sum runs
+// in a fixed order, so the gradients are deterministic.
 #include <stdlib.h>
 #include <string.h>
 

@@ -29,6 +29,8 @@ EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_sc
            "m3_chunk_scan_bwd_ws_bytes", "m3_chunk_scan_bwd", "m3_chunk_scan_fwd_shared",
            "m3_chunk_scan_bwd_shared_ws_bytes", "m3_chunk_scan_bwd_shared", "m3_chunk_scan_saved_bytes",
            "m3_chunk_scan_fwd_train", "m3_chunk_scan_bwd_saved_ws_bytes", "m3_chunk_scan_bwd_saved",
+           "m3_chunk_scan_fwd_train_shared", "m3_chunk_scan_bwd_saved_shared_ws_bytes",
+           "m3_chunk_scan_bwd_saved_shared",
            "m3_decode_step",
            "m3_layer_pre", "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu", "m3_block_act", "m3_block_act_norm",
            "m3_log_softmax")
@@ -53,6 +55,9 @@ _SIGS = {
     "m3_chunk_scan_fwd_train": ([_P] * 12 + [_I] * 9 + [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P], _I),
     "m3_chunk_scan_bwd_saved_ws_bytes": ([_I] * 9, ctypes.c_size_t),
     "m3_chunk_scan_bwd_saved": ([_P] * 23 + [_I] * 9 + [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P], _I),
+    "m3_chunk_scan_fwd_train_shared": ([_P] * 12 + [_I] * 8 + [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P], _I),
+    "m3_chunk_scan_bwd_saved_shared_ws_bytes": ([_I] * 8, ctypes.c_size_t),
+    "m3_chunk_scan_bwd_saved_shared": ([_P] * 23 + [_I] * 8 + [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P], _I),
     "m3_layer_pre": ([_P] * 12 + [_I] * 6 + [ctypes.c_float, ctypes.c_float, _I, _P], _I),
     "m3_layer_scan": ([_P] * 3 + [_I] + [_P] * 8 + [_I] * 8 + [_P, ctypes.c_size_t, _P], _I),
     "m3_layer_post": ([_P] * 3 + [_I] * 3 + [ctypes.c_float, _I, _P], _I),

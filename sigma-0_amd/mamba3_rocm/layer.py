@@ -23,7 +23,7 @@ from typing import Dict
 import torch
 
 from . import _lib
-from .ops import _IO, _ptr, _stream, mamba3_ssd_chunked_shared_hip
+from .ops import _IO, _ptr, _stream, mamba3_ssd_chunked_shared_hip, pallas_compute_dtype
 
 PARAM_NAMES = ("in_proj", "dt_bias", "B_bias", "C_bias", "B_norm", "C_norm", "D", "out_norm", "out_proj")
 
@@ -60,6 +60,7 @@ class Mamba3Layer:
         self.w_in = self.params["in_proj"].to(dtype).contiguous()
         self.w_out = self.params["out_proj"].to(dtype).contiguous()
         self.last_scan = None      # "in_place" or "copies": how the last forward fed x and z to the scan
+        self.last_compute_dtype = None   # the scan's operand dtype in the last forward
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """x (B, L, d_model) or (L, d_model) -> the same shape, in the compute dtype."""
@@ -89,11 +90,15 @@ class Mamba3Layer:
         # Q = C, K = B (_forward_pallas, mamba3.py:413-425).  x and z are read in place
         # from proj when its rows and the x block are 16-byte aligned and the shape has
         # the chunked kernel (m3_layer_scan's conditions); otherwise they are copied.
+        # MAMBA3_PALLAS_DTYPE may ask for scan operands in another dtype than the
+        # layer's (mamba3_pallas.py:112-122, 838-839): then the copies are cast to it.
+        cdt = pallas_compute_dtype(dt)
         es = proj.element_size()
-        in_place = ((self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
+        in_place = (cdt == dt and (self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
                     and proj.data_ptr() % 16 == 0
                     and lib.m3_chunk_scan_impl(io, N, hd, R, self.chunk_size) == _lib.IMPL_CHUNKED_MFMA)
         self.last_scan = "in_place" if in_place else "copies"
+        self.last_compute_dtype = cdt
         if in_place:
             pre(None, None)
             y = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
@@ -108,7 +113,7 @@ class Mamba3Layer:
             Z = torch.empty_like(V)
             pre(V, Z)
             y = mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, Ang, pp["C_bias"], pp["B_bias"], pp["D"], Z,
-                                              chunk_size=self.chunk_size)
+                                              chunk_size=self.chunk_size, compute_dtype=cdt)
         yn = torch.empty(B, L, self.d_inner, device=dev, dtype=dt)
         _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), B, L, self.d_inner, self.eps, io,
                                      _stream(y)), "m3_layer_post")

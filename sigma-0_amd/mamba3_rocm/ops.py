@@ -44,6 +44,23 @@ def mamba3_contraction_precision_mode() -> str:
     return mode
 
 
+_DTYPE_NAMES = {"float32": torch.float32, "bfloat16": torch.bfloat16}
+
+
+def pallas_compute_dtype(default: torch.dtype = torch.float32) -> torch.dtype:
+    """The fused path's operand-dtype knob (src/base_model/models/mamba3_pallas.py:
+    112-122): MAMBA3_PALLAS_DTYPE ("float32" or "bfloat16") overrides; unset or
+    empty, the layer's compute dtype ``default`` decides; anything else raises
+    ValueError with the reference's message.  Read on every call, as there.  The
+    kernels here take their MFMA operands in the I/O dtype, so the shared-B/C entry
+    points cast Q, K, V and Z to this dtype (float32 accumulation either way) and
+    return the output in V's dtype."""
+    name = os.environ.get("MAMBA3_PALLAS_DTYPE") or {v: k for k, v in _DTYPE_NAMES.items()}.get(default, "")
+    if name not in _DTYPE_NAMES:
+        raise ValueError("MAMBA3_PALLAS_DTYPE must be float32 or bfloat16")
+    return _DTYPE_NAMES[name]
+
+
 def _req(cond: bool, msg: str) -> None:
     if not cond:
         raise ValueError(msg)
@@ -311,9 +328,10 @@ def mamba3_siso_hip_carry(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None
 
 
 # ----------------------------------------------------------------- shared B/C
-def _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z):
+def _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z, cdt=None):
     """Validate and normalise the fused path's layout: Q, K (B, L, N) and angle
-    rates (B, L, R), shared over the H heads of V (B, L, H, P)."""
+    rates (B, L, R), shared over the H heads of V (B, L, H, P); Q, K, V and Z in
+    the compute dtype cdt (default: pallas_compute_dtype of V's dtype)."""
     mamba3_contraction_precision_mode()
     unbatched = V.dim() == 3
     if unbatched:
@@ -341,38 +359,68 @@ def _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z):
         _req(tuple(D.shape) == (H,), f"D must be {(H,)}, got {tuple(D.shape)}")
     if Z is not None:
         _req(tuple(Z.shape) == (B, L, H, P), f"Z must be {(B, L, H, P)}, got {tuple(Z.shape)}")
-    dt = V.dtype
-    _req(dt in _IO, f"V dtype must be float32 or bfloat16, got {dt}")
-    p = dict(Q=Q.to(dt).contiguous(), K=K.to(dt).contiguous(), V=V.contiguous(), ADT=_f32(ADT), DT=_f32(DT),
+    _req(V.dtype in _IO, f"V dtype must be float32 or bfloat16, got {V.dtype}")
+    dt = cdt or pallas_compute_dtype(V.dtype)
+    p = dict(Q=Q.to(dt).contiguous(), K=K.to(dt).contiguous(), V=V.to(dt).contiguous(), ADT=_f32(ADT), DT=_f32(DT),
              Trap=_f32(Trap), Q_bias=_f32(Q_bias), K_bias=_f32(K_bias), Angles=_f32(angles),
              D=None if D is None else _f32(D), Z=None if Z is None else Z.to(dt).contiguous())
     return p, (B, L, H, N, P, R), unbatched
 
 
-def _shared_forward(args, chunk_size, seq_split):
-    p, (B, L, H, N, P, R), unbatched = _prep_shared(*args)
+def _shared_forward(args, chunk_size, seq_split, train=False, cdt=None):
+    """The fused path's forward; with ``train`` also the residuals of its backward
+    (None where the shape has no saved-state path).  Returns (out, saved), out in V's
+    dtype."""
+    p, (B, L, H, N, P, R), unbatched = _prep_shared(*args, cdt=cdt)
     out = torch.empty_like(p["V"])
+    saved = None
     if out.numel():
         lib = _lib.load()
         io = _IO[p["V"].dtype]
         ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, H, N, P, R, int(chunk_size), io) if seq_split else 0
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=p["V"].device)
-        rc = lib.m3_chunk_scan_fwd_shared(
-            _ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
-            _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(out),
-            B, L, H, N, P, R, int(chunk_size), io, ws.data_ptr() if ws_bytes else None, ws_bytes,
-            _stream(p["V"]))
-        _lib.check(rc, "m3_chunk_scan_fwd_shared")
-    return out[0] if unbatched else out
+        common = (_ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
+                  _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(out),
+                  B, L, H, N, P, R, int(chunk_size), io)
+        nbytes = lib.m3_chunk_scan_saved_bytes(B, L, H, N, P, R, io) if train else 0
+        kbwd = 64 if io == _lib.DTYPE_BF16 else 32
+        if nbytes and int(chunk_size) % kbwd == 0 and \
+                lib.m3_chunk_scan_impl(io, N, P, R, int(chunk_size)) == _lib.IMPL_CHUNKED_MFMA:
+            saved = torch.empty(nbytes, dtype=torch.uint8, device=p["V"].device)
+            rc = lib.m3_chunk_scan_fwd_train_shared(*common, saved.data_ptr(), nbytes,
+                                                    ws.data_ptr() if ws_bytes else None, ws_bytes, _stream(p["V"]))
+            _lib.check(rc, "m3_chunk_scan_fwd_train_shared")
+        else:
+            rc = lib.m3_chunk_scan_fwd_shared(*common, ws.data_ptr() if ws_bytes else None, ws_bytes,
+                                              _stream(p["V"]))
+            _lib.check(rc, "m3_chunk_scan_fwd_shared")
+    out = out.to(args[2].dtype)
+    return (out[0] if unbatched else out), saved
+
+
+def mamba3_ssd_chunked_shared_hip_fwd_train(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D=None, Z=None,
+                                            chunk_size: int = 64, seq_split: bool = True, compute_dtype=None):
+    """The fused path's forward with the residuals its backward reads (the state and
+    rope angle entering every chunk and, float32, the output before the gate), as
+    the reference's fused chunk scan saves them (chunk_scan_fwd_rule,
+    mamba3_pallas.py:602-604).  Returns (out, saved); saved is None where the shape
+    has no saved-state path."""
+    return _shared_forward((Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z), chunk_size, seq_split,
+                           train=True, cdt=compute_dtype)
 
 
 def mamba3_ssd_chunked_shared_hip_bwd(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z, dOut,
-                                      chunk_size: int = 64):
+                                      chunk_size: int = 64, saved: Optional[torch.Tensor] = None,
+                                      compute_dtype=None):
     """All eleven input gradients of mamba3_ssd_chunked_shared_hip, in its argument
     order (Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z); dQ, dK and dangles
-    are summed over heads (shaped like the shared inputs); dD, dZ None when absent."""
+    are summed over heads (shaped like the shared inputs); dD, dZ None when absent.
+    dQ, dK, dV and dZ come in the compute dtype.  ``saved``: the residuals of
+    mamba3_ssd_chunked_shared_hip_fwd_train on the same inputs (with the same compute
+    dtype); without them the chunk states are recomputed."""
     ang_in = angles
-    p, (B, L, H, N, P, R), unbatched = _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z)
+    p, (B, L, H, N, P, R), unbatched = _prep_shared(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z,
+                                                    cdt=compute_dtype)
     io = _IO[p["V"].dtype]
     dO = (dOut[None] if unbatched else dOut).to(p["V"].dtype).contiguous()
     _req(tuple(dO.shape) == (B, L, H, P), f"dOut must be {(B, L, H, P)}, got {tuple(dOut.shape)}")
@@ -385,17 +433,24 @@ def mamba3_ssd_chunked_shared_hip_bwd(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_
              Z=None if p["Z"] is None else torch.empty_like(p["Z"]))
     if B and L:
         lib = _lib.load()
-        ws_bytes = lib.m3_chunk_scan_bwd_shared_ws_bytes(B, L, H, N, P, R, int(chunk_size), io)
+        if saved is None:
+            ws_bytes = lib.m3_chunk_scan_bwd_shared_ws_bytes(B, L, H, N, P, R, int(chunk_size), io)
+        else:
+            ws_bytes = lib.m3_chunk_scan_bwd_saved_shared_ws_bytes(B, L, H, N, P, R, int(chunk_size), io)
         if ws_bytes == 0:
             raise _lib.Mamba3LibraryError(
                 f"no backward kernel for dtype={p['V'].dtype} d_state={N} headdim={P} rope angles={R}")
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        rc = lib.m3_chunk_scan_bwd_shared(
-            _ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
-            _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(dO),
-            _ptr(g["Q"]), _ptr(g["K"]), _ptr(g["V"]), _ptr(g["ADT"]), _ptr(g["DT"]), _ptr(g["Trap"]),
-            _ptr(g["Q_bias"]), _ptr(g["K_bias"]), _ptr(g["Angles"]), _ptr(g["D"]), _ptr(g["Z"]),
-            B, L, H, N, P, R, int(chunk_size), io, ws.data_ptr(), ws_bytes, _stream(p["V"]))
+        ptrs = (_ptr(p["Q"]), _ptr(p["K"]), _ptr(p["V"]), _ptr(p["ADT"]), _ptr(p["DT"]), _ptr(p["Trap"]),
+                _ptr(p["Q_bias"]), _ptr(p["K_bias"]), _ptr(p["Angles"]), _ptr(p["D"]), _ptr(p["Z"]), _ptr(dO),
+                _ptr(g["Q"]), _ptr(g["K"]), _ptr(g["V"]), _ptr(g["ADT"]), _ptr(g["DT"]), _ptr(g["Trap"]),
+                _ptr(g["Q_bias"]), _ptr(g["K_bias"]), _ptr(g["Angles"]), _ptr(g["D"]), _ptr(g["Z"]),
+                B, L, H, N, P, R, int(chunk_size), io)
+        if saved is None:
+            rc = lib.m3_chunk_scan_bwd_shared(*ptrs, ws.data_ptr(), ws_bytes, _stream(p["V"]))
+        else:
+            rc = lib.m3_chunk_scan_bwd_saved_shared(*ptrs, saved.data_ptr(), saved.numel(), ws.data_ptr(),
+                                                    ws_bytes, _stream(p["V"]))
         _lib.check(rc, "m3_chunk_scan_bwd_shared")
     else:
         for t in g.values():
@@ -412,36 +467,52 @@ def mamba3_ssd_chunked_shared_hip_bwd(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_
 
 class _Mamba3Shared(torch.autograd.Function):
     """mamba3_ssd_chunked_shared_hip with its backward (the fused path is
-    differentiable, mamba3_pallas.py:824-830)."""
+    differentiable, mamba3_pallas.py:824-830).  As the reference's fused chunk scan
+    (chunk_scan_fwd_rule / chunk_scan_bwd_rule, mamba3_pallas.py:602-645), the
+    forward saves the states entering every chunk, which the backward reads instead
+    of recomputing them."""
 
     @staticmethod
-    def forward(ctx, chunk_size, seq_split, *args):
-        ctx.chunk_size = chunk_size
-        ctx.save_for_backward(*(t if isinstance(t, torch.Tensor) else None for t in args))
-        return _shared_forward(args, chunk_size, seq_split)
+    def forward(ctx, chunk_size, seq_split, cdt, *args):
+        ctx.chunk_size, ctx.cdt = chunk_size, cdt
+        out, saved = _shared_forward(args, chunk_size, seq_split, train=True, cdt=cdt)
+        ctx.save_for_backward(*(t if isinstance(t, torch.Tensor) else None for t in args), saved)
+        return out
 
     @staticmethod
     def backward(ctx, dout):
-        args = ctx.saved_tensors
-        grads = mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=ctx.chunk_size)
-        return (None, None, *(None if t is None or gr is None else gr.to(t.dtype) for t, gr in zip(args, grads)))
+        *args, saved = ctx.saved_tensors
+        grads = mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=ctx.chunk_size, saved=saved,
+                                                  compute_dtype=ctx.cdt)
+        return (None, None, None,
+                *(None if t is None or gr is None else gr.to(t.dtype) for t, gr in zip(args, grads)))
 
 
 def mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D=None, Z=None,
-                                  chunk_size: int = 64, seq_split: bool = True) -> torch.Tensor:
+                                  chunk_size: int = 64, seq_split: bool = True,
+                                  compute_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """The reference's fused-path entry with B and C shared over heads,
     mamba3_ssd_chunked_pallas(Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z,
     chunk_size) (src/base_model/models/mamba3_pallas.py:813-849): Q, K (L, N) shared
     over heads; angles (L, R), (L, 1, R) or (L, nh, R); V, Z (L, nh, P); ADT, DT, Trap
     (nh, L); Q_bias, K_bias (nh, N); D (nh,); optionally a leading batch dim on
     every per-sequence input.  Same result as the per-head scan with Q, K and angles
-    repeated over heads.  Differentiable (torch autograd)."""
+    repeated over heads.  Differentiable (torch autograd).
+
+    ``compute_dtype``: the MFMA operand dtype (the reference's compute_dtype,
+    mamba3_pallas.py:817-839); None reads MAMBA3_PALLAS_DTYPE, then V's dtype
+    (pallas_compute_dtype).  Q, K, V and Z are cast to it; the output comes back in
+    V's dtype."""
+    cdt = compute_dtype or pallas_compute_dtype(V.dtype)
+    _req(cdt in _IO, f"compute_dtype must be float32 or bfloat16, got {cdt}")
     per_head = angles.dim() == (4 if V.dim() == 4 else 3) and angles.shape[-2] > 1
     if per_head:
         # angle rates per head: the per-head path with one shared Q/K head (Hqk = 1)
-        return mamba3_siso_hip(Q.unsqueeze(-2), K.unsqueeze(-2), V, ADT, DT, Trap, Q_bias, K_bias, angles,
-                               D, Z, chunk_size=chunk_size, seq_split=seq_split)
+        Zc = None if Z is None else Z.to(cdt)
+        out = mamba3_siso_hip(Q.unsqueeze(-2).to(cdt), K.unsqueeze(-2).to(cdt), V.to(cdt), ADT, DT, Trap,
+                              Q_bias, K_bias, angles, D, Zc, chunk_size=chunk_size, seq_split=seq_split)
+        return out.to(V.dtype)
     args = (Q, K, V, ADT, DT, Trap, angles, Q_bias, K_bias, D, Z)
     if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in args):
-        return _Mamba3Shared.apply(int(chunk_size), bool(seq_split), *args)
-    return _shared_forward(args, chunk_size, seq_split)
+        return _Mamba3Shared.apply(int(chunk_size), bool(seq_split), cdt, *args)
+    return _shared_forward(args, chunk_size, seq_split, cdt=cdt)[0]

@@ -131,15 +131,7 @@ def test_gradients_with_more_items_than_compute_units(B, L, H, Hqk, N, P, R, bf1
     _check(B, L, H, Hqk, N, P, R, bf16=bf16, seed=37)
 
 
-@pytest.mark.parametrize("B,L,H,Hqk,N,P,R,bf16,split", [
-    (1, 200, 2, 2, 128, 64, 32, True, False),
-    (2, 130, 4, 2, 128, 64, 32, True, False),     # GQA
-    (1, 1100, 3, 3, 128, 64, 32, True, True),     # the forward takes the sequence split
-    (1, 150, 2, 2, 64, 32, 16, False, False),
-    (1, 150, 2, 2, 128, 64, 32, False, False),
-    (2, 100, 4, 2, 128, 64, 64, False, False),    # float32 GQA, rope on every pair
-])
-def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_route):
+def _training_pair(B, L, H, Hqk, N, P, R, bf16, split, route, no_z=False, seed=41):
     """The training forward (the reference's mamba3_siso_fwd, which returns the
     per-chunk states with its output, mamba3_ops.py:788-818) gives the plain forward's
     output bitwise, and the backward that reads its saved chunk states gives the
@@ -147,40 +139,47 @@ def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_rout
     same kernel code (bf16 one pass; float32 at d_state 128, whose state pass is the
     float32 kernel's), within rounding where the forward's states come from another
     kernel (float32 at d_state 64, the split), and within the bars against the
-    oracle.  On the reverse walk's route the comparison is within rounding: its
-    training-pair variant forms dZ from the saved output before the gate (the
-    reference's Out_v residual, in the I/O type) where the recompute forms it from its
-    own float32 product, and it is compiled apart."""
+    oracle.  With Z on the reverse walk's route the comparison is within rounding:
+    the walk's float32 training-pair variant forms dZ from the saved output before
+    the gate (the reference's Out_v residual) where the recompute forms it from its
+    own float32 product, and every training-pair variant is compiled apart."""
     torch = _torch()
     from mamba3_rocm import mamba3_siso_hip, mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
     from mamba3_rocm import _lib
-    d = I.scan_inputs(B, L, H, N, P, R, seed=41, Hqk=Hqk, bf16=bf16)
-    cot = V.cotangent(B, L, H, P, seed=42)
+    d = I.scan_inputs(B, L, H, N, P, R, seed=seed, Hqk=Hqk, bf16=bf16)
+    cot = V.cotangent(B, L, H, P, seed=seed + 1)
     tdt = torch.bfloat16 if bf16 else torch.float32
     if bf16:
         cot = I.bf16_round(cot)
-    print(f"case training pair {(B, L, H, Hqk, N, P, R)} bf16={bf16} split={split}", flush=True)
+    print(f"case training pair {(B, L, H, Hqk, N, P, R)} bf16={bf16} split={split} no_z={no_z} "
+          f"route={route}", flush=True)
     t = to_dev(d, tdt)
+    if no_z:
+        t["Z"] = None
     args = tuple(t[k] for k in V.NAMES)
     io = _lib.DTYPE_BF16 if bf16 else _lib.DTYPE_F32
     assert (_lib.load().m3_chunk_scan_ws_bytes(B, L, H, N, P, R, 64, io) > 0) == split
     out_tr, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=64)
     out = mamba3_siso_hip(*args, chunk_size=64)
     torch.cuda.synchronize()
-    assert saved is not None
+    assert saved is not None, "the shape has a backward but no residual-writing forward"
     assert torch.equal(out_tr, out), "training forward output differs from the forward"
     dout = torch.from_numpy(np.ascontiguousarray(cot)).to("cuda").to(tdt)
     g_saved = mamba3_siso_hip_bwd(*args, dout, chunk_size=64, saved=saved)
     g_re = mamba3_siso_hip_bwd(*args, dout, chunk_size=64)
     torch.cuda.synchronize()
-    _, ref = V.vjp(d, cot, 16)
-    # bitwise on the chunk-parallel route; the reverse walk's training-pair variant is
-    # compiled apart (dZ from the saved output before the gate), so within rounding
-    exact = ((bf16 and not split) or (not bf16 and N == 128)) and bwd_route == "chunks"
+    _, ref = V.vjp(d, cot, 16, no_z=no_z)
+    same_states = (bf16 and not split) or (not bf16 and N == 128)
+    exact = same_states and (route == "chunks" or no_z or bf16)
     for name, a, b, r in zip(V.NAMES, g_saved, g_re, ref):
         if r is None:
+            assert a is None and b is None, name
             continue
         a, b = a.float().cpu().numpy(), b.float().cpu().numpy()
+        assert a.shape == r.shape, (name, a.shape, r.shape)
+        if r.size == 0:          # dAngles without rope
+            continue
+        assert np.isfinite(a).all(), f"d{name} has non-finite entries"
         if exact and name != "Z":
             assert np.array_equal(a, b), f"d{name}: saved-state backward differs from the recompute"
         else:
@@ -188,33 +187,29 @@ def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_rout
         assert rel(a, r) <= (BF16_TOL if bf16 else F32_TOL), (name, rel(a, r))
 
 
-@pytest.mark.parametrize("bf16", [True, False])
-def test_training_pair_without_z(bf16, bwd_route):
-    """Without Z the training forward saves no output before the gate and the backward
-    from its residuals gives the recompute's gradients (dZ None)."""
-    torch = _torch()
-    from mamba3_rocm import mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
-    B, L, H, N, P, R = 1, 150, 2, 128, 64, 32
-    d = I.scan_inputs(B, L, H, N, P, R, seed=43, bf16=bf16)
-    cot = V.cotangent(B, L, H, P, seed=44)
-    tdt = torch.bfloat16 if bf16 else torch.float32
-    if bf16:
-        cot = I.bf16_round(cot)
-    print(f"case training pair without Z bf16={bf16}", flush=True)
-    t = to_dev(d, tdt)
-    t["Z"] = None
-    args = tuple(t[k] for k in V.NAMES)
-    out_tr, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=64)
-    assert saved is not None
-    dout = torch.from_numpy(np.ascontiguousarray(cot)).to("cuda").to(tdt)
-    g_saved = mamba3_siso_hip_bwd(*args, dout, chunk_size=64, saved=saved)
-    g_re = mamba3_siso_hip_bwd(*args, dout, chunk_size=64)
-    torch.cuda.synchronize()
-    _, ref = V.vjp(d, cot, 16, no_z=True)
-    for name, a, b, r in zip(V.NAMES, g_saved, g_re, ref):
-        if r is None:
-            assert a is None and b is None, name
-            continue
-        a, b = a.float().cpu().numpy(), b.float().cpu().numpy()
-        assert np.array_equal(a, b), f"d{name}: saved-state backward differs from the recompute"
-        assert rel(a, r) <= (BF16_TOL if bf16 else F32_TOL), (name, rel(a, r))
+# Every shape whose forward writes the backward's residuals: the bf16 list of
+# m3_scan_chunked.hip (M3_SAVE_SHAPES) and the float32 list of m3_scan_chunked_f32.hip
+# (M3_F32_SAVE_SHAPES), as (N, P, R).
+BF16_SAVE = [(128, 64, 32), (128, 64, 64), (128, 64, 0), (64, 64, 16), (64, 32, 16)]
+F32_SAVE = [(128, 64, 32), (128, 64, 64), (64, 64, 16), (64, 32, 16)]
+SAVE_CASES = [(N, P, R, True) for N, P, R in BF16_SAVE] + [(N, P, R, False) for N, P, R in F32_SAVE]
+
+
+@pytest.mark.parametrize("no_z", [False, True], ids=["z", "no_z"])
+@pytest.mark.parametrize("N,P,R,bf16", SAVE_CASES)
+def test_training_pair_every_saved_shape(N, P, R, bf16, no_z, bwd_route):
+    """Every residual-writing forward instantiation and both backward variants that
+    read it (with Z the float32 walk's saved-output variant), ragged L over three
+    chunks."""
+    _training_pair(1, 150, 2, 2, N, P, R, bf16, False, bwd_route, no_z=no_z)
+
+
+@pytest.mark.parametrize("B,L,H,Hqk,N,P,R,bf16,split", [
+    (2, 130, 4, 2, 128, 64, 32, True, False),     # GQA
+    (1, 1100, 3, 3, 128, 64, 32, True, True),     # the forward takes the sequence split
+    (2, 100, 4, 2, 128, 64, 64, False, False),    # float32 GQA, rope on every pair
+    (2, 90, 4, 1, 64, 64, 16, False, False),      # float32 GQA at d_state 64
+])
+def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_route):
+    """The training pair with GQA and with a forward that takes the sequence split."""
+    _training_pair(B, L, H, Hqk, N, P, R, bf16, split, bwd_route)

@@ -43,7 +43,9 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_shared", "m3_chunk_scan_bwd_shared_ws_bytes",
                             "m3_chunk_scan_bwd_shared", "m3_chunk_scan_saved_bytes",
                             "m3_chunk_scan_fwd_train", "m3_chunk_scan_bwd_saved_ws_bytes",
-                            "m3_chunk_scan_bwd_saved", "m3_decode_step", "m3_layer_pre",
+                            "m3_chunk_scan_bwd_saved", "m3_chunk_scan_fwd_train_shared",
+                            "m3_chunk_scan_bwd_saved_shared_ws_bytes", "m3_chunk_scan_bwd_saved_shared",
+                            "m3_decode_step", "m3_layer_pre",
                             "m3_layer_scan", "m3_layer_post", "m3_block_norm", "m3_block_gelu",
                             "m3_block_act", "m3_block_act_norm", "m3_log_softmax"])
     for n in names:
@@ -54,7 +56,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_constants(lib):
     from mamba3_rocm import _lib
-    assert lib.m3_abi_version() == 100
+    assert lib.m3_abi_version() == 101
     assert _lib.DTYPE_F32 == _header_define("M3_DTYPE_F32")
     assert _lib.DTYPE_BF16 == _header_define("M3_DTYPE_BF16")
     assert _lib.IMPL_CHUNKED_MFMA == _header_define("M3_IMPL_CHUNKED_MFMA")
@@ -395,3 +397,28 @@ def test_contraction_precision_knob(monkeypatch):
             mamba3_siso_hip(t, t, torch.zeros(4, 2, 8), t, t, t, t, t, t)
         with pytest.raises(ValueError, match="MAMBA3_CONTRACTION_PRECISION must be highest or default"):
             rnn_step_hip((t, t, t, t), (t,) * 8, t, t, t)
+
+
+def test_pallas_dtype_knob(monkeypatch):
+    """MAMBA3_PALLAS_DTYPE follows the reference's contract (mamba3_pallas.py:112-122):
+    unset or empty, the layer's dtype decides; "float32" / "bfloat16" override it;
+    anything else raises its ValueError -- at the shared-B/C entry point too, before
+    any device work."""
+    import torch
+    from mamba3_rocm import mamba3_ssd_chunked_shared_hip, pallas_compute_dtype
+    monkeypatch.delenv("MAMBA3_PALLAS_DTYPE", raising=False)
+    assert pallas_compute_dtype() == torch.float32
+    assert pallas_compute_dtype(torch.bfloat16) == torch.bfloat16
+    monkeypatch.setenv("MAMBA3_PALLAS_DTYPE", "")
+    assert pallas_compute_dtype(torch.bfloat16) == torch.bfloat16
+    monkeypatch.setenv("MAMBA3_PALLAS_DTYPE", "float32")
+    assert pallas_compute_dtype(torch.bfloat16) == torch.float32
+    monkeypatch.setenv("MAMBA3_PALLAS_DTYPE", "bfloat16")
+    assert pallas_compute_dtype(torch.float32) == torch.bfloat16
+    for bad in ("fp32", "bf16", "float16", "BFLOAT16"):
+        monkeypatch.setenv("MAMBA3_PALLAS_DTYPE", bad)
+        with pytest.raises(ValueError, match="MAMBA3_PALLAS_DTYPE must be float32 or bfloat16"):
+            pallas_compute_dtype()
+        t = torch.zeros(1)
+        with pytest.raises(ValueError, match="MAMBA3_PALLAS_DTYPE must be float32 or bfloat16"):
+            mamba3_ssd_chunked_shared_hip(t, t, torch.zeros(4, 2, 8), t, t, t, t, t, t)

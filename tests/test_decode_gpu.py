@@ -2,7 +2,7 @@
 
 Covers both input dtypes, the reference's mode knobs (mamba3.py:28-45),
 multi-step accumulation, the headline decode shape (config 4: B=512, H=32,
-P=64, N=128) on a subset of batch rows, and the prefill -> decode handoff:
+P=64, N=128) over its whole 256-step chain (three batch rows checked), and the prefill -> decode handoff:
 decoding T tokens after a prefill of L tokens equals a prefill of L + T
 (chunked == recurrent, test_backbone_contracts.py:81-111).
 """
@@ -100,6 +100,61 @@ def test_decode_headline_shape_subset():
         ref_carry, yr = M.rnn_step(ref_carry, ref_in, d["B_bias"], d["C_bias"], d["D"])
         assert rel(y.cpu().numpy()[rows], yr) <= 1e-4
     assert rel(carry[1].cpu().numpy()[rows], ref_carry[1]) <= 1e-4
+
+
+def test_decode_config4_full_chain():
+    """Config 4 as BASELINE states it: B=512, H=32, P=64, N=128, R=32, 256 consecutive
+    steps in place on one carry (bf16 step inputs, float32 state), generated on the
+    device with the configuration's distributions.  Rows 0, 200 and 511 follow the
+    float64 rnn_step (mamba3.py:498-562) over the whole chain: y at every step
+    (steps 1, 128 and 256 named in the message) and the final carry, at the float32
+    bar 1e-4."""
+    import math
+    import torch
+    from mamba3_rocm import rnn_step_hip
+    B, H, N, P, R, T = 512, 32, 128, 64, 32, 256
+    rows = [0, 200, 511]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    f = dict(device="cuda", dtype=torch.float32, generator=g)
+    sN = 1.0 / math.sqrt(N)
+    carry = (torch.rand(B, H, R, **f) * 2 * math.pi, torch.randn(B, H, P, N, **f) * 0.1,
+             torch.randn(B, H, N, **f) * sN, torch.randn(B, H, P, **f))
+    bf = torch.bfloat16
+    A = -torch.exp(torch.rand(H, **f) * math.log(16.0))
+    Bb, Cb, D = torch.randn(H, N, **f) * sN, torch.randn(H, N, **f) * sN, torch.randn(H, **f)
+    host = lambda t: t.double().cpu().numpy()  # noqa: E731
+    ref_carry = tuple(host(c[rows]) for c in carry)
+    ptrs = [c.data_ptr() for c in carry]
+    print(f"case decode config 4 full chain B={B} H={H} steps={T}", flush=True)
+    worst = {}
+    for s in range(T):
+        x = torch.randn(B, H, P, **f).to(bf)
+        z = torch.randn(B, H, P, **f).to(bf)
+        bt = (torch.randn(B, H, N, **f) * sN).to(bf)
+        ct = (torch.randn(B, H, N, **f) * sN).to(bf)
+        dt = torch.nn.functional.softplus(torch.randn(B, H, **f) * 0.5 - 2.0)
+        adt = A[None, :] * dt
+        trap = torch.sigmoid(torch.rand(B, H, **f))
+        ang = (torch.rand(B, H, R, **f) * 2 - 1) * math.pi
+        carry, y = rnn_step_hip(carry, (x, z, bt, ct, adt, dt, trap, ang), Bb, Cb, D)
+        ref_in = tuple(host(t[rows]) for t in (x, z, bt, ct, adt, dt, trap, ang))
+        ref_carry, yr = M.rnn_step(ref_carry, ref_in, host(Bb), host(Cb), host(D))
+        err = rel(y[rows].cpu().numpy(), yr)
+        worst[s + 1] = err
+        assert err <= 1e-4, f"y at step {s + 1}: rel {err:.2e}"
+    assert [c.data_ptr() for c in carry] == ptrs, "the carry was not updated in place"
+    names = ("theta", "h", "k_prev", "v_prev")
+    cerr = {n: rel(c[rows].cpu().numpy(), r) for n, c, r in zip(names, carry, ref_carry)}
+    # the angle state is wrapped into [0, 2 pi): compare it on the circle, so that a value
+    # next to the wrap that rounding puts on the other side is not an error of 2 pi
+    dth = carry[0][rows].double().cpu().numpy() - ref_carry[0]
+    cerr["theta"] = float(np.abs((dth + np.pi) % (2 * np.pi) - np.pi).max() / (2 * np.pi))
+    print(f"  y rel at steps 1/128/256: {worst[1]:.1e} {worst[128]:.1e} {worst[256]:.1e}; "
+          f"max {max(worst.values()):.1e}; final carry " +
+          " ".join(f"{k}:{v:.1e}" for k, v in cerr.items()), flush=True)
+    bad = {k: v for k, v in cerr.items() if v > 1e-4}
+    assert not bad, f"final carry above 1e-4: {bad}"
 
 
 @pytest.mark.parametrize("bf16", [False, True])

@@ -45,6 +45,31 @@ def test_layer_matches_oracle(B, L, d_model, N, headdim, bf16, path, split):
     assert err <= (2e-2 if bf16 else 1e-4)
 
 
+@pytest.mark.parametrize("layer_bf16,knob", [(True, "float32"), (False, "bfloat16")])
+def test_layer_honours_pallas_dtype_knob(layer_bf16, knob, monkeypatch):
+    """MAMBA3_PALLAS_DTYPE (mamba3_pallas.py:112-122) sets the scan's operand dtype
+    apart from the layer's: the layer copies x and z and hands the scan operands in
+    the knob's dtype.  The output stays in the layer's dtype and follows the oracle
+    of the layer's dtype within the bf16 bar (one side of the comparison rounds to
+    bf16)."""
+    import torch
+    from mamba3_rocm import Mamba3Layer
+    B, L, d_model, N, headdim = 2, 200, 256, 128, 64
+    monkeypatch.setenv("MAMBA3_PALLAS_DTYPE", knob)
+    p = ML.init_params(d_model, seed=53, d_state=N, headdim=headdim)
+    x = np.random.default_rng(54).standard_normal((B, L, d_model)).astype(np.float32)
+    dt = torch.bfloat16 if layer_bf16 else torch.float32
+    layer = Mamba3Layer({k: torch.from_numpy(v).cuda() for k, v in p.items()}, d_model, d_state=N,
+                        headdim=headdim, dtype=dt)
+    y = layer(torch.from_numpy(x).cuda())
+    assert y.dtype == dt
+    assert layer.last_scan == "copies" and layer.last_compute_dtype == getattr(torch, knob)
+    ref = ML.layer_forward(p, x, d_state=N, headdim=headdim, bf16=layer_bf16)
+    err = rel(y.float().cpu().numpy(), ref)
+    print(f"layer knob={knob} layer_bf16={layer_bf16} rel={err:.3e}", flush=True)
+    assert err <= 2e-2
+
+
 @pytest.mark.parametrize("activation,prenorm,bf16", [
     ("half_glu1", True, True), ("full_glu", False, True), ("half_glu2", True, False), ("gelu", False, False),
 ])

@@ -7,6 +7,7 @@ also takes (B and C repeated over heads before BCNorm, mamba3.py:236-242 and
 output projection.
 """
 import numpy as np
+import pytest
 
 from oracle import mamba3_layer as ML
 from oracle import mamba3_ref as M
@@ -151,3 +152,132 @@ def test_stack_oracle_glu_variants_closed_forms():
     assert np.allclose(block("half_glu2"), m * gate, atol=1e-10)
     assert np.allclose(block("full_glu"), g * gate, atol=1e-10)
     assert not np.allclose(block("half_glu2"), m * MS.sigmoid(alpha * m), atol=1e-3)
+
+
+# ---------------------------------------------------------------- wiring pins
+# The split order of in_proj's output and the decay are fixed here by special
+# parameters whose layer output has a form computed without the oracle's own split
+# (the column offsets below are written out from mamba3.py:212-219's order
+# [z, x, B, C, dd_dt, dd_A, trap, angles]), so that a swapped block fails.
+WIRE = dict(d_model=32, N=16, headdim=16)
+
+
+def _offsets(d_model, N, headdim):
+    nh, hd, R, dproj = ML.dims(d_model, N, 2, headdim)
+    di = nh * hd
+    o = {"z": 0, "x": di, "B": 2 * di, "C": 2 * di + N, "dd_dt": 2 * di + 2 * N}
+    o["dd_A"] = o["dd_dt"] + nh
+    o["trap"] = o["dd_A"] + nh
+    o["ang"] = o["trap"] + nh
+    assert o["ang"] + R == dproj
+    return nh, hd, R, di, o
+
+
+def _out_norm_proj(p, y):
+    """_post_norm_and_project (mamba3.py:281-325) on float64 y (B, L, d_inner)."""
+    yn = y / np.sqrt(np.mean(y * y, axis=-1, keepdims=True) + ML.EPS)
+    return (yn * p["out_norm"]) @ p["out_proj"].astype(np.float64)
+
+
+def _skip_only_case(seed=20):
+    """B, C and angle columns of in_proj zero, B and C biases zero: the normalised B
+    and C rows are zero, so the scan is its skip term alone, y = D x silu(z)."""
+    d_model, N, headdim = WIRE["d_model"], WIRE["N"], WIRE["headdim"]
+    p = ML.init_params(d_model, seed, d_state=N, headdim=headdim)
+    nh, hd, R, di, o = _offsets(d_model, N, headdim)
+    W = p["in_proj"].copy()
+    W[:, o["B"]:o["dd_dt"]] = 0.0
+    W[:, o["ang"]:] = 0.0
+    p.update(in_proj=W, B_bias=np.zeros_like(p["B_bias"]), C_bias=np.zeros_like(p["C_bias"]))
+    x = np.random.default_rng(seed + 1).standard_normal((2, 40, d_model)).astype(np.float32)
+    proj = x.astype(np.float64) @ W.astype(np.float64)
+    B_, L = x.shape[:2]
+    xv = proj[..., o["x"]:o["x"] + di].reshape(B_, L, nh, hd)
+    z = proj[..., o["z"]:o["z"] + di].reshape(B_, L, nh, hd)
+    y = (p["D"][:, None] * xv * z / (1 + np.exp(-z))).reshape(B_, L, di)
+    return p, x, _out_norm_proj(p, y)
+
+
+def _constant_feature_case(seed=21):
+    """The input's last feature is 1 and the dd_dt, dd_A, trap and angle columns of
+    in_proj are zero except in that feature's row: every token of a head sees the
+    same chosen dd_dt, dd_A, trap and angle rate.  The expected output is the
+    brute-force quadratic form (oracle/pins.py) on inputs cut from the projection at
+    the reference's offsets, with A = -softplus(dd_A) and DT = softplus(dd_dt +
+    dt_bias) formed here."""
+    from oracle import pins
+    d_model, N, headdim = WIRE["d_model"], WIRE["N"], WIRE["headdim"]
+    p = ML.init_params(d_model, seed, d_state=N, headdim=headdim)
+    nh, hd, R, di, o = _offsets(d_model, N, headdim)
+    rng = np.random.default_rng(seed + 1)
+    consts = {"dd_dt": rng.uniform(-1.5, 0.5, nh), "dd_A": rng.uniform(-0.5, 2.0, nh),
+              "trap": rng.uniform(-1.5, 1.5, nh), "ang": rng.uniform(-2.0, 2.0, R)}
+    consts = {k: c.astype(np.float32).astype(np.float64) for k, c in consts.items()}   # in_proj is float32
+    W = p["in_proj"].copy()
+    for k, c in consts.items():
+        W[:, o[k]:o[k] + len(c)] = 0.0
+        W[-1, o[k]:o[k] + len(c)] = c
+    p["in_proj"] = W.astype(np.float32)
+    L = 24
+    x = rng.standard_normal((1, L, d_model)).astype(np.float32)
+    x[..., -1] = 1.0
+    proj = (x.astype(np.float64) @ p["in_proj"].astype(np.float64))[0]
+    A = -np.log1p(np.exp(consts["dd_A"]))
+    DT = np.log1p(np.exp(consts["dd_dt"] + p["dt_bias"].astype(np.float64)))
+    assert np.all(A < -1e-4)                                   # above the floor
+    cols = lambda k, w: proj[:, o[k]:o[k] + w]                  # noqa: E731
+    Cn, Bn = ML.rmsnorm(cols("C", N), p["C_norm"]), ML.rmsnorm(cols("B", N), p["B_norm"])
+    rep = lambda a: np.repeat(a[:, None, :], nh, axis=1)        # noqa: E731
+    y = pins.quadratic_form(
+        rep(Cn), rep(Bn), cols("x", di).reshape(L, nh, hd),
+        np.repeat((A * DT)[:, None], L, axis=1), np.repeat(DT[:, None], L, axis=1),
+        np.repeat(consts["trap"][:, None], L, axis=1), np.broadcast_to(consts["ang"], (L, nh, R)),
+        p["C_bias"], p["B_bias"], p["D"], cols("z", di).reshape(L, nh, hd))
+    return p, x, _out_norm_proj(p, y.reshape(1, L, di))
+
+
+def test_layer_oracle_skip_term_fixes_z_and_x():
+    p, x, want = _skip_only_case()
+    got = ML.layer_forward(p, x, d_state=WIRE["N"], headdim=WIRE["headdim"], chunk_size=16)
+    assert np.abs(got - want).max() <= 1e-10 * np.abs(want).max()
+
+
+def test_layer_oracle_wiring_matches_quadratic_form():
+    p, x, want = _constant_feature_case()
+    got = ML.layer_forward(p, x, d_state=WIRE["N"], headdim=WIRE["headdim"], chunk_size=8)
+    assert np.abs(got - want).max() <= 1e-9 * np.abs(want).max()
+
+
+def _plant_wiring(monkeypatch, which):
+    split = ML.split_proj
+
+    def swapped(proj, di, N, nh):
+        z, xv, Bm, Cm, dd_dt, dd_A, trap, ang = split(proj, di, N, nh)
+        if which == "z_x":
+            z, xv = xv, z
+        elif which == "B_C":
+            Bm, Cm = Cm, Bm
+        elif which == "dd_dt_dd_A":
+            dd_dt, dd_A = dd_A, dd_dt
+        elif which == "dd_A_trap":
+            dd_A, trap = trap, dd_A
+        return z, xv, Bm, Cm, dd_dt, dd_A, trap, ang
+    monkeypatch.setattr(ML, "split_proj", swapped)
+
+
+@pytest.mark.parametrize("which", ["z_x", "B_C", "dd_dt_dd_A", "dd_A_trap"])
+def test_planted_wiring_swaps_fail_the_pins(monkeypatch, which):
+    cases = [_constant_feature_case()] + ([_skip_only_case()] if which == "z_x" else [])
+    _plant_wiring(monkeypatch, which)
+    for p, x, want in cases:
+        got = ML.layer_forward(p, x, d_state=WIRE["N"], headdim=WIRE["headdim"], chunk_size=8)
+        assert np.abs(got - want).max() > 1e-3 * np.abs(want).max(), which
+
+
+def test_planted_decay_mistake_fails_the_pin(monkeypatch):
+    """A decay that forgets the dt bias (DT = softplus(dd_dt)) fails the wiring pin."""
+    monkeypatch.setattr(ML, "decay", lambda dd_dt, dd_A, dt_bias, A_floor:
+                        (np.minimum(-ML.softplus(dd_A), -A_floor), ML.softplus(dd_dt)))
+    p, x, want = _constant_feature_case()
+    got = ML.layer_forward(p, x, d_state=WIRE["N"], headdim=WIRE["headdim"], chunk_size=8)
+    assert np.abs(got - want).max() > 1e-3 * np.abs(want).max()

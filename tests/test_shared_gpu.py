@@ -106,3 +106,88 @@ def test_per_head_angles_take_the_per_head_path():
     t["Angles"] = torch.from_numpy(rep["Angles"]).to("cuda")
     y = _call(t, 64).float().cpu().numpy()
     assert rel(y, oracle_scan(rep, 64)) <= 2e-2
+
+
+@pytest.mark.parametrize("B,L,H,N,P,R,bf16", [
+    (2, 200, 4, 128, 64, 32, True),
+    (1, 1100, 3, 128, 64, 32, True),      # B*H small: the training forward takes the sequence split
+    (1, 150, 4, 128, 64, 32, False),
+    (2, 90, 2, 64, 32, 16, False),
+])
+def test_shared_training_pair(B, L, H, N, P, R, bf16, bwd_route):
+    """The fused path's training pair (the forward that saves the chunk states, the
+    backward that reads them, as the reference's chunk_scan_fwd_rule /
+    chunk_scan_bwd_rule, mamba3_pallas.py:602-645): the forward's output equals the
+    plain forward bitwise, and the gradients equal the recomputing backward's
+    (bitwise where both produce the chunk states with the same kernel code: bf16
+    without the split, float32 at d_state 128 without Z on the walk) and the
+    repeated-input oracle within the bars."""
+    torch = _torch()
+    from mamba3_rocm import mamba3_ssd_chunked_shared_hip_bwd, mamba3_ssd_chunked_shared_hip_fwd_train
+    shared, rep = _inputs(B, L, H, N, P, R, seed=45, bf16=bf16)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    t = _dev(shared, dt)
+    names = ("Q", "K", "V", "ADT", "DT", "Trap", "Angles", "Q_bias", "K_bias", "D", "Z")
+    args = tuple(t[k] for k in names)
+    print(f"case shared training pair {(B, L, H, N, P, R)} bf16={bf16} route={bwd_route}", flush=True)
+    out_tr, saved = mamba3_ssd_chunked_shared_hip_fwd_train(*args, chunk_size=64)
+    out = _call(t, 64)
+    torch.cuda.synchronize()
+    assert saved is not None
+    assert torch.equal(out_tr, out), "training forward output differs from the forward"
+    cot = V.cotangent(B, L, H, P, seed=46)
+    if bf16:
+        cot = I.bf16_round(cot)
+    dout = torch.from_numpy(cot).to("cuda").to(dt)
+    g_saved = mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=64, saved=saved)
+    g_re = mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=64)
+    torch.cuda.synchronize()
+    _, ref = V.vjp(rep, cot, 16)
+    ref = dict(zip(V.NAMES, ref))
+    ref["Q"], ref["K"] = ref["Q"][:, :, 0], ref["K"][:, :, 0]
+    ref["Angles"] = ref["Angles"].sum(axis=2)
+    split = L > 1000
+    exact = (bf16 and not split) or (not bf16 and N == 128 and bwd_route == "chunks")
+    tol = 3e-2 if bf16 else 2e-5
+    for k, a, b in zip(names, g_saved, g_re):
+        a, b = a.float().cpu().numpy(), b.float().cpu().numpy()
+        if exact and k != "Z":
+            assert np.array_equal(a, b), f"d{k}: saved-state backward differs from the recompute"
+        else:
+            assert rel(a, b) <= (1e-2 if bf16 else 1e-5), (k, rel(a, b))
+        assert rel(a, ref[k]) <= tol, (k, rel(a, ref[k]))
+
+
+@pytest.mark.parametrize("io_bf16", [False, True])
+def test_shared_compute_dtype_knob(io_bf16, monkeypatch):
+    """MAMBA3_PALLAS_DTYPE sets the operand dtype of the fused path's kernels
+    (mamba3_pallas.py:112-122, 838-839): with float32 inputs and the knob at
+    bfloat16 the result is the bf16 kernel's on the inputs rounded to bf16, returned
+    in float32; with bf16 inputs and the knob at float32 it is the float32 kernel's on
+    the widened inputs, returned in bf16.  Gradients under the knob follow the oracle
+    at the compute dtype's bar."""
+    torch = _torch()
+    B, L, H, N, P, R = 2, 200, 4, 128, 64, 32
+    shared, rep = _inputs(B, L, H, N, P, R, seed=47, bf16=True)
+    io = torch.bfloat16 if io_bf16 else torch.float32
+    cdt = torch.float32 if io_bf16 else torch.bfloat16
+    t = _dev(shared, io)
+    monkeypatch.delenv("MAMBA3_PALLAS_DTYPE", raising=False)
+    y_plain = _call(_dev(shared, cdt), 64)
+    monkeypatch.setenv("MAMBA3_PALLAS_DTYPE", "float32" if cdt == torch.float32 else "bfloat16")
+    y = _call(t, 64)
+    torch.cuda.synchronize()
+    assert y.dtype == io
+    assert torch.equal(y, y_plain.to(io)), "the knob's result differs from the kernel of its dtype"
+    names = ("Q", "K", "V", "ADT", "DT", "Trap", "Angles", "Q_bias", "K_bias", "D", "Z")
+    leaves = {k: t[k].clone().requires_grad_(True) for k in names}
+    cot = I.bf16_round(V.cotangent(B, L, H, P, seed=48))
+    _call(leaves, 64).backward(torch.from_numpy(cot).to("cuda").to(io))
+    _, ref = V.vjp(rep, cot, 16)
+    ref = dict(zip(V.NAMES, ref))
+    ref["Q"], ref["K"] = ref["Q"][:, :, 0], ref["K"][:, :, 0]
+    ref["Angles"] = ref["Angles"].sum(axis=2)
+    errs = {k: rel(leaves[k].grad.float().cpu().numpy(), ref[k]) for k in names}
+    print(f"shared knob io_bf16={io_bf16} " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+    tol = 3e-2 if cdt == torch.bfloat16 else 1e-2    # bf16 inputs: the gradients are rounded to bf16
+    assert all(v <= tol for v in errs.values()), errs
