@@ -14,7 +14,7 @@ Also reported on the same JSON line:
                 (oracle/, the reference's own JAX is not installed) timed on
                 the host on a bounded sample (one of the 8 sequences)
   secondary     decode state update (config 4, HBM GB/s), the long-context
-                scan (config 3), the shared-B/C scan and its backward (recomputing,
+                scan (config 3, bf16 and float32 I/O), the shared-B/C scan and its backward (recomputing,
                 and the training pair), the float32-I/O scan, the scan backward at
                 config 2 and at config 3's shape (recomputing its chunk states) and the
                 training pair (forward with residuals, backward from them), with bf16
@@ -549,7 +549,7 @@ def main():
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--io", choices=("bf16", "f32"), default="bf16", help="--mode bwd / train: the I/O dtype")
+    ap.add_argument("--io", choices=("bf16", "f32"), default="bf16", help="--mode bwd / train / long: the I/O dtype")
     args = ap.parse_args()
 
     if args.mode == "traffic":
@@ -620,7 +620,11 @@ def main():
         return
     if args.mode == "long":
         # config 3 alone (B*H = 32: the sequence split runs), for profiling
-        r = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3)
+        r = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3, io_dtype=io)
+        if io == torch.float32:
+            print(json.dumps({"mode": "long", "io_dtype": "f32", "tokens_per_s": round(32768 / r["wall_s"], 1),
+                              **fp32_fwd_line(r)}), flush=True)
+            return
         print(json.dumps({"mode": "long", "kernel_ms": round(r["kernel_s"] * 1e3, 4),
                           "tokens_per_s": round(32768 / r["wall_s"], 1),
                           "achieved_gbs": round(r["achieved_gbs"], 1),
@@ -658,6 +662,8 @@ def main():
     if not args.no_secondary:
         dec = bench_decode(torch, 512, 32, 128, 64, 32, 256, 16, seed=4)
         lc = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3)
+        lc32 = bench_scan(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 5), 3, seed=3,
+                          io_dtype=torch.float32)
         bw = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         tr = bench_train(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         bw32 = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 10), 2, seed=2,
@@ -681,6 +687,8 @@ def main():
                                      "tokens_per_s": round(32768 / lc["wall_s"], 1),
                                      "achieved_gbs": round(lc["achieved_gbs"], 1),
                                      "frac_hbm": round(lc["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "long_context_fp32_io_config3": {"B": 1, "L": 32768, "H": 32, "chunk": 128, "io_dtype": "f32",
+                                             "tokens_per_s": round(32768 / lc32["wall_s"], 1), **fp32_fwd_line(lc32)},
             "shared_bc_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64,
                                   "kernel_ms": round(sh["kernel_s"] * 1e3, 4),
                                   "tokens_per_s": round(8 * 4096 / sh["wall_s"], 1),

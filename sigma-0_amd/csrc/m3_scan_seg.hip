@@ -149,8 +149,10 @@ void seg_combine_kernel(ScanArgs a, int nseg, Carries loc, Carries in) {
 
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS) {
   const int len = seg_len_for(B, H, L);
-  // the model's shapes (bf16, d_state 128, headdim 64); others run one pass
-  if (len == 0 || !bf16_io || N != 128 || P != 64 || !scan_state_supported(bf16_io, 64, N, P, R) ||
+  // the model's shapes (d_state 128, headdim 64; bf16, and float32, the I/O the
+  // model's mamba3_siso_triton call hands over) with a state-only pass; others run
+  // one pass
+  if (len == 0 || N != 128 || P != 64 || !scan_state_supported(bf16_io, 64, N, P, R) ||
       !scan_chunked_supported(bf16_io, CS, N, P, R))
     return 0;
   const long bhs = (long)B * H * ((L + len - 1) / len);
@@ -173,7 +175,7 @@ hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStrea
   p1.chunk_h = nullptr;                              // the saved residuals come from pass 3
   p1.chunk_th = nullptr;
   p1.out_v = nullptr;
-  p1.CS = 64;
+  p1.CS = 64;                                        // 64-token (bf16) or 32-token (float32) sub-chunks
   hipError_t e = scan_state_launch(p1, bf16_io, st);
   if (e != hipSuccess) return e;
 

@@ -169,7 +169,7 @@ def _training_pair(B, L, H, Hqk, N, P, R, bf16, split, route, no_z=False, seed=4
     g_re = mamba3_siso_hip_bwd(*args, dout, chunk_size=64)
     torch.cuda.synchronize()
     _, ref = V.vjp(d, cot, 16, no_z=no_z)
-    same_states = (bf16 and not split) or (not bf16 and N == 128)
+    same_states = not split and (bf16 or N == 128)
     exact = same_states and (route == "chunks" or no_z or bf16)
     for name, a, b, r in zip(V.NAMES, g_saved, g_re, ref):
         if r is None:
@@ -209,6 +209,7 @@ def test_training_pair_every_saved_shape(N, P, R, bf16, no_z, bwd_route):
     (1, 1100, 3, 3, 128, 64, 32, True, True),     # the forward takes the sequence split
     (2, 100, 4, 2, 128, 64, 64, False, False),    # float32 GQA, rope on every pair
     (2, 90, 4, 1, 64, 64, 16, False, False),      # float32 GQA at d_state 64
+    (1, 1100, 3, 3, 128, 64, 32, False, True),    # float32, the forward takes the sequence split
 ])
 def test_training_pair_saved_states(B, L, H, Hqk, N, P, R, bf16, split, bwd_route):
     """The training pair with GQA and with a forward that takes the sequence split."""

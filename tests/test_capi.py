@@ -84,9 +84,9 @@ def test_kernel_selection(lib):
 
 def test_split_workspace_sizes(lib):
     """Workspace for the sequence split: per (b, h, segment) two carries (P x N state,
-    N key, P value, R angles, each array 256-byte aligned) and one log-decay; none
-    when B*H already fills the chip, for short sequences, fp32, or shapes without the
-    state-only pass."""
+    N key, P value, R angles, each array 256-byte aligned) and one log-decay (float32
+    whatever the I/O type); none when B*H already fills the chip, for short sequences,
+    or shapes without the state-only pass."""
     f = lib.m3_chunk_scan_ws_bytes
     bf, f32 = 1, 0
     al = lambda n: (n * 4 + 255) // 256 * 256  # noqa: E731
@@ -96,7 +96,8 @@ def test_split_workspace_sizes(lib):
                                                      + al(bhs))
     assert f(8, 4096, 32, 128, 64, 32, 64, bf) == 0          # config 2: 256 (b, h) pairs
     assert f(1, 400, 2, 128, 64, 32, 64, bf) == 0            # too short to split
-    assert f(1, 4096, 2, 128, 64, 32, 64, f32) == 0          # fp32: one pass
+    assert f(1, 4096, 2, 128, 64, 32, 64, f32) == f(1, 4096, 2, 128, 64, 32, 64, bf) > 0   # fp32: the same carries
+    assert f(1, 4096, 2, 64, 64, 16, 64, f32) == 0           # fp32 d_state 64: no state-only pass
     assert f(1, 4096, 2, 64, 64, 16, 64, bf) == 0            # no state-only pass for d_state 64
     assert f(1, 4096, 2, 128, 64, 32, 48, bf) == 0           # chunk 48: generic kernel
     assert f(1, 1061, 3, 128, 64, 32, 64, bf) > 0
