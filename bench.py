@@ -29,7 +29,7 @@ launches of a process); the JSON line reports this as ``clock_settle``, apart fr
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-secondary]
-                       [--mode scan|decode|long|bwd|train|shared|shared_bwd|layer|stack|copy|fp32]
+                       [--mode scan|decode|long|bwd|bwd3|train|shared|shared_bwd|layer|stack|copy|fp32]
                        [--io bf16|f32]   (--mode bwd / train)
        python bench.py --mode traffic --pmc-dir DIR   (writes the traffic JSON of
                        the headline kernel from rocprofv3 --pmc FETCH_SIZE /
@@ -512,11 +512,11 @@ def fp32_fwd_line(r):
             "flop_count": FLOP_COUNT_NOTE}
 
 
-def train_line(r, fp32=False):
+def train_line(r, fp32=False, tokens=8 * 4096):
     """The JSON fields of a training-pair measurement (forward with residuals, backward
     from them); the backward's roofline as in bwd_line."""
     d = {"fwd_with_residuals_ms": round(r["fwd_s"] * 1e3, 4), "bwd_from_residuals_ms": round(r["bwd_s"] * 1e3, 4),
-         "step_ms": round((r["fwd_s"] + r["bwd_s"]) * 1e3, 4), "tokens_per_s": round(8 * 4096 / r["wall_s"], 1),
+         "step_ms": round((r["fwd_s"] + r["bwd_s"]) * 1e3, 4), "tokens_per_s": round(tokens / r["wall_s"], 1),
          "residual_bytes": r["saved_bytes"], "bwd_achieved_gbs": round(r["bwd_gbs"], 1),
          "bwd_frac_hbm": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4)}
     if fp32:
@@ -544,7 +544,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "train", "shared", "shared_bwd", "layer",
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "bwd3", "train", "shared", "shared_bwd", "layer",
                                        "stack", "copy", "fp32", "traffic"), default="scan")
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -582,6 +582,13 @@ def main():
         # backward at config 2 alone, for profiling
         r = bench_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, args.steps, args.warmup, seed=2, io_dtype=io)
         print(json.dumps({"mode": "bwd", "io_dtype": args.io, **bwd_line(r)}), flush=True)
+        return
+    if args.mode == "bwd3":
+        # the backward and the training pair at config 3's shape (B*H = 32: the split walk)
+        r = bench_bwd(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3, io_dtype=io)
+        t = bench_train(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3, io_dtype=io)
+        print(json.dumps({"mode": "bwd3", "io_dtype": args.io, **bwd_line(r, tokens=32768),
+                          "training_pair": train_line(t, tokens=32768)}), flush=True)
         return
     if args.mode == "train":
         # the training pair at config 2 (forward with residuals, backward from them)
@@ -673,6 +680,7 @@ def main():
         sh = bench_shared(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         shb = bench_shared_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         bw3 = bench_bwd(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 10), 2, seed=3)
+        tr3 = bench_train(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 10), 2, seed=3)
         f32 = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2,
                          io_dtype=torch.float32)
         bb = bench_stack(torch, 4, 12288, 768, 12, 2112, 5, 2, seed=5)
@@ -700,6 +708,8 @@ def main():
             "backward_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **bwd_line(bw)},
             "backward_config3_shape": {"B": 1, "L": 32768, "H": 32, "chunk": 128,
                                        **bwd_line(bw3, tokens=32768)},
+            "training_pair_config3_shape": {"B": 1, "L": 32768, "H": 32, "chunk": 128,
+                                            **train_line(tr3, tokens=32768)},
             "training_pair_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **train_line(tr)},
             "backward_fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",
                                          **bwd_line(bw32, fp32=True)},

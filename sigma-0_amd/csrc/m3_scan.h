@@ -147,6 +147,11 @@ hipError_t block_elt_launch(BlockEltArgs a, bool gelu_only, bool bf16_io, hipStr
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS);
 hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStream_t st);
+// The backward's state-only pass (a.chunk_h / a.chunk_th, no initial carry) split the
+// same way: the segments' exit carries, their combine, then every segment's state-only
+// pass from its entering carry writes the states entering its chunks.  Workspace:
+// scan_split_ws_bytes(bf16_io, B, L, H, N, P, R, 64).
+hipError_t scan_split_state_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStream_t st);
 
 // Arguments of one decode step (layouts in m3_decode.hip).
 struct DecodeArgs {

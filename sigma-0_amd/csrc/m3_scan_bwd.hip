@@ -41,6 +41,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "m3_chunk_common.h"
@@ -175,6 +176,13 @@ struct BwdArgs {
   int nc;
   const void* yv;              // (B, L, H, P) T: the output before the gate, saved by the
                                // training forward (the walk then forms dZ = y_v fz), or null
+  // The walk split into segments of seg_nc chunks (nseg > 1: grid (B*H, nseg)), for few
+  // (b, h) pairs.  Partials (pqb, pkb, pd, ctot) are then per (b, h, segment), and the
+  // walk of segment i starts from gin[bh][i] ([p][n] f32), the adjoint state after it.
+  int nseg = 1, seg_nc = 0;
+  float* gin = nullptr;        // [bh][nseg][P][N] adjoint entering each segment from the right
+  float* gloc = nullptr;       // [bh][nseg][P][N] each segment's own adjoint (segments 1..)
+  float* dseg = nullptr;       // [bh][nseg] each segment's total log-decay
 };
 
 // Per-chunk token constants shared by the adjoint and gradient kernels: lane = token.
@@ -245,80 +253,146 @@ struct AdjSmem {
   static constexpr int PAD = std::is_same<T, bf16>::value ? 8 : 4;
   alignas(16) T qt[CS][N + PAD];      // q~ of the chunk
   alignas(16) T dye[CS][P + PAD];     // e^{A_cum} dy
-  float ac[CS], gam[CS], scl[CS], dtv[CS];
-  float aend;
+  float qb[N];                         // the head's Q bias
 };
 
+// One chunk's inputs of the adjoint pass, requested a chunk ahead of their use (lane
+// = token; the wave's Q groups g = wave + 8 k and dOut/Z groups likewise).  Every load
+// is unconditional, from a clamped valid address: lanes past the sequence end read the
+// last token's row, and their values are ignored (dt = 0 there makes their angle
+// increments 0, and their q~ and dy are stored as zeros).
 template <typename T, int CS, int N, int P, int R>
+struct AdjLoads {
+  static constexpr int GQ = (N / 8 + kBwdWaves - 1) / kBwdWaves;
+  static constexpr int GV = (P / 8 + kBwdWaves - 1) / kBwdWaves;
+  Vec8<T> q[GQ], dy[GV], z[GV];
+  float4 rt[GQ], th[GQ];
+  float adt, dt;
+  __device__ __forceinline__ void issue(const BwdArgs& a, int c, int bh, int wave, int lane) {
+    const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, b = bh / H, h = bh % H, hq = h / (H / HQ);
+    const int t = min(c * CS + (lane & (CS - 1)), L - 1);
+    adt = a.s.adt[(long)bh * L + t];
+    dt = a.s.dt[(long)bh * L + t];
+#pragma unroll
+    for (int k = 0; k < GQ; ++k) {
+      const int g = min(wave + kBwdWaves * k, N / 8 - 1);
+      q[k].load(reinterpret_cast<const T*>(a.s.q) + (((long)b * L + t) * HQ + hq) * N + 8 * g);
+      rt[k] = th[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (R > 0) {
+        const int gr = min(g, R / 4 - 1);
+        const long arow = a.s.ang_shared ? (long)b * L + t : ((long)b * L + t) * H + h;
+        rt[k] = *reinterpret_cast<const float4*>(a.s.ang + arow * R + 4 * gr);
+        th[k] = *reinterpret_cast<const float4*>(a.th0 + ((long)bh * a.nc + c) * R + 4 * gr);
+      }
+    }
+    const T* gdo = reinterpret_cast<const T*>(a.dout);
+    const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) : gdo;
+#pragma unroll
+    for (int k = 0; k < GV; ++k) {
+      const int g = min(wave + kBwdWaves * k, P / 8 - 1);
+      const long row = (((long)b * L + t) * H + h) * P + 8 * g;
+      dy[k].load(gdo + row);
+      z[k].load(gz + row);
+    }
+  }
+};
+
+// SEG: the split walk's adjoint-only pass.  Block (bh, i) walks segment i + 1's chunks
+// from a zero adjoint and leaves the segment's own adjoint state, sum over its tokens
+// of e^{A_t - A(segment start)} dy_t (x) q~_t, in gloc ([p][n] f32), and its total
+// log-decay in dseg; no per-chunk states are stored.
+template <typename T, int CS, int N, int P, int R, bool SEG>
 __global__ __launch_bounds__(kBwdThreads, 1)
 void scan_adjoint_kernel(BwdArgs a) {
   typedef MF16<T> W;
   typedef AdjSmem<T, CS, N, P, R> S;
+  typedef AdjLoads<T, CS, N, P, R> Loads;
   __shared__ S sm;
   constexpr int PAD = S::PAD, KS = W::KSTEP;
   constexpr int NTILE = (P / 16) * (N / 16), TPW = (NTILE + kBwdWaves - 1) / kBwdWaves;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bh = blockIdx.x, b = bh / a.s.H, h = bh % a.s.H;
-  const int hq = h / (a.s.H / a.s.Hqk);
-  const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
-  const T* gq = reinterpret_cast<const T*>(a.s.q);
-  const T* gdo = reinterpret_cast<const T*>(a.dout);
-  const T* gz = reinterpret_cast<const T*>(a.s.z);
+  const int bh = blockIdx.x, h = bh % a.s.H;
+  const int L = a.s.L, nc = a.nc;
+  const int seg = SEG ? (int)blockIdx.y + 1 : 0;
+  const int c_lo = SEG ? seg * a.seg_nc : 0, c_hi = SEG ? min(nc, c_lo + a.seg_nc) : nc;
+  const bool has_z = a.s.z != nullptr;
   T* gs = reinterpret_cast<T*>(a.gs);
+  for (int i = tid; i < N; i += kBwdThreads) sm.qb[i] = a.s.qbias[(long)h * N + i];
 
   f32x4 G[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) G[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float logdec = 0.0f;                                 // SEG: the segment's total log-decay
 
-  for (int c = nc - 1; c >= 0; --c) {
+  Loads cur;
+  cur.issue(a, c_hi - 1, bh, wave, lane);
+  __syncthreads();                                     // the biases
+  for (int c = c_hi - 1; c >= c_lo; --c) {
     const int t0 = c * CS;
     // adjoint state beyond chunk c, [n][p]
+    if constexpr (!SEG) {
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int tile = wave + kBwdWaves * i;
-      if (tile < NTILE) {
-        const int pt = tile / (N / 16), nt = tile % (N / 16);
-        const int n = 16 * nt + (lane & 15), p = 16 * pt + 4 * (lane >> 4);
-        const float gv[4] = {G[i][0], G[i][1], G[i][2], G[i][3]};
-        store4(gs + (((long)bh * nc + c) * N + n) * P + p, gv);
-      }
-    }
-    if (wave == 0) chunk_scalars<CS>(a, bh, t0, lane, sm.ac, sm.gam, sm.scl, sm.dtv, &sm.aend);
-    __syncthreads();
-    const bool tok = lane < CS && t0 + lane < L;
-    const float dtl = tok ? a.s.dt[(long)bh * L + t0 + lane] : 0.0f;
-    for (int g = wave; g < N / 8; g += kBwdWaves) {
-      float q[8] = {0, 0, 0, 0, 0, 0, 0, 0}, th4[4];
-      group_theta<CS, R>(a, bh, c, g, group_rates<CS, R>(a, b, h, t0, g, lane), dtl, th4);
-      if (tok) {
-        load8(gq + (((long)b * L + t0 + lane) * HQ + hq) * N + 8 * g, q);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) q[e] += a.s.qbias[(long)h * N + 8 * g + e];
-        rope8<R>(q, th4, g, 1.0f);
-      }
-      if (lane < CS) store8(&sm.qt[lane][8 * g], q);
-    }
-    for (int g = wave; g < P / 8; g += kBwdWaves) {
-      float dy[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (tok) {
-        const long row = (((long)b * L + t0 + lane) * H + h) * P + 8 * g;
-        load8(gdo + row, dy);
-        if (gz) {
-          float z[8];
-          load8(gz + row, z);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dy[e] *= z[e] / (1.0f + expf(-z[e]));
+      for (int i = 0; i < TPW; ++i) {
+        const int tile = wave + kBwdWaves * i;
+        if (tile < NTILE) {
+          const int pt = tile / (N / 16), nt = tile % (N / 16);
+          const int n = 16 * nt + (lane & 15), p = 16 * pt + 4 * (lane >> 4);
+          const float gv[4] = {G[i][0], G[i][1], G[i][2], G[i][3]};
+          store4(gs + (((long)bh * nc + c) * N + n) * P + p, gv);
         }
-        const float ea = expf(sm.ac[lane]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dy[e] *= ea;
       }
-      if (lane < CS) store8(&sm.dye[lane][8 * g], dy);
     }
+    // lane = token; every wave forms the chunk's decay prefix itself
+    const bool tok = lane < CS && t0 + lane < L;
+    const float dtl = tok ? cur.dt : 0.0f;
+    const float acum = wave_incl_scan(tok ? cur.adt : 0.0f);
+    const float aend = __shfl(acum, CS - 1, 64);
+#pragma unroll
+    for (int k = 0; k < Loads::GQ; ++k) {
+      const int g = wave + kBwdWaves * k;
+      if (g < N / 8) {
+        float q[8], th4[4];
+        cur.q[k].to_f(q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) th4[j] = 0.0f;
+        if constexpr (R > 0) {
+          if (4 * g < R) {
+            const float rv[4] = {cur.rt[k].x, cur.rt[k].y, cur.rt[k].z, cur.rt[k].w};
+            const float t0c[4] = {cur.th[k].x, cur.th[k].y, cur.th[k].z, cur.th[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (4 * g + j < R) th4[j] = __builtin_amdgcn_fractf(t0c[j] + wave_incl_scan(angle_step(rv[j], dtl)));
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = tok ? q[e] + sm.qb[8 * g + e] : 0.0f;
+        rope8<R>(q, th4, g, 1.0f);
+        if (lane < CS) store8(&sm.qt[lane][8 * g], q);
+      }
+    }
+    const float ea = tok ? expf(acum) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < Loads::GV; ++k) {
+      const int g = wave + kBwdWaves * k;
+      if (g < P / 8) {
+        float dy[8], z[8];
+        cur.dy[k].to_f(dy);
+        cur.z[k].to_f(z);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (has_z) dy[e] *= z[e] / (1.0f + expf(-z[e]));
+          dy[e] *= ea;
+        }
+        if (lane < CS) store8(&sm.dye[lane][8 * g], dy);
+      }
+    }
+    // every use of this chunk's loads is above: request the next chunk's
+    if (c > c_lo) cur.issue(a, c - 1, bh, wave, lane);
     __syncthreads();
     // G <- e^{A_end} G + sum_t e^{A_cum,t} dy_t (x) q~_t
-    const float dec = expf(sm.aend);
+    const float dec = expf(aend);
+    logdec += aend;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int tile = wave + kBwdWaves * i;
@@ -333,6 +407,36 @@ void scan_adjoint_kernel(BwdArgs a) {
       }
     }
     __syncthreads();
+  }
+  if constexpr (SEG) {
+    const long slot = (long)bh * a.nseg + seg;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = wave + kBwdWaves * i;
+      if (tile < NTILE) {
+        const int pt = tile / (N / 16), nt = tile % (N / 16);
+        const int n = 16 * nt + (lane & 15), p = 16 * pt + 4 * (lane >> 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a.gloc[(slot * P + p + r) * N + n] = G[i][r];
+      }
+    }
+    if (tid == 0) a.dseg[slot] = logdec;
+  }
+}
+
+// The split walk's combine, thread = adjoint element (p, n) of one (b, h): the adjoint
+// entering segment i from the right is G_i = gloc_{i+1} + e^{dseg_{i+1}} G_{i+1}, with
+// G_{nseg-1} = 0 (the last segment's walk starts from zero and reads nothing).
+__global__ __launch_bounds__(256)
+void seg_adjoint_combine_kernel(BwdArgs a) {
+  const int bh = blockIdx.y, PN = a.s.P * a.s.N;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= PN) return;
+  const long s0 = (long)bh * a.nseg;
+  float g = 0.0f;
+  for (int i = a.nseg - 2; i >= 0; --i) {
+    g = a.gloc[(s0 + i + 1) * PN + e] + expf(a.dseg[s0 + i + 1]) * g;
+    a.gin[(s0 + i) * PN + e] = g;
   }
 }
 
@@ -1062,6 +1166,11 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
   const bool qkw = wave < GH;
   const int bh = blockIdx.x, b = bh / H, h = bh % H, hq = h / (H / HQ);
+  // the chunks of this block's segment (the whole sequence without the split) and the
+  // slot of its partial sums
+  const int seg = blockIdx.y;
+  const int c_lo = a.nseg > 1 ? seg * a.seg_nc : 0, c_hi = a.nseg > 1 ? min(nc, c_lo + a.seg_nc) : nc;
+  const long ps = (long)bh * a.nseg + seg;
   const T* gz = reinterpret_cast<const T*>(a.s.z);
   const float Dh = a.s.D ? a.s.D[h] : 0.0f;
   T* const smk = sm.smk();
@@ -1072,6 +1181,19 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   f32x4 G[TPW];                                        // adjoint state tiles [p][n]
 #pragma unroll
   for (int i = 0; i < TPW; ++i) G[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.nseg > 1 && seg + 1 < a.nseg) {
+    // the adjoint state after this segment, which the later segments leave
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = wave + kBwdWaves * i;
+      if (tile < NTILE) {
+        const int n = 16 * (tile % NT) + (lane & 15), p = 16 * (tile / NT) + 4 * (lane >> 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) G[i][r] = a.gin[(ps * P + p + r) * N + n];
+      }
+    }
+  }
   // Bias gradients: per pass (q~ half 0, half 1, k~ half 0, half 1), thread (n, tg) sums
   // column n of the half over the tokens of its token group tg, over the whole walk.
   constexpr int TPG = CS * NH / kBwdThreads;           // tokens per group
@@ -1105,14 +1227,14 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   Loads cur;
   {
     const int tid = threadIdx.x;
-    cur.issue_all(a, nc - 1, bh, tid, wave, tid & 63);
+    cur.issue_all(a, c_hi - 1, bh, tid, wave, tid & 63);
     // the head's biases into LDS (read by every chunk's preparation)
     if (tid < N) {
       sm.qb[tid] = a.s.qbias[(long)h * N + tid];
       sm.kb[tid] = a.s.kbias[(long)h * N + tid];
     }
   }
-  for (int c = nc - 1; c >= 0; --c) {
+  for (int c = c_hi - 1; c >= c_lo; --c) {
     // lane and thread indices made opaque per chunk, so that the compiler forms the
     // lane-dependent LDS and global addresses inside the chunk instead of hoisting them
     // all out of the walk and keeping each live in a register for the whole loop
@@ -1333,7 +1455,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         dsum += sm.dqk[lane];                         // padding tokens hold dy = 0
       }
     }
-    if (c > 0) cur.template issue<0>(a, c - 1, bh, tid, wave, lane);   // every use of chunk c's loads is above
+    if (c > c_lo) cur.template issue<0>(a, c - 1, bh, tid, wave, lane);   // every use of chunk c's loads is above
 
     // ---- S = q~ k~^T and dP = dy v^T, masked (s < t) and decayed e^{A_t - A_s}.  Each
     // wave's tiles form a fixed number of iterations without branches (the tiles above
@@ -1367,7 +1489,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       store4(dst + t * (CS + PAD) + s0, val);
     }
     __syncthreads();
-    if (c > 0) cur.template issue<1>(a, c - 1, bh, tid, wave, lane);
+    if (c > c_lo) cur.template issue<1>(a, c - 1, bh, tid, wave, lane);
 
     // ---- y (for dZ) and dV as transposed 16 x 16 tiles [p][token]: each lane holds 4
     // consecutive p of one token, written to the output tiles in LDS
@@ -1533,7 +1655,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
       for (int i = 0; i < TPW; ++i) G[i] = acc[i];
     }
-    if (c > 0) cur.template issue<2>(a, c - 1, bh, tid, wave, lane);
+    if (c > c_lo) cur.template issue<2>(a, c - 1, bh, tid, wave, lane);
 
     // ---- dq~ then dk~, half the columns at a time, each followed by its chain rule
     // (passes: q~ half 0, q~ half 1, k~ half 0, k~ half 1)
@@ -1852,7 +1974,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         } else if (q < 7) {
           quarter_mfma(q + 1, sm.rq((q + 1) & 1), std::true_type());
         }
-        if (q == 3 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
+        if (q == 3 && c > c_lo) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
         // the tiles read above are written two quarters on; the last quarter's
         // per-token sums are read by the dA below
         __syncthreads();
@@ -1873,7 +1995,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         if (pass < 3) pass_mfma(pass + 1, rbuf[(pass + 1) & 1]);
         pass_regs(pass);
         chain_compute(pass, dx, sc, gqk);
-        if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
+        if (pass == 1 && c > c_lo) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
         // the tile read above is written by pass p + 2's products; the last pass's
         // per-token sums are read by the dA below
         __syncthreads();
@@ -1940,7 +2062,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           }
         }
         // (bf16) the next pass writes res and lo after its residual barrier
-        if (pass == 1 && c > 0) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
+        if (pass == 1 && c > c_lo) cur.template issue<3>(a, c - 1, bh, tid, wave, lane);
       }
     }
 
@@ -1985,7 +2107,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         v += __shfl_xor(v, 1, 64);
         v += __shfl_xor(v, 2, 64);
         v += __shfl_xor(v, 4, 64);
-        if ((lane & 7) == 0) (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + 8 * wave + (lane >> 3)] = v;
+        if ((lane & 7) == 0) (pass < 2 ? a.pqb : a.pkb)[ps * N + (pass & 1) * NH + 8 * wave + (lane >> 3)] = v;
       }
     } else if constexpr (kDirect) {
       // sums over the token lanes (the lanes of one hf hold the same columns)
@@ -1999,7 +2121,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
             for (int m = 1; m < CS; m <<= 1) v += __shfl_xor(v, m, 64);
             if (tkn == 0)
-              (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + 8 * wave + EL * hf + e] = v;
+              (pass < 2 ? a.pqb : a.pkb)[ps * N + (pass & 1) * NH + 8 * wave + EL * hf + e] = v;
           }
       }
     } else {
@@ -2012,7 +2134,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         if (tid < NH) {
           float s = 0.0f;
           for (int i = 0; i < kBwdThreads / NH; ++i) s += res[i * (NH + 4) + tid];
-          (pass < 2 ? a.pqb : a.pkb)[(long)bh * N + (pass & 1) * NH + tid] = s;
+          (pass < 2 ? a.pqb : a.pkb)[ps * N + (pass & 1) * NH + tid] = s;
         }
       }
     }
@@ -2023,14 +2145,14 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
         for (int j = 0; j < PRS; ++j) {
           const int r = 4 * (hh * GH + wave) + PRS * hf + j;
-          if (r < R && tkn == 0) a.ctot[(long)bh * (R + 1) + 1 + r] = cth[hh][j];
+          if (r < R && tkn == 0) a.ctot[ps * (R + 1) + 1 + r] = cth[hh][j];
         }
     }
     if (wave == kQkWave) {
       const float tot = wave_sum(dsum);
-      if (lane == 0 && a.pd) a.pd[bh] = tot;
+      if (lane == 0 && a.pd) a.pd[ps] = tot;
     }
-    if (wave == kDaWave && lane == 0) a.ctot[(long)bh * (R + 1)] = cda;
+    if (wave == kDaWave && lane == 0) a.ctot[ps * (R + 1)] = cda;
   }
 }
 
@@ -2046,17 +2168,28 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 // Then dAngles = S pi dt (1 - tanh^2 rate), the angle part of dDT = pi sum_r S tanh,
 // du_t = d(scale)_{t-1}, dDT = dgamma sigmoid + du (1 - sigmoid) + angle part and
 // dTrap = (dgamma - du) dt sigmoid (1 - sigmoid).
+// With the walk split into segments, dADT and dAngles hold each segment's own suffix
+// sums and ctot each segment's totals: S_t adds the totals of the later segments
+// (off), and T is the sum over all segments.
 template <int CS>
 __global__ __launch_bounds__(256)
 void scan_bwd_walk_finish_kernel(BwdArgs a) {
-  __shared__ float tot[65];
+  __shared__ float tot[65], off[65];
   __shared__ float dts[CS], angp[CS];
   const int tid = threadIdx.x;
   const int c = blockIdx.x, bh = blockIdx.y, b = bh / a.s.H, h = bh % a.s.H;
   const int L = a.s.L, H = a.s.H, R = a.s.R;
   const int t0 = c * CS, nt = min(CS, L - t0);
-  const float* ct = a.ctot + (long)bh * (R + 1);
-  if (tid <= R) tot[tid] = ct[tid];
+  if (tid <= R) {
+    const int nseg = a.nseg, seg = nseg > 1 ? c / a.seg_nc : 0;
+    const float* ct = a.ctot + (long)bh * nseg * (R + 1) + tid;
+    float later = 0.0f;
+    for (int j = nseg - 1; j > seg; --j) later += ct[(long)j * (R + 1)];
+    float all = later;
+    for (int j = seg; j >= 0; --j) all += ct[(long)j * (R + 1)];
+    off[tid] = later;
+    tot[tid] = all;
+  }
   if (tid < CS) {
     dts[tid] = tid < nt ? a.s.dt[(long)bh * L + t0 + tid] : 0.0f;
     angp[tid] = 0.0f;
@@ -2080,7 +2213,7 @@ void scan_bwd_walk_finish_kernel(BwdArgs a) {
         const float f = kPi * dts[tt];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float v = sv[j] - tot[1 + 4 * q + j] * w;
+          const float v = (sv[j] + off[1 + 4 * q + j]) - tot[1 + 4 * q + j] * w;
           const float tn = tanhf(rv[j]);
           sv[j] = v * f * (1.0f - tn * tn);
           part += v * tn;
@@ -2102,7 +2235,7 @@ void scan_bwd_walk_finish_kernel(BwdArgs a) {
     const float du = t > 0 ? a.dsc[o - 1] : 0.0f;
     const float dg = a.ddt[o];
     const float sg = 1.0f / (1.0f + expf(-a.s.trap[o]));
-    a.dadt[o] -= tot[0] * (float)(L - t) / (float)L;
+    a.dadt[o] = (a.dadt[o] + off[0]) - tot[0] * (float)(L - t) / (float)L;
     a.ddt[o] = dg * sg + du * (1.0f - sg) + angp[tid];
     a.dtrap[o] = (dg - du) * dt * sg * (1.0f - sg);
   }
@@ -2280,7 +2413,7 @@ __global__ void scan_bwd_gqa_kernel(BwdArgs a) {
 size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct BwdWs {
-  size_t hs, gs, th, pqb, pkb, pd, dsc, ctot, dqh, dkh, dangh, total;
+  size_t hs, gs, th, pqb, pkb, pd, dsc, ctot, dqh, dkh, dangh, gin, gloc, dseg, split, total;
 };
 
 // Route of the backward.  The reverse walk runs one workgroup per (b, h), so it fills
@@ -2291,13 +2424,37 @@ struct BwdWs {
 // H=24) and 128 (1.12 / 1.54 ms), the chunks at 32 (2.11 / 1.60 ms at L=8192).  The
 // environment variable M3_BWD_ROUTE = "walk" or "chunks" forces one of them (tests,
 // measurements).
+// Below kWalkMinBH pairs the walk is split into sequence segments when the sequence
+// has at least two segments of kWalkMinSegChunks chunks: about kWalkTargetBlocks
+// workgroups (one wave of blocks on the chip), each walking its segment from the
+// adjoint state that the later segments leave (an adjoint-only pass per segment and a
+// reverse combine, the backward's form of the forward's sequence split).  Shorter
+// sequences take the chunk-parallel route.  M3_BWD_ROUTE = "segments" forces the split
+// walk (segments of at least two chunks), "walk" the one-segment walk.
 constexpr long kWalkMinBH = 80;
-bool bwd_walk(int B, int H) {
+constexpr int kWalkTargetBlocks = 256;
+constexpr int kWalkMinSegChunks = 4;
+struct BwdRoute {
+  bool walk;
+  int nseg, seg_nc;
+};
+BwdRoute bwd_route(int B, int H, int L, int CS) {
+  const long bh = (long)B * H, nc = (L + CS - 1) / CS;
+  auto split = [&](int min_chunks) {
+    const long s = std::min<long>(kWalkTargetBlocks / std::max<long>(bh, 1), nc / min_chunks);
+    if (s < 2) return BwdRoute{true, 1, (int)nc};
+    const int seg_nc = (int)((nc + s - 1) / s);
+    return BwdRoute{true, (int)((nc + seg_nc - 1) / seg_nc), seg_nc};
+  };
   const char* e = getenv("M3_BWD_ROUTE");
-  if (e && !strcmp(e, "walk")) return true;
-  if (e && !strcmp(e, "chunks")) return false;
-  return (long)B * H >= kWalkMinBH;
+  if (e && !strcmp(e, "walk")) return {true, 1, (int)nc};
+  if (e && !strcmp(e, "chunks")) return {false, 1, (int)nc};
+  if (e && !strcmp(e, "segments")) return split(2);
+  if (bh >= kWalkMinBH) return {true, 1, (int)nc};
+  const BwdRoute r = split(kWalkMinSegChunks);
+  return r.nseg > 1 ? r : BwdRoute{false, 1, (int)nc};
 }
+bool bwd_walk(int B, int H, int L, int CS) { return bwd_route(B, H, L, CS).walk; }
 
 // The chunk states and angles the backward reads: computed by its own state-only pass
 // (in the workspace), or saved by the training forward (scan_bwd_saved_bytes, in the
@@ -2316,7 +2473,8 @@ size_t saved_th_bytes(bool bf16_io, int B, int L, int H, int R) {
 BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R, bool ang_shared,
                  bool saved = false) {
   const int CS = bf16_io ? 64 : 32;
-  const bool walk = bwd_walk(B, H);
+  const BwdRoute route = bwd_route(B, H, L, CS);
+  const bool walk = route.walk;
   const long nc = (L + CS - 1) / CS, bhc = (long)B * H * nc;
   const size_t ts = bf16_io ? 2 : 4;
   BwdWs w;
@@ -2334,6 +2492,14 @@ BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R
   w.dqh = gqa ? take((size_t)B * L * H * N * 4) : 0;
   w.dkh = gqa ? take((size_t)B * L * H * N * 4) : 0;
   w.dangh = ang_shared && R > 0 ? take((size_t)B * L * H * R * 4) : 0;      // per-head dAngles
+  // the split walk: the segments' adjoint states and log-decays
+  const size_t bhs = (size_t)B * H * route.nseg;
+  w.gin = route.nseg > 1 ? take(bhs * P * N * 4) : 0;
+  w.gloc = route.nseg > 1 ? take(bhs * P * N * 4) : 0;
+  w.dseg = route.nseg > 1 ? take(bhs * 4) : 0;
+  // the state-only pass split across compute units (few pairs, long sequences)
+  const size_t sp = saved ? 0 : scan_split_ws_bytes(bf16_io, B, L, H, N, P, R, 64);
+  w.split = sp ? take(sp) : 0;
   w.total = off;
   return w;
 }
@@ -2398,6 +2564,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   const ScanArgs& s = g.fwd;
   const int CS = bf16_io ? 64 : 32;
   const BwdWs w = bwd_layout(bf16_io, s.B, s.L, s.H, s.Hqk, s.N, s.P, s.R, s.ang_shared != 0, saved != nullptr);
+  const BwdRoute route = bwd_route(s.B, s.H, s.L, CS);
   char* base = reinterpret_cast<char*>(ws);
   BwdArgs a;
   a.s = s;
@@ -2417,12 +2584,12 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
     a.th0 = sth;
     // the float32 walk reads the saved output before the gate (the chunk-parallel
     // route and bf16 recompute it)
-    if (s.z && !bf16_io && bwd_walk(s.B, s.H)) a.yv = syv;
+    if (s.z && !bf16_io && route.walk) a.yv = syv;
   } else {
     a.hs = base + w.hs;
     a.th0 = reinterpret_cast<float*>(base + w.th);
   }
-  a.gs = bwd_walk(s.B, s.H) ? nullptr : base + w.gs;
+  a.gs = route.walk ? nullptr : base + w.gs;
   a.pqb = reinterpret_cast<float*>(base + w.pqb);
   a.pkb = reinterpret_cast<float*>(base + w.pkb);
   a.pd = reinterpret_cast<float*>(base + w.pd);
@@ -2431,8 +2598,16 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.dsc = reinterpret_cast<float*>(base + w.dsc);
   a.ctot = reinterpret_cast<float*>(base + w.ctot);
   a.nc = (s.L + CS - 1) / CS;
+  a.nseg = route.nseg;
+  a.seg_nc = route.seg_nc;
+  if (route.nseg > 1) {
+    a.gin = reinterpret_cast<float*>(base + w.gin);
+    a.gloc = reinterpret_cast<float*>(base + w.gloc);
+    a.dseg = reinterpret_cast<float*>(base + w.dseg);
+  }
 
-  // 1. chunk states and angles (the forward's state-only pass), unless saved
+  // 1. chunk states and angles (the forward's state-only pass, split across compute
+  // units for few pairs and long sequences), unless saved
   hipError_t e = hipSuccess;
   if (!saved) {
     ScanArgs p1 = s;
@@ -2443,17 +2618,26 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
     p1.fin_logdec = nullptr;
     p1.chunk_h = base + w.hs;
     p1.chunk_th = s.R > 0 ? reinterpret_cast<float*>(base + w.th) : nullptr;
-    e = scan_state_launch(p1, bf16_io, st);
+    e = w.split ? scan_split_state_launch(p1, bf16_io, base + w.split, st) : scan_state_launch(p1, bf16_io, st);
     if (e != hipSuccess) return e;
   }
 
   const dim3 grid_bh(s.B * s.H), grid_c(a.nc, s.B * s.H);
   bool found = false;
-  if (bwd_walk(s.B, s.H)) {
+  if (route.walk) {
 #define X(T, cs, n, p, r)                                                                                  \
   if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
     found = true;                                                                                          \
-    launch_walk<T, cs, n, p, r>(grid_bh, st, a);                                                           \
+    if (a.nseg > 1) {                                                                                      \
+      /* each later segment's own adjoint, then the adjoint entering every segment */                     \
+      hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r, true>), dim3(s.B * s.H, a.nseg - 1),         \
+                         dim3(kBwdThreads), 0, st, a);                                                     \
+      if ((e = hipGetLastError()) != hipSuccess) return e;                                                 \
+      hipLaunchKernelGGL(seg_adjoint_combine_kernel, dim3((s.P * s.N + 255) / 256, s.B * s.H), dim3(256),   \
+                         0, st, a);                                                                        \
+      if ((e = hipGetLastError()) != hipSuccess) return e;                                                 \
+    }                                                                                                      \
+    launch_walk<T, cs, n, p, r>(dim3(s.B * s.H, a.nseg), st, a);                                           \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
     if (a.dqh) {                                                                                           \
       hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \
@@ -2471,14 +2655,14 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     BwdArgs ar = a;
-    ar.nc = 1;                                   // one bias/D partial per (b, h)
+    ar.nc = a.nseg;                              // one bias/D partial per (b, h, segment)
     hipLaunchKernelGGL(scan_bwd_reduce_kernel, dim3(s.H, (s.N + 15) / 16), dim3(256), 0, st, ar);
     return hipGetLastError();
   }
 #define X(T, cs, n, p, r)                                                                                  \
   if (!found && (std::is_same<T, bf16>::value == bf16_io) && s.N == n && s.P == p && s.R == r) {           \
     found = true;                                                                                          \
-    hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r>), grid_bh, dim3(kBwdThreads), 0, st, a);       \
+    hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r, false>), grid_bh, dim3(kBwdThreads), 0, st, a); \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
     hipLaunchKernelGGL((scan_bwd_chunk_kernel<T, cs, n, p, r>), grid_c, dim3(kBwdThreads), 0, st, a);      \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \

@@ -193,4 +193,41 @@ hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStrea
   return scan_chunked_launch(p3, bf16_io, st);
 }
 
+hipError_t scan_split_state_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStream_t st) {
+  const int len = seg_len_for(a.B, a.H, a.L);
+  const int nseg = (a.L + len - 1) / len;
+  const long bhs = (long)a.B * a.H * nseg;
+  Carries loc, in;
+  carve(reinterpret_cast<char*>(ws), bhs, a.N, a.P, a.R, &loc, &in);
+
+  ScanArgs p1 = a;                                   // pass 1: exit carries from a zero carry
+  p1.seg_len = len;
+  p1.init_theta = p1.init_h = p1.init_k = p1.init_v = nullptr;
+  p1.fin_h = loc.h; p1.fin_k = loc.k; p1.fin_v = loc.v; p1.fin_theta = a.R > 0 ? loc.th : nullptr;
+  p1.fin_logdec = loc.ld;
+  p1.init_per_seg = 0;
+  p1.fin_per_seg = 1;
+  p1.chunk_h = nullptr;
+  p1.chunk_th = nullptr;
+  hipError_t e = scan_state_launch(p1, bf16_io, st);
+  if (e != hipSuccess) return e;
+
+  ScanArgs p2 = a;                                   // pass 2: entering carries (none from the caller)
+  p2.seg_len = len;
+  p2.init_theta = p2.init_h = p2.init_k = p2.init_v = nullptr;
+  hipLaunchKernelGGL(seg_combine_kernel, dim3((a.P * a.N + kCombineThreads - 1) / kCombineThreads, a.B * a.H),
+                     dim3(kCombineThreads), 0, st, p2, nseg, loc, in);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+
+  ScanArgs p3 = a;                                   // pass 3: the states entering every chunk
+  p3.seg_len = len;
+  p3.init_h = in.h; p3.init_k = in.k; p3.init_v = in.v; p3.init_theta = a.R > 0 ? in.th : nullptr;
+  p3.init_per_seg = 1;
+  p3.fin_theta = p3.fin_h = p3.fin_k = p3.fin_v = nullptr;
+  p3.fin_logdec = nullptr;
+  p3.fin_per_seg = 0;
+  return scan_state_launch(p3, bf16_io, st);
+}
+
 }  // namespace m3

@@ -32,10 +32,12 @@ def pytest_collection_modifyitems(config, items):
             item.add_marker(skip)
 
 
-@pytest.fixture(params=["chunks", "walk"])
+@pytest.fixture(params=["chunks", "walk", "segments"])
 def bwd_route(request, monkeypatch):
-    """Runs a backward test on both routes of the library's backward: the
-    chunk-parallel kernels and the reverse walk (the library reads M3_BWD_ROUTE at
-    each call; unset, it picks by B * H)."""
+    """Runs a backward test on every route of the library's backward: the
+    chunk-parallel kernels, the reverse walk, and the walk split into sequence
+    segments (forced here down to segments of two chunks, so that the short test
+    sequences split too); the library reads M3_BWD_ROUTE at each call; unset, it
+    picks by B * H and the length."""
     monkeypatch.setenv("M3_BWD_ROUTE", request.param)
     return request.param

@@ -103,24 +103,61 @@ def test_split_workspace_sizes(lib):
     assert f(1, 1061, 3, 128, 64, 32, 64, bf) > 0
 
 
+def _walk_segments(B, H, L, cs):
+    """Segments of the backward's walk: one at 80 pairs or more; below, about 256
+    blocks of at least 4 chunks each when that gives two or more (else the
+    chunk-parallel route: 0)."""
+    nc = (L + cs - 1) // cs
+    if B * H >= 80:
+        return 1
+    s = min(256 // (B * H), nc // 4)
+    if s < 2:
+        return 0
+    seg_nc = (nc + s - 1) // s
+    return (nc + seg_nc - 1) // seg_nc
+
+
+def _split_ws(B, H, L, N, P, R):
+    """The sequence split's carries (test_split_workspace_sizes): two sets per
+    (b, h, segment) and one log-decay; 0 without a split."""
+    al = lambda n: (n * 4 + 255) // 256 * 256  # noqa: E731
+    bh = B * H
+    if bh * 2 > 256 or L < 512 or N != 128 or P != 64:
+        return 0
+    s = min(256 // bh, L // 256)
+    if s < 2:
+        return 0
+    ln = ((L + s - 1) // s + 127) // 128 * 128
+    nseg = (L + ln - 1) // ln
+    if nseg < 2:
+        return 0
+    bhs = bh * nseg
+    return 2 * (al(bhs * P * N) + al(bhs * N) + al(bhs * P) + al(bhs * max(R, 1))) + al(bhs)
+
+
 def _bwd_ws_expect(B, L, H, Hqk, N, P, R, io, saved=False):
     """Backward workspace: chunk-entering states (B*H*nc*P*N in the I/O type, 64-token
     chunks for bf16, 32 for fp32) and chunk angles (unless the training forward saved
-    them), adjoint states after each chunk (chunk-parallel route, B*H < 128, only),
-    bias and D partials, per-token d(scale), chunk sums of dA and d(theta), and
-    per-head dQ/dK (float32) when Hqk < H."""
+    them), adjoint states after each chunk (chunk-parallel route only), bias and D
+    partials, per-token d(scale), chunk sums of dA and d(theta), per-head dQ/dK
+    (float32) when Hqk < H, the split walk's segment adjoints (two float32 P x N
+    states per (b, h, segment) and a log-decay) and the split state pass's carries."""
     al = lambda n: (n + 255) // 256 * 256  # noqa: E731
     cs = 64 if io == 1 else 32
     bhc = B * H * ((L + cs - 1) // cs)
     ts = 2 if io == 1 else 4
-    walk = B * H >= 80
+    nseg = _walk_segments(B, H, L, cs)
     n = 2 * al(bhc * N * 4) + al(bhc * 4) + al(B * H * L * 4) + al(bhc * (R + 1) * 4)
     if not saved:
         n += al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4)
-    if not walk:
+    if nseg == 0:
         n += al(bhc * P * N * ts)
     if Hqk < H:
         n += 2 * al(B * L * H * N * 4)
+    if nseg > 1:
+        n += 2 * al(B * H * nseg * P * N * 4) + al(B * H * nseg * 4)
+    if not saved:
+        n += _split_ws(B, H, L, N, P, R)
     return n
 
 
@@ -130,10 +167,15 @@ def test_backward_workspace_sizes(lib, monkeypatch):
     bf, f32 = 1, 0
     assert f(8, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(8, 4096, 32, 32, 128, 64, 32, bf)
     assert f(2, 300, 4, 2, 64, 32, 16, 64, f32) == _bwd_ws_expect(2, 300, 4, 2, 64, 32, 16, f32)
-    # float32 at the model's geometry (what Mamba3SSM hands its scan), both routes
+    # float32 at the model's geometry (what Mamba3SSM hands its scan): the walk, and
+    # for few pairs the split walk and split state pass
     for B, H in ((8, 32), (1, 4)):
         for R in (32, 64):
             assert f(B, 4096, H, H, 128, 64, R, 64, f32) == _bwd_ws_expect(B, 4096, H, H, 128, 64, R, f32)
+    # config 3's shape: 8 walk segments of 64 chunks, 8 state-pass segments of 4096 tokens
+    assert _walk_segments(1, 32, 32768, 64) == 8
+    assert f(1, 32768, 32, 32, 128, 64, 32, 128, bf) == _bwd_ws_expect(1, 32768, 32, 32, 128, 64, 32, bf)
+    assert f(1, 200, 2, 2, 128, 64, 32, 64, bf) == _bwd_ws_expect(1, 200, 2, 2, 128, 64, 32, bf)  # chunks
     assert f(1, 100, 2, 2, 64, 16, 16, 64, bf) == 0        # headdim 16: no backward kernel
     assert f(1, 100, 2, 2, 128, 64, 32, 64, 7) == 0        # unknown dtype
     assert f(1, 100, 3, 2, 128, 64, 32, 64, bf) == 0       # H not a multiple of Hqk
