@@ -179,10 +179,12 @@ struct BwdArgs {
   // The walk split into segments of seg_nc chunks (nseg > 1: grid (B*H, nseg)), for few
   // (b, h) pairs.  Partials (pqb, pkb, pd, ctot) are then per (b, h, segment), and the
   // walk of segment i starts from gin[bh][i] ([p][n] f32), the adjoint state after it.
-  int nseg = 1, seg_nc = 0;
+  // The adjoint-only pass runs adj_sub sub-segments per walk segment (more workgroups
+  // in flight than the walk's one per segment).
+  int nseg = 1, seg_nc = 0, adj_sub = 1;
   float* gin = nullptr;        // [bh][nseg][P][N] adjoint entering each segment from the right
-  float* gloc = nullptr;       // [bh][nseg][P][N] each segment's own adjoint (segments 1..)
-  float* dseg = nullptr;       // [bh][nseg] each segment's total log-decay
+  float* gloc = nullptr;       // [bh][nseg * adj_sub][P][N] each sub-segment's own adjoint
+  float* dseg = nullptr;       // [bh][nseg * adj_sub] each sub-segment's total log-decay
 };
 
 // Per-chunk token constants shared by the adjoint and gradient kernels: lane = token.
@@ -297,12 +299,13 @@ struct AdjLoads {
   }
 };
 
-// SEG: the split walk's adjoint-only pass.  Block (bh, i) walks segment i + 1's chunks
-// from a zero adjoint and leaves the segment's own adjoint state, sum over its tokens
-// of e^{A_t - A(segment start)} dy_t (x) q~_t, in gloc ([p][n] f32), and its total
-// log-decay in dseg; no per-chunk states are stored.
+// SEG: the split walk's adjoint-only pass.  Block (bh, j) walks sub-segment j + adj_sub
+// (sub-segment k of walk segment i is number i adj_sub + k; those of walk segment 0
+// are never needed) from a zero adjoint and leaves its own adjoint state, sum over its
+// tokens of e^{A_t - A(sub-segment start)} dy_t (x) q~_t, in gloc ([p][n] f32), and its
+// total log-decay in dseg; no per-chunk states are stored.  Two blocks fit a CU.
 template <typename T, int CS, int N, int P, int R, bool SEG>
-__global__ __launch_bounds__(kBwdThreads, 1)
+__global__ __launch_bounds__(kBwdThreads, SEG ? 2 : 1)
 void scan_adjoint_kernel(BwdArgs a) {
   typedef MF16<T> W;
   typedef AdjSmem<T, CS, N, P, R> S;
@@ -314,8 +317,13 @@ void scan_adjoint_kernel(BwdArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh = blockIdx.x, h = bh % a.s.H;
   const int L = a.s.L, nc = a.nc;
-  const int seg = SEG ? (int)blockIdx.y + 1 : 0;
-  const int c_lo = SEG ? seg * a.seg_nc : 0, c_hi = SEG ? min(nc, c_lo + a.seg_nc) : nc;
+  // SEG: sub-segment j of the walk's segments; its chunks (none when a short last
+  // walk segment leaves it empty)
+  const int sub = SEG ? (int)blockIdx.y + a.adj_sub : 0;
+  const int sub_nc = (a.seg_nc + a.adj_sub - 1) / a.adj_sub;
+  const int s0 = (sub / a.adj_sub) * a.seg_nc, s1 = min(nc, s0 + a.seg_nc);
+  const int c_lo = SEG ? min(s1, s0 + (sub % a.adj_sub) * sub_nc) : 0;
+  const int c_hi = SEG ? min(s1, c_lo + sub_nc) : nc;
   const bool has_z = a.s.z != nullptr;
   T* gs = reinterpret_cast<T*>(a.gs);
   for (int i = tid; i < N; i += kBwdThreads) sm.qb[i] = a.s.qbias[(long)h * N + i];
@@ -326,7 +334,7 @@ void scan_adjoint_kernel(BwdArgs a) {
   float logdec = 0.0f;                                 // SEG: the segment's total log-decay
 
   Loads cur;
-  cur.issue(a, c_hi - 1, bh, wave, lane);
+  if (c_hi > c_lo) cur.issue(a, c_hi - 1, bh, wave, lane);
   __syncthreads();                                     // the biases
   for (int c = c_hi - 1; c >= c_lo; --c) {
     const int t0 = c * CS;
@@ -409,7 +417,7 @@ void scan_adjoint_kernel(BwdArgs a) {
     __syncthreads();
   }
   if constexpr (SEG) {
-    const long slot = (long)bh * a.nseg + seg;
+    const long slot = (long)bh * a.nseg * a.adj_sub + sub;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int tile = wave + kBwdWaves * i;
@@ -424,19 +432,21 @@ void scan_adjoint_kernel(BwdArgs a) {
   }
 }
 
-// The split walk's combine, thread = adjoint element (p, n) of one (b, h): the adjoint
-// entering segment i from the right is G_i = gloc_{i+1} + e^{dseg_{i+1}} G_{i+1}, with
-// G_{nseg-1} = 0 (the last segment's walk starts from zero and reads nothing).
+// The split walk's combine, thread = adjoint element (p, n) of one (b, h): walking the
+// sub-segments from the last, g_j = gloc_j + e^{dseg_j} g_{j+1} is the adjoint after
+// sub-segment j - 1, so at the first sub-segment of walk segment i + 1 it is the
+// adjoint entering walk segment i from the right (the last walk segment starts from
+// zero and reads nothing).
 __global__ __launch_bounds__(256)
 void seg_adjoint_combine_kernel(BwdArgs a) {
-  const int bh = blockIdx.y, PN = a.s.P * a.s.N;
+  const int bh = blockIdx.y, PN = a.s.P * a.s.N, k = a.adj_sub;
   const int e = blockIdx.x * 256 + threadIdx.x;
   if (e >= PN) return;
-  const long s0 = (long)bh * a.nseg;
+  const long l0 = (long)bh * a.nseg * k, i0 = (long)bh * a.nseg;
   float g = 0.0f;
-  for (int i = a.nseg - 2; i >= 0; --i) {
-    g = a.gloc[(s0 + i + 1) * PN + e] + expf(a.dseg[s0 + i + 1]) * g;
-    a.gin[(s0 + i) * PN + e] = g;
+  for (int j = a.nseg * k - 1; j >= k; --j) {
+    g = a.gloc[(l0 + j) * PN + e] + expf(a.dseg[l0 + j]) * g;
+    if (j % k == 0) a.gin[(i0 + j / k - 1) * PN + e] = g;
   }
 }
 
@@ -2437,6 +2447,9 @@ constexpr int kWalkMinSegChunks = 4;
 struct BwdRoute {
   bool walk;
   int nseg, seg_nc;
+  // sub-segments per walk segment of the adjoint-only pass: segments of 8 chunks or
+  // more are cut in up to four
+  int adj_sub() const { return nseg > 1 ? std::max(1, std::min(4, seg_nc / 8)) : 1; }
 };
 BwdRoute bwd_route(int B, int H, int L, int CS) {
   const long bh = (long)B * H, nc = (L + CS - 1) / CS;
@@ -2493,10 +2506,10 @@ BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R
   w.dkh = gqa ? take((size_t)B * L * H * N * 4) : 0;
   w.dangh = ang_shared && R > 0 ? take((size_t)B * L * H * R * 4) : 0;      // per-head dAngles
   // the split walk: the segments' adjoint states and log-decays
-  const size_t bhs = (size_t)B * H * route.nseg;
+  const size_t bhs = (size_t)B * H * route.nseg, bhsub = bhs * route.adj_sub();
   w.gin = route.nseg > 1 ? take(bhs * P * N * 4) : 0;
-  w.gloc = route.nseg > 1 ? take(bhs * P * N * 4) : 0;
-  w.dseg = route.nseg > 1 ? take(bhs * 4) : 0;
+  w.gloc = route.nseg > 1 ? take(bhsub * P * N * 4) : 0;
+  w.dseg = route.nseg > 1 ? take(bhsub * 4) : 0;
   // the state-only pass split across compute units (few pairs, long sequences)
   const size_t sp = saved ? 0 : scan_split_ws_bytes(bf16_io, B, L, H, N, P, R, 64);
   w.split = sp ? take(sp) : 0;
@@ -2600,6 +2613,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.nc = (s.L + CS - 1) / CS;
   a.nseg = route.nseg;
   a.seg_nc = route.seg_nc;
+  a.adj_sub = route.adj_sub();
   if (route.nseg > 1) {
     a.gin = reinterpret_cast<float*>(base + w.gin);
     a.gloc = reinterpret_cast<float*>(base + w.gloc);
@@ -2630,7 +2644,8 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
     found = true;                                                                                          \
     if (a.nseg > 1) {                                                                                      \
       /* each later segment's own adjoint, then the adjoint entering every segment */                     \
-      hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r, true>), dim3(s.B * s.H, a.nseg - 1),         \
+      hipLaunchKernelGGL((scan_adjoint_kernel<T, cs, n, p, r, true>),                                      \
+                         dim3(s.B * s.H, (a.nseg - 1) * a.adj_sub),                                        \
                          dim3(kBwdThreads), 0, st, a);                                                     \
       if ((e = hipGetLastError()) != hipSuccess) return e;                                                 \
       hipLaunchKernelGGL(seg_adjoint_combine_kernel, dim3((s.P * s.N + 255) / 256, s.B * s.H), dim3(256),   \

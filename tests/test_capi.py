@@ -104,17 +104,17 @@ def test_split_workspace_sizes(lib):
 
 
 def _walk_segments(B, H, L, cs):
-    """Segments of the backward's walk: one at 80 pairs or more; below, about 256
-    blocks of at least 4 chunks each when that gives two or more (else the
-    chunk-parallel route: 0)."""
+    """(segments, chunks per segment) of the backward's walk: one segment at 80 pairs
+    or more; below, about 256 blocks of at least 4 chunks each when that gives two or
+    more (else the chunk-parallel route: 0 segments)."""
     nc = (L + cs - 1) // cs
     if B * H >= 80:
-        return 1
+        return 1, nc
     s = min(256 // (B * H), nc // 4)
     if s < 2:
-        return 0
+        return 0, nc
     seg_nc = (nc + s - 1) // s
-    return (nc + seg_nc - 1) // seg_nc
+    return (nc + seg_nc - 1) // seg_nc, seg_nc
 
 
 def _split_ws(B, H, L, N, P, R):
@@ -141,12 +141,14 @@ def _bwd_ws_expect(B, L, H, Hqk, N, P, R, io, saved=False):
     them), adjoint states after each chunk (chunk-parallel route only), bias and D
     partials, per-token d(scale), chunk sums of dA and d(theta), per-head dQ/dK
     (float32) when Hqk < H, the split walk's segment adjoints (two float32 P x N
-    states per (b, h, segment) and a log-decay) and the split state pass's carries."""
+    states per (b, h, segment) of the walk or of the adjoint pass's sub-segments, and a
+    log-decay per sub-segment) and the split state pass's carries."""
     al = lambda n: (n + 255) // 256 * 256  # noqa: E731
     cs = 64 if io == 1 else 32
     bhc = B * H * ((L + cs - 1) // cs)
     ts = 2 if io == 1 else 4
-    nseg = _walk_segments(B, H, L, cs)
+    nseg, seg_nc = _walk_segments(B, H, L, cs)
+    sub = max(1, min(4, seg_nc // 8))          # the adjoint pass's sub-segments per segment
     n = 2 * al(bhc * N * 4) + al(bhc * 4) + al(B * H * L * 4) + al(bhc * (R + 1) * 4)
     if not saved:
         n += al(bhc * P * N * ts) + al(bhc * max(R, 1) * 4)
@@ -155,7 +157,7 @@ def _bwd_ws_expect(B, L, H, Hqk, N, P, R, io, saved=False):
     if Hqk < H:
         n += 2 * al(B * L * H * N * 4)
     if nseg > 1:
-        n += 2 * al(B * H * nseg * P * N * 4) + al(B * H * nseg * 4)
+        n += al(B * H * nseg * P * N * 4) + al(B * H * nseg * sub * P * N * 4) + al(B * H * nseg * sub * 4)
     if not saved:
         n += _split_ws(B, H, L, N, P, R)
     return n
@@ -172,8 +174,9 @@ def test_backward_workspace_sizes(lib, monkeypatch):
     for B, H in ((8, 32), (1, 4)):
         for R in (32, 64):
             assert f(B, 4096, H, H, 128, 64, R, 64, f32) == _bwd_ws_expect(B, 4096, H, H, 128, 64, R, f32)
-    # config 3's shape: 8 walk segments of 64 chunks, 8 state-pass segments of 4096 tokens
-    assert _walk_segments(1, 32, 32768, 64) == 8
+    # config 3's shape: 8 walk segments of 64 chunks (the adjoint pass in 32 sub-segments
+    # of 16), 8 state-pass segments of 4096 tokens
+    assert _walk_segments(1, 32, 32768, 64) == (8, 64)
     assert f(1, 32768, 32, 32, 128, 64, 32, 128, bf) == _bwd_ws_expect(1, 32768, 32, 32, 128, 64, 32, bf)
     assert f(1, 200, 2, 2, 128, 64, 32, 64, bf) == _bwd_ws_expect(1, 200, 2, 2, 128, 64, 32, bf)  # chunks
     assert f(1, 100, 2, 2, 64, 16, 16, 64, bf) == 0        # headdim 16: no backward kernel
