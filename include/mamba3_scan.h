@@ -163,7 +163,9 @@ size_t m3_chunk_scan_bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, in
  *   NULL), summed over the batch.
  * The chunk size does not change the gradients (the chunked form is exact).  The
  * workspace (>= m3_chunk_scan_bwd_ws_bytes, 16-byte aligned) is scratch for the
- * call.  Deterministic: no atomics, fixed summation order.
+ * call.  Q, K, V, Z, Angles, dOut and every io-dtype gradient and dAngles must be
+ * 16-byte aligned (M3_E_ALIGN otherwise).  Deterministic: no atomics, fixed
+ * summation order.
  */
 int m3_chunk_scan_bwd(const void* Q, const void* K, const void* V,
                       const float* ADT, const float* DT, const float* Trap,

@@ -315,9 +315,10 @@ int scan_bwd(const void* Q, const void* K, const void* V,
       !dV || !dADT || !dDT || !dTrap || !dQ_bias || !dK_bias || (R > 0 && !dAngles))
     return fail(M3_E_ARG, "NULL required pointer");
   if ((Z == nullptr) != (dZ == nullptr)) return fail(M3_E_ARG, "pass dZ exactly when Z is given");
-  const void* vec_ptrs[] = {Q, K, V, Z, dOut, dQ, dK, dV, dZ};
+  const void* vec_ptrs[] = {Q, K, V, Z, dOut, dQ, dK, dV, dZ, Angles, dAngles};
   for (const void* p : vec_ptrs)
-    if (!aligned16(p)) return fail(M3_E_ALIGN, "Q, K, V, Z, dOut and their gradients must be 16-byte aligned");
+    if (!aligned16(p))
+      return fail(M3_E_ALIGN, "Q, K, V, Z, Angles, dOut and their gradients must be 16-byte aligned");
   const size_t need = m3::scan_bwd_ws_bytes(bf, B, L, H, Hqk, N, P, R, ang_shared, saved != nullptr);
   if (ws == nullptr || ws_bytes < need)
     return fail(M3_E_ARG, "workspace of %zu bytes, the backward needs %zu (m3_chunk_scan_bwd%s_ws_bytes)", ws_bytes,

@@ -170,7 +170,7 @@ struct BwdArgs {
   const float* th0;            // [bh][nc][R] revolutions: angle entering each chunk
   float* pqb; float* pkb;      // [bh][nc][N] partial bias gradients
   float* pd;                   // [bh][nc] partial D gradient
-  float* dqh; float* dkh;      // GQA: per-head dQ, dK (B, L, H, N) f32, else null
+  void* dqh; void* dkh;        // GQA: per-head dQ, dK (B, L, H, N) in the I/O type, else null
   float* dsc;                  // [bh][L] d(scale) per token
   float* ctot;                 // [bh][nc][1 + R] chunk sums of dA and of d(theta) per pair
   int nc;
@@ -859,7 +859,7 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
         }
         // dQ / dK rows
         if (a.dqh) {
-          float* dst = (isq ? a.dqh : a.dkh) + (((long)b * L + t0 + lane) * H + h) * N + 8 * g;
+          T* dst = reinterpret_cast<T*>(isq ? a.dqh : a.dkh) + (((long)b * L + t0 + lane) * H + h) * N + 8 * g;
           store8(dst, out);
         } else {
           T* dst = reinterpret_cast<T*>(isq ? a.dq : a.dk) + qrow + 8 * g;
@@ -1796,7 +1796,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
           const long row = (long)b * L + t0 + tkn;
           const int col = n0 + 8 * wave + EL * hf;
           if (a.dqh) {
-            float* dst = (isq ? a.dqh : a.dkh) + (row * H + h) * N + col;
+            T* dst = reinterpret_cast<T*>(isq ? a.dqh : a.dkh) + (row * H + h) * N + col;
             if constexpr (EL == 4) store4(dst, out); else store8(dst, out);
           } else {
             T* dst = reinterpret_cast<T*>(isq ? a.dq : a.dk) + (row * HQ + hq) * N + col;
@@ -2048,7 +2048,8 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
               for (int e = 0; e < 8; ++e) o8[e] = res[row * (NH + 4) + 8 * pc + e];
               if (a.dqh) {
-                store8((isq ? a.dqh : a.dkh) + (((long)b * L + t0 + row) * H + h) * N + n0 + 8 * pc, o8);
+                store8(reinterpret_cast<T*>(isq ? a.dqh : a.dkh) + (((long)b * L + t0 + row) * H + h) * N + n0 + 8 * pc,
+                       o8);
               } else {
                 store8(reinterpret_cast<T*>(isq ? a.dq : a.dk) + (((long)b * L + t0 + row) * HQ + hq) * N + n0 + 8 * pc,
                        o8);
@@ -2387,36 +2388,95 @@ void scan_bwd_reduce_kernel(BwdArgs a) {
 }
 
 // Shared angle rates: dAngles (B, L, R) = sum over heads of the per-head gradients.
-__global__ void scan_bwd_angle_heads_kernel(BwdArgs a, float* dang_out) {
-  const int H = a.s.H, R = a.s.R;
-  const long total = (long)a.s.B * a.s.L * R;
+// Thread = four consecutive pairs of one (b, t) (R is a multiple of 4); the heads are
+// summed in order, eight 16-byte loads in flight.
+__global__ __launch_bounds__(256) void scan_bwd_angle_heads_kernel(BwdArgs a, float* dang_out) {
+  const int H = a.s.H, R4 = a.s.R / 4;
+  const long total = (long)a.s.B * a.s.L * R4;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
-    const int r = i % R;
-    const long bt = i / R;
-    float s = 0.0f;
-    for (int h = 0; h < H; ++h) s += a.dang[(bt * H + h) * R + r];
-    dang_out[i] = s;
+    const long bt = i / R4;
+    const float4* src = reinterpret_cast<const float4*>(a.dang) + bt * H * R4 + i % R4;
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int h = 0;
+    for (; h + 8 <= H; h += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = src[(long)(h + j) * R4];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s = make_float4(s.x + v[j].x, s.y + v[j].y, s.z + v[j].z, s.w + v[j].w);
+    }
+    for (; h < H; ++h) {
+      const float4 v = src[(long)h * R4];
+      s = make_float4(s.x + v.x, s.y + v.y, s.z + v.z, s.w + v.w);
+    }
+    reinterpret_cast<float4*>(dang_out)[i] = s;
   }
 }
 
-// GQA: dQ, dK of a Q/K head = sum over the value heads that share it.
+// Four consecutive elements of the I/O type as floats (8 bytes of bf16, 16 of float).
+__device__ __forceinline__ void load4f(const bf16* p, float f[4]) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  f[0] = __uint_as_float(w.x << 16);
+  f[1] = __uint_as_float(w.x & 0xffff0000u);
+  f[2] = __uint_as_float(w.y << 16);
+  f[3] = __uint_as_float(w.y & 0xffff0000u);
+}
+__device__ __forceinline__ void load4f(const float* p, float f[4]) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+}
+
+// GQA: dQ, dK of a Q/K head = sum over the value heads that share it, in float32 over
+// the per-head partials (in the I/O type: with bf16 I/O the partials exchanged are
+// bf16, as the reference's fused path exchanges its per-head gradient tiles in its io
+// dtype, mamba3_pallas.py:832-836).  Thread = four consecutive columns of one
+// (b, t, hq) row of both; the heads are summed in order, eight loads of each in flight.
 template <typename T>
-__global__ void scan_bwd_gqa_kernel(BwdArgs a) {
-  const int B = a.s.B, L = a.s.L, H = a.s.H, HQ = a.s.Hqk, N = a.s.N, rep = H / HQ;
-  const long total = (long)B * L * HQ * N;
+__global__ __launch_bounds__(256) void scan_bwd_gqa_kernel(BwdArgs a) {
+  const int B = a.s.B, L = a.s.L, H = a.s.H, HQ = a.s.Hqk, N = a.s.N, N4 = N / 4, rep = H / HQ;
+  const long total = (long)B * L * HQ * N4;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
-    const int n = i % N;
-    const long row = i / N;                      // (b, t, hq)
+    const int n4 = i % N4;
+    const long row = i / N4;                     // (b, t, hq)
     const int hq = row % HQ;
     const long bt = row / HQ;
-    float sq = 0.0f, sk = 0.0f;
-    for (int j = 0; j < rep; ++j) {
-      const long src = (bt * H + hq * rep + j) * N + n;
-      sq += a.dqh[src];
-      sk += a.dkh[src];
+    const long s0 = (bt * H + (long)hq * rep) * N + 4 * n4;
+    const T* q = reinterpret_cast<const T*>(a.dqh) + s0;
+    const T* k = reinterpret_cast<const T*>(a.dkh) + s0;
+    float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int j = 0;
+    for (; j + 8 <= rep; j += 8) {
+      float vq[8][4], vk[8][4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        load4f(q + (long)(j + u) * N, vq[u]);
+        load4f(k + (long)(j + u) * N, vk[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sq[e] += vq[u][e];
+          sk[e] += vk[u][e];
+        }
     }
-    reinterpret_cast<T*>(a.dq)[i] = (T)sq;
-    reinterpret_cast<T*>(a.dk)[i] = (T)sk;
+    for (; j < rep; ++j) {
+      float vq[4], vk[4];
+      load4f(q + (long)j * N, vq);
+      load4f(k + (long)j * N, vk);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sq[e] += vq[e];
+        sk[e] += vk[e];
+      }
+    }
+    T* dq = reinterpret_cast<T*>(a.dq) + 4 * i;
+    T* dk = reinterpret_cast<T*>(a.dk) + 4 * i;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dq[e] = (T)sq[e];
+      dk[e] = (T)sk[e];
+    }
   }
 }
 
@@ -2502,8 +2562,8 @@ BwdWs bwd_layout(bool bf16_io, int B, int L, int H, int Hqk, int N, int P, int R
   w.dsc = take((size_t)B * H * L * 4);
   w.ctot = take(bhc * (R + 1) * 4);
   const bool gqa = Hqk < H;
-  w.dqh = gqa ? take((size_t)B * L * H * N * 4) : 0;
-  w.dkh = gqa ? take((size_t)B * L * H * N * 4) : 0;
+  w.dqh = gqa ? take((size_t)B * L * H * N * ts) : 0;
+  w.dkh = gqa ? take((size_t)B * L * H * N * ts) : 0;
   w.dangh = ang_shared && R > 0 ? take((size_t)B * L * H * R * 4) : 0;      // per-head dAngles
   // the split walk: the segments' adjoint states and log-decays
   const size_t bhs = (size_t)B * H * route.nseg, bhsub = bhs * route.adj_sub();
@@ -2606,8 +2666,8 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   a.pqb = reinterpret_cast<float*>(base + w.pqb);
   a.pkb = reinterpret_cast<float*>(base + w.pkb);
   a.pd = reinterpret_cast<float*>(base + w.pd);
-  a.dqh = w.dqh ? reinterpret_cast<float*>(base + w.dqh) : nullptr;
-  a.dkh = w.dkh ? reinterpret_cast<float*>(base + w.dkh) : nullptr;
+  a.dqh = w.dqh ? base + w.dqh : nullptr;
+  a.dkh = w.dkh ? base + w.dkh : nullptr;
   a.dsc = reinterpret_cast<float*>(base + w.dsc);
   a.ctot = reinterpret_cast<float*>(base + w.ctot);
   a.nc = (s.L + CS - 1) / CS;
@@ -2655,7 +2715,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
     launch_walk<T, cs, n, p, r>(dim3(s.B * s.H, a.nseg), st, a);                                           \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
     if (a.dqh) {                                                                                           \
-      hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \
+      hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(2048), dim3(256), 0, st, a);                       \
       if ((e = hipGetLastError()) != hipSuccess) return e;                                                 \
     }                                                                                                      \
   }
@@ -2666,7 +2726,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
     else hipLaunchKernelGGL(scan_bwd_walk_finish_kernel<32>, grid_c, dim3(256), 0, st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (w.dangh) {
-      hipLaunchKernelGGL(scan_bwd_angle_heads_kernel, dim3(1024), dim3(256), 0, st, a, g.dang);
+      hipLaunchKernelGGL(scan_bwd_angle_heads_kernel, dim3(2048), dim3(256), 0, st, a, g.dang);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     BwdArgs ar = a;
@@ -2682,7 +2742,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
     hipLaunchKernelGGL((scan_bwd_chunk_kernel<T, cs, n, p, r>), grid_c, dim3(kBwdThreads), 0, st, a);      \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                                   \
     if (a.dqh) {                                                                                           \
-      hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(1024), dim3(256), 0, st, a);                       \
+      hipLaunchKernelGGL((scan_bwd_gqa_kernel<T>), dim3(2048), dim3(256), 0, st, a);                       \
       if ((e = hipGetLastError()) != hipSuccess) return e;                                                 \
     }                                                                                                      \
   }
@@ -2693,7 +2753,7 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   else hipLaunchKernelGGL(scan_bwd_finish_kernel<32>, grid_c, dim3(64 * kFinWaves), 0, st, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (w.dangh) {
-    hipLaunchKernelGGL(scan_bwd_angle_heads_kernel, dim3(1024), dim3(256), 0, st, a, g.dang);
+    hipLaunchKernelGGL(scan_bwd_angle_heads_kernel, dim3(2048), dim3(256), 0, st, a, g.dang);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   hipLaunchKernelGGL(scan_bwd_reduce_kernel, dim3(s.H, (s.N + 15) / 16), dim3(256), 0, st, a);

@@ -140,7 +140,7 @@ def _bwd_ws_expect(B, L, H, Hqk, N, P, R, io, saved=False):
     chunks for bf16, 32 for fp32) and chunk angles (unless the training forward saved
     them), adjoint states after each chunk (chunk-parallel route only), bias and D
     partials, per-token d(scale), chunk sums of dA and d(theta), per-head dQ/dK
-    (float32) when Hqk < H, the split walk's segment adjoints (two float32 P x N
+    (in the I/O type) when Hqk < H, the split walk's segment adjoints (two float32 P x N
     states per (b, h, segment) of the walk or of the adjoint pass's sub-segments, and a
     log-decay per sub-segment) and the split state pass's carries."""
     al = lambda n: (n + 255) // 256 * 256  # noqa: E731
@@ -155,7 +155,7 @@ def _bwd_ws_expect(B, L, H, Hqk, N, P, R, io, saved=False):
     if nseg == 0:
         n += al(bhc * P * N * ts)
     if Hqk < H:
-        n += 2 * al(B * L * H * N * 4)
+        n += 2 * al(B * L * H * N * ts)
     if nseg > 1:
         n += al(B * H * nseg * P * N * 4) + al(B * H * nseg * sub * P * N * 4) + al(B * H * nseg * sub * 4)
     if not saved:
@@ -280,6 +280,18 @@ def test_misaligned_pointer_rejected(lib):
     bad = ctypes.c_void_p(4098)
     assert _scan_call(lib, Q=bad, K=ok, V=ok, ADT=ok, DT=ok, Trap=ok, Qb=ok, Kb=ok, Ang=ok,
                       Out=ok) == E_ALIGN
+
+
+def test_backward_misaligned_angle_gradient_rejected(lib):
+    """The backward stores dAngles and reads Angles as 16-byte pieces: a misaligned
+    pointer is refused before any launch."""
+    E_ALIGN = _header_define("M3_E_ALIGN")
+    ok, bad = ctypes.c_void_p(4096), ctypes.c_void_p(4100)
+    ws = lib.m3_chunk_scan_bwd_ws_bytes(1, 128, 2, 2, 128, 64, 32, 64, 1)
+    for ang, dang in ((bad, ok), (ok, bad)):
+        args = [ok] * 8 + [ang] + [ok] * 3 + [ok] * 8 + [dang] + [ok, ok]
+        rc = lib.m3_chunk_scan_bwd(*args, 1, 128, 2, 2, 128, 64, 32, 64, 1, ok, ws, None)
+        assert rc == E_ALIGN and b"16-byte aligned" in lib.m3_last_error()
 
 
 def test_carry_arguments_all_or_none(lib):
