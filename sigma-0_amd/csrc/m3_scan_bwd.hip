@@ -1146,8 +1146,13 @@ template <> struct WalkMma<float> {
 };
 
 // YV: the training pair's variant that reads the saved output before the gate (a.yv)
-// and forms dZ from it in the preparation instead of recomputing y.
-template <typename T, int CS, int N, int P, int R, bool YV>
+// and forms dZ from it in the preparation instead of recomputing y.  SEGW: the walk
+// split into segments (grid (B*H, nseg), each block one segment from its entering
+// adjoint); without it the walk covers the whole sequence, compiled without the
+// segment bounds.
+// GQA: Q/K heads shared by several value heads (a.dqh set): the per-head dQ/dK go to
+// the partials that scan_bwd_gqa_kernel sums; without it they go straight to dQ/dK.
+template <typename T, int CS, int N, int P, int R, bool YV, bool SEGW, bool GQA>
 __global__ __launch_bounds__(kBwdThreads, 1)
 void scan_bwd_walk_kernel(BwdArgs a) {
   typedef WalkMma<T> W;
@@ -1178,9 +1183,9 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   const int bh = blockIdx.x, b = bh / H, h = bh % H, hq = h / (H / HQ);
   // the chunks of this block's segment (the whole sequence without the split) and the
   // slot of its partial sums
-  const int seg = blockIdx.y;
-  const int c_lo = a.nseg > 1 ? seg * a.seg_nc : 0, c_hi = a.nseg > 1 ? min(nc, c_lo + a.seg_nc) : nc;
-  const long ps = (long)bh * a.nseg + seg;
+  const int seg = SEGW ? (int)blockIdx.y : 0;
+  const int c_lo = SEGW ? seg * a.seg_nc : 0, c_hi = SEGW ? min(nc, c_lo + a.seg_nc) : nc;
+  const long ps = SEGW ? (long)bh * a.nseg + seg : bh;
   const T* gz = reinterpret_cast<const T*>(a.s.z);
   const float Dh = a.s.D ? a.s.D[h] : 0.0f;
   T* const smk = sm.smk();
@@ -1191,7 +1196,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   f32x4 G[TPW];                                        // adjoint state tiles [p][n]
 #pragma unroll
   for (int i = 0; i < TPW; ++i) G[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (a.nseg > 1 && seg + 1 < a.nseg) {
+  if (SEGW && seg + 1 < a.nseg) {
     // the adjoint state after this segment, which the later segments leave
     const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -1795,7 +1800,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         if (tok) {
           const long row = (long)b * L + t0 + tkn;
           const int col = n0 + 8 * wave + EL * hf;
-          if (a.dqh) {
+          if constexpr (GQA) {
             T* dst = reinterpret_cast<T*>(isq ? a.dqh : a.dkh) + (row * H + h) * N + col;
             if constexpr (EL == 4) store4(dst, out); else store8(dst, out);
           } else {
@@ -2047,7 +2052,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
               float o8[8];
 #pragma unroll
               for (int e = 0; e < 8; ++e) o8[e] = res[row * (NH + 4) + 8 * pc + e];
-              if (a.dqh) {
+              if constexpr (GQA) {
                 store8(reinterpret_cast<T*>(isq ? a.dqh : a.dkh) + (((long)b * L + t0 + row) * H + h) * N + n0 + 8 * pc,
                        o8);
               } else {
@@ -2621,16 +2626,28 @@ void scan_bwd_saved_ptrs(void* saved, bool bf16_io, int B, int L, int H, int N, 
 }
 
 // The walk, in its training-pair variant when the forward saved the output before the
-// gate (float32 only: a.yv is never set for bf16).
-template <typename T, int CS, int N, int P, int R>
-void launch_walk(dim3 grid, hipStream_t st, const BwdArgs& a) {
+// gate (float32 only: a.yv is never set for bf16), split into segments when a.nseg > 1.
+template <typename T, int CS, int N, int P, int R, bool SEGW, bool GQA>
+void launch_walk_seg(dim3 grid, hipStream_t st, const BwdArgs& a) {
   if constexpr (std::is_same<T, float>::value) {
     if (a.yv) {
-      hipLaunchKernelGGL((scan_bwd_walk_kernel<T, CS, N, P, R, true>), grid, dim3(kBwdThreads), 0, st, a);
+      hipLaunchKernelGGL((scan_bwd_walk_kernel<T, CS, N, P, R, true, SEGW, GQA>), grid, dim3(kBwdThreads), 0, st,
+                         a);
       return;
     }
   }
-  hipLaunchKernelGGL((scan_bwd_walk_kernel<T, CS, N, P, R, false>), grid, dim3(kBwdThreads), 0, st, a);
+  hipLaunchKernelGGL((scan_bwd_walk_kernel<T, CS, N, P, R, false, SEGW, GQA>), grid, dim3(kBwdThreads), 0, st, a);
+}
+template <typename T, int CS, int N, int P, int R>
+void launch_walk(dim3 grid, hipStream_t st, const BwdArgs& a) {
+  const bool gqa = a.dqh != nullptr;
+  if (a.nseg > 1) {
+    if (gqa) launch_walk_seg<T, CS, N, P, R, true, true>(grid, st, a);
+    else launch_walk_seg<T, CS, N, P, R, true, false>(grid, st, a);
+  } else {
+    if (gqa) launch_walk_seg<T, CS, N, P, R, false, true>(grid, st, a);
+    else launch_walk_seg<T, CS, N, P, R, false, false>(grid, st, a);
+  }
 }
 
 hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t st, const void* saved) {
