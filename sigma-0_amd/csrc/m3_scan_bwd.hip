@@ -2193,7 +2193,9 @@ void scan_bwd_walk_finish_kernel(BwdArgs a) {
   __shared__ float tot[65], off[65];
   __shared__ float dts[CS], angp[CS];
   const int tid = threadIdx.x;
-  const int c = blockIdx.x, bh = blockIdx.y, b = bh / a.s.H, h = bh % a.s.H;
+  // grid (B*H, chunks): consecutive blocks take the heads of one chunk, so that the
+  // blocks in flight read whole (token, all heads) rows of dAngles and the rates
+  const int c = blockIdx.y, bh = blockIdx.x, b = bh / a.s.H, h = bh % a.s.H;
   const int L = a.s.L, H = a.s.H, R = a.s.R;
   const int t0 = c * CS, nt = min(CS, L - t0);
   if (tid <= R) {
@@ -2739,8 +2741,9 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
     M3_BWD_SHAPES(X)
 #undef X
     if (!found) return hipErrorInvalidValue;
-    if (CS == 64) hipLaunchKernelGGL(scan_bwd_walk_finish_kernel<64>, grid_c, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(scan_bwd_walk_finish_kernel<32>, grid_c, dim3(256), 0, st, a);
+    const dim3 grid_hc(s.B * s.H, a.nc);
+    if (CS == 64) hipLaunchKernelGGL(scan_bwd_walk_finish_kernel<64>, grid_hc, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(scan_bwd_walk_finish_kernel<32>, grid_hc, dim3(256), 0, st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (w.dangh) {
       hipLaunchKernelGGL(scan_bwd_angle_heads_kernel, dim3(2048), dim3(256), 0, st, a, g.dang);
