@@ -25,7 +25,7 @@
 // from HBM once and the output written once.
 #include <type_traits>
 
-#include "m3_chunk_common.h"
+#include "m3_chunk_block.h"
 
 namespace m3 {
 namespace chunked_f32 {
@@ -47,34 +47,18 @@ __device__ __forceinline__ void half_incl_scan2(float v[2]) {
 
 // Compile-time geometry of one instantiation.
 template <typename T, int CS_, int N_, int P_, int R_, int NW_>
-struct Geo {
-  static constexpr bool BF = std::is_same<T, bf16>::value;
-  static constexpr int CS = CS_, N = N_, P = P_, R = R_, NW = NW_, NT = 64 * NW_;
-  static constexpr int NWY = 4;                             // output waves 0..3
-  static constexpr int NST = 4;                             // state waves 4..7
-  static constexpr int NAUX = NW - NWY - NST;               // auxiliary waves 8..11
-  static constexpr int KSTEP = MF16<T>::KSTEP;
-  static constexpr int LB16 = CS / 16, PT = P / 16;         // 16-row query blocks, 16-col p-tiles
-  static constexpr int NB16 = N / 16;                       // 16-row state tiles per p-tile
-  static constexpr int SPT = NST / PT;                      // state waves per p-tile
-  static constexpr int TS = BF ? 2 : 4;
-  static constexpr int PAD = BF ? 8 : 4;
-  static constexpr int LDQ = N + PAD;                       // sQ, sK rows (elements)
-  static constexpr int LDY = P + (BF ? 8 : 2);              // sY rows (io precision)
-  static constexpr int QG = N / 8, QGW = 2;                // Q/K 8-column groups, at most 2 per wave
-  // 16-byte staging slots per row: Q/K, V, rotation rates
-  static constexpr int SQ = N * TS / 16, SV = P * TS / 16, SA = R / 4 > 0 ? R / 4 : 1;
+struct Geo : GeoBase<T, CS_, N_, P_, R_, NW_> {
+  typedef GeoBase<T, CS_, N_, P_, R_, NW_> B;
+  static constexpr int LDY = B::P + (B::BF ? 8 : 2);       // sY rows (io precision)
   // LDS bytes besides the Q/K staging.  The Q/K staging is double-buffered where it
   // fits; otherwise (rotation width N/2 at d_state 128) it is single-buffered and its
   // loads wait until the preparation phase has consumed it.
-  static constexpr int FIXED = 2 * CS * LDQ * TS + 2 * CS * LDY * TS + 16 * LDY * TS + (2 * CS * SV + 2 * CS * SA) * 16 +
-                               2 * 3 * (CS + 4) * 4 + 8 * N + 2 * 6 * CS * 4 + 64;
-  static constexpr bool DBQK = FIXED + 4 * CS * SQ * 16 <= 160 * 1024 - 512;
+  static constexpr int FIXED = 2 * B::CS * B::LDQ * B::TS + 2 * B::CS * LDY * B::TS + 16 * LDY * B::TS +
+                               (2 * B::CS * B::SV + 2 * B::CS * B::SA) * 16 + 2 * 3 * (B::CS + 4) * 4 + 8 * B::N +
+                               2 * 6 * B::CS * 4 + 64;
+  static constexpr bool DBQK = FIXED + 4 * B::CS * B::SQ * 16 <= 160 * 1024 - 512;
   static constexpr int NQK = DBQK ? 2 : 1;
-  static_assert(CS <= 64 && LB16 <= NWY, "one token per lane, one query block per output wave");
-  static_assert(SPT >= 1 && NST % PT == 0 && LB16 % SPT == 0, "state-wave split");
-  static_assert(NAUX == 4, "12 waves");
-  static_assert(QG <= 2 * NAUX + NWY + NST, "column groups per wave");
+  static_assert(B::SPT >= 1 && B::NST % B::PT == 0 && B::LB16 % B::SPT == 0, "state-wave split");
   // Q/K 8-column group k (< QGW) of a wave, or QG for none.  The first groups are the
   // rope columns, and their owner also computes their angles for the next chunk.  Full
   // pass: the output and auxiliary waves take the first groups, one each, so the angle
@@ -86,6 +70,7 @@ struct Geo {
   // of the rest, which halves the angle work per wave.
   template <bool SO>
   __device__ static int qgroup(int wave, int k) {
+    constexpr int NWY = B::NWY, NST = B::NST, NAUX = B::NAUX, QG = B::QG;
     int g;
     if constexpr (SO) {
       if (wave < NWY) g = k == 0 ? wave : QG;
@@ -98,8 +83,6 @@ struct Geo {
     }
     return g < QG ? g : QG;
   }
-  static_assert(R % 4 == 0 && 2 * R <= N, "rotation width: a multiple of 4, at most N/2");
-  static_assert((SQ & (SQ - 1)) == 0 && (SV & (SV - 1)) == 0 && (SA & (SA - 1)) == 0, "swizzle widths");
 };
 
 template <typename G>
@@ -152,52 +135,17 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __builtin_assume(wave >= 0 && wave < NW);
-  const int bh = xcd_bh(blockIdx.x, gridDim.x, a.Hqk, a.H);
-  const int b = bh / a.H, h = bh % a.H;
-  const int hq = h / (a.H / a.Hqk);
-  const int Lg = a.L, H = a.H, HQ = a.Hqk;
-  // this block's tokens [tb, tb + L); Lnx counts the tokens from tb to the sequence
-  // end (the trapezoid weight of a segment's last token reads the next one)
-  const int seg = blockIdx.y, nseg = gridDim.y;
-  const int tb = a.seg_len > 0 ? seg * a.seg_len : 0;
-  const int L = a.seg_len > 0 ? min(Lg - tb, a.seg_len) : Lg;
-  const int Lnx = Lg - tb;
-  const int nc = (L + CS - 1) / CS;
-  // chunk-state outputs (the backward's saved states, chunk_h / chunk_th): indexed by
-  // the chunk over the whole sequence, so that the segments of a split pass write theirs
-  const long ch0 = (long)bh * ((Lg + CS - 1) / CS) + tb / CS;
-  // carry slots: per (b, h) or per (b, h, segment)
-  const int ci_in = a.init_per_seg ? bh * nseg + seg : bh;
-  const int ci_out = a.fin_per_seg ? bh * nseg + seg : bh;
-  const bool has_init = a.init_per_seg || seg == 0;
-  const bool fin_here = a.fin_per_seg || seg == nseg - 1;
-  T* gO = reinterpret_cast<T*>(a.out);
-  const T* gZ = reinterpret_cast<const T*>(a.z);
-  const float* gadt = a.adt + (long)bh * Lg + tb;
-  const float* gdt = a.dt + (long)bh * Lg + tb;
-  const float* gtr = a.trap + (long)bh * Lg + tb;
-  const float Dh = a.D ? a.D[h] : 0.0f;
-  const bool has_z = a.z != nullptr;
-
-  // ---- element offsets of row (b, t=0, head) in each input; rows advance by the stride
-  const int AH = a.ang_shared ? 1 : H;                 // angle rows per token
-  // row strides (elements) are 32-bit; offsets along the sequence are formed in 64 bits
-  const int qk_stride = HQ * N, v_stride = H * P, a_stride = AH * R;
-  // V and Z rows: contiguous (B, L, H, P), or in place in wider rows
-  const int vz_stride = a.vz_tok ? (int)a.vz_tok : v_stride;
-  const long vz_batch = a.vz_bat ? a.vz_bat : (long)Lg * v_stride;
-  // this block's first row of each input (and of the output); the loop only adds t * stride
-  const T* q_base = reinterpret_cast<const T*>(a.q) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
-  const T* k_base = reinterpret_cast<const T*>(a.k) + ((long)b * Lg * HQ + hq) * N + (long)tb * qk_stride;
-  const long vz_row = (long)b * vz_batch + (long)h * P + (long)tb * vz_stride;
-  const T* v_base = reinterpret_cast<const T*>(a.v) + vz_row;
-  const T* z_base = gZ + vz_row;
-  T* o_base = gO + ((long)b * Lg * H + h) * P + (long)tb * v_stride;
-  const float* ang_base = a.ang + ((long)b * Lg * AH + (a.ang_shared ? 0 : h)) * R + (long)tb * a_stride;
-  for (int i = tid; i < N; i += G::NT) {
-    sm.qb[i] = a.qbias[(long)h * N + i];
-    sm.kb[i] = a.kbias[(long)h * N + i];
-  }
+  const ChunkBlock<T> cb = chunk_block<T, CS, N, P, R>(a);
+  const int L = cb.L, Lnx = cb.Lnx, nc = cb.nc;
+  const long ch0 = cb.ch0;
+  const int ci_in = cb.ci_in, ci_out = cb.ci_out;
+  const bool has_init = cb.has_init, fin_here = cb.fin_here, has_z = cb.has_z;
+  const float Dh = cb.Dh;
+  const int v_stride = cb.v_stride, vz_stride = cb.vz_stride;
+  const T* z_base = cb.z_base;
+  T* o_base = cb.o_base;
+  T* gO = cb.gO;
+  stage_biases<N, G::NT>(sm.qb, sm.kb, a, cb.h, tid);
 
   // ---- staging.  Q/K of chunk c into buffer c % NQK, V into parity c & 1, rotation
   // rates and scalars into parity c & 1.  A wave waits while the CU's load path drains
@@ -207,53 +155,9 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   // waves 0 and 1 (the two lightest query blocks) at the start of the matrix phase.
   constexpr int kWQ0 = G::DBQK ? 0 : 8, kWQ1 = G::DBQK ? 1 : 9, kWK0 = G::DBQK ? 2 : 10, kWK1 = G::DBQK ? 3 : 11;
   constexpr int kWV = 0, kWA = 1;
-  auto stage_qk = [&](int c) {
-    const int t0 = c * CS;
-    const int valid = L - t0;
-    constexpr int JQ = CS * G::SQ / 64;
-    const char* q0 = reinterpret_cast<const char*>(q_base + (long)t0 * qk_stride);
-    const char* k0 = reinterpret_cast<const char*>(k_base + (long)t0 * qk_stride);
-    lds_uint4* dq = (lds_uint4*)sm.rq[c % G::NQK];
-    lds_uint4* dk = (lds_uint4*)sm.rk[c % G::NQK];
-    if (!SO && wave == kWQ0) stage_rows<CS, G::SQ, 0, JQ / 2>(dq, q0, qk_stride * G::TS, valid, lane);
-    if (!SO && wave == kWQ1) stage_rows<CS, G::SQ, JQ / 2, JQ>(dq, q0, qk_stride * G::TS, valid, lane);
-    if (wave == kWK0) stage_rows<CS, G::SQ, 0, JQ / 2>(dk, k0, qk_stride * G::TS, valid, lane);
-    if (wave == kWK1) stage_rows<CS, G::SQ, JQ / 2, JQ>(dk, k0, qk_stride * G::TS, valid, lane);
-  };
-  auto stage_v = [&](int c) {
-    const int t0 = c * CS;
-    constexpr int JV = CS * G::SV / 64;
-    if (wave == kWV) {
-      const char* v0 = reinterpret_cast<const char*>(v_base + (long)t0 * vz_stride);
-      stage_rows<CS, G::SV, 0, JV>((lds_uint4*)sm.rv[c & 1], v0, vz_stride * G::TS, L - t0, lane);
-    }
-  };
-  auto stage_ars = [&](int c) {
-    const int t0 = c * CS;
-    const int valid = L - t0;
-    constexpr int JA = CS * G::SA / 64;
-    if (wave == kWA) {
-      if (R > 0) {
-        const char* a0 = reinterpret_cast<const char*>(ang_base + (long)t0 * a_stride);
-        stage_rows<CS, G::SA, 0, JA>((lds_uint4*)sm.ra[c & 1], a0, a_stride * 4, valid, lane);
-      }
-      // the bases are made opaque here so that no derived pointer is hoisted out of the
-      // chunk loop (and spilled)
-      const float* pa = gadt + t0;
-      const float* pd = gdt + t0;
-      const float* pt = gtr + t0;
-      asm volatile("" : "+s"(pa), "+s"(pd), "+s"(pt));
-      if (lane < CS && lane < valid) {
-        lds_dma4(pa, 4u * lane, (lds_float*)&sm.rs[c & 1][0][0]);
-        lds_dma4(pd, 4u * lane, (lds_float*)&sm.rs[c & 1][1][0]);
-        lds_dma4(pt, 4u * lane, (lds_float*)&sm.rs[c & 1][2][0]);
-      }
-      if (lane == 0 && t0 + CS < Lnx) {
-        lds_dma4(pd, 4u * CS, (lds_float*)&sm.rs[c & 1][1][CS]);
-        lds_dma4(pt, 4u * CS, (lds_float*)&sm.rs[c & 1][2][CS]);
-      }
-    }
-  };
+  auto stage_qk = [&](int c) { stage_qk_chunk<G, SO, kWQ0, kWQ1, kWK0, kWK1>(sm, cb, c, wave, lane); };
+  auto stage_v = [&](int c) { stage_v_chunk<G, kWV>(sm, cb, c, wave, lane); };
+  auto stage_ars = [&](int c) { stage_ars_chunk<G, kWA>(sm, cb, c, wave, lane); };
 
   // ---- gate (phase 7): thread -> (row, 8-column group) of a chunk's Y tile
   // (the state waves' threads: their share of the preparation is the lightest)
@@ -312,20 +216,7 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   const int pcol = 16 * pr + (lane & 15);
   const int g4 = 4 * (lane >> 4);              // C-tile row offset of this lane
   f32x4 hs[G::NB16];
-  {
-    // effective entering state: h0 + (1 - sigmoid(trap_0)) dt_0 (v0 (x) k0)
-    const bool own = a.init_h && has_init && swave;
-    const float cinit = own ? (1.0f - sigmoid_fast(gtr[0])) * gdt[0] : 0.0f;
-    const float v0 = own ? a.init_v[(long)ci_in * P + pcol] : 0.0f;
-#pragma unroll
-    for (int nb = 0; nb < G::NB16; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = 16 * nb + g4 + r;
-        hs[nb][r] = own ? a.init_h[((long)ci_in * P + pcol) * N + n] + cinit * v0 * a.init_k[(long)ci_in * N + n]
-                        : 0.0f;
-      }
-  }
+  entering_state<G>(hs, a, cb, swave, pcol, g4);
   // The Q/K column groups are worked on with two lanes per token: lane = token tkn
   // (< CS = 32) in half hf of the wave, which takes columns 8 g + 4 hf .. + 3 of group
   // g, i.e. its rope pairs 4 g + 2 hf + {0, 1}.
@@ -339,14 +230,7 @@ void scan_chunked_f32_kernel(ScanArgs a) {
       const int r = 4 * G::template qgroup<SO>(wave, k) + 2 * hf + j;
       carry[k][j] = (a.init_theta && has_init && r < R) ? a.init_theta[(long)ci_in * R + r] * kInvTwoPi : 0.0f;
     }
-  // staging never holds uninitialised bits: rows past the sequence end are not loaded
-  for (int i = tid; i < G::NQK * G::CS * G::SQ; i += G::NT) {
-    (&sm.rq[0][0])[i] = make_uint4(0, 0, 0, 0);
-    (&sm.rk[0][0])[i] = make_uint4(0, 0, 0, 0);
-  }
-  for (int i = tid; i < 2 * G::CS * G::SV; i += G::NT) (&sm.rv[0][0])[i] = make_uint4(0, 0, 0, 0);
-  for (int i = tid; i < 2 * G::CS * G::SA; i += G::NT) (&sm.ra[0][0])[i] = make_uint4(0, 0, 0, 0);
-  for (int i = tid; i < 2 * 3 * (G::CS + 4); i += G::NT) (&sm.rs[0][0][0])[i] = 0.0f;
+  zero_staging<G>(sm, tid);
 
   // ---- chunk constants and rotations of chunk cc, computed a chunk ahead.  Wave
   // kScalarWave writes the per-token constants to LDS (lane = token); every wave keeps
@@ -362,16 +246,8 @@ void scan_chunked_f32_kernel(ScanArgs a) {
     const int tl = lane < CS ? lane : 0;
     const float s_dt = tok ? sm.rs[pb][1][tl] : 0.0f;
     if (wave == kScalarWave) {
-      const float s_adt = tok ? sm.rs[pb][0][tl] : 0.0f;
-      const float s_tr = tok ? sm.rs[pb][2][tl] : 0.0f;
-      const float sig = sigmoid_fast(s_tr);
-      const float gam = s_dt * sig;
-      const float u = s_dt * (1.0f - sig);                                 // dt (1 - sigmoid), this token
-      float un = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x130, 0xf, 0xf, false));  // next token
-      if (lane == CS - 1) un = (t0 + CS < Lnx) ? sm.rs[pb][1][CS] * (1.0f - sigmoid_fast(sm.rs[pb][2][CS])) : 0.0f;
-      const float scl = gam + un;
-      const float acum = wave_incl_scan(lane < CS ? s_adt : 0.0f);
-      const float aend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), CS - 1));
+      const TokenScalars ts = token_scalars<CS>(sm.rs[pb], s_dt, tok, tl, t0, Lnx, lane);
+      const float gam = ts.gam, scl = ts.scl, acum = ts.acum, aend = ts.aend;
       if (lane < CS) {
         const float ablk = __shfl(acum, lane | 15, 64);
         sm.scl[pb][lane] = scl;
@@ -644,14 +520,7 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   }
   if (!SO && nc > 0) gate(nc - 1);
 
-  // final carry: k of the last token (kept in LDS by its preparation) and its v (still
-  // in the last chunk's staged rows)
-  if (a.fin_k && fin_here && nc > 0) {
-    for (int i = tid; i < N; i += G::NT) a.fin_k[(long)ci_out * N + i] = sm.fink[i];
-    for (int i = tid; i < P; i += G::NT)
-      a.fin_v[(long)ci_out * P + i] =
-          Elem<T>::to_f(*staged_elem<G::SV, T>(sm.rv[(nc - 1) & 1], L - 1 - (nc - 1) * CS, i));
-  }
+  final_kv<G>(a, sm, cb, tid);
   if (a.fin_h && fin_here && swave && part == 0) {
 #pragma unroll
     for (int nb = 0; nb < G::NB16; ++nb)
