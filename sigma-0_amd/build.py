@@ -27,6 +27,19 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
+# The chunk states come from two instantiations of each chunked kernel: the state-only
+# pass (the recomputing backward, the sequence split) and the full pass that saves them
+# (the training forward).  HIP's default contraction (fast) lets the backend fuse a
+# multiply into a later add across statements, so the same source could round
+# differently in the two (a last-bit difference in a rope'd key or a key weight that
+# the bf16 operand rounding then occasionally turns into a different state element).
+# Contraction within an expression only (on) makes every instantiation compute the
+# same operations; it leaves these kernels' instruction counts unchanged to within
+# 0.3%.
+FILE_CFLAGS = {
+    "m3_scan_chunked.hip": ["-ffp-contract=on"],
+    "m3_scan_chunked_f32.hip": ["-ffp-contract=on"],
+}
 
 
 def hipcc() -> str:
@@ -56,7 +69,7 @@ def build(verbose: bool = False) -> str:
     objs = [os.path.join(build_dir, s[:-4] + ".o") for s in srcs]
     t0 = time.time()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        futs = [ex.submit(_run, [cc, *CFLAGS, "-c", os.path.join(CSRC, s), "-o", o], verbose)
+        futs = [ex.submit(_run, [cc, *CFLAGS, *FILE_CFLAGS.get(s, []), "-c", os.path.join(CSRC, s), "-o", o], verbose)
                 for s, o in zip(srcs, objs)]
         for f in futs:
             f.result()

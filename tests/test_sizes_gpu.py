@@ -14,6 +14,10 @@ that the float64 oracle finishes quickly).
   32768 tokens against the float64 oracle, and every head against the
   chunk-parallel route (2e-2; 5e-2 for the whole-sequence cumsums dAngles and dADT,
   whose bf16 rounding grows with the length).
+* The backward at configuration 2's full shape (B=8, L=4096, H=32: the walk on all
+  256 workgroups at once): two (batch, head) pairs against the float64 oracle, every
+  gradient against the chunk-parallel route, and the training pair's backward equal to
+  the recomputing one bitwise.
 * Configuration 5, the 12-layer backbone at L=12288: batch row 0 against the oracle
   backbone's log-probabilities (a committed fixture, tests/golden/
   make_golden_config5.py: the oracle takes minutes at this size): 64 positions within
@@ -135,6 +139,63 @@ def test_backward_config3_full_size_split_walk(monkeypatch):
     assert not bad, f"gradients above their bar: {bad}"
     bad = {k: v for k, v in e_alt.items() if v > bar(k)}
     assert not bad, f"split walk and chunk route differ: {bad}"
+
+
+
+@pytest.mark.timeout(300)
+def test_backward_config2_full_size_walk(monkeypatch):
+    """The backward at configuration 2's own shape (B=8, L=4096, H=32; 256 pairs, so the
+    walk runs unsplit on every workgroup at once, the bench's configuration): pairs
+    (b, h) = (0, 0) and (5, 19) against autograd of the float64 oracle on their own
+    problem; every gradient of every pair against the chunk-parallel route (no shared
+    code with the walk beyond the state pass); the training pair's backward (the saved
+    chunk states instead of the state pass) equal to the recomputing one bitwise."""
+    import torch
+    from mamba3_rocm import mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
+    from oracle import mamba3_vjp as V
+    B, L, H, N, P, R, CS = 8, 4096, 32, 128, 64, 32, 64
+    print(f"[sizes] backward config 2 {(B, L, H, N, P, R, CS)} walk", flush=True)
+    monkeypatch.delenv("M3_BWD_ROUTE", raising=False)
+    t = device_scan_inputs(B, L, H, N, P, R, seed=42, io_dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(43)
+    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(torch.bfloat16)
+    args = tuple(t[k] for k in V.NAMES)
+    got = mamba3_siso_hip_bwd(*args, dout, chunk_size=CS)
+    _, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=CS)
+    from_saved = mamba3_siso_hip_bwd(*args, dout, chunk_size=CS, saved=saved)
+    monkeypatch.setenv("M3_BWD_ROUTE", "chunks")
+    alt = mamba3_siso_hip_bwd(*args, dout, chunk_size=CS)
+    torch.cuda.synchronize()
+    for k, a, b in zip(V.NAMES, got, from_saved):
+        assert torch.equal(a, b), f"training pair differs from the recomputing backward in d{k}"
+    e_alt = {k: rel(a.float().cpu().numpy(), b.float().cpu().numpy()) for k, a, b in zip(V.NAMES, got, alt)}
+    print("  walk vs chunk route: " + " ".join(f"{k}:{v:.1e}" for k, v in e_alt.items()), flush=True)
+    # per-(b, h) inputs and gradients: batch and head axes of each tensor (biases and D
+    # are per head, their gradients summed over the batch: checked against the chunk
+    # route only)
+    axes = {"Q": (0, 2), "K": (0, 2), "V": (0, 2), "Z": (0, 2), "Angles": (0, 2), "ADT": (0, 1), "DT": (0, 1),
+            "Trap": (0, 1), "Q_bias": (None, 0), "K_bias": (None, 0), "D": (None, 0)}
+    def pick(x, name, b, h):
+        ba, ha = axes[name]
+        x = x.narrow(ha, h, 1)
+        return x.narrow(ba, b, 1) if ba is not None else x
+    for b, h in ((0, 0), (5, 19)):
+        d = {k: pick(t[k], k, b, h).float().cpu().numpy() for k in V.NAMES}
+        cot = dout[b:b + 1, :, h:h + 1].float().cpu().numpy()
+        _, ref = V.vjp(d, cot, CS)
+        errs = {}
+        for name, a, r in zip(V.NAMES, got, ref):
+            if axes[name][0] is None:
+                continue
+            a = pick(a, name, b, h).float().cpu().numpy()
+            assert np.isfinite(a).all(), name
+            errs[name] = rel(a, r)
+        print(f"  pair {(b, h)} vs oracle: " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+        bad = {k: v for k, v in errs.items() if v > GRAD_TOL}
+        assert not bad, f"pair {(b, h)}: gradients above {GRAD_TOL}: {bad}"
+    bad = {k: v for k, v in e_alt.items() if v > GRAD_TOL}
+    assert not bad, f"walk and chunk route differ: {bad}"
 
 
 def _torch_params(p):
