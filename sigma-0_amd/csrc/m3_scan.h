@@ -44,6 +44,10 @@ struct ScanArgs {
   // in the I/O type, which the backward multiplies into dZ instead of recomputing it
   // (last, so that the other members keep their kernel-argument offsets).
   void* out_v = nullptr;
+  // State-only pass of a sequence split: the last segment's block exits at once (the
+  // split reads the exit carries of the other segments only; the last segment's final
+  // carry comes from the full pass).
+  int so_skip_last = 0;
 };
 
 // Block order for launches whose heads share Q/K rows: blocks are handed to the 8

@@ -130,6 +130,9 @@ void scan_chunked_f32_kernel(ScanArgs a) {
   typedef MF16<T> W;
   static_assert(sizeof(Smem<G>) <= 160 * 1024, "LDS budget");
   __shared__ Smem<G> sm;
+  if constexpr (SO) {
+    if (a.so_skip_last && blockIdx.y + 1 == gridDim.y) return;   // before any barrier: the whole block
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;

@@ -176,6 +176,7 @@ hipError_t scan_split_launch(const ScanArgs& a, bool bf16_io, void* ws, hipStrea
   p1.chunk_th = nullptr;
   p1.out_v = nullptr;
   p1.CS = 64;                                        // 64-token (bf16) or 32-token (float32) sub-chunks
+  p1.so_skip_last = 1;                               // no segment reads the last one's exit carry
   hipError_t e = scan_state_launch(p1, bf16_io, st);
   if (e != hipSuccess) return e;
 
@@ -209,6 +210,7 @@ hipError_t scan_split_state_launch(const ScanArgs& a, bool bf16_io, void* ws, hi
   p1.fin_per_seg = 1;
   p1.chunk_h = nullptr;
   p1.chunk_th = nullptr;
+  p1.so_skip_last = 1;                               // no segment reads the last one's exit carry
   hipError_t e = scan_state_launch(p1, bf16_io, st);
   if (e != hipSuccess) return e;
 
