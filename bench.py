@@ -56,8 +56,9 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "scan_chunked_bf16_config2_traffic
 SCAN_KERNEL = "scan_chunked_kernelIDF16bLi64ELi128ELi64ELi32ELi12ELb0E"
 # the sources the headline kernel is built from: the traffic measured for one
 # version of them says nothing about another
-KERNEL_SOURCES = ("sigma-0_amd/csrc/m3_scan_chunked.hip", "sigma-0_amd/csrc/m3_chunk_common.h",
-                  "sigma-0_amd/csrc/m3_common.h", "sigma-0_amd/csrc/m3_scan.h")
+KERNEL_SOURCES = ("sigma-0_amd/csrc/m3_scan_chunked.hip", "sigma-0_amd/csrc/m3_chunk_block.h",
+                  "sigma-0_amd/csrc/m3_chunk_common.h", "sigma-0_amd/csrc/m3_common.h", "sigma-0_amd/csrc/m3_scan.h",
+                  "sigma-0_amd/build.py")       # the compile flags too
 
 
 def kernel_sources_sha():
