@@ -1072,6 +1072,9 @@ struct WalkSmem {
   alignas(16) T dpm[CS][CS + PAD];     // dP masked and decayed
   alignas(16) char u[U];
   alignas(16) float ac[CS];
+  // e^{A_cum,t} and e^{A_end - A_cum,t}, formed once per chunk: the row factors of
+  // Y_off (y), of dv's and dk~'s G terms, of dq~'s h term and of the adjoint update
+  alignas(16) float ea[CS], eb[CS];
   float gam[CS], scl[CS], dtv[CS], qk[CS], dqk[CS];
   // per token, one row per column-group wave (its two groups): q^.k^, then
   // q~.dq~ - k~.dk~; dk~ . rot(k^)
@@ -1326,6 +1329,8 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       const float ae = __shfl(acum, CS - 1, 64);
       if (lane < CS) {
         sm.ac[lane] = acum;
+        sm.ea[lane] = exp2_fast(acum * kLog2e);
+        sm.eb[lane] = exp2_fast((ae - acum) * kLog2e);
         sm.gam[lane] = gm;
         sm.scl[lane] = tok ? gm + un : 0.0f;
         sm.dtv[lane] = dtl;
@@ -1537,7 +1542,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         float vv[4], ff[4], o[4];
         load4(&sm.v[tl][p], vv);
         load4(&sm.fz[tl][p], ff);
-        const float ea = exp2_fast(sm.ac[tl] * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = sm.ea[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
         store4(sm.outs(0) + tl * (P + PAD) + p, o);
@@ -1567,7 +1572,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
         float yy[4], o[4];
         load4(&sm.dy[tl][p], yy);
-        const float ea = exp2_fast((aend - sm.ac[tl]) * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = sm.eb[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
         store4(sm.outs(1) + tl * (P + PAD) + p, o);
@@ -1612,7 +1617,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         float vv[4], ff[4], o[4];
         load4(&sm.v[tl][p], vv);
         load4(&sm.fz[tl][p], ff);
-        const float ea = exp2_fast(sm.ac[tl] * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = sm.ea[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
         store4(sm.outs(0) + tl * (P + PAD) + p, o);
@@ -1627,7 +1632,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
                         acc2);
         float yy[4], o[4];
         load4(&sm.dy[tl][p], yy);
-        const float ea = exp2_fast((aend - sm.ac[tl]) * kLog2e), dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = sm.eb[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
         store4(sm.outs(1) + tl * (P + PAD) + p, o);
@@ -1659,7 +1664,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       for (int k0 = 0; k0 < CS; k0 += KS) {
         float w[W::WN];
 #pragma unroll
-        for (int j = 0; j < W::WN; ++j) w[j] = exp2_fast(sm.ac[W::ktok(k0, lane) + j] * kLog2e);
+        for (int j = 0; j < W::WN; ++j) w[j] = sm.ea[W::ktok(k0, lane) + j];
         const typename W::frag qf = W::scale(W::ldt(&sm.qt[0][0], N + PADN, k0, 16 * ntile, lane), w);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
@@ -1742,7 +1747,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * rt + 4 * (lane >> 4) + r;
-          const float w = exp2_fast((isq ? sm.ac[t] : aend - sm.ac[t]) * kLog2e);
+          const float w = isq ? sm.ea[t] : sm.eb[t];
           rb[t * (NH + 4) + nl] = acc[r] + w * acc2[r];
         }
       }
@@ -1964,7 +1969,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * (ra + 2 * u2) + 4 * (lane >> 4) + r;
-            const float w = exp2_fast((isq ? sm.ac[t] : aend - sm.ac[t]) * kLog2e);
+            const float w = isq ? sm.ea[t] : sm.eb[t];
             rb[t * (S::NQ + 4) + nl] = acc[r] + w * acc2[r];
           }
         }
