@@ -1482,31 +1482,63 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     // the diagonal are computed and masked like the others), so that their loads and
     // MFMA chains interleave.
     static_assert(2 * TB * TB % kBwdWaves == 0, "S/dP tiles: whole rounds");
+    if constexpr (TB * TB % kBwdWaves == 0) {
+      // a wave takes whole (query block, key block) pairs: its S and dP tiles share the
+      // decay factors, and the two MFMA chains interleave
 #pragma unroll
-    for (int j = 0; j < 2 * TB * TB / kBwdWaves; ++j) {
-      const int i = wave + kBwdWaves * j;
-      const int which = i / (TB * TB), tt = (i % (TB * TB)) / TB, st = (i % (TB * TB)) % TB;
-      // transposed tiles [s][t]: each lane holds 4 consecutive keys s of one query t
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (which == 0) {
+      for (int j = 0; j < TB * TB / kBwdWaves; ++j) {
+        const int i = wave + kBwdWaves * j;
+        const int tt = i / TB, st = i % TB;
+        // transposed tiles [s][t]: each lane holds 4 consecutive keys s of one query t
+        f32x4 accs = {0.0f, 0.0f, 0.0f, 0.0f}, accp = accs;
 #pragma unroll
         for (int k0 = 0; k0 < N; k0 += KS)
-          acc = W::mma(W::ld(&sm.kt[0][0], N + PADN, 16 * st, k0, lane), W::ld(&sm.qt[0][0], N + PADN, 16 * tt, k0, lane),
-                       acc);
-      } else {
+          accs = W::mma(W::ld(&sm.kt[0][0], N + PADN, 16 * st, k0, lane), W::ld(&sm.qt[0][0], N + PADN, 16 * tt, k0, lane),
+                        accs);
 #pragma unroll
         for (int k0 = 0; k0 < P; k0 += KS)
-          acc = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * st, k0, lane), W::ld(&sm.dy[0][0], P + PAD, 16 * tt, k0, lane),
-                       acc);
-      }
-      const int t = 16 * tt + (lane & 15), s0 = 16 * st + 4 * (lane >> 4);
-      T* dst = which == 0 ? smk : &sm.dpm[0][0];
-      const float at = sm.ac[t];
-      float as[4], val[4];
-      load4(&sm.ac[s0], as);
+          accp = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * st, k0, lane), W::ld(&sm.dy[0][0], P + PAD, 16 * tt, k0, lane),
+                        accp);
+        const int t = 16 * tt + (lane & 15), s0 = 16 * st + 4 * (lane >> 4);
+        const float at = sm.ac[t];
+        float as[4], vs[4], vp[4];
+        load4(&sm.ac[s0], as);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) val[r] = s0 + r < t ? acc[r] * exp2_fast((at - as[r]) * kLog2e) : 0.0f;
-      store4(dst + t * (CS + PAD) + s0, val);
+        for (int r = 0; r < 4; ++r) {
+          const float e = exp2_fast((at - as[r]) * kLog2e);
+          vs[r] = s0 + r < t ? accs[r] * e : 0.0f;
+          vp[r] = s0 + r < t ? accp[r] * e : 0.0f;
+        }
+        store4(smk + t * (CS + PAD) + s0, vs);
+        store4(&sm.dpm[0][0] + t * (CS + PAD) + s0, vp);
+      }
+    } else {
+      // (32-token chunks: four pairs, so the S and dP tiles of a pair go to two waves)
+#pragma unroll
+      for (int j = 0; j < 2 * TB * TB / kBwdWaves; ++j) {
+        const int i = wave + kBwdWaves * j;
+        const int which = i / (TB * TB), tt = (i % (TB * TB)) / TB, st = (i % (TB * TB)) % TB;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (which == 0) {
+#pragma unroll
+          for (int k0 = 0; k0 < N; k0 += KS)
+            acc = W::mma(W::ld(&sm.kt[0][0], N + PADN, 16 * st, k0, lane), W::ld(&sm.qt[0][0], N + PADN, 16 * tt, k0, lane),
+                         acc);
+        } else {
+#pragma unroll
+          for (int k0 = 0; k0 < P; k0 += KS)
+            acc = W::mma(W::ld(&sm.v[0][0], P + PAD, 16 * st, k0, lane), W::ld(&sm.dy[0][0], P + PAD, 16 * tt, k0, lane),
+                         acc);
+        }
+        const int t = 16 * tt + (lane & 15), s0 = 16 * st + 4 * (lane >> 4);
+        T* dst = which == 0 ? smk : &sm.dpm[0][0];
+        const float at = sm.ac[t];
+        float as[4], val[4];
+        load4(&sm.ac[s0], as);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) val[r] = s0 + r < t ? acc[r] * exp2_fast((at - as[r]) * kLog2e) : 0.0f;
+        store4(dst + t * (CS + PAD) + s0, val);
+      }
     }
     __syncthreads();
     if (c > c_lo) cur.template issue<1>(a, c - 1, bh, tid, wave, lane);
