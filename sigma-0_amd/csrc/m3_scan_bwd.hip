@@ -2473,54 +2473,57 @@ __device__ __forceinline__ void load4f(const float* p, float f[4]) {
 // GQA: dQ, dK of a Q/K head = sum over the value heads that share it, in float32 over
 // the per-head partials (in the I/O type: with bf16 I/O the partials exchanged are
 // bf16, as the reference's fused path exchanges its per-head gradient tiles in its io
-// dtype, mamba3_pallas.py:832-836).  Thread = four consecutive columns of one
-// (b, t, hq) row of both; the heads are summed in order, eight loads of each in flight.
+// dtype, mamba3_pallas.py:832-836).  Thread = eight consecutive columns of one
+// (b, t, hq) row of both (16-byte loads and stores at bf16); the heads are summed in
+// order, eight loads of each in flight.
 template <typename T>
 __global__ __launch_bounds__(256) void scan_bwd_gqa_kernel(BwdArgs a) {
-  const int B = a.s.B, L = a.s.L, H = a.s.H, HQ = a.s.Hqk, N = a.s.N, N4 = N / 4, rep = H / HQ;
-  const long total = (long)B * L * HQ * N4;
+  const int B = a.s.B, L = a.s.L, H = a.s.H, HQ = a.s.Hqk, N = a.s.N, N8 = N / 8, rep = H / HQ;
+  const long total = (long)B * L * HQ * N8;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
-    const int n4 = i % N4;
-    const long row = i / N4;                     // (b, t, hq)
+    const int n8 = i % N8;
+    const long row = i / N8;                     // (b, t, hq)
     const int hq = row % HQ;
     const long bt = row / HQ;
-    const long s0 = (bt * H + (long)hq * rep) * N + 4 * n4;
+    const long s0 = (bt * H + (long)hq * rep) * N + 8 * n8;
     const T* q = reinterpret_cast<const T*>(a.dqh) + s0;
     const T* k = reinterpret_cast<const T*>(a.dkh) + s0;
-    float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float sq[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, sk[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     int j = 0;
     for (; j + 8 <= rep; j += 8) {
-      float vq[8][4], vk[8][4];
+      Vec8<T> vq[8], vk[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        load4f(q + (long)(j + u) * N, vq[u]);
-        load4f(k + (long)(j + u) * N, vk[u]);
+        vq[u].load(q + (long)(j + u) * N);
+        vk[u].load(k + (long)(j + u) * N);
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < 8; ++u) {
+        float fq[8], fk[8];
+        vq[u].to_f(fq);
+        vk[u].to_f(fk);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sq[e] += vq[u][e];
-          sk[e] += vk[u][e];
+        for (int e = 0; e < 8; ++e) {
+          sq[e] += fq[e];
+          sk[e] += fk[e];
         }
+      }
     }
     for (; j < rep; ++j) {
-      float vq[4], vk[4];
-      load4f(q + (long)j * N, vq);
-      load4f(k + (long)j * N, vk);
+      Vec8<T> vq, vk;
+      vq.load(q + (long)j * N);
+      vk.load(k + (long)j * N);
+      float fq[8], fk[8];
+      vq.to_f(fq);
+      vk.to_f(fk);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sq[e] += vq[e];
-        sk[e] += vk[e];
+      for (int e = 0; e < 8; ++e) {
+        sq[e] += fq[e];
+        sk[e] += fk[e];
       }
     }
-    T* dq = reinterpret_cast<T*>(a.dq) + 4 * i;
-    T* dk = reinterpret_cast<T*>(a.dk) + 4 * i;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      dq[e] = (T)sq[e];
-      dk[e] = (T)sk[e];
-    }
+    store8(reinterpret_cast<T*>(a.dq) + 8 * i, sq);
+    store8(reinterpret_cast<T*>(a.dk) + 8 * i, sk);
   }
 }
 
