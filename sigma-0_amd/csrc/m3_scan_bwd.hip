@@ -1179,6 +1179,19 @@ void scan_bwd_walk_kernel(BwdArgs a) {
   // bf16 shapes keep the row stores from LDS after each pass
   constexpr bool kQP = S::QP;
   constexpr bool kDirect = !BF || kQP;
+  // The per-token decay factors e^{A_t} and e^{A_end - A_t} are read from LDS (formed
+  // once per chunk) and a wave's S and dP tiles of a block share theirs, except with
+  // rope on every pair (R = N/2), whose instantiations are the tightest in registers:
+  // there the loads kept live cost more in spills than the exponentials they replace.
+  constexpr bool kHoist = 2 * R < N;
+  auto exp_a = [&](int t) -> float {
+    if constexpr (kHoist) return sm.ea[t];
+    else return exp2_fast(sm.ac[t] * kLog2e);
+  };
+  auto exp_b = [&](int t, float ae) -> float {
+    if constexpr (kHoist) return sm.eb[t];
+    else return exp2_fast((ae - sm.ac[t]) * kLog2e);
+  };
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __builtin_assume(wave >= 0 && wave < kBwdWaves);
   const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc;
@@ -1482,7 +1495,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
     // the diagonal are computed and masked like the others), so that their loads and
     // MFMA chains interleave.
     static_assert(2 * TB * TB % kBwdWaves == 0, "S/dP tiles: whole rounds");
-    if constexpr (TB * TB % kBwdWaves == 0) {
+    if constexpr (kHoist && TB * TB % kBwdWaves == 0) {
       // a wave takes whole (query block, key block) pairs: its S and dP tiles share the
       // decay factors, and the two MFMA chains interleave
 #pragma unroll
@@ -1574,7 +1587,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         float vv[4], ff[4], o[4];
         load4(&sm.v[tl][p], vv);
         load4(&sm.fz[tl][p], ff);
-        const float ea = sm.ea[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = exp_a(tl), dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
         store4(sm.outs(0) + tl * (P + PAD) + p, o);
@@ -1604,7 +1617,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         const f32x4 acc = u2 ? c1 : c0, acc2 = u2 ? d1 : d0;
         float yy[4], o[4];
         load4(&sm.dy[tl][p], yy);
-        const float ea = sm.eb[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = exp_b(tl, aend), dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
         store4(sm.outs(1) + tl * (P + PAD) + p, o);
@@ -1649,7 +1662,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
         float vv[4], ff[4], o[4];
         load4(&sm.v[tl][p], vv);
         load4(&sm.fz[tl][p], ff);
-        const float ea = sm.ea[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = exp_a(tl), dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = (acc[r] + ea * acc2[r] + dg * vv[r]) * ff[r];
         store4(sm.outs(0) + tl * (P + PAD) + p, o);
@@ -1664,7 +1677,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
                         acc2);
         float yy[4], o[4];
         load4(&sm.dy[tl][p], yy);
-        const float ea = sm.eb[tl], dg = Dh + sm.gam[tl] * sm.qk[tl];
+        const float ea = exp_b(tl, aend), dg = Dh + sm.gam[tl] * sm.qk[tl];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = acc[r] + ea * acc2[r] + dg * yy[r];
         store4(sm.outs(1) + tl * (P + PAD) + p, o);
@@ -1696,7 +1709,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       for (int k0 = 0; k0 < CS; k0 += KS) {
         float w[W::WN];
 #pragma unroll
-        for (int j = 0; j < W::WN; ++j) w[j] = sm.ea[W::ktok(k0, lane) + j];
+        for (int j = 0; j < W::WN; ++j) w[j] = exp_a(W::ktok(k0, lane) + j);
         const typename W::frag qf = W::scale(W::ldt(&sm.qt[0][0], N + PADN, k0, 16 * ntile, lane), w);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
@@ -1779,7 +1792,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * rt + 4 * (lane >> 4) + r;
-          const float w = isq ? sm.ea[t] : sm.eb[t];
+          const float w = isq ? exp_a(t) : exp_b(t, aend);
           rb[t * (NH + 4) + nl] = acc[r] + w * acc2[r];
         }
       }
@@ -2001,7 +2014,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * (ra + 2 * u2) + 4 * (lane >> 4) + r;
-            const float w = isq ? sm.ea[t] : sm.eb[t];
+            const float w = isq ? exp_a(t) : exp_b(t, aend);
             rb[t * (S::NQ + 4) + nl] = acc[r] + w * acc2[r];
           }
         }
