@@ -19,8 +19,10 @@ Also reported on the same JSON line:
                 config 2 and at config 3's shape (recomputing its chunk states) and the
                 training pair (forward with residuals, backward from them), with bf16
                 and with float32 I/O (what the model's training hands the scan),
-                each with its own roofline, and the 12-layer backbone prefill with
-                its log-probabilities (config 5)
+                each with its own roofline, the scan forward, backward and training
+                pair at config 5's layer shape (B=4, L=12288, 24 heads: 96 pairs, the
+                sequence split and the split walk), and the 12-layer backbone prefill
+                with its log-probabilities (config 5)
 
 Before the warm-up of the headline, the kernel is launched untimed until at least
 100 launches and 0.3 s have run (the GPU clocks ramp up over the first ~100
@@ -29,7 +31,7 @@ launches of a process); the JSON line reports this as ``clock_settle``, apart fr
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-secondary]
-                       [--mode scan|decode|long|bwd|bwd3|train|shared|shared_bwd|layer|stack|copy|fp32]
+                       [--mode scan|decode|long|bwd|bwd3|bwd5|train|shared|shared_bwd|layer|stack|copy|fp32]
                        [--io bf16|f32]   (--mode bwd / train)
        python bench.py --mode traffic --pmc-dir DIR   (writes the traffic JSON of
                        the headline kernel from rocprofv3 --pmc FETCH_SIZE /
@@ -545,7 +547,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "bwd3", "train", "shared", "shared_bwd", "layer",
+    ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "bwd3", "bwd5", "train", "shared", "shared_bwd",
+                                       "layer",
                                        "stack", "copy", "fp32", "traffic"), default="scan")
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -590,6 +593,17 @@ def main():
         t = bench_train(torch, 1, 32768, 32, 128, 64, 32, 128, args.steps, args.warmup, seed=3, io_dtype=io)
         print(json.dumps({"mode": "bwd3", "io_dtype": args.io, **bwd_line(r, tokens=32768),
                           "training_pair": train_line(t, tokens=32768)}), flush=True)
+        return
+    if args.mode == "bwd5":
+        # the scan forward, backward and training pair at config 5's layer shape (B*H = 96:
+        # the sequence split and the split walk)
+        f = bench_scan(torch, 4, 12288, 24, 128, 64, 32, 64, args.steps, args.warmup, seed=5, io_dtype=io)
+        r = bench_bwd(torch, 4, 12288, 24, 128, 64, 32, 64, args.steps, args.warmup, seed=5, io_dtype=io)
+        t = bench_train(torch, 4, 12288, 24, 128, 64, 32, 64, args.steps, args.warmup, seed=5, io_dtype=io)
+        print(json.dumps({"mode": "bwd5", "io_dtype": args.io, "scan_kernel_ms": round(f["kernel_s"] * 1e3, 4),
+                          "scan_frac_hbm": round(f["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                          **bwd_line(r, tokens=4 * 12288), "training_pair": train_line(t, tokens=4 * 12288)}),
+              flush=True)
         return
     if args.mode == "train":
         # the training pair at config 2 (forward with residuals, backward from them)
@@ -682,6 +696,9 @@ def main():
         shb = bench_shared_bwd(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2)
         bw3 = bench_bwd(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 10), 2, seed=3)
         tr3 = bench_train(torch, 1, 32768, 32, 128, 64, 32, 128, max(5, args.steps // 10), 2, seed=3)
+        sc5 = bench_scan(torch, 4, 12288, 24, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=5)
+        bw5 = bench_bwd(torch, 4, 12288, 24, 128, 64, 32, 64, max(5, args.steps // 10), 2, seed=5)
+        tr5 = bench_train(torch, 4, 12288, 24, 128, 64, 32, 64, max(5, args.steps // 10), 2, seed=5)
         f32 = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2,
                          io_dtype=torch.float32)
         bb = bench_stack(torch, 4, 12288, 768, 12, 2112, 5, 2, seed=5)
@@ -712,6 +729,15 @@ def main():
             "training_pair_config3_shape": {"B": 1, "L": 32768, "H": 32, "chunk": 128,
                                             **train_line(tr3, tokens=32768)},
             "training_pair_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, **train_line(tr)},
+            "scan_config5_layer_shape": {"B": 4, "L": 12288, "H": 24, "chunk": 64,
+                                         "kernel_ms": round(sc5["kernel_s"] * 1e3, 4),
+                                         "tokens_per_s": round(4 * 12288 / sc5["wall_s"], 1),
+                                         "achieved_gbs": round(sc5["achieved_gbs"], 1),
+                                         "frac_hbm": round(sc5["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+            "backward_config5_layer_shape": {"B": 4, "L": 12288, "H": 24, "chunk": 64,
+                                             **bwd_line(bw5, tokens=4 * 12288)},
+            "training_pair_config5_layer_shape": {"B": 4, "L": 12288, "H": 24, "chunk": 64,
+                                                  **train_line(tr5, tokens=4 * 12288)},
             "backward_fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",
                                          **bwd_line(bw32, fp32=True)},
             "training_pair_fp32_io_config2": {"B": 8, "L": 4096, "H": 32, "chunk": 64, "io_dtype": "f32",

@@ -2550,20 +2550,22 @@ struct BwdWs {
 // the chip only when B * H is large; below kWalkMinBH the chunk-parallel kernels (one
 // workgroup per (chunk, b, h), with the adjoint pass before them) run instead.
 // Measured (bf16, d_state 128, headdim 64): the routes tie at 64 pairs (1.08 / 1.05
-// ms at L=4096), the walk wins at 96 (3.25 / 3.97 ms at config 5's B=4, L=12288,
-// H=24) and 128 (1.12 / 1.54 ms), the chunks at 32 (2.11 / 1.60 ms at L=8192).  The
-// environment variable M3_BWD_ROUTE = "walk" or "chunks" forces one of them (tests,
-// measurements).
-// Below kWalkMinBH pairs the walk is split into sequence segments when the sequence
-// has at least two segments of kWalkMinSegChunks chunks: about kWalkTargetBlocks
-// workgroups (one wave of blocks on the chip), each walking its segment from the
-// adjoint state that the later segments leave (an adjoint-only pass per segment and a
-// reverse combine, the backward's form of the forward's sequence split).  Shorter
-// sequences take the chunk-parallel route.  M3_BWD_ROUTE = "segments" forces the split
-// walk (segments of at least two chunks), "walk" the one-segment walk.
+// ms at L=4096), the one-segment walk wins at 96 (3.25 / 3.97 ms at config 5's B=4,
+// L=12288, H=24) and 128 (1.12 / 1.54 ms), the chunks at 32 (2.11 / 1.60 ms at
+// L=8192).  The environment variable M3_BWD_ROUTE = "walk" or "chunks" forces one of
+// them (tests, measurements).
+// Below kWalkTargetBlocks pairs the walk is split into sequence segments, each walked
+// from the adjoint state that the later segments leave (an adjoint-only pass per
+// segment and a reverse combine, the backward's form of the forward's sequence split),
+// when the sequence holds at least two segments of kWalkMinSegChunks chunks and the
+// split's modelled time (split_cost) is at most 0.8 of the one-segment walk's; below
+// kWalkMinBH pairs whenever it can, and otherwise shorter sequences take the
+// chunk-parallel route.  M3_BWD_ROUTE = "segments" forces the split walk (segments
+// of at least two chunks), "walk" the one-segment walk.
 constexpr long kWalkMinBH = 80;
 constexpr int kWalkTargetBlocks = 256;
 constexpr int kWalkMinSegChunks = 4;
+constexpr int kWalkMaxRounds = 4;
 struct BwdRoute {
   bool walk;
   int nseg, seg_nc;
@@ -2571,20 +2573,48 @@ struct BwdRoute {
   // more are cut in up to four
   int adj_sub() const { return nseg > 1 ? std::max(1, std::min(4, seg_nc / 8)) : 1; }
 };
+// Modelled time of the split walk, in half-chunks of one walk block.  The walk's n
+// blocks of seg_nc chunks take ceil(n / 256) rounds of seg_nc chunks (12.6-13.0 us
+// per chunk at 256 blocks, split or not); the adjoint-only pass runs two blocks per
+// compute unit, each at about half a walk chunk's time per chunk (203 us for 896
+// blocks of 16 chunks).  At config 5's layer shape (96 pairs, 192 chunks) the model
+// picks 8 segments of 24 chunks: the backward took 1.66 against 2.76 ms with the
+// one-segment walk, and 1.26 against 2.39 ms from the training forward's residuals.
+long split_cost(long bh, const BwdRoute& r) {
+  const long sub = r.adj_sub(), sub_nc = (r.seg_nc + sub - 1) / sub;
+  const long walk_rounds = (bh * r.nseg + kWalkTargetBlocks - 1) / kWalkTargetBlocks;
+  const long adj_rounds = (bh * (r.nseg - 1) * sub + 2 * kWalkTargetBlocks - 1) / (2 * kWalkTargetBlocks);
+  return 2 * walk_rounds * r.seg_nc + adj_rounds * sub_nc;
+}
 BwdRoute bwd_route(int B, int H, int L, int CS) {
   const long bh = (long)B * H, nc = (L + CS - 1) / CS;
+  // the segment count with the least modelled time (the fewest on ties), or one segment
   auto split = [&](int min_chunks) {
-    const long s = std::min<long>(kWalkTargetBlocks / std::max<long>(bh, 1), nc / min_chunks);
-    if (s < 2) return BwdRoute{true, 1, (int)nc};
-    const int seg_nc = (int)((nc + s - 1) / s);
-    return BwdRoute{true, (int)((nc + seg_nc - 1) / seg_nc), seg_nc};
+    const long smax = std::min<long>(nc / min_chunks, kWalkMaxRounds * kWalkTargetBlocks / std::max<long>(bh, 1));
+    BwdRoute best{true, 1, (int)nc};
+    long best_cost = 0;
+    for (long s = 2; s <= smax; ++s) {
+      const int seg_nc = (int)((nc + s - 1) / s);
+      const BwdRoute r{true, (int)((nc + seg_nc - 1) / seg_nc), seg_nc};
+      if (r.nseg < 2) continue;
+      const long cost = split_cost(bh, r);
+      if (best.nseg == 1 || cost < best_cost) {
+        best = r;
+        best_cost = cost;
+      }
+    }
+    return best;
   };
   const char* e = getenv("M3_BWD_ROUTE");
   if (e && !strcmp(e, "walk")) return {true, 1, (int)nc};
   if (e && !strcmp(e, "chunks")) return {false, 1, (int)nc};
   if (e && !strcmp(e, "segments")) return split(2);
-  if (bh >= kWalkMinBH) return {true, 1, (int)nc};
+  if (bh >= kWalkTargetBlocks) return {true, 1, (int)nc};
   const BwdRoute r = split(kWalkMinSegChunks);
+  if (bh >= kWalkMinBH) {
+    // the one-segment walk: ceil(bh / 256) = 1 round of nc chunks (2 nc half-chunks)
+    return r.nseg > 1 && 10 * split_cost(bh, r) <= 8 * 2 * nc ? r : BwdRoute{true, 1, (int)nc};
+  }
   return r.nseg > 1 ? r : BwdRoute{false, 1, (int)nc};
 }
 bool bwd_walk(int B, int H, int L, int CS) { return bwd_route(B, H, L, CS).walk; }

@@ -30,17 +30,39 @@ namespace {
 constexpr int kCombineThreads = 256;
 constexpr int kTargetBlocks = 256;     // MI355X compute units
 constexpr int kMinSegment = 256;       // tokens
+constexpr int kMaxRounds = 4;          // rounds of blocks on the chip, at most
 
 // Segment length for a (B, H, L) launch, or 0 for no split.  Segments are whole
 // multiples of 128 tokens, so every interior segment ends on a kernel chunk.
+// Time model: n blocks of len tokens take ceil(n / kTargetBlocks) rounds of len (one
+// block per compute unit), and the state-only pass, which runs every segment but the
+// last, half the full pass's time per token.  The segment count with the least
+// modelled time is taken (the fewest on ties).  For 96 pairs (config 5's layer) that
+// is eight segments, three whole rounds of 256 blocks, rather than two (192 blocks,
+// and 96 in the state-only pass): in the 12-layer stack the layer's three launches
+// took 375 against 417 us.  The model takes a block's time per chunk as fixed; with
+// per-head B/C rows at the same shape, where the chip's memory traffic is larger, the
+// full pass gained less (285 against 293 us) and the three launches took 1.5% longer
+// (0.459 against 0.452 ms by bench.py).
 int seg_len_for(int B, int H, int L) {
   const int bh = B * H;
   if (bh <= 0 || bh * 2 > kTargetBlocks || L < 2 * kMinSegment) return 0;
-  // whole waves of blocks only: a partly filled second wave costs a full segment time
-  const int s = min(kTargetBlocks / bh, L / kMinSegment);
-  if (s < 2) return 0;
-  const int len = ((L + s - 1) / s + 127) / 128 * 128;
-  return (L + len - 1) / len >= 2 ? len : 0;
+  const int smax = min(L / kMinSegment, kMaxRounds * kTargetBlocks / bh);
+  int best = 0;
+  long best_cost = 0;
+  for (int s = 2; s <= smax; ++s) {
+    const int len = ((L + s - 1) / s + 127) / 128 * 128;
+    const long ns = (L + len - 1) / len;
+    if (ns < 2) continue;
+    const long rounds = (bh * ns + kTargetBlocks - 1) / kTargetBlocks;
+    const long so_rounds = (bh * (ns - 1) + kTargetBlocks - 1) / kTargetBlocks;
+    const long cost = (2 * rounds + so_rounds) * len;     // in half-token units of one block
+    if (best == 0 || cost < best_cost) {
+      best = len;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 struct Carries {

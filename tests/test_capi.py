@@ -101,37 +101,75 @@ def test_split_workspace_sizes(lib):
     assert f(1, 4096, 2, 64, 64, 16, 64, bf) == 0            # no state-only pass for d_state 64
     assert f(1, 4096, 2, 128, 64, 32, 48, bf) == 0           # chunk 48: generic kernel
     assert f(1, 1061, 3, 128, 64, 32, 64, bf) > 0
+    # config 5's layer: B*H = 96 -> 8 segments of 1536 tokens (768 blocks: three whole
+    # rounds of 256), not 2 (192 blocks, and 96 in the state-only pass)
+    assert _fwd_segments(4, 24, 12288) == (8, 1536)
+    bhs = 96 * 8
+    assert f(4, 12288, 24, 128, 64, 32, 64, bf) == (2 * (al(bhs * 64 * 128) + al(bhs * 128) + al(bhs * 64) + al(bhs * 32))
+                                                    + al(bhs))
+    assert _fwd_segments(1, 32, 32768) == (8, 4096)
+    assert _fwd_segments(2, 64, 8192) == (2, 4096)     # 128 pairs: one round of 256 blocks
+
+
+def _fwd_segments(B, H, L):
+    """(segments, tokens per segment) of the forward's sequence split, or (0, 0).
+    Segments are multiples of 128 tokens, at least 256, at most four rounds of 256
+    blocks.  Each block takes a fixed time per token, so n blocks of len tokens take
+    ceil(n / 256) rounds of len; the state-only pass (every segment but the last) runs
+    at half the full pass's time per token.  The count with the least time (the fewest
+    on ties) is taken."""
+    bh = B * H
+    if bh * 2 > 256 or L < 512:
+        return 0, 0
+    best, best_cost = (0, 0), None
+    for s in range(2, min(L // 256, 4 * 256 // bh) + 1):
+        ln = ((L + s - 1) // s + 127) // 128 * 128
+        ns = (L + ln - 1) // ln
+        if ns < 2:
+            continue
+        cost = (2 * -(-bh * ns // 256) + -(-bh * (ns - 1) // 256)) * ln
+        if best_cost is None or cost < best_cost:
+            best, best_cost = (ns, ln), cost
+    return best
 
 
 def _walk_segments(B, H, L, cs):
-    """(segments, chunks per segment) of the backward's walk: one segment at 80 pairs
-    or more; below, about 256 blocks of at least 4 chunks each when that gives two or
-    more (else the chunk-parallel route: 0 segments)."""
+    """(segments, chunks per segment) of the backward's walk (0 segments: the
+    chunk-parallel route).  Split candidates: at least two segments of at least 4
+    chunks, at most four rounds of 256 blocks; their time, in half-chunks of one walk
+    block: 2 ceil(walk blocks / 256) seg_nc for the walk, plus ceil(adjoint blocks /
+    512) chunks per adjoint block for the adjoint-only pass (sub-segments: seg_nc // 8,
+    between 1 and 4, per segment but the last; two blocks per compute unit).  The count
+    with the least time (the fewest on ties) is taken.  256 pairs or more: one segment;
+    80 or more: the split if it takes at most 0.8 of the one-segment walk (2 nc), else
+    one segment; fewer: the split if there is one, else the chunk-parallel route."""
     nc = (L + cs - 1) // cs
-    if B * H >= 80:
+    bh = B * H
+    if bh >= 256:
         return 1, nc
-    s = min(256 // (B * H), nc // 4)
-    if s < 2:
-        return 0, nc
-    seg_nc = (nc + s - 1) // s
-    return (nc + seg_nc - 1) // seg_nc, seg_nc
+    best, best_cost = None, None
+    for s in range(2, min(nc // 4, 4 * 256 // bh) + 1):
+        seg_nc = (nc + s - 1) // s
+        ns = (nc + seg_nc - 1) // seg_nc
+        if ns < 2:
+            continue
+        sub = max(1, min(4, seg_nc // 8))
+        cost = 2 * -(-bh * ns // 256) * seg_nc + -(-bh * (ns - 1) * sub // 512) * -(-seg_nc // sub)
+        if best_cost is None or cost < best_cost:
+            best, best_cost = (ns, seg_nc), cost
+    if bh >= 80:
+        return best if best is not None and 10 * best_cost <= 16 * nc else (1, nc)
+    return best if best is not None else (0, nc)
 
 
 def _split_ws(B, H, L, N, P, R):
     """The sequence split's carries (test_split_workspace_sizes): two sets per
     (b, h, segment) and one log-decay; 0 without a split."""
     al = lambda n: (n * 4 + 255) // 256 * 256  # noqa: E731
-    bh = B * H
-    if bh * 2 > 256 or L < 512 or N != 128 or P != 64:
+    nseg, _ = _fwd_segments(B, H, L)
+    if nseg < 2 or N != 128 or P != 64:
         return 0
-    s = min(256 // bh, L // 256)
-    if s < 2:
-        return 0
-    ln = ((L + s - 1) // s + 127) // 128 * 128
-    nseg = (L + ln - 1) // ln
-    if nseg < 2:
-        return 0
-    bhs = bh * nseg
+    bhs = B * H * nseg
     return 2 * (al(bhs * P * N) + al(bhs * N) + al(bhs * P) + al(bhs * max(R, 1))) + al(bhs)
 
 
@@ -177,6 +215,15 @@ def test_backward_workspace_sizes(lib, monkeypatch):
     # config 3's shape: 8 walk segments of 64 chunks (the adjoint pass in 32 sub-segments
     # of 16), 8 state-pass segments of 4096 tokens
     assert _walk_segments(1, 32, 32768, 64) == (8, 64)
+    # config 5's layer (96 pairs, 192 chunks): 8 segments of 24 chunks (three rounds of
+    # 256 blocks) instead of the one-segment walk on 96 compute units; 128 pairs at
+    # L=4096: two segments of 32 chunks; 160 pairs: the one-segment walk
+    assert _walk_segments(4, 24, 12288, 64) == (8, 24)
+    assert _walk_segments(4, 32, 4096, 64) == (2, 32)
+    assert _walk_segments(5, 32, 4096, 64) == (1, 64)
+    assert f(4, 12288, 24, 24, 128, 64, 32, 64, bf) == _bwd_ws_expect(4, 12288, 24, 24, 128, 64, 32, bf)
+    assert f(4, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(4, 4096, 32, 32, 128, 64, 32, bf)
+    assert f(5, 4096, 32, 32, 128, 64, 32, 64, bf) == _bwd_ws_expect(5, 4096, 32, 32, 128, 64, 32, bf)
     assert f(1, 32768, 32, 32, 128, 64, 32, 128, bf) == _bwd_ws_expect(1, 32768, 32, 32, 128, 64, 32, bf)
     assert f(1, 200, 2, 2, 128, 64, 32, 64, bf) == _bwd_ws_expect(1, 200, 2, 2, 128, 64, 32, bf)  # chunks
     assert f(1, 100, 2, 2, 64, 16, 16, 64, bf) == 0        # headdim 16: no backward kernel
