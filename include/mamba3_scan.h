@@ -120,14 +120,14 @@ int m3_chunk_scan_fwd_ws(const void* Q, const void* K, const void* V,
 
 /*
  * m3_chunk_scan_fwd_ws without the workspace argument: the split's scratch is a
- * device array of 17 MiB that the library holds for the life of the process, one
+ * device array of 67 MiB that the library holds for the life of the process, one
  * copy per GPU (its address is looked up on the first call with a stream of that
  * device, NULL meaning the current device; a failed lookup is reported and tried
  * again on the next call; make the first call on each device outside graph capture).  No
  * counterpart in the reference: this entry point is for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It allocates nothing and calls no allocating routine.  Shapes whose
- * split would need more than the 17 MiB (m3_chunk_scan_ws_bytes) are rejected with
+ * split would need more than the 67 MiB (m3_chunk_scan_ws_bytes) are rejected with
  * M3_E_ARG; shapes that run as one pass need no scratch.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller.  Nothing in the array needs

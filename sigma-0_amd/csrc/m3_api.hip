@@ -182,12 +182,13 @@ int m3_chunk_scan_fwd_shared(const void* Q, const void* K, const void* V,
 // ---- the allocation-free split prefill (m3_chunk_scan_fwd_noalloc)
 // The sequence split's carry workspace lives in a device array that the library
 // holds for the process, one copy per GPU, instead of memory from the caller.  Every
-// split shape needs at most 256 (batch, head, segment) carry slots (the split targets
-// one wave of 256 blocks), which at d_state 128, headdim 64 and R <= 64 is at most
-// 16.5 MB; the array holds 17 MiB.  Nothing in it needs to start at zero: the first
-// kernel of a split call writes every carry slot that the later ones read.
+// split shape needs at most 1024 (batch, head, segment) carry slots (the split
+// launches at most four rounds of 256 blocks), which at d_state 128, headdim 64 and
+// R <= 64 is at most 69,208,064 bytes; the array holds 67 MiB.  Nothing in it needs to
+// start at zero: the first kernel of a split call writes every carry slot that the
+// later ones read.
 namespace m3 {
-constexpr size_t kNoallocScratchBytes = size_t(17) << 20;
+constexpr size_t kNoallocScratchBytes = size_t(67) << 20;
 __device__ __align__(256) char scratch[kNoallocScratchBytes];
 }  // namespace m3
 

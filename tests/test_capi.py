@@ -111,6 +111,19 @@ def test_split_workspace_sizes(lib):
     assert _fwd_segments(2, 64, 8192) == (2, 4096)     # 128 pairs: one round of 256 blocks
 
 
+def test_split_workspace_fits_the_noalloc_scratch(lib):
+    """m3_chunk_scan_fwd_noalloc holds 67 MiB per GPU: every split shape fits (at most
+    four rounds of 256 blocks, 1024 carry slots, at d_state 128, headdim 64, R <= 64)."""
+    f = lib.m3_chunk_scan_ws_bytes
+    worst = 0
+    for H in (1, 2, 3, 5, 8, 16, 24, 32, 48, 64, 96, 128):
+        for L in (512, 1000, 2048, 4096, 12288, 32768, 100000, 1 << 20):
+            worst = max(worst, f(1, L, H, 128, 64, 64, 64, 1), f(1, L, H, 128, 64, 64, 64, 0))
+    assert 0 < worst <= 67 << 20
+    assert f(4, 2048, 24, 128, 64, 32, 64, 1) > 17 << 20        # the no-alloc GPU test's first shape
+    assert _fwd_segments(4, 24, 2048) == (8, 256)
+
+
 def _fwd_segments(B, H, L):
     """(segments, tokens per segment) of the forward's sequence split, or (0, 0).
     Segments are multiples of 128 tokens, at least 256, at most four rounds of 256

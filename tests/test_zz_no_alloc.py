@@ -29,7 +29,9 @@ def _call(lib, fn, t, out, init, fin, dims, CS, ws=None):
     assert rc == 0, lib.m3_last_error().decode()
 
 
-@pytest.mark.parametrize("B,L,H,with_init", [(1, 4096, 8, False), (1, 1100, 4, True)])
+# (4, 2048, 24): 96 pairs in 8 segments, three rounds of 256 blocks and 51 MB of the
+# scratch (the split's largest kind of need); the later shapes are smaller
+@pytest.mark.parametrize("B,L,H,with_init", [(4, 2048, 24, False), (1, 4096, 8, False), (1, 1100, 4, True)])
 def test_noalloc_equals_workspace_entry(B, L, H, with_init):
     import torch
     from mamba3_rocm import _lib
