@@ -18,6 +18,10 @@ that the float64 oracle finishes quickly).
   256 workgroups at once): two (batch, head) pairs against the float64 oracle, every
   gradient against the chunk-parallel route, and the training pair's backward equal to
   the recomputing one bitwise.
+* The backward at configuration 5's layer shape (B=4, L=12288, H=24: 96 pairs, the
+  split walk in 8 segments): two pairs against the float64 oracle, every gradient
+  against the one-segment walk (the bars of configuration 3's shape), and the
+  training pair's backward equal to the recomputing one bitwise.
 * Configuration 5, the 12-layer backbone at L=12288: batch row 0 against the oracle
   backbone's log-probabilities (a committed fixture, tests/golden/
   make_golden_config5.py: the oracle takes minutes at this size): 64 positions within
@@ -196,6 +200,62 @@ def test_backward_config2_full_size_walk(monkeypatch):
         assert not bad, f"pair {(b, h)}: gradients above {GRAD_TOL}: {bad}"
     bad = {k: v for k, v in e_alt.items() if v > GRAD_TOL}
     assert not bad, f"walk and chunk route differ: {bad}"
+
+
+@pytest.mark.timeout(300)
+def test_backward_config5_layer_shape_split_walk(monkeypatch):
+    """The backward at configuration 5's layer shape (B=4, L=12288, H=24: 96 pairs, so
+    the walk is split into 8 segments of 24 chunks, three rounds of 256 workgroups, and
+    its state pass into the forward's 8-segment split): pairs (b, h) = (0, 0) and
+    (3, 17) against autograd of the float64 oracle on their own problem; every
+    gradient of every pair against the one-segment walk; the training pair's backward
+    equal to the recomputing one bitwise."""
+    import torch
+    from mamba3_rocm import mamba3_siso_hip_bwd, mamba3_siso_hip_fwd_train
+    from oracle import mamba3_vjp as V
+    B, L, H, N, P, R, CS = 4, 12288, 24, 128, 64, 32, 64
+    print(f"[sizes] backward config 5 layer {(B, L, H, N, P, R, CS)} split walk", flush=True)
+    monkeypatch.delenv("M3_BWD_ROUTE", raising=False)
+    t = device_scan_inputs(B, L, H, N, P, R, seed=52, io_dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(53)
+    dout = torch.randn(B, L, H, P, device="cuda", generator=g).to(torch.bfloat16)
+    args = tuple(t[k] for k in V.NAMES)
+    got = mamba3_siso_hip_bwd(*args, dout, chunk_size=CS)
+    _, saved = mamba3_siso_hip_fwd_train(*args, chunk_size=CS)
+    from_saved = mamba3_siso_hip_bwd(*args, dout, chunk_size=CS, saved=saved)
+    monkeypatch.setenv("M3_BWD_ROUTE", "walk")
+    alt = mamba3_siso_hip_bwd(*args, dout, chunk_size=CS)
+    torch.cuda.synchronize()
+    for k, a, b in zip(V.NAMES, got, from_saved):
+        assert torch.equal(a, b), f"training pair differs from the recomputing backward in d{k}"
+    e_alt = {k: rel(a.float().cpu().numpy(), b.float().cpu().numpy()) for k, a, b in zip(V.NAMES, got, alt)}
+    print("  split vs one-segment walk: " + " ".join(f"{k}:{v:.1e}" for k, v in e_alt.items()), flush=True)
+    # the whole-sequence reverse cumsums dAngles and dADT lose precision with the length
+    # as at config 3's shape: 5e-2 for them, 2e-2 for the others
+    bar = lambda k: 5e-2 if k in ("Angles", "ADT") else GRAD_TOL  # noqa: E731
+    axes = {"Q": (0, 2), "K": (0, 2), "V": (0, 2), "Z": (0, 2), "Angles": (0, 2), "ADT": (0, 1), "DT": (0, 1),
+            "Trap": (0, 1), "Q_bias": (None, 0), "K_bias": (None, 0), "D": (None, 0)}
+    def pick(x, name, b, h):
+        ba, ha = axes[name]
+        x = x.narrow(ha, h, 1)
+        return x.narrow(ba, b, 1) if ba is not None else x
+    for b, h in ((0, 0), (3, 17)):
+        d = {k: pick(t[k], k, b, h).float().cpu().numpy() for k in V.NAMES}
+        cot = dout[b:b + 1, :, h:h + 1].float().cpu().numpy()
+        _, ref = V.vjp(d, cot, CS)
+        errs = {}
+        for name, a, r in zip(V.NAMES, got, ref):
+            if axes[name][0] is None:
+                continue
+            a = pick(a, name, b, h).float().cpu().numpy()
+            assert np.isfinite(a).all(), name
+            errs[name] = rel(a, r)
+        print(f"  pair {(b, h)} vs oracle: " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+        bad = {k: v for k, v in errs.items() if v > bar(k)}
+        assert not bad, f"pair {(b, h)}: gradients above their bar: {bad}"
+    bad = {k: v for k, v in e_alt.items() if v > bar(k)}
+    assert not bad, f"split and one-segment walk differ: {bad}"
 
 
 def _torch_params(p):
