@@ -31,7 +31,7 @@ launches of a process); the JSON line reports this as ``clock_settle``, apart fr
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-secondary]
-                       [--mode scan|decode|long|bwd|bwd3|bwd5|train|shared|shared_bwd|layer|stack|copy|fp32]
+                       [--mode scan|decode|long|bwd|bwd3|bwd5|train|shared|shared_bwd|layer|layer_train|stack|copy|fp32]
                        [--io bf16|f32]   (--mode bwd / train)
        python bench.py --mode traffic --pmc-dir DIR   (writes the traffic JSON of
                        the headline kernel from rocprofv3 --pmc FETCH_SIZE /
@@ -317,6 +317,28 @@ def bench_stack(torch, B, L, d_model, n_layers, vocab, steps, warmup, seed):
     return dict(wall_s=wall, kernel_s=kern, gemm_flops=gemm_flops)
 
 
+def bench_layer_train(torch, B, L, d_model, steps, warmup, seed):
+    """The mixer layer's training step at config 5's layer shape: train_forward and the
+    backward to x and every parameter (bf16 compute, float32 parameters), timed
+    together and the backward alone."""
+    from mamba3_rocm import Mamba3Layer
+    from mamba3_rocm.layer import init_params
+    params = {k: v.requires_grad_(True) for k, v in init_params(d_model, seed, "cuda").items()}
+    layer = Mamba3Layer(params, d_model, dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    x = torch.randn(B, L, d_model, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    dout = torch.randn(B, L, d_model, device="cuda", generator=g).to(torch.bfloat16)
+
+    def step():
+        for t in [x, *params.values()]:
+            t.grad = None
+        layer.train_forward(x).backward(dout)
+    wall, kern = time_calls(torch, step, steps, warmup)
+    fwd_wall, fwd_kern = time_calls(torch, lambda: layer(x), steps, warmup)
+    return dict(wall_s=wall, kernel_s=kern, fwd_s=fwd_kern)
+
+
 def bench_decode(torch, B, H, N, P, R, steps, warmup, seed):
     """Config 4: `steps` consecutive decode steps in place on a B=512 carry."""
     from mamba3_rocm import rnn_step_hip
@@ -548,7 +570,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "bwd3", "bwd5", "train", "shared", "shared_bwd",
-                                       "layer",
+                                       "layer", "layer_train",
                                        "stack", "copy", "fp32", "traffic"), default="scan")
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -615,6 +637,12 @@ def main():
         print(json.dumps({"mode": "layer", "ms": round(r["kernel_s"] * 1e3, 4),
                           "tokens_per_s": round(4 * 12288 / r["wall_s"], 1),
                           "gemm_tflop": round(r["gemm_flops"] / 1e12, 4)}), flush=True)
+        return
+    if args.mode == "layer_train":
+        r = bench_layer_train(torch, 4, 12288, 768, args.steps, args.warmup, seed=5)
+        print(json.dumps({"mode": "layer_train", "step_ms": round(r["kernel_s"] * 1e3, 4),
+                          "fwd_ms": round(r["fwd_s"] * 1e3, 4),
+                          "tokens_per_s": round(4 * 12288 / r["wall_s"], 1)}), flush=True)
         return
     if args.mode == "stack":
         r = bench_stack(torch, 4, 12288, 768, 12, 2112, args.steps, args.warmup, seed=5)

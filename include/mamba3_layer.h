@@ -63,6 +63,38 @@ int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
  */
 int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, int D, float eps, int io_dtype,
                   void* stream);
+/*
+ * The layer's backward, the gradients autodiff of _post_norm_and_project and
+ * _preprocess (mamba3.py:203-331) gives, in float32 arithmetic, deterministic
+ * (parameter gradients summed over the tokens in a fixed order through the
+ * workspace of the matching _ws_bytes call).  With the library GEMMs' gradients and
+ * m3_chunk_scan_bwd_shared of mamba3_scan.h between them, they give the gradients of
+ * x and every parameter of the layer.
+ *
+ * m3_layer_post's backward: from y (B, L, D) and d_out = dL/d(out) (B, L, D) in
+ * io_dtype and scale (D,), dy = dL/dy (B, L, D) in io_dtype and d_scale (D,)
+ * float32.  D a multiple of 8, at most 2048 (M3_E_UNSUPPORTED otherwise); y, d_out,
+ * dy and ws 16-byte aligned (M3_E_ALIGN otherwise).
+ */
+size_t m3_layer_post_bwd_ws_bytes(int B, int L, int D);
+int m3_layer_post_bwd(const void* y, const void* d_out, const float* scale, void* dy, float* d_scale, int B, int L,
+                      int D, float eps, int io_dtype, void* ws, size_t ws_bytes, void* stream);
+/*
+ * m3_layer_pre's backward: from proj and the parameters m3_layer_pre read, and the
+ * gradients of its outputs -- dQ and dK of the normalised C and B (B, L, N), dV and
+ * dZ (B, L, H, P), all in io_dtype (m3_chunk_scan_bwd_shared's dQ, dK, dV, dZ), and
+ * dADT, dDT, dTrap (B, H, L) and dAngles (B, L, R) float32 -- d_proj like proj (every
+ * column written: the gradient of the in_proj output) and d_dt_bias (H,),
+ * d_B_norm_scale, d_C_norm_scale (N,) float32.  The A_floor clip passes the gradient
+ * where -softplus(dd_A) is below -A_floor and half of it on a tie.  d_state at most
+ * 256 (M3_E_UNSUPPORTED otherwise).
+ */
+size_t m3_layer_pre_bwd_ws_bytes(int B, int L, int H, int N);
+int m3_layer_pre_bwd(const void* proj, const float* dt_bias, const float* B_norm_scale, const float* C_norm_scale,
+                     const void* dQ, const void* dK, const void* dV, const void* dZ, const float* dADT,
+                     const float* dDT, const float* dTrap, const float* dAngles, void* d_proj, float* d_dt_bias,
+                     float* d_B_norm_scale, float* d_C_norm_scale, int B, int L, int H, int P, int N, int R,
+                     float A_floor, float eps, int io_dtype, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * The backbone block around the mixer: SequenceLayer.__call__

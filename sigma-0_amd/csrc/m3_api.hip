@@ -53,7 +53,7 @@ bool decode_supported(int N, int P, int R) {
 
 extern "C" {
 
-int m3_abi_version(void) { return 101; }
+int m3_abi_version(void) { return 102; }
 
 const char* m3_last_error(void) { return g_err; }
 
@@ -568,6 +568,70 @@ int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, in
   a.y = y; a.scale = scale; a.out = out; a.B = B; a.L = L; a.D = D; a.eps = eps;
   return check_launch(m3::layer_post_launch(a, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
                       "layer post");
+}
+
+size_t m3_layer_post_bwd_ws_bytes(int B, int L, int D) {
+  if (B <= 0 || L <= 0 || D <= 0) return 0;
+  return (size_t)m3::layer_post_bwd_parts(B, L) * D * sizeof(float);
+}
+
+int m3_layer_post_bwd(const void* y, const void* d_out, const float* scale, void* dy, float* d_scale, int B, int L,
+                      int D, float eps, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (D % 8 != 0 || D > m3::kLayerPostBwdMaxD)
+    return fail(M3_E_UNSUPPORTED, "D=%d: the backward takes multiples of 8 up to %d", D, m3::kLayerPostBwdMaxD);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!y || !d_out || !scale || !dy || !d_scale || !ws) return fail(M3_E_ARG, "NULL required pointer");
+  if (ws_bytes < m3_layer_post_bwd_ws_bytes(B, L, D))
+    return fail(M3_E_ARG, "workspace of %zu bytes, %zu needed", ws_bytes, m3_layer_post_bwd_ws_bytes(B, L, D));
+  const size_t es = io_dtype == M3_DTYPE_BF16 ? 2 : 4;
+  if ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(d_out) | reinterpret_cast<uintptr_t>(dy) |
+       reinterpret_cast<uintptr_t>(ws)) % 16 != 0 || (D * es) % 16 != 0)
+    return fail(M3_E_ALIGN, "y, d_out, dy and ws must be 16-byte aligned");
+  m3::LayerPostBwdArgs a;
+  a.y = y; a.dn = d_out; a.scale = scale; a.dy = dy; a.part = reinterpret_cast<float*>(ws);
+  a.B = B; a.L = L; a.D = D; a.eps = eps;
+  return check_launch(m3::layer_post_bwd_launch(a, d_scale, io_dtype == M3_DTYPE_BF16,
+                                                reinterpret_cast<hipStream_t>(stream)), "layer post backward");
+}
+
+size_t m3_layer_pre_bwd_ws_bytes(int B, int L, int H, int N) {
+  if (B <= 0 || L <= 0 || H <= 0 || N <= 0) return 0;
+  return (size_t)m3::layer_pre_bwd_parts(B, L) * (2 * N + H) * sizeof(float);
+}
+
+int m3_layer_pre_bwd(const void* proj, const float* dt_bias, const float* B_norm_scale, const float* C_norm_scale,
+                     const void* dQ, const void* dK, const void* dV, const void* dZ, const float* dADT,
+                     const float* dDT, const float* dTrap, const float* dAngles, void* d_proj, float* d_dt_bias,
+                     float* d_B_norm_scale, float* d_C_norm_scale, int B, int L, int H, int P, int N, int R,
+                     float A_floor, float eps, int io_dtype, void* ws, size_t ws_bytes, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || H <= 0 || P <= 0 || N <= 0 || R < 0)
+    return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d H=%d P=%d N=%d R=%d)", B, L, H, P, N, R);
+  if (N > m3::kLayerPreBwdMaxN) return fail(M3_E_UNSUPPORTED, "d_state %d above the backward's %d", N, m3::kLayerPreBwdMaxN);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!proj || !dt_bias || !B_norm_scale || !C_norm_scale || !dQ || !dK || !dV || !dZ || !dADT || !dDT || !dTrap ||
+      (R > 0 && !dAngles) || !d_proj || !d_dt_bias || !d_B_norm_scale || !d_C_norm_scale || !ws)
+    return fail(M3_E_ARG, "NULL required pointer");
+  if (ws_bytes < m3_layer_pre_bwd_ws_bytes(B, L, H, N))
+    return fail(M3_E_ARG, "workspace of %zu bytes, %zu needed", ws_bytes, m3_layer_pre_bwd_ws_bytes(B, L, H, N));
+  m3::LayerPreBwdArgs a;
+  a.proj = proj; a.dt_bias = dt_bias; a.b_scale = B_norm_scale; a.c_scale = C_norm_scale;
+  a.dq = dQ; a.dk = dK; a.dv = dV; a.dz = dZ; a.dadt = dADT; a.ddt = dDT; a.dtrap = dTrap; a.dang = dAngles;
+  a.dproj = d_proj; a.part = reinterpret_cast<float*>(ws);
+  a.B = B; a.L = L; a.H = H; a.P = P; a.N = N; a.R = R; a.A_floor = A_floor; a.eps = eps;
+  return check_launch(m3::layer_pre_bwd_launch(a, d_B_norm_scale, d_C_norm_scale, d_dt_bias,
+                                               io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "layer pre backward");
 }
 
 int m3_block_norm(const float* x, const float* scale, const float* bias, void* out, int B, int L, int D, float eps,

@@ -1,0 +1,287 @@
+// Backward of the mixer layer's elementwise kernels (m3_layer.hip), as autodiff of
+// Mamba3SSM._preprocess and _post_norm_and_project (src/base_model/models/
+// mamba3.py:203-331) gives it, with float32 arithmetic:
+//   layer_post_bwd_kernel  the output RMSNorm n = y r scale, r = rsqrt(mean(y^2) + eps):
+//                          dy = r (dn scale) - r^3 y mean(dn scale y), one wave per run of
+//                          kPostTok tokens; the scale's gradient sum_t dn y r as one
+//                          partial row per wave
+//   layer_pre_bwd_kernel   d(proj) from the scan's gradients, one workgroup per tile of
+//                          kPreTile tokens of one batch row: dZ and dV into the z and x
+//                          columns, BCNorm's backward into B and C (one wave per token),
+//                          the decay's chain rule into dd_dt and dd_A and dTrap into trap
+//                          (lanes along the tokens, one head per wave at a time), dAngles
+//                          into the angle columns; the norm scales' and dt_bias's gradients
+//                          as one partial row per workgroup
+//   reduce_slices_kernel,  the partial rows summed in a fixed order (the gradients are
+//   reduce_final_kernel    deterministic): kReduceSlices slices of rows side by side,
+//                          then the slices' sums
+// Each is one read of its inputs and one write of its outputs: HBM-bound.
+#include "m3_scan.h"
+
+namespace m3 {
+namespace {
+
+constexpr int kBwdElThreads = 256;
+constexpr int kPostTok = 32;            // tokens per wave, layer_post_bwd
+constexpr int kPreTile = 64;            // tokens per workgroup, layer_pre_bwd (one per lane)
+constexpr int kPostChunks = kLayerPostBwdMaxD / (64 * 8);   // 8-element chunks per lane
+constexpr int kPreCols = kLayerPreBwdMaxN / 64;             // B / C columns per lane
+constexpr int kReduceSlices = 16;                           // row slices of the partial sums
+
+__device__ __forceinline__ float softplus_f(float x) {     // as layer_pre: logaddexp(x, 0)
+  return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+
+template <typename T>
+__device__ __forceinline__ void copy_row(T* dst, const T* src, int n, int lane) {
+  constexpr int V = 16 / sizeof(T);
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && n % V == 0) {
+    for (int i = lane; i < n / V; i += 64) reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+  } else {
+    for (int i = lane; i < n; i += 64) dst[i] = src[i];
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBwdElThreads)
+void layer_post_bwd_kernel(LayerPostBwdArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long run = (long)blockIdx.x * (kBwdElThreads / 64) + wave;
+  const long rows = (long)a.B * a.L, t0 = run * kPostTok;
+  if (t0 >= rows) return;                             // whole waves only: no barrier below
+  const int D = a.D, nch = D / 8;
+  const float invD = 1.0f / (float)D;
+  float sc[kPostChunks][8], acc[kPostChunks][8];
+#pragma unroll
+  for (int j = 0; j < kPostChunks; ++j) {
+    const int c = lane + 64 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sc[j][e] = c < nch ? a.scale[8 * c + e] : 0.0f;
+      acc[j][e] = 0.0f;
+    }
+  }
+  const long t1 = t0 + kPostTok < rows ? t0 + kPostTok : rows;
+  for (long t = t0; t < t1; ++t) {
+    const T* yr = reinterpret_cast<const T*>(a.y) + t * D;
+    const T* dr = reinterpret_cast<const T*>(a.dn) + t * D;
+    float yv[kPostChunks][8], dv[kPostChunks][8];
+    float ss = 0.0f, sd = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPostChunks; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nch) {
+        Vec8<T> v;
+        v.load(yr + 8 * c);
+        v.to_f(yv[j]);
+        v.load(dr + 8 * c);
+        v.to_f(dv[j]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ss += yv[j][e] * yv[j][e];
+          sd += dv[j][e] * sc[j][e] * yv[j][e];
+        }
+      }
+    }
+    ss = group_sum<64>(ss);
+    sd = group_sum<64>(sd);
+    const float r = rsqrtf(ss * invD + a.eps);
+    const float k = r * r * r * (sd * invD);
+    T* out = reinterpret_cast<T*>(a.dy) + t * D;
+#pragma unroll
+    for (int j = 0; j < kPostChunks; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nch) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          o[e] = r * (dv[j][e] * sc[j][e]) - k * yv[j][e];
+          acc[j][e] += dv[j][e] * yv[j][e] * r;
+        }
+        store8(out + 8 * c, o);
+      }
+    }
+  }
+  float* part = a.part + run * D;
+#pragma unroll
+  for (int j = 0; j < kPostChunks; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) store8(part + 8 * c, acc[j]);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBwdElThreads)
+void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
+  __shared__ float red[kBwdElThreads / 64][2][kLayerPreBwdMaxN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tiles = (a.L + kPreTile - 1) / kPreTile;
+  const int b = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * kPreTile;
+  const int nt = a.L - t0 < kPreTile ? a.L - t0 : kPreTile;
+  const int H = a.H, N = a.N, R = a.R, di = H * a.P;
+  const int dp = 2 * di + 2 * N + 3 * H + R;
+  const int oB = 2 * di, oC = oB + N, oT = oC + N;      // dd_dt at oT, dd_A at oT + H, trap at oT + 2H,
+  const long row0 = (long)b * a.L + t0;                  // angles at oT + 3H
+  const T* proj = reinterpret_cast<const T*>(a.proj) + row0 * dp;
+  T* dproj = reinterpret_cast<T*>(a.dproj) + row0 * dp;
+  const int nparts = 2 * N + H;
+  float* part = a.part + (long)blockIdx.x * nparts;
+
+  // ---- one wave per token: dZ, dV into the z and x columns; BCNorm's backward
+  float accB[kPreCols], accC[kPreCols];
+#pragma unroll
+  for (int k = 0; k < kPreCols; ++k) accB[k] = accC[k] = 0.0f;
+  const float invN = 1.0f / (float)N;
+  for (int i = wave; i < nt; i += kBwdElThreads / 64) {
+    const long row = row0 + i;
+    T* dpr = dproj + (long)i * dp;
+    const T* pr = proj + (long)i * dp;
+    copy_row(dpr, reinterpret_cast<const T*>(a.dz) + row * di, di, lane);
+    copy_row(dpr + di, reinterpret_cast<const T*>(a.dv) + row * di, di, lane);
+    // n = m rsqrt(mean m^2 + eps) scale  (B: K's, C: Q's)
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      const T* g = reinterpret_cast<const T*>(side ? a.dq : a.dk) + row * N;
+      const float* scale = side ? a.c_scale : a.b_scale;
+      const int o = side ? oC : oB;
+      float m[kPreCols], ds[kPreCols], ss = 0.0f, sd = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kPreCols; ++k) {
+        const int n = lane + 64 * k;
+        m[k] = n < N ? Elem<T>::to_f(pr[o + n]) : 0.0f;
+        const float dn = n < N ? Elem<T>::to_f(g[n]) : 0.0f;
+        ds[k] = n < N ? dn * scale[n] : 0.0f;
+        ss += m[k] * m[k];
+        sd += ds[k] * m[k];
+      }
+      ss = group_sum<64>(ss);
+      sd = group_sum<64>(sd);
+      const float r = rsqrtf(ss * invN + a.eps);
+      const float kk = r * r * r * (sd * invN);
+#pragma unroll
+      for (int k = 0; k < kPreCols; ++k) {
+        const int n = lane + 64 * k;
+        if (n < N) {
+          dpr[o + n] = Elem<T>::from_f(r * ds[k] - kk * m[k]);
+          // the scale's gradient: dn m r
+          const float gs = Elem<T>::to_f(g[n]) * m[k] * r;
+          if (side) accC[k] += gs;
+          else accB[k] += gs;
+        }
+      }
+    }
+  }
+  // ---- lanes along the tokens, one head per wave at a time: DT = softplus(dd_dt +
+  // dt_bias), A = min(-softplus(dd_A), -A_floor), ADT = A DT; trap passes through
+  for (int h = wave; h < H; h += kBwdElThreads / 64) {
+    float du = 0.0f;
+    if (lane < nt) {
+      const long hl = ((long)b * H + h) * a.L + t0 + lane;
+      const float dadt = a.dadt[hl], ddt = a.ddt[hl], dtrap = a.dtrap[hl];
+      const T* pr = proj + (long)lane * dp;
+      const float u = Elem<T>::to_f(pr[oT + h]) + a.dt_bias[h];
+      const float ddA = Elem<T>::to_f(pr[oT + H + h]);
+      const float DTv = softplus_f(u), sp = softplus_f(ddA);
+      const float A = fminf(-sp, -a.A_floor);
+      du = (ddt + dadt * A) * (1.0f / (1.0f + expf(-u)));
+      // the clip passes the gradient below -A_floor, half of it on a tie (jax's min)
+      const float gate = -sp < -a.A_floor ? 1.0f : (-sp == -a.A_floor ? 0.5f : 0.0f);
+      const float dA = -(dadt * DTv) * gate * (1.0f / (1.0f + expf(-ddA)));
+      T* dpr = dproj + (long)lane * dp;
+      dpr[oT + h] = Elem<T>::from_f(du);
+      dpr[oT + H + h] = Elem<T>::from_f(dA);
+      dpr[oT + 2 * H + h] = Elem<T>::from_f(dtrap);
+    }
+    du = group_sum<64>(du);
+    if (lane == 0) part[2 * N + h] = du;
+  }
+  // ---- the angle rates' gradients into their columns
+  for (int e = tid; e < nt * R; e += kBwdElThreads) {
+    const int i = e / R, r = e % R;
+    dproj[(long)i * dp + oT + 3 * H + r] = Elem<T>::from_f(a.dang[(row0 + i) * R + r]);
+  }
+  // ---- the norm scales' partial sums over the tile: the four waves' rows added in order
+#pragma unroll
+  for (int k = 0; k < kPreCols; ++k) {
+    const int n = lane + 64 * k;
+    if (n < N) {
+      red[wave][0][n] = accB[k];
+      red[wave][1][n] = accC[k];
+    }
+  }
+  __syncthreads();
+  for (int n = tid; n < 2 * N; n += kBwdElThreads) {
+    const int side = n / N, c = n % N;
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kBwdElThreads / 64; ++w) s += red[w][side][c];
+    part[n] = s;
+  }
+}
+
+// mid[y][c] = sum of part[r][c] over slice y of the rows (kReduceSlices slices): 64
+// columns per workgroup, four row phases per column, added in a fixed order.
+__global__ __launch_bounds__(kBwdElThreads)
+void reduce_slices_kernel(const float* part, long rows, int cols, float* mid) {
+  __shared__ float red[4][64];
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63), g = threadIdx.x >> 6;
+  const long r0 = rows * blockIdx.y / kReduceSlices, r1 = rows * (blockIdx.y + 1) / kReduceSlices;
+  float s = 0.0f;
+  if (c < cols)
+    for (long r = r0 + g; r < r1; r += 4) s += part[r * cols + c];
+  red[g][threadIdx.x & 63] = s;
+  __syncthreads();
+  if (g == 0 && c < cols) mid[(long)blockIdx.y * cols + c] = red[0][threadIdx.x] + red[1][threadIdx.x] +
+                                                             red[2][threadIdx.x] + red[3][threadIdx.x];
+}
+// out[c] = sum of mid[y][c] over the slices in order; column c goes to out0 (c < n0),
+// out1 (c < n0 + n1) or out2.
+__global__ __launch_bounds__(kBwdElThreads)
+void reduce_final_kernel(const float* mid, int cols, float* out0, int n0, float* out1, int n1, float* out2) {
+  const int c = blockIdx.x * kBwdElThreads + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.0f;
+  for (int y = 0; y < kReduceSlices; ++y) s += mid[(long)y * cols + c];
+  if (c < n0) out0[c] = s;
+  else if (c < n0 + n1) out1[c - n0] = s;
+  else out2[c - n0 - n1] = s;
+}
+
+hipError_t reduce_rows(const float* part, long rows, int cols, float* mid, float* out0, int n0, float* out1, int n1,
+                       float* out2, hipStream_t st) {
+  hipLaunchKernelGGL(reduce_slices_kernel, dim3((cols + 63) / 64, kReduceSlices), dim3(kBwdElThreads), 0, st, part,
+                     rows, cols, mid);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(reduce_final_kernel, dim3((cols + kBwdElThreads - 1) / kBwdElThreads), dim3(kBwdElThreads), 0,
+                     st, mid, cols, out0, n0, out1, n1, out2);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+long layer_post_bwd_parts(int B, int L) { return ((long)B * L + kPostTok - 1) / kPostTok + kReduceSlices; }
+long layer_pre_bwd_parts(int B, int L) { return (long)B * ((L + kPreTile - 1) / kPreTile) + kReduceSlices; }
+
+hipError_t layer_post_bwd_launch(const LayerPostBwdArgs& a, float* dscale, bool bf16_io, hipStream_t st) {
+  const long runs = layer_post_bwd_parts(a.B, a.L) - kReduceSlices;   // the rest of the rows: the slices' sums
+  const dim3 grid((unsigned)((runs + kBwdElThreads / 64 - 1) / (kBwdElThreads / 64)));
+  if (bf16_io) hipLaunchKernelGGL(layer_post_bwd_kernel<bf16>, grid, dim3(kBwdElThreads), 0, st, a);
+  else hipLaunchKernelGGL(layer_post_bwd_kernel<float>, grid, dim3(kBwdElThreads), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return reduce_rows(a.part, runs, a.D, a.part + runs * a.D, dscale, a.D, nullptr, 0, nullptr, st);
+}
+
+hipError_t layer_pre_bwd_launch(const LayerPreBwdArgs& a, float* d_b_scale, float* d_c_scale, float* d_dt_bias,
+                                bool bf16_io, hipStream_t st) {
+  const long blocks = layer_pre_bwd_parts(a.B, a.L) - kReduceSlices;
+  if (bf16_io) hipLaunchKernelGGL(layer_pre_bwd_kernel<bf16>, dim3((unsigned)blocks), dim3(kBwdElThreads), 0, st, a);
+  else hipLaunchKernelGGL(layer_pre_bwd_kernel<float>, dim3((unsigned)blocks), dim3(kBwdElThreads), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int cols = 2 * a.N + a.H;
+  return reduce_rows(a.part, blocks, cols, a.part + blocks * cols, d_b_scale, a.N, d_c_scale, a.N, d_dt_bias, st);
+}
+
+}  // namespace m3

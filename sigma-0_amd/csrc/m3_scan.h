@@ -120,6 +120,36 @@ hipError_t layer_pre_launch(LayerPreArgs a, bool bf16_io, hipStream_t st);
 size_t layer_pre_lds_bytes(int tile, int seg, int N, size_t es);
 hipError_t layer_post_launch(const LayerPostArgs& a, bool bf16_io, hipStream_t st);
 
+// The layer's elementwise backward (m3_layer_bwd.hip).  Partial rows of the parameter
+// gradients go to `part` (float32, layer_*_bwd_parts rows: the kernels' partial rows,
+// then those of the slice sums), then are summed in order.
+constexpr int kLayerPostBwdMaxD = 2048;    // layer_post_bwd: D a multiple of 8, at most this
+constexpr int kLayerPreBwdMaxN = 256;      // layer_pre_bwd: d_state at most this
+struct LayerPostBwdArgs {
+  const void* y; const void* dn; const float* scale;   // (B, L, D) io, (B, L, D) io, (D,)
+  void* dy;                                             // (B, L, D) io
+  float* part;                                          // (parts, D)
+  int B, L, D;
+  float eps;
+};
+struct LayerPreBwdArgs {
+  const void* proj;                                     // (B, L, 2HP + 2N + 3H + R) io
+  const float* dt_bias; const float* b_scale; const float* c_scale;
+  const void* dq; const void* dk;                       // d(normalised C), d(normalised B): (B, L, N) io
+  const void* dv; const void* dz;                       // (B, L, H, P) io
+  const float* dadt; const float* ddt; const float* dtrap;   // (B, H, L)
+  const float* dang;                                    // (B, L, R)
+  void* dproj;                                          // like proj
+  float* part;                                          // (parts, 2N + H)
+  int B, L, H, P, N, R;
+  float A_floor, eps;
+};
+long layer_post_bwd_parts(int B, int L);
+long layer_pre_bwd_parts(int B, int L);
+hipError_t layer_post_bwd_launch(const LayerPostBwdArgs& a, float* dscale, bool bf16_io, hipStream_t st);
+hipError_t layer_pre_bwd_launch(const LayerPreBwdArgs& a, float* d_b_scale, float* d_c_scale, float* d_dt_bias,
+                                bool bf16_io, hipStream_t st);
+
 // The backbone block's norm and elementwise kernels (m3_block.hip).  `vec` is set by
 // the launchers (16-byte paths).
 struct BlockNormArgs {

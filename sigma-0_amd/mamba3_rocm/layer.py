@@ -11,6 +11,13 @@ heads).
 Where the projection rows are not a multiple of 16 bytes, m3_layer_pre also copies
 x and z out of proj and the scan is m3_chunk_scan_fwd_shared on the copies.
 
+``Mamba3Layer.train_forward`` is the same forward made differentiable (gradients for
+x and for every parameter, as autodiff of Mamba3SSM gives them): its backward is the
+library GEMMs' gradients, m3_layer_post_bwd (the output RMSNorm), the shared scan's
+backward (m3_chunk_scan_bwd_shared) and m3_layer_pre_bwd (BCNorm, the decay's chain
+rule with the A_floor clip, trap and angles, written into the in_proj output's
+gradient).
+
 Parameters keep the reference's names and layouts (flax Dense kernels are
 (in, out)) and stay float32; ``dtype`` is the compute dtype of the projections
 and the scan's operands (the reference's ``dtype`` field, mamba3.py:103-110).
@@ -23,7 +30,8 @@ from typing import Dict
 import torch
 
 from . import _lib
-from .ops import _IO, _ptr, _stream, mamba3_ssd_chunked_shared_hip, pallas_compute_dtype
+from .ops import (_IO, _ptr, _stream, mamba3_ssd_chunked_shared_hip, mamba3_ssd_chunked_shared_hip_bwd,
+                  pallas_compute_dtype)
 
 PARAM_NAMES = ("in_proj", "dt_bias", "B_bias", "C_bias", "B_norm", "C_norm", "D", "out_norm", "out_proj")
 
@@ -64,13 +72,25 @@ class Mamba3Layer:
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """x (B, L, d_model) or (L, d_model) -> the same shape, in the compute dtype."""
+        return self._run(x, self.w_in, self.w_out)[0]
+
+    def train_forward(self, x: torch.Tensor) -> torch.Tensor:
+        """forward, differentiable: gradients flow to x and to the parameter tensors the
+        layer was built with (``self.params``, float32; those with requires_grad get
+        theirs).  The compute-dtype copies of the projection kernels are taken from the
+        parameters at every call, so updates in place are seen."""
+        return _LayerTrain.apply(self, x, *(self.params[k] for k in PARAM_NAMES))
+
+    def _run(self, x: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor, keep: bool = False):
+        """The forward; with ``keep`` also the intermediates the backward reads."""
         unbatched = x.dim() == 2
         if unbatched:
             x = x[None]
         B, L, _ = x.shape
         dt, dev = self.dtype, x.device
         nh, hd, N, R = self.nh, self.hd, self.N, self.R
-        proj = torch.matmul(x.to(dt), self.w_in).contiguous()         # (B, L, d_in_proj)
+        xin = x.to(dt)
+        proj = torch.matmul(xin, w_in).contiguous()                  # (B, L, d_in_proj)
         Q = torch.empty(B, L, N, device=dev, dtype=dt)
         K = torch.empty_like(Q)
         f32 = dict(device=dev, dtype=torch.float32)
@@ -117,10 +137,85 @@ class Mamba3Layer:
         yn = torch.empty(B, L, self.d_inner, device=dev, dtype=dt)
         _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), B, L, self.d_inner, self.eps, io,
                                      _stream(y)), "m3_layer_post")
-        out = torch.matmul(yn, self.w_out)
-        return out[0] if unbatched else out
+        out = torch.matmul(yn, w_out)
+        saved = (dict(xin=xin, proj=proj, Q=Q, K=K, ADT=ADT, DT=DT, Trap=Trap, Ang=Ang, y=y, yn=yn, cdt=cdt)
+                 if keep else None)
+        return (out[0] if unbatched else out), saved
+
+    def _backward(self, saved, dout: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor):
+        """Gradients of x and of the parameters (PARAM_NAMES order, float32) from the
+        output cotangent, as autodiff of Mamba3SSM.__call__ (mamba3.py:191-331) gives
+        them: the GEMMs' gradients (library GEMMs in the compute dtype, as the
+        reference's bf16 layer differentiates its bf16 dots), m3_layer_post_bwd, the
+        shared scan's backward and m3_layer_pre_bwd; the roundings of the compute
+        dtype pass gradients through unchanged."""
+        xin, proj, y, yn = saved["xin"], saved["proj"], saved["y"], saved["yn"]
+        B, L, _ = xin.shape
+        dt, dev = self.dtype, xin.device
+        nh, hd, N, R, di, eps = self.nh, self.hd, self.N, self.R, self.d_inner, self.eps
+        pp = self.params
+        lib = _lib.load()
+        io = _IO[dt]
+        f32 = dict(device=dev, dtype=torch.float32)
+        d_out = dout.reshape(B, L, self.d_model).to(dt).contiguous()
+        # out = (y rsqrt(mean y^2 + eps) out_norm) @ out_proj  (_post_norm_and_project, :281-331)
+        g_out_proj = (yn.reshape(-1, di).t() @ d_out.reshape(-1, self.d_model)).float()
+        d_yn = torch.matmul(d_out, w_out.t()).contiguous()
+        d_y = torch.empty_like(d_yn)
+        g_out_norm = torch.empty(di, **f32)
+        ws = torch.empty(max(lib.m3_layer_post_bwd_ws_bytes(B, L, di), 16), dtype=torch.uint8, device=dev)
+        _lib.check(lib.m3_layer_post_bwd(_ptr(y), _ptr(d_yn), _ptr(pp["out_norm"]), _ptr(d_y), _ptr(g_out_norm), B, L,
+                                         di, eps, io, ws.data_ptr(), ws.numel(), _stream(y)), "m3_layer_post_bwd")
+        # the scan (Q = C, K = B shared over heads; x and z from proj)
+        Vv = proj[..., di:2 * di].reshape(B, L, nh, hd).contiguous()
+        Zv = proj[..., :di].reshape(B, L, nh, hd).contiguous()
+        g = mamba3_ssd_chunked_shared_hip_bwd(saved["Q"], saved["K"], Vv, saved["ADT"], saved["DT"], saved["Trap"],
+                                              saved["Ang"], pp["C_bias"], pp["B_bias"], pp["D"], Zv,
+                                              d_y.reshape(B, L, nh, hd), chunk_size=self.chunk_size,
+                                              compute_dtype=saved["cdt"])
+        dC, dB, dV, dADT, dDT, dTrap, dAng, g_C_bias, g_B_bias, g_D, dZ = g
+        # _preprocess (:203-268): BCNorm, the decay, trap and angles back to the in_proj output
+        d_proj = torch.empty_like(proj)
+        g_dt_bias, g_B_norm, g_C_norm = torch.empty(nh, **f32), torch.empty(N, **f32), torch.empty(N, **f32)
+        ws = torch.empty(max(lib.m3_layer_pre_bwd_ws_bytes(B, L, nh, N), 16), dtype=torch.uint8, device=dev)
+        c = lambda t: t.to(dt).contiguous()  # noqa: E731
+        dC, dB, dV, dZ = c(dC), c(dB), c(dV), c(dZ)
+        _lib.check(lib.m3_layer_pre_bwd(_ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]),
+                                        _ptr(dC), _ptr(dB), _ptr(dV), _ptr(dZ), _ptr(dADT), _ptr(dDT), _ptr(dTrap),
+                                        _ptr(dAng), _ptr(d_proj), _ptr(g_dt_bias), _ptr(g_B_norm), _ptr(g_C_norm),
+                                        B, L, nh, hd, N, R, self.A_floor, eps, io, ws.data_ptr(), ws.numel(),
+                                        _stream(proj)), "m3_layer_pre_bwd")
+        g_in_proj = (xin.reshape(-1, self.d_model).t() @ d_proj.reshape(-1, self.d_in_proj)).float()
+        dx = torch.matmul(d_proj, w_in.t())
+        grads = dict(in_proj=g_in_proj, dt_bias=g_dt_bias, B_bias=g_B_bias, C_bias=g_C_bias, B_norm=g_B_norm,
+                     C_norm=g_C_norm, D=g_D, out_norm=g_out_norm, out_proj=g_out_proj)
+        return dx, [grads[k] for k in PARAM_NAMES]
 
     __call__ = forward
+
+
+class _LayerTrain(torch.autograd.Function):
+    """Mamba3Layer.train_forward: x and the layer's float32 parameters in, the layer's
+    output out; the backward returns the gradient of x (in x's dtype) and of each
+    parameter (float32)."""
+
+    @staticmethod
+    def forward(ctx, layer, x, *params):
+        w_in = params[PARAM_NAMES.index("in_proj")].to(layer.dtype).contiguous()
+        w_out = params[PARAM_NAMES.index("out_proj")].to(layer.dtype).contiguous()
+        unbatched = x.dim() == 2
+        out, saved = layer._run(x, w_in, w_out, keep=True)
+        ctx.layer, ctx.saved, ctx.w = layer, saved, (w_in, w_out)
+        ctx.unbatched, ctx.x_dtype = unbatched, x.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        layer = ctx.layer
+        dx, dparams = layer._backward(ctx.saved, dout, *ctx.w)
+        ctx.saved = None
+        dx = dx.to(ctx.x_dtype)
+        return (None, dx[0] if ctx.unbatched else dx, *dparams)
 
 
 def init_params(d_model: int, seed: int, device, d_state: int = 128, expand: int = 2, headdim: int = 64,

@@ -1,0 +1,103 @@
+"""The mixer layer's backward (Mamba3Layer.train_forward).
+
+* float32 compute against central finite differences of the float64 layer oracle
+  (oracle/mamba3_layer.py): for a fixed output cotangent g, f(theta) =
+  sum(g * layer(theta)); for each input (x and every parameter) a random direction u
+  of its shape, and the directional derivative <grad, u> from the backward against
+  (f(theta + e u) - f(theta - e u)) / 2e.  A mistake in any one gradient fails its
+  own direction.  Bar 1e-3: the float64 difference quotient is exact to about 1e-8,
+  the float32 scan's gradients are within 2e-5 of the oracle's, and the layer's norms
+  add a few multiples of that.
+* bf16 compute against the float32 backward of the same layer (same parameters and
+  input), every gradient within the reference's bf16 gradient bar of 1e-1
+  (tests/integration/test_mamba3_pallas_gpu.py:66-69), relative in norm.  A
+  difference quotient of the bf16 layer itself would measure its rounding steps.
+"""
+import numpy as np
+import pytest
+
+from _util import rel
+from oracle import mamba3_layer as ML
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("in_proj", "dt_bias", "B_bias", "C_bias", "B_norm", "C_norm", "D", "out_norm", "out_proj")
+
+
+def _grads(p, x, g, d_model, N, headdim, dtype, path):
+    """Output and gradients (x first, then NAMES) of train_forward, as float64 numpy."""
+    import torch
+    from mamba3_rocm import Mamba3Layer
+    params = {k: torch.from_numpy(v).cuda().requires_grad_(True) for k, v in p.items()}
+    layer = Mamba3Layer(params, d_model, d_state=N, headdim=headdim, dtype=dtype)
+    for k in NAMES:
+        assert layer.params[k] is params[k], "the layer keeps the caller's float32 parameters"
+    xt = torch.from_numpy(x).cuda().requires_grad_(True)
+    out = layer.train_forward(xt)
+    assert layer.last_scan == path
+    (out.float() * torch.from_numpy(g).float().cuda()).sum().backward()
+    torch.cuda.synchronize()
+    # the differentiable forward is the layer's forward
+    assert torch.equal(out, layer(torch.from_numpy(x).cuda()))
+    grads = {"x": xt.grad.float().cpu().numpy().astype(np.float64)}
+    for k in NAMES:
+        assert params[k].grad is not None and params[k].grad.dtype == torch.float32, k
+        grads[k] = params[k].grad.cpu().numpy().astype(np.float64)
+        assert np.isfinite(grads[k]).all(), k
+    assert np.isfinite(grads["x"]).all()
+    return grads
+
+
+def _setup(B, L, d_model, N, headdim):
+    p = ML.init_params(d_model, seed=61, d_state=N, headdim=headdim)
+    rng = np.random.default_rng(62)
+    x = rng.standard_normal((B, L, d_model)).astype(np.float32)
+    g = rng.standard_normal((B, L, d_model))
+    return p, x, g
+
+
+@pytest.mark.parametrize("B,L,d_model,N,headdim,path", [
+    (2, 150, 64, 64, 32, "in_place"),      # the chunked float32 kernels at d_state 64
+    (2, 200, 128, 128, 64, "in_place"),    # the model's geometry per head (812-wide float32 rows)
+])
+def test_layer_backward_f32_matches_finite_differences(B, L, d_model, N, headdim, path):
+    import torch
+    p, x, g = _setup(B, L, d_model, N, headdim)
+    grads = _grads(p, x, g, d_model, N, headdim, torch.float32, path)
+    errs = {}
+    for i, name in enumerate(("x",) + NAMES):
+        base = x if name == "x" else p[name]
+        u = np.random.default_rng(100 + i).standard_normal(base.shape)
+        e = 1e-3 * max(1.0, float(np.abs(base).max()))
+
+        def at(s):
+            pp = dict(p)
+            xx = x
+            if name == "x":
+                xx = x + s * e * u
+            else:
+                pp[name] = p[name] + s * e * u
+            return float(np.sum(g * ML.layer_forward(pp, xx, d_state=N, headdim=headdim)))
+        fd = (at(1.0) - at(-1.0)) / (2.0 * e)
+        an = float(np.sum(grads[name] * u))
+        errs[name] = abs(an - fd) / max(abs(fd), 1e-12)
+    print(f"layer bwd f32 {(B, L, d_model, N, headdim)}: " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()),
+          flush=True)
+    bad = {k: v for k, v in errs.items() if v > 1e-3}
+    assert not bad, f"directional derivatives above 1e-3: {bad}"
+
+
+@pytest.mark.parametrize("B,L,d_model,N,headdim,path", [
+    (2, 330, 256, 128, 64, "in_place"),    # 1336-wide bf16 rows: x and z read in place
+    (2, 200, 128, 128, 64, "copies"),      # 812-wide bf16 rows: x and z copied
+])
+def test_layer_backward_bf16_matches_f32(B, L, d_model, N, headdim, path):
+    import torch
+    p, x, g = _setup(B, L, d_model, N, headdim)
+    ref = _grads(p, x, g, d_model, N, headdim, torch.float32, "in_place")
+    got = _grads(p, x, g, d_model, N, headdim, torch.bfloat16, path)
+    errs = {k: rel(got[k], ref[k]) for k in ref}
+    print(f"layer bwd bf16 vs f32 {(B, L, d_model, N, headdim)}: " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()),
+          flush=True)
+    bad = {k: v for k, v in errs.items() if v > 1e-1}
+    assert not bad, f"bf16 gradients above 1e-1 of the float32 ones: {bad}"
