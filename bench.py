@@ -21,8 +21,12 @@ Also reported on the same JSON line:
                 and with float32 I/O (what the model's training hands the scan),
                 each with its own roofline, the scan forward, backward and training
                 pair at config 5's layer shape (B=4, L=12288, 24 heads: 96 pairs, the
-                sequence split and the split walk), and the 12-layer backbone prefill
-                with its log-probabilities (config 5)
+                sequence split and the split walk), the 12-layer backbone prefill
+                with its log-probabilities (config 5), the mixer layer's training step
+                at config 5's layer shape, and, at the shape the reference publishes its
+                per-layer training times for (d_model 1024, one 13,000-token
+                sequence: docs/training.md:106-112, 283-294), the fused path's scan
+                forward + backward and the layer's training step beside those times
 
 Before the warm-up of the headline, the kernel is launched untimed until at least
 100 launches and 0.3 s have run (the GPU clocks ramp up over the first ~100
@@ -318,9 +322,10 @@ def bench_stack(torch, B, L, d_model, n_layers, vocab, steps, warmup, seed):
 
 
 def bench_layer_train(torch, B, L, d_model, steps, warmup, seed):
-    """The mixer layer's training step at config 5's layer shape: train_forward and the
-    backward to x and every parameter (bf16 compute, float32 parameters), timed
-    together and the backward alone."""
+    """The mixer layer's training step (24 heads of 64 at config 5's d_model 768, 32 at
+    the reference's published d_model 1024): train_forward and the backward to x and
+    every parameter (bf16 compute, float32 parameters, no optimizer), and the plain
+    forward on its own."""
     from mamba3_rocm import Mamba3Layer
     from mamba3_rocm.layer import init_params
     params = {k: v.requires_grad_(True) for k, v in init_params(d_model, seed, "cuda").items()}
@@ -730,6 +735,9 @@ def main():
         f32 = bench_scan(torch, 8, 4096, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=2,
                          io_dtype=torch.float32)
         bb = bench_stack(torch, 4, 12288, 768, 12, 2112, 5, 2, seed=5)
+        lt5 = bench_layer_train(torch, 4, 12288, 768, max(5, args.steps // 10), 2, seed=5)
+        rs = bench_shared_bwd(torch, 1, 13000, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=6)
+        rl = bench_layer_train(torch, 1, 13000, 1024, max(5, args.steps // 5), 3, seed=6)
         out["secondary"] = {
             "decode_config4": {"B": 512, "H": 32, "P": 64, "N": 128, "steps": 256,
                                "us_per_step": round(dec["kernel_s"] * 1e6, 2),
@@ -775,6 +783,20 @@ def main():
                                          "ms": round(bb["kernel_s"] * 1e3, 4),
                                          "tokens_per_s": round(4 * 12288 / bb["wall_s"], 1),
                                          "gemm_tflops": round(bb["gemm_flops"] / bb["kernel_s"] / 1e12, 1)},
+            "layer_train_config5": {"B": 4, "L": 12288, "d_model": 768, "H": 24, "dtype": "bf16",
+                                    "step_ms": round(lt5["kernel_s"] * 1e3, 4),
+                                    "fwd_ms": round(lt5["fwd_s"] * 1e3, 4),
+                                    "tokens_per_s": round(4 * 12288 / lt5["wall_s"], 1)},
+            "reference_layer_shape": {
+                "B": 1, "L": 13000, "d_model": 1024, "H": 32, "chunk": 64, "dtype": "bf16",
+                "ssd_fwd_bwd_ms": round((rs["fwd_train_s"] + rs["bwd_saved_s"]) * 1e3, 4),
+                "ssd_fwd_train_ms": round(rs["fwd_train_s"] * 1e3, 4),
+                "ssd_bwd_saved_ms": round(rs["bwd_saved_s"] * 1e3, 4),
+                "layer_step_ms": round(rl["kernel_s"] * 1e3, 4),
+                "layer_fwd_ms": round(rl["fwd_s"] * 1e3, 4),
+                "published_gh200": {"ssd_fwd_bwd_ms": 6.6, "ssd_fwd_ms": 1.7, "layer_step_ms": 13.0,
+                                    "source": "docs/training.md:283,291",
+                                    "note": "one GH200; its layer step includes the optimizer's share"}},
         }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

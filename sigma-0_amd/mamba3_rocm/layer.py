@@ -12,11 +12,13 @@ Where the projection rows are not a multiple of 16 bytes, m3_layer_pre also copi
 x and z out of proj and the scan is m3_chunk_scan_fwd_shared on the copies.
 
 ``Mamba3Layer.train_forward`` is the same forward made differentiable (gradients for
-x and for every parameter, as autodiff of Mamba3SSM gives them): its backward is the
-library GEMMs' gradients, m3_layer_post_bwd (the output RMSNorm), the shared scan's
-backward (m3_chunk_scan_bwd_shared) and m3_layer_pre_bwd (BCNorm, the decay's chain
-rule with the A_floor clip, trap and angles, written into the in_proj output's
-gradient).
+x and for every parameter, as autodiff of Mamba3SSM gives them).  Its scan is the
+shared training pair: m3_layer_pre copies x and z (the backward kernels read them
+contiguous) and m3_chunk_scan_fwd_train_shared saves the states entering every
+chunk, which m3_chunk_scan_bwd_saved_shared reads instead of recomputing them.  The
+backward is the library GEMMs' gradients, m3_layer_post_bwd (the output RMSNorm),
+the scan's backward and m3_layer_pre_bwd (BCNorm, the decay's chain rule with the
+A_floor clip, trap and angles, written into the in_proj output's gradient).
 
 Parameters keep the reference's names and layouts (flax Dense kernels are
 (in, out)) and stay float32; ``dtype`` is the compute dtype of the projections
@@ -31,7 +33,7 @@ import torch
 
 from . import _lib
 from .ops import (_IO, _ptr, _stream, mamba3_ssd_chunked_shared_hip, mamba3_ssd_chunked_shared_hip_bwd,
-                  pallas_compute_dtype)
+                  mamba3_ssd_chunked_shared_hip_fwd_train, pallas_compute_dtype)
 
 PARAM_NAMES = ("in_proj", "dt_bias", "B_bias", "C_bias", "B_norm", "C_norm", "D", "out_norm", "out_proj")
 
@@ -67,7 +69,9 @@ class Mamba3Layer:
         # the projections' operands in the compute dtype (nn.Dense(dtype=...) casts them)
         self.w_in = self.params["in_proj"].to(dtype).contiguous()
         self.w_out = self.params["out_proj"].to(dtype).contiguous()
-        self.last_scan = None      # "in_place" or "copies": how the last forward fed x and z to the scan
+        # "in_place", "copies" or "train_pair" (train_forward: copies and the scan's
+        # training forward): how the last forward fed x and z to the scan
+        self.last_scan = None
         self.last_compute_dtype = None   # the scan's operand dtype in the last forward
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -82,7 +86,8 @@ class Mamba3Layer:
         return _LayerTrain.apply(self, x, *(self.params[k] for k in PARAM_NAMES))
 
     def _run(self, x: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor, keep: bool = False):
-        """The forward; with ``keep`` also the intermediates the backward reads."""
+        """The forward; with ``keep`` (train_forward) also the intermediates the backward
+        reads, the scan then on copies of x and z with its residuals saved."""
         unbatched = x.dim() == 2
         if unbatched:
             x = x[None]
@@ -114,10 +119,10 @@ class Mamba3Layer:
         # layer's (mamba3_pallas.py:112-122, 838-839): then the copies are cast to it.
         cdt = pallas_compute_dtype(dt)
         es = proj.element_size()
-        in_place = (cdt == dt and (self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
+        in_place = (not keep and cdt == dt and (self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
                     and proj.data_ptr() % 16 == 0
                     and lib.m3_chunk_scan_impl(io, N, hd, R, self.chunk_size) == _lib.IMPL_CHUNKED_MFMA)
-        self.last_scan = "in_place" if in_place else "copies"
+        self.last_scan = "in_place" if in_place else ("train_pair" if keep else "copies")
         self.last_compute_dtype = cdt
         if in_place:
             pre(None, None)
@@ -132,14 +137,18 @@ class Mamba3Layer:
             V = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
             Z = torch.empty_like(V)
             pre(V, Z)
-            y = mamba3_ssd_chunked_shared_hip(Q, K, V, ADT, DT, Trap, Ang, pp["C_bias"], pp["B_bias"], pp["D"], Z,
-                                              chunk_size=self.chunk_size, compute_dtype=cdt)
+            scan_args = (Q, K, V, ADT, DT, Trap, Ang, pp["C_bias"], pp["B_bias"], pp["D"], Z)
+            if keep:
+                y, scan_saved = mamba3_ssd_chunked_shared_hip_fwd_train(*scan_args, chunk_size=self.chunk_size,
+                                                                        compute_dtype=cdt)
+            else:
+                y = mamba3_ssd_chunked_shared_hip(*scan_args, chunk_size=self.chunk_size, compute_dtype=cdt)
         yn = torch.empty(B, L, self.d_inner, device=dev, dtype=dt)
         _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), B, L, self.d_inner, self.eps, io,
                                      _stream(y)), "m3_layer_post")
         out = torch.matmul(yn, w_out)
-        saved = (dict(xin=xin, proj=proj, Q=Q, K=K, ADT=ADT, DT=DT, Trap=Trap, Ang=Ang, y=y, yn=yn, cdt=cdt)
-                 if keep else None)
+        saved = (dict(xin=xin, proj=proj, Q=Q, K=K, V=V, Z=Z, ADT=ADT, DT=DT, Trap=Trap, Ang=Ang, y=y, yn=yn,
+                      cdt=cdt, scan=scan_saved) if keep else None)
         return (out[0] if unbatched else out), saved
 
     def _backward(self, saved, dout: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor):
@@ -166,13 +175,12 @@ class Mamba3Layer:
         ws = torch.empty(max(lib.m3_layer_post_bwd_ws_bytes(B, L, di), 16), dtype=torch.uint8, device=dev)
         _lib.check(lib.m3_layer_post_bwd(_ptr(y), _ptr(d_yn), _ptr(pp["out_norm"]), _ptr(d_y), _ptr(g_out_norm), B, L,
                                          di, eps, io, ws.data_ptr(), ws.numel(), _stream(y)), "m3_layer_post_bwd")
-        # the scan (Q = C, K = B shared over heads; x and z from proj)
-        Vv = proj[..., di:2 * di].reshape(B, L, nh, hd).contiguous()
-        Zv = proj[..., :di].reshape(B, L, nh, hd).contiguous()
-        g = mamba3_ssd_chunked_shared_hip_bwd(saved["Q"], saved["K"], Vv, saved["ADT"], saved["DT"], saved["Trap"],
-                                              saved["Ang"], pp["C_bias"], pp["B_bias"], pp["D"], Zv,
-                                              d_y.reshape(B, L, nh, hd), chunk_size=self.chunk_size,
-                                              compute_dtype=saved["cdt"])
+        # the scan (Q = C, K = B shared over heads), from the training forward's residuals
+        # (recomputed where the shape has none)
+        g = mamba3_ssd_chunked_shared_hip_bwd(saved["Q"], saved["K"], saved["V"], saved["ADT"], saved["DT"],
+                                              saved["Trap"], saved["Ang"], pp["C_bias"], pp["B_bias"], pp["D"],
+                                              saved["Z"], d_y.reshape(B, L, nh, hd), chunk_size=self.chunk_size,
+                                              saved=saved["scan"], compute_dtype=saved["cdt"])
         dC, dB, dV, dADT, dDT, dTrap, dAng, g_C_bias, g_B_bias, g_D, dZ = g
         # _preprocess (:203-268): BCNorm, the decay, trap and angles back to the in_proj output
         d_proj = torch.empty_like(proj)

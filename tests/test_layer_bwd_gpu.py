@@ -25,7 +25,9 @@ NAMES = ("in_proj", "dt_bias", "B_bias", "C_bias", "B_norm", "C_norm", "D", "out
 
 
 def _grads(p, x, g, d_model, N, headdim, dtype, path):
-    """Output and gradients (x first, then NAMES) of train_forward, as float64 numpy."""
+    """Output and gradients (x first, then NAMES) of train_forward, as float64 numpy.
+    train_forward runs the scan's training pair on copies of x and z; its output must
+    equal the plain forward's (route ``path``) bitwise."""
     import torch
     from mamba3_rocm import Mamba3Layer
     params = {k: torch.from_numpy(v).cuda().requires_grad_(True) for k, v in p.items()}
@@ -34,11 +36,14 @@ def _grads(p, x, g, d_model, N, headdim, dtype, path):
         assert layer.params[k] is params[k], "the layer keeps the caller's float32 parameters"
     xt = torch.from_numpy(x).cuda().requires_grad_(True)
     out = layer.train_forward(xt)
-    assert layer.last_scan == path
+    assert layer.last_scan == "train_pair"
     (out.float() * torch.from_numpy(g).float().cuda()).sum().backward()
     torch.cuda.synchronize()
     # the differentiable forward is the layer's forward
-    assert torch.equal(out, layer(torch.from_numpy(x).cuda()))
+    plain = layer(torch.from_numpy(x).cuda())
+    assert layer.last_scan == path
+    assert torch.equal(out, plain), "train_forward's output differs from the forward's"
+
     grads = {"x": xt.grad.float().cpu().numpy().astype(np.float64)}
     for k in NAMES:
         assert params[k].grad is not None and params[k].grad.dtype == torch.float32, k
@@ -90,6 +95,7 @@ def test_layer_backward_f32_matches_finite_differences(B, L, d_model, N, headdim
 @pytest.mark.parametrize("B,L,d_model,N,headdim,path", [
     (2, 330, 256, 128, 64, "in_place"),    # 1336-wide bf16 rows: x and z read in place
     (2, 200, 128, 128, 64, "copies"),      # 812-wide bf16 rows: x and z copied
+    (1, 1100, 256, 128, 64, "in_place"),   # 8 pairs: the scan's sequence splits, forward and backward
 ])
 def test_layer_backward_bf16_matches_f32(B, L, d_model, N, headdim, path):
     import torch
