@@ -2,16 +2,18 @@
 // Mamba3SSM._preprocess and _post_norm_and_project (src/base_model/models/
 // mamba3.py:203-331) gives it, with float32 arithmetic:
 //   layer_post_bwd_kernel  the output RMSNorm n = y r scale, r = rsqrt(mean(y^2) + eps):
-//                          dy = r (dn scale) - r^3 y mean(dn scale y), one wave per run of
-//                          kPostTok tokens; the scale's gradient sum_t dn y r as one
-//                          partial row per wave
+//                          dy = r (dn scale) - r^3 y mean(dn scale y), one workgroup per
+//                          kPostTok tokens, its waves on every fourth token (each loading
+//                          its next token before working on the current one); the
+//                          scale's gradient sum_t dn y r as one partial row per workgroup
 //   layer_pre_bwd_kernel   d(proj) from the scan's gradients, one workgroup per tile of
 //                          kPreTile tokens of one batch row: dZ and dV into the z and x
-//                          columns, BCNorm's backward into B and C (one wave per token),
-//                          the decay's chain rule into dd_dt and dd_A and dTrap into trap
-//                          (lanes along the tokens, one head per wave at a time), dAngles
-//                          into the angle columns; the norm scales' and dt_bias's gradients
-//                          as one partial row per workgroup
+//                          columns and BCNorm's backward into B and C (one wave per token,
+//                          both rows' loads issued before their stores), the decay's chain
+//                          rule into dd_dt and dd_A and dTrap into trap (lanes along the
+//                          tokens, one head per wave at a time), dAngles into the angle
+//                          columns; the norm scales' and dt_bias's gradients as one partial
+//                          row per workgroup
 //   reduce_slices_kernel,  the partial rows summed in a fixed order (the gradients are
 //   reduce_final_kernel    deterministic): kReduceSlices slices of rows side by side,
 //                          then the slices' sums
@@ -22,9 +24,10 @@ namespace m3 {
 namespace {
 
 constexpr int kBwdElThreads = 256;
-constexpr int kPostTok = 32;            // tokens per wave, layer_post_bwd
+constexpr int kPostTok = 16;            // tokens per workgroup, layer_post_bwd
 constexpr int kPreTile = 64;            // tokens per workgroup, layer_pre_bwd (one per lane)
-constexpr int kPostChunks = kLayerPostBwdMaxD / (64 * 8);   // 8-element chunks per lane
+constexpr int kPreThreads = 512;        // layer_pre_bwd's workgroup: eight waves
+constexpr int kPostChunks = kLayerPostBwdMaxD / (64 * 8);   // 8-element chunks per lane, at most
 constexpr int kPreCols = kLayerPreBwdMaxN / 64;             // B / C columns per lane
 constexpr int kReduceSlices = 16;                           // row slices of the partial sums
 
@@ -32,28 +35,53 @@ __device__ __forceinline__ float softplus_f(float x) {     // as layer_pre: loga
   return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
 }
 
+// Two rows of n elements, s0 -> d0 and s1 -> d1, by one wave: 16-byte pieces when all
+// four are 16-byte aligned, every load of a lane issued before its stores.
 template <typename T>
-__device__ __forceinline__ void copy_row(T* dst, const T* src, int n, int lane) {
+__device__ __forceinline__ void copy_two_rows(T* __restrict__ d0, const T* __restrict__ s0, T* __restrict__ d1,
+                                              const T* __restrict__ s1, int n, int lane) {
   constexpr int V = 16 / sizeof(T);
-  if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && n % V == 0) {
-    for (int i = lane; i < n / V; i += 64) reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+  if (((reinterpret_cast<uintptr_t>(d0) | reinterpret_cast<uintptr_t>(s0) | reinterpret_cast<uintptr_t>(d1) |
+        reinterpret_cast<uintptr_t>(s1)) & 15) == 0 && n % V == 0) {
+    const int nv = n / V;
+    const uint4* v0 = reinterpret_cast<const uint4*>(s0);
+    const uint4* v1 = reinterpret_cast<const uint4*>(s1);
+    uint4* w0 = reinterpret_cast<uint4*>(d0);
+    uint4* w1 = reinterpret_cast<uint4*>(d1);
+    for (int i = lane; i < nv; i += 4 * 64) {
+      const bool k1 = i + 64 < nv, k2 = i + 128 < nv, k3 = i + 192 < nv;
+      const uint4 a0 = v0[i], c0 = v1[i];
+      uint4 a1 = {}, c1 = {}, a2 = {}, c2 = {}, a3 = {}, c3 = {};
+      if (k1) { a1 = v0[i + 64]; c1 = v1[i + 64]; }
+      if (k2) { a2 = v0[i + 128]; c2 = v1[i + 128]; }
+      if (k3) { a3 = v0[i + 192]; c3 = v1[i + 192]; }
+      w0[i] = a0;
+      w1[i] = c0;
+      if (k1) { w0[i + 64] = a1; w1[i + 64] = c1; }
+      if (k2) { w0[i + 128] = a2; w1[i + 128] = c2; }
+      if (k3) { w0[i + 192] = a3; w1[i + 192] = c3; }
+    }
   } else {
-    for (int i = lane; i < n; i += 64) dst[i] = src[i];
+    for (int i = lane; i < n; i += 64) {
+      d0[i] = s0[i];
+      d1[i] = s1[i];
+    }
   }
 }
 
-template <typename T>
+// CH: 8-element chunks per lane, ceil(D / 512).
+template <typename T, int CH>
 __global__ __launch_bounds__(kBwdElThreads)
 void layer_post_bwd_kernel(LayerPostBwdArgs a) {
+  __shared__ float red[kBwdElThreads / 64][kLayerPostBwdMaxD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const long run = (long)blockIdx.x * (kBwdElThreads / 64) + wave;
-  const long rows = (long)a.B * a.L, t0 = run * kPostTok;
-  if (t0 >= rows) return;                             // whole waves only: no barrier below
+  const long rows = (long)a.B * a.L, t0 = (long)blockIdx.x * kPostTok;
+  const long t1 = t0 + kPostTok < rows ? t0 + kPostTok : rows;
   const int D = a.D, nch = D / 8;
   const float invD = 1.0f / (float)D;
-  float sc[kPostChunks][8], acc[kPostChunks][8];
+  float sc[CH][8], acc[CH][8];
 #pragma unroll
-  for (int j = 0; j < kPostChunks; ++j) {
+  for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -61,21 +89,33 @@ void layer_post_bwd_kernel(LayerPostBwdArgs a) {
       acc[j][e] = 0.0f;
     }
   }
-  const long t1 = t0 + kPostTok < rows ? t0 + kPostTok : rows;
-  for (long t = t0; t < t1; ++t) {
+  Vec8<T> ny[CH], nd[CH];                              // the wave's next token
+  auto issue = [&](long t) {
     const T* yr = reinterpret_cast<const T*>(a.y) + t * D;
     const T* dr = reinterpret_cast<const T*>(a.dn) + t * D;
-    float yv[kPostChunks][8], dv[kPostChunks][8];
-    float ss = 0.0f, sd = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kPostChunks; ++j) {
+    for (int j = 0; j < CH; ++j) {
       const int c = lane + 64 * j;
       if (c < nch) {
-        Vec8<T> v;
-        v.load(yr + 8 * c);
-        v.to_f(yv[j]);
-        v.load(dr + 8 * c);
-        v.to_f(dv[j]);
+        ny[j].load(yr + 8 * c);
+        nd[j].load(dr + 8 * c);
+      }
+    }
+  };
+  constexpr int kW = kBwdElThreads / 64;
+  if (t0 + wave < t1) issue(t0 + wave);
+  for (long t = t0 + wave; t < t1; t += kW) {
+    float yv[CH][8], dv[CH][8];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      ny[j].to_f(yv[j]);
+      nd[j].to_f(dv[j]);
+    }
+    if (t + kW < t1) issue(t + kW);
+    float ss = 0.0f, sd = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      if (lane + 64 * j < nch) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           ss += yv[j][e] * yv[j][e];
@@ -89,7 +129,7 @@ void layer_post_bwd_kernel(LayerPostBwdArgs a) {
     const float k = r * r * r * (sd * invD);
     T* out = reinterpret_cast<T*>(a.dy) + t * D;
 #pragma unroll
-    for (int j = 0; j < kPostChunks; ++j) {
+    for (int j = 0; j < CH; ++j) {
       const int c = lane + 64 * j;
       if (c < nch) {
         float o[8];
@@ -102,18 +142,24 @@ void layer_post_bwd_kernel(LayerPostBwdArgs a) {
       }
     }
   }
-  float* part = a.part + run * D;
+  // the workgroup's partial row: the four waves' sums added in wave order
 #pragma unroll
-  for (int j = 0; j < kPostChunks; ++j) {
+  for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
-    if (c < nch) store8(part + 8 * c, acc[j]);
+    if (c < nch)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wave][8 * c + e] = acc[j][e];
   }
+  __syncthreads();
+  float* part = a.part + (long)blockIdx.x * D;
+  for (int c = threadIdx.x; c < D; c += kBwdElThreads) part[c] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
 }
 
 template <typename T>
-__global__ __launch_bounds__(kBwdElThreads)
+__global__ __launch_bounds__(kPreThreads)
 void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
-  __shared__ float red[kBwdElThreads / 64][2][kLayerPreBwdMaxN];
+  constexpr int kW = kPreThreads / 64;
+  __shared__ float red[kW][2][kLayerPreBwdMaxN];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tiles = (a.L + kPreTile - 1) / kPreTile;
   const int b = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * kPreTile;
@@ -132,25 +178,25 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
 #pragma unroll
   for (int k = 0; k < kPreCols; ++k) accB[k] = accC[k] = 0.0f;
   const float invN = 1.0f / (float)N;
-  for (int i = wave; i < nt; i += kBwdElThreads / 64) {
+  for (int i = wave; i < nt; i += kW) {
     const long row = row0 + i;
     T* dpr = dproj + (long)i * dp;
     const T* pr = proj + (long)i * dp;
-    copy_row(dpr, reinterpret_cast<const T*>(a.dz) + row * di, di, lane);
-    copy_row(dpr + di, reinterpret_cast<const T*>(a.dv) + row * di, di, lane);
+    copy_two_rows(dpr, reinterpret_cast<const T*>(a.dz) + row * di, dpr + di, reinterpret_cast<const T*>(a.dv) + row * di,
+                  di, lane);
     // n = m rsqrt(mean m^2 + eps) scale  (B: K's, C: Q's)
 #pragma unroll
     for (int side = 0; side < 2; ++side) {
       const T* g = reinterpret_cast<const T*>(side ? a.dq : a.dk) + row * N;
       const float* scale = side ? a.c_scale : a.b_scale;
       const int o = side ? oC : oB;
-      float m[kPreCols], ds[kPreCols], ss = 0.0f, sd = 0.0f;
+      float m[kPreCols], dn[kPreCols], ds[kPreCols], ss = 0.0f, sd = 0.0f;
 #pragma unroll
       for (int k = 0; k < kPreCols; ++k) {
         const int n = lane + 64 * k;
         m[k] = n < N ? Elem<T>::to_f(pr[o + n]) : 0.0f;
-        const float dn = n < N ? Elem<T>::to_f(g[n]) : 0.0f;
-        ds[k] = n < N ? dn * scale[n] : 0.0f;
+        dn[k] = n < N ? Elem<T>::to_f(g[n]) : 0.0f;
+        ds[k] = n < N ? dn[k] * scale[n] : 0.0f;
         ss += m[k] * m[k];
         sd += ds[k] * m[k];
       }
@@ -164,7 +210,7 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
         if (n < N) {
           dpr[o + n] = Elem<T>::from_f(r * ds[k] - kk * m[k]);
           // the scale's gradient: dn m r
-          const float gs = Elem<T>::to_f(g[n]) * m[k] * r;
+          const float gs = dn[k] * m[k] * r;
           if (side) accC[k] += gs;
           else accB[k] += gs;
         }
@@ -173,7 +219,7 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
   }
   // ---- lanes along the tokens, one head per wave at a time: DT = softplus(dd_dt +
   // dt_bias), A = min(-softplus(dd_A), -A_floor), ADT = A DT; trap passes through
-  for (int h = wave; h < H; h += kBwdElThreads / 64) {
+  for (int h = wave; h < H; h += kW) {
     float du = 0.0f;
     if (lane < nt) {
       const long hl = ((long)b * H + h) * a.L + t0 + lane;
@@ -196,11 +242,11 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
     if (lane == 0) part[2 * N + h] = du;
   }
   // ---- the angle rates' gradients into their columns
-  for (int e = tid; e < nt * R; e += kBwdElThreads) {
+  for (int e = tid; e < nt * R; e += kPreThreads) {
     const int i = e / R, r = e % R;
     dproj[(long)i * dp + oT + 3 * H + r] = Elem<T>::from_f(a.dang[(row0 + i) * R + r]);
   }
-  // ---- the norm scales' partial sums over the tile: the four waves' rows added in order
+  // ---- the norm scales' partial sums over the tile: the waves' rows added in order
 #pragma unroll
   for (int k = 0; k < kPreCols; ++k) {
     const int n = lane + 64 * k;
@@ -210,11 +256,11 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
     }
   }
   __syncthreads();
-  for (int n = tid; n < 2 * N; n += kBwdElThreads) {
+  for (int n = tid; n < 2 * N; n += kPreThreads) {
     const int side = n / N, c = n % N;
     float s = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kBwdElThreads / 64; ++w) s += red[w][side][c];
+    for (int w = 0; w < kW; ++w) s += red[w][side][c];
     part[n] = s;
   }
 }
@@ -265,9 +311,16 @@ long layer_pre_bwd_parts(int B, int L) { return (long)B * ((L + kPreTile - 1) / 
 
 hipError_t layer_post_bwd_launch(const LayerPostBwdArgs& a, float* dscale, bool bf16_io, hipStream_t st) {
   const long runs = layer_post_bwd_parts(a.B, a.L) - kReduceSlices;   // the rest of the rows: the slices' sums
-  const dim3 grid((unsigned)((runs + kBwdElThreads / 64 - 1) / (kBwdElThreads / 64)));
-  if (bf16_io) hipLaunchKernelGGL(layer_post_bwd_kernel<bf16>, grid, dim3(kBwdElThreads), 0, st, a);
-  else hipLaunchKernelGGL(layer_post_bwd_kernel<float>, grid, dim3(kBwdElThreads), 0, st, a);
+  const dim3 grid((unsigned)runs);
+  const int ch = (a.D / 8 + 63) / 64;
+  static_assert(kPostChunks == 4, "layer_post_bwd instantiations");
+#define M3_POST_BWD(CH)                                                                                  \
+  if (ch == CH) {                                                                                        \
+    if (bf16_io) hipLaunchKernelGGL((layer_post_bwd_kernel<bf16, CH>), grid, dim3(kBwdElThreads), 0, st, a); \
+    else hipLaunchKernelGGL((layer_post_bwd_kernel<float, CH>), grid, dim3(kBwdElThreads), 0, st, a);        \
+  }
+  M3_POST_BWD(1) M3_POST_BWD(2) M3_POST_BWD(3) M3_POST_BWD(4)
+#undef M3_POST_BWD
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return reduce_rows(a.part, runs, a.D, a.part + runs * a.D, dscale, a.D, nullptr, 0, nullptr, st);
@@ -276,8 +329,8 @@ hipError_t layer_post_bwd_launch(const LayerPostBwdArgs& a, float* dscale, bool 
 hipError_t layer_pre_bwd_launch(const LayerPreBwdArgs& a, float* d_b_scale, float* d_c_scale, float* d_dt_bias,
                                 bool bf16_io, hipStream_t st) {
   const long blocks = layer_pre_bwd_parts(a.B, a.L) - kReduceSlices;
-  if (bf16_io) hipLaunchKernelGGL(layer_pre_bwd_kernel<bf16>, dim3((unsigned)blocks), dim3(kBwdElThreads), 0, st, a);
-  else hipLaunchKernelGGL(layer_pre_bwd_kernel<float>, dim3((unsigned)blocks), dim3(kBwdElThreads), 0, st, a);
+  if (bf16_io) hipLaunchKernelGGL(layer_pre_bwd_kernel<bf16>, dim3((unsigned)blocks), dim3(kPreThreads), 0, st, a);
+  else hipLaunchKernelGGL(layer_pre_bwd_kernel<float>, dim3((unsigned)blocks), dim3(kPreThreads), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int cols = 2 * a.N + a.H;
