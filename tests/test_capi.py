@@ -465,6 +465,53 @@ def test_layer_scan_validation(lib):
                             2, 64, H, P, N, R, 1e-4, 1e-6, _lib.DTYPE_BF16, None) == _lib.M3_E_ARG
 
 
+def test_layer_backward_entry_points_validate(lib):
+    """m3_layer_post_bwd and m3_layer_pre_bwd reject bad dtypes, dimensions, shapes
+    above their limits, NULL pointers, short workspaces and (post) misaligned rows
+    before any launch; an empty batch is a no-op; the workspace sizes are 0 for
+    non-positive dimensions and grow with the row count and the columns."""
+    from mamba3_rocm import _lib
+    fake = 1 << 20                      # never dereferenced: every call fails validation or is empty
+    bf, f32 = _lib.DTYPE_BF16, _lib.DTYPE_F32
+    B, L, D = 2, 64, 256
+    ws = lib.m3_layer_post_bwd_ws_bytes(B, L, D)
+    assert ws > 0 and ws % (4 * D) == 0
+    assert lib.m3_layer_post_bwd_ws_bytes(0, L, D) == 0 and lib.m3_layer_post_bwd_ws_bytes(B, L, 0) == 0
+    assert lib.m3_layer_post_bwd_ws_bytes(B, 4 * L, D) > ws
+    assert lib.m3_layer_post_bwd_ws_bytes(B, L, 2 * D) == 2 * ws
+
+    def post(y=fake, dn=fake, sc=fake, dy=fake, dsc=fake, B=B, L=L, D=D, io=bf, w=fake, wsb=ws):
+        return lib.m3_layer_post_bwd(y, dn, sc, dy, dsc, B, L, D, 1e-6, io, w, wsb, None)
+    assert post(io=9) == _lib.M3_E_ARG
+    assert post(D=0) == _lib.M3_E_ARG
+    assert post(D=260) == _lib.M3_E_UNSUPPORTED                    # not a multiple of 8
+    assert post(D=4096, wsb=1 << 30) == _lib.M3_E_UNSUPPORTED       # above 2048
+    assert post(B=0, y=None) == _lib.M3_OK
+    assert post(dsc=None) == _lib.M3_E_ARG
+    assert post(w=None) == _lib.M3_E_ARG
+    assert post(wsb=ws - 4) == _lib.M3_E_ARG and b"workspace" in lib.m3_last_error()
+    assert post(dy=fake + 8) == _lib.M3_E_ALIGN
+    assert post(D=8, io=f32, wsb=lib.m3_layer_post_bwd_ws_bytes(B, L, 8), dy=None) == _lib.M3_E_ARG
+
+    H, P, N, R = 4, 64, 128, 32
+    wsp = lib.m3_layer_pre_bwd_ws_bytes(B, L, H, N)
+    assert wsp > 0 and wsp % (4 * (2 * N + H)) == 0
+    assert lib.m3_layer_pre_bwd_ws_bytes(B, L, 0, N) == 0 and lib.m3_layer_pre_bwd_ws_bytes(B, 0, H, N) == 0
+    assert lib.m3_layer_pre_bwd_ws_bytes(B, 4 * L, H, N) > wsp
+
+    def pre(proj=fake, dang=fake, dproj=fake, B=B, L=L, H=H, N=N, R=R, io=bf, w=fake, wsb=wsp):
+        return lib.m3_layer_pre_bwd(proj, fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, dang, dproj,
+                                    fake, fake, fake, B, L, H, P, N, R, 1e-4, 1e-6, io, w, wsb, None)
+    assert pre(io=3) == _lib.M3_E_ARG
+    assert pre(H=0) == _lib.M3_E_ARG
+    assert pre(N=512, wsb=1 << 30) == _lib.M3_E_UNSUPPORTED and b"d_state" in lib.m3_last_error()
+    assert pre(B=0, proj=None) == _lib.M3_OK
+    assert pre(proj=None) == _lib.M3_E_ARG
+    assert pre(dang=None) == _lib.M3_E_ARG                         # R > 0 needs dAngles
+    assert pre(w=None) == _lib.M3_E_ARG
+    assert pre(wsb=wsp - 4) == _lib.M3_E_ARG and b"workspace" in lib.m3_last_error()
+
+
 def test_block_entry_points_validate(lib):
     """The backbone block's C entry points (LayerNorm, gelu, activation epilogue)
     reject bad dtypes, activations and missing Dense outputs before any launch, and
