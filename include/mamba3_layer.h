@@ -8,6 +8,9 @@
  *                  proj (or m3_chunk_scan_fwd_shared of mamba3_scan.h on copies)
  *   m3_layer_post: output RMSNorm
  *   out = m3_layer_post(...) @ out_proj                 (library GEMM)
+ * and its backward: m3_layer_post_bwd, m3_layer_scan_bwd (after m3_layer_scan_train,
+ * the forward that saves the scan's residuals), m3_layer_pre_bwd, with the GEMMs'
+ * gradients between them.
  * Same conventions as mamba3_scan.h: device pointers, io_dtype M3_DTYPE_F32 or
  * M3_DTYPE_BF16, asynchronous on `stream`, 0 or an M3_E* code (m3_last_error).
  */
@@ -54,6 +57,32 @@ int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
                   const float* Q_bias, const float* K_bias, const float* D, void* Out,
                   int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
                   void* ws, size_t ws_bytes, void* stream);
+/*
+ * The layer's training pair with x and z in place: m3_chunk_scan_fwd_train_shared and
+ * m3_chunk_scan_bwd_saved_shared of mamba3_scan.h (the fused path's chunk_scan_fwd_rule /
+ * chunk_scan_bwd_rule, mamba3_pallas.py:602-645) with V and Z read from proj as
+ * m3_layer_scan reads them, and the backward's dV and dZ written into the x and z
+ * columns [HP, 2HP) and [0, HP) of d_proj (B, L, d_in_proj, io_dtype), which
+ * m3_layer_pre_bwd then completes (called with dV = dZ = NULL).  Same layout
+ * conditions and errors as m3_layer_scan, for proj and d_proj alike.
+ * m3_layer_scan_train: saved of m3_chunk_scan_saved_bytes, workspace of
+ * m3_chunk_scan_ws_bytes.  m3_layer_scan_bwd: with saved, the workspace of
+ * m3_chunk_scan_bwd_saved_shared_ws_bytes; with saved = NULL the chunk states are
+ * recomputed, workspace of m3_chunk_scan_bwd_shared_ws_bytes.  Z is always present
+ * (the layer's gate).
+ */
+int m3_layer_scan_train(const void* Q, const void* K, const void* proj, int d_in_proj,
+                        const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                        const float* Q_bias, const float* K_bias, const float* D, void* Out,
+                        int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                        void* saved, size_t saved_bytes, void* ws, size_t ws_bytes, void* stream);
+int m3_layer_scan_bwd(const void* Q, const void* K, const void* proj, int d_in_proj,
+                      const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                      const float* Q_bias, const float* K_bias, const float* D, const void* dOut,
+                      void* dQ, void* dK, void* d_proj, float* dADT, float* dDT, float* dTrap,
+                      float* dQ_bias, float* dK_bias, float* dAngles, float* dD,
+                      int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                      const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Replaces the RMSNorm of Mamba3SSM._post_norm_and_project (mamba3.py:281-312,
@@ -82,7 +111,8 @@ int m3_layer_post_bwd(const void* y, const void* d_out, const float* scale, void
 /*
  * m3_layer_pre's backward: from proj and the parameters m3_layer_pre read, and the
  * gradients of its outputs -- dQ and dK of the normalised C and B (B, L, N), dV and
- * dZ (B, L, H, P), all in io_dtype (m3_chunk_scan_bwd_shared's dQ, dK, dV, dZ), and
+ * dZ (B, L, H, P), all in io_dtype (m3_chunk_scan_bwd_shared's dQ, dK, dV, dZ; dV and dZ
+ * both NULL when m3_layer_scan_bwd wrote them into d_proj already), and
  * dADT, dDT, dTrap (B, H, L) and dAngles (B, L, R) float32 -- d_proj like proj (every
  * column written: the gradient of the in_proj output) and d_dt_bias (H,),
  * d_B_norm_scale, d_C_norm_scale (N,) float32.  The A_floor clip passes the gradient

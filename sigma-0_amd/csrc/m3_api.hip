@@ -53,7 +53,7 @@ bool decode_supported(int N, int P, int R) {
 
 extern "C" {
 
-int m3_abi_version(void) { return 102; }
+int m3_abi_version(void) { return 103; }
 
 const char* m3_last_error(void) { return g_err; }
 
@@ -297,7 +297,8 @@ int scan_bwd(const void* Q, const void* K, const void* V,
              float* dQ_bias, float* dK_bias, float* dAngles, float* dD, void* dZ,
              int B, int L, int H, int Hqk, int N, int P, int R,
              int chunk_size, int io_dtype, void* ws, size_t ws_bytes, void* stream, bool ang_shared,
-             const void* saved = nullptr, size_t saved_bytes = 0) {
+             const void* saved = nullptr, size_t saved_bytes = 0, long vz_tok = 0, long vz_bat = 0,
+             long dvz_tok = 0, long dvz_bat = 0) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || Hqk <= 0 || N <= 0 || P <= 0 || R < 0 || chunk_size <= 0)
@@ -340,6 +341,8 @@ int scan_bwd(const void* Q, const void* K, const void* V,
   a.fin_theta = a.fin_h = a.fin_k = a.fin_v = nullptr;
   a.B = B; a.L = L; a.H = H; a.Hqk = Hqk; a.N = N; a.P = P; a.R = R; a.CS = chunk_size;
   a.ang_shared = ang_shared ? 1 : 0;
+  a.vz_tok = vz_tok; a.vz_bat = vz_bat;
+  g.dvz_tok = dvz_tok; g.dvz_bat = dvz_bat;
   g.dout = dOut;
   g.dq = dQ; g.dk = dK; g.dv = dV; g.dz = dZ;
   g.dadt = dADT; g.ddt = dDT; g.dtrap = dTrap; g.dang = dAngles;
@@ -529,16 +532,19 @@ int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_sca
                       "layer pre");
 }
 
-int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
-                  const float* ADT, const float* DT, const float* Trap, const float* Angles,
-                  const float* Q_bias, const float* K_bias, const float* D, void* Out,
-                  int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
-                  void* ws, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// The in-place layout of the layer's scan entry points: projection rows exactly
+// 2HP + 2N + 3H + R wide (the layout m3_layer_pre reads) and a multiple of 16 bytes;
+// z in columns [0, HP) and x in [HP, 2HP).  On success *pz, *px point at row 0's z and
+// x of `base` (proj, or d_proj for the gradients).
+int layer_rows(const void* base, int d_in_proj, int H, int N, int P, int R, int io_dtype, const char** pz,
+               const char** px) {
   if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (H <= 0 || P <= 0 || N <= 0 || R < 0)
     return fail(M3_E_ARG, "non-positive dimension (H=%d N=%d P=%d R=%d)", H, N, P, R);
-  // the projection layout that m3_layer_pre reads too: no padded rows
   if ((long)d_in_proj != 2L * H * P + 2L * N + 3L * H + R)
     return fail(M3_E_ARG, "d_in_proj=%d is not the projection's width (2HP + 2N + 3H + R = %ld)", d_in_proj,
                 2L * H * P + 2L * N + 3L * H + R);
@@ -546,12 +552,57 @@ int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
   if (((long)d_in_proj * es) % 16 != 0)
     return fail(M3_E_ALIGN, "projection rows of %ld bytes: the in-place read of x and z needs a multiple of 16",
                 (long)d_in_proj * es);
-  if (!proj) return fail(M3_E_ARG, "NULL required pointer");
-  const char* pz = reinterpret_cast<const char*>(proj);          // z: columns [0, HP)
-  const char* pv = pz + (long)H * P * es;                          // x: columns [HP, 2HP)
+  if (!base) return fail(M3_E_ARG, "NULL required pointer");
+  *pz = reinterpret_cast<const char*>(base);
+  *px = *pz + (long)H * P * es;
+  return M3_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
+                  const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                  const float* Q_bias, const float* K_bias, const float* D, void* Out,
+                  int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                  void* ws, size_t ws_bytes, void* stream) {
+  const char *pz, *pv;
+  const int rc = layer_rows(proj, d_in_proj, H, N, P, R, io_dtype, &pz, &pv);
+  if (rc != M3_OK) return rc;
   return scan_fwd(Q, K, pv, ADT, DT, Trap, Q_bias, K_bias, Angles, D, pz, Out, nullptr, nullptr, nullptr, nullptr,
                   nullptr, nullptr, nullptr, nullptr, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes, stream,
                   true, d_in_proj, (long)L * d_in_proj);
+}
+
+int m3_layer_scan_train(const void* Q, const void* K, const void* proj, int d_in_proj,
+                        const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                        const float* Q_bias, const float* K_bias, const float* D, void* Out,
+                        int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                        void* saved, size_t saved_bytes, void* ws, size_t ws_bytes, void* stream) {
+  const char *pz, *pv;
+  const int rc = layer_rows(proj, d_in_proj, H, N, P, R, io_dtype, &pz, &pv);
+  if (rc != M3_OK) return rc;
+  if (saved == nullptr) return fail(M3_E_ARG, "NULL saved-state buffer");
+  return scan_fwd(Q, K, pv, ADT, DT, Trap, Q_bias, K_bias, Angles, D, pz, Out, nullptr, nullptr, nullptr, nullptr,
+                  nullptr, nullptr, nullptr, nullptr, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes, stream,
+                  true, d_in_proj, (long)L * d_in_proj, saved, saved_bytes);
+}
+
+int m3_layer_scan_bwd(const void* Q, const void* K, const void* proj, int d_in_proj,
+                      const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                      const float* Q_bias, const float* K_bias, const float* D, const void* dOut,
+                      void* dQ, void* dK, void* d_proj, float* dADT, float* dDT, float* dTrap,
+                      float* dQ_bias, float* dK_bias, float* dAngles, float* dD,
+                      int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                      const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes, void* stream) {
+  const char *pz, *pv, *gz, *gv;
+  int rc = layer_rows(proj, d_in_proj, H, N, P, R, io_dtype, &pz, &pv);
+  if (rc != M3_OK) return rc;
+  if ((rc = layer_rows(d_proj, d_in_proj, H, N, P, R, io_dtype, &gz, &gv)) != M3_OK) return rc;
+  const long tok = d_in_proj, bat = (long)L * d_in_proj;
+  return scan_bwd(Q, K, pv, ADT, DT, Trap, Q_bias, K_bias, Angles, D, pz, dOut, dQ, dK, const_cast<char*>(gv),
+                  dADT, dDT, dTrap, dQ_bias, dK_bias, dAngles, dD, const_cast<char*>(gz), B, L, H, 1, N, P, R,
+                  chunk_size, io_dtype, ws, ws_bytes, stream, true, saved, saved_bytes, tok, bat, tok, bat);
 }
 
 int m3_layer_post(const void* y, const float* scale, void* out, int B, int L, int D, float eps, int io_dtype,
@@ -619,9 +670,11 @@ int m3_layer_pre_bwd(const void* proj, const float* dt_bias, const float* B_norm
     g_err[0] = '\0';
     return M3_OK;
   }
-  if (!proj || !dt_bias || !B_norm_scale || !C_norm_scale || !dQ || !dK || !dV || !dZ || !dADT || !dDT || !dTrap ||
+  if (!proj || !dt_bias || !B_norm_scale || !C_norm_scale || !dQ || !dK || !dADT || !dDT || !dTrap ||
       (R > 0 && !dAngles) || !d_proj || !d_dt_bias || !d_B_norm_scale || !d_C_norm_scale || !ws)
     return fail(M3_E_ARG, "NULL required pointer");
+  if ((dV == nullptr) != (dZ == nullptr))
+    return fail(M3_E_ARG, "pass dV and dZ together (both NULL: already in d_proj's x and z columns)");
   if (ws_bytes < m3_layer_pre_bwd_ws_bytes(B, L, H, N))
     return fail(M3_E_ARG, "workspace of %zu bytes, %zu needed", ws_bytes, m3_layer_pre_bwd_ws_bytes(B, L, H, N));
   m3::LayerPreBwdArgs a;

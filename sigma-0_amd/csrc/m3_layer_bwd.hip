@@ -8,8 +8,9 @@
 //                          scale's gradient sum_t dn y r as one partial row per workgroup
 //   layer_pre_bwd_kernel   d(proj) from the scan's gradients, one workgroup per tile of
 //                          kPreTile tokens of one batch row: dZ and dV into the z and x
-//                          columns and BCNorm's backward into B and C (one wave per token,
-//                          both rows' loads issued before their stores), the decay's chain
+//                          columns (unless m3_layer_scan_bwd wrote them there) and BCNorm's
+//                          backward into B and C (one wave per token, both rows' loads
+//                          issued before their stores), the decay's chain
 //                          rule into dd_dt and dd_A and dTrap into trap (lanes along the
 //                          tokens, one head per wave at a time), dAngles into the angle
 //                          columns; the norm scales' and dt_bias's gradients as one partial
@@ -182,8 +183,9 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
     const long row = row0 + i;
     T* dpr = dproj + (long)i * dp;
     const T* pr = proj + (long)i * dp;
-    copy_two_rows(dpr, reinterpret_cast<const T*>(a.dz) + row * di, dpr + di, reinterpret_cast<const T*>(a.dv) + row * di,
-                  di, lane);
+    if (a.dz)   // else the scan's backward wrote them there
+      copy_two_rows(dpr, reinterpret_cast<const T*>(a.dz) + row * di, dpr + di,
+                    reinterpret_cast<const T*>(a.dv) + row * di, di, lane);
     // n = m rsqrt(mean m^2 + eps) scale  (B: K's, C: Q's)
 #pragma unroll
     for (int side = 0; side < 2; ++side) {

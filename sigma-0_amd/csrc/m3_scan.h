@@ -38,7 +38,8 @@ struct ScanArgs {
   int ang_shared = 0;
   // Token and batch strides (elements) of V and Z when they are read in place from
   // wider rows (the mixer layer's input projection); 0: the contiguous (B, L, H, P)
-  // layout.  Honoured by the chunked kernel only; the output stays contiguous.
+  // layout.  Honoured by the chunked kernels and the backward; the output stays
+  // contiguous.
   long vz_tok = 0, vz_bat = 0;
   // With chunk_h (the training forward) and Z: the output before the gate, (B, L, H, P)
   // in the I/O type, which the backward multiplies into dZ instead of recomputing it
@@ -81,6 +82,10 @@ struct ScanBwd {
   void* dq; void* dk; void* dv; void* dz;              // io dtype; dz null without Z
   float* dadt; float* ddt; float* dtrap; float* dang;  // like ADT, DT, Trap, Angles
   float* dqb; float* dkb; float* dD;                   // (H, N), (H, N), (H,) or null
+  // Token and batch strides (elements) of dV and dZ when they are written into wider
+  // rows (the mixer layer's in_proj gradient); 0: the contiguous (B, L, H, P) layout.
+  // V and Z are read with fwd.vz_tok / fwd.vz_bat.
+  long dvz_tok = 0, dvz_bat = 0;
 };
 bool scan_bwd_supported(bool bf16_io, int N, int P, int R);
 // saved: the chunk states come from the training forward (no state-only pass)
@@ -136,7 +141,7 @@ struct LayerPreBwdArgs {
   const void* proj;                                     // (B, L, 2HP + 2N + 3H + R) io
   const float* dt_bias; const float* b_scale; const float* c_scale;
   const void* dq; const void* dk;                       // d(normalised C), d(normalised B): (B, L, N) io
-  const void* dv; const void* dz;                       // (B, L, H, P) io
+  const void* dv; const void* dz;                       // (B, L, H, P) io, or both null: in dproj already
   const float* dadt; const float* ddt; const float* dtrap;   // (B, H, L)
   const float* dang;                                    // (B, L, R)
   void* dproj;                                          // like proj

@@ -185,6 +185,11 @@ struct BwdArgs {
   float* gin = nullptr;        // [bh][nseg][P][N] adjoint entering each segment from the right
   float* gloc = nullptr;       // [bh][nseg * adj_sub][P][N] each sub-segment's own adjoint
   float* dseg = nullptr;       // [bh][nseg * adj_sub] each sub-segment's total log-decay
+  // Rows of V and Z (s.vz_tok, s.vz_bat) and of dV and dZ (dvz_tok, dvz_bat): element
+  // offset b * bat + t * tok + h * P.  The launcher sets both, to the contiguous
+  // (B, L, H, P) layout's L H P and H P where the caller gives none.  dOut and the
+  // saved output before the gate stay contiguous.
+  long dvz_tok = 0, dvz_bat = 0;
 };
 
 // Per-chunk token constants shared by the adjoint and gradient kernels: lane = token.
@@ -287,14 +292,13 @@ struct AdjLoads {
         th[k] = *reinterpret_cast<const float4*>(a.th0 + ((long)bh * a.nc + c) * R + 4 * gr);
       }
     }
-    const T* gdo = reinterpret_cast<const T*>(a.dout);
-    const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) : gdo;
+    const T* gdo = reinterpret_cast<const T*>(a.dout) + (((long)b * L + t) * H + h) * P;
+    const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) + a.s.vz_bat * b + a.s.vz_tok * t + (long)h * P : gdo;
 #pragma unroll
     for (int k = 0; k < GV; ++k) {
       const int g = min(wave + kBwdWaves * k, P / 8 - 1);
-      const long row = (((long)b * L + t) * H + h) * P + 8 * g;
-      dy[k].load(gdo + row);
-      z[k].load(gz + row);
+      dy[k].load(gdo + 8 * g);
+      z[k].load(gz + 8 * g);
     }
   }
 };
@@ -494,7 +498,8 @@ struct ItemLoads {
     const int L = a.s.L, H = a.s.H, HQ = a.s.Hqk, nc = a.nc, t0 = c * CS;
     const int tcl = min(t0 + lane, L - 1);
     const long qrow = (((long)b * L + tcl) * HQ + hq) * N;
-    const long vrow = (((long)b * L + tcl) * H + h) * P;
+    const long vrow = (((long)b * L + tcl) * H + h) * P;                 // dOut
+    const long vzrow = a.s.vz_bat * b + a.s.vz_tok * tcl + (long)h * P;    // V, Z
     const T* hsrc = reinterpret_cast<const T*>(a.hs) + ((long)bh * nc + c) * P * N;
     const T* gsrc = reinterpret_cast<const T*>(a.gs) + ((long)bh * nc + c) * N * P;
 #pragma unroll
@@ -520,9 +525,9 @@ struct ItemLoads {
 #pragma unroll
     for (int k = 0; k < VGW; ++k) {
       const int g = min(wave + k * kBwdWaves, P / 8 - 1);
-      vraw[k].load(gv + vrow + 8 * g);
+      vraw[k].load(gv + vzrow + 8 * g);
       dyraw[k].load(reinterpret_cast<const T*>(a.dout) + vrow + 8 * g);
-      zraw[k].load(gz + vrow + 8 * g);
+      zraw[k].load(gz + vzrow + 8 * g);
     }
   }
 };
@@ -721,7 +726,7 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * rt + 4 * (lane >> 4) + r;
         if (t0 + t < L) {
-          const long o = (((long)b * L + t0 + t) * H + h) * P + p;
+          const long o = a.dvz_bat * b + a.dvz_tok * (t0 + t) + (long)h * P + p;
           const float y = acc[r] + exp2_fast(sm.ac[t] * kLog2e) * acc2[r] +
                           (Dh + sm.gam[t] * sm.qk[t]) * (float)sm.v[t][p];
           reinterpret_cast<T*>(a.dz)[o] = (T)(y * (float)sm.fz[t][p]);
@@ -742,7 +747,7 @@ void scan_bwd_chunk_kernel(BwdArgs a) {
         if (t0 + s < L) {
           const float dv = acc[r] + exp2_fast((aend - sm.ac[s]) * kLog2e) * acc2[r] +
                            (Dh + sm.gam[s] * sm.qk[s]) * (float)sm.dy[s][p];
-          reinterpret_cast<T*>(a.dv)[(((long)b * L + t0 + s) * H + h) * P + p] = (T)dv;
+          reinterpret_cast<T*>(a.dv)[a.dvz_bat * b + a.dvz_tok * (t0 + s) + (long)h * P + p] = (T)dv;
         }
       }
     }
@@ -979,15 +984,18 @@ struct WalkLoads {
         kpc[k].load(reinterpret_cast<const T*>(a.s.k) + row);
       }
     } else if constexpr (PART == 2) {
-      const T* gv = reinterpret_cast<const T*>(a.s.v);
-      const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) : gv;
+      const T* gv = reinterpret_cast<const T*>(a.s.v) + a.s.vz_bat * b + (long)h * P;
+      const T* gz = a.s.z ? reinterpret_cast<const T*>(a.s.z) + a.s.vz_bat * b + (long)h * P : gv;
 #pragma unroll
       for (int k = 0; k < VPT; ++k) {
         const int p = min(tid + k * kBwdThreads, CS * P / 8 - 1);
-        const long row = (((long)b * L + min(t0 + p / (P / 8), L - 1)) * H + h) * P + 8 * (p % (P / 8));
-        vpc[k].load(gv + row);
+        const long tk = min(t0 + p / (P / 8), L - 1);
+        const int col = 8 * (p % (P / 8));
+        const long row = (((long)b * L + tk) * H + h) * P + col;          // dOut, y_v
+        const long vzr = a.s.vz_tok * tk + col;                           // V, Z
+        vpc[k].load(gv + vzr);
         dypc[k].load(reinterpret_cast<const T*>(a.dout) + row);
-        zpc[k].load(gz + row);
+        zpc[k].load(gz + vzr);
         if constexpr (YV) ypc[k].load(reinterpret_cast<const T*>(a.yv) + row);
       }
     } else {
@@ -1465,7 +1473,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
               cur.ypc[k].to_f(yv);
 #pragma unroll
               for (int e = 0; e < 8; ++e) yv[e] *= fz[e];
-              store8(reinterpret_cast<T*>(a.dz) + (((long)b * L + t0 + row) * H + h) * P + 8 * pc, yv);
+              store8(reinterpret_cast<T*>(a.dz) + a.dvz_bat * b + a.dvz_tok * (t0 + row) + (long)h * P + 8 * pc, yv);
             }
           }
 #pragma unroll
@@ -1691,7 +1699,7 @@ void scan_bwd_walk_kernel(BwdArgs a) {
       for (int p = tid; p < 2 * CS * (P / 8); p += kBwdThreads) {
         const int w = p / (CS * (P / 8)), q = p % (CS * (P / 8)), row = q / (P / 8), pc = q % (P / 8);
         if (row < nt && (w == 1 || (gz && gdz && !YV))) {
-          const long o = (((long)b * L + t0 + row) * H + h) * P + 8 * pc;
+          const long o = a.dvz_bat * b + a.dvz_tok * (t0 + row) + (long)h * P + 8 * pc;
           *reinterpret_cast<Vec8<T>*>((w ? gdv : gdz) + o) =
               *reinterpret_cast<const Vec8<T>*>(sm.outs(w) + row * (P + PAD) + 8 * pc);
         }
@@ -2744,6 +2752,12 @@ hipError_t scan_bwd_launch(const ScanBwd& g, bool bf16_io, void* ws, hipStream_t
   BwdArgs a;
   a.s = s;
   a.s.CS = CS;
+  if (a.s.vz_tok == 0) {
+    a.s.vz_tok = (long)s.H * s.P;
+    a.s.vz_bat = (long)s.L * s.H * s.P;
+  }
+  a.dvz_tok = g.dvz_tok ? g.dvz_tok : (long)s.H * s.P;
+  a.dvz_bat = g.dvz_tok ? g.dvz_bat : (long)s.L * s.H * s.P;
   a.dout = g.dout;
   a.dq = g.dq; a.dk = g.dk; a.dv = g.dv; a.dz = g.dz;
   a.dadt = g.dadt; a.ddt = g.ddt; a.dtrap = g.dtrap;

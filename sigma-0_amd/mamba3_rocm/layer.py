@@ -13,10 +13,12 @@ x and z out of proj and the scan is m3_chunk_scan_fwd_shared on the copies.
 
 ``Mamba3Layer.train_forward`` is the same forward made differentiable (gradients for
 x and for every parameter, as autodiff of Mamba3SSM gives them).  Its scan is the
-shared training pair: m3_layer_pre copies x and z (the backward kernels read them
-contiguous) and m3_chunk_scan_fwd_train_shared saves the states entering every
-chunk, which m3_chunk_scan_bwd_saved_shared reads instead of recomputing them.  The
-backward is the library GEMMs' gradients, m3_layer_post_bwd (the output RMSNorm),
+training pair, which saves the states entering every chunk for the backward instead
+of recomputing them: m3_layer_scan_train (x and z read in place) and
+m3_layer_scan_bwd, which writes dV and dZ straight into the x and z columns of the
+in_proj output's gradient; where the rows do not allow that, m3_layer_pre copies x
+and z and the pair is m3_chunk_scan_fwd_train_shared / m3_chunk_scan_bwd_saved_shared.
+The backward is the library GEMMs' gradients, m3_layer_post_bwd (the output RMSNorm),
 the scan's backward and m3_layer_pre_bwd (BCNorm, the decay's chain rule with the
 A_floor clip, trap and angles, written into the in_proj output's gradient).
 
@@ -69,8 +71,8 @@ class Mamba3Layer:
         # the projections' operands in the compute dtype (nn.Dense(dtype=...) casts them)
         self.w_in = self.params["in_proj"].to(dtype).contiguous()
         self.w_out = self.params["out_proj"].to(dtype).contiguous()
-        # "in_place", "copies" or "train_pair" (train_forward: copies and the scan's
-        # training forward): how the last forward fed x and z to the scan
+        # "in_place" or "copies", prefixed "train_" for train_forward (the scan's training
+        # forward): how the last forward fed x and z to the scan
         self.last_scan = None
         self.last_compute_dtype = None   # the scan's operand dtype in the last forward
 
@@ -87,7 +89,7 @@ class Mamba3Layer:
 
     def _run(self, x: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor, keep: bool = False):
         """The forward; with ``keep`` (train_forward) also the intermediates the backward
-        reads, the scan then on copies of x and z with its residuals saved."""
+        reads, the scan's residuals among them."""
         unbatched = x.dim() == 2
         if unbatched:
             x = x[None]
@@ -119,20 +121,35 @@ class Mamba3Layer:
         # layer's (mamba3_pallas.py:112-122, 838-839): then the copies are cast to it.
         cdt = pallas_compute_dtype(dt)
         es = proj.element_size()
-        in_place = (not keep and cdt == dt and (self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
+        in_place = (cdt == dt and (self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
                     and proj.data_ptr() % 16 == 0
                     and lib.m3_chunk_scan_impl(io, N, hd, R, self.chunk_size) == _lib.IMPL_CHUNKED_MFMA)
-        self.last_scan = "in_place" if in_place else ("train_pair" if keep else "copies")
+        sbytes = 0
+        if keep and in_place:
+            # in place in training: the saved-state pair must exist for the shape (a
+            # backward kernel, and the forward's chunk a multiple of the backward's)
+            kbwd = 64 if io == _lib.DTYPE_BF16 else 32
+            if (self.chunk_size % kbwd == 0
+                    and lib.m3_chunk_scan_bwd_saved_shared_ws_bytes(B, L, nh, N, hd, R, self.chunk_size, io)):
+                sbytes = lib.m3_chunk_scan_saved_bytes(B, L, nh, N, hd, R, io)
+            in_place = sbytes > 0
+        self.last_scan = ("train_" if keep else "") + ("in_place" if in_place else "copies")
         self.last_compute_dtype = cdt
+        V = Z = scan_saved = None
         if in_place:
             pre(None, None)
             y = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
             ws_bytes = lib.m3_chunk_scan_ws_bytes(B, L, nh, N, hd, R, self.chunk_size, io)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-            _lib.check(lib.m3_layer_scan(_ptr(Q), _ptr(K), _ptr(proj), self.d_in_proj, _ptr(ADT), _ptr(DT),
-                                         _ptr(Trap), _ptr(Ang), _ptr(pp["C_bias"]), _ptr(pp["B_bias"]),
-                                         _ptr(pp["D"]), _ptr(y), B, L, nh, N, hd, R, self.chunk_size, io,
-                                         ws.data_ptr() if ws_bytes else None, ws_bytes, st), "m3_layer_scan")
+            args = (_ptr(Q), _ptr(K), _ptr(proj), self.d_in_proj, _ptr(ADT), _ptr(DT), _ptr(Trap), _ptr(Ang),
+                    _ptr(pp["C_bias"]), _ptr(pp["B_bias"]), _ptr(pp["D"]), _ptr(y), B, L, nh, N, hd, R,
+                    self.chunk_size, io)
+            wsa = (ws.data_ptr() if ws_bytes else None, ws_bytes, st)
+            if keep:
+                scan_saved = torch.empty(sbytes, dtype=torch.uint8, device=dev)
+                _lib.check(lib.m3_layer_scan_train(*args, scan_saved.data_ptr(), sbytes, *wsa), "m3_layer_scan_train")
+            else:
+                _lib.check(lib.m3_layer_scan(*args, *wsa), "m3_layer_scan")
         else:
             V = torch.empty(B, L, nh, hd, device=dev, dtype=dt)
             Z = torch.empty_like(V)
@@ -148,7 +165,7 @@ class Mamba3Layer:
                                      _stream(y)), "m3_layer_post")
         out = torch.matmul(yn, w_out)
         saved = (dict(xin=xin, proj=proj, Q=Q, K=K, V=V, Z=Z, ADT=ADT, DT=DT, Trap=Trap, Ang=Ang, y=y, yn=yn,
-                      cdt=cdt, scan=scan_saved) if keep else None)
+                      cdt=cdt, scan=scan_saved, in_place=in_place) if keep else None)
         return (out[0] if unbatched else out), saved
 
     def _backward(self, saved, dout: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor):
@@ -177,17 +194,34 @@ class Mamba3Layer:
                                          di, eps, io, ws.data_ptr(), ws.numel(), _stream(y)), "m3_layer_post_bwd")
         # the scan (Q = C, K = B shared over heads), from the training forward's residuals
         # (recomputed where the shape has none)
-        g = mamba3_ssd_chunked_shared_hip_bwd(saved["Q"], saved["K"], saved["V"], saved["ADT"], saved["DT"],
-                                              saved["Trap"], saved["Ang"], pp["C_bias"], pp["B_bias"], pp["D"],
-                                              saved["Z"], d_y.reshape(B, L, nh, hd), chunk_size=self.chunk_size,
-                                              saved=saved["scan"], compute_dtype=saved["cdt"])
-        dC, dB, dV, dADT, dDT, dTrap, dAng, g_C_bias, g_B_bias, g_D, dZ = g
-        # _preprocess (:203-268): BCNorm, the decay, trap and angles back to the in_proj output
         d_proj = torch.empty_like(proj)
+        if saved["in_place"]:
+            # dV and dZ straight into d_proj's x and z columns
+            dC, dB = torch.empty_like(saved["Q"]), torch.empty_like(saved["K"])
+            dADT, dDT, dTrap = (torch.empty(B, nh, L, **f32) for _ in range(3))
+            dAng = torch.empty(B, L, R, **f32)
+            g_C_bias, g_B_bias, g_D = torch.empty(nh, N, **f32), torch.empty(nh, N, **f32), torch.empty(nh, **f32)
+            sb = saved["scan"]
+            wsb = lib.m3_chunk_scan_bwd_saved_shared_ws_bytes(B, L, nh, N, hd, R, self.chunk_size, io)
+            ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+            _lib.check(lib.m3_layer_scan_bwd(
+                _ptr(saved["Q"]), _ptr(saved["K"]), _ptr(proj), self.d_in_proj, _ptr(saved["ADT"]), _ptr(saved["DT"]),
+                _ptr(saved["Trap"]), _ptr(saved["Ang"]), _ptr(pp["C_bias"]), _ptr(pp["B_bias"]), _ptr(pp["D"]),
+                _ptr(d_y), _ptr(dC), _ptr(dB), _ptr(d_proj), _ptr(dADT), _ptr(dDT), _ptr(dTrap), _ptr(g_C_bias),
+                _ptr(g_B_bias), _ptr(dAng), _ptr(g_D), B, L, nh, N, hd, R, self.chunk_size, io, sb.data_ptr(),
+                sb.numel(), ws.data_ptr(), wsb, _stream(proj)), "m3_layer_scan_bwd")
+            dV = dZ = None
+        else:
+            g = mamba3_ssd_chunked_shared_hip_bwd(saved["Q"], saved["K"], saved["V"], saved["ADT"], saved["DT"],
+                                                  saved["Trap"], saved["Ang"], pp["C_bias"], pp["B_bias"], pp["D"],
+                                                  saved["Z"], d_y.reshape(B, L, nh, hd), chunk_size=self.chunk_size,
+                                                  saved=saved["scan"], compute_dtype=saved["cdt"])
+            dC, dB, dV, dADT, dDT, dTrap, dAng, g_C_bias, g_B_bias, g_D, dZ = g
+            c = lambda t: t.to(dt).contiguous()  # noqa: E731
+            dC, dB, dV, dZ = c(dC), c(dB), c(dV), c(dZ)
+        # _preprocess (:203-268): BCNorm, the decay, trap and angles back to the in_proj output
         g_dt_bias, g_B_norm, g_C_norm = torch.empty(nh, **f32), torch.empty(N, **f32), torch.empty(N, **f32)
         ws = torch.empty(max(lib.m3_layer_pre_bwd_ws_bytes(B, L, nh, N), 16), dtype=torch.uint8, device=dev)
-        c = lambda t: t.to(dt).contiguous()  # noqa: E731
-        dC, dB, dV, dZ = c(dC), c(dB), c(dV), c(dZ)
         _lib.check(lib.m3_layer_pre_bwd(_ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]),
                                         _ptr(dC), _ptr(dB), _ptr(dV), _ptr(dZ), _ptr(dADT), _ptr(dDT), _ptr(dTrap),
                                         _ptr(dAng), _ptr(d_proj), _ptr(g_dt_bias), _ptr(g_B_norm), _ptr(g_C_norm),

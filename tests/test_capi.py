@@ -46,7 +46,8 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_bwd_saved", "m3_chunk_scan_fwd_train_shared",
                             "m3_chunk_scan_bwd_saved_shared_ws_bytes", "m3_chunk_scan_bwd_saved_shared",
                             "m3_decode_step", "m3_layer_pre",
-                            "m3_layer_scan", "m3_layer_post", "m3_layer_post_bwd_ws_bytes", "m3_layer_post_bwd",
+                            "m3_layer_scan", "m3_layer_scan_train", "m3_layer_scan_bwd", "m3_layer_post",
+                            "m3_layer_post_bwd_ws_bytes", "m3_layer_post_bwd",
                             "m3_layer_pre_bwd_ws_bytes", "m3_layer_pre_bwd", "m3_block_norm", "m3_block_gelu",
                             "m3_block_act", "m3_block_act_norm", "m3_log_softmax"])
     for n in names:
@@ -57,7 +58,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_constants(lib):
     from mamba3_rocm import _lib
-    assert lib.m3_abi_version() == 102
+    assert lib.m3_abi_version() == 103
     assert _lib.DTYPE_F32 == _header_define("M3_DTYPE_F32")
     assert _lib.DTYPE_BF16 == _header_define("M3_DTYPE_BF16")
     assert _lib.IMPL_CHUNKED_MFMA == _header_define("M3_IMPL_CHUNKED_MFMA")
@@ -463,6 +464,23 @@ def test_layer_scan_validation(lib):
     assert scan(None, full8, heads=8) == _lib.M3_E_ARG
     assert lib.m3_layer_pre(fake, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, fake,
                             2, 64, H, P, N, R, 1e-4, 1e-6, _lib.DTYPE_BF16, None) == _lib.M3_E_ARG
+    # the training pair in place: the same layout checks, for d_proj too, and the residuals
+    tr = lambda proj, d_in, saved, io=_lib.DTYPE_BF16, heads=H: lib.m3_layer_scan_train(  # noqa: E731
+        fake, fake, proj, d_in, fake, fake, fake, fake, fake, fake, fake, fake, 2, 64, heads, N, P, R, 64, io,
+        saved, 1 << 20, None, 0, None)
+    assert tr(fake, full, fake, io=7) == _lib.M3_E_ARG
+    assert tr(fake, full + 8, fake) == _lib.M3_E_ARG
+    assert tr(fake, full, fake) == _lib.M3_E_ALIGN
+    assert tr(fake, full8, None, heads=8) == _lib.M3_E_ARG and b"saved" in lib.m3_last_error()
+
+    def bw(proj, dproj, d_in, heads=H):
+        return lib.m3_layer_scan_bwd(fake, fake, proj, d_in, fake, fake, fake, fake, fake, fake, fake, fake,
+                                     fake, fake, dproj, fake, fake, fake, fake, fake, fake, fake,
+                                     2, 64, heads, N, P, R, 64, _lib.DTYPE_BF16, None, 0, fake, 1 << 30, None)
+    assert bw(fake, fake, full - 2) == _lib.M3_E_ARG
+    assert bw(fake, fake, full) == _lib.M3_E_ALIGN
+    assert bw(fake, None, full8, heads=8) == _lib.M3_E_ARG
+    assert bw(None, fake, full8, heads=8) == _lib.M3_E_ARG
 
 
 def test_layer_backward_entry_points_validate(lib):
@@ -510,6 +528,9 @@ def test_layer_backward_entry_points_validate(lib):
     assert pre(dang=None) == _lib.M3_E_ARG                         # R > 0 needs dAngles
     assert pre(w=None) == _lib.M3_E_ARG
     assert pre(wsb=wsp - 4) == _lib.M3_E_ARG and b"workspace" in lib.m3_last_error()
+    one_of = lib.m3_layer_pre_bwd(fake, fake, fake, fake, fake, fake, None, fake, fake, fake, fake, fake, fake,
+                                  fake, fake, fake, B, L, H, P, N, R, 1e-4, 1e-6, bf, fake, wsp, None)
+    assert one_of == _lib.M3_E_ARG and b"together" in lib.m3_last_error()
 
 
 def test_block_entry_points_validate(lib):

@@ -12,6 +12,9 @@
   input), every gradient within the reference's bf16 gradient bar of 1e-1
   (tests/integration/test_mamba3_pallas_gpu.py:66-69), relative in norm.  A
   difference quotient of the bf16 layer itself would measure its rounding steps.
+* The layer's in-place training pair (m3_layer_scan_train, m3_layer_scan_bwd: x and z
+  read from the projection rows, dV and dZ written into the gradient's rows) against
+  the contiguous pair on copies, bitwise: only the addressing differs.
 """
 import numpy as np
 import pytest
@@ -36,7 +39,7 @@ def _grads(p, x, g, d_model, N, headdim, dtype, path):
         assert layer.params[k] is params[k], "the layer keeps the caller's float32 parameters"
     xt = torch.from_numpy(x).cuda().requires_grad_(True)
     out = layer.train_forward(xt)
-    assert layer.last_scan == "train_pair"
+    assert layer.last_scan == "train_" + path
     (out.float() * torch.from_numpy(g).float().cuda()).sum().backward()
     torch.cuda.synchronize()
     # the differentiable forward is the layer's forward
@@ -107,3 +110,80 @@ def test_layer_backward_bf16_matches_f32(B, L, d_model, N, headdim, path):
           flush=True)
     bad = {k: v for k, v in errs.items() if v > 1e-1}
     assert not bad, f"bf16 gradients above 1e-1 of the float32 ones: {bad}"
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+@pytest.mark.parametrize("B,L,H,bf16", [
+    (2, 330, 8, True),      # 16 pairs, short: the chunk-parallel route
+    (1, 2100, 8, True),     # 8 pairs, long: the split walk and its adjoint pass
+    (4, 256, 64, True),     # 256 pairs: the one-segment walk
+    (2, 200, 4, False),     # float32 I/O (the saved output before the gate)
+])
+def test_layer_scan_pair_in_place_matches_contiguous(B, L, H, bf16):
+    import torch
+    from _util import I
+    from mamba3_rocm import _lib, mamba3_ssd_chunked_shared_hip_bwd, mamba3_ssd_chunked_shared_hip_fwd_train
+    N, P, R, CS = 128, 64, 32, 64
+    dt = torch.bfloat16 if bf16 else torch.float32
+    io = _lib.DTYPE_BF16 if bf16 else _lib.DTYPE_F32
+    d = I.scan_inputs(B, L, H, N, P, R, seed=71, Hqk=1, bf16=bf16)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")  # noqa: E731
+    Q, K = dev(d["Q"][:, :, 0]).to(dt), dev(d["K"][:, :, 0]).to(dt)
+    V, Z = dev(d["V"]).to(dt), dev(d["Z"]).to(dt)
+    ADT, DT, Trap, Qb, Kb, D = (dev(d[k]) for k in ("ADT", "DT", "Trap", "Q_bias", "K_bias", "D"))
+    Ang = dev(d["Angles"][:, :, 0])
+    width = 2 * H * P + 2 * N + 3 * H + R
+    rng = np.random.default_rng(72)
+    proj = dev(rng.standard_normal((B, L, width)).astype(np.float32)).to(dt)
+    proj[..., :H * P] = Z.reshape(B, L, H * P)
+    proj[..., H * P:2 * H * P] = V.reshape(B, L, H * P)
+    dout = dev(rng.standard_normal((B, L, H, P)).astype(np.float32)).to(dt)
+    print(f"case layer scan pair in place {(B, L, H)} bf16={bf16}", flush=True)
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    args = (Q, K, V, ADT, DT, Trap, Ang, Qb, Kb, D, Z)
+
+    # forward with residuals
+    out_c, saved_c = mamba3_ssd_chunked_shared_hip_fwd_train(*args, chunk_size=CS)
+    assert saved_c is not None
+    out_i = torch.empty_like(out_c)
+    saved_i = torch.empty_like(saved_c)
+    wsb = lib.m3_chunk_scan_ws_bytes(B, L, H, N, P, R, CS, io)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+    _lib.check(lib.m3_layer_scan_train(_ptr(Q), _ptr(K), _ptr(proj), width, _ptr(ADT), _ptr(DT), _ptr(Trap),
+                                       _ptr(Ang), _ptr(Qb), _ptr(Kb), _ptr(D), _ptr(out_i), B, L, H, N, P, R, CS, io,
+                                       _ptr(saved_i), saved_i.numel(), ws.data_ptr() if wsb else None, wsb, st),
+               "m3_layer_scan_train")
+    torch.cuda.synchronize()
+    assert torch.equal(out_i, out_c), "in-place training forward output"
+    assert torch.equal(saved_i, saved_c), "in-place training forward residuals"
+
+    names = ("Q", "K", "V", "ADT", "DT", "Trap", "Angles", "Q_bias", "K_bias", "D", "Z")
+    f32 = dict(device="cuda", dtype=torch.float32)
+    for with_saved in (True, False):
+        ref = dict(zip(names, mamba3_ssd_chunked_shared_hip_bwd(*args, dout, chunk_size=CS,
+                                                                saved=saved_c if with_saved else None)))
+        g = dict(Q=torch.empty_like(Q), K=torch.empty_like(K), ADT=torch.empty(B, H, L, **f32),
+                 DT=torch.empty(B, H, L, **f32), Trap=torch.empty(B, H, L, **f32), Angles=torch.empty(B, L, R, **f32),
+                 Q_bias=torch.empty(H, N, **f32), K_bias=torch.empty(H, N, **f32), D=torch.empty(H, **f32))
+        d_proj = torch.full_like(proj, 7.0)
+        if with_saved:
+            wsb = lib.m3_chunk_scan_bwd_saved_shared_ws_bytes(B, L, H, N, P, R, CS, io)
+        else:
+            wsb = lib.m3_chunk_scan_bwd_shared_ws_bytes(B, L, H, N, P, R, CS, io)
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        _lib.check(lib.m3_layer_scan_bwd(
+            _ptr(Q), _ptr(K), _ptr(proj), width, _ptr(ADT), _ptr(DT), _ptr(Trap), _ptr(Ang), _ptr(Qb), _ptr(Kb),
+            _ptr(D), _ptr(dout), _ptr(g["Q"]), _ptr(g["K"]), _ptr(d_proj), _ptr(g["ADT"]), _ptr(g["DT"]),
+            _ptr(g["Trap"]), _ptr(g["Q_bias"]), _ptr(g["K_bias"]), _ptr(g["Angles"]), _ptr(g["D"]),
+            B, L, H, N, P, R, CS, io, _ptr(saved_c) if with_saved else None, saved_c.numel() if with_saved else 0,
+            ws.data_ptr(), wsb, st), "m3_layer_scan_bwd")
+        torch.cuda.synchronize()
+        g["Z"] = d_proj[..., :H * P].reshape(B, L, H, P)
+        g["V"] = d_proj[..., H * P:2 * H * P].reshape(B, L, H, P)
+        for k in names:
+            assert torch.equal(g[k], ref[k].reshape(g[k].shape)), f"d{k} (saved={with_saved})"
+        assert bool((d_proj[..., 2 * H * P:] == 7.0).all()), "columns past x written"
