@@ -28,6 +28,7 @@ constexpr int kBwdElThreads = 256;
 constexpr int kPostTok = 16;            // tokens per workgroup, layer_post_bwd
 constexpr int kPreTile = 64;            // tokens per workgroup, layer_pre_bwd (one per lane)
 constexpr int kPreThreads = 512;        // layer_pre_bwd's workgroup: eight waves
+constexpr int kPreHG = 32;              // layer_pre_bwd: heads per LDS-staged group
 constexpr int kPostChunks = kLayerPostBwdMaxD / (64 * 8);   // 8-element chunks per lane, at most
 constexpr int kPreCols = kLayerPreBwdMaxN / 64;             // B / C columns per lane
 constexpr int kReduceSlices = 16;                           // row slices of the partial sums
@@ -161,6 +162,8 @@ __global__ __launch_bounds__(kPreThreads)
 void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
   constexpr int kW = kPreThreads / 64;
   __shared__ float red[kW][2][kLayerPreBwdMaxN];
+  __shared__ float sdd[kPreTile][2 * kPreHG + 1];     // a head group's dd_dt, dd_A per token
+  __shared__ float sgo[kPreTile][3 * kPreHG + 1];     // and their gradients, with trap's
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tiles = (a.L + kPreTile - 1) / kPreTile;
   const int b = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * kPreTile;
@@ -186,18 +189,30 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
     if (a.dz)   // else the scan's backward wrote them there
       copy_two_rows(dpr, reinterpret_cast<const T*>(a.dz) + row * di, dpr + di,
                     reinterpret_cast<const T*>(a.dv) + row * di, di, lane);
-    // n = m rsqrt(mean m^2 + eps) scale  (B: K's, C: Q's)
+    // n = m rsqrt(mean m^2 + eps) scale  (B: K's, C: Q's).  Both sides' rows are loaded
+    // before either side's stores (which could alias them as far as the compiler knows).
+    float mv[2][kPreCols], dnv[2][kPreCols];
 #pragma unroll
     for (int side = 0; side < 2; ++side) {
       const T* g = reinterpret_cast<const T*>(side ? a.dq : a.dk) + row * N;
-      const float* scale = side ? a.c_scale : a.b_scale;
       const int o = side ? oC : oB;
-      float m[kPreCols], dn[kPreCols], ds[kPreCols], ss = 0.0f, sd = 0.0f;
 #pragma unroll
       for (int k = 0; k < kPreCols; ++k) {
         const int n = lane + 64 * k;
-        m[k] = n < N ? Elem<T>::to_f(pr[o + n]) : 0.0f;
-        dn[k] = n < N ? Elem<T>::to_f(g[n]) : 0.0f;
+        mv[side][k] = n < N ? Elem<T>::to_f(pr[o + n]) : 0.0f;
+        dnv[side][k] = n < N ? Elem<T>::to_f(g[n]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      const float* scale = side ? a.c_scale : a.b_scale;
+      const int o = side ? oC : oB;
+      const float* m = mv[side];
+      const float* dn = dnv[side];
+      float ds[kPreCols], ss = 0.0f, sd = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kPreCols; ++k) {
+        const int n = lane + 64 * k;
         ds[k] = n < N ? dn[k] * scale[n] : 0.0f;
         ss += m[k] * m[k];
         sd += ds[k] * m[k];
@@ -220,28 +235,45 @@ void layer_pre_bwd_kernel(LayerPreBwdArgs a) {
     }
   }
   // ---- lanes along the tokens, one head per wave at a time: DT = softplus(dd_dt +
-  // dt_bias), A = min(-softplus(dd_A), -A_floor), ADT = A DT; trap passes through
-  for (int h = wave; h < H; h += kW) {
-    float du = 0.0f;
-    if (lane < nt) {
-      const long hl = ((long)b * H + h) * a.L + t0 + lane;
-      const float dadt = a.dadt[hl], ddt = a.ddt[hl], dtrap = a.dtrap[hl];
-      const T* pr = proj + (long)lane * dp;
-      const float u = Elem<T>::to_f(pr[oT + h]) + a.dt_bias[h];
-      const float ddA = Elem<T>::to_f(pr[oT + H + h]);
-      const float DTv = softplus_f(u), sp = softplus_f(ddA);
-      const float A = fminf(-sp, -a.A_floor);
-      du = (ddt + dadt * A) * (1.0f / (1.0f + expf(-u)));
-      // the clip passes the gradient below -A_floor, half of it on a tie (jax's min)
-      const float gate = -sp < -a.A_floor ? 1.0f : (-sp == -a.A_floor ? 0.5f : 0.0f);
-      const float dA = -(dadt * DTv) * gate * (1.0f / (1.0f + expf(-ddA)));
-      T* dpr = dproj + (long)lane * dp;
-      dpr[oT + h] = Elem<T>::from_f(du);
-      dpr[oT + H + h] = Elem<T>::from_f(dA);
-      dpr[oT + 2 * H + h] = Elem<T>::from_f(dtrap);
+  // dt_bias), A = min(-softplus(dd_A), -A_floor), ADT = A DT; trap passes through.  The
+  // heads go in groups of kPreHG: the group's dd_dt and dd_A columns come in through
+  // LDS and its three gradient columns go out through LDS, as row pieces.
+  for (int h0 = 0; h0 < H; h0 += kPreHG) {
+    const int hg = H - h0 < kPreHG ? H - h0 : kPreHG;
+    __syncthreads();   // the previous group's sdd reads and sgo stores are done
+    for (int e = tid; e < nt * 2 * hg; e += kPreThreads) {
+      const int i = e / (2 * hg), j = e - i * 2 * hg;
+      const int col = j < hg ? oT + h0 + j : oT + H + h0 + (j - hg);
+      sdd[i][j] = Elem<T>::to_f(proj[(long)i * dp + col]);
     }
-    du = group_sum<64>(du);
-    if (lane == 0) part[2 * N + h] = du;
+    __syncthreads();
+    for (int hl = wave; hl < hg; hl += kW) {
+      const int h = h0 + hl;
+      float du = 0.0f;
+      if (lane < nt) {
+        const long hi = ((long)b * H + h) * a.L + t0 + lane;
+        const float dadt = a.dadt[hi], ddt = a.ddt[hi], dtrap = a.dtrap[hi];
+        const float u = sdd[lane][hl] + a.dt_bias[h];
+        const float ddA = sdd[lane][hg + hl];
+        const float DTv = softplus_f(u), sp = softplus_f(ddA);
+        const float A = fminf(-sp, -a.A_floor);
+        du = (ddt + dadt * A) * (1.0f / (1.0f + expf(-u)));
+        // the clip passes the gradient below -A_floor, half of it on a tie (jax's min)
+        const float gate = -sp < -a.A_floor ? 1.0f : (-sp == -a.A_floor ? 0.5f : 0.0f);
+        const float dA = -(dadt * DTv) * gate * (1.0f / (1.0f + expf(-ddA)));
+        sgo[lane][hl] = du;
+        sgo[lane][hg + hl] = dA;
+        sgo[lane][2 * hg + hl] = dtrap;
+      }
+      du = group_sum<64>(du);
+      if (lane == 0) part[2 * N + h] = du;
+    }
+    __syncthreads();
+    for (int e = tid; e < nt * 3 * hg; e += kPreThreads) {
+      const int i = e / (3 * hg), j = e - i * 3 * hg;
+      const int q = j / hg, jj = j - q * hg;           // 0: dd_dt, 1: dd_A, 2: trap
+      dproj[(long)i * dp + oT + q * H + h0 + jj] = Elem<T>::from_f(sgo[i][j]);
+    }
   }
   // ---- the angle rates' gradients into their columns
   for (int e = tid; e < nt * R; e += kPreThreads) {
