@@ -120,7 +120,9 @@ def _ptr(t):
     (2, 330, 8, True),      # 16 pairs, short: the chunk-parallel route
     (1, 2100, 8, True),     # 8 pairs, long: the split walk and its adjoint pass
     (4, 256, 64, True),     # 256 pairs: the one-segment walk
-    (2, 200, 4, False),     # float32 I/O (the saved output before the gate)
+    (2, 200, 4, False),     # float32 I/O, the chunk-parallel route
+    (1, 2100, 8, False),    # float32, the split walk (dZ from the saved output before the gate)
+    (4, 256, 64, False),    # float32, the one-segment walk
 ])
 def test_layer_scan_pair_in_place_matches_contiguous(B, L, H, bf16):
     import torch
