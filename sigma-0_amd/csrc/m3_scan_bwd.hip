@@ -317,6 +317,7 @@ void scan_adjoint_kernel(BwdArgs a) {
   __shared__ S sm;
   constexpr int PAD = S::PAD, KS = W::KSTEP;
   constexpr int NTILE = (P / 16) * (N / 16), TPW = (NTILE + kBwdWaves - 1) / kBwdWaves;
+  static_assert(R % 4 == 0, "rope pairs in whole 8-column groups");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh = blockIdx.x, h = bh % a.s.H;
@@ -370,11 +371,16 @@ void scan_adjoint_kernel(BwdArgs a) {
         for (int j = 0; j < 4; ++j) th4[j] = 0.0f;
         if constexpr (R > 0) {
           if (4 * g < R) {
+            // R is a multiple of 4: the group's four pairs all rotate; their angle
+            // prefixes advance side by side
             const float rv[4] = {cur.rt[k].x, cur.rt[k].y, cur.rt[k].z, cur.rt[k].w};
             const float t0c[4] = {cur.th[k].x, cur.th[k].y, cur.th[k].z, cur.th[k].w};
+            float st[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (4 * g + j < R) th4[j] = __builtin_amdgcn_fractf(t0c[j] + wave_incl_scan(angle_step(rv[j], dtl)));
+            for (int j = 0; j < 4; ++j) st[j] = angle_step(rv[j], dtl);
+            wave_incl_scan4(st);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) th4[j] = __builtin_amdgcn_fractf(t0c[j] + st[j]);
           }
         }
 #pragma unroll
@@ -383,7 +389,8 @@ void scan_adjoint_kernel(BwdArgs a) {
         if (lane < CS) store8(&sm.qt[lane][8 * g], q);
       }
     }
-    const float ea = tok ? expf(acum) : 0.0f;
+    // the decay and gate factors with the walk's arithmetic
+    const float ea = tok ? exp2_fast(acum * kLog2e) : 0.0f;
 #pragma unroll
     for (int k = 0; k < Loads::GV; ++k) {
       const int g = wave + kBwdWaves * k;
@@ -393,7 +400,7 @@ void scan_adjoint_kernel(BwdArgs a) {
         cur.z[k].to_f(z);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          if (has_z) dy[e] *= z[e] / (1.0f + expf(-z[e]));
+          if (has_z) dy[e] *= z[e] * sigmoid_fast(z[e]);
           dy[e] *= ea;
         }
         if (lane < CS) store8(&sm.dye[lane][8 * g], dy);
@@ -403,7 +410,7 @@ void scan_adjoint_kernel(BwdArgs a) {
     if (c > c_lo) cur.issue(a, c - 1, bh, wave, lane);
     __syncthreads();
     // G <- e^{A_end} G + sum_t e^{A_cum,t} dy_t (x) q~_t
-    const float dec = expf(aend);
+    const float dec = exp2_fast(aend * kLog2e);
     logdec += aend;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
