@@ -190,6 +190,46 @@ int m3_block_act_norm(const void* y, const void* h1, const void* h2, const float
  */
 int m3_log_softmax(const float* x, float* out, int B, int L, int V, void* stream);
 
+/*
+ * The backbone's backward around the mixer, as autodiff of SequenceLayer.__call__
+ * (layers.py:108-160) and of the head's log_softmax (lob_seq_model.py:530-542) gives
+ * it, in float32 arithmetic; the forward's roundings to io_dtype pass gradients
+ * unchanged.  The Dense layers' gradients are library GEMMs between these calls.
+ *
+ * m3_block_act_bwd: from d_out (B, L, D) float32, the gradient of the activation's
+ * output (the residual stream's gradient), and y, h1, h2 as m3_block_act read them:
+ * with s = sigmoid(h2) rounded to io_dtype, dh2 = d_out u s (1 - s), u = h1
+ * (full_glu), gelu(y) rounded (half_glu1) or y (half_glu2), and dd = d_out s, the
+ * gradient of that other factor (h1, gelu(y), y); gelu: dd = d_out gelu'(y) is the
+ * mixer output's gradient and dh2 is not written.  dh2, dd (B, L, D) in io_dtype.
+ *
+ * m3_block_gelu_bwd: after the GEMMs that give dg, the gradient of gelu(y) through the
+ * Dense layers (full_glu: both): dy = (dg + dd) gelu'(y) (half_glu1), dg gelu'(y)
+ * (full_glu, dd unused), dg gelu'(y) + dd (half_glu2).  All (B, L, D) io_dtype.
+ *
+ * m3_block_norm_bwd: LayerNorm's backward (eps as the forward's) from its float32
+ * input x (B, L, D), scale (D,) and the output's gradient d_norm (B, L, D, io_dtype):
+ * dx = d_res + the LayerNorm's input gradient (float32; d_res may be NULL), and the
+ * scale's and bias's gradients (D,) float32, summed over the tokens in a fixed order
+ * through the workspace of m3_block_norm_bwd_ws_bytes.  D a multiple of 4, at most
+ * 2048 (M3_E_UNSUPPORTED otherwise); pointers 16-byte aligned (M3_E_ALIGN).
+ *
+ * m3_log_softmax_nll: per token, loss = logsumexp(z) - z[target] (float32, B*L
+ * values) and, in place over the float32 logits z (B, L, V), the gradient of
+ * weight * sum(loss): (softmax(z) - onehot(target)) * weight.  targets (B, L) int32;
+ * one outside [0, V) gives a NaN loss and no one-hot term.
+ */
+int m3_block_act_bwd(const float* d_out, const void* y, const void* h1, const void* h2, void* dh2, void* dd, int B,
+                     int L, int D, int activation, int io_dtype, void* stream);
+int m3_block_gelu_bwd(const void* dg, const void* dd, const void* y, void* dy, int B, int L, int D, int activation,
+                      int io_dtype, void* stream);
+size_t m3_block_norm_bwd_ws_bytes(int B, int L, int D);
+int m3_block_norm_bwd(const float* x, const float* scale, const void* d_norm, const float* d_res, float* dx,
+                      float* d_scale, float* d_bias, int B, int L, int D, float eps, int io_dtype, void* ws,
+                      size_t ws_bytes, void* stream);
+int m3_log_softmax_nll(float* logits, const int* targets, float* loss, int B, int L, int V, float weight,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

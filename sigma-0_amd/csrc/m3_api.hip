@@ -53,7 +53,7 @@ bool decode_supported(int N, int P, int R) {
 
 extern "C" {
 
-int m3_abi_version(void) { return 103; }
+int m3_abi_version(void) { return 104; }
 
 const char* m3_last_error(void) { return g_err; }
 
@@ -774,6 +774,92 @@ int m3_block_act(const void* y, const void* h1, const void* h2, const float* ski
   a.y = y; a.h1 = h1; a.h2 = h2; a.skip = skip; a.out = out; a.n = (long)B * L * D; a.act = activation;
   return check_launch(m3::block_elt_launch(a, false, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
                       "block activation");
+}
+
+int m3_block_act_bwd(const float* d_out, const void* y, const void* h1, const void* h2, void* dh2, void* dd, int B,
+                     int L, int D, int activation, int io_dtype, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (activation < M3_ACT_GELU || activation > M3_ACT_HALF_GLU2)
+    return fail(M3_E_ARG, "activation must be one of M3_ACT_GELU..M3_ACT_HALF_GLU2, got %d", activation);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!d_out || !y || !dd) return fail(M3_E_ARG, "NULL required pointer");
+  if (activation == M3_ACT_FULL_GLU && !h1) return fail(M3_E_ARG, "full_glu needs h1 (the out1 Dense output)");
+  if (activation != M3_ACT_GELU && (!h2 || !dh2))
+    return fail(M3_E_ARG, "the GLU activations need h2 and dh2 (the out2 Dense output and its gradient)");
+  m3::BlockBwdArgs a{};
+  a.da = d_out; a.y = y; a.h1 = activation == M3_ACT_FULL_GLU ? h1 : nullptr;
+  a.h2 = activation != M3_ACT_GELU ? h2 : nullptr; a.dh2 = activation != M3_ACT_GELU ? dh2 : nullptr;
+  a.dd = dd; a.n = (long)B * L * D; a.act = activation;
+  return check_launch(m3::block_act_bwd_launch(a, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "block activation backward");
+}
+
+int m3_block_gelu_bwd(const void* dg, const void* dd, const void* y, void* dy, int B, int L, int D, int activation,
+                      int io_dtype, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (activation < M3_ACT_FULL_GLU || activation > M3_ACT_HALF_GLU2)
+    return fail(M3_E_ARG, "the gelu backward follows a GLU activation (M3_ACT_FULL_GLU..M3_ACT_HALF_GLU2), got %d",
+                activation);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!dg || !y || !dy || (activation != M3_ACT_FULL_GLU && !dd)) return fail(M3_E_ARG, "NULL required pointer");
+  m3::BlockBwdArgs a{};
+  a.dg = dg; a.dd_in = activation != M3_ACT_FULL_GLU ? dd : nullptr; a.y = y; a.dy = dy;
+  a.n = (long)B * L * D; a.act = activation;
+  return check_launch(m3::block_gelu_bwd_launch(a, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
+                      "block gelu backward");
+}
+
+size_t m3_block_norm_bwd_ws_bytes(int B, int L, int D) {
+  if (B <= 0 || L <= 0 || D <= 0) return 0;
+  return (size_t)m3::block_norm_bwd_parts((long)B * L) * 2 * D * sizeof(float);
+}
+
+int m3_block_norm_bwd(const float* x, const float* scale, const void* d_norm, const float* d_res, float* dx,
+                      float* d_scale, float* d_bias, int B, int L, int D, float eps, int io_dtype, void* ws,
+                      size_t ws_bytes, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (B < 0 || L < 0 || D <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d D=%d)", B, L, D);
+  if (D % 4 != 0 || D > m3::kBlockNormBwdMaxD)
+    return fail(M3_E_UNSUPPORTED, "D=%d: the LayerNorm backward takes multiples of 4 up to %d", D,
+                m3::kBlockNormBwdMaxD);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!x || !scale || !d_norm || !dx || !d_scale || !d_bias || !ws) return fail(M3_E_ARG, "NULL required pointer");
+  if (ws_bytes < m3_block_norm_bwd_ws_bytes(B, L, D))
+    return fail(M3_E_ARG, "workspace of %zu bytes, %zu needed", ws_bytes, m3_block_norm_bwd_ws_bytes(B, L, D));
+  if (!aligned16(x) || !aligned16(scale) || !aligned16(d_norm) || (d_res && !aligned16(d_res)) || !aligned16(dx) ||
+      !aligned16(ws))
+    return fail(M3_E_ALIGN, "x, scale, d_norm, d_res, dx and ws must be 16-byte aligned");
+  m3::BlockNormBwdArgs a;
+  a.x = x; a.scale = scale; a.dn = d_norm; a.dres = d_res; a.dx = dx; a.part = reinterpret_cast<float*>(ws);
+  a.rows = (long)B * L; a.D = D; a.eps = eps;
+  return check_launch(m3::block_norm_bwd_launch(a, d_scale, d_bias, io_dtype == M3_DTYPE_BF16,
+                                                reinterpret_cast<hipStream_t>(stream)), "LayerNorm backward");
+}
+
+int m3_log_softmax_nll(float* logits, const int* targets, float* loss, int B, int L, int V, float weight,
+                       void* stream) {
+  if (B < 0 || L < 0 || V <= 0) return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d V=%d)", B, L, V);
+  if (B == 0 || L == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!logits || !targets || !loss) return fail(M3_E_ARG, "NULL required pointer");
+  return check_launch(m3::nll_launch(logits, targets, loss, (long)B * L, V, weight,
+                                     reinterpret_cast<hipStream_t>(stream)), "log_softmax NLL");
 }
 
 }  // extern "C"

@@ -14,6 +14,28 @@
 //                      layer rounds it, then out = skip + that, in float32.
 // All three read and write each element once: HBM-bound, one wave per row for
 // the norm (its statistics), eight elements per lane for the elementwise pair.
+//
+// Their backward, and that of the per-token head's log_softmax with the tokens'
+// negative log-likelihood, as autodiff of the same code gives it, in float32
+// arithmetic (the forward's roundings to the compute dtype pass gradients unchanged;
+// the rounded values are the operands):
+//   block_act_bwd_kernel   from da, the gradient of the block's output (float32, the
+//                          residual stream's): with s = sigmoid(h2) rounded as the
+//                          forward rounds it, dh2 = da u s (1 - s), u the gated factor
+//                          (h1, gelu(y) rounded, y), and dd = da s, the gradient of the
+//                          other factor (full_glu: h1; half_glu1: gelu(y); half_glu2:
+//                          y); gelu: dd = da gelu'(y), which is dy
+//   block_gelu_bwd_kernel  dy = (dg + [half_glu1] dd) gelu'(y) + [half_glu2] dd, with dg
+//                          the Dense layers' input gradient (library GEMMs)
+//   block_norm_bwd_kernel  LayerNorm's backward from its float32 input x, one wave per
+//                          row, kNormBwdRows rows per workgroup: dx = dres + rs (w -
+//                          mean(w) - xh mean(w xh)), w = dn scale, xh = (x - mean) rs;
+//                          the scale's and bias's gradients (sums of dn xh and dn) as one
+//                          partial row per workgroup, its waves' sums added in LDS in
+//                          wave order, then summed over the rows in a fixed order
+//   nll_kernel             one wave per token (lob_seq_model.py:530-542's log_softmax):
+//                          loss = logsumexp(z) - z[target], and in place dz =
+//                          (softmax(z) - onehot(target)) w
 #include "../../include/mamba3_layer.h"
 #include "m3_scan.h"
 
@@ -324,6 +346,248 @@ void log_softmax_kernel(const float* x, float* out, long rows, int V, int vec) {
   }
 }
 
+// d/dx of gelu_tanh: x s(u2), u2 = 2 sqrt(2/pi) (x + k x^3), gives s + x s (1 - s) u2'
+// with u2' = 2 sqrt(2/pi) (1 + 3 k x^2).
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  const float c = 1.5957691216057308f;
+  const float s = __builtin_amdgcn_rcpf(1.0f + __expf(-c * fmaf(0.044715f * x * x, x, x)));
+  return fmaf(x * s * (1.0f - s), c * fmaf(3.0f * 0.044715f * x, x, 1.0f), s);
+}
+
+template <typename T>
+__device__ __forceinline__ void act_bwd(int act, float da, float y, float h1, float h2, float& dh2, float& dd) {
+  if (act == M3_ACT_GELU) {
+    dh2 = 0.0f;
+    dd = da * gelu_tanh_grad(y);
+    return;
+  }
+  const float s = rnd<T>(sigmoid_f(h2));
+  const float u = act == M3_ACT_FULL_GLU ? h1 : (act == M3_ACT_HALF_GLU1 ? rnd<T>(gelu_tanh(y)) : y);
+  dh2 = da * u * (s * (1.0f - s));
+  dd = da * s;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlockThreads)
+void block_act_bwd_kernel(BlockBwdArgs a) {
+  const long i = (long)blockIdx.x * kBlockThreads + threadIdx.x;
+  const T* y = reinterpret_cast<const T*>(a.y);
+  const T* h1 = reinterpret_cast<const T*>(a.h1);
+  const T* h2 = reinterpret_cast<const T*>(a.h2);
+  T* dh2 = reinterpret_cast<T*>(a.dh2);
+  T* dd = reinterpret_cast<T*>(a.dd);
+  const int act = a.act;
+  if (a.vec) {
+    if (8 * i >= a.n) return;
+    float da[8], fy[8], f1[8] = {}, f2[8] = {}, o2[8], od[8];
+    Vec8<float> d;
+    d.load(a.da + 8 * i);
+    d.to_f(da);
+    Vec8<T> v;
+    v.load(y + 8 * i);
+    v.to_f(fy);
+    if (act == M3_ACT_FULL_GLU) {
+      v.load(h1 + 8 * i);
+      v.to_f(f1);
+    }
+    if (act != M3_ACT_GELU) {
+      v.load(h2 + 8 * i);
+      v.to_f(f2);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) act_bwd<T>(act, da[e], fy[e], f1[e], f2[e], o2[e], od[e]);
+    if (act != M3_ACT_GELU) store8(dh2 + 8 * i, o2);
+    store8(dd + 8 * i, od);
+  } else if (i < a.n) {
+    const float f1 = act == M3_ACT_FULL_GLU ? Elem<T>::to_f(h1[i]) : 0.0f;
+    const float f2 = act != M3_ACT_GELU ? Elem<T>::to_f(h2[i]) : 0.0f;
+    float o2, od;
+    act_bwd<T>(act, a.da[i], Elem<T>::to_f(y[i]), f1, f2, o2, od);
+    if (act != M3_ACT_GELU) dh2[i] = Elem<T>::from_f(o2);
+    dd[i] = Elem<T>::from_f(od);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlockThreads)
+void block_gelu_bwd_kernel(BlockBwdArgs a) {
+  const long i = (long)blockIdx.x * kBlockThreads + threadIdx.x;
+  const T* dg = reinterpret_cast<const T*>(a.dg);
+  const T* dd = reinterpret_cast<const T*>(a.dd_in);
+  const T* y = reinterpret_cast<const T*>(a.y);
+  T* dy = reinterpret_cast<T*>(a.dy);
+  const float kg = a.act == M3_ACT_HALF_GLU1 ? 1.0f : 0.0f, ky = a.act == M3_ACT_HALF_GLU2 ? 1.0f : 0.0f;
+  const bool use_dd = kg != 0.0f || ky != 0.0f;
+  if (a.vec) {
+    if (8 * i >= a.n) return;
+    float fg[8], fd[8] = {}, fy[8], o[8];
+    Vec8<T> v;
+    v.load(dg + 8 * i);
+    v.to_f(fg);
+    if (use_dd) {
+      v.load(dd + 8 * i);
+      v.to_f(fd);
+    }
+    v.load(y + 8 * i);
+    v.to_f(fy);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = fmaf(fmaf(kg, fd[e], fg[e]), gelu_tanh_grad(fy[e]), ky * fd[e]);
+    store8(dy + 8 * i, o);
+  } else if (i < a.n) {
+    const float fd = use_dd ? Elem<T>::to_f(dd[i]) : 0.0f;
+    dy[i] = Elem<T>::from_f(fmaf(fmaf(kg, fd, Elem<T>::to_f(dg[i])), gelu_tanh_grad(Elem<T>::to_f(y[i])), ky * fd));
+  }
+}
+
+constexpr int kNormBwdRows = 16;          // rows per workgroup, block_norm_bwd
+
+// CH: float4 pieces per lane, ceil(D / 256).  Dynamic LDS: 4 waves x 2 x D floats.
+template <typename T, int CH>
+__global__ __launch_bounds__(kBlockThreads)
+void block_norm_bwd_kernel(BlockNormBwdArgs a) {
+  extern __shared__ float red[];              // [wave][2][D]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int D = a.D, n4 = D / 4;
+  const float inv_d = 1.0f / (float)D;
+  const long r0 = (long)blockIdx.x * kNormBwdRows;
+  const long r1 = r0 + kNormBwdRows < a.rows ? r0 + kNormBwdRows : a.rows;
+  float sc[CH][4], as[CH][4], ab[CH][4];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int i = lane + 64 * k;
+    const float4 v = i < n4 ? reinterpret_cast<const float4*>(a.scale)[i] : make_float4(0, 0, 0, 0);
+    sc[k][0] = v.x; sc[k][1] = v.y; sc[k][2] = v.z; sc[k][3] = v.w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) as[k][j] = ab[k][j] = 0.0f;
+  }
+  for (long r = r0 + wave; r < r1; r += kBlockThreads / 64) {
+    const float* xr = a.x + r * D;
+    const T* dnr = reinterpret_cast<const T*>(a.dn) + r * D;
+    float xv[CH][4], dn[CH][4];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int i = lane + 64 * k;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[k][j] = dn[k][j] = 0.0f;
+      if (i < n4) {
+        load4<float>(xr + 4 * i, xv[k]);
+        load4<T>(dnr + 4 * i, dn[k]);
+      }
+      s += (xv[k][0] + xv[k][1]) + (xv[k][2] + xv[k][3]);
+    }
+    const float mean = group_sum<64>(s) * inv_d;
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+      if (lane + 64 * k < n4)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss += (xv[k][j] - mean) * (xv[k][j] - mean);
+    const float rs = rsqrtf(group_sum<64>(ss) * inv_d + a.eps);
+    float sw = 0.0f, swx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xv[k][j] = (xv[k][j] - mean) * rs;      // xh (0 past D: dn is 0 there)
+        const float w = dn[k][j] * sc[k][j];
+        sw += w;
+        swx += w * xv[k][j];
+        as[k][j] += dn[k][j] * xv[k][j];
+        ab[k][j] += dn[k][j];
+      }
+    sw = group_sum<64>(sw) * inv_d;
+    swx = group_sum<64>(swx) * inv_d;
+    float* dxr = a.dx + r * D;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int i = lane + 64 * k;
+      if (i < n4) {
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (a.dres) load4<float>(a.dres + r * D + 4 * i, o);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] += rs * (dn[k][j] * sc[k][j] - sw - xv[k][j] * swx);
+        store4<float>(dxr + 4 * i, o);
+      }
+    }
+  }
+  // the workgroup's partial row: [scale | bias], the waves' sums added in wave order
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int i = lane + 64 * k;
+    if (i < n4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[(2 * wave) * D + 4 * i + j] = as[k][j];
+        red[(2 * wave + 1) * D + 4 * i + j] = ab[k][j];
+      }
+  }
+  __syncthreads();
+  float* part = a.part + (long)blockIdx.x * 2 * D;
+  for (int c = threadIdx.x; c < 2 * D; c += kBlockThreads) {
+    const int side = c / D, col = c - side * D;
+    part[c] = ((red[side * D + col] + red[(2 + side) * D + col]) + red[(4 + side) * D + col]) +
+              red[(6 + side) * D + col];
+  }
+}
+
+// One wave per row; the vector path (V a multiple of 4, at most 64 * 4 * kSoftmaxVec,
+// 16-byte rows) keeps the row in registers, otherwise three passes over memory.
+__global__ __launch_bounds__(kBlockThreads)
+void nll_kernel(float* z, const int* targets, float* loss, long rows, int V, float w, int vec) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long row = (long)blockIdx.x * (kBlockThreads / 64) + wave;
+  if (row >= rows) return;                             // whole waves only: no barrier below
+  float* zr = z + row * V;
+  const int t = targets[row];
+  const bool ok = t >= 0 && t < V;
+  const float zt = ok ? zr[t] : NAN;                   // read before the row is overwritten
+  auto wave_max = [](float m) {
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    return m;
+  };
+  if (vec) {
+    const int n4 = V / 4;
+    float4 v[kSoftmaxVec];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kSoftmaxVec; ++k) {
+      const int i = lane + 64 * k;
+      v[k] = i < n4 ? reinterpret_cast<const float4*>(zr)[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kSoftmaxVec; ++k)
+      if (lane + 64 * k < n4) s += (expf(v[k].x - m) + expf(v[k].y - m)) + (expf(v[k].z - m) + expf(v[k].w - m));
+    const float lse = m + logf(group_sum<64>(s));
+#pragma unroll
+    for (int k = 0; k < kSoftmaxVec; ++k) {
+      const int i = lane + 64 * k;
+      if (i < n4) {
+        float4 o = make_float4(expf(v[k].x - lse) * w, expf(v[k].y - lse) * w, expf(v[k].z - lse) * w,
+                               expf(v[k].w - lse) * w);
+        if (ok && t / 4 == i) {
+          const int j = t % 4;
+          if (j == 0) o.x -= w; else if (j == 1) o.y -= w; else if (j == 2) o.z -= w; else o.w -= w;
+        }
+        reinterpret_cast<float4*>(zr)[i] = o;
+      }
+    }
+    if (lane == 0) loss[row] = lse - zt;
+  } else {
+    float m = -INFINITY;
+    for (int i = lane; i < V; i += 64) m = fmaxf(m, zr[i]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int i = lane; i < V; i += 64) s += expf(zr[i] - m);
+    const float lse = m + logf(group_sum<64>(s));
+    for (int i = lane; i < V; i += 64) zr[i] = expf(zr[i] - lse) * w - (ok && i == t ? w : 0.0f);
+    if (lane == 0) loss[row] = lse - zt;
+  }
+}
+
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -368,6 +632,55 @@ hipError_t block_elt_launch(BlockEltArgs a, bool gelu_only, bool bf16_io, hipStr
     if (bf16_io) hipLaunchKernelGGL(block_act_kernel<bf16>, grid, dim3(kBlockThreads), 0, st, a);
     else hipLaunchKernelGGL(block_act_kernel<float>, grid, dim3(kBlockThreads), 0, st, a);
   }
+  return hipGetLastError();
+}
+
+hipError_t block_act_bwd_launch(BlockBwdArgs a, bool bf16_io, hipStream_t st) {
+  a.vec = a.n % 8 == 0 && al16(a.da) && al16(a.y) && al16(a.dd) && (!a.h1 || al16(a.h1)) && (!a.h2 || al16(a.h2)) &&
+          (!a.dh2 || al16(a.dh2));
+  const long lanes = a.vec ? a.n / 8 : a.n;
+  const dim3 grid((unsigned)((lanes + kBlockThreads - 1) / kBlockThreads));
+  if (bf16_io) hipLaunchKernelGGL(block_act_bwd_kernel<bf16>, grid, dim3(kBlockThreads), 0, st, a);
+  else hipLaunchKernelGGL(block_act_bwd_kernel<float>, grid, dim3(kBlockThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t block_gelu_bwd_launch(BlockBwdArgs a, bool bf16_io, hipStream_t st) {
+  a.vec = a.n % 8 == 0 && al16(a.dg) && al16(a.y) && al16(a.dy) && (!a.dd_in || al16(a.dd_in));
+  const long lanes = a.vec ? a.n / 8 : a.n;
+  const dim3 grid((unsigned)((lanes + kBlockThreads - 1) / kBlockThreads));
+  if (bf16_io) hipLaunchKernelGGL(block_gelu_bwd_kernel<bf16>, grid, dim3(kBlockThreads), 0, st, a);
+  else hipLaunchKernelGGL(block_gelu_bwd_kernel<float>, grid, dim3(kBlockThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+long block_norm_bwd_parts(long rows) { return (rows + kNormBwdRows - 1) / kNormBwdRows + kReduceSlices; }
+
+hipError_t block_norm_bwd_launch(const BlockNormBwdArgs& a, float* dscale, float* dbias, bool bf16_io,
+                                 hipStream_t st) {
+  const long blocks = block_norm_bwd_parts(a.rows) - kReduceSlices;
+  const int ch = (a.D / 4 + 63) / 64;
+  const size_t lds = (size_t)(kBlockThreads / 64) * 2 * a.D * sizeof(float);
+#define M3_NORM_BWD(CH)                                                                                            \
+  if (ch == CH) {                                                                                                  \
+    if (bf16_io) hipLaunchKernelGGL((block_norm_bwd_kernel<bf16, CH>), dim3((unsigned)blocks), dim3(kBlockThreads), \
+                                    lds, st, a);                                                                   \
+    else hipLaunchKernelGGL((block_norm_bwd_kernel<float, CH>), dim3((unsigned)blocks), dim3(kBlockThreads), lds,  \
+                            st, a);                                                                                \
+  }
+  M3_NORM_BWD(1) M3_NORM_BWD(2) M3_NORM_BWD(3) M3_NORM_BWD(4)
+  M3_NORM_BWD(5) M3_NORM_BWD(6) M3_NORM_BWD(7) M3_NORM_BWD(8)
+#undef M3_NORM_BWD
+  static_assert(kBlockNormBwdMaxD == 64 * 4 * 8, "block_norm_bwd instantiations");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return reduce_rows(a.part, blocks, 2 * a.D, a.part + blocks * 2 * a.D, dscale, a.D, dbias, a.D, nullptr, st);
+}
+
+hipError_t nll_launch(float* z, const int* targets, float* loss, long rows, int V, float w, hipStream_t st) {
+  const int vec = V % 4 == 0 && V <= 64 * 4 * kSoftmaxVec && al16(z);
+  const dim3 grid((unsigned)((rows + kBlockThreads / 64 - 1) / (kBlockThreads / 64)));
+  hipLaunchKernelGGL(nll_kernel, grid, dim3(kBlockThreads), 0, st, z, targets, loss, rows, V, w, vec);
   return hipGetLastError();
 }
 

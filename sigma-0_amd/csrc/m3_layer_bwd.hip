@@ -31,7 +31,6 @@ constexpr int kPreThreads = 512;        // layer_pre_bwd's workgroup: eight wave
 constexpr int kPreHG = 32;              // layer_pre_bwd: heads per LDS-staged group
 constexpr int kPostChunks = kLayerPostBwdMaxD / (64 * 8);   // 8-element chunks per lane, at most
 constexpr int kPreCols = kLayerPreBwdMaxN / 64;             // B / C columns per lane
-constexpr int kReduceSlices = 16;                           // row slices of the partial sums
 
 __device__ __forceinline__ float softplus_f(float x) {     // as layer_pre: logaddexp(x, 0)
   return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
@@ -327,6 +326,8 @@ void reduce_final_kernel(const float* mid, int cols, float* out0, int n0, float*
   else out2[c - n0 - n1] = s;
 }
 
+}  // namespace
+
 hipError_t reduce_rows(const float* part, long rows, int cols, float* mid, float* out0, int n0, float* out1, int n1,
                        float* out2, hipStream_t st) {
   hipLaunchKernelGGL(reduce_slices_kernel, dim3((cols + 63) / 64, kReduceSlices), dim3(kBwdElThreads), 0, st, part,
@@ -337,8 +338,6 @@ hipError_t reduce_rows(const float* part, long rows, int cols, float* mid, float
                      st, mid, cols, out0, n0, out1, n1, out2);
   return hipGetLastError();
 }
-
-}  // namespace
 
 long layer_post_bwd_parts(int B, int L) { return ((long)B * L + kPostTok - 1) / kPostTok + kReduceSlices; }
 long layer_pre_bwd_parts(int B, int L) { return (long)B * ((L + kPreTile - 1) / kPreTile) + kReduceSlices; }

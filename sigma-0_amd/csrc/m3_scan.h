@@ -151,6 +151,12 @@ struct LayerPreBwdArgs {
 };
 long layer_post_bwd_parts(int B, int L);
 long layer_pre_bwd_parts(int B, int L);
+// Partial rows (float32, `rows` of `cols`) summed in a fixed order: kReduceSlices
+// slices of the rows side by side into mid (kReduceSlices rows of cols), then the
+// slices' sums; column c goes to out0 (c < n0), out1 (c < n0 + n1) or out2.
+constexpr int kReduceSlices = 16;
+hipError_t reduce_rows(const float* part, long rows, int cols, float* mid, float* out0, int n0, float* out1, int n1,
+                       float* out2, hipStream_t st);
 hipError_t layer_post_bwd_launch(const LayerPostBwdArgs& a, float* dscale, bool bf16_io, hipStream_t st);
 hipError_t layer_pre_bwd_launch(const LayerPreBwdArgs& a, float* d_b_scale, float* d_c_scale, float* d_dt_bias,
                                 bool bf16_io, hipStream_t st);
@@ -182,6 +188,39 @@ hipError_t block_norm_launch(BlockNormArgs a, bool bf16_out, hipStream_t st);
 hipError_t block_act_norm_launch(BlockActNormArgs a, bool bf16_io, bool bf16_ln, hipStream_t st);
 hipError_t log_softmax_launch(const float* x, float* out, long rows, int V, hipStream_t st);
 hipError_t block_elt_launch(BlockEltArgs a, bool gelu_only, bool bf16_io, hipStream_t st);
+
+// Their backward (m3_block.hip).  da: the gradient of the block's output (float32);
+// y, h1, h2 as the forward read them; the element kernels write dh2 and dd (the
+// gradient of the activation's other factor, or dy for gelu), then dy from the Dense
+// layers' input gradient dg.  `vec` is set by the launchers.
+struct BlockBwdArgs {
+  const float* da; const void* y; const void* h1; const void* h2;   // n elements each
+  const void* dg; const void* dd_in;                                // gelu backward's inputs
+  void* dh2; void* dd; void* dy;                                    // outputs
+  long n;
+  int act;   // M3_ACT_*
+  int vec;
+};
+// LayerNorm's backward from its float32 input x (rows, D), scale (D,), the output's
+// gradient dn (rows, D, io type) and the residual path's gradient dres (or null):
+// dx (rows, D) float32; the scale's and bias's gradients through `part`
+// (block_norm_bwd_parts rows of 2 D floats).
+constexpr int kBlockNormBwdMaxD = 2048;    // D a multiple of 4, at most this
+struct BlockNormBwdArgs {
+  const float* x; const float* scale; const void* dn; const float* dres;
+  float* dx; float* part;
+  long rows; int D;
+  float eps;
+};
+hipError_t block_act_bwd_launch(BlockBwdArgs a, bool bf16_io, hipStream_t st);
+hipError_t block_gelu_bwd_launch(BlockBwdArgs a, bool bf16_io, hipStream_t st);
+long block_norm_bwd_parts(long rows);
+hipError_t block_norm_bwd_launch(const BlockNormBwdArgs& a, float* dscale, float* dbias, bool bf16_io,
+                                 hipStream_t st);
+// log_softmax with each row's negative log-likelihood at its target: loss[row] =
+// logsumexp(z) - z[target] and, in place, z = (softmax(z) - onehot(target)) w.  A
+// target outside [0, V) gives a NaN loss and no one-hot term.
+hipError_t nll_launch(float* z, const int* targets, float* loss, long rows, int V, float w, hipStream_t st);
 
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS);

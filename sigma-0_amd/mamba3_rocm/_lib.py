@@ -36,7 +36,8 @@ EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_sc
            "m3_layer_post_bwd_ws_bytes", "m3_layer_post_bwd",
            "m3_layer_pre_bwd_ws_bytes", "m3_layer_pre_bwd",
            "m3_block_norm", "m3_block_gelu", "m3_block_act", "m3_block_act_norm",
-           "m3_log_softmax")
+           "m3_log_softmax", "m3_block_act_bwd", "m3_block_gelu_bwd", "m3_block_norm_bwd_ws_bytes",
+           "m3_block_norm_bwd", "m3_log_softmax_nll")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -75,6 +76,11 @@ _SIGS = {
     "m3_block_act": ([_P] * 5 + [_I] * 5 + [_P], _I),
     "m3_block_act_norm": ([_P] * 8 + [_I] * 3 + [ctypes.c_float] + [_I] * 3 + [_P], _I),
     "m3_log_softmax": ([_P] * 2 + [_I] * 3 + [_P], _I),
+    "m3_block_act_bwd": ([_P] * 6 + [_I] * 5 + [_P], _I),
+    "m3_block_gelu_bwd": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "m3_block_norm_bwd_ws_bytes": ([_I] * 3, ctypes.c_size_t),
+    "m3_block_norm_bwd": ([_P] * 7 + [_I] * 3 + [ctypes.c_float, _I, _P, ctypes.c_size_t, _P], _I),
+    "m3_log_softmax_nll": ([_P] * 3 + [_I] * 3 + [ctypes.c_float, _P], _I),
     "m3_decode_step": ([_P] * 16 + [_I] * 9 + [_P], _I),
 }
 

@@ -13,8 +13,15 @@ block's LayerNorm in one pass; postnorm: this block's).  The Dense layers are
 library GEMMs; the embedding lookup is torch's gather.
 ``logits`` adds the LOB models' per-token head (mode "none"): the decoder Dense
 on the float32 features (a library GEMM), then log_softmax in float32 with
-m3_log_softmax (lob_seq_model.py:530-542).
-Inference only (dropout is the identity).
+m3_log_softmax (lob_seq_model.py:530-542).  Dropout is the identity.
+``loss_and_grads`` is a training step's loss and gradients (prenorm stacks): the
+mean negative log-likelihood of target tokens under that head, and the gradient of
+every parameter as autodiff of the same model gives it.  The backward runs the
+hand-written kernels too: m3_log_softmax_nll (the head), m3_block_act_bwd and
+m3_block_gelu_bwd (the activation epilogue around the Dense layers' gradients,
+library GEMMs), the mixer's backward (Mamba3Layer) and m3_block_norm_bwd (the
+prenorm LayerNorm into the residual stream's gradient); the embedding's gradient is
+torch's index_add (its float32 sums over repeated tokens are not in a fixed order).
 """
 from __future__ import annotations
 
@@ -24,7 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .layer import Mamba3Layer
+from .layer import PARAM_NAMES, Mamba3Layer
 from .ops import _IO, _ptr, _stream
 
 ACTIVATIONS = ("gelu", "full_glu", "half_glu1", "half_glu2")
@@ -103,6 +110,110 @@ class Mamba3Stack:
         return x
 
     __call__ = forward
+
+    def loss_and_grads(self, ids: torch.Tensor, targets: torch.Tensor):
+        """Mean negative log-likelihood of ``targets`` (B, L) under the per-token head
+        (log_softmax of the decoder Dense on the features of ``ids``), and its
+        gradients, float32, in the layouts of the parameters the stack was built from
+        (flax Dense kernels (in, out)): a dict with embed, layers (per block: mixer
+        (Mamba3Layer's parameter names), ln_scale, ln_bias, out1_w, out1_b, out2_w,
+        out2_b), decoder_w, decoder_b.  Parameters unused by the activation get zero
+        gradients.  The weights are the compute-dtype copies taken when the stack was
+        built.  Returns (loss (0-d float32 tensor), grads)."""
+        if not self.prenorm:
+            raise NotImplementedError("loss_and_grads covers prenorm stacks")
+        if self.decoder_w is None:
+            raise ValueError("loss_and_grads needs decoder_w and decoder_b in the parameters")
+        lib, io, dt = _lib.load(), _IO[self.dtype], self.dtype
+        Bn, L = ids.shape
+        D, V = self.d_model, self.decoder_w.shape[0]
+        act = _ACT[self.activation]
+        x = self.embed[ids].contiguous()
+        st = _stream(x)
+        f32 = dict(device=x.device, dtype=torch.float32)
+        # ---- forward, keeping each block's intermediates
+        b0 = self.blocks[0]
+        xin = torch.empty(Bn, L, D, device=x.device, dtype=dt)
+        _lib.check(lib.m3_block_norm(_ptr(x), _ptr(b0["ln_scale"]), _ptr(b0["ln_bias"]), _ptr(xin), Bn, L, D, 1e-6, io,
+                                     st), "m3_block_norm")
+        saves = []
+        for i, b in enumerate(self.blocks):
+            mixer = b["mixer"]
+            y, msaved = mixer._run(xin, mixer.w_in, mixer.w_out, keep=True)
+            y = y.contiguous()
+            g = h1 = h2 = None
+            if self.activation != "gelu":
+                g = torch.empty_like(y)
+                _lib.check(lib.m3_block_gelu(_ptr(y), _ptr(g), Bn, L, D, io, st), "m3_block_gelu")
+                h2 = F.linear(g, b["out2_w"], b["out2_b"])
+                if self.activation == "full_glu":
+                    h1 = F.linear(g, b["out1_w"], b["out1_b"])
+            nxt = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
+            out = torch.empty_like(x)
+            xn = None
+            if nxt is None:
+                _lib.check(lib.m3_block_act(_ptr(y), _ptr(h1), _ptr(h2), _ptr(x), _ptr(out), Bn, L, D, act, io, st),
+                           "m3_block_act")
+            else:
+                xn = torch.empty(Bn, L, D, device=x.device, dtype=dt)
+                _lib.check(lib.m3_block_act_norm(_ptr(y), _ptr(h1), _ptr(h2), _ptr(x), _ptr(out),
+                                                 _ptr(nxt["ln_scale"]), _ptr(nxt["ln_bias"]), _ptr(xn), Bn, L, D,
+                                                 1e-6, act, io, io, st), "m3_block_act_norm")
+            saves.append(dict(x=x, y=y, g=g, h1=h1, h2=h2, m=msaved))
+            x, xin = out, xn
+        # ---- the head: loss and, in place, the logits' gradient
+        z = F.linear(x, self.decoder_w, self.decoder_b).contiguous()
+        tg = targets.to(device=z.device, dtype=torch.int32).contiguous()
+        if tuple(tg.shape) != (Bn, L):
+            raise ValueError(f"targets must be {(Bn, L)}, got {tuple(tg.shape)}")
+        rows = Bn * L
+        loss_rows = torch.empty(rows, **f32)
+        _lib.check(lib.m3_log_softmax_nll(_ptr(z), _ptr(tg), _ptr(loss_rows), Bn, L, V, 1.0 / rows, st),
+                   "m3_log_softmax_nll")
+        loss = loss_rows.sum() / rows
+        dz = z.reshape(rows, V)
+        grads = dict(decoder_w=x.reshape(rows, D).t() @ dz, decoder_b=dz.sum(0))
+        dres = (dz @ self.decoder_w).reshape(Bn, L, D)           # the features' gradient, float32
+        # ---- the blocks in reverse
+        layers = [None] * len(self.blocks)
+        for i in reversed(range(len(self.blocks))):
+            sv, b = saves[i], self.blocks[i]
+            y = sv["y"]
+            lg = dict(out1_w=torch.zeros(D, D, **f32), out1_b=torch.zeros(D, **f32),
+                      out2_w=torch.zeros(D, D, **f32), out2_b=torch.zeros(D, **f32))
+            dd = torch.empty_like(y)
+            dh2 = torch.empty_like(y) if self.activation != "gelu" else None
+            _lib.check(lib.m3_block_act_bwd(_ptr(dres), _ptr(y), _ptr(sv["h1"]), _ptr(sv["h2"]), _ptr(dh2), _ptr(dd),
+                                            Bn, L, D, act, io, st), "m3_block_act_bwd")
+            if self.activation == "gelu":
+                dy = dd
+            else:
+                g2 = sv["g"].reshape(rows, D)
+                dg = dh2 @ b["out2_w"]                            # F.linear's (out, in) kernel: dh2 W
+                lg["out2_w"] = (g2.t() @ dh2.reshape(rows, D)).float()
+                lg["out2_b"] = dh2.reshape(rows, D).float().sum(0)
+                if self.activation == "full_glu":
+                    dg = dg + dd @ b["out1_w"]
+                    lg["out1_w"] = (g2.t() @ dd.reshape(rows, D)).float()
+                    lg["out1_b"] = dd.reshape(rows, D).float().sum(0)
+                dy = torch.empty_like(y)
+                _lib.check(lib.m3_block_gelu_bwd(_ptr(dg.contiguous()), _ptr(dd), _ptr(y), _ptr(dy), Bn, L, D, act,
+                                                 io, st), "m3_block_gelu_bwd")
+            mixer = b["mixer"]
+            dxin, mgrads = mixer._backward(sv["m"], dy, mixer.w_in, mixer.w_out)
+            lg["mixer"] = dict(zip(PARAM_NAMES, mgrads))
+            # the prenorm LayerNorm, and the residual path
+            dx = torch.empty_like(sv["x"])
+            lg["ln_scale"], lg["ln_bias"] = torch.empty(D, **f32), torch.empty(D, **f32)
+            ws = torch.empty(max(lib.m3_block_norm_bwd_ws_bytes(Bn, L, D), 16), dtype=torch.uint8, device=x.device)
+            _lib.check(lib.m3_block_norm_bwd(_ptr(sv["x"]), _ptr(b["ln_scale"]), _ptr(dxin.contiguous()), _ptr(dres),
+                                             _ptr(dx), _ptr(lg["ln_scale"]), _ptr(lg["ln_bias"]), Bn, L, D, 1e-6,
+                                             io, ws.data_ptr(), ws.numel(), st), "m3_block_norm_bwd")
+            layers[i] = lg
+            dres = dx
+        grads["layers"] = layers
+        grads["embed"] = torch.zeros_like(self.embed).index_add_(0, ids.reshape(-1), dres.reshape(rows, D))
+        return loss, grads
 
     def logits(self, ids: torch.Tensor) -> torch.Tensor:
         """Per-token log-probabilities (B, L, vocab), float32."""
