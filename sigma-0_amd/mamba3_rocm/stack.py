@@ -191,11 +191,11 @@ class Mamba3Stack:
                 g2 = sv["g"].reshape(rows, D)
                 dg = dh2 @ b["out2_w"]                            # F.linear's (out, in) kernel: dh2 W
                 lg["out2_w"] = (g2.t() @ dh2.reshape(rows, D)).float()
-                lg["out2_b"] = dh2.reshape(rows, D).float().sum(0)
+                lg["out2_b"] = dh2.reshape(rows, D).sum(0, dtype=torch.float32)
                 if self.activation == "full_glu":
                     dg = dg + dd @ b["out1_w"]
                     lg["out1_w"] = (g2.t() @ dd.reshape(rows, D)).float()
-                    lg["out1_b"] = dd.reshape(rows, D).float().sum(0)
+                    lg["out1_b"] = dd.reshape(rows, D).sum(0, dtype=torch.float32)
                 dy = torch.empty_like(y)
                 _lib.check(lib.m3_block_gelu_bwd(_ptr(dg.contiguous()), _ptr(dd), _ptr(y), _ptr(dy), Bn, L, D, act,
                                                  io, st), "m3_block_gelu_bwd")
