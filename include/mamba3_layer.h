@@ -58,6 +58,21 @@ int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
                   int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
                   void* ws, size_t ws_bytes, void* stream);
 /*
+ * m3_layer_scan with the recurrent carry of m3_chunk_scan_fwd_carry (mamba3_scan.h):
+ * initial (theta, ssm, k, v) in, final out, each all four or none, float32 in the
+ * decode layout (theta (B,H,R) radians, ssm (B,H,P,N), k (B,H,N) the last token's
+ * biased and rotated key, v (B,H,P) its x).  A prefill whose final carry
+ * m3_decode_step continues token by token (Mamba3SSM.__call_rnn__,
+ * mamba3.py:466-568), or a prefill in pieces.
+ */
+int m3_layer_scan_carry(const void* Q, const void* K, const void* proj, int d_in_proj,
+                        const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                        const float* Q_bias, const float* K_bias, const float* D, void* Out,
+                        const float* init_theta, const float* init_ssm, const float* init_k, const float* init_v,
+                        float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                        int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                        void* ws, size_t ws_bytes, void* stream);
+/*
  * The layer's training pair with x and z in place: m3_chunk_scan_fwd_train_shared and
  * m3_chunk_scan_bwd_saved_shared of mamba3_scan.h (the fused path's chunk_scan_fwd_rule /
  * chunk_scan_bwd_rule, mamba3_pallas.py:602-645) with V and Z read from proj as

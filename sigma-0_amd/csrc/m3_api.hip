@@ -53,7 +53,7 @@ bool decode_supported(int N, int P, int R) {
 
 extern "C" {
 
-int m3_abi_version(void) { return 104; }
+int m3_abi_version(void) { return 105; }
 
 const char* m3_last_error(void) { return g_err; }
 
@@ -574,6 +574,21 @@ int m3_layer_scan(const void* Q, const void* K, const void* proj, int d_in_proj,
                   true, d_in_proj, (long)L * d_in_proj);
 }
 
+int m3_layer_scan_carry(const void* Q, const void* K, const void* proj, int d_in_proj,
+                        const float* ADT, const float* DT, const float* Trap, const float* Angles,
+                        const float* Q_bias, const float* K_bias, const float* D, void* Out,
+                        const float* init_theta, const float* init_ssm, const float* init_k, const float* init_v,
+                        float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
+                        int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
+                        void* ws, size_t ws_bytes, void* stream) {
+  const char *pz, *pv;
+  const int rc = layer_rows(proj, d_in_proj, H, N, P, R, io_dtype, &pz, &pv);
+  if (rc != M3_OK) return rc;
+  return scan_fwd(Q, K, pv, ADT, DT, Trap, Q_bias, K_bias, Angles, D, pz, Out, init_theta, init_ssm, init_k, init_v,
+                  fin_theta, fin_ssm, fin_k, fin_v, B, L, H, 1, N, P, R, chunk_size, io_dtype, ws, ws_bytes, stream,
+                  true, d_in_proj, (long)L * d_in_proj);
+}
+
 int m3_layer_scan_train(const void* Q, const void* K, const void* proj, int d_in_proj,
                         const float* ADT, const float* DT, const float* Trap, const float* Angles,
                         const float* Q_bias, const float* K_bias, const float* D, void* Out,
@@ -665,7 +680,8 @@ int m3_layer_pre_bwd(const void* proj, const float* dt_bias, const float* B_norm
     return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
   if (B < 0 || L < 0 || H <= 0 || P <= 0 || N <= 0 || R < 0)
     return fail(M3_E_ARG, "non-positive dimension (B=%d L=%d H=%d P=%d N=%d R=%d)", B, L, H, P, N, R);
-  if (N > m3::kLayerPreBwdMaxN) return fail(M3_E_UNSUPPORTED, "d_state %d above the backward's %d", N, m3::kLayerPreBwdMaxN);
+  if (N > m3::kLayerPreBwdMaxN)
+    return fail(M3_E_UNSUPPORTED, "d_state %d above the backward's %d", N, m3::kLayerPreBwdMaxN);
   if (B == 0 || L == 0) {
     g_err[0] = '\0';
     return M3_OK;

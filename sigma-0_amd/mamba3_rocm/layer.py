@@ -34,8 +34,9 @@ from typing import Dict
 import torch
 
 from . import _lib
-from .ops import (_IO, _ptr, _stream, mamba3_ssd_chunked_shared_hip, mamba3_ssd_chunked_shared_hip_bwd,
-                  mamba3_ssd_chunked_shared_hip_fwd_train, pallas_compute_dtype)
+from .ops import (_IO, _ptr, _stream, mamba3_siso_hip_carry, mamba3_ssd_chunked_shared_hip,
+                  mamba3_ssd_chunked_shared_hip_bwd, mamba3_ssd_chunked_shared_hip_fwd_train, new_carry,
+                  pallas_compute_dtype)
 
 PARAM_NAMES = ("in_proj", "dt_bias", "B_bias", "C_bias", "B_norm", "C_norm", "D", "out_norm", "out_proj")
 
@@ -80,6 +81,49 @@ class Mamba3Layer:
         """x (B, L, d_model) or (L, d_model) -> the same shape, in the compute dtype."""
         return self._run(x, self.w_in, self.w_out)[0]
 
+    def new_carry(self, batch: int, device=None):
+        """The zero recurrent carry of ``batch`` sequences: theta (B, H, R), ssm (B, H, P,
+        N), k (B, H, N), v (B, H, P), float32 (the reference's decode carry,
+        layers.py:243-256, without its singleton dims)."""
+        return new_carry(batch, self.nh, self.N, self.hd, self.R, device or self.w_in.device)
+
+    def prefill(self, x: torch.Tensor, carry=None):
+        """The forward on x (B, L, d_model) that also continues from a carry (or from
+        zero) and returns the carry after the last token, so that step() or another
+        prefill continues the sequences.  Returns (out, carry)."""
+        out, _, fin = self._run(x, self.w_in, self.w_out, init=carry, want_carry=True)
+        return out, fin
+
+    def step(self, x_t: torch.Tensor, carry):
+        """One token per sequence, as Mamba3SSM.__call_rnn__ runs it (mamba3.py:466-568):
+        x_t (B, d_model) -> (out (B, d_model) in the compute dtype, carry), the carry
+        updated in place.  The in_proj GEMM, m3_layer_pre on the token, m3_decode_step
+        (B and C shared over heads, trap through the sigmoid as the reference's
+        recurrent path applies it), m3_layer_post and the out_proj GEMM."""
+        from .decode import rnn_step_hip
+        Bn = x_t.shape[0]
+        dt, dev = self.dtype, x_t.device
+        nh, hd, N, R = self.nh, self.hd, self.N, self.R
+        lib, io, pp = _lib.load(), _IO[dt], self.params
+        proj = torch.matmul(x_t.to(dt).reshape(Bn, 1, self.d_model), self.w_in).contiguous()
+        Q = torch.empty(Bn, 1, N, device=dev, dtype=dt)
+        K = torch.empty_like(Q)
+        V = torch.empty(Bn, 1, nh, hd, device=dev, dtype=dt)
+        Z = torch.empty_like(V)
+        f32 = dict(device=dev, dtype=torch.float32)
+        ADT, DT, Trap = (torch.empty(Bn, nh, 1, **f32) for _ in range(3))
+        Ang = torch.empty(Bn, 1, R, **f32)
+        _lib.check(lib.m3_layer_pre(_ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]),
+                                    _ptr(Q), _ptr(K), _ptr(V), _ptr(Z), _ptr(ADT), _ptr(DT), _ptr(Trap), _ptr(Ang),
+                                    Bn, 1, nh, hd, N, R, self.A_floor, self.eps, io, _stream(proj)), "m3_layer_pre")
+        inputs = (V[:, 0], Z[:, 0], K.expand(Bn, nh, N), Q.expand(Bn, nh, N), ADT[..., 0], DT[..., 0],
+                  torch.sigmoid(Trap[..., 0]), Ang.expand(Bn, nh, R))
+        carry, y = rnn_step_hip(carry, inputs, pp["B_bias"], pp["C_bias"], pp["D"], out_dtype=dt)
+        yn = torch.empty(Bn, 1, self.d_inner, device=dev, dtype=dt)
+        _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), Bn, 1, self.d_inner, self.eps, io,
+                                     _stream(y)), "m3_layer_post")
+        return torch.matmul(yn, self.w_out).reshape(Bn, self.d_model), carry
+
     def train_forward(self, x: torch.Tensor) -> torch.Tensor:
         """forward, differentiable: gradients flow to x and to the parameter tensors the
         layer was built with (``self.params``, float32; those with requires_grad get
@@ -87,9 +131,14 @@ class Mamba3Layer:
         parameters at every call, so updates in place are seen."""
         return _LayerTrain.apply(self, x, *(self.params[k] for k in PARAM_NAMES))
 
-    def _run(self, x: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor, keep: bool = False):
+    def _run(self, x: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor, keep: bool = False, init=None,
+             want_carry: bool = False):
         """The forward; with ``keep`` (train_forward) also the intermediates the backward
-        reads, the scan's residuals among them."""
+        reads, the scan's residuals among them; with ``want_carry`` the scan continues
+        from ``init`` (or zero) and the carry after the last token is returned.
+        Returns (out, saved, carry)."""
+        if keep and want_carry:
+            raise ValueError("the training forward takes no carry")
         unbatched = x.dim() == 2
         if unbatched:
             x = x[None]
@@ -124,6 +173,15 @@ class Mamba3Layer:
         in_place = (cdt == dt and (self.d_in_proj * es) % 16 == 0 and (self.d_inner * es) % 16 == 0
                     and proj.data_ptr() % 16 == 0
                     and lib.m3_chunk_scan_impl(io, N, hd, R, self.chunk_size) == _lib.IMPL_CHUNKED_MFMA)
+        carry = None
+        if want_carry:
+            if init is not None:
+                init = tuple(t.to(torch.float32).contiguous() for t in init)
+                shapes = [(B, nh, R), (B, nh, hd, N), (B, nh, N), (B, nh, hd)]
+                for t, s_, n in zip(init, shapes, ("theta", "ssm", "k", "v")):
+                    if tuple(t.shape) != s_:
+                        raise ValueError(f"carry {n} must be {s_}, got {tuple(t.shape)}")
+            carry = new_carry(B, nh, N, hd, R, dev)
         sbytes = 0
         if keep and in_place:
             # in place in training: the saved-state pair must exist for the shape (a
@@ -148,6 +206,10 @@ class Mamba3Layer:
             if keep:
                 scan_saved = torch.empty(sbytes, dtype=torch.uint8, device=dev)
                 _lib.check(lib.m3_layer_scan_train(*args, scan_saved.data_ptr(), sbytes, *wsa), "m3_layer_scan_train")
+            elif want_carry:
+                cin = tuple(_ptr(t) for t in init) if init is not None else (None,) * 4
+                _lib.check(lib.m3_layer_scan_carry(*args[:12], *cin, *(_ptr(t) for t in carry), *args[12:], *wsa),
+                           "m3_layer_scan_carry")
             else:
                 _lib.check(lib.m3_layer_scan(*args, *wsa), "m3_layer_scan")
         else:
@@ -158,6 +220,14 @@ class Mamba3Layer:
             if keep:
                 y, scan_saved = mamba3_ssd_chunked_shared_hip_fwd_train(*scan_args, chunk_size=self.chunk_size,
                                                                         compute_dtype=cdt)
+            elif want_carry:
+                # the per-head carry contract with one Q/K head shared by all and the
+                # shared angle rates repeated over the heads
+                c = lambda t: t.to(cdt)  # noqa: E731
+                y, carry = mamba3_siso_hip_carry(c(Q)[:, :, None], c(K)[:, :, None], c(V), ADT, DT, Trap,
+                                                 pp["C_bias"], pp["B_bias"], Ang[:, :, None].expand(B, L, nh, R),
+                                                 pp["D"], c(Z), chunk_size=self.chunk_size, initial_carry=init)
+                y = y.to(dt)
             else:
                 y = mamba3_ssd_chunked_shared_hip(*scan_args, chunk_size=self.chunk_size, compute_dtype=cdt)
         yn = torch.empty(B, L, self.d_inner, device=dev, dtype=dt)
@@ -166,7 +236,7 @@ class Mamba3Layer:
         out = torch.matmul(yn, w_out)
         saved = (dict(xin=xin, proj=proj, Q=Q, K=K, V=V, Z=Z, ADT=ADT, DT=DT, Trap=Trap, Ang=Ang, y=y, yn=yn,
                       cdt=cdt, scan=scan_saved, in_place=in_place) if keep else None)
-        return (out[0] if unbatched else out), saved
+        return (out[0] if unbatched else out), saved, carry
 
     def _backward(self, saved, dout: torch.Tensor, w_in: torch.Tensor, w_out: torch.Tensor):
         """Gradients of x and of the parameters (PARAM_NAMES order, float32) from the
@@ -246,7 +316,7 @@ class _LayerTrain(torch.autograd.Function):
         w_in = params[PARAM_NAMES.index("in_proj")].to(layer.dtype).contiguous()
         w_out = params[PARAM_NAMES.index("out_proj")].to(layer.dtype).contiguous()
         unbatched = x.dim() == 2
-        out, saved = layer._run(x, w_in, w_out, keep=True)
+        out, saved, _ = layer._run(x, w_in, w_out, keep=True)
         ctx.layer, ctx.saved, ctx.w = layer, saved, (w_in, w_out)
         ctx.unbatched, ctx.x_dtype = unbatched, x.dtype
         return out

@@ -62,14 +62,16 @@ class Mamba3Stack:
             self.decoder_w = params["decoder_w"].float().t().contiguous()
             self.decoder_b = params["decoder_b"].float().contiguous()
 
-    def _block(self, b, x, xin, nxt):
+    def _block(self, b, x, xin, nxt, mixer=None):
         """SequenceLayer.__call__ (layers.py:108-160) on the float32 residual x (B, L, D).
         Prenorm: xin is this block's normalised input, made by the previous block's
         epilogue (or by m3_block_norm for the first block), and the epilogue makes the
-        next block's (nxt) the same way.  Returns (residual, next block's input)."""
+        next block's (nxt) the same way.  ``mixer`` replaces the mixer's forward (the
+        prefill and the decode step).  Returns (residual, next block's input)."""
         lib, io, st = _lib.load(), _IO[self.dtype], _stream(x)
         Bn, L, D = x.shape
-        y = b["mixer"](xin if self.prenorm else x).contiguous()     # compute dtype
+        mixer = mixer or b["mixer"]
+        y = mixer(xin if self.prenorm else x).contiguous()         # compute dtype
         h1 = h2 = None
         if self.activation != "gelu":
             g = torch.empty_like(y)
@@ -95,7 +97,9 @@ class Mamba3Stack:
                    "m3_block_act_norm")
         return out, None
 
-    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+    def forward(self, ids: torch.Tensor, mixers=None) -> torch.Tensor:
+        """Features (B, L, d_model) float32 of token ids (B, L); ``mixers`` (one per
+        block) replace the mixers' forward."""
         x = self.embed[ids].contiguous()
         xin = None
         if self.prenorm and self.blocks:
@@ -106,8 +110,47 @@ class Mamba3Stack:
                                                  _stream(x)), "m3_block_norm")
         for i, b in enumerate(self.blocks):
             nxt = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
-            x, xin = self._block(b, x, xin, nxt)
+            x, xin = self._block(b, x, xin, nxt, mixers[i] if mixers else None)
         return x
+
+    def _head(self, x: torch.Tensor) -> torch.Tensor:
+        """log_softmax of the decoder Dense on float32 features (..., d_model)."""
+        if self.decoder_w is None:
+            raise ValueError("the head needs decoder_w and decoder_b in the parameters")
+        z = F.linear(x, self.decoder_w, self.decoder_b).contiguous()
+        rows = z.numel() // z.shape[-1]
+        _lib.check(_lib.load().m3_log_softmax(_ptr(z), _ptr(z), 1, rows, z.shape[-1], _stream(z)), "m3_log_softmax")
+        return z
+
+    def prefill(self, ids: torch.Tensor, state=None):
+        """Per-token log-probabilities (B, L, vocab) of ids (B, L), continuing each
+        block's recurrent carry from ``state`` (a list, one carry per block; None:
+        from zero), and the state after the last token, for step() or another prefill
+        (the LOB models' generation: prefill, then one token at a time)."""
+        new_state = []
+
+        def prefill_mixer(i):
+            def run(t):
+                out, carry = self.blocks[i]["mixer"].prefill(t, state[i] if state else None)
+                new_state.append(carry)
+                return out
+            return run
+        x = self.forward(ids, mixers=[prefill_mixer(i) for i in range(len(self.blocks))])
+        return self._head(x), new_state
+
+    def step(self, ids_t: torch.Tensor, state):
+        """One token per sequence: ids_t (B,) -> (log-probabilities (B, vocab), state),
+        every block's mixer through its decode step (Mamba3Layer.step), the carries
+        in ``state`` updated in place."""
+        Bn = ids_t.shape[0]
+
+        def step_mixer(i):
+            def run(t):
+                out, _ = self.blocks[i]["mixer"].step(t.reshape(Bn, self.d_model), state[i])
+                return out.reshape(Bn, 1, self.d_model)
+            return run
+        x = self.forward(ids_t.reshape(Bn, 1), mixers=[step_mixer(i) for i in range(len(self.blocks))])
+        return self._head(x)[:, 0], state
 
     __call__ = forward
 
@@ -139,7 +182,7 @@ class Mamba3Stack:
         saves = []
         for i, b in enumerate(self.blocks):
             mixer = b["mixer"]
-            y, msaved = mixer._run(xin, mixer.w_in, mixer.w_out, keep=True)
+            y, msaved, _ = mixer._run(xin, mixer.w_in, mixer.w_out, keep=True)
             y = y.contiguous()
             g = h1 = h2 = None
             if self.activation != "gelu":
@@ -217,12 +260,7 @@ class Mamba3Stack:
 
     def logits(self, ids: torch.Tensor) -> torch.Tensor:
         """Per-token log-probabilities (B, L, vocab), float32."""
-        if self.decoder_w is None:
-            raise ValueError("logits needs decoder_w and decoder_b in the parameters")
-        z = F.linear(self.forward(ids), self.decoder_w, self.decoder_b).contiguous()
-        _lib.check(_lib.load().m3_log_softmax(_ptr(z), _ptr(z), z.shape[0], z.shape[1], z.shape[2], _stream(z)),
-                   "m3_log_softmax")
-        return z
+        return self._head(self.forward(ids))
 
 
 def init_params(vocab: int, d_model: int, n_layers: int, seed: int, device, d_state: int = 128,

@@ -46,7 +46,8 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_bwd_saved", "m3_chunk_scan_fwd_train_shared",
                             "m3_chunk_scan_bwd_saved_shared_ws_bytes", "m3_chunk_scan_bwd_saved_shared",
                             "m3_decode_step", "m3_layer_pre",
-                            "m3_layer_scan", "m3_layer_scan_train", "m3_layer_scan_bwd", "m3_layer_post",
+                            "m3_layer_scan", "m3_layer_scan_carry", "m3_layer_scan_train", "m3_layer_scan_bwd",
+                            "m3_layer_post",
                             "m3_layer_post_bwd_ws_bytes", "m3_layer_post_bwd",
                             "m3_layer_pre_bwd_ws_bytes", "m3_layer_pre_bwd", "m3_block_norm", "m3_block_gelu",
                             "m3_block_act", "m3_block_act_norm", "m3_log_softmax", "m3_block_act_bwd",
@@ -60,7 +61,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_constants(lib):
     from mamba3_rocm import _lib
-    assert lib.m3_abi_version() == 104
+    assert lib.m3_abi_version() == 105
     assert _lib.DTYPE_F32 == _header_define("M3_DTYPE_F32")
     assert _lib.DTYPE_BF16 == _header_define("M3_DTYPE_BF16")
     assert _lib.IMPL_CHUNKED_MFMA == _header_define("M3_IMPL_CHUNKED_MFMA")

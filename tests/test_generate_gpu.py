@@ -1,0 +1,94 @@
+"""Generation through the layer and the backbone: prefill with the recurrent carry,
+then one token at a time (Mamba3SSM.__call_rnn__, mamba3.py:466-568).
+
+Chunked == recurrent is the reference's own contract for the scan
+(test_backbone_contracts.py:81-111, rtol 2e-5): a prefill of the first L0 tokens
+followed by decode steps must give the outputs of the forward over the whole
+sequence at the later positions, and so must a prefill in two pieces.  Bars: float32
+1e-4 and bf16 2e-2 relative in norm (the forward's own bars against the oracle; the
+decode step computes in float32 from bf16 operands where the chunked kernel rounds
+its MFMA operands to bf16).  The prefill's own output equals the forward's bitwise in
+bf16 (observed on both routes); in float32 the carry-writing kernel differs from the
+plain one at rounding level (1.2e-7 observed, bar 1e-6).
+"""
+import numpy as np
+import pytest
+
+from _util import rel
+from oracle import mamba3_layer as ML
+from oracle import mamba3_stack as MS
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("B,L0,S,d_model,N,hd,bf16,path", [
+    (2, 150, 20, 256, 128, 64, True, "in_place"),     # 1336-wide bf16 rows
+    (2, 150, 20, 128, 128, 64, True, "copies"),       # 812-wide bf16 rows: x and z copied
+    (2, 150, 20, 64, 64, 32, False, "in_place"),      # float32, 412-wide rows
+    (1, 1100, 12, 256, 128, 64, True, "in_place"),    # 8 pairs: the prefill takes the sequence split
+])
+def test_layer_prefill_then_decode_matches_forward(B, L0, S, d_model, N, hd, bf16, path):
+    import torch
+    from mamba3_rocm import Mamba3Layer
+    dt = torch.bfloat16 if bf16 else torch.float32
+    p = ML.init_params(d_model, seed=91, d_state=N, headdim=hd)
+    layer = Mamba3Layer({k: torch.from_numpy(v).cuda() for k, v in p.items()}, d_model, d_state=N, headdim=hd,
+                        dtype=dt)
+    x = torch.from_numpy(np.random.default_rng(92).standard_normal((B, L0 + S, d_model)).astype(np.float32)).cuda()
+    print(f"case layer generate {(B, L0, S, d_model, N, hd)} bf16={bf16} {path}", flush=True)
+    full = layer(x)
+    assert layer.last_scan == path
+    out0, carry = layer.prefill(x[:, :L0].contiguous())
+    assert layer.last_scan == path
+    e_pre = rel(out0.float().cpu().numpy(), full[:, :L0].float().cpu().numpy())
+    print(f"layer generate: prefill against the forward {e_pre:.2e} (bitwise: {torch.equal(out0, full[:, :L0])})",
+          flush=True)
+    if path == "in_place" and bf16:
+        assert torch.equal(out0, full[:, :L0]), "prefill output differs from the forward's"
+    else:
+        assert e_pre <= 1e-6
+    # a prefill in two pieces
+    h = L0 // 2 + 3
+    _, c1 = layer.prefill(x[:, :h].contiguous())
+    o2, _ = layer.prefill(x[:, h:L0].contiguous(), c1)
+    bar = 2e-2 if bf16 else 1e-4
+    e_two = rel(o2.float().cpu().numpy(), full[:, h:L0].float().cpu().numpy())
+    # decode steps after the prefill
+    outs = []
+    for t in range(S):
+        o, carry = layer.step(x[:, L0 + t].contiguous(), carry)
+        outs.append(o)
+    torch.cuda.synchronize()
+    dec = torch.stack(outs, 1).float().cpu().numpy()
+    e_dec = rel(dec, full[:, L0:].float().cpu().numpy())
+    print(f"layer generate: two-piece prefill {e_two:.2e}, decode {e_dec:.2e}", flush=True)
+    assert e_two <= bar and e_dec <= bar
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_stack_prefill_then_decode_matches_logits(bf16):
+    import torch
+    from mamba3_rocm import Mamba3Stack
+    N, hd, D, V = (128, 64, 128, 53) if bf16 else (64, 32, 64, 37)
+    p = MS.init_params(vocab=V, d_model=D, n_layers=2, seed=93, d_state=N, headdim=hd)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()   # noqa: E731
+    tp = dict(embed=t(p["embed"]), decoder_w=t(p["decoder_w"]), decoder_b=t(p["decoder_b"]),
+              layers=[{k: ({kk: t(vv) for kk, vv in v.items()} if k == "mixer" else t(v)) for k, v in lp.items()}
+                      for lp in p["layers"]])
+    stack = Mamba3Stack(tp, D, activation="half_glu1", prenorm=True, d_state=N, headdim=hd,
+                        dtype=torch.bfloat16 if bf16 else torch.float32)
+    B, L0, S = 2, 140, 16
+    ids = torch.from_numpy(np.random.default_rng(94).integers(0, V, size=(B, L0 + S))).cuda()
+    print(f"case stack generate bf16={bf16}", flush=True)
+    full = stack.logits(ids)
+    lp0, state = stack.prefill(ids[:, :L0])
+    assert rel(lp0.cpu().numpy(), full[:, :L0].cpu().numpy()) <= 1e-6
+    outs = []
+    for i in range(S):
+        lpt, state = stack.step(ids[:, L0 + i], state)
+        outs.append(lpt)
+    torch.cuda.synchronize()
+    dec = torch.stack(outs, 1).cpu().numpy()
+    err = rel(dec, full[:, L0:].cpu().numpy())
+    print(f"stack generate bf16={bf16}: decode log-probabilities {err:.2e}", flush=True)
+    assert err <= (2e-2 if bf16 else 1e-4)
