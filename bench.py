@@ -22,8 +22,9 @@ Also reported on the same JSON line:
                 each with its own roofline, the scan forward, backward and training
                 pair at config 5's layer shape (B=4, L=12288, 24 heads: 96 pairs, the
                 sequence split and the split walk), the 12-layer backbone prefill
-                with its log-probabilities (config 5) and its training step (loss and
-                gradients), the mixer layer's training step
+                with its log-probabilities (config 5), its training step (loss and
+                gradients) and its generation step (one token for each of 512 sequences
+                through every layer's decode kernel), the mixer layer's training step
                 at config 5's layer shape, and, at the shape the reference publishes its
                 per-layer training times for (d_model 1024, one 13,000-token
                 sequence: docs/training.md:106-112, 283-294), the fused path's scan
@@ -36,7 +37,8 @@ launches of a process); the JSON line reports this as ``clock_settle``, apart fr
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-secondary]
-                       [--mode scan|decode|long|bwd|bwd3|bwd5|train|shared|shared_bwd|layer|layer_train|stack|stack_train|copy|fp32]
+                       [--mode scan|decode|long|bwd|bwd3|bwd5|train|shared|shared_bwd|layer|layer_train|stack|stack_train|
+                               stack_step|copy|fp32]
                        [--io bf16|f32]   (--mode bwd / train)
        python bench.py --mode traffic --pmc-dir DIR   (writes the traffic JSON of
                        the headline kernel from rocprofv3 --pmc FETCH_SIZE /
@@ -338,6 +340,24 @@ def bench_stack_train(torch, B, L, d_model, n_layers, vocab, steps, warmup, seed
     return dict(wall_s=wall, kernel_s=kern)
 
 
+def bench_stack_step(torch, B, L0, d_model, n_layers, vocab, steps, warmup, seed):
+    """Config 5's backbone generating: a prefill of L0 tokens per sequence (untimed),
+    then Mamba3Stack.step, one token for each of the B sequences per step (every
+    layer's decode kernel on its carry, the block kernels and the head's
+    log-probabilities)."""
+    from mamba3_rocm import Mamba3Stack
+    from mamba3_rocm.stack import init_params
+    params = init_params(vocab, d_model, n_layers, seed, "cuda")
+    stack = Mamba3Stack(params, d_model, activation="half_glu1", prenorm=True, dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    ids = torch.randint(0, vocab, (B, L0 + 1), device="cuda", generator=g)
+    _, state = stack.prefill(ids[:, :L0])
+    tok = ids[:, L0].contiguous()
+    wall, kern = time_calls(torch, lambda: stack.step(tok, state), steps, warmup)
+    return dict(wall_s=wall, kernel_s=kern)
+
+
 def bench_layer_train(torch, B, L, d_model, steps, warmup, seed):
     """The mixer layer's training step (24 heads of 64 at config 5's d_model 768, 32 at
     the reference's published d_model 1024): train_forward and the backward to x and
@@ -593,7 +613,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--mode", choices=("scan", "decode", "long", "bwd", "bwd3", "bwd5", "train", "shared", "shared_bwd",
                                        "layer", "layer_train",
-                                       "stack", "stack_train", "copy", "fp32", "traffic"), default="scan")
+                                       "stack", "stack_train", "stack_step", "copy", "fp32", "traffic"),
+                    default="scan")
     ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
@@ -665,6 +686,11 @@ def main():
         print(json.dumps({"mode": "layer_train", "step_ms": round(r["kernel_s"] * 1e3, 4),
                           "fwd_ms": round(r["fwd_s"] * 1e3, 4),
                           "tokens_per_s": round(4 * 12288 / r["wall_s"], 1)}), flush=True)
+        return
+    if args.mode == "stack_step":
+        r = bench_stack_step(torch, 512, 64, 768, 12, 2112, args.steps, args.warmup, seed=5)
+        print(json.dumps({"mode": "stack_step", "B": 512, "ms_per_step": round(r["kernel_s"] * 1e3, 4),
+                          "tokens_per_s": round(512 / r["wall_s"], 1)}), flush=True)
         return
     if args.mode == "stack_train":
         r = bench_stack_train(torch, 4, 12288, 768, 12, 2112, args.steps, args.warmup, seed=5)
@@ -759,6 +785,7 @@ def main():
         bb = bench_stack(torch, 4, 12288, 768, 12, 2112, 5, 2, seed=5)
         lt5 = bench_layer_train(torch, 4, 12288, 768, max(5, args.steps // 10), 2, seed=5)
         st5 = bench_stack_train(torch, 4, 12288, 768, 12, 2112, 3, 1, seed=5)
+        sd5 = bench_stack_step(torch, 512, 64, 768, 12, 2112, 20, 5, seed=5)
         rs = bench_shared_bwd(torch, 1, 13000, 32, 128, 64, 32, 64, max(5, args.steps // 5), 3, seed=6)
         rl = bench_layer_train(torch, 1, 13000, 1024, max(5, args.steps // 5), 3, seed=6)
         out["secondary"] = {
@@ -811,6 +838,9 @@ def main():
                                        "loss": "mean next-token NLL, random targets; no optimizer",
                                        "step_ms": round(st5["kernel_s"] * 1e3, 4),
                                        "tokens_per_s": round(4 * 12288 / st5["wall_s"], 1)},
+            "backbone_decode_config5": {"B": 512, "prefill": 64, "layers": 12, "d_model": 768, "vocab": 2112,
+                                        "dtype": "bf16", "ms_per_step": round(sd5["kernel_s"] * 1e3, 4),
+                                        "tokens_per_s": round(512 / sd5["wall_s"], 1)},
             "layer_train_config5": {"B": 4, "L": 12288, "d_model": 768, "H": 24, "dtype": "bf16",
                                     "step_ms": round(lt5["kernel_s"] * 1e3, 4),
                                     "fwd_ms": round(lt5["fwd_s"] * 1e3, 4),
