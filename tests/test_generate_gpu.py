@@ -9,7 +9,8 @@ sequence at the later positions, and so must a prefill in two pieces.  Bars: flo
 decode step computes in float32 from bf16 operands where the chunked kernel rounds
 its MFMA operands to bf16).  The prefill's own output equals the forward's bitwise in
 bf16 (observed on both routes); in float32 the carry-writing kernel differs from the
-plain one at rounding level (1.2e-7 observed, bar 1e-6).
+plain one at rounding level (1.2e-7 observed, bar 1e-6).  The last test runs the
+shape bench.py's generation line times (config 5's backbone, 512 sequences).
 """
 import numpy as np
 import pytest
@@ -92,3 +93,35 @@ def test_stack_prefill_then_decode_matches_logits(bf16):
     err = rel(dec, full[:, L0:].cpu().numpy())
     print(f"stack generate bf16={bf16}: decode log-probabilities {err:.2e}", flush=True)
     assert err <= (2e-2 if bf16 else 1e-4)
+
+
+def test_stack_generation_at_the_bench_shape():
+    """Config 5's backbone as bench.py's generation line runs it: 12 layers, d_model
+    768, 24 heads, vocab 2112, 512 sequences, a 64-token prefill, then decode steps;
+    every step's log-probabilities against the forward's logits over the whole
+    sequence (the same bars as above)."""
+    import torch
+    from mamba3_rocm import Mamba3Stack
+    from mamba3_rocm.stack import init_params
+    B, L0, S, V = 512, 64, 8, 2112
+    stack = Mamba3Stack(init_params(V, 768, 12, 95, "cuda"), 768, activation="half_glu1", prenorm=True,
+                        dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(96)
+    ids = torch.randint(0, V, (B, L0 + S), device="cuda", generator=g)
+    print("case stack generate config 5, B=512", flush=True)
+    full = stack.logits(ids)
+    lp0, state = stack.prefill(ids[:, :L0])
+    e_pre = rel(lp0.cpu().numpy(), full[:, :L0].cpu().numpy())
+    outs = []
+    for i in range(S):
+        lpt, state = stack.step(ids[:, L0 + i].contiguous(), state)
+        outs.append(lpt)
+    torch.cuda.synchronize()
+    dec = torch.stack(outs, 1).cpu().numpy()
+    ref = full[:, L0:].cpu().numpy()
+    err = rel(dec, ref)
+    agree = float(np.mean(dec.argmax(-1) == ref.argmax(-1)))
+    print(f"stack generate config 5: prefill {e_pre:.2e}, decode {err:.2e}, argmax agreement {agree:.4f}", flush=True)
+    assert e_pre <= 1e-6
+    assert err <= 2e-2
