@@ -344,7 +344,8 @@ def bench_stack_step(torch, B, L0, d_model, n_layers, vocab, steps, warmup, seed
     """Config 5's backbone generating: a prefill of L0 tokens per sequence (untimed),
     then Mamba3Stack.step, one token for each of the B sequences per step (every
     layer's decode kernel on its carry, the block kernels and the head's
-    log-probabilities)."""
+    log-probabilities), issued from the host step by step and replayed as one HIP
+    graph (Mamba3Stack.step_graph)."""
     from mamba3_rocm import Mamba3Stack
     from mamba3_rocm.stack import init_params
     params = init_params(vocab, d_model, n_layers, seed, "cuda")
@@ -355,7 +356,9 @@ def bench_stack_step(torch, B, L0, d_model, n_layers, vocab, steps, warmup, seed
     _, state = stack.prefill(ids[:, :L0])
     tok = ids[:, L0].contiguous()
     wall, kern = time_calls(torch, lambda: stack.step(tok, state), steps, warmup)
-    return dict(wall_s=wall, kernel_s=kern)
+    graph = stack.step_graph(state)
+    gwall, gkern = time_calls(torch, lambda: graph(tok), steps, warmup)
+    return dict(wall_s=wall, kernel_s=kern, graph_wall_s=gwall, graph_kernel_s=gkern)
 
 
 def bench_layer_train(torch, B, L, d_model, steps, warmup, seed):
@@ -690,7 +693,9 @@ def main():
     if args.mode == "stack_step":
         r = bench_stack_step(torch, 512, 64, 768, 12, 2112, args.steps, args.warmup, seed=5)
         print(json.dumps({"mode": "stack_step", "B": 512, "ms_per_step": round(r["kernel_s"] * 1e3, 4),
-                          "tokens_per_s": round(512 / r["wall_s"], 1)}), flush=True)
+                          "tokens_per_s": round(512 / r["wall_s"], 1),
+                          "graph_ms_per_step": round(r["graph_kernel_s"] * 1e3, 4),
+                          "graph_tokens_per_s": round(512 / r["graph_wall_s"], 1)}), flush=True)
         return
     if args.mode == "stack_train":
         r = bench_stack_train(torch, 4, 12288, 768, 12, 2112, args.steps, args.warmup, seed=5)
@@ -840,7 +845,9 @@ def main():
                                        "tokens_per_s": round(4 * 12288 / st5["wall_s"], 1)},
             "backbone_decode_config5": {"B": 512, "prefill": 64, "layers": 12, "d_model": 768, "vocab": 2112,
                                         "dtype": "bf16", "ms_per_step": round(sd5["kernel_s"] * 1e3, 4),
-                                        "tokens_per_s": round(512 / sd5["wall_s"], 1)},
+                                        "tokens_per_s": round(512 / sd5["wall_s"], 1),
+                                        "graph_ms_per_step": round(sd5["graph_kernel_s"] * 1e3, 4),
+                                        "graph_tokens_per_s": round(512 / sd5["graph_wall_s"], 1)},
             "layer_train_config5": {"B": 4, "L": 12288, "d_model": 768, "H": 24, "dtype": "bf16",
                                     "step_ms": round(lt5["kernel_s"] * 1e3, 4),
                                     "fwd_ms": round(lt5["fwd_s"] * 1e3, 4),

@@ -8,6 +8,8 @@
  *                  proj (or m3_chunk_scan_fwd_shared of mamba3_scan.h on copies)
  *   m3_layer_post: output RMSNorm
  *   out = m3_layer_post(...) @ out_proj                 (library GEMM)
+ * and, generating one token at a time, m3_layer_decode_step in place of
+ * m3_layer_pre and the scan;
  * and its backward: m3_layer_post_bwd, m3_layer_scan_bwd (after m3_layer_scan_train,
  * the forward that saves the scan's residuals), m3_layer_pre_bwd, with the GEMMs'
  * gradients between them.
@@ -72,6 +74,21 @@ int m3_layer_scan_carry(const void* Q, const void* K, const void* proj, int d_in
                         float* fin_theta, float* fin_ssm, float* fin_k, float* fin_v,
                         int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype,
                         void* ws, size_t ws_bytes, void* stream);
+/*
+ * The layer's decode step (Mamba3SSM.__call_rnn__, mamba3.py:466-568, one token per
+ * sequence): m3_layer_pre on the token followed by m3_decode_step, in one launch.
+ * proj (B, 2HP + 2N + 3H + R) in io_dtype is the token's projection row, the layout
+ * m3_layer_pre reads; B and C are normalised as m3_layer_pre normalises them (scales
+ * B_norm_scale / C_norm_scale (N,), eps), dt, A (A_floor) likewise, trap = sigmoid of
+ * the row's trap field (the reference's recurrent path applies it), the angle rates
+ * shared by the heads.  The carry (theta, ssm, k, v), B_bias / C_bias (H, N), D (H,)
+ * or NULL, angle_mode and diag_mode are m3_decode_step's; y (B, H, P) is written in
+ * io_dtype (the input of m3_layer_post).  The same shape limits as m3_decode_step.
+ */
+int m3_layer_decode_step(const void* proj, const float* dt_bias, const float* B_norm_scale,
+                         const float* C_norm_scale, const float* B_bias, const float* C_bias, const float* D,
+                         float* theta, float* ssm, float* k, float* v, void* y, int B, int H, int P, int N, int R,
+                         float A_floor, float eps, int io_dtype, int angle_mode, int diag_mode, void* stream);
 /*
  * The layer's training pair with x and z in place: m3_chunk_scan_fwd_train_shared and
  * m3_chunk_scan_bwd_saved_shared of mamba3_scan.h (the fused path's chunk_scan_fwd_rule /

@@ -53,7 +53,7 @@ bool decode_supported(int N, int P, int R) {
 
 extern "C" {
 
-int m3_abi_version(void) { return 105; }
+int m3_abi_version(void) { return 106; }
 
 const char* m3_last_error(void) { return g_err; }
 
@@ -530,6 +530,41 @@ int m3_layer_pre(const void* proj, const float* dt_bias, const float* B_norm_sca
   a.B = B; a.L = L; a.H = H; a.P = P; a.N = N; a.R = R; a.A_floor = A_floor; a.eps = eps;
   return check_launch(m3::layer_pre_launch(a, io_dtype == M3_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream)),
                       "layer pre");
+}
+
+int m3_layer_decode_step(const void* proj, const float* dt_bias, const float* B_norm_scale,
+                         const float* C_norm_scale, const float* B_bias, const float* C_bias, const float* D,
+                         float* theta, float* ssm, float* k, float* v, void* y, int B, int H, int P, int N, int R,
+                         float A_floor, float eps, int io_dtype, int angle_mode, int diag_mode, void* stream) {
+  if (io_dtype != M3_DTYPE_F32 && io_dtype != M3_DTYPE_BF16)
+    return fail(M3_E_ARG, "io_dtype must be M3_DTYPE_F32 or M3_DTYPE_BF16, got %d", io_dtype);
+  if (angle_mode != 0 && angle_mode != 1)
+    return fail(M3_E_ARG, "angle_mode must be 1 (wrapped) or 0 (legacy_unbounded), got %d", angle_mode);
+  if (diag_mode != 0 && diag_mode != 1)
+    return fail(M3_E_ARG, "diag_mode must be 0 (current) or 1 (legacy_double), got %d", diag_mode);
+  if (B < 0 || H <= 0 || N <= 0 || P <= 0 || R < 0)
+    return fail(M3_E_ARG, "non-positive dimension (B=%d H=%d N=%d P=%d R=%d)", B, H, N, P, R);
+  if (2 * R > N) return fail(M3_E_ARG, "num rope angles R=%d must be <= d_state/2 = %d", R, N / 2);
+  if (!m3::decode_supported(N, P, R))
+    return fail(M3_E_UNSUPPORTED, "decode needs d_state a multiple of 4 with d_state/4 a power of two "
+                "<= 64, headdim <= 256 and headdim*d_state <= 16384 (got N=%d P=%d)", N, P);
+  if (B == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!proj || !dt_bias || !B_norm_scale || !C_norm_scale || !B_bias || !C_bias || !ssm || !k || !v || !y ||
+      (R > 0 && !theta))
+    return fail(M3_E_ARG, "NULL required pointer");
+  if (!aligned16(ssm)) return fail(M3_E_ALIGN, "ssm state must be 16-byte aligned");
+  m3::DecodeArgs a{};
+  a.theta = theta; a.h = ssm; a.kprev = k; a.vprev = v;
+  a.bbias = B_bias; a.cbias = C_bias; a.D = D; a.y = y;
+  a.B = B; a.H = H; a.N = N; a.P = P; a.R = R;
+  a.wrapped = angle_mode; a.legacy_double = diag_mode;
+  a.proj = proj; a.dt_bias = dt_bias; a.b_scale = B_norm_scale; a.c_scale = C_norm_scale;
+  a.A_floor = A_floor; a.eps = eps;
+  const bool bf = io_dtype == M3_DTYPE_BF16;
+  return check_launch(m3::decode_step_launch(a, bf, bf, reinterpret_cast<hipStream_t>(stream)), "layer decode step");
 }
 
 }  // extern "C"

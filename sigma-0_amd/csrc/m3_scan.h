@@ -241,6 +241,14 @@ struct DecodeArgs {
   int B, H, N, P, R;
   int wrapped;        // 1: wrapped angle state (default), 0: legacy_unbounded
   int legacy_double;  // 1: add the explicit QK diagonal a second time
+  // The mixer layer's decode (m3_layer_decode_step): with proj set, x, z, B, C, the
+  // per-head dt/A/trap fields and the angle rates come from the token's projection row
+  // (batch b's row of 2HP + 2N + 3H + R elements, the layout m3_layer_pre reads), B
+  // and C RMS-normalised as m3_layer_pre does; x, z, bt, ct, adt, dt, trap and ang are
+  // then unused.
+  const void* proj = nullptr;
+  const float* dt_bias = nullptr; const float* b_scale = nullptr; const float* c_scale = nullptr;
+  float A_floor = 0.0f, eps = 0.0f;
 };
 
 bool decode_supported(int N, int P, int R);

@@ -97,28 +97,31 @@ class Mamba3Layer:
     def step(self, x_t: torch.Tensor, carry):
         """One token per sequence, as Mamba3SSM.__call_rnn__ runs it (mamba3.py:466-568):
         x_t (B, d_model) -> (out (B, d_model) in the compute dtype, carry), the carry
-        updated in place.  The in_proj GEMM, m3_layer_pre on the token, m3_decode_step
-        (B and C shared over heads, trap through the sigmoid as the reference's
-        recurrent path applies it), m3_layer_post and the out_proj GEMM."""
-        from .decode import rnn_step_hip
+        updated in place.  The in_proj GEMM, m3_layer_decode_step (m3_layer_pre's work on
+        the token and the decode update in one launch: B and C shared over heads, trap
+        through the sigmoid as the reference's recurrent path applies it),
+        m3_layer_post and the out_proj GEMM."""
+        from .decode import recurrent_angle_mode, recurrent_diagonal_mode
+        from .ops import mamba3_contraction_precision_mode
         Bn = x_t.shape[0]
         dt, dev = self.dtype, x_t.device
         nh, hd, N, R = self.nh, self.hd, self.N, self.R
         lib, io, pp = _lib.load(), _IO[dt], self.params
+        theta, ssm, kprev, vprev = carry
+        for name, t, shape in (("theta", theta, (Bn, nh, R)), ("ssm", ssm, (Bn, nh, hd, N)),
+                               ("k", kprev, (Bn, nh, N)), ("v", vprev, (Bn, nh, hd))):
+            if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and tuple(t.shape) == shape):
+                raise ValueError(f"carry {name} must be a contiguous float32 device tensor of shape {shape} "
+                                 "(it is updated in place)")
+        mamba3_contraction_precision_mode()     # the reference's decode reads it too (mamba3.py:545)
+        angle, diag = recurrent_angle_mode(), recurrent_diagonal_mode()
         proj = torch.matmul(x_t.to(dt).reshape(Bn, 1, self.d_model), self.w_in).contiguous()
-        Q = torch.empty(Bn, 1, N, device=dev, dtype=dt)
-        K = torch.empty_like(Q)
-        V = torch.empty(Bn, 1, nh, hd, device=dev, dtype=dt)
-        Z = torch.empty_like(V)
-        f32 = dict(device=dev, dtype=torch.float32)
-        ADT, DT, Trap = (torch.empty(Bn, nh, 1, **f32) for _ in range(3))
-        Ang = torch.empty(Bn, 1, R, **f32)
-        _lib.check(lib.m3_layer_pre(_ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]),
-                                    _ptr(Q), _ptr(K), _ptr(V), _ptr(Z), _ptr(ADT), _ptr(DT), _ptr(Trap), _ptr(Ang),
-                                    Bn, 1, nh, hd, N, R, self.A_floor, self.eps, io, _stream(proj)), "m3_layer_pre")
-        inputs = (V[:, 0], Z[:, 0], K.expand(Bn, nh, N), Q.expand(Bn, nh, N), ADT[..., 0], DT[..., 0],
-                  torch.sigmoid(Trap[..., 0]), Ang.expand(Bn, nh, R))
-        carry, y = rnn_step_hip(carry, inputs, pp["B_bias"], pp["C_bias"], pp["D"], out_dtype=dt)
+        y = torch.empty(Bn, 1, self.d_inner, device=dev, dtype=dt)
+        _lib.check(lib.m3_layer_decode_step(
+            _ptr(proj), _ptr(pp["dt_bias"]), _ptr(pp["B_norm"]), _ptr(pp["C_norm"]), _ptr(pp["B_bias"]),
+            _ptr(pp["C_bias"]), _ptr(pp["D"]), _ptr(theta), _ptr(ssm), _ptr(kprev), _ptr(vprev), _ptr(y),
+            Bn, nh, hd, N, R, self.A_floor, self.eps, io, 1 if angle == "wrapped" else 0,
+            1 if diag == "legacy_double" else 0, _stream(proj)), "m3_layer_decode_step")
         yn = torch.empty(Bn, 1, self.d_inner, device=dev, dtype=dt)
         _lib.check(lib.m3_layer_post(_ptr(y), _ptr(pp["out_norm"]), _ptr(yn), Bn, 1, self.d_inner, self.eps, io,
                                      _stream(y)), "m3_layer_post")

@@ -22,6 +22,7 @@ m3_block_gelu_bwd (the activation epilogue around the Dense layers' gradients,
 library GEMMs), the mixer's backward (Mamba3Layer) and m3_block_norm_bwd (the
 prenorm LayerNorm into the residual stream's gradient); the embedding's gradient is
 torch's index_add (its float32 sums over repeated tokens are not in a fixed order).
+``step_graph`` captures the generation step in a HIP graph.
 """
 from __future__ import annotations
 
@@ -261,6 +262,46 @@ class Mamba3Stack:
     def logits(self, ids: torch.Tensor) -> torch.Tensor:
         """Per-token log-probabilities (B, L, vocab), float32."""
         return self._head(self.forward(ids))
+
+    def step_graph(self, state) -> "StepGraph":
+        """``step`` on the carries of ``state`` captured once in a HIP graph (see
+        StepGraph): the generation loop's steps then replay it."""
+        return StepGraph(self, state)
+
+
+class StepGraph:
+    """Mamba3Stack.step for one batch of carries, captured once in a HIP graph
+    (torch.cuda.CUDAGraph): a call copies the token ids (B,) into the graph's input and
+    replays every launch of the step (about 300 at config 5: the GEMMs, the layer,
+    decode and block kernels, the head) with no host work between them.  It returns
+    the log-probabilities (B, vocab) in the graph's output buffer, which the next call
+    overwrites, and advances the carries of ``state`` in place, as step does.  The
+    decode mode knobs (MAMBA3_RECURRENT_*) are read once, at capture.  Nothing in the
+    step records a memset node: the library has none, and its buffers are written
+    whole by their kernels."""
+
+    def __init__(self, stack: Mamba3Stack, state):
+        dev = state[0][1].device
+        B = state[0][1].shape[0]
+        self.state = state
+        self.ids = torch.zeros(B, dtype=torch.long, device=dev)
+        # One eager step first, on copies of the carries, for the libraries' first-call
+        # set-up (which capture would not allow); then the capture, which runs nothing.
+        cur = torch.cuda.current_stream(dev)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            stack.step(self.ids, [tuple(t.clone() for t in c) for c in state])
+        cur.wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out, _ = stack.step(self.ids, state)
+
+    def __call__(self, ids_t: torch.Tensor) -> torch.Tensor:
+        self.ids.copy_(ids_t)
+        self.graph.replay()
+        return self.out
 
 
 def init_params(vocab: int, d_model: int, n_layers: int, seed: int, device, d_state: int = 128,

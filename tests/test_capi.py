@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_train", "m3_chunk_scan_bwd_saved_ws_bytes",
                             "m3_chunk_scan_bwd_saved", "m3_chunk_scan_fwd_train_shared",
                             "m3_chunk_scan_bwd_saved_shared_ws_bytes", "m3_chunk_scan_bwd_saved_shared",
-                            "m3_decode_step", "m3_layer_pre",
+                            "m3_decode_step", "m3_layer_pre", "m3_layer_decode_step",
                             "m3_layer_scan", "m3_layer_scan_carry", "m3_layer_scan_train", "m3_layer_scan_bwd",
                             "m3_layer_post",
                             "m3_layer_post_bwd_ws_bytes", "m3_layer_post_bwd",
@@ -61,7 +61,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_constants(lib):
     from mamba3_rocm import _lib
-    assert lib.m3_abi_version() == 105
+    assert lib.m3_abi_version() == 106
     assert _lib.DTYPE_F32 == _header_define("M3_DTYPE_F32")
     assert _lib.DTYPE_BF16 == _header_define("M3_DTYPE_BF16")
     assert _lib.IMPL_CHUNKED_MFMA == _header_define("M3_IMPL_CHUNKED_MFMA")
@@ -382,6 +382,26 @@ def test_decode_validation(lib):
     assert call(dm=3) == E_ARG and b"diag_mode" in lib.m3_last_error()
     assert call(R=33) == E_ARG
     assert call(N=12, R=4) == E_UNSUP                   # d_state/4 not a power of two
+    assert call(B=0) == 0
+
+
+def test_layer_decode_validation(lib):
+    E_ARG, E_UNSUP = _header_define("M3_E_ARG"), _header_define("M3_E_UNSUPPORTED")
+    p = ctypes.c_void_p(4096)
+
+    def call(ptrs=None, **kw):
+        d = dict(B=2, H=2, P=32, N=64, R=16, io=1, am=1, dm=0)
+        d.update(kw)
+        return lib.m3_layer_decode_step(*(ptrs or [p] * 12), d["B"], d["H"], d["P"], d["N"], d["R"], 1e-4, 1e-6,
+                                        d["io"], d["am"], d["dm"], None)
+    assert call(io=7) == E_ARG and b"io_dtype" in lib.m3_last_error()
+    assert call(am=2) == E_ARG and b"angle_mode" in lib.m3_last_error()
+    assert call(dm=3) == E_ARG and b"diag_mode" in lib.m3_last_error()
+    assert call(R=33) == E_ARG
+    assert call(H=0) == E_ARG
+    assert call(N=12, R=4) == E_UNSUP                   # d_state/4 not a power of two
+    assert call(ptrs=[None] + [p] * 11) == E_ARG and b"NULL" in lib.m3_last_error()
+    assert call(ptrs=[p] * 8 + [ctypes.c_void_p(4100)] + [p] * 3) == _header_define("M3_E_ALIGN")
     assert call(B=0) == 0
 
 

@@ -125,3 +125,41 @@ def test_stack_generation_at_the_bench_shape():
     print(f"stack generate config 5: prefill {e_pre:.2e}, decode {err:.2e}, argmax agreement {agree:.4f}", flush=True)
     assert e_pre <= 1e-6
     assert err <= 2e-2
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_stack_step_graph_matches_eager_steps(bf16):
+    """Mamba3Stack.step_graph: the step captured once in a HIP graph and replayed.
+    Every replay against an eager step from a copy of the same carries, with eager work
+    and a synchronisation between the replays (graph nodes that hold stale values show
+    on the replays after the first); log-probabilities and carries to 1e-6 relative
+    (the same kernels in the same order: bitwise equal is what is expected)."""
+    import torch
+    from mamba3_rocm import Mamba3Stack
+    N, hd, D, V = (128, 64, 128, 53) if bf16 else (64, 32, 64, 37)
+    p = MS.init_params(vocab=V, d_model=D, n_layers=2, seed=97, d_state=N, headdim=hd)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()   # noqa: E731
+    tp = dict(embed=t(p["embed"]), decoder_w=t(p["decoder_w"]), decoder_b=t(p["decoder_b"]),
+              layers=[{k: ({kk: t(vv) for kk, vv in v.items()} if k == "mixer" else t(v)) for k, v in lp.items()}
+                      for lp in p["layers"]])
+    stack = Mamba3Stack(tp, D, activation="half_glu1", prenorm=True, d_state=N, headdim=hd,
+                        dtype=torch.bfloat16 if bf16 else torch.float32)
+    B, L0, S = 3, 70, 6
+    ids = torch.from_numpy(np.random.default_rng(98).integers(0, V, size=(B, L0 + S))).cuda()
+    print(f"case stack step graph bf16={bf16}", flush=True)
+    _, st_e = stack.prefill(ids[:, :L0])
+    st_g = [tuple(x.clone() for x in c) for c in st_e]
+    graph = stack.step_graph(st_g)
+    worst, same = 0.0, True
+    for i in range(S):
+        lp_g = graph(ids[:, L0 + i]).clone()
+        lp_e, _ = stack.step(ids[:, L0 + i].contiguous(), st_e)
+        torch.cuda.synchronize()
+        same = same and torch.equal(lp_g, lp_e)
+        worst = max(worst, rel(lp_g.cpu().numpy(), lp_e.cpu().numpy()))
+    for ce, cg in zip(st_e, st_g):
+        for a, b in zip(ce, cg):
+            same = same and torch.equal(a, b)
+            worst = max(worst, rel(b.cpu().numpy(), a.cpu().numpy()))
+    print(f"stack step graph bf16={bf16}: worst {worst:.2e}, bitwise {same}", flush=True)
+    assert worst <= 1e-6
