@@ -64,6 +64,7 @@ void decode_step_kernel(DecodeArgs a) {
   __shared__ float sB[kDecMaxN], sKp[kDecMaxN], sC[kDecMaxN];
   __shared__ float sX[kDecMaxP], sVp[kDecMaxP], sY[kDecMaxP];
   __shared__ float sQK[kDecThreads / 64];   // legacy_double: per-wave sums of the QK dot
+  __shared__ float sScal[3];                // LAYER: the head's dt, decay and trap (wave 2)
 
   // 1. issue the state loads first
   f32x4* hrow = reinterpret_cast<f32x4*>(a.h + (long)bh * P * N);
@@ -76,7 +77,22 @@ void decode_step_kernel(DecodeArgs a) {
 
   // 2. preamble: carries and step inputs into LDS, angle update
   const long bhN = (long)bh * N, bhP = (long)bh * P, bhR = (long)bh * R;
-  float dtv, trv, dec;
+  float dtv = 0.0f, trv = 0.0f, dec = 0.0f;
+  // theta += tanh(rate) pi dt, wrapped; its cos and sin for the rope of step 3
+  auto angle = [&](int r, float rate) {
+    float th = a.theta[bhR + r] + tanh_fast(rate) * kPi * dtv;
+    if (a.wrapped) th = wrap_2pi(th);
+    a.theta[bhR + r] = th;
+    float c, s;
+    if (a.wrapped) {
+      sincos_wrapped(th, &c, &s);
+    } else {
+      c = cosf(th);
+      s = sinf(th);
+    }
+    sCos[r] = c;
+    sSin[r] = s;
+  };
   // LAYER: the token's projection row [z | x | B | C | dd_dt | dd_A | trap | rates]
   const TI* row = nullptr;
   long ox = 0, oz = 0, oang = 0;          // offsets of x_h, z_h and the rates in row
@@ -86,13 +102,20 @@ void decode_step_kernel(DecodeArgs a) {
     oz = (long)hh * P;
     ox = DI + oz;
     oang = 2L * DI + 2 * N + 3 * H;
-    const TI* hd = row + 2L * DI + 2 * N;
-    dtv = softplus_f(Elem<TI>::to_f(hd[hh]) + a.dt_bias[hh]);
-    const float A = fminf(-softplus_f(Elem<TI>::to_f(hd[H + hh])), -a.A_floor);
-    dec = exp_fast(A * dtv);
-    trv = 1.0f / (1.0f + expf(-Elem<TI>::to_f(hd[2 * H + hh])));
     const int wave = tid >> 6, lane = tid & 63;
-    if (wave < 2) {   // BCNorm: wave 0 B (the key), wave 1 C (the query); N <= 256
+    if (wave == 2) {   // the head's scalars (the other waves read them after the barrier), angles
+      const TI* hd = row + 2L * DI + 2 * N;
+      dtv = softplus_f(Elem<TI>::to_f(hd[hh]) + a.dt_bias[hh]);
+      const float A = fminf(-softplus_f(Elem<TI>::to_f(hd[H + hh])), -a.A_floor);
+      dec = exp_fast(A * dtv);
+      trv = 1.0f / (1.0f + expf(-Elem<TI>::to_f(hd[2 * H + hh])));
+      if (lane == 0) {
+        sScal[0] = dtv;
+        sScal[1] = dec;
+        sScal[2] = trv;
+      }
+      for (int r = lane; r < R; r += 64) angle(r, Elem<TI>::to_f(row[oang + r]));
+    } else if (wave < 2) {   // BCNorm: wave 0 B (the key), wave 1 C (the query); N <= 256
       const TI* src = row + 2L * DI + wave * N;
       const float* sc = wave ? a.c_scale : a.b_scale;
       float xv[kDecMaxN / 64], scv[kDecMaxN / 64];
@@ -124,20 +147,8 @@ void decode_step_kernel(DecodeArgs a) {
     sVp[p] = a.vprev[bhP + p];
     sX[p] = LAYER ? Elem<TI>::to_f(row[ox + p]) : ld_f<TI>(a.x, bhP + p);
   }
-  for (int r = tid; r < R; r += kDecThreads) {
-    const float rate = LAYER ? Elem<TI>::to_f(row[oang + r]) : a.ang[bhR + r];
-    float th = a.theta[bhR + r] + tanh_fast(rate) * kPi * dtv;
-    if (a.wrapped) th = wrap_2pi(th);
-    a.theta[bhR + r] = th;
-    float c, s;
-    if (a.wrapped) {
-      sincos_wrapped(th, &c, &s);
-    } else {
-      c = cosf(th);
-      s = sinf(th);
-    }
-    sCos[r] = c;
-    sSin[r] = s;
+  if constexpr (!LAYER) {
+    for (int r = tid; r < R; r += kDecThreads) angle(r, a.ang[bhR + r]);
   }
   // step 3's global inputs, requested before the barrier (none depends on step 2):
   // thread j < N/2 owns the pair (2j, 2j + 1); N/2 <= 128 < kDecThreads
@@ -157,6 +168,11 @@ void decode_step_kernel(DecodeArgs a) {
     }
   }
   __syncthreads();
+  if constexpr (LAYER) {
+    dtv = sScal[0];
+    dec = sScal[1];
+    trv = sScal[2];
+  }
 
   // 3. rotated key/query for this step; new carries
   float qk_part = 0.0f;
