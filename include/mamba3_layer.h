@@ -262,6 +262,19 @@ int m3_block_norm_bwd(const float* x, const float* scale, const void* d_norm, co
 int m3_log_softmax_nll(float* logits, const int* targets, float* loss, int B, int L, int V, float weight,
                        void* stream);
 
+/*
+ * No counterpart in the reference: the operands of a float32 product computed as
+ * three bf16 products with float32 accumulation (a_hi b_hi + a_hi b_lo + a_lo b_hi,
+ * the head's decoder Dense and its gradients in a bf16 model; relative error about
+ * 1e-5 against 5e-4 for TF32, which gfx950's matrix cores do not have).  x (rows, K)
+ * float32 contiguous; hi = bf16(x) (round to nearest even) is written to hi_a and, when
+ * not NULL, to hi_b, and lo = bf16(x - hi) to lo: rows of K elements at row stride ld
+ * (ld >= K), so that the three land side by side in one (rows, 3K) operand (ld = 3K,
+ * pointers K apart) or stacked in one (3 rows, K) operand (ld = K, pointers rows * K
+ * apart).
+ */
+int m3_split_bf16x3(const float* x, void* hi_a, void* hi_b, void* lo, long rows, int K, long ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

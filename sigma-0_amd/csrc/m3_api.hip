@@ -53,7 +53,7 @@ bool decode_supported(int N, int P, int R) {
 
 extern "C" {
 
-int m3_abi_version(void) { return 106; }
+int m3_abi_version(void) { return 107; }
 
 const char* m3_last_error(void) { return g_err; }
 
@@ -911,6 +911,18 @@ int m3_log_softmax_nll(float* logits, const int* targets, float* loss, int B, in
   if (!logits || !targets || !loss) return fail(M3_E_ARG, "NULL required pointer");
   return check_launch(m3::nll_launch(logits, targets, loss, (long)B * L, V, weight,
                                      reinterpret_cast<hipStream_t>(stream)), "log_softmax NLL");
+}
+
+int m3_split_bf16x3(const float* x, void* hi_a, void* hi_b, void* lo, long rows, int K, long ld, void* stream) {
+  if (rows < 0 || K <= 0) return fail(M3_E_ARG, "non-positive dimension (rows=%ld K=%d)", rows, K);
+  if (ld < K) return fail(M3_E_ARG, "row stride ld=%ld is below the row length K=%d", ld, K);
+  if (rows == 0) {
+    g_err[0] = '\0';
+    return M3_OK;
+  }
+  if (!x || !hi_a || !lo) return fail(M3_E_ARG, "NULL required pointer");
+  return check_launch(m3::split3_launch(x, hi_a, hi_b, lo, rows, K, ld, reinterpret_cast<hipStream_t>(stream)),
+                      "split bf16x3");
 }
 
 }  // extern "C"

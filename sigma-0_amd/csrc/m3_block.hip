@@ -36,6 +36,13 @@
 //   nll_kernel             one wave per token (lob_seq_model.py:530-542's log_softmax):
 //                          loss = logsumexp(z) - z[target], and in place dz =
 //                          (softmax(z) - onehot(target)) w
+//
+// split3_kernel writes the bfloat16 operands of a float32 product computed as three
+// bf16 products with float32 accumulation (the head's decoder Dense and its
+// gradients in a bf16 model): hi = bf16(x) rounded to nearest even, lo = bf16(x - hi),
+// so that a b = a_hi b_hi + a_hi b_lo + a_lo b_hi up to the omitted a_lo b_lo and the
+// rounding of lo (relative 2^-16 per element).  gfx950's matrix cores have no
+// reduced-precision float32 type; bf16 runs at 16 times the float32 MFMA rate.
 #include "../../include/mamba3_layer.h"
 #include "m3_scan.h"
 
@@ -590,7 +597,53 @@ void nll_kernel(float* z, const int* targets, float* loss, long rows, int V, flo
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// hi to a (and b when given), lo to c: rows of K elements at row stride ld; x is
+// (rows, K) contiguous.  vec: eight elements per thread (K a multiple of 8, 16-byte
+// aligned rows).
+__global__ __launch_bounds__(kBlockThreads)
+void split3_kernel(const float* x, bf16* a, bf16* b, bf16* c, long rows, int K, long ld, int vec) {
+  const long i = (long)blockIdx.x * kBlockThreads + threadIdx.x;
+  if (vec) {
+    const int kv = K / 8;
+    if (i >= rows * kv) return;
+    const long r = i / kv;
+    const int q = (int)(i - r * kv);
+    const float4* src = reinterpret_cast<const float4*>(x + r * K + 8 * q);
+    const float4 v0 = src[0], v1 = src[1];
+    const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      hi[e] = (float)(bf16)f[e];
+      lo[e] = f[e] - hi[e];
+    }
+    const long o = r * ld + 8 * q;
+    store8(a + o, hi);
+    if (b) store8(b + o, hi);
+    store8(c + o, lo);
+  } else {
+    if (i >= rows * K) return;
+    const long r = i / K;
+    const int k = (int)(i - r * K);
+    const float f = x[i];
+    const bf16 h = (bf16)f;
+    const long o = r * ld + k;
+    a[o] = h;
+    if (b) b[o] = h;
+    c[o] = (bf16)(f - (float)h);
+  }
+}
+
 }  // namespace
+
+hipError_t split3_launch(const float* x, void* a, void* b, void* c, long rows, int K, long ld, hipStream_t st) {
+  const int vec = K % 8 == 0 && ld % 8 == 0 && al16(x) && al16(a) && al16(c) && (!b || al16(b));
+  const long work = vec ? rows * (K / 8) : rows * K;
+  const dim3 grid((unsigned)((work + kBlockThreads - 1) / kBlockThreads));
+  hipLaunchKernelGGL(split3_kernel, grid, dim3(kBlockThreads), 0, st, x, reinterpret_cast<bf16*>(a),
+                     reinterpret_cast<bf16*>(b), reinterpret_cast<bf16*>(c), rows, K, ld, vec);
+  return hipGetLastError();
+}
 
 hipError_t block_norm_launch(BlockNormArgs a, bool bf16_out, hipStream_t st) {
   a.vec = a.D % 4 == 0 && a.D <= 64 * 4 * kNormVec && al16(a.x) && al16(a.out) && al16(a.scale) && al16(a.bias);

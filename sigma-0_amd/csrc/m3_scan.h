@@ -221,6 +221,7 @@ hipError_t block_norm_bwd_launch(const BlockNormBwdArgs& a, float* dscale, float
 // logsumexp(z) - z[target] and, in place, z = (softmax(z) - onehot(target)) w.  A
 // target outside [0, V) gives a NaN loss and no one-hot term.
 hipError_t nll_launch(float* z, const int* targets, float* loss, long rows, int V, float w, hipStream_t st);
+hipError_t split3_launch(const float* x, void* a, void* b, void* c, long rows, int K, long ld, hipStream_t st);
 
 // Sequence split across compute units: workspace bytes (0 = no split) and launch.
 size_t scan_split_ws_bytes(bool bf16_io, int B, int L, int H, int N, int P, int R, int CS);

@@ -33,7 +33,7 @@ EXPORTS = ("m3_abi_version", "m3_last_error", "m3_chunk_scan_impl", "m3_chunk_sc
            "m3_chunk_scan_bwd_saved_shared",
            "m3_decode_step",
            "m3_layer_pre", "m3_layer_scan", "m3_layer_scan_carry", "m3_layer_scan_train", "m3_layer_scan_bwd",
-           "m3_layer_decode_step",
+           "m3_layer_decode_step", "m3_split_bf16x3",
            "m3_layer_post",
            "m3_layer_post_bwd_ws_bytes", "m3_layer_post_bwd",
            "m3_layer_pre_bwd_ws_bytes", "m3_layer_pre_bwd",
@@ -66,6 +66,7 @@ _SIGS = {
     "m3_chunk_scan_bwd_saved_shared": ([_P] * 23 + [_I] * 8 + [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P], _I),
     "m3_layer_pre": ([_P] * 12 + [_I] * 6 + [ctypes.c_float, ctypes.c_float, _I, _P], _I),
     "m3_layer_decode_step": ([_P] * 12 + [_I] * 5 + [ctypes.c_float] * 2 + [_I] * 3 + [_P], _I),
+    "m3_split_bf16x3": ([_P] * 4 + [ctypes.c_long, _I, ctypes.c_long, _P], _I),
     "m3_layer_scan": ([_P] * 3 + [_I] + [_P] * 8 + [_I] * 8 + [_P, ctypes.c_size_t, _P], _I),
     "m3_layer_scan_carry": ([_P] * 3 + [_I] + [_P] * 16 + [_I] * 8 + [_P, ctypes.c_size_t, _P], _I),
     "m3_layer_scan_train": ([_P] * 3 + [_I] + [_P] * 8 + [_I] * 8 + [_P, ctypes.c_size_t] * 2 + [_P], _I),

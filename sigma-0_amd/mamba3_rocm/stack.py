@@ -23,6 +23,12 @@ library GEMMs), the mixer's backward (Mamba3Layer) and m3_block_norm_bwd (the
 prenorm LayerNorm into the residual stream's gradient); the embedding's gradient is
 torch's index_add (its float32 sums over repeated tokens are not in a fixed order).
 ``step_graph`` captures the generation step in a HIP graph.
+In a bf16 stack the head's float32 products (the decoder Dense, and in the training
+step its two gradients) run as three bf16 products with float32 accumulation:
+a b = a_hi b_hi + a_hi b_lo + a_lo b_hi with hi = bf16(a), lo = bf16(a - hi) (split by
+m3_split_bf16x3), relative error about 1e-5.  gfx950's matrix cores have no TF32-like
+float32 mode and run bf16 at 16 times their float32 rate.  A float32 stack keeps
+float32 products.
 """
 from __future__ import annotations
 
@@ -59,9 +65,18 @@ class Mamba3Stack:
                 b[n + "_b"] = lp[n + "_b"].to(dtype)
             self.blocks.append(b)
         self.decoder_w = self.decoder_b = None
+        self._dec_w3 = self._dec_w3b = None
         if "decoder_w" in params:
             self.decoder_w = params["decoder_w"].float().t().contiguous()
             self.decoder_b = params["decoder_b"].float().contiguous()
+            if dtype == torch.bfloat16:
+                # split-bf16 operands of the decoder weight (V, D): [hi | lo | hi] along D
+                # against the features' [hi | hi | lo], and the same stacked along V
+                # against the logits' gradient
+                wh = self.decoder_w.to(torch.bfloat16)
+                wl = (self.decoder_w - wh.float()).to(torch.bfloat16)
+                self._dec_w3 = torch.cat([wh, wl, wh], 1).contiguous()
+                self._dec_w3b = torch.cat([wh, wl, wh], 0).contiguous()
 
     def _block(self, b, x, xin, nxt, mixer=None):
         """SequenceLayer.__call__ (layers.py:108-160) on the float32 residual x (B, L, D).
@@ -118,10 +133,19 @@ class Mamba3Stack:
         """log_softmax of the decoder Dense on float32 features (..., d_model)."""
         if self.decoder_w is None:
             raise ValueError("the head needs decoder_w and decoder_b in the parameters")
-        z = F.linear(x, self.decoder_w, self.decoder_b).contiguous()
+        z = self._decoder(x)
         rows = z.numel() // z.shape[-1]
         _lib.check(_lib.load().m3_log_softmax(_ptr(z), _ptr(z), 1, rows, z.shape[-1], _stream(z)), "m3_log_softmax")
         return z
+
+    def _decoder(self, x: torch.Tensor) -> torch.Tensor:
+        """The decoder Dense on float32 features (..., d_model): float32 logits, split-bf16
+        products in a bf16 stack."""
+        if self._dec_w3 is None:
+            return F.linear(x, self.decoder_w, self.decoder_b).contiguous()
+        x2 = x.reshape(-1, self.d_model).contiguous()
+        z = torch.addmm(self.decoder_b, split_bf16x3(x2), self._dec_w3.t(), out_dtype=torch.float32)
+        return z.reshape(*x.shape[:-1], z.shape[-1])
 
     def prefill(self, ids: torch.Tensor, state=None):
         """Per-token log-probabilities (B, L, vocab) of ids (B, L), continuing each
@@ -206,7 +230,7 @@ class Mamba3Stack:
             saves.append(dict(x=x, y=y, g=g, h1=h1, h2=h2, m=msaved))
             x, xin = out, xn
         # ---- the head: loss and, in place, the logits' gradient
-        z = F.linear(x, self.decoder_w, self.decoder_b).contiguous()
+        z = self._decoder(x)
         tg = targets.to(device=z.device, dtype=torch.int32).contiguous()
         if tuple(tg.shape) != (Bn, L):
             raise ValueError(f"targets must be {(Bn, L)}, got {tuple(tg.shape)}")
@@ -216,8 +240,15 @@ class Mamba3Stack:
                    "m3_log_softmax_nll")
         loss = loss_rows.sum() / rows
         dz = z.reshape(rows, V)
-        grads = dict(decoder_w=x.reshape(rows, D).t() @ dz, decoder_b=dz.sum(0))
-        dres = (dz @ self.decoder_w).reshape(Bn, L, D)           # the features' gradient, float32
+        x2 = x.reshape(rows, D)
+        if self._dec_w3 is None:
+            gw = x2.t() @ dz
+            dres = (dz @ self.decoder_w).reshape(Bn, L, D)       # the features' gradient, float32
+        else:   # split-bf16 products: x_hi dz_hi + x_lo dz_hi + x_hi dz_lo, and dz W likewise
+            gw = torch.mm(split_bf16x3(x2, stacked=True, lo_mid=True).t(), split_bf16x3(dz, stacked=True),
+                          out_dtype=torch.float32)
+            dres = torch.mm(split_bf16x3(dz), self._dec_w3b, out_dtype=torch.float32).reshape(Bn, L, D)
+        grads = dict(decoder_w=gw, decoder_b=dz.sum(0))
         # ---- the blocks in reverse
         layers = [None] * len(self.blocks)
         for i in reversed(range(len(self.blocks))):
@@ -302,6 +333,23 @@ class StepGraph:
         self.ids.copy_(ids_t)
         self.graph.replay()
         return self.out
+
+
+def split_bf16x3(x: torch.Tensor, stacked: bool = False, lo_mid: bool = False) -> torch.Tensor:
+    """The bf16 operand of a split-bf16 product from x (M, K) float32 contiguous, hi =
+    bf16(x) and lo = bf16(x - hi) by m3_split_bf16x3: side by side (M, 3K) = [hi | hi |
+    lo], or stacked (3M, K) = [hi; hi; lo] ([hi; lo; hi] with lo_mid)."""
+    M, K = x.shape
+    if stacked:
+        out = torch.empty(3 * M, K, device=x.device, dtype=torch.bfloat16)
+        parts, ld = (out[:M], out[M:2 * M], out[2 * M:]), K
+    else:
+        out = torch.empty(M, 3 * K, device=x.device, dtype=torch.bfloat16)
+        parts, ld = (out[:, :K], out[:, K:2 * K], out[:, 2 * K:]), 3 * K
+    hi_a, hi_b, lo = (parts[0], parts[2], parts[1]) if lo_mid else parts
+    _lib.check(_lib.load().m3_split_bf16x3(_ptr(x), hi_a.data_ptr(), hi_b.data_ptr(), lo.data_ptr(), M, K, ld,
+                                           _stream(x)), "m3_split_bf16x3")
+    return out
 
 
 def init_params(vocab: int, d_model: int, n_layers: int, seed: int, device, d_state: int = 128,

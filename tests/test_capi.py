@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
                             "m3_chunk_scan_fwd_train", "m3_chunk_scan_bwd_saved_ws_bytes",
                             "m3_chunk_scan_bwd_saved", "m3_chunk_scan_fwd_train_shared",
                             "m3_chunk_scan_bwd_saved_shared_ws_bytes", "m3_chunk_scan_bwd_saved_shared",
-                            "m3_decode_step", "m3_layer_pre", "m3_layer_decode_step",
+                            "m3_decode_step", "m3_layer_pre", "m3_layer_decode_step", "m3_split_bf16x3",
                             "m3_layer_scan", "m3_layer_scan_carry", "m3_layer_scan_train", "m3_layer_scan_bwd",
                             "m3_layer_post",
                             "m3_layer_post_bwd_ws_bytes", "m3_layer_post_bwd",
@@ -61,7 +61,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_constants(lib):
     from mamba3_rocm import _lib
-    assert lib.m3_abi_version() == 106
+    assert lib.m3_abi_version() == 107
     assert _lib.DTYPE_F32 == _header_define("M3_DTYPE_F32")
     assert _lib.DTYPE_BF16 == _header_define("M3_DTYPE_BF16")
     assert _lib.IMPL_CHUNKED_MFMA == _header_define("M3_IMPL_CHUNKED_MFMA")
@@ -403,6 +403,17 @@ def test_layer_decode_validation(lib):
     assert call(ptrs=[None] + [p] * 11) == E_ARG and b"NULL" in lib.m3_last_error()
     assert call(ptrs=[p] * 8 + [ctypes.c_void_p(4100)] + [p] * 3) == _header_define("M3_E_ALIGN")
     assert call(B=0) == 0
+
+
+def test_split_bf16x3_validation(lib):
+    E_ARG = _header_define("M3_E_ARG")
+    p = ctypes.c_void_p(4096)
+    assert lib.m3_split_bf16x3(p, p, None, p, -1, 8, 8, None) == E_ARG
+    assert lib.m3_split_bf16x3(p, p, None, p, 4, 0, 8, None) == E_ARG
+    assert lib.m3_split_bf16x3(p, p, None, p, 4, 8, 7, None) == E_ARG and b"stride" in lib.m3_last_error()
+    assert lib.m3_split_bf16x3(None, p, None, p, 4, 8, 8, None) == E_ARG and b"NULL" in lib.m3_last_error()
+    assert lib.m3_split_bf16x3(p, p, p, None, 4, 8, 8, None) == E_ARG
+    assert lib.m3_split_bf16x3(p, p, None, p, 0, 8, 8, None) == 0
 
 
 def test_wrappers_refuse_cpu_tensors():
