@@ -618,13 +618,15 @@ def main():
                                        "layer", "layer_train",
                                        "stack", "stack_train", "stack_step", "copy", "fp32", "traffic"),
                     default="scan")
-    ap.add_argument("--pmc-dir", default="gpurun_out/prof", help="--mode traffic: the rocprofv3 --pmc run folders")
+    ap.add_argument("--pmc-dir", default=None, help="--mode traffic: the folder holding the rocprofv3 --pmc runs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--io", choices=("bf16", "f32"), default="bf16", help="--mode bwd / train / long: the I/O dtype")
     args = ap.parse_args()
 
     if args.mode == "traffic":
+        if not args.pmc_dir:
+            ap.error("--mode traffic needs --pmc-dir")
         write_traffic(args.pmc_dir)
         return
 
