@@ -66,8 +66,12 @@ def test_layer_prefill_then_decode_matches_forward(B, L0, S, d_model, N, hd, bf1
     assert e_two <= bar and e_dec <= bar
 
 
-@pytest.mark.parametrize("bf16", [False, True])
-def test_stack_prefill_then_decode_matches_logits(bf16):
+@pytest.mark.parametrize("bf16,activation,prenorm", [
+    (False, "half_glu1", True), (True, "half_glu1", True),       # the LOB models' block
+    (False, "full_glu", False), (True, "half_glu2", False),      # postnorm: the LayerNorm on the residual
+    (False, "gelu", True),
+])
+def test_stack_prefill_then_decode_matches_logits(bf16, activation, prenorm):
     import torch
     from mamba3_rocm import Mamba3Stack
     N, hd, D, V = (128, 64, 128, 53) if bf16 else (64, 32, 64, 37)
@@ -76,11 +80,11 @@ def test_stack_prefill_then_decode_matches_logits(bf16):
     tp = dict(embed=t(p["embed"]), decoder_w=t(p["decoder_w"]), decoder_b=t(p["decoder_b"]),
               layers=[{k: ({kk: t(vv) for kk, vv in v.items()} if k == "mixer" else t(v)) for k, v in lp.items()}
                       for lp in p["layers"]])
-    stack = Mamba3Stack(tp, D, activation="half_glu1", prenorm=True, d_state=N, headdim=hd,
+    stack = Mamba3Stack(tp, D, activation=activation, prenorm=prenorm, d_state=N, headdim=hd,
                         dtype=torch.bfloat16 if bf16 else torch.float32)
     B, L0, S = 2, 140, 16
     ids = torch.from_numpy(np.random.default_rng(94).integers(0, V, size=(B, L0 + S))).cuda()
-    print(f"case stack generate bf16={bf16}", flush=True)
+    print(f"case stack generate bf16={bf16} {activation} prenorm={prenorm}", flush=True)
     full = stack.logits(ids)
     lp0, state = stack.prefill(ids[:, :L0])
     assert rel(lp0.cpu().numpy(), full[:, :L0].cpu().numpy()) <= 1e-6
@@ -91,7 +95,8 @@ def test_stack_prefill_then_decode_matches_logits(bf16):
     torch.cuda.synchronize()
     dec = torch.stack(outs, 1).cpu().numpy()
     err = rel(dec, full[:, L0:].cpu().numpy())
-    print(f"stack generate bf16={bf16}: decode log-probabilities {err:.2e}", flush=True)
+    print(f"stack generate bf16={bf16} {activation} prenorm={prenorm}: decode log-probabilities {err:.2e}",
+          flush=True)
     assert err <= (2e-2 if bf16 else 1e-4)
 
 
