@@ -141,7 +141,8 @@ size_t m3_layer_post_bwd_ws_bytes(int B, int L, int D);
 int m3_layer_post_bwd(const void* y, const void* d_out, const float* scale, void* dy, float* d_scale, int B, int L,
                       int D, float eps, int io_dtype, void* ws, size_t ws_bytes, void* stream);
 /*
- * m3_layer_pre's backward: from proj and the parameters m3_layer_pre read, and the
+ * m3_layer_pre's backward (autodiff of Mamba3SSM._preprocess, shared_bc,
+ * src/base_model/models/mamba3.py:203-268): from proj and the parameters m3_layer_pre read, and the
  * gradients of its outputs -- dQ and dK of the normalised C and B (B, L, N), dV and
  * dZ (B, L, H, P), all in io_dtype (m3_chunk_scan_bwd_shared's dQ, dK, dV, dZ; dV and dZ
  * both NULL when m3_layer_scan_bwd wrote them into d_proj already), and

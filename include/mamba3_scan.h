@@ -45,13 +45,15 @@ extern "C" {
 #define M3_IMPL_CHUNKED_MFMA 1
 #define M3_IMPL_GENERIC 2
 
-/* ABI version (major * 100 + minor). */
+/* ABI version (major * 100 + minor).  No counterpart in the reference (library plumbing). */
 int m3_abi_version(void);
 
-/* Message for the last failing call on this host thread ("" if none). */
+/* Message for the last failing call on this host thread ("" if none).  No counterpart in
+ * the reference (library plumbing; the reference's FFI raises instead). */
 const char* m3_last_error(void);
 
-/* Which prefill kernel serves this shape (M3_IMPL_*), without launching. */
+/* Which prefill kernel serves this shape (M3_IMPL_*), without launching.  No counterpart
+ * in the reference (library plumbing). */
 int m3_chunk_scan_impl(int io_dtype, int N, int P, int R, int chunk_size);
 
 /*
@@ -94,7 +96,9 @@ int m3_chunk_scan_fwd_carry(const void* Q, const void* K, const void* V,
  * Device workspace (bytes) that m3_chunk_scan_fwd_ws uses to split each sequence
  * into segments running on separate compute units; 0 when the shape runs as one
  * pass.  The split pays off when B*H is well below the compute-unit count
- * (single-sequence prefill, long context).  Hqk does not matter.
+ * (single-sequence prefill, long context).  Hqk does not matter.  No counterpart in the
+ * reference, whose long-context forward passes states in blocks inside its kernel
+ * (src/base_model/models/mamba3_pallas.py:679-727).
  */
 size_t m3_chunk_scan_ws_bytes(int B, int L, int H, int N, int P, int R, int chunk_size, int io_dtype);
 
@@ -146,7 +150,9 @@ int m3_chunk_scan_fwd_noalloc(const void* Q, const void* K, const void* V,
 /*
  * Device workspace (bytes) that m3_chunk_scan_bwd needs for a shape; 0 when the
  * backward has no kernel for (io_dtype, N, P, R).  About 2 * B*H*L*P*N/CS * the
- * element size (the state entering and the adjoint state after each chunk).
+ * element size (the state entering and the adjoint state after each chunk).  The
+ * reference's custom_vjp backward (src/base_model/models/mamba3_ops.py:821-902) holds
+ * its residuals in XLA buffers instead.
  */
 size_t m3_chunk_scan_bwd_ws_bytes(int B, int L, int H, int Hqk, int N, int P, int R, int chunk_size,
                                   int io_dtype);
