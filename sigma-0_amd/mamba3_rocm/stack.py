@@ -339,6 +339,8 @@ def split_bf16x3(x: torch.Tensor, stacked: bool = False, lo_mid: bool = False) -
     """The bf16 operand of a split-bf16 product from x (M, K) float32 contiguous, hi =
     bf16(x) and lo = bf16(x - hi) by m3_split_bf16x3: side by side (M, 3K) = [hi | hi |
     lo], or stacked (3M, K) = [hi; hi; lo] ([hi; lo; hi] with lo_mid)."""
+    if x.dim() != 2 or x.dtype != torch.float32 or not x.is_contiguous() or not x.is_cuda:
+        raise ValueError("split_bf16x3 takes a contiguous 2-D float32 device tensor")
     M, K = x.shape
     if stacked:
         out = torch.empty(3 * M, K, device=x.device, dtype=torch.bfloat16)

@@ -643,3 +643,11 @@ def test_pallas_dtype_knob(monkeypatch):
         t = torch.zeros(1)
         with pytest.raises(ValueError, match="MAMBA3_PALLAS_DTYPE must be float32 or bfloat16"):
             mamba3_ssd_chunked_shared_hip(t, t, torch.zeros(4, 2, 8), t, t, t, t, t, t)
+
+
+def test_split_bf16x3_wrapper_refuses_other_tensors():
+    import torch
+    from mamba3_rocm.stack import split_bf16x3
+    for bad in (torch.zeros(4, 8), torch.zeros(4, 8, dtype=torch.bfloat16), torch.zeros(2, 4, 8)):
+        with pytest.raises(ValueError, match="contiguous 2-D float32 device tensor"):
+            split_bf16x3(bad)
